@@ -1,0 +1,215 @@
+/*
+ * xsimgs_amd C-ABI: the Gaussian-splatting rasterization hot path of xsimgs on MI355X (gfx950).
+ *
+ * Every entry point takes device pointers, explicit sizes and a HIP stream, never allocates
+ * device memory (scratch comes in through a `workspace` argument sized by the matching
+ * *_workspace_bytes query), and returns XSG_OK or a negative error code; xsg_last_error()
+ * then holds a message (thread-local). Work is enqueued on `stream`; the only blocking call is
+ * xsg_isect_count, which copies the intersection total to the host (as the reference's
+ * `.item()` does).
+ *
+ * Reference interfaces replaced (whesense/xsimgs, pybind module xsimgs._C):
+ *   xsg_ut_project            <Camera>.projection_utgs[_phm]   include/cameras/bind.h:82-114,
+ *                             ut_kernels.h:249-305, ut_phm_kernels.h:125-173
+ *   xsg_project_points        <Camera>.projection[_nojac]       bind.h:66-81, projection_kernels.h:259-309
+ *   xsg_camera_rays           <Camera>.camera_rays (forward)    bind.h:47-53, ray_kernels.h:7-59
+ *   xsg_pixel_time*           <Camera>.pixel_time*              bind.h:54-65, time_kernels.h:5-241
+ *   xsg_sh_fwd / xsg_sh_bwd   spherical_harmonics_fused_{fwd,bwd} csrc/color/sh_fwd.cu:248-259,
+ *                             sh_bwd.cu:379-390
+ *   xsg_mask_radii[_packed]   mask_radii / mask_radii_packed    csrc/tiling/mask_radii.cu:82-88
+ *   xsg_isect_count + xsg_isect_fill
+ *                             isect_regular_tiles / isect_lidar_tiles / isect_spherical_tiles
+ *                             regular_tiling.cu:138-146, phm_lidar_tiling.cu:354-375,
+ *                             phm_spherical_tiling.cu:294-314
+ *   xsg_radix_sort_pairs_u64_i32
+ *                             sort_intersections (cub SortPairs) tiling_common.cu:102-162
+ *   xsg_isect_offset_encode   isect_offset_encode               tiling_common.cu:165-168
+ *   xsg_eval3d_fwd / xsg_eval3d_bwd (static and dynamic)
+ *                             rasterize_eval3d_[dynamic_]{fwd,bwd} eval3d_fwd.cu:310-316,
+ *                             eval3d_bwd.cu:406-408, eval3d_dynamic_fwd.cu:325-332,
+ *                             eval3d_dynamic_bwd.cu:322-432
+ *   xsg_eval3d_supported_ndims eval3d_supported_ndims           eval3d_bind.cpp:12-15
+ */
+#ifndef XSIMGS_AMD_H
+#define XSIMGS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XSG_ABI_VERSION 1
+
+/* return codes */
+#define XSG_OK 0
+#define XSG_ERR_INVALID (-1)     /* bad argument (shape, dtype-implied size, degree, CDIM ...) */
+#define XSG_ERR_LDS (-2)         /* tile too large for the local data share */
+#define XSG_ERR_LAUNCH (-3)      /* HIP launch / runtime failure */
+#define XSG_ERR_UNSUPPORTED (-4) /* feature not provided by this build */
+
+/* camera kinds and projection modes (enum class ProjectionMode, include/cameras/camera.h:15-19) */
+#define XSG_CAM_PINHOLE 0
+#define XSG_CAM_SPHERICAL 1
+#define XSG_CAM_LIDAR 2
+#define XSG_MODE_CENTRAL 0
+#define XSG_MODE_NEGATIVE 1
+#define XSG_MODE_POSITIVE 2
+
+/* tiling kinds */
+#define XSG_TILING_REGULAR 0    /* isect_regular_tiles: exclusive rectangle, flags ignored */
+#define XSG_TILING_LIDAR 1      /* isect_lidar_tiles: irregular elevation grid, inclusive */
+#define XSG_TILING_SPHERICAL 2  /* isect_spherical_tiles: regular angular grid, exclusive */
+
+typedef struct ihipStream_t* xsg_stream_t; /* == hipStream_t */
+
+const char* xsg_last_error(void);
+int xsg_abi_version(void);
+
+/* Number of float32 elements of a camera pack of `kind` (pinhole/spherical 21, lidar 23).
+ * Replaces Camera<Impl>::pack_elements (camera.h:141-143); the layout is documented in
+ * xsimgs_amd/csrc/xsg_common.h. */
+int xsg_camera_pack_elements(int kind);
+
+/* ---------------------------------------------------------------- cameras */
+int xsg_ut_project(int kind, int phm, const float* pack, int64_t n, const float* means,
+                   const float* velocity, const float* scales, const float* quats,
+                   const float* opacity, float width, float height, float ut_alpha, float ut_beta,
+                   float ut_kappa, float residual_thr, float max_residual, float max_margin,
+                   uint8_t* flags, float* radii, float* means2d, float* depths, xsg_stream_t stream);
+
+int xsg_project_points(int kind, const float* pack, int64_t n, const float* points,
+                       const float* velocity, float residual_thr, float max_residual,
+                       float max_margin, int mode, int no_jacobian, float* uvdt, uint8_t* mask,
+                       xsg_stream_t stream);
+
+int xsg_camera_rays(int kind, const float* pack, int width, int height, int world_space,
+                    int normalized, float* ray_o, float* ray_d, uint8_t* valid,
+                    xsg_stream_t stream);
+
+/* per-pixel (uv == NULL) or per-uv capture time; `delta` subtracts the pose time */
+int xsg_pixel_time(int kind, const float* pack, int width, int height, const float* uv, int64_t n_uv,
+                   int delta, float* out, xsg_stream_t stream);
+
+/* ------------------------------------------------------- spherical harmonics */
+int xsg_sh_fwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
+               const float* coeffs, const float* coeffs_dc, const uint32_t* mask, int layout_3kn,
+               float* out, xsg_stream_t stream);
+
+size_t xsg_sh_bwd_workspace_bytes(int64_t n);
+/* d_coeffs (every band written), d_coeffs_dc (if has_dc), d_positions and d_origin[3] are outputs;
+ * none needs zero-initialisation. */
+int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
+               const float* coeffs, const uint32_t* mask, int layout_3kn, const float* d_output,
+               int has_dc, float* d_coeffs, float* d_coeffs_dc, float* d_positions,
+               float* d_origin, void* workspace, xsg_stream_t stream);
+
+/* ------------------------------------------------------------------ binning */
+int xsg_mask_radii(int64_t n, const uint8_t* mask, float* radii, xsg_stream_t stream);
+int xsg_mask_radii_packed(int64_t n, const uint32_t* packed_mask, float* radii, xsg_stream_t stream);
+
+typedef struct {
+    int kind;                 /* XSG_TILING_* */
+    int n_cams;               /* >= 1; inputs are [n_cams, n] camera-major, keys carry the camera id */
+    int64_t n;                /* Gaussians per camera */
+    const float* means2d;     /* [n_cams, n, 2] pixels */
+    const float* radii;       /* [n_cams, n, 2] */
+    const float* depths;      /* [n_cams, n] */
+    const uint8_t* flags;     /* [n_cams, n]; lidar / spherical only */
+    /* lidar / spherical seam re-projection (flag == 2); NULL for regular tiling */
+    const float* camera_pack;
+    const float* points;      /* [n, 3] */
+    const float* velocity;    /* [n, 3] or NULL */
+    const float* scales;      /* [n, 3] */
+    const float* quats;       /* [n, 4] */
+    const float* opacity;     /* [n] or NULL */
+    const float* elev_boundaries; /* lidar: [n_elev] */
+    int n_elev;
+    float img_width, img_height;  /* image size (float, as the reference lidar/spherical ops take it) */
+    int tile_w, tile_h;
+    float ut_alpha, ut_beta, ut_kappa;
+} xsg_isect_desc;
+
+/* geometry derived from a descriptor: tiles along u / v, tile count, key bits above 32 */
+int xsg_isect_geometry(const xsg_isect_desc* d, int* n_tiles_w, int* n_tiles_h, int* tile_n_bits,
+                       int* key_bits_above_32);
+
+size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d);
+/* Pass 1: tiles per Gaussian into tiles_per_gauss [n_cams*n]; *n_isects (host) receives the total
+ * and *n_visible the number of non-empty spans, which xsg_isect_fill takes back. Blocks on
+ * `stream` for that one device->host copy. `workspace` carries state into xsg_isect_fill. */
+int xsg_isect_count(const xsg_isect_desc* d, int32_t* tiles_per_gauss, void* workspace,
+                    int64_t* n_isects, int64_t* n_visible, xsg_stream_t stream);
+
+size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible);
+/* Pass 2: intersection keys ((cam | tile) << 32 | depth bits) and flattened Gaussian ids
+ * (cam * n + gaussian); sorted by key bits [0, 32 + key_bits_above_32) with ties in fill order
+ * when `sort`, else in the reference's fill order. Consumes (overwrites) count_workspace. */
+int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int sort,
+                   void* count_workspace, void* fill_workspace, int64_t* isect_ids,
+                   int32_t* flatten_ids, xsg_stream_t stream);
+
+/* offsets [n_cams, n_tiles_h, n_tiles_w]: first sorted index of every (camera, tile) */
+int xsg_isect_offset_encode(const int64_t* isect_ids, int64_t n_isects, int n_tiles_w, int n_tiles_h,
+                            int n_cams, int32_t* offsets, xsg_stream_t stream);
+
+/* Stable LSD radix sort of (key, value) pairs by key bits [begin_bit, end_bit).
+ * The sorted data ends in (keys, vals) when *selector == 0, else in (keys_alt, vals_alt). */
+size_t xsg_radix_sort_workspace_bytes(int64_t n);
+int xsg_radix_sort_pairs_u64_i32(int64_t* keys, int32_t* vals, int64_t* keys_alt, int32_t* vals_alt,
+                                 int64_t n, int begin_bit, int end_bit, void* workspace,
+                                 int* selector, xsg_stream_t stream);
+
+/* ------------------------------------------------------------ compositing */
+/* Writes the supported colour dimensions (common.h:5-25) into out[0..cap) and returns their count. */
+int xsg_eval3d_supported_ndims(int* out, int cap);
+
+typedef struct {
+    int cdim;                      /* colour channels; 0 = no colours */
+    int64_t n;                     /* Gaussians */
+    int n_cams;                    /* >= 1; cameras batched camera-major */
+    const float* means;            /* [n, 3] */
+    const float* quats;            /* [n, 4] (w, x, y, z), normalised inside */
+    const float* scales;           /* [n, 3] activated */
+    const float* colors;           /* [n_cams, n, cdim] or NULL */
+    const float* opacities;        /* [n] activated */
+    const float* velocity;         /* dynamic scenes: [n, 3], else NULL */
+    const float* ray_time_delta;   /* dynamic scenes: [n_cams, H, W], else NULL */
+    const float* ray_o;            /* [n_cams, H, W, 3] */
+    const float* ray_d;            /* [n_cams, H, W, 3] */
+    int width, height, tile_w, tile_h, n_tiles_w, n_tiles_h;
+    const int32_t* tile_offsets;   /* [n_cams, n_tiles_h, n_tiles_w] */
+    const int32_t* flatten_ids;    /* [n_isects], values cam * n + gaussian */
+    int64_t n_isects;
+    /* forward outputs */
+    float* out_rgb;                /* [n_cams, H, W, cdim] */
+    float* out_depth;              /* [n_cams, H, W] */
+    float* out_alpha;              /* [n_cams, H, W] */
+    int32_t* out_last_ids;         /* [n_cams, H, W] */
+    /* backward inputs */
+    const float* render_alpha;
+    const int32_t* last_ids;
+    const float* v_rgb;            /* [n_cams, H, W, cdim] or NULL */
+    const float* v_depth;
+    const float* v_alpha;
+    /* backward outputs: accumulated with atomics, zero-initialised by xsg_eval3d_bwd itself */
+    float* v_means;
+    float* v_quats;
+    float* v_scales;
+    float* v_opacities;
+    float* v_colors;               /* NULL when cdim == 0 */
+    float* v_ray_o;
+    float* v_ray_d;
+    float* v_velocity;             /* dynamic only */
+    float* v_time_delta;           /* dynamic only */
+} xsg_eval3d_args;
+
+int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream);
+size_t xsg_eval3d_bwd_workspace_bytes(int64_t n, int cdim);
+int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

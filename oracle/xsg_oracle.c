@@ -1,0 +1,1148 @@
+/*
+ * CPU oracle for the xsimgs Gaussian-splatting hot path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Restates the reference algorithm (whesense/xsimgs) on the CPU, one function per
+ * reference kernel, each citing the reference file:line it follows. Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load this library, and
+ * only as the checker or the timed CPU baseline; the product path never does.
+ *
+ * Parity pins (what checks each function against something other than itself):
+ *   orc_ut_weights            closed form (tests/test_oracle_pins.py)
+ *   orc_project_utgs          on-axis closed form, EWA small-scale limit,
+ *                             rolling-shutter residual invariant
+ *   orc_project_utgs_phm      seam flag cases built by hand; phm seam selection
+ *                             end-to-end is "parity unpinned" beyond those cases
+ *   orc_camera_rays           closed form pinhole / spherical / lidar rays
+ *   orc_sh_fwd / orc_sh_bwd   scipy.special.sph_harm basis, fp64 finite differences
+ *   orc_isect_*               brute-force tile enumeration in Python, numpy stable sort
+ *   orc_sort_pairs            numpy argsort(kind="stable")
+ *   orc_offset_encode         numpy searchsorted
+ *   orc_eval3d_fwd            one-Gaussian closed form, two-Gaussian analytic
+ *                             composite, depth-sorted brute force without tiles
+ *   orc_eval3d_bwd            fp64 finite differences of orc_eval3d_fwd (no-clamp
+ *                             regime); the 0.99 clamp branch is pinned only by
+ *                             code reading ("parity unpinned" inside that band)
+ */
+#include "xsg_oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define K(x) ((real)(x))
+#ifdef ORC_DOUBLE
+#define SQRT sqrt
+#define EXP exp
+#define LOG log
+#define FLOOR floor
+#define CEIL ceil
+#define ATAN2 atan2
+#define ASIN asin
+#define SIN sin
+#define COS cos
+#define FABS fabs
+#define COPYSIGN copysign
+#define FMIN fmin
+#define FMAX fmax
+#define ORC_PI 3.14159265358979323846
+#else
+#define SQRT sqrtf
+#define EXP expf
+#define LOG logf
+#define FLOOR floorf
+#define CEIL ceilf
+#define ATAN2 atan2f
+#define ASIN asinf
+#define SIN sinf
+#define COS cosf
+#define FABS fabsf
+#define COPYSIGN copysignf
+#define FMIN fminf
+#define FMAX fmaxf
+#define ORC_PI ((float)3.14159265358979323846)
+#endif
+
+#define ALPHA_THR_MIN (K(1.0) / K(255.0))
+
+typedef struct { real x, y; } v2;
+typedef struct { real x, y, z; } v3;
+/* glm-style 3x3 matrix: m[col][row] */
+typedef struct { real m[3][3]; } m3;
+
+static inline v3 V3(real x, real y, real z) { v3 r = {x, y, z}; return r; }
+static inline v3 add3(v3 a, v3 b) { return V3(a.x + b.x, a.y + b.y, a.z + b.z); }
+static inline v3 sub3(v3 a, v3 b) { return V3(a.x - b.x, a.y - b.y, a.z - b.z); }
+static inline v3 scl3(v3 a, real s) { return V3(a.x * s, a.y * s, a.z * s); }
+static inline real dot3(v3 a, v3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+static inline v3 cross3(v3 a, v3 b) {
+    return V3(a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x);
+}
+static inline v3 ld3(const real *p) { return V3(p[0], p[1], p[2]); }
+static inline v3 mv(const m3 *M, v3 v) { /* glm M * v */
+    return V3(M->m[0][0] * v.x + M->m[1][0] * v.y + M->m[2][0] * v.z,
+              M->m[0][1] * v.x + M->m[1][1] * v.y + M->m[2][1] * v.z,
+              M->m[0][2] * v.x + M->m[1][2] * v.y + M->m[2][2] * v.z);
+}
+static inline m3 transpose3(const m3 *A) {
+    m3 r;
+    for (int c = 0; c < 3; ++c) for (int k = 0; k < 3; ++k) r.m[c][k] = A->m[k][c];
+    return r;
+}
+static inline v3 normalize3(v3 v) { real l = SQRT(dot3(v, v)); return scl3(v, K(1.0) / l); }
+
+/* ------------------------------------------------------------------------- */
+/* UT weights: include/cameras/ut_kernels.h:17-36                           */
+/* ------------------------------------------------------------------------- */
+void orc_ut_weights(real ut_alpha, real ut_beta, real ut_kappa, real *out4) {
+    const real lam = ut_alpha * ut_alpha * (K(3) + ut_kappa) - K(3);
+    out4[0] = lam / (K(3) + lam);
+    out4[1] = lam / (K(3) + lam) + (K(1) - ut_alpha * ut_alpha + ut_beta);
+    out4[2] = K(1) / (K(2) * (K(3) + lam));
+    out4[3] = SQRT(lam + K(3));
+}
+
+/* ------------------------------------------------------------------------- */
+/* Rolling-shutter projection: include/cameras/projection_kernels.h:12-256   */
+/* ------------------------------------------------------------------------- */
+static void jac_quat_from_axis_angle(v3 w, real t, real *qw, v3 *qxyz, real *dqw, v3 *dqxyz) {
+    /* projection_kernels.h:12-36 */
+    const real w_norm2 = dot3(w, w);
+    const real w_norm = SQRT(w_norm2);
+    const real theta = w_norm * FABS(t);
+    const real sin_half = SIN(K(0.5) * theta), cos_half = COS(K(0.5) * theta);
+    const real scale = (theta < K(1e-2)) ? K(0.5) - theta * theta * (K(1.0) / K(48.0))
+                                         : sin_half / theta;
+    *qw = cos_half;
+    *qxyz = scl3(scl3(w, scale), t);
+    *dqw = K(-0.5) * COPYSIGN(K(1.0), t) * sin_half * w_norm;
+    *dqxyz = scl3(w, K(0.5) * cos_half);
+}
+
+static v3 quat_apply(real w, v3 xyz, v3 p) { /* projection_kernels.h:67-71 */
+    const v3 uv = cross3(xyz, p);
+    const v3 uuv = cross3(xyz, uv);
+    return add3(p, scl3(add3(scl3(uv, w), uuv), K(2.0)));
+}
+
+static void jac_world_to_camera(const orc_camera *c, v3 point, v3 pvel, real time,
+                                v3 *result, v3 *d_result) {
+    /* projection_kernels.h:74-113 (quat_mul :38-51, quat_apply jac :53-65) */
+    real w1, dw1; v3 xyz1, dxyz1;
+    jac_quat_from_axis_angle(ld3(c->w), time, &w1, &xyz1, &dw1, &dxyz1);
+    const real w2 = c->q[0];
+    const v3 xyz2 = V3(c->q[1], c->q[2], c->q[3]);
+    real w = w1 * w2 - dot3(xyz1, xyz2);
+    v3 xyz = add3(add3(scl3(xyz2, w1), scl3(xyz1, w2)), cross3(xyz1, xyz2));
+    real dw = dw1 * w2 - dot3(dxyz1, xyz2);
+    v3 dxyz = add3(add3(scl3(xyz2, dw1), scl3(dxyz1, w2)), cross3(dxyz1, xyz2));
+    xyz = scl3(xyz, K(-1));
+    dxyz = scl3(dxyz, K(-1));
+    const v3 vdiff = sub3(pvel, ld3(c->v));
+    const v3 p = add3(sub3(point, ld3(c->t)), scl3(vdiff, time));
+    const v3 uv = cross3(xyz, p);
+    const v3 uuv = cross3(xyz, uv);
+    *result = add3(p, scl3(add3(scl3(uv, w), uuv), K(2.0)));
+    const v3 duv = cross3(dxyz, p);
+    const v3 dp = scl3(add3(add3(scl3(uv, dw), scl3(duv, w)), add3(cross3(dxyz, uv), cross3(xyz, duv))),
+                       K(2.0));
+    *d_result = add3(dp, quat_apply(w, xyz, vdiff));
+}
+
+static real u_pose_of(const orc_camera *c) { /* spherical.h:113-114 */
+    return (FABS(c->rolling[0]) > K(0)) ? (c->pose_time - c->trigger_time) / c->rolling[0] : K(0.5);
+}
+
+static v2 angles_to_uv(const orc_camera *c, int mode, real phi, real theta) {
+    /* csrc/cameras/spherical.h:109-125 */
+    real u = (phi - c->impl[0]) / c->impl[1];
+    const real u_pose = u_pose_of(c);
+    const real u_offset = (K(2.0) * ORC_PI / FABS(c->impl[1]));
+    if (c->rolling[0] > 0) {
+        if (mode == ORC_MODE_NEG && u > u_pose) u = u - u_offset;
+        if (mode == ORC_MODE_POS && u < u_pose) u = u + u_offset;
+    } else {
+        if (mode == ORC_MODE_NEG && u < u_pose) u = u + u_offset;
+        if (mode == ORC_MODE_POS && u > u_pose) u = u - u_offset;
+    }
+    const real v = (theta - c->impl[2]) / c->impl[3];
+    v2 r = {u, v};
+    return r;
+}
+
+static void point_to_uvd_jacob(const orc_camera *c, int mode, v3 p, v3 dp, v3 *uvd, v2 *du_dv) {
+    if (c->kind == ORC_PINHOLE) {
+        /* csrc/cameras/perspective.cu:36-52 */
+        const real fx = c->impl[0], fy = c->impl[1], cx = c->impl[2], cy = c->impl[3];
+        *uvd = V3(p.x * fx / p.z + cx, p.y * fy / p.z + cy, p.z);
+        du_dv->x = fx * (dp.x - uvd->x * dp.z) / uvd->z;
+        du_dv->y = fy * (dp.y - uvd->y * dp.z) / uvd->z;
+    } else {
+        /* csrc/cameras/spherical.h:133-153 */
+        const real x2y2 = p.x * p.x + p.y * p.y;
+        const real r = SQRT(x2y2 + p.z * p.z);
+        const real phi = ATAN2(-p.x, -p.y) + ORC_PI;
+        const real theta = ASIN(p.z / r);
+        const v2 uv = angles_to_uv(c, mode, phi, theta);
+        *uvd = V3(uv.x, uv.y, r);
+        const real x2y2_sqrt = SQRT(x2y2);
+        const real r2 = r * r;
+        const real mul = p.z / (r2 * x2y2_sqrt);
+        du_dv->x = ((-p.x * dp.y + p.y * dp.x) / x2y2) / c->impl[1];
+        du_dv->y = ((x2y2_sqrt * dp.z) / r2 - mul * (p.x * dp.x + p.y * dp.y)) / c->impl[3];
+    }
+}
+
+static void camera_projection(const orc_camera *c, v3 p_world, v3 p_vel, real thr, real max_res,
+                              real margin, int mode, real uvdt[4], int *valid) {
+    /* projection_kernels.h:201-256 with jac_camera_projection_iteration :116-174 */
+    v3 uvd = V3(0, 0, 0);
+    real p_time = 0;
+    if (mode == ORC_MODE_NEG) p_time = -FABS(c->rolling[0]) * K(0.5);
+    else if (mode == ORC_MODE_POS) p_time = FABS(c->rolling[0]) * K(0.5);
+    real residual = 0;
+    for (int i = 0; i < 5; ++i) {
+        v3 pc, jpc; v2 du_dv;
+        jac_world_to_camera(c, p_world, p_vel, p_time, &pc, &jpc);
+        point_to_uvd_jacob(c, mode, pc, jpc, &uvd, &du_dv);
+        const real assumed = c->pose_time + p_time;
+        const real real_time = c->trigger_time + (uvd.x * c->rolling[0] + uvd.y * c->rolling[1]);
+        residual = assumed - real_time;
+        const real d_res = K(1.0) - (du_dv.x * c->rolling[0] + du_dv.y * c->rolling[1]);
+        p_time -= residual / d_res;
+        if ((uvd.z <= K(0)) || (uvd.x < -margin) || (uvd.x > K(1) + margin) ||
+            (uvd.y < -margin) || (uvd.y > K(1) + margin)) {
+            *valid = 0;
+            uvdt[0] = uvdt[1] = uvdt[2] = uvdt[3] = 0;
+            return;
+        }
+        if (FABS(residual) < thr) break;
+    }
+    uvdt[0] = uvd.x; uvdt[1] = uvd.y; uvdt[2] = uvd.z; uvdt[3] = p_time;
+    *valid = *valid && (FABS(residual) < max_res) && (uvd.z > K(0));
+}
+
+/* unscented_transform_deltas: ut_kernels.h:38-49. deltas[i] = column i of R(q) * s_i * sqrt(3+lambda).
+ * The quaternion is normalised first (unit-quaternion assumption; toast's to_matrix is not in the tree). */
+static void ut_deltas(real sqrt_dl, const real *q, const real *s, v3 d[3]) {
+    real w = q[0], x = q[1], y = q[2], z = q[3];
+    const real inv = K(1.0) / SQRT(w * w + x * x + y * y + z * z);
+    w *= inv; x *= inv; y *= inv; z *= inv;
+    const v3 c0 = V3(K(1) - K(2) * (y * y + z * z), K(2) * (x * y + w * z), K(2) * (x * z - w * y));
+    const v3 c1 = V3(K(2) * (x * y - w * z), K(1) - K(2) * (x * x + z * z), K(2) * (y * z + w * x));
+    const v3 c2 = V3(K(2) * (x * z + w * y), K(2) * (y * z - w * x), K(1) - K(2) * (x * x + y * y));
+    d[0] = scl3(c0, s[0] * sqrt_dl);
+    d[1] = scl3(c1, s[1] * sqrt_dl);
+    d[2] = scl3(c2, s[2] * sqrt_dl);
+}
+
+static int unscented_transform(const orc_camera *c, const real ut[4], v2 img, int mode, real thr,
+                               real max_res, real margin, v3 p_world, v3 p_vel, const v3 d[3],
+                               v2 *mean2d, real *depth, real *u_distance, v3 *cov2d) {
+    /* ut_kernels.h:52-137 */
+    real uvdt[4]; int valid = 1;
+    v2 pts[7];
+    camera_projection(c, p_world, p_vel, thr, max_res, margin, mode, uvdt, &valid);
+    if (!valid) return 0;
+    pts[0].x = uvdt[0] * img.x; pts[0].y = uvdt[1] * img.y;
+    mean2d->x = ut[0] * pts[0].x; mean2d->y = ut[0] * pts[0].y;
+    *depth = uvdt[2];
+    real u_min = pts[0].x, u_max = pts[0].x;
+    real sign = K(1.0);
+    for (int i = 0; i < 6; ++i) {
+        camera_projection(c, add3(p_world, scl3(d[i / 2], sign)), p_vel, thr, max_res, margin, mode,
+                          uvdt, &valid);
+        pts[i + 1].x = uvdt[0] * img.x; pts[i + 1].y = uvdt[1] * img.y;
+        mean2d->x += ut[2] * pts[i + 1].x; mean2d->y += ut[2] * pts[i + 1].y;
+        u_min = FMIN(u_min, pts[i + 1].x);
+        u_max = FMAX(u_max, pts[i + 1].x);
+        sign *= K(-1.0);
+    }
+    if (!valid) return 0;
+    *u_distance = u_max - u_min;
+    real vx = pts[0].x - mean2d->x, vy = pts[0].y - mean2d->y;
+    *cov2d = V3(ut[1] * (vx * vx), ut[1] * (vx * vy), ut[1] * (vy * vy));
+    for (int i = 1; i < 7; ++i) {
+        vx = pts[i].x - mean2d->x; vy = pts[i].y - mean2d->y;
+        cov2d->x += ut[2] * (vx * vx); cov2d->y += ut[2] * (vx * vy); cov2d->z += ut[2] * (vy * vy);
+    }
+    const real det = cov2d->x * cov2d->z - cov2d->y * cov2d->y;
+    if (det <= K(0) || cov2d->x < 0 || cov2d->z < 0) return 0;
+    return 1;
+}
+
+static int ut_projection(const orc_camera *c, int mode, const real ut[4], v2 img, real thr,
+                         real max_res, real margin, v3 p_world, v3 p_vel, real opac,
+                         const v3 d[3], v2 *mean2d, v2 *radii, real *depth, real *u_distance) {
+    /* ut_kernels.h:140-184 */
+    v3 cov2d = V3(0, 0, 0);
+    const int result = unscented_transform(c, ut, img, mode, thr, max_res, margin, p_world, p_vel, d,
+                                           mean2d, depth, u_distance, &cov2d);
+    const real extend = FMIN(K(3.33), SQRT(K(2.0) * LOG(opac / ALPHA_THR_MIN)));
+    radii->x = extend * SQRT(FMAX(K(0), cov2d.x));
+    radii->y = extend * SQRT(FMAX(K(0), cov2d.z));
+    const int ix = !(((mean2d->x + radii->x) < 0) || (img.x < (mean2d->x - radii->x)));
+    const int iy = !(((mean2d->y + radii->y) < 0) || (img.y < (mean2d->y - radii->y)));
+    return result && ix && iy;
+}
+
+/* Projection of points (uvdt + mask): projection_kernels.h:259-309 (jacobian variant). */
+void orc_projection(const orc_camera *c, int n, const real *pts, const real *vel, real thr,
+                    real max_res, real margin, int mode, real *uvdt_out, uint8_t *mask_out) {
+    for (int i = 0; i < n; ++i) {
+        int valid = 1; real uvdt[4];
+        const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
+        camera_projection(c, ld3(pts + 3 * i), pv, thr, max_res, margin, mode, uvdt, &valid);
+        uvdt[3] += c->pose_time;
+        memcpy(uvdt_out + 4 * i, uvdt, sizeof(uvdt));
+        valid = valid && (uvdt[0] >= 0 && uvdt[1] >= 0) && (uvdt[0] <= 1 && uvdt[1] <= 1);
+        mask_out[i] = (uint8_t)valid;
+    }
+}
+
+/* UT projection: unscented_transform_kernel ut_kernels.h:187-246 + launcher :249-305.
+ * Outputs are zero for culled Gaussians (the reference zero-initialises, :276-280). */
+void orc_project_utgs(const orc_camera *c, int n, const real *means, const real *vel,
+                      const real *scales, const real *quats, const real *opacity, real width,
+                      real height, const real ut[4], real thr, real max_res, real margin,
+                      uint8_t *flags, real *radii, real *means2d, real *depths) {
+    const v2 img = {width, height};
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < n; ++i) {
+        flags[i] = 0; radii[2 * i] = radii[2 * i + 1] = 0;
+        means2d[2 * i] = means2d[2 * i + 1] = 0; depths[i] = 0;
+        const real op = opacity ? opacity[i] : K(1.0);
+        if (op < ALPHA_THR_MIN) continue;
+        v3 d[3];
+        ut_deltas(ut[3], quats + 4 * i, scales + 3 * i, d);
+        v2 m2, r2; real depth = 0, udist = 0;
+        const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
+        const int ok = ut_projection(c, ORC_MODE_CENTRAL, ut, img, thr, max_res, margin,
+                                     ld3(means + 3 * i), pv, op, d, &m2, &r2, &depth, &udist);
+        if (!ok) continue;
+        radii[2 * i] = r2.x; radii[2 * i + 1] = r2.y;
+        flags[i] = 1;
+        means2d[2 * i] = m2.x; means2d[2 * i + 1] = m2.y;
+        depths[i] = depth;
+    }
+}
+
+/* Phase-modelled UT: unscented_transform_phm_kernel ut_phm_kernels.h:13-114. */
+void orc_project_utgs_phm(const orc_camera *c, int n, const real *means, const real *vel,
+                          const real *scales, const real *quats, const real *opacity, real width,
+                          real height, const real ut[4], real thr, real max_res, real margin,
+                          uint8_t *flags, real *radii, real *means2d, real *depths) {
+    const v2 img = {width, height};
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < n; ++i) {
+        flags[i] = 0; radii[2 * i] = radii[2 * i + 1] = 0;
+        means2d[2 * i] = means2d[2 * i + 1] = 0; depths[i] = 0;
+        const real op = opacity ? opacity[i] : K(1.0);
+        if (op < ALPHA_THR_MIN) continue;
+        v3 d[3];
+        ut_deltas(ut[3], quats + 4 * i, scales + 3 * i, d);
+        const v3 pw = ld3(means + 3 * i);
+        const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
+        v2 rc = {0, 0}, rl = {0, 0}, rr = {0, 0}, mc = {0, 0}, ml = {0, 0}, mr = {0, 0};
+        real dc = 0, dl = 0, dr = 0, ud = 0;
+        int res = ut_projection(c, ORC_MODE_CENTRAL, ut, img, thr, max_res, margin, pw, pv, op, d,
+                                &mc, &rc, &dc, &ud);
+        if (!res) continue;
+        const real u_pi = ORC_PI * img.x / FABS(c->impl[1]);
+        const int r_c = res * ((ud > u_pi) + 1);
+        res = ut_projection(c, ORC_MODE_NEG, ut, img, thr, max_res, margin, pw, pv, op, d, &ml, &rl,
+                            &dl, &ud);
+        const int r_l = res * ((ud > u_pi) + 1);
+        res = ut_projection(c, ORC_MODE_POS, ut, img, thr, max_res, margin, pw, pv, op, d, &mr, &rr,
+                            &dr, &ud);
+        const int r_r = res * ((ud > u_pi) + 1);
+        if (r_l == 1 && r_r == 1) {
+            flags[i] = 2; radii[2 * i] = rl.x; radii[2 * i + 1] = rl.y;
+            means2d[2 * i] = ml.x; means2d[2 * i + 1] = ml.y; depths[i] = dl;
+            continue;
+        }
+        if (r_c == 1) {
+            flags[i] = 1; radii[2 * i] = rc.x; radii[2 * i + 1] = rc.y;
+            means2d[2 * i] = mc.x; means2d[2 * i + 1] = mc.y; depths[i] = dc;
+            continue;
+        }
+        if (r_l != 1 && r_r != 1) continue;
+        const int use_left = r_l != 1;  /* reference selects the non-compact side's partner */
+        flags[i] = 1;
+        radii[2 * i] = use_left ? rl.x : rr.x; radii[2 * i + 1] = use_left ? rl.y : rr.y;
+        means2d[2 * i] = use_left ? ml.x : mr.x; means2d[2 * i + 1] = use_left ? ml.y : mr.y;
+        depths[i] = use_left ? dl : dr;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Camera rays: ray_kernels.h:7-59, camera.h:85-131, base_camera_impl.h:9-14 */
+/* ------------------------------------------------------------------------- */
+static v3 pixel_to_camera_ray(const orc_camera *c, real u, real v) {
+    if (c->kind == ORC_PINHOLE) { /* perspective.cu:13-16 */
+        return V3((u - c->impl[2]) / c->impl[0], (v - c->impl[3]) / c->impl[1], K(1.0));
+    }
+    /* spherical.h:9-22, 121-127 */
+    const real az = c->impl[0] + u * c->impl[1];
+    const real el = c->impl[2] + v * c->impl[3];
+    const real xy = K(1.0) * COS(el);
+    return V3(xy * SIN(az), xy * COS(az), K(1.0) * SIN(el));
+}
+
+void orc_camera_rays(const orc_camera *c, int width, int height, int world_space, int normalized,
+                     real *ray_o, real *ray_d) {
+    for (int idx = 0; idx < width * height; ++idx) {
+        const int px = idx % width, py = idx / width;
+        const real u = ((real)px + K(0.5)) / (real)width;
+        const real v = (c->kind == ORC_LIDAR) ? c->beam_v[py] : ((real)py + K(0.5)) / (real)height;
+        v3 ray = pixel_to_camera_ray(c, u, v);
+        if (normalized) ray = normalize3(ray);
+        v3 o = V3(0, 0, 0);
+        if (world_space) {
+            /* camera.h:101-103,125-131: pose at the pixel's time delta, q = exp(w dt) * q0, t = t0 + v dt */
+            const real dt = c->trigger_time + (u * c->rolling[0] + v * c->rolling[1]) - c->pose_time;
+            real w1, dw1; v3 xyz1, dxyz1;
+            jac_quat_from_axis_angle(ld3(c->w), dt, &w1, &xyz1, &dw1, &dxyz1);
+            const real w2 = c->q[0];
+            const v3 xyz2 = V3(c->q[1], c->q[2], c->q[3]);
+            const real qw = w1 * w2 - dot3(xyz1, xyz2);
+            const v3 qv = add3(add3(scl3(xyz2, w1), scl3(xyz1, w2)), cross3(xyz1, xyz2));
+            o = add3(ld3(c->t), scl3(ld3(c->v), dt));
+            ray = quat_apply(qw, qv, ray);
+        }
+        ray_o[3 * idx] = o.x; ray_o[3 * idx + 1] = o.y; ray_o[3 * idx + 2] = o.z;
+        ray_d[3 * idx] = ray.x; ray_d[3 * idx + 1] = ray.y; ray_d[3 * idx + 2] = ray.z;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Spherical harmonics: csrc/color/sh_fwd.cu:16-159, sh_bwd.cu:20-315         */
+/* ------------------------------------------------------------------------- */
+static real sh_eval(int deg, v3 dir, const real *cf, const real *dc, long bo) {
+    /* sh_fwd.cu:16-115; cf points at band 0 (or band 1 when dc != NULL) of one channel */
+    real result;
+    const real *c;
+    if (dc) { result = K(0.2820947917738781) * dc[0]; c = cf - bo; }
+    else { result = K(0.2820947917738781) * cf[0]; c = cf; }
+    if (deg >= 1) {
+        const real x = dir.x, y = dir.y, z = dir.z;
+        result += K(0.48860251190292) * (-y * c[bo] + z * c[2 * bo] - x * c[3 * bo]);
+        if (deg >= 2) {
+            const real z2 = z * z;
+            const real fTmp0B = K(-1.092548430592079) * z;
+            const real fC1 = x * x - y * y, fS1 = K(2) * x * y;
+            const real p6 = K(0.9461746957575601) * z2 - K(0.3153915652525201);
+            const real p7 = fTmp0B * x, p5 = fTmp0B * y;
+            const real p8 = K(0.5462742152960395) * fC1, p4 = K(0.5462742152960395) * fS1;
+            result += p4 * c[4 * bo] + p5 * c[5 * bo] + p6 * c[6 * bo] + p7 * c[7 * bo] + p8 * c[8 * bo];
+            if (deg >= 3) {
+                const real fTmp0C = K(-2.285228997322329) * z2 + K(0.4570457994644658);
+                const real fTmp1B = K(1.445305721320277) * z;
+                const real fC2 = x * fC1 - y * fS1, fS2 = x * fS1 + y * fC1;
+                const real p12 = z * (K(1.865881662950577) * z2 - K(1.119528997770346));
+                const real p13 = fTmp0C * x, p11 = fTmp0C * y;
+                const real p14 = fTmp1B * fC1, p10 = fTmp1B * fS1;
+                const real p15 = K(-0.5900435899266435) * fC2, p9 = K(-0.5900435899266435) * fS2;
+                result += p9 * c[9 * bo] + p10 * c[10 * bo] + p11 * c[11 * bo] + p12 * c[12 * bo] +
+                          p13 * c[13 * bo] + p14 * c[14 * bo] + p15 * c[15 * bo];
+                if (deg >= 4) {
+                    const real fTmp0D = z * (K(-4.683325804901025) * z2 + K(2.007139630671868));
+                    const real fTmp1C = K(3.31161143515146) * z2 - K(0.47308734787878);
+                    const real fTmp2B = K(-1.770130769779931) * z;
+                    const real fC3 = x * fC2 - y * fS2, fS3 = x * fS2 + y * fC2;
+                    const real p20 = K(1.984313483298443) * z * p12 - K(1.006230589874905) * p6;
+                    const real p21 = fTmp0D * x, p19 = fTmp0D * y;
+                    const real p22 = fTmp1C * fC1, p18 = fTmp1C * fS1;
+                    const real p23 = fTmp2B * fC2, p17 = fTmp2B * fS2;
+                    const real p24 = K(0.6258357354491763) * fC3, p16 = K(0.6258357354491763) * fS3;
+                    result += p16 * c[16 * bo] + p17 * c[17 * bo] + p18 * c[18 * bo] + p19 * c[19 * bo] +
+                              p20 * c[20 * bo] + p21 * c[21 * bo] + p22 * c[22 * bo] + p23 * c[23 * bo] +
+                              p24 * c[24 * bo];
+                }
+            }
+        }
+    }
+    return result;
+}
+
+static inline int mask_bit(const uint32_t *mask, long idx) {
+    return mask ? ((mask[idx / 32] & (1u << (idx % 32))) != 0) : 1;
+}
+
+/* spherical_harmonics_fused_fwd: sh_fwd.cu:119-245. out must be zero-initialised by the caller
+ * (masked Gaussians keep the caller's values, sh_fwd.cu:136, 212). */
+void orc_sh_fwd(int deg, const real *origin, int n, int dim, const real *pos, const real *coeffs,
+                const real *dc, const uint32_t *mask, int layout_3kn, real *out) {
+    const v3 o = ld3(origin);
+#pragma omp parallel for schedule(static)
+    for (long i = 0; i < n; ++i) {
+        if (!mask_bit(mask, i)) continue;
+        const v3 dir = normalize3(sub3(ld3(pos + 3 * i), o));
+        for (int ch = 0; ch < 3; ++ch) {
+            if (layout_3kn) {
+                const real *cf = coeffs + (long)ch * n * dim + i;
+                const real *dcp = dc ? dc + (long)ch * n + i : NULL;
+                out[3 * i + ch] = sh_eval(deg, dir, cf, dcp, n) + K(0.5);
+            } else {
+                const real *cf = coeffs + i * dim * 3 + ch;
+                const real *dcp = dc ? dc + i * 3 + ch : NULL;
+                out[3 * i + ch] = sh_eval(deg, dir, cf, dcp, 3) + K(0.5);
+            }
+        }
+    }
+}
+
+static void sh_eval_bwd(int deg, v3 dir, const real *cf, long bo, real d_out, real *dcf, real *ddc,
+                        v3 *d_dir) {
+    /* sh_bwd.cu:20-247 */
+    const real *c; real *dc;
+    if (ddc) { ddc[0] = K(0.2820947917738781) * d_out; c = cf - bo; dc = dcf - bo; }
+    else { dcf[0] = K(0.2820947917738781) * d_out; c = cf; dc = dcf; }
+    if (deg < 1) return;
+    const real x = dir.x, y = dir.y, z = dir.z;
+    dc[bo] = K(-0.48860251190292) * y * d_out;
+    dc[2 * bo] = K(0.48860251190292) * z * d_out;
+    dc[3 * bo] = K(-0.48860251190292) * x * d_out;
+    d_dir->x += K(-0.48860251190292) * c[3 * bo] * d_out;
+    d_dir->y += K(-0.48860251190292) * c[1 * bo] * d_out;
+    d_dir->z += K(0.48860251190292) * c[2 * bo] * d_out;
+    if (deg < 2) return;
+    const real z2 = z * z;
+    const real fTmp0B = K(-1.092548430592079) * z;
+    const real fC1 = x * x - y * y, fS1 = K(2) * x * y;
+    const real p6 = K(0.9461746957575601) * z2 - K(0.3153915652525201);
+    const real p7 = fTmp0B * x, p5 = fTmp0B * y;
+    const real p8 = K(0.5462742152960395) * fC1, p4 = K(0.5462742152960395) * fS1;
+    dc[4 * bo] = p4 * d_out; dc[5 * bo] = p5 * d_out; dc[6 * bo] = p6 * d_out;
+    dc[7 * bo] = p7 * d_out; dc[8 * bo] = p8 * d_out;
+    const real fTmp0B_z = K(-1.092548430592079);
+    const real fC1_x = K(2) * x, fC1_y = K(-2) * y, fS1_x = K(2) * y, fS1_y = K(2) * x;
+    const real p6_z = K(2) * K(0.9461746957575601) * z;
+    const real p7_x = fTmp0B, p7_z = fTmp0B_z * x, p5_y = fTmp0B, p5_z = fTmp0B_z * y;
+    const real p8_x = K(0.5462742152960395) * fC1_x, p8_y = K(0.5462742152960395) * fC1_y;
+    const real p4_x = K(0.5462742152960395) * fS1_x, p4_y = K(0.5462742152960395) * fS1_y;
+    d_dir->x += d_out * (p4_x * c[4 * bo] + p8_x * c[8 * bo] + p7_x * c[7 * bo]);
+    d_dir->y += d_out * (p4_y * c[4 * bo] + p8_y * c[8 * bo] + p5_y * c[5 * bo]);
+    d_dir->z += d_out * (p6_z * c[6 * bo] + p7_z * c[7 * bo] + p5_z * c[5 * bo]);
+    if (deg < 3) return;
+    const real fTmp0C = K(-2.285228997322329) * z2 + K(0.4570457994644658);
+    const real fTmp1B = K(1.445305721320277) * z;
+    const real fC2 = x * fC1 - y * fS1, fS2 = x * fS1 + y * fC1;
+    const real p12 = z * (K(1.865881662950577) * z2 - K(1.119528997770346));
+    const real p13 = fTmp0C * x, p11 = fTmp0C * y;
+    const real p14 = fTmp1B * fC1, p10 = fTmp1B * fS1;
+    const real p15 = K(-0.5900435899266435) * fC2, p9 = K(-0.5900435899266435) * fS2;
+    dc[9 * bo] = p9 * d_out; dc[10 * bo] = p10 * d_out; dc[11 * bo] = p11 * d_out;
+    dc[12 * bo] = p12 * d_out; dc[13 * bo] = p13 * d_out; dc[14 * bo] = p14 * d_out;
+    dc[15 * bo] = p15 * d_out;
+    const real fTmp0C_z = K(-2.285228997322329) * K(2) * z;
+    const real fTmp1B_z = K(1.445305721320277);
+    const real fC2_x = fC1 + x * fC1_x - y * fS1_x;
+    const real fC2_y = x * fC1_y - fS1 - y * fS1_y;
+    const real fS2_x = fS1 + x * fS1_x + y * fC1_x;
+    const real fS2_y = x * fS1_y + fC1 + y * fC1_y;
+    const real p12_z = K(3) * K(1.865881662950577) * z2 - K(1.119528997770346);
+    const real p13_x = fTmp0C, p13_z = fTmp0C_z * x, p11_y = fTmp0C, p11_z = fTmp0C_z * y;
+    const real p14_x = fTmp1B * fC1_x, p14_y = fTmp1B * fC1_y, p14_z = fTmp1B_z * fC1;
+    const real p10_x = fTmp1B * fS1_x, p10_y = fTmp1B * fS1_y, p10_z = fTmp1B_z * fS1;
+    const real p15_x = K(-0.5900435899266435) * fC2_x, p15_y = K(-0.5900435899266435) * fC2_y;
+    const real p9_x = K(-0.5900435899266435) * fS2_x, p9_y = K(-0.5900435899266435) * fS2_y;
+    d_dir->x += d_out * (p9_x * c[9 * bo] + p15_x * c[15 * bo] + p10_x * c[10 * bo] +
+                         p14_x * c[14 * bo] + p13_x * c[13 * bo]);
+    d_dir->y += d_out * (p9_y * c[9 * bo] + p15_y * c[15 * bo] + p10_y * c[10 * bo] +
+                         p14_y * c[14 * bo] + p11_y * c[11 * bo]);
+    d_dir->z += d_out * (p12_z * c[12 * bo] + p13_z * c[13 * bo] + p11_z * c[11 * bo] +
+                         p14_z * c[14 * bo] + p10_z * c[10 * bo]);
+    if (deg < 4) return;
+    const real fTmp0D = z * (K(-4.683325804901025) * z2 + K(2.007139630671868));
+    const real fTmp1C = K(3.31161143515146) * z2 - K(0.47308734787878);
+    const real fTmp2B = K(-1.770130769779931) * z;
+    const real fC3 = x * fC2 - y * fS2, fS3 = x * fS2 + y * fC2;
+    const real p20 = K(1.984313483298443) * z * p12 + K(-1.006230589874905) * p6;
+    const real p21 = fTmp0D * x, p19 = fTmp0D * y;
+    const real p22 = fTmp1C * fC1, p18 = fTmp1C * fS1;
+    const real p23 = fTmp2B * fC2, p17 = fTmp2B * fS2;
+    const real p24 = K(0.6258357354491763) * fC3, p16 = K(0.6258357354491763) * fS3;
+    dc[16 * bo] = p16 * d_out; dc[17 * bo] = p17 * d_out; dc[18 * bo] = p18 * d_out;
+    dc[19 * bo] = p19 * d_out; dc[20 * bo] = p20 * d_out; dc[21 * bo] = p21 * d_out;
+    dc[22 * bo] = p22 * d_out; dc[23 * bo] = p23 * d_out; dc[24 * bo] = p24 * d_out;
+    const real fTmp0D_z = K(3) * K(-4.683325804901025) * z2 + K(2.007139630671868);
+    const real fTmp1C_z = K(2) * K(3.31161143515146) * z;
+    const real fTmp2B_z = K(-1.770130769779931);
+    const real fC3_x = fC2 + x * fC2_x - y * fS2_x;
+    const real fC3_y = x * fC2_y - fS2 - y * fS2_y;
+    const real fS3_x = fS2 + y * fC2_x + x * fS2_x;
+    const real fS3_y = x * fS2_y + fC2 + y * fC2_y;
+    const real p20_z = K(1.984313483298443) * (p12 + z * p12_z) + K(-1.006230589874905) * p6_z;
+    const real p21_x = fTmp0D, p21_z = fTmp0D_z * x, p19_y = fTmp0D, p19_z = fTmp0D_z * y;
+    const real p22_x = fTmp1C * fC1_x, p22_y = fTmp1C * fC1_y, p22_z = fTmp1C_z * fC1;
+    const real p18_x = fTmp1C * fS1_x, p18_y = fTmp1C * fS1_y, p18_z = fTmp1C_z * fS1;
+    const real p23_x = fTmp2B * fC2_x, p23_y = fTmp2B * fC2_y, p23_z = fTmp2B_z * fC2;
+    const real p17_x = fTmp2B * fS2_x, p17_y = fTmp2B * fS2_y, p17_z = fTmp2B_z * fS2;
+    const real p24_x = K(0.6258357354491763) * fC3_x, p24_y = K(0.6258357354491763) * fC3_y;
+    const real p16_x = K(0.6258357354491763) * fS3_x, p16_y = K(0.6258357354491763) * fS3_y;
+    d_dir->x += d_out * (p16_x * c[16 * bo] + p24_x * c[24 * bo] + p17_x * c[17 * bo] +
+                         p23_x * c[23 * bo] + p18_x * c[18 * bo] + p22_x * c[22 * bo] +
+                         p21_x * c[21 * bo]);
+    d_dir->y += d_out * (p16_y * c[16 * bo] + p24_y * c[24 * bo] + p17_y * c[17 * bo] +
+                         p23_y * c[23 * bo] + p18_y * c[18 * bo] + p22_y * c[22 * bo] +
+                         p19_y * c[19 * bo]);
+    d_dir->z += d_out * (p20_z * c[20 * bo] + p21_z * c[21 * bo] + p19_z * c[19 * bo] +
+                         p22_z * c[22 * bo] + p18_z * c[18 * bo] + p23_z * c[23 * bo] +
+                         p17_z * c[17 * bo]);
+}
+
+/* spherical_harmonics_fused_bwd: sh_bwd.cu:250-376. Outputs must be zero-initialised.
+ * d_origin[3] = -sum of d_positions (sh_bwd.cu:306, 375). */
+void orc_sh_bwd(int deg, const real *origin, int n, int dim, const real *pos, const real *coeffs,
+                const uint32_t *mask, int layout_3kn, const real *d_output, int has_dc,
+                real *d_coeffs, real *d_dc, real *d_pos, real *d_origin) {
+    const v3 o = ld3(origin);
+    double so[3] = {0, 0, 0};
+    for (long i = 0; i < n; ++i) {
+        if (!mask_bit(mask, i)) continue;
+        const v3 diff = sub3(ld3(pos + 3 * i), o);
+        const v3 dir = normalize3(diff);
+        v3 dsum = V3(0, 0, 0);
+        for (int ch = 0; ch < 3; ++ch) {
+            const real d_out = d_output[3 * i + ch];
+            v3 ddir = V3(0, 0, 0);
+            if (layout_3kn) {
+                sh_eval_bwd(deg, dir, coeffs + (long)ch * n * dim + i, n, d_out,
+                            d_coeffs + (long)ch * n * dim + i, has_dc ? d_dc + (long)ch * n + i : NULL,
+                            &ddir);
+            } else {
+                sh_eval_bwd(deg, dir, coeffs + i * dim * 3 + ch, 3, d_out, d_coeffs + i * dim * 3 + ch,
+                            has_dc ? d_dc + i * 3 + ch : NULL, &ddir);
+            }
+            /* normalize_bwd (toast): d_v = (d_n - (d_n . n) n) / |v| */
+            const real il = K(1.0) / SQRT(dot3(diff, diff));
+            const real il3 = il * il * il;
+            const v3 dd = sub3(scl3(ddir, il), scl3(diff, il3 * dot3(ddir, diff)));
+            dsum = add3(dsum, dd);
+        }
+        d_pos[3 * i] += dsum.x; d_pos[3 * i + 1] += dsum.y; d_pos[3 * i + 2] += dsum.z;
+        so[0] -= dsum.x; so[1] -= dsum.y; so[2] -= dsum.z;
+    }
+    d_origin[0] = (real)so[0]; d_origin[1] = (real)so[1]; d_origin[2] = (real)so[2];
+}
+
+/* ------------------------------------------------------------------------- */
+/* Tile binning                                                              */
+/* ------------------------------------------------------------------------- */
+static inline int imin(int a, int b) { return a < b ? a : b; }
+static inline int imax(int a, int b) { return a > b ? a : b; }
+
+static void regular_rect(const float *means2d, const float *radii, long i, float tsx, float tsy,
+                         int ntx, int nty, int *tmin_x, int *tmin_y, int *tmax_x, int *tmax_y) {
+    /* regular_tiling.cu:41-56: float32 division by tile size, floor/ceil, clamp to [0, n] */
+    const float mx = means2d[2 * i] / tsx, my = means2d[2 * i + 1] / tsy;
+    const float rx = radii[2 * i] / tsx, ry = radii[2 * i + 1] / tsy;
+    *tmin_x = imin(ntx, imax(0, (int)floorf(mx - rx)));
+    *tmin_y = imin(nty, imax(0, (int)floorf(my - ry)));
+    *tmax_x = imin(ntx, imax(0, (int)ceilf(mx + rx)));
+    *tmax_y = imin(nty, imax(0, (int)ceilf(my + ry)));
+}
+
+/* isect_tiles_kernel<true>: regular_tiling.cu:13-69 (count pass). Binning is always float32,
+ * whatever REAL is, because it must be bit-exact with the reference. */
+void orc_isect_regular_count(int n, const float *means2d, const float *radii, int width, int height,
+                             int tsx, int tsy, int32_t *tiles_per_gauss) {
+    const int ntx = (width + tsx - 1) / tsx, nty = (height + tsy - 1) / tsy;
+    for (long i = 0; i < n; ++i) {
+        if (radii[2 * i] <= 0 || radii[2 * i + 1] <= 0) { tiles_per_gauss[i] = 0; continue; }
+        int a, b, c, d;
+        regular_rect(means2d, radii, i, (float)tsx, (float)tsy, ntx, nty, &a, &b, &c, &d);
+        tiles_per_gauss[i] = (d - b) * (c - a);
+    }
+}
+
+static inline int64_t make_key(int64_t tile_id, float depth) {
+    int32_t bits; memcpy(&bits, &depth, 4);
+    return (tile_id << 32) | (int64_t)bits;   /* tiling_common.cuh:37, 62, 68: sign-extended */
+}
+
+/* isect_tiles_kernel<false> + fill_tiles_exclusive: regular_tiling.cu:58-64, tiling_common.cuh:50-73 */
+void orc_isect_regular_fill(int n, const float *means2d, const float *radii, const float *depths,
+                            int width, int height, int tsx, int tsy, const int64_t *cum,
+                            int64_t *isect_ids, int32_t *flatten_ids) {
+    const int ntx = (width + tsx - 1) / tsx, nty = (height + tsy - 1) / tsy;
+    for (long i = 0; i < n; ++i) {
+        if (radii[2 * i] <= 0 || radii[2 * i + 1] <= 0) continue;
+        int a, b, c, d;
+        regular_rect(means2d, radii, i, (float)tsx, (float)tsy, ntx, nty, &a, &b, &c, &d);
+        if ((d - b) * (c - a) <= 0) continue;
+        int64_t off = i > 0 ? cum[i - 1] : 0;
+        for (int y = b; y < d; ++y)
+            for (int x = a; x < c; ++x) {
+                isect_ids[off] = make_key((int64_t)y * ntx + x, depths[i]);
+                flatten_ids[off] = (int32_t)i;
+                ++off;
+            }
+    }
+}
+
+/* phm_lidar_tiling.cu:16-91 */
+static void find_bounds_increasing(float vmin, float vmax, int n, const float *values, int *tmin, int *tmax) {
+    int i = 0;
+    while (i < n && values[i] < vmin) ++i;
+    *tmin = imin(imax(i - 1, 0), n - 1);
+    while (i < n && values[i] < vmax) ++i;
+    *tmax = imin(imax(i - 1, 0), n - 1);
+}
+
+static void tile_limits_irregular(float mx, float my, float rx, float ry, float u_min, float u_max,
+                                  float u_per_tile, int n_elev, const float *elev, int *tmin_x,
+                                  int *tmin_y, int *tmax_x, int *tmax_y, int *num) {
+    *tmin_x = 0; *tmin_y = 0; *tmax_x = -1; *tmax_y = -1;
+    const float lo = fmaxf(mx - rx, u_min), hi = fminf(mx + rx, u_max);
+    if (hi <= lo) return;
+    *tmin_x = (int)floorf(lo / u_per_tile);
+    *tmax_x = (int)ceilf(hi / u_per_tile) - 1;
+    find_bounds_increasing(my - ry, my + ry, n_elev, elev, tmin_y, tmax_y);
+    *num += (*tmax_y - *tmin_y + 1) * (*tmax_x - *tmin_x + 1);
+}
+
+/* phm_spherical_tiling.cu:15-45 */
+static void tile_limits_regular(float mx, float my, float rx, float ry, float u_min, float u_max,
+                                float u_per_tile, int n_v, float v_per_tile, int *tmin_x, int *tmin_y,
+                                int *tmax_x, int *tmax_y, int *num) {
+    *tmin_x = 0; *tmin_y = 0; *tmax_x = 0; *tmax_y = 0;
+    const float lo = fmaxf(mx - rx, u_min), hi = fminf(mx + rx, u_max);
+    if (hi <= lo) return;
+    *tmin_x = (int)floorf(lo / u_per_tile);
+    *tmin_y = imin(n_v, imax(0, (int)floorf((my - ry) / v_per_tile)));
+    *tmax_x = (int)ceilf(hi / u_per_tile);
+    *tmax_y = imin(n_v, imax(0, (int)ceilf((my + ry) / v_per_tile)));
+    *num += (*tmax_y - *tmin_y) * (*tmax_x - *tmin_x);
+}
+
+/* The float32 camera for the seam re-projection inside the lidar/spherical binning. */
+typedef struct {
+    orc_camera cam;
+    float ut[4];
+} orc_bin_ctx;
+
+/* isect_lidar_tiles_kernel (phm_lidar_tiling.cu:96-234) and isect_spherical_tiles_kernel
+ * (phm_spherical_tiling.cu:47-174). kind: 0 = lidar (irregular v grid, inclusive),
+ * 1 = spherical (regular grid, exclusive). cum == NULL selects the count pass. */
+void orc_isect_spherical_family(int kind, const orc_camera *cam, const real *ut, int n,
+                                const real *points, const real *vel, const real *scale,
+                                const real *quat, const real *opacity, const uint8_t *flags,
+                                const float *means2d, const float *radii, const float *depths,
+                                const float *elev, int n_elev, int tsx, int tsy, float img_w,
+                                float img_h, const int64_t *cum, int32_t *tiles_per_gauss,
+                                int64_t *isect_ids, int32_t *flatten_ids) {
+    const int lidar = kind == 0;
+    int n_az, n_el;
+    float u_per_tile, v_per_tile = 0;
+    if (lidar) {
+        n_az = ((int)img_w + tsx - 1) / tsx;
+        n_el = n_elev;
+        u_per_tile = (float)tsx / img_w;
+    } else {
+        n_az = (int)ceilf(img_w / (float)tsx);
+        n_el = (int)ceilf(img_h / (float)tsy);
+        u_per_tile = (float)tsx / img_w;
+        v_per_tile = (float)tsy / img_h;
+    }
+    const v2 img = {img_w, img_h};
+    for (long i = 0; i < n; ++i) {
+        const int first = cum == NULL;
+        float rx = radii[2 * i], ry = radii[2 * i + 1];
+        const int flag = flags[i];
+        if (rx <= 0 || ry <= 0 || flag == 0) { if (first) tiles_per_gauss[i] = 0; continue; }
+        int a, b, c, d, num = 0;
+        int64_t off = 0;
+        float u_min = 0.0f, u_max = 1.0f;
+        const float u_pose = (float)u_pose_of(cam);
+        if (flag == 2) { if (cam->rolling[0] > 0) u_max = u_pose; else u_min = u_pose; }
+        float mx = means2d[2 * i] / img_w, my = means2d[2 * i + 1] / img_h;
+        rx /= img_w; ry /= img_h;
+        if (lidar) tile_limits_irregular(mx, my, rx, ry, u_min, u_max, u_per_tile, n_el, elev, &a, &b, &c, &d, &num);
+        else tile_limits_regular(mx, my, rx, ry, u_min, u_max, u_per_tile, n_el, v_per_tile, &a, &b, &c, &d, &num);
+        if (!first) {
+            off = i > 0 ? cum[i - 1] : 0;
+            const int ye = lidar ? d + 1 : d, xe = lidar ? c + 1 : c;
+            for (int y = b; y < ye; ++y)
+                for (int x = a; x < xe; ++x) {
+                    isect_ids[off] = make_key((int64_t)y * n_az + x, depths[i]);
+                    flatten_ids[off] = (int32_t)i;
+                    ++off;
+                }
+        }
+        if (flag == 2) {
+            v3 dl[3];
+            ut_deltas(ut[3], quat + 4 * i, scale + 3 * i, dl);
+            const real op = opacity ? opacity[i] : K(1.0);
+            v2 m2, r2; real depth = 0, udist = 0;
+            const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
+            const int ok = ut_projection(cam, ORC_MODE_POS, ut, img, K(1e-4), K(0.002), K(1.0),
+                                         ld3(points + 3 * i), pv, op, dl, &m2, &r2, &depth, &udist);
+            if (ok) {
+                if (cam->rolling[0] > 0) {
+                    u_min = ceilf(u_pose / u_per_tile) * u_per_tile + 1e-6f;
+                    u_max = 1.0f;
+                } else {
+                    u_min = 0.0f;
+                    u_max = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f;
+                }
+                const float m2x = (float)m2.x / img_w, m2y = (float)m2.y / img_h;
+                const float r2x = (float)r2.x / img_w, r2y = (float)r2.y / img_h;
+                if (lidar) tile_limits_irregular(m2x, m2y, r2x, r2y, u_min, u_max, u_per_tile, n_el, elev, &a, &b, &c, &d, &num);
+                else tile_limits_regular(m2x, m2y, r2x, r2y, u_min, u_max, u_per_tile, n_el, v_per_tile, &a, &b, &c, &d, &num);
+                if (!first) {
+                    const int ye = lidar ? d + 1 : d, xe = lidar ? c + 1 : c;
+                    for (int y = b; y < ye; ++y)
+                        for (int x = a; x < xe; ++x) {
+                            isect_ids[off] = make_key((int64_t)y * n_az + x, (float)depth);
+                            flatten_ids[off] = (int32_t)i;
+                            ++off;
+                        }
+                }
+            }
+        }
+        if (first) tiles_per_gauss[i] = num;
+    }
+}
+
+/* Stable sort of (key, value) pairs by key bits [0, end_bit) -- cub::DeviceRadixSort::SortPairs
+ * semantics as used by sort_intersections (tiling_common.cu:102-162). LSD radix, 8-bit digits. */
+void orc_sort_pairs(int64_t n, int64_t *keys, int32_t *vals, int end_bit) {
+    if (n <= 0) return;
+    int64_t *k2 = (int64_t *)malloc(sizeof(int64_t) * n);
+    int32_t *v2b = (int32_t *)malloc(sizeof(int32_t) * n);
+    int64_t *ks = keys, *kd = k2; int32_t *vs = vals, *vd = v2b;
+    const uint64_t mask = end_bit >= 64 ? ~0ull : ((1ull << end_bit) - 1);
+    for (int shift = 0; shift < end_bit; shift += 8) {
+        int64_t count[257];
+        memset(count, 0, sizeof(count));
+        for (int64_t i = 0; i < n; ++i) count[(((uint64_t)ks[i] & mask) >> shift & 255) + 1]++;
+        for (int b = 0; b < 256; ++b) count[b + 1] += count[b];
+        for (int64_t i = 0; i < n; ++i) {
+            const int dg = (int)((((uint64_t)ks[i] & mask) >> shift) & 255);
+            const int64_t p = count[dg]++;
+            kd[p] = ks[i]; vd[p] = vs[i];
+        }
+        int64_t *tk = ks; ks = kd; kd = tk;
+        int32_t *tv = vs; vs = vd; vd = tv;
+    }
+    if (ks != keys) { memcpy(keys, ks, sizeof(int64_t) * n); memcpy(vals, vs, sizeof(int32_t) * n); }
+    free(k2); free(v2b);
+}
+
+/* isect_offset_encode_kernel: tiling_common.cu:25-99 (camera id above tile_n_bits, :41-44). */
+void orc_offset_encode(int64_t n, const int64_t *isect_ids, int n_tiles, int n_cams, int32_t *offsets) {
+    const int total = n_tiles * n_cams;
+    if (n == 0) { for (int i = 0; i < total; ++i) offsets[i] = 0; return; }
+    const uint32_t tile_n_bits = (uint32_t)floorf(log2f((float)n_tiles)) + 1;
+    for (int64_t idx = 0; idx < n; ++idx) {
+        const int64_t cur = isect_ids[idx] >> 32;
+        const int64_t id_cur = (cur >> tile_n_bits) * n_tiles + (cur & ((1 << tile_n_bits) - 1));
+        if (idx == 0) for (int64_t i = 0; i < id_cur + 1; ++i) offsets[i] = 0;
+        if (idx == n - 1) for (int64_t i = id_cur + 1; i < total; ++i) offsets[i] = (int32_t)n;
+        if (idx > 0) {
+            const int64_t prev = isect_ids[idx - 1] >> 32;
+            if (prev == cur) continue;
+            const int64_t id_prev = (prev >> tile_n_bits) * n_tiles + (prev & ((1 << tile_n_bits) - 1));
+            for (int64_t i = id_prev + 1; i < id_cur + 1; ++i) offsets[i] = (int32_t)idx;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* eval3d compositing: csrc/rasterization/eval3d_fwd.cu, eval3d_bwd.cu, utils.h */
+/* ------------------------------------------------------------------------- */
+static m3 quat_to_rotmat(const real *q) { /* utils.h:61-83 */
+    real w = q[0], x = q[1], y = q[2], z = q[3];
+    const real inv = K(1.0) / SQRT(x * x + y * y + z * z + w * w);
+    x *= inv; y *= inv; z *= inv; w *= inv;
+    const real x2 = x * x, y2 = y * y, z2 = z * z, xy = x * y, xz = x * z, yz = y * z;
+    const real wx = w * x, wy = w * y, wz = w * z;
+    m3 R;
+    R.m[0][0] = K(1) - K(2) * (y2 + z2); R.m[0][1] = K(2) * (xy + wz); R.m[0][2] = K(2) * (xz - wy);
+    R.m[1][0] = K(2) * (xy - wz); R.m[1][1] = K(1) - K(2) * (x2 + z2); R.m[1][2] = K(2) * (yz + wx);
+    R.m[2][0] = K(2) * (xz + wy); R.m[2][1] = K(2) * (yz - wx); R.m[2][2] = K(1) - K(2) * (x2 + y2);
+    return R;
+}
+
+/* iscl_rot = S^-1 R^T, glm m[col][row]: m[c][r] = R[r][c] / s_r (eval3d_fwd.cu:92-107) */
+static m3 iscl_rot_of(const m3 *R, const real *s) {
+    m3 M;
+    for (int c = 0; c < 3; ++c)
+        for (int r = 0; r < 3; ++r) M.m[c][r] = (K(1.0) / s[r]) * R->m[r][c];
+    return M;
+}
+
+static v3 safe_normalize(v3 v) { /* utils.h:85-88 */
+    const real l = dot3(v, v);
+    return l > 0 ? scl3(v, K(1.0) / SQRT(l)) : v;
+}
+
+typedef struct {
+    int width, height, tile_w, tile_h, n_tiles_w, n_tiles_h;
+    int64_t n_isects;
+} orc_grid;
+
+static void tile_range(const orc_grid *g, const int32_t *offsets, int tile, int64_t *start, int64_t *end) {
+    /* utils.h:48-58 */
+    *start = offsets[tile];
+    *end = (tile == g->n_tiles_w * g->n_tiles_h - 1) ? g->n_isects : offsets[tile + 1];
+}
+
+/* rasterize_eval3d_fwd_kernel: eval3d_fwd.cu:34-166 (+ dynamic eval3d_dynamic_fwd.cu:125 when
+ * velocity != NULL: mean(t) = mean + dt_pixel * velocity). counters[0] += evaluated pairs,
+ * counters[1] += contributing pairs. */
+void orc_eval3d_fwd(int cdim, int n, const real *means, const real *quats, const real *scales,
+                    const real *colors, const real *opac, const real *velocity,
+                    const real *ray_time_delta, int width, int height, int tile_w, int tile_h,
+                    const real *ray_o, const real *ray_d, const int32_t *offsets, int n_tiles_w,
+                    int n_tiles_h, int64_t n_isects, const int32_t *flatten_ids, real *out_rgb,
+                    real *out_depth, real *out_alpha, int32_t *last_ids, int64_t *counters) {
+    (void)n;
+    const orc_grid g = {width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_isects};
+    const int n_tiles = n_tiles_w * n_tiles_h;
+    int64_t evaluated = 0, contributing = 0;
+#pragma omp parallel for schedule(dynamic, 4) reduction(+ : evaluated, contributing)
+    for (int tile = 0; tile < n_tiles; ++tile) {
+        const int ty = tile / n_tiles_w, tx = tile % n_tiles_w;
+        int64_t rs, re;
+        tile_range(&g, offsets, tile, &rs, &re);
+        const int64_t cnt = re > rs ? re - rs : 0;
+        m3 *Ms = (m3 *)malloc(sizeof(m3) * (cnt ? cnt : 1));
+        for (int64_t k = 0; k < cnt; ++k) {
+            const int32_t gid = flatten_ids[rs + k];
+            m3 R = quat_to_rotmat(quats + 4 * gid);
+            Ms[k] = iscl_rot_of(&R, scales + 3 * gid);
+        }
+        real *pix = (real *)malloc(sizeof(real) * (cdim > 0 ? cdim : 1));
+        for (int yy = 0; yy < tile_h; ++yy)
+            for (int xx = 0; xx < tile_w; ++xx) {
+                const int i = ty * tile_h + yy, j = tx * tile_w + xx;
+                if (!(i < height && j < width)) continue;
+                const long pid = (long)i * width + j;
+                const v3 ro = ld3(ray_o + 3 * pid), rd = ld3(ray_d + 3 * pid);
+                const real dtp = ray_time_delta ? ray_time_delta[pid] : K(0);
+                real T = K(1.0), depth = K(0);
+                int32_t cur = 0;
+                for (int k = 0; k < cdim; ++k) pix[k] = 0;
+                for (int64_t k = 0; k < cnt; ++k) {
+                    const int32_t gid = flatten_ids[rs + k];
+                    v3 xyz = ld3(means + 3 * gid);
+                    if (velocity) xyz = add3(xyz, scl3(ld3(velocity + 3 * gid), dtp));
+                    const v3 gro = mv(&Ms[k], sub3(ro, xyz));
+                    const v3 grd = mv(&Ms[k], rd);
+                    const v3 gcrod = cross3(safe_normalize(grd), gro);
+                    const real power = K(-0.5) * dot3(gcrod, gcrod);
+                    const real alpha = FMIN(K(0.999), opac[gid] * EXP(power));
+                    ++evaluated;
+                    if (alpha < K(1.0) / K(255.0)) continue;
+                    const real hit_t = -dot3(gro, grd) / dot3(grd, grd);
+                    const real next_T = T * (K(1.0) - alpha);
+                    if (next_T <= K(1e-4)) break;
+                    const real vis = alpha * T;
+                    depth += vis * hit_t;
+                    for (int c = 0; c < cdim; ++c) pix[c] += colors[(long)gid * cdim + c] * vis;
+                    cur = (int32_t)(rs + k);
+                    T = next_T;
+                    ++contributing;
+                }
+                out_alpha[pid] = K(1.0) - T;
+                out_depth[pid] = depth;
+                for (int c = 0; c < cdim; ++c) out_rgb[pid * cdim + c] = pix[c];
+                last_ids[pid] = cur;
+            }
+        free(pix);
+        free(Ms);
+    }
+    if (counters) { counters[0] += evaluated; counters[1] += contributing; }
+}
+
+static void quat_to_rotmat_vjp(const real *quat, const m3 *v_R, real *v_quat) {
+    /* utils.h:208-230, v_R glm-indexed [col][row] */
+    real w = quat[0], x = quat[1], y = quat[2], z = quat[3];
+    const real inv = K(1.0) / SQRT(x * x + y * y + z * z + w * w);
+    x *= inv; y *= inv; z *= inv; w *= inv;
+    const real (*V)[3] = v_R->m;
+    real vqn[4];
+    vqn[0] = K(2) * (x * (V[1][2] - V[2][1]) + y * (V[2][0] - V[0][2]) + z * (V[0][1] - V[1][0]));
+    vqn[1] = K(2) * (K(-2) * x * (V[1][1] + V[2][2]) + y * (V[0][1] + V[1][0]) + z * (V[0][2] + V[2][0]) +
+                     w * (V[1][2] - V[2][1]));
+    vqn[2] = K(2) * (x * (V[0][1] + V[1][0]) - K(2) * y * (V[0][0] + V[2][2]) + z * (V[1][2] + V[2][1]) +
+                     w * (V[2][0] - V[0][2]));
+    vqn[3] = K(2) * (x * (V[0][2] + V[2][0]) + y * (V[1][2] + V[2][1]) - K(2) * z * (V[0][0] + V[1][1]) +
+                     w * (V[0][1] - V[1][0]));
+    const real qn[4] = {w, x, y, z};
+    const real dp = vqn[0] * qn[0] + vqn[1] * qn[1] + vqn[2] * qn[2] + vqn[3] * qn[3];
+    for (int k = 0; k < 4; ++k) v_quat[k] += (vqn[k] - dp * qn[k]) * inv;
+}
+
+static void quat_scale_to_preci_half_vjp(const real *quat, const real *scale, const m3 *R,
+                                         const m3 *v_M, real *v_quat, real *v_scale) {
+    /* utils.h:232-263: M = R S, S = diag(1/scale) */
+    const real s[3] = {K(1.0) / scale[0], K(1.0) / scale[1], K(1.0) / scale[2]};
+    m3 v_R;
+    for (int c = 0; c < 3; ++c)
+        for (int r = 0; r < 3; ++r) v_R.m[c][r] = v_M->m[c][r] * s[c];
+    quat_to_rotmat_vjp(quat, &v_R, v_quat);
+    for (int c = 0; c < 3; ++c)
+        v_scale[c] += -s[c] * s[c] *
+                      (R->m[c][0] * v_M->m[c][0] + R->m[c][1] * v_M->m[c][1] + R->m[c][2] * v_M->m[c][2]);
+}
+
+#ifdef _OPENMP
+#define ATOMIC_ADD(p, v) do { _Pragma("omp atomic") *(p) += (v); } while (0)
+#else
+#define ATOMIC_ADD(p, v) (*(p) += (v))
+#endif
+
+/* rasterize_eval3d_bwd_kernel: eval3d_bwd.cu:42-294 (dynamic: eval3d_dynamic_bwd.cu adds
+ * v_velocity = -v_(o-mu) * dt and v_dt = -v_(o-mu) . velocity). Gradient outputs must be
+ * zero-initialised; v_ray_o / v_ray_d are written for every pixel inside the image. */
+void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *scales,
+                    const real *colors, const real *opac, const real *velocity,
+                    const real *ray_time_delta, int width, int height, int tile_w, int tile_h,
+                    const real *ray_o, const real *ray_d, const int32_t *offsets, int n_tiles_w,
+                    int n_tiles_h, int64_t n_isects, const int32_t *flatten_ids,
+                    const real *render_alpha, const int32_t *last_ids, const real *v_rgb,
+                    const real *v_depth, const real *v_alpha, real *v_means, real *v_quats,
+                    real *v_scales, real *v_opac, real *v_colors, real *v_ray_o, real *v_ray_d,
+                    real *v_velocity, real *v_time_delta) {
+    const orc_grid g = {width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_isects};
+    const int n_tiles = n_tiles_w * n_tiles_h;
+    const real MAX_ALPHA = K(0.99);
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int tile = 0; tile < n_tiles; ++tile) {
+        const int ty = tile / n_tiles_w, tx = tile % n_tiles_w;
+        int64_t rs, re;
+        tile_range(&g, offsets, tile, &rs, &re);
+        real *buffer = (real *)malloc(sizeof(real) * (cdim > 0 ? cdim : 1));
+        for (int yy = 0; yy < tile_h; ++yy)
+            for (int xx = 0; xx < tile_w; ++xx) {
+                const int i = ty * tile_h + yy, j = tx * tile_w + xx;
+                if (!(i < height && j < width)) continue;
+                const long pid = (long)i * width + j;
+                const v3 ro = ld3(ray_o + 3 * pid), rd = ld3(ray_d + 3 * pid);
+                const real dtp = ray_time_delta ? ray_time_delta[pid] : K(0);
+                const real T_final = K(1.0) - render_alpha[pid];
+                real T = T_final;
+                for (int c = 0; c < cdim; ++c) buffer[c] = 0;
+                const int64_t bin_final = last_ids[pid];
+                const real vd = v_depth[pid], va = v_alpha[pid];
+                const real *vc = v_rgb ? v_rgb + pid * cdim : NULL;
+                v3 v_ro = V3(0, 0, 0), v_rd = V3(0, 0, 0);
+                real depth_buffer = 0, v_dt = 0;
+                for (int64_t idx = re - 1; idx >= rs; --idx) {
+                    if (idx > bin_final) continue;
+                    const int32_t gid = flatten_ids[idx];
+                    const real op = opac[gid];
+                    v3 xyz = ld3(means + 3 * gid);
+                    const v3 vel = velocity ? ld3(velocity + 3 * gid) : V3(0, 0, 0);
+                    if (velocity) xyz = add3(xyz, scl3(vel, dtp));
+                    const real *scale = scales + 3 * gid;
+                    const real *quat = quats + 4 * gid;
+                    const m3 R = quat_to_rotmat(quat);
+                    const m3 Mt = iscl_rot_of(&R, scale);   /* transpose(R * S) */
+                    const v3 omm = sub3(ro, xyz);
+                    const v3 gro = mv(&Mt, omm);
+                    const v3 grd = mv(&Mt, rd);
+                    const v3 grd_n = safe_normalize(grd);
+                    const v3 gcrod = cross3(grd_n, gro);
+                    const real power = K(-0.5) * dot3(gcrod, gcrod);
+                    const real vis = EXP(power);
+                    const real alpha = FMIN(MAX_ALPHA, op * vis);
+                    if (alpha < K(1.0) / K(255.0)) continue;
+                    const real last_hit_T = -dot3(grd, gro) / dot3(grd, grd);
+                    const real ra = K(1.0) / FMAX(K(1e-6), K(1.0) - alpha);
+                    T *= ra;
+                    const real fac = alpha * T;
+                    const real *rgb = colors ? colors + (long)gid * cdim : NULL;
+                    /* grad_alpha: eval3d_bwd.cu:42-63 */
+                    real v_a = 0;
+                    for (int c = 0; c < cdim; ++c) v_a += (rgb[c] * T - buffer[c] * ra) * vc[c];
+                    v_a += (last_hit_T * T - depth_buffer * ra) * vd;
+                    v_a += T_final * ra * va;
+                    for (int c = 0; c < cdim; ++c) ATOMIC_ADD(&v_colors[(long)gid * cdim + c], vc[c] * fac);
+                    const real dd = dot3(grd, grd), od = dot3(gro, grd);
+                    const real dL_dhitT = vd * fac;
+                    v3 v_gro = scl3(scl3(grd, K(-1)), dL_dhitT / dd);
+                    v3 v_grd = scl3(sub3(scl3(grd, K(2.0) * od), scl3(gro, dd)), dL_dhitT / (dd * dd));
+                    if (op * vis <= MAX_ALPHA) {
+                        const real v_vis = op * v_a;
+                        const real v_gd = K(-0.5) * vis * v_vis;
+                        const v3 v_gcrod = scl3(gcrod, K(2.0) * v_gd);
+                        const v3 v_grd_n = scl3(cross3(v_gcrod, gro), K(-1));
+                        v_gro = add3(v_gro, cross3(v_gcrod, grd_n));
+                        { /* safe_normalize_bwd: utils.h:198-206 */
+                            const real l = dot3(grd, grd);
+                            if (l > 0) {
+                                const real il = K(1.0) / SQRT(l), il3 = il * il * il;
+                                v_grd = add3(v_grd, sub3(scl3(v_grd_n, il), scl3(grd, il3 * dot3(v_grd_n, grd))));
+                            } else {
+                                v_grd = add3(v_grd, v_grd_n);
+                            }
+                        }
+                        m3 v_Mt; /* outerProduct(v_grd, rd) + outerProduct(v_gro, omm): [col j][row i] */
+                        const real a3[3] = {v_grd.x, v_grd.y, v_grd.z}, b3[3] = {v_gro.x, v_gro.y, v_gro.z};
+                        const real d3[3] = {rd.x, rd.y, rd.z}, o3[3] = {omm.x, omm.y, omm.z};
+                        for (int cj = 0; cj < 3; ++cj)
+                            for (int ri = 0; ri < 3; ++ri) v_Mt.m[cj][ri] = a3[ri] * d3[cj] + b3[ri] * o3[cj];
+                        const m3 trMt = transpose3(&Mt);
+                        const v3 v_omm = mv(&trMt, v_gro);
+                        ATOMIC_ADD(&v_means[3 * gid], -v_omm.x);
+                        ATOMIC_ADD(&v_means[3 * gid + 1], -v_omm.y);
+                        ATOMIC_ADD(&v_means[3 * gid + 2], -v_omm.z);
+                        if (velocity) {
+                            ATOMIC_ADD(&v_velocity[3 * gid], -v_omm.x * dtp);
+                            ATOMIC_ADD(&v_velocity[3 * gid + 1], -v_omm.y * dtp);
+                            ATOMIC_ADD(&v_velocity[3 * gid + 2], -v_omm.z * dtp);
+                            v_dt += -dot3(v_omm, vel);
+                        }
+                        v_ro = add3(v_ro, v_omm);
+                        v_rd = add3(v_rd, mv(&trMt, v_grd));
+                        const m3 v_M = transpose3(&v_Mt);
+                        real vq[4] = {0, 0, 0, 0}, vs[3] = {0, 0, 0};
+                        quat_scale_to_preci_half_vjp(quat, scale, &R, &v_M, vq, vs);
+                        for (int k = 0; k < 4; ++k) ATOMIC_ADD(&v_quats[4 * gid + k], vq[k]);
+                        for (int k = 0; k < 3; ++k) ATOMIC_ADD(&v_scales[3 * gid + k], vs[k]);
+                        ATOMIC_ADD(&v_opac[gid], vis * v_a);
+                    }
+                    for (int c = 0; c < cdim; ++c) buffer[c] += rgb[c] * fac;
+                    depth_buffer += fac * last_hit_T;
+                }
+                v_ray_o[3 * pid] = v_ro.x; v_ray_o[3 * pid + 1] = v_ro.y; v_ray_o[3 * pid + 2] = v_ro.z;
+                v_ray_d[3 * pid] = v_rd.x; v_ray_d[3 * pid + 1] = v_rd.y; v_ray_d[3 * pid + 2] = v_rd.z;
+                if (v_time_delta) v_time_delta[pid] = v_dt;
+            }
+        free(buffer);
+    }
+}
+
+/* Host-side mask_radii: mask_radii.cu:10-58 (bool and packed uint32 masks). */
+void orc_mask_radii(int n, const uint8_t *mask, const uint32_t *packed, float *radii) {
+    for (int i = 0; i < n; ++i) {
+        const int keep = packed ? ((packed[i / 32] & (1u << (i % 32))) != 0) : (mask[i] != 0);
+        if (!keep) { radii[2 * i] = 0; radii[2 * i + 1] = 0; }
+    }
+}
+
+int orc_real_bytes(void) { return (int)sizeof(real); }
+
+int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}

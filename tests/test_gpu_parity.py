@@ -1,0 +1,194 @@
+"""GPU parity of every hot-path stage against the CPU oracle, on identical seeded inputs.
+
+Each stage is fed the same inputs on both sides (the GPU's own upstream results), so a stage is
+judged on its own: binning, sort and tile ranges must be bit-exact; renders within 1e-4 absolute;
+gradients within 1e-3 relative with a 1e-5 absolute floor.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from xsimgs_amd import _C, frame, synthetic
+from tests._util import GRAD_ATOL, GRAD_RTOL, RENDER_ATOL, frac_close, np_, report
+
+pytestmark = pytest.mark.gpu
+
+
+def _cam_pack(spec, dev):
+    return frame.make_camera(spec, dev).pack
+
+
+@pytest.fixture(scope="module")
+def cfg0(dev):
+    sc = synthetic.make_cfg0()
+    st = frame.prepare(sc, dev, requires_grad=False)
+    return sc, st
+
+
+# ------------------------------------------------------------------ SH
+@pytest.mark.parametrize("degree,layout_3kn,with_dc,with_mask", [
+    (0, False, False, False), (3, False, False, False), (3, True, False, False), (3, False, True, True),
+    (4, True, True, False), (2, False, False, True), (1, True, False, True)])
+def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask):
+    g = torch.Generator().manual_seed(7 + degree)
+    n = 3001
+    K = (degree + 1) ** 2 + 2            # extra unused bands must come back zero in d_coeffs
+    pos = torch.randn(n, 3, generator=g) * 5
+    origin = torch.tensor([0.3, -0.2, 0.1])
+    kb = K - (1 if with_dc else 0)
+    coeffs = torch.randn(3, kb, n, generator=g) if layout_3kn else torch.randn(n, kb, 3, generator=g)
+    dc = (torch.randn(3, n, generator=g) if layout_3kn else torch.randn(n, 3, generator=g)) if with_dc else None
+    mask = torch.randint(-2**31, 2**31 - 1, ((n + 31) // 32,), generator=g, dtype=torch.int32) if with_mask else None
+    d_out = torch.randn(n, 3, generator=g)
+    D = lambda t: None if t is None else t.to(dev)
+    out = _C.spherical_harmonics_fused_fwd(degree, D(origin), D(pos), D(coeffs), D(mask), layout_3kn, D(dc))
+    m_np = None if mask is None else mask.numpy().view(np.uint32)
+    ref = O.sh_fwd(degree, origin, pos, coeffs, dc=dc, mask=m_np, layout_3kn=layout_3kn)
+    print(report("sh_fwd", np_(out), ref))
+    assert frac_close(np_(out), ref, RENDER_ATOL) == 1.0
+    dco, ddc, dpos, dori = _C.spherical_harmonics_fused_bwd(degree, D(origin), D(pos), D(coeffs), D(mask),
+                                                            layout_3kn, D(d_out), D(dc))
+    rdco, rddc, rdpos, rdori = O.sh_bwd(degree, origin, pos, coeffs, d_out, dc=dc, mask=m_np, layout_3kn=layout_3kn)
+    for name, a, b in (("d_coeffs", dco, rdco), ("d_dc", ddc, rddc), ("d_pos", dpos, rdpos), ("d_origin", dori, rdori)):
+        print(report(name, np_(a), b))
+        assert np_(a).shape == b.shape, name
+        assert frac_close(np_(a), b, GRAD_ATOL, GRAD_RTOL) == 1.0, name
+
+
+# ------------------------------------------------------------------ projection, rays
+def test_ut_projection_pinhole(dev, cfg0):
+    sc, st = cfg0
+    spec = sc.cameras[0]
+    pack = _cam_pack(spec, dev)
+    flags, radii, m2, dep = _C.PerspectiveCamera.projection_utgs(
+        pack, st.means, None, torch.exp(st.log_scales), st.quats, torch.sigmoid(st.opacity_logits),
+        spec.width, spec.height)
+    rf, rr, rm, rd = O.project_utgs(spec, sc.means, sc.scales, sc.quats, sc.opacity, spec.width, spec.height)
+    f = np_(flags)
+    agree = (f == rf).mean()
+    print("flags agree", agree, "visible", int(f.sum()))
+    assert agree > 0.999
+    both = (f > 0) & (rf > 0)
+    print(report("means2d", np_(m2)[both], rm[both]), report("radii", np_(radii)[both], rr[both]),
+          report("depth", np_(dep)[both], rd[both]))
+    assert frac_close(np_(m2)[both], rm[both], 2e-2, 1e-5) > 0.999
+    assert frac_close(np_(radii)[both], rr[both], 2e-2, 1e-4) > 0.999
+    assert frac_close(np_(dep)[both], rd[both], 1e-5, 1e-6) == 1.0
+    # culled Gaussians are all zeros
+    assert np.all(np_(radii)[f == 0] == 0) and np.all(np_(m2)[f == 0] == 0) and np.all(np_(dep)[f == 0] == 0)
+
+
+@pytest.mark.parametrize("cfg", ["cfg0", "cfg3"])
+def test_camera_rays(dev, cfg):
+    sc = synthetic.make_cfg0() if cfg == "cfg0" else synthetic.make_cfg3(n=1000)
+    spec = sc.cameras[0]
+    cam = frame.make_camera(spec, dev)
+    ro, rd = cam.camera_rays(spec.width, spec.height)
+    rro, rrd = O.camera_rays(spec, spec.width, spec.height)
+    print(report("ray_d", np_(rd), rrd))
+    assert np.abs(np_(ro) - rro).max() <= 1e-6
+    assert np.abs(np_(rd) - rrd).max() <= 2e-6
+
+
+# ------------------------------------------------------------------ binning
+def _ut(st, spec, dev, phm=False):
+    cam = frame.make_camera(spec, dev)
+    fn = cam.ext_cls.projection_utgs_phm if phm else cam.ext_cls.projection_utgs
+    return cam, fn(cam.pack, st.means, None, torch.exp(st.log_scales), st.quats,
+                   torch.sigmoid(st.opacity_logits), spec.width, spec.height)
+
+
+@pytest.mark.parametrize("sort", [True, False])
+def test_isect_regular_bitexact(dev, cfg0, sort):
+    sc, st = cfg0
+    spec = sc.cameras[0]
+    _, (flags, radii, m2, dep) = _ut(st, spec, dev)
+    tpg, ids, fl = _C.isect_regular_tiles(m2, radii, dep, spec.width, spec.height, 16, 16, sort=sort)
+    rtpg, rids, rfl = O.isect_regular(np_(m2), np_(radii), np_(dep), spec.width, spec.height, 16, 16, sort=sort)
+    assert np.array_equal(np_(tpg), rtpg)
+    assert np.array_equal(np_(ids), rids)
+    assert np.array_equal(np_(fl), rfl)
+    if sort:  # tile ranges are defined for sorted keys only (the reference's encoder races otherwise)
+        off = _C.isect_offset_encode(ids, 16, 16)
+        assert np.array_equal(np_(off), O.offset_encode(rids, 16, 16))
+
+
+def test_isect_regular_edge_cases(dev):
+    # empty input, all-culled input, Gaussians on tile borders and outside the image, negative depth
+    W, H = 100, 70
+    m2 = torch.tensor([[0.0, 0.0], [16.0, 16.0], [99.9, 69.9], [-30.0, 10.0], [50.0, 35.0], [50.0, 35.0],
+                       [200.0, 200.0], [8.0, 8.0]])
+    r = torch.tensor([[1.0, 1.0], [16.0, 0.5], [3.0, 3.0], [31.0, 2.0], [0.0, 5.0], [7.5, 7.5],
+                      [500.0, 500.0], [2.0, 2.0]])
+    d = torch.tensor([1.0, 2.0, 2.0, 3.0, 4.0, 2.0, 9.0, -1.5])
+    # the last Gaussian has a negative depth: its sign-extended key (tiling_common.cuh:37) saturates
+    # the tile bits, which the sort must reproduce; tile ranges are only defined without it
+    for n in (0, m2.shape[0] - 1, m2.shape[0]):
+        tpg, ids, fl = _C.isect_regular_tiles(m2[:n].to(dev).contiguous(), r[:n].to(dev).contiguous(),
+                                              d[:n].to(dev).contiguous(), W, H, 16, 16)
+        rtpg, rids, rfl = O.isect_regular(m2[:n], r[:n], d[:n], W, H, 16, 16)
+        assert np.array_equal(np_(tpg), rtpg) and np.array_equal(np_(ids), rids) and np.array_equal(np_(fl), rfl)
+        if n < m2.shape[0]:
+            off = _C.isect_offset_encode(ids, 7, 5)
+            assert np.array_equal(np_(off), O.offset_encode(rids, 7, 5))
+
+
+def test_radix_sort_pairs(dev):
+    g = np.random.default_rng(3)
+    for n, bits in ((1, 45), (1000, 45), (300_001, 45), (70_000, 13), (12345, 64)):
+        keys = g.integers(0, 2**62, n, dtype=np.int64) & ((1 << min(bits, 63)) - 1)
+        keys[: n // 3] = keys[n // 2] if n > 3 else keys[0]       # heavy ties
+        vals = np.arange(n, dtype=np.int32)
+        k, v = _C.radix_sort_pairs(torch.from_numpy(keys).to(dev), torch.from_numpy(vals).to(dev), 0, bits)
+        rk, rv = O.sort_pairs(keys, vals, bits)
+        mask = np.uint64((1 << bits) - 1) if bits < 64 else np.uint64(0xFFFFFFFFFFFFFFFF)
+        order = np.argsort(keys.view(np.uint64) & mask, kind="stable")
+        assert np.array_equal(np_(k), rk) and np.array_equal(np_(v), rv)
+        assert np.array_equal(rv, vals[order])
+
+
+# ------------------------------------------------------------------ compositing
+def _binned(st, sc, dev):
+    spec = sc.cameras[0]
+    cam, (flags, radii, m2, dep) = _ut(st, spec, dev, sc.use_phm)
+    tsx, tsy = sc.tile_size
+    tpg, ids, fl = cam.isect_gs_tiles(st.means, torch.exp(st.log_scales), st.quats, spec.width, spec.height,
+                                      flags, radii, m2, dep, opacity=torch.sigmoid(st.opacity_logits),
+                                      tile_size_x=tsx, tile_size_y=tsy)
+    off = _C.isect_offset_encode(ids, (spec.width + tsx - 1) // tsx, (spec.height + tsy - 1) // tsy)
+    ro, rd = cam.camera_rays(spec.width, spec.height)
+    return cam, off, fl, ro, rd
+
+
+def test_eval3d_fwd_bwd_cfg0(dev, cfg0):
+    sc, st = cfg0
+    spec = sc.cameras[0]
+    cam, off, fl, ro, rd = _binned(st, sc, dev)
+    scales = torch.exp(st.log_scales)
+    opac = torch.sigmoid(st.opacity_logits)
+    colors = _C.spherical_harmonics_fused_fwd(0, cam.pose.t, st.means, st.sh, None, False)
+    rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(st.means, st.quats, scales, colors.unsqueeze(0),
+                                                      opac.view(1, -1), spec.width, spec.height, 16, 16, ro, rd,
+                                                      off, fl)
+    ref = O.eval3d_fwd(np_(st.means), np_(st.quats), np_(scales), np_(colors), np_(opac), np_(ro), np_(rd),
+                       np_(off), np_(fl), 16, 16)
+    for name, a, b in (("rgb", rgb, ref[0]), ("depth", depth, ref[1]), ("alpha", alpha, ref[2])):
+        print(report(name, np_(a), b), "frac", frac_close(np_(a), b, RENDER_ATOL))
+        assert frac_close(np_(a), b, RENDER_ATOL) > 0.999, name
+    print("last_ids agree", (np_(last) == ref[3]).mean())
+    assert (np_(last) == ref[3]).mean() > 0.999
+    g = torch.Generator().manual_seed(11)
+    vr = (torch.randn(spec.height, spec.width, 3, generator=g) * 1e-3).to(dev)
+    vd = (torch.randn(spec.height, spec.width, generator=g) * 1e-3).to(dev)
+    va = (torch.randn(spec.height, spec.width, generator=g) * 1e-3).to(dev)
+    grads = _C.rasterize_eval3d_bwd(st.means, scales, st.quats, opac, colors, ro, rd, 16, 16, off, fl, alpha, last,
+                                    vr, vd, va)
+    rg = O.eval3d_bwd(np_(st.means), np_(st.quats), np_(scales), np_(colors), np_(opac), np_(ro), np_(rd),
+                      np_(off), np_(fl), np_(alpha), np_(last), np_(vr), np_(vd), np_(va), 16, 16)
+    names = ["v_means", "v_quats", "v_scales", "v_opacity", "v_colors", "v_ray_o", "v_ray_d"]
+    for name, a in zip(names, grads):
+        b = rg[name]
+        fc = frac_close(np_(a), b, GRAD_ATOL, GRAD_RTOL)
+        print(report(name, np_(a), b), "frac", fc)
+        assert fc > 0.999, name

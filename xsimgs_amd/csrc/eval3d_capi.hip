@@ -1,0 +1,182 @@
+// C-ABI entry points of the eval3d compositor and the per-Gaussian backward epilogue.
+#include <algorithm>
+
+#include "xsg_eval3d.h"
+
+namespace xsg {
+namespace {
+
+constexpr int kBlock = 256;
+
+__global__ __launch_bounds__(kBlock) void zero_kernel(float* __restrict__ a, int64_t na, float* __restrict__ b,
+                                                      int64_t nb, float* __restrict__ c, int64_t nc,
+                                                      float* __restrict__ d, int64_t nd, float* __restrict__ e,
+                                                      int64_t ne) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < na + nb + nc + nd + ne; i += stride) {
+        int64_t k = i;
+        if (k < na) { a[k] = 0.f; continue; }
+        k -= na;
+        if (k < nb) { b[k] = 0.f; continue; }
+        k -= nb;
+        if (k < nc) { c[k] = 0.f; continue; }
+        k -= nc;
+        if (k < nd) { d[k] = 0.f; continue; }
+        k -= nd;
+        e[k] = 0.f;
+    }
+}
+
+// quat_scale_to_preci_half_vjp + quat_to_rotmat_vjp (utils.h:208-263) applied once per Gaussian to
+// the accumulated dL/dM^T. vmt holds M^T gradients row-major: vmt[c*3 + r] is the glm element
+// v_M[c][r] of the reference (v_M = transpose(v_Mt)).
+__global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const float4* __restrict__ quats,
+                                                              const float* __restrict__ scales,
+                                                              const float* __restrict__ vmt,
+                                                              float4* __restrict__ v_quats,
+                                                              float* __restrict__ v_scales) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const float4 q = quats[i];
+    float w = q.x, x = q.y, y = q.z, z = q.w;
+    const float inv_norm = rsqrtf(x * x + y * y + z * z + w * w);
+    x *= inv_norm; y *= inv_norm; z *= inv_norm; w *= inv_norm;
+    const float s[3] = {1.0f / scales[3 * i], 1.0f / scales[3 * i + 1], 1.0f / scales[3 * i + 2]};
+    float vm[3][3];  // glm v_M[c][r]
+#pragma unroll
+    for (int cc = 0; cc < 3; ++cc)
+#pragma unroll
+        for (int r = 0; r < 3; ++r) vm[cc][r] = vmt[9 * i + 3 * cc + r];
+    // v_R = v_M * S  -> glm v_R[c][r] = v_M[c][r] * s_c
+    float V[3][3];
+#pragma unroll
+    for (int cc = 0; cc < 3; ++cc)
+#pragma unroll
+        for (int r = 0; r < 3; ++r) V[cc][r] = vm[cc][r] * s[cc];
+    float vq[4];
+    vq[0] = 2.f * (x * (V[1][2] - V[2][1]) + y * (V[2][0] - V[0][2]) + z * (V[0][1] - V[1][0]));
+    vq[1] = 2.f * (-2.f * x * (V[1][1] + V[2][2]) + y * (V[0][1] + V[1][0]) + z * (V[0][2] + V[2][0]) +
+                   w * (V[1][2] - V[2][1]));
+    vq[2] = 2.f * (x * (V[0][1] + V[1][0]) - 2.f * y * (V[0][0] + V[2][2]) + z * (V[1][2] + V[2][1]) +
+                   w * (V[2][0] - V[0][2]));
+    vq[3] = 2.f * (x * (V[0][2] + V[2][0]) + y * (V[1][2] + V[2][1]) - 2.f * z * (V[0][0] + V[1][1]) +
+                   w * (V[0][1] - V[1][0]));
+    const float qn[4] = {w, x, y, z};
+    const float dp = vq[0] * qn[0] + vq[1] * qn[1] + vq[2] * qn[2] + vq[3] * qn[3];
+    v_quats[i] = make_float4((vq[0] - dp * qn[0]) * inv_norm, (vq[1] - dp * qn[1]) * inv_norm,
+                             (vq[2] - dp * qn[2]) * inv_norm, (vq[3] - dp * qn[3]) * inv_norm);
+    // R columns (glm R[c]) from quat_to_rotmat (utils.h:61-83)
+    const float x2 = x * x, y2 = y * y, z2 = z * z, xy = x * y, xz = x * z, yz = y * z;
+    const float wx = w * x, wy = w * y, wz = w * z;
+    const float R[3][3] = {{1.f - 2.f * (y2 + z2), 2.f * (xy + wz), 2.f * (xz - wy)},
+                           {2.f * (xy - wz), 1.f - 2.f * (x2 + z2), 2.f * (yz + wx)},
+                           {2.f * (xz + wy), 2.f * (yz - wx), 1.f - 2.f * (x2 + y2)}};
+#pragma unroll
+    for (int cc = 0; cc < 3; ++cc)
+        v_scales[3 * i + cc] = -s[cc] * s[cc] * (R[cc][0] * vm[cc][0] + R[cc][1] * vm[cc][1] + R[cc][2] * vm[cc][2]);
+}
+
+bool cdim_supported(int c) {
+    switch (c) {
+#define XSG_CASE(C) case C: return true;
+        XSG_CDIM_LIST(XSG_CASE)
+#undef XSG_CASE
+        default: return false;
+    }
+}
+
+int fill_params(const xsg_eval3d_args* a, Eval3dParams& p, const char* who) {
+    if (!a) return xsg_fail(XSG_ERR_INVALID, "%s: null arguments", who);
+    if (!cdim_supported(a->cdim)) return xsg_fail(XSG_ERR_INVALID, "Unsupported number of channels: %d", a->cdim);
+    if (a->tile_w <= 0 || a->tile_h <= 0 || a->width < 0 || a->height < 0 || a->n_cams < 1 || a->n < 0 ||
+        a->n_isects < 0 || a->n_tiles_w <= 0 || a->n_tiles_h <= 0)
+        return xsg_fail(XSG_ERR_INVALID, "%s: invalid sizes", who);
+    if (a->tile_w * a->tile_h > kTileThreads)
+        return xsg_fail(XSG_ERR_LDS, "Failed to set maximum shared memory size (tile %dx%d has more than %d pixels), "
+                        "try lowering tile_size.", a->tile_w, a->tile_h, kTileThreads);
+    if ((int64_t)a->n_tiles_w * a->tile_w < a->width || (int64_t)a->n_tiles_h * a->tile_h < a->height)
+        return xsg_fail(XSG_ERR_INVALID, "%s: tile grid %dx%d of %dx%d tiles does not cover %dx%d pixels", who,
+                        a->n_tiles_w, a->n_tiles_h, a->tile_w, a->tile_h, a->width, a->height);
+    if (a->cdim > 0 && !a->colors) return xsg_fail(XSG_ERR_INVALID, "%s: colors missing for cdim %d", who, a->cdim);
+    if (!a->means || !a->quats || !a->scales || !a->opacities || !a->ray_o || !a->ray_d || !a->tile_offsets ||
+        (a->n_isects > 0 && !a->flatten_ids))
+        return xsg_fail(XSG_ERR_INVALID, "%s: null input", who);
+    p = Eval3dParams{};
+    p.g = TileGrid{a->width, a->height, a->tile_w, a->tile_h, a->n_tiles_w, a->n_tiles_h, a->n_cams, a->n,
+                   a->n_isects};
+    p.means = a->means; p.quats = (const float4*)a->quats; p.scales = a->scales; p.colors = a->colors;
+    p.opac = a->opacities; p.velocity = a->velocity; p.rtd = a->ray_time_delta;
+    p.ray_o = a->ray_o; p.ray_d = a->ray_d; p.offsets = a->tile_offsets; p.flatten = a->flatten_ids;
+    return XSG_OK;
+}
+
+}  // namespace
+}  // namespace xsg
+
+using namespace xsg;
+
+extern "C" int xsg_eval3d_supported_ndims(int* out, int cap) {
+    static const int dims[] = {
+#define XSG_ITEM(C) C,
+        XSG_CDIM_LIST(XSG_ITEM)
+#undef XSG_ITEM
+    };
+    const int n = (int)(sizeof(dims) / sizeof(dims[0]));
+    for (int i = 0; i < n && i < cap && out; ++i) out[i] = dims[i];
+    return n;
+}
+
+extern "C" int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream) {
+    Eval3dParams p;
+    int rc = fill_params(a, p, "xsg_eval3d_fwd");
+    if (rc) return rc;
+    if (!a->out_depth || !a->out_alpha || !a->out_last_ids || (a->cdim > 0 && !a->out_rgb))
+        return xsg_fail(XSG_ERR_INVALID, "xsg_eval3d_fwd: null output");
+    if ((int64_t)a->width * a->height == 0) return XSG_OK;
+    p.out_rgb = a->out_rgb; p.out_depth = a->out_depth; p.out_alpha = a->out_alpha; p.out_last = a->out_last_ids;
+    const bool dyn = a->velocity != nullptr || a->ray_time_delta != nullptr;
+    rc = eval3d_fwd_launch(a->cdim, dyn, p, (hipStream_t)stream);
+    if (rc) return rc;
+    XSG_TRY_LAUNCH("eval3d_fwd");
+    return XSG_OK;
+}
+
+extern "C" size_t xsg_eval3d_bwd_workspace_bytes(int64_t n, int cdim) {
+    (void)cdim;
+    return (size_t)(n > 0 ? n : 1) * 9 * sizeof(float);
+}
+
+extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_stream_t stream) {
+    Eval3dParams p;
+    int rc = fill_params(a, p, "xsg_eval3d_bwd");
+    if (rc) return rc;
+    const bool dyn = a->velocity != nullptr;
+    if (dyn && !a->ray_time_delta)
+        return xsg_fail(XSG_ERR_INVALID, "dynamic backward needs both velocity and ray_time_delta");
+    if (!a->render_alpha || !a->last_ids || !a->v_depth || !a->v_alpha || (a->cdim > 0 && !a->v_rgb) ||
+        !a->v_means || !a->v_quats || !a->v_scales || !a->v_opacities || (a->cdim > 0 && !a->v_colors) ||
+        !a->v_ray_o || !a->v_ray_d || (dyn && (!a->v_velocity || !a->v_time_delta)) || !workspace)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_eval3d_bwd: null buffer");
+    const hipStream_t s = (hipStream_t)stream;
+    p.render_alpha = a->render_alpha; p.last_ids = a->last_ids; p.v_rgb = a->v_rgb; p.v_depth = a->v_depth;
+    p.v_alpha = a->v_alpha; p.v_means = a->v_means; p.v_opac = a->v_opacities; p.v_colors = a->v_colors;
+    p.v_ray_o = a->v_ray_o; p.v_ray_d = a->v_ray_d; p.v_velocity = a->v_velocity; p.v_time = a->v_time_delta;
+    p.v_mt = (float*)workspace;
+    const int64_t n = a->n;
+    const int64_t ncol = a->cdim > 0 ? (int64_t)a->n_cams * n * a->cdim : 0;
+    const int64_t total = 3 * n + n + ncol + 9 * n + (dyn ? 3 * n : 0);
+    if (total > 0) {
+        const unsigned grid = (unsigned)std::min<int64_t>((total + kBlock - 1) / kBlock, 4096);
+        zero_kernel<<<grid, kBlock, 0, s>>>(a->v_means, 3 * n, a->v_opacities, n, a->v_colors, ncol, p.v_mt, 9 * n,
+                                            a->v_velocity, dyn ? 3 * n : 0);
+    }
+    if ((int64_t)a->width * a->height > 0) {
+        rc = eval3d_bwd_launch(a->cdim, dyn, p, s);
+        if (rc) return rc;
+    }
+    if (n > 0)
+        bwd_epilogue_kernel<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, s>>>(
+            n, (const float4*)a->quats, a->scales, p.v_mt, (float4*)a->v_quats, a->v_scales);
+    XSG_TRY_LAUNCH("eval3d_bwd");
+    return XSG_OK;
+}

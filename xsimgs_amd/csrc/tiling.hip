@@ -1,0 +1,685 @@
+// Tile binning: per-Gaussian tile rectangles, intersection keys, stable sort, per-tile ranges.
+//
+// Reference: csrc/tiling/regular_tiling.cu, phm_lidar_tiling.cu, phm_spherical_tiling.cu,
+// tiling_common.cu(h), mask_radii.cu.
+//
+// The reference sorts 64-bit keys (tile << 32 | depth bits) over bits [0, 32 + tile_n_bits) with a
+// stable radix sort whose input is in Gaussian order. This build produces the identical arrays
+// with less traffic:
+//   1. count  : one thread per Gaussian instance computes its tile rectangle(s) (the seam
+//               re-projection of lidar / spherical flag-2 Gaussians happens here, once) and
+//               writes tiles_per_gauss plus the rectangles.
+//   2. compact: one packed 64-bit scan ((count > 0) << 32 | count) gives every visible
+//               instance both its intersection offset and its rank among visible instances.
+//   3. depth  : the visible instances are sorted stably by the low 32 key bits (depth bits).
+//   4. expand : a merge-path expansion writes (key bits >= 32, instance) pairs in that order,
+//               coalesced, one output per thread.
+//   5. tile   : a stable sort on the remaining key bits (tile, camera) finishes the order and
+//               the last pass writes the 64-bit keys and flattened ids.
+// Stable by (high bits, low bits, Gaussian order) in both cases, so the result is bit-identical
+// to sorting the reference keys; ties keep Gaussian order as the reference's fill does.
+#include "xsg_sort.h"
+
+UtWeights xsg_ut_weights(float a, float b, float k);
+
+namespace {
+using namespace xsg;
+
+constexpr int kBlock = 256;
+constexpr int kExpandPerBlock = 1024;
+
+struct Rect { uint16_t x0, y0, x1, y1; };  // exclusive [x0, x1) x [y0, y1)
+
+XSG_DEV uint32_t rect_count(Rect r) { return (uint32_t)(r.x1 - r.x0) * (uint32_t)(r.y1 - r.y0); }
+XSG_DEV uint64_t pack_count(uint32_t c) { return ((uint64_t)(c > 0) << 32) | (uint64_t)c; }
+
+// regular_tiling.cu:35-56
+XSG_DEV Rect regular_rect(float2 m, float2 r, float tsx, float tsy, int ntx, int nty) {
+    Rect out = {0, 0, 0, 0};
+    if (r.x <= 0 || r.y <= 0) return out;
+    const float mx = m.x / tsx, my = m.y / tsy;
+    const float rx = r.x / tsx, ry = r.y / tsy;
+    out.x0 = (uint16_t)min(ntx, max(0, (int)floorf(mx - rx)));
+    out.y0 = (uint16_t)min(nty, max(0, (int)floorf(my - ry)));
+    out.x1 = (uint16_t)min(ntx, max(0, (int)ceilf(mx + rx)));
+    out.y1 = (uint16_t)min(nty, max(0, (int)ceilf(my + ry)));
+    return out;
+}
+
+// find_bounds_increasing + tile_limits_irregular (phm_lidar_tiling.cu:35-91), inclusive bounds
+// returned as an exclusive rectangle.
+XSG_DEV Rect lidar_rect(float mx, float my, float rx, float ry, float u_min, float u_max, float u_per_tile,
+                        int n_elev, const float* __restrict__ elev) {
+    Rect out = {0, 0, 0, 0};
+    const float lo = fmaxf(mx - rx, u_min), hi = fminf(mx + rx, u_max);
+    if (hi <= lo) return out;
+    const int x0 = (int)floorf(lo / u_per_tile);
+    const int x1 = (int)ceilf(hi / u_per_tile) - 1;
+    const float vmin = my - ry, vmax = my + ry;
+    int i = 0;
+    while (i < n_elev && elev[i] < vmin) ++i;
+    const int y0 = min(max(i - 1, 0), n_elev - 1);
+    while (i < n_elev && elev[i] < vmax) ++i;
+    const int y1 = min(max(i - 1, 0), n_elev - 1);
+    out.x0 = (uint16_t)x0; out.x1 = (uint16_t)(x1 + 1);
+    out.y0 = (uint16_t)y0; out.y1 = (uint16_t)(y1 + 1);
+    return out;
+}
+
+// tile_limits_regular (phm_spherical_tiling.cu:15-45)
+XSG_DEV Rect spherical_rect(float mx, float my, float rx, float ry, float u_min, float u_max, float u_per_tile,
+                            int n_v, float v_per_tile) {
+    Rect out = {0, 0, 0, 0};
+    const float lo = fmaxf(mx - rx, u_min), hi = fminf(mx + rx, u_max);
+    if (hi <= lo) return out;
+    out.x0 = (uint16_t)(int)floorf(lo / u_per_tile);
+    out.y0 = (uint16_t)min(n_v, max(0, (int)floorf((my - ry) / v_per_tile)));
+    out.x1 = (uint16_t)(int)ceilf(hi / u_per_tile);
+    out.y1 = (uint16_t)min(n_v, max(0, (int)ceilf((my + ry) / v_per_tile)));
+    return out;
+}
+
+struct Geometry {
+    int kind, n_cams;
+    int64_t n;          // Gaussians per camera
+    int ntx, nty;       // tiles along u / v
+    int n_tiles;
+    int tnb;            // tile_n_bits
+    int cam_bits;
+    int spans;          // virtual instances per Gaussian instance: 1 (regular) or 2 (seam split)
+};
+
+// Count pass over Gaussian instances. A block covers kSortTile virtual instances (kSortTile /
+// SPANS Gaussians); it writes tiles_per_gauss, the rectangle, count and depth bits of every
+// virtual instance, and the block's packed count sum.
+__global__ __launch_bounds__(kBlock) void count_regular_kernel(
+    int64_t n_total, const float2* __restrict__ means2d, const float2* __restrict__ radii,
+    const float* __restrict__ depths, float tsx, float tsy, int ntx, int nty, int32_t* __restrict__ tpg,
+    Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
+    uint64_t* __restrict__ partials) {
+    __shared__ uint64_t lds[kWaves];
+    uint64_t acc = 0;
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
+        if (j < n_total) {
+            const Rect r = regular_rect(means2d[j], radii[j], tsx, tsy, ntx, nty);
+            const uint32_t c = rect_count(r);
+            tpg[j] = (int32_t)c;
+            rects[j] = r;
+            vcnt[j] = c;
+            vkey[j] = __float_as_uint(depths[j]);
+            acc += pack_count(c);
+        }
+    }
+    acc = block_reduce_sum<uint64_t>(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+}
+
+// isect_lidar_tiles_kernel (phm_lidar_tiling.cu:96-234) / isect_spherical_tiles_kernel
+// (phm_spherical_tiling.cu:47-174), count part. Flag-2 Gaussians are re-projected with
+// PositiveDelta once here; their second span (virtual instance 2j+1) carries the re-projected
+// depth, as the reference's second fill_tiles call does (phm_lidar_tiling.cu:224-226).
+template <int KIND, bool LIDAR>
+__global__ __launch_bounds__(kBlock) void count_spherical_kernel(
+    int64_t n, const float* __restrict__ pack, UtWeights ut, f2 img, const float* __restrict__ points,
+    const float* __restrict__ vel, const float* __restrict__ scales, const float4* __restrict__ quats,
+    const float* __restrict__ opacity, const uint8_t* __restrict__ flags, const float2* __restrict__ means2d,
+    const float2* __restrict__ radii, const float* __restrict__ depths, const float* __restrict__ elev,
+    int n_elev, float u_per_tile, float v_per_tile, int n_v, int32_t* __restrict__ tpg,
+    Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
+    uint64_t* __restrict__ partials) {
+    __shared__ uint64_t lds[kWaves];
+    const Camera cam = load_camera(pack, KIND);
+    const bool is_static = camera_is_static(cam, vel != nullptr);
+    uint64_t acc = 0;
+    const int64_t base = (int64_t)blockIdx.x * (kSortTile / 2);
+    for (int k = 0; k < kSortItems / 2; ++k) {
+        const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
+        if (j >= n) continue;
+        const float2 r = radii[j];
+        const int flag = flags[j];
+        Rect a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+        float dep2 = 0.f;
+        if (!(r.x <= 0 || r.y <= 0 || flag == 0)) {
+            float u_min = 0.0f, u_max = 1.0f;
+            const float u_pose = u_pose_of(cam);
+            if (flag == 2) {
+                if (cam.roll_u > 0) u_max = u_pose; else u_min = u_pose;
+            }
+            const float2 m = means2d[j];
+            const float mx = m.x / img.x, my = m.y / img.y, rx = r.x / img.x, ry = r.y / img.y;
+            if (LIDAR) a = lidar_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, elev);
+            else a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile);
+            if (flag == 2) {
+                f3 d[3];
+                ut_deltas(ut.sqrt_dl, quats[j], ld3(scales + 3 * j), d);
+                const float op = opacity ? opacity[j] : 1.0f;
+                const f3 pv = vel ? ld3(vel + 3 * j) : mk3(0.f, 0.f, 0.f);
+                const ProjParams pp{1e-4f, 0.002f, 1.0f};
+                f2 m2 = mk2(0.f, 0.f), r2 = mk2(0.f, 0.f);
+                float dd = 0.f, ud = 0.f;
+                if (ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, ld3(points + 3 * j), pv, op, d,
+                                        is_static, m2, r2, dd, ud)) {
+                    if (cam.roll_u > 0) {
+                        u_min = ceilf(u_pose / u_per_tile) * u_per_tile + 1e-6f;
+                        u_max = 1.0f;
+                    } else {
+                        u_min = 0.0f;
+                        u_max = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f;
+                    }
+                    const float mx2 = m2.x / img.x, my2 = m2.y / img.y, rx2 = r2.x / img.x, ry2 = r2.y / img.y;
+                    if (LIDAR) b = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev);
+                    else b = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile);
+                    dep2 = dd;
+                }
+            }
+        }
+        const uint32_t ca = rect_count(a), cb = rect_count(b);
+        tpg[j] = (int32_t)(ca + cb);
+        rects[2 * j] = a;
+        rects[2 * j + 1] = b;
+        vcnt[2 * j] = ca;
+        vcnt[2 * j + 1] = cb;
+        vkey[2 * j] = __float_as_uint(depths[j]);
+        vkey[2 * j + 1] = __float_as_uint(dep2);
+        acc += pack_count(ca) + pack_count(cb);
+    }
+    acc = block_reduce_sum<uint64_t>(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+}
+
+// single block: exclusive scan of the block partials in place, grand total at partials[nb]
+template <typename T>
+__global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb) {
+    __shared__ T lds[kWaves];
+    T carry = 0;
+    for (unsigned start = 0; start < nb; start += kBlock) {
+        const unsigned i = start + threadIdx.x;
+        const T v = i < nb ? partials[i] : (T)0;
+        T tot;
+        const T ex = block_exclusive_scan<T>(v, lds, tot);
+        if (i < nb) partials[i] = carry + ex;
+        carry += tot;
+    }
+    if (threadIdx.x == 0) partials[nb] = carry;
+}
+
+// Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
+__global__ __launch_bounds__(kBlock) void compact_kernel(
+    int64_t n_virtual, const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vkey,
+    const uint64_t* __restrict__ partials, uint32_t* __restrict__ comp_id, uint32_t* __restrict__ comp_off,
+    uint32_t* __restrict__ comp_key) {
+    __shared__ uint64_t lds[kWaves];
+    uint64_t carry = partials[blockIdx.x];
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        if (base + (int64_t)k * kBlock >= n_virtual) break;  // block-uniform
+        const int64_t v = base + (int64_t)k * kBlock + threadIdx.x;
+        const uint32_t c = v < n_virtual ? vcnt[v] : 0u;
+        uint64_t tot;
+        const uint64_t s = carry + block_exclusive_scan<uint64_t>(pack_count(c), lds, tot);
+        carry += tot;
+        if (c > 0) {
+            const uint64_t p = s >> 32;
+            if (p < (uint64_t)n_virtual) {
+                comp_id[p] = (uint32_t)v;
+                comp_off[p] = (uint32_t)s;
+                comp_key[p] = vkey[v];
+            }
+        }
+    }
+}
+
+// counts of the depth-sorted virtual instances -> exclusive offsets (reduce / scan partials / scan)
+__global__ __launch_bounds__(kBlock) void gather_reduce_kernel(int64_t m, const uint32_t* __restrict__ ids,
+                                                               const uint32_t* __restrict__ vcnt,
+                                                               uint32_t* __restrict__ partials) {
+    __shared__ uint32_t lds[kWaves];
+    uint32_t acc = 0;
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
+        if (p < m) acc += vcnt[ids[p]];
+    }
+    acc = block_reduce_sum<uint32_t>(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void gather_scan_kernel(int64_t m, const uint32_t* __restrict__ ids,
+                                                             const uint32_t* __restrict__ vcnt,
+                                                             const uint32_t* __restrict__ partials,
+                                                             uint32_t* __restrict__ offs) {
+    __shared__ uint32_t lds[kWaves];
+    uint32_t carry = partials[blockIdx.x];
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        if (base + (int64_t)k * kBlock >= m) break;
+        const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
+        const uint32_t c = p < m ? vcnt[ids[p]] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(c, lds, tot);
+        if (p < m) offs[p] = carry + ex;
+        carry += tot;
+    }
+}
+
+// 64-bit key exactly as tiling_common.cuh:37,68 builds it: (tile << 32) | sign-extended depth bits
+XSG_DEV int64_t make_key(uint32_t tile_hi, uint32_t depth_bits) {
+    return (int64_t)(((uint64_t)tile_hi) << 32) | (int64_t)(int32_t)depth_bits;
+}
+
+struct PairsOut {  // key bits >= 32 under the sort mask, and the virtual instance, for the tile sort
+    uint32_t* hi;
+    uint32_t* id;
+    uint32_t mask;
+    XSG_DEV void put(int64_t o, uint32_t tile_hi, uint32_t v, uint32_t dbits, int spans) const {
+        (void)spans;
+        hi[o] = ((int32_t)dbits < 0) ? mask : (tile_hi & mask);
+        id[o] = v;
+    }
+};
+
+struct FinalOut {  // unsorted output in the reference's fill order
+    int64_t* keys;
+    int32_t* ids;
+    XSG_DEV void put(int64_t o, uint32_t tile_hi, uint32_t v, uint32_t dbits, int spans) const {
+        keys[o] = make_key(tile_hi, dbits);
+        ids[o] = (int32_t)(v / (uint32_t)spans);
+    }
+};
+
+// Last tile-sort pass: 64-bit key with the virtual instance's depth bits, and the instance id.
+struct SortedKeyOut {
+    int64_t* keys;
+    int32_t* ids;
+    const uint32_t* vkey;
+    int spans;
+    XSG_DEV void put(int64_t pos, uint32_t hi, uint32_t v) const {
+        keys[pos] = make_key(hi, vkey[v]);
+        ids[pos] = (int32_t)(v / (uint32_t)spans);
+    }
+};
+
+// Merge-path expansion: block b produces outputs [b * E, (b + 1) * E); the visible virtual
+// instances overlapping that range (at most E, every count >= 1) are staged in LDS, each
+// thread binary-searches its output's instance and decodes the tile from the rectangle.
+template <typename Out>
+__global__ __launch_bounds__(kBlock) void expand_kernel(
+    int64_t n_out, const uint32_t* __restrict__ offs, const uint32_t* __restrict__ ids,
+    const uint32_t* __restrict__ keys, int64_t m, const Rect* __restrict__ rects, int ntx, int tnb,
+    int64_t n_per_cam, int spans, Out out) {
+    __shared__ uint32_t s_off[kExpandPerBlock];
+    __shared__ uint32_t s_id[kExpandPerBlock];
+    __shared__ uint32_t s_dep[kExpandPerBlock];
+    __shared__ Rect s_r[kExpandPerBlock];
+    __shared__ int64_t s_range[2];
+    const int64_t o0 = (int64_t)blockIdx.x * kExpandPerBlock;
+    const int64_t o_end = min(n_out, o0 + kExpandPerBlock);
+    if (threadIdx.x < 2) {
+        const int64_t x = threadIdx.x == 0 ? o0 : o_end - 1;
+        int64_t lo = 0, hi = m - 1;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if ((int64_t)offs[mid] <= x) lo = mid; else hi = mid - 1;
+        }
+        s_range[threadIdx.x] = lo;
+    }
+    __syncthreads();
+    const int64_t p_lo = s_range[0];
+    const int cnt = (int)min<int64_t>(s_range[1] - p_lo + 1, kExpandPerBlock);
+    for (int e = threadIdx.x; e < cnt; e += kBlock) {
+        const int64_t p = p_lo + e;
+        const uint32_t v = ids[p];
+        s_off[e] = offs[p];
+        s_id[e] = v;
+        s_dep[e] = keys[p];
+        s_r[e] = rects[v];
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < kExpandPerBlock; q += kBlock) {
+        const int64_t o = o0 + q;
+        if (o >= o_end) break;
+        int lo = 0, hi = cnt - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if ((int64_t)s_off[mid] <= o) lo = mid; else hi = mid - 1;
+        }
+        const uint32_t l = (uint32_t)(o - (int64_t)s_off[lo]);
+        const uint32_t v = s_id[lo];
+        const Rect r = s_r[lo];
+        const uint32_t wx = (uint32_t)(r.x1 - r.x0);
+        const uint32_t yy = l / wx;
+        const uint32_t tile = (r.y0 + yy) * (uint32_t)ntx + (r.x0 + (l - yy * wx));
+        const uint32_t inst = v / (uint32_t)spans;
+        const uint32_t cid = n_per_cam > 0 ? (uint32_t)(inst / (uint64_t)n_per_cam) : 0u;
+        out.put(o, (cid << tnb) | tile, v, s_dep[lo], spans);
+    }
+}
+
+// isect_offset_encode_kernel (tiling_common.cu:25-71); writes are clamped to the offsets array.
+__global__ __launch_bounds__(kBlock) void offset_encode_kernel(const int64_t* __restrict__ ids, int64_t n,
+                                                               int n_tiles, int tnb, int64_t total,
+                                                               int32_t* __restrict__ offsets) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const int64_t tmask = (1ll << tnb) - 1;
+    const int64_t cur = ids[i] >> 32;
+    const int64_t id_cur = (cur >> tnb) * n_tiles + (cur & tmask);
+    if (i == 0)
+        for (int64_t t = 0; t < id_cur + 1 && t < total; ++t) offsets[t] = 0;
+    if (i == n - 1)
+        for (int64_t t = max<int64_t>(id_cur + 1, 0); t < total; ++t) offsets[t] = (int32_t)n;
+    if (i > 0) {
+        const int64_t prev = ids[i - 1] >> 32;
+        if (prev == cur) return;
+        const int64_t id_prev = (prev >> tnb) * n_tiles + (prev & tmask);
+        for (int64_t t = max<int64_t>(id_prev + 1, 0); t < id_cur + 1 && t < total; ++t) offsets[t] = (int32_t)i;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// mask_radii_kernel / mask_radii_packed_kernel (mask_radii.cu:10-58)
+__global__ __launch_bounds__(kBlock) void mask_radii_kernel(int64_t n, const uint8_t* __restrict__ mask,
+                                                            const uint32_t* __restrict__ packed,
+                                                            float2* __restrict__ radii) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    const bool keep = packed ? ((packed[i / 32] & (1u << (i % 32))) != 0) : (mask[i] != 0);
+    if (!keep) radii[i] = make_float2(0.f, 0.f);
+}
+
+int tile_n_bits_of(int n_tiles) {  // regular_tiling.cu:96-97
+    return (int)floorf(log2f((float)n_tiles)) + 1;
+}
+
+int geometry_of(const xsg_isect_desc* d, Geometry& g) {
+    if (!d) return xsg_fail(XSG_ERR_INVALID, "null isect descriptor");
+    if (d->n < 0 || d->n_cams < 1 || d->tile_w <= 0 || d->tile_h <= 0)
+        return xsg_fail(XSG_ERR_INVALID, "invalid isect descriptor (n=%lld cams=%d tile=%dx%d)",
+                        (long long)d->n, d->n_cams, d->tile_w, d->tile_h);
+    g.kind = d->kind;
+    g.n_cams = d->n_cams;
+    g.n = d->n;
+    g.spans = 1;
+    switch (d->kind) {
+        case XSG_TILING_REGULAR: {
+            const int w = (int)d->img_width, h = (int)d->img_height;
+            g.ntx = (w + d->tile_w - 1) / d->tile_w;
+            g.nty = (h + d->tile_h - 1) / d->tile_h;
+            break;
+        }
+        case XSG_TILING_LIDAR:
+            if (d->n_cams != 1) return xsg_fail(XSG_ERR_UNSUPPORTED, "lidar tiling takes one camera");
+            if (!d->elev_boundaries || d->n_elev <= 0)
+                return xsg_fail(XSG_ERR_INVALID, "lidar tiling needs elevation boundaries");
+            g.ntx = ((int)d->img_width + d->tile_w - 1) / d->tile_w;
+            g.nty = d->n_elev;
+            g.spans = 2;
+            break;
+        case XSG_TILING_SPHERICAL:
+            if (d->n_cams != 1) return xsg_fail(XSG_ERR_UNSUPPORTED, "spherical tiling takes one camera");
+            g.ntx = (int)ceilf(d->img_width / (float)d->tile_w);
+            g.nty = (int)ceilf(d->img_height / (float)d->tile_h);
+            g.spans = 2;
+            break;
+        default: return xsg_fail(XSG_ERR_INVALID, "unknown tiling kind %d", d->kind);
+    }
+    if (g.ntx <= 0 || g.nty <= 0 || g.ntx > 65535 || g.nty > 65535)
+        return xsg_fail(XSG_ERR_INVALID, "tile grid %d x %d out of range", g.ntx, g.nty);
+    g.n_tiles = g.ntx * g.nty;
+    g.tnb = tile_n_bits_of(g.n_tiles);
+    g.cam_bits = 0;
+    while ((1 << g.cam_bits) < d->n_cams) ++g.cam_bits;
+    if (g.tnb + g.cam_bits > 31) return xsg_fail(XSG_ERR_INVALID, "too many tiles / cameras for 64-bit keys");
+    if (g.n * g.n_cams * g.spans >= (1ll << 31)) return xsg_fail(XSG_ERR_INVALID, "too many Gaussians");
+    return XSG_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
+struct CountWs {
+    Rect* rects; uint32_t* vcnt; uint32_t* vkey; uint64_t* partials;
+    uint32_t* comp_id; uint32_t* comp_off; uint32_t* comp_key;
+    int64_t n_virtual; unsigned nb;
+    size_t bytes;
+};
+
+CountWs count_ws_layout(const Geometry& g, void* base) {
+    CountWs w;
+    w.n_virtual = g.n * g.n_cams * g.spans;
+    const int64_t nv = w.n_virtual;
+    w.nb = sort_blocks(nv > 0 ? nv : 1);
+    char* p = (char*)base;
+    size_t off = 0;
+    w.rects = (Rect*)(p + off); off += align256(sizeof(Rect) * nv);
+    w.vcnt = (uint32_t*)(p + off); off += align256(4 * nv);
+    w.vkey = (uint32_t*)(p + off); off += align256(4 * nv);
+    w.partials = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * (w.nb + 1));
+    w.comp_id = (uint32_t*)(p + off); off += align256(4 * nv);
+    w.comp_off = (uint32_t*)(p + off); off += align256(4 * nv);
+    w.comp_key = (uint32_t*)(p + off); off += align256(4 * nv);
+    w.bytes = off;
+    return w;
+}
+
+struct FillWs {
+    uint32_t* alt_key; uint32_t* alt_id;                              // depth sort ping-pong [m]
+    uint32_t* soffs; uint32_t* spart;                                 // offsets in depth order
+    uint32_t* hi_a; uint32_t* id_a; uint32_t* hi_b; uint32_t* id_b;  // tile sort [n_isects]
+    uint32_t* hist; uint32_t* dtot;
+    size_t bytes;
+};
+
+FillWs fill_ws_layout(int64_t m, int64_t n_isects, void* base) {
+    char* p = (char*)base;
+    FillWs w;
+    size_t off = 0;
+    const unsigned nb_m = sort_blocks(m > 0 ? m : 1), nb_i = sort_blocks(n_isects > 0 ? n_isects : 1);
+    const unsigned nb_h = max(nb_m, nb_i);
+    w.alt_key = (uint32_t*)(p + off); off += align256(4 * m);
+    w.alt_id = (uint32_t*)(p + off); off += align256(4 * m);
+    w.soffs = (uint32_t*)(p + off); off += align256(4 * m);
+    w.spart = (uint32_t*)(p + off); off += align256(4 * ((size_t)nb_m + 1));
+    w.hi_a = (uint32_t*)(p + off); off += align256(4 * n_isects);
+    w.id_a = (uint32_t*)(p + off); off += align256(4 * n_isects);
+    w.hi_b = (uint32_t*)(p + off); off += align256(4 * n_isects);
+    w.id_b = (uint32_t*)(p + off); off += align256(4 * n_isects);
+    w.hist = (uint32_t*)(p + off); off += align256(4 * (size_t)kRadix * nb_h);
+    w.dtot = (uint32_t*)(p + off); off += align256(4 * kRadix);
+    w.bytes = off;
+    return w;
+}
+
+}  // namespace
+
+extern "C" int xsg_isect_geometry(const xsg_isect_desc* d, int* ntw, int* nth, int* tnb, int* bits_above) {
+    Geometry g;
+    const int rc = geometry_of(d, g);
+    if (rc) return rc;
+    if (ntw) *ntw = g.ntx;
+    if (nth) *nth = g.nty;
+    if (tnb) *tnb = g.tnb;
+    if (bits_above) *bits_above = g.tnb + g.cam_bits;
+    return XSG_OK;
+}
+
+extern "C" size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d) {
+    Geometry g;
+    if (geometry_of(d, g)) return 0;
+    return count_ws_layout(g, nullptr).bytes;
+}
+
+extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* workspace, int64_t* n_isects,
+                               int64_t* n_visible, xsg_stream_t stream) {
+    Geometry g;
+    int rc = geometry_of(d, g);
+    if (rc) return rc;
+    const int64_t nt = g.n * g.n_cams;
+    if (n_isects) *n_isects = 0;
+    if (n_visible) *n_visible = 0;
+    if (nt == 0) return XSG_OK;
+    if (!workspace || !tpg || !d->means2d || !d->radii || !d->depths)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_isect_count: null pointer");
+    const hipStream_t s = (hipStream_t)stream;
+    const CountWs w = count_ws_layout(g, workspace);
+    if (g.kind == XSG_TILING_REGULAR) {
+        count_regular_kernel<<<w.nb, kBlock, 0, s>>>(nt, (const float2*)d->means2d, (const float2*)d->radii,
+                                                     d->depths, (float)d->tile_w, (float)d->tile_h, g.ntx,
+                                                     g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials);
+    } else {
+        if (!d->camera_pack || !d->flags || !d->points || !d->scales || !d->quats)
+            return xsg_fail(XSG_ERR_INVALID, "lidar / spherical tiling needs camera and Gaussian tensors");
+        const UtWeights ut = xsg_ut_weights(d->ut_alpha, d->ut_beta, d->ut_kappa);
+        const f2 img = mk2(d->img_width, d->img_height);
+        const float u_per_tile = (float)d->tile_w / d->img_width;
+        const float v_per_tile = (float)d->tile_h / d->img_height;
+        if (g.kind == XSG_TILING_LIDAR) {
+            count_spherical_kernel<XSG_CAM_LIDAR, true><<<w.nb, kBlock, 0, s>>>(
+                nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
+                d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
+                d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey,
+                w.partials);
+        } else {
+            count_spherical_kernel<XSG_CAM_SPHERICAL, false><<<w.nb, kBlock, 0, s>>>(
+                nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
+                d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths, nullptr,
+                0, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials);
+        }
+    }
+    scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb);
+    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
+                                           w.comp_key);
+    XSG_TRY_LAUNCH("isect_count");
+    uint64_t total = 0;
+    if (hipMemcpyAsync(&total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return xsg_launch_status("isect_count readback");
+    const int64_t isects = (int64_t)(total & 0xffffffffull);
+    const int64_t vis = (int64_t)(total >> 32);
+    if (isects >= (1ll << 31)) return xsg_fail(XSG_ERR_INVALID, "intersection count overflows int32");
+    if (n_isects) *n_isects = isects;
+    if (n_visible) *n_visible = vis;
+    return XSG_OK;
+}
+
+extern "C" size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible) {
+    (void)d;
+    return fill_ws_layout(n_visible, n_isects, nullptr).bytes;
+}
+
+extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int sort,
+                              void* count_workspace, void* fill_workspace, int64_t* isect_ids,
+                              int32_t* flatten_ids, xsg_stream_t stream) {
+    Geometry g;
+    int rc = geometry_of(d, g);
+    if (rc) return rc;
+    if (n_isects == 0) return XSG_OK;
+    const CountWs cw = count_ws_layout(g, count_workspace);
+    if (n_isects < 0 || n_visible <= 0 || n_visible > cw.n_virtual || !count_workspace || !isect_ids ||
+        !flatten_ids)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: bad arguments");
+    const hipStream_t s = (hipStream_t)stream;
+    const int64_t m = n_visible;
+    const int64_t n_per_cam = g.n_cams > 1 ? g.n : 0;
+    const unsigned nb_expand = (unsigned)((n_isects + kExpandPerBlock - 1) / kExpandPerBlock);
+    if (!sort) {
+        expand_kernel<FinalOut><<<nb_expand, kBlock, 0, s>>>(n_isects, cw.comp_off, cw.comp_id, cw.comp_key, m,
+                                                             cw.rects, g.ntx, g.tnb, n_per_cam, g.spans,
+                                                             FinalOut{isect_ids, flatten_ids});
+        XSG_TRY_LAUNCH("isect_fill (unsorted)");
+        return XSG_OK;
+    }
+    if (!fill_workspace) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: null fill workspace");
+    const FillWs fw = fill_ws_layout(m, n_isects, fill_workspace);
+    // depth pre-order of the visible virtual instances: stable, 4 passes, result back in comp_*
+    radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>>(
+        cw.comp_key, cw.comp_id, fw.alt_key, fw.alt_id, m, 0, 32, fw.hist, fw.dtot,
+        PlainOut<uint32_t, uint32_t>{cw.comp_key, cw.comp_id}, s);
+    // intersection offsets of the instances in depth order
+    const unsigned nb_m = sort_blocks(m);
+    gather_reduce_kernel<<<nb_m, kBlock, 0, s>>>(m, cw.comp_id, cw.vcnt, fw.spart);
+    scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(fw.spart, nb_m);
+    gather_scan_kernel<<<nb_m, kBlock, 0, s>>>(m, cw.comp_id, cw.vcnt, fw.spart, fw.soffs);
+    // expansion into (tile bits, virtual instance) pairs
+    const int bits = g.tnb + g.cam_bits;
+    const uint32_t mask = (uint32_t)((1ull << bits) - 1);
+    expand_kernel<PairsOut><<<nb_expand, kBlock, 0, s>>>(n_isects, fw.soffs, cw.comp_id, cw.comp_key, m,
+                                                         cw.rects, g.ntx, g.tnb, n_per_cam, g.spans,
+                                                         PairsOut{fw.hi_a, fw.id_a, mask});
+    // stable sort on the tile bits; the last pass writes the final keys and ids
+    radix_sort_passes<uint32_t, uint32_t, SortedKeyOut>(fw.hi_a, fw.id_a, fw.hi_b, fw.id_b, n_isects, 0, bits,
+                                                        fw.hist, fw.dtot,
+                                                        SortedKeyOut{isect_ids, flatten_ids, cw.vkey, g.spans}, s);
+    XSG_TRY_LAUNCH("isect_fill");
+    return XSG_OK;
+}
+
+extern "C" int xsg_isect_offset_encode(const int64_t* isect_ids, int64_t n_isects, int n_tiles_w, int n_tiles_h,
+                                       int n_cams, int32_t* offsets, xsg_stream_t stream) {
+    if (n_tiles_w <= 0 || n_tiles_h <= 0 || n_cams < 1 || !offsets || n_isects < 0)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_isect_offset_encode: bad arguments");
+    const hipStream_t s = (hipStream_t)stream;
+    const int n_tiles = n_tiles_w * n_tiles_h;
+    const int64_t total = (int64_t)n_tiles * n_cams;
+    if (n_isects == 0) {  // tiling_common.cu:86-88
+        fill_i32_kernel<<<xsg_blocks(total, kBlock), kBlock, 0, s>>>(offsets, total, 0);
+    } else {
+        offset_encode_kernel<<<xsg_blocks(n_isects, kBlock), kBlock, 0, s>>>(isect_ids, n_isects, n_tiles,
+                                                                            tile_n_bits_of(n_tiles), total,
+                                                                            offsets);
+    }
+    XSG_TRY_LAUNCH("isect_offset_encode");
+    return XSG_OK;
+}
+
+extern "C" int xsg_mask_radii(int64_t n, const uint8_t* mask, float* radii, xsg_stream_t stream) {
+    if (n < 0 || (!mask && n) || (!radii && n)) return xsg_fail(XSG_ERR_INVALID, "xsg_mask_radii: bad arguments");
+    if (n == 0) return XSG_OK;
+    mask_radii_kernel<<<xsg_blocks(n, kBlock), kBlock, 0, (hipStream_t)stream>>>(n, mask, nullptr, (float2*)radii);
+    XSG_TRY_LAUNCH("mask_radii");
+    return XSG_OK;
+}
+
+extern "C" int xsg_mask_radii_packed(int64_t n, const uint32_t* packed, float* radii, xsg_stream_t stream) {
+    if (n < 0 || (!packed && n) || (!radii && n))
+        return xsg_fail(XSG_ERR_INVALID, "xsg_mask_radii_packed: bad arguments");
+    if (n == 0) return XSG_OK;
+    mask_radii_kernel<<<xsg_blocks(n, kBlock), kBlock, 0, (hipStream_t)stream>>>(n, nullptr, packed, (float2*)radii);
+    XSG_TRY_LAUNCH("mask_radii_packed");
+    return XSG_OK;
+}
+
+// ------------------------------------------------------------------ generic sort (C-ABI)
+extern "C" size_t xsg_radix_sort_workspace_bytes(int64_t n) {
+    return align256(4 * (size_t)kRadix * sort_blocks(n > 0 ? n : 1)) + align256(4 * kRadix);
+}
+
+extern "C" int xsg_radix_sort_pairs_u64_i32(int64_t* keys, int32_t* vals, int64_t* keys_alt, int32_t* vals_alt,
+                                            int64_t n, int begin_bit, int end_bit, void* workspace, int* selector,
+                                            xsg_stream_t stream) {
+    if (n < 0 || begin_bit < 0 || end_bit > 64 || begin_bit > end_bit || !selector)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_radix_sort_pairs_u64_i32: bad arguments");
+    *selector = 0;
+    if (n == 0 || begin_bit == end_bit) return XSG_OK;
+    if (!workspace || !keys || !vals || !keys_alt || !vals_alt)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_radix_sort_pairs_u64_i32: null pointer");
+    uint32_t* hist = (uint32_t*)workspace;
+    uint32_t* dtot = (uint32_t*)((char*)workspace + align256(4 * (size_t)kRadix * sort_blocks(n)));
+    using K = uint64_t;
+    using V = uint32_t;
+    K* k0 = (K*)keys; V* v0 = (V*)vals; K* k1 = (K*)keys_alt; V* v1 = (V*)vals_alt;
+    const int passes = (end_bit - begin_bit + 7) / 8;
+    const bool in_alt = (passes % 2) == 1;
+    PlainOut<K, V> fin{in_alt ? k1 : k0, in_alt ? v1 : v0};
+    radix_sort_passes<K, V, PlainOut<K, V>>(k0, v0, k1, v1, n, begin_bit, end_bit, hist, dtot, fin,
+                                            (hipStream_t)stream);
+    *selector = in_alt ? 1 : 0;
+    XSG_TRY_LAUNCH("radix_sort_pairs");
+    return XSG_OK;
+}

@@ -1,0 +1,695 @@
+// xsimgs_amd._C: the reference's pybind surface (xsimgs._C, csrc/ext.cpp:12-20) re-exported over the
+// xsimgs_amd C-ABI. This file validates and allocates exactly as the reference ops do, then calls
+// the HIP kernels through include/xsimgs_amd.h on the current stream of the input's device.
+#include <torch/extension.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "../../include/xsimgs_amd.h"
+
+namespace {
+
+using at::Tensor;
+using OptT = std::optional<Tensor>;
+
+void check_rc(int rc) {
+    if (rc != XSG_OK) throw std::runtime_error(xsg_last_error());
+}
+
+xsg_stream_t stream_of(const Tensor& t) {
+    TORCH_CHECK(t.is_cuda(), "xsimgs_amd ops take GPU tensors (got a tensor on ", t.device(), ")");
+    return reinterpret_cast<xsg_stream_t>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
+}
+
+const float* fptr(const Tensor& t) { return t.data_ptr<float>(); }
+const float* fptr(const OptT& t) { return t.has_value() ? t->data_ptr<float>() : nullptr; }
+
+void check_f32(const Tensor& t, const char* name) {
+    TORCH_CHECK(t.scalar_type() == at::kFloat, name, " must be a float32 tensor");
+}
+
+void check_same_device(const std::vector<Tensor>& ts) {  // toast check_same_device
+    for (size_t i = 1; i < ts.size(); ++i)
+        TORCH_CHECK(ts[i].device() == ts[0].device(), "All tensors must be on the same device");
+}
+
+void all_contiguous(const std::vector<Tensor>& ts) {  // toast all_contiguous
+    for (const auto& t : ts) TORCH_CHECK(t.is_contiguous(), "All tensors must be contiguous");
+}
+
+Tensor workspace(const Tensor& like, size_t bytes) {
+    return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
+}
+
+// ------------------------------------------------------------------ compositing
+std::vector<int> eval3d_supported_ndims() {
+    int dims[64];
+    const int n = xsg_eval3d_supported_ndims(dims, 64);
+    return std::vector<int>(dims, dims + n);
+}
+
+xsg_eval3d_args base_args(const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors,
+                          const Tensor& opac, int cdim, int width, int height, int tw, int th,
+                          const Tensor& ray_o, const Tensor& ray_d, const Tensor& offsets, const Tensor& flat) {
+    for (const Tensor* t : {&means, &quats, &scales, &opac, &ray_o, &ray_d}) check_f32(*t, "Gaussian / ray tensors");
+    TORCH_CHECK(offsets.scalar_type() == at::kInt && flat.scalar_type() == at::kInt,
+                "tile_offsets and flatten_ids must be int32");
+    all_contiguous({means, quats, scales, opac, ray_o, ray_d, offsets, flat});
+    if (colors.has_value()) { check_f32(*colors, "colors"); all_contiguous({*colors}); }
+    xsg_eval3d_args a{};
+    a.cdim = cdim;
+    a.n = means.numel() / 3;
+    a.n_cams = 1;
+    a.means = fptr(means); a.quats = fptr(quats); a.scales = fptr(scales);
+    a.colors = fptr(colors); a.opacities = fptr(opac);
+    a.ray_o = fptr(ray_o); a.ray_d = fptr(ray_d);
+    a.width = width; a.height = height; a.tile_w = tw; a.tile_h = th;
+    a.n_tiles_w = (int)offsets.size(-1);
+    a.n_tiles_h = (int)offsets.size(-2);
+    a.tile_offsets = offsets.data_ptr<int32_t>();
+    a.flatten_ids = flat.data_ptr<int32_t>();
+    a.n_isects = flat.numel();
+    return a;
+}
+
+// rasterize_eval3d_fwd (eval3d_fwd.cu:248-316) and its dynamic twin (eval3d_dynamic_fwd.cu:249-332)
+std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
+    const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
+    const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tsw, int64_t tsh,
+    const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta, const Tensor& tile_offsets,
+    const Tensor& flatten_ids) {
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(means.device());
+    auto opt = means.options();
+    const int64_t channels = colors.has_value() ? colors->size(-1) : 0;
+    Tensor renders = at::empty({image_height, image_width, channels}, opt);
+    Tensor depths = at::empty({image_height, image_width}, opt);
+    Tensor alphas = at::empty({image_height, image_width}, opt);
+    Tensor last_ids = at::empty({image_height, image_width}, opt.dtype(at::kInt));
+    xsg_eval3d_args a = base_args(means, quats, scales, colors, opacities, (int)channels, (int)image_width,
+                                  (int)image_height, (int)tsw, (int)tsh, ray_origs, ray_dirs, tile_offsets,
+                                  flatten_ids);
+    if (velocity.has_value()) { check_f32(*velocity, "velocity"); all_contiguous({*velocity}); }
+    if (ray_time_delta.has_value()) { check_f32(*ray_time_delta, "ray_time_delta"); all_contiguous({*ray_time_delta}); }
+    a.velocity = fptr(velocity);
+    a.ray_time_delta = fptr(ray_time_delta);
+    a.out_rgb = renders.data_ptr<float>(); a.out_depth = depths.data_ptr<float>();
+    a.out_alpha = alphas.data_ptr<float>(); a.out_last_ids = last_ids.data_ptr<int32_t>();
+    check_rc(xsg_eval3d_fwd(&a, stream_of(means)));
+    return {renders, depths, alphas, last_ids};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_fwd(
+    const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors, const Tensor& opacities,
+    int64_t image_width, int64_t image_height, int64_t tile_size_width, int64_t tile_size_height,
+    const Tensor& ray_origs, const Tensor& ray_dirs, const Tensor& tile_offsets, const Tensor& flatten_ids) {
+    return eval3d_fwd_impl(means, std::nullopt, quats, scales, colors, opacities, image_width, image_height,
+                           tile_size_width, tile_size_height, ray_origs, ray_dirs, std::nullopt, tile_offsets,
+                           flatten_ids);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_fwd(
+    const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
+    const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tile_size_width,
+    int64_t tile_size_height, const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta,
+    const Tensor& tile_offsets, const Tensor& flatten_ids) {
+    return eval3d_fwd_impl(means, velocity, quats, scales, colors, opacities, image_width, image_height,
+                           tile_size_width, tile_size_height, ray_origs, ray_dirs, ray_time_delta, tile_offsets,
+                           flatten_ids);
+}
+
+struct BwdOut {
+    Tensor v_points, v_velocity, v_quat, v_scale, v_opacity;
+    std::optional<Tensor> v_colors;
+    Tensor v_ray_o, v_ray_d, v_time_delta;
+};
+
+// rasterize_eval3d_bwd (eval3d_bwd.cu:297-403) / rasterize_eval3d_dynamic_bwd (eval3d_dynamic_bwd.cu:312-427)
+BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor& scale, const Tensor& quat,
+                       const Tensor& opacity, const OptT& colors, const Tensor& ray_origins,
+                       const Tensor& ray_directions, const OptT& ray_time_delta, int64_t tile_size_x,
+                       int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
+                       const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors,
+                       const Tensor& v_render_depth, const Tensor& v_render_alpha) {
+    if (v_render_colors.has_value() && !v_render_colors->is_contiguous())
+        throw std::runtime_error("v_render_colors must be contiguous");
+    all_contiguous({v_render_depth, v_render_alpha, render_alpha, last_ids});
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(points.device());
+    const int64_t width = ray_origins.size(1), height = ray_origins.size(0);
+    BwdOut o;
+    o.v_points = at::zeros_like(points);
+    o.v_scale = at::empty_like(scale);
+    o.v_quat = at::empty_like(quat);
+    o.v_opacity = at::zeros_like(opacity);
+    int cdim = 0;
+    if (colors.has_value()) {
+        o.v_colors = at::zeros_like(*colors);
+        cdim = (int)colors->size(1);
+    }
+    o.v_ray_o = at::empty_like(ray_origins);
+    o.v_ray_d = at::empty_like(ray_directions);
+    xsg_eval3d_args a = base_args(points, quat, scale, colors, opacity, cdim, (int)width, (int)height,
+                                  (int)tile_size_x, (int)tile_size_y, ray_origins, ray_directions, tile_offsets,
+                                  flatten_ids);
+    if (velocity.has_value()) {
+        check_f32(*velocity, "velocity");
+        all_contiguous({*velocity, *ray_time_delta});
+        o.v_velocity = at::zeros_like(*velocity);
+        o.v_time_delta = at::empty_like(*ray_time_delta);
+        a.velocity = fptr(velocity);
+        a.ray_time_delta = fptr(ray_time_delta);
+        a.v_velocity = o.v_velocity.data_ptr<float>();
+        a.v_time_delta = o.v_time_delta.data_ptr<float>();
+    }
+    a.render_alpha = fptr(render_alpha);
+    a.last_ids = last_ids.data_ptr<int32_t>();
+    a.v_rgb = fptr(v_render_colors);
+    a.v_depth = fptr(v_render_depth);
+    a.v_alpha = fptr(v_render_alpha);
+    a.v_means = o.v_points.data_ptr<float>();
+    a.v_quats = o.v_quat.data_ptr<float>();
+    a.v_scales = o.v_scale.data_ptr<float>();
+    a.v_opacities = o.v_opacity.data_ptr<float>();
+    a.v_colors = o.v_colors.has_value() ? o.v_colors->data_ptr<float>() : nullptr;
+    a.v_ray_o = o.v_ray_o.data_ptr<float>();
+    a.v_ray_d = o.v_ray_d.data_ptr<float>();
+    Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(a.n, cdim));
+    check_rc(xsg_eval3d_bwd(&a, ws.data_ptr(), stream_of(points)));
+    return o;
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, Tensor, Tensor> rasterize_eval3d_bwd(
+    const Tensor& points, const Tensor& scale, const Tensor& quat, const Tensor& opacity, const OptT& colors,
+    const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
+    const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
+    const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha) {
+    BwdOut o = eval3d_bwd_impl(points, std::nullopt, scale, quat, opacity, colors, ray_origins, ray_directions,
+                               std::nullopt, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha);
+    return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_bwd(
+    const Tensor& points, const Tensor& velocity, const Tensor& scale, const Tensor& quat, const Tensor& opacity,
+    const OptT& colors, const Tensor& ray_origins, const Tensor& ray_directions, const Tensor& ray_time_delta,
+    int64_t tile_size_x, int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
+    const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors, const Tensor& v_render_depth,
+    const Tensor& v_render_alpha) {
+    BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
+                               ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha);
+    return {o.v_points, o.v_velocity, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
+            o.v_time_delta};
+}
+
+// ------------------------------------------------------------------ spherical harmonics
+void sh_checks(int64_t degree, const Tensor& origin, const Tensor& positions, const Tensor& coeffs, const OptT& mask,
+               bool layout_3kn, const OptT& coeffs_dc, int64_t& N, int64_t& dim) {
+    std::vector<Tensor> ts{origin, positions, coeffs};
+    if (coeffs_dc.has_value()) ts.push_back(*coeffs_dc);
+    if (mask.has_value()) ts.push_back(*mask);
+    check_same_device(ts);
+    all_contiguous(ts);
+    N = layout_3kn ? coeffs.size(2) : coeffs.size(0);
+    dim = coeffs.size(1);
+    TORCH_CHECK(coeffs.size(layout_3kn ? 0 : 2) == 3,
+                "coeffs tensor must be [3, K, N] if layout_3kn else [N, K, 3]");
+    if (degree < 0 || degree > 4)
+        throw std::runtime_error("Unsupported spherical harmonics degree: " + std::to_string(degree));
+    static const int64_t ref_dims[5] = {1, 4, 9, 16, 25};
+    const bool has_dc = coeffs_dc.has_value();
+    const int64_t required = ref_dims[degree] - (has_dc ? 1 : 0);
+    TORCH_CHECK(dim >= required, "Number of harmonics band in coeffs tensor must be higher or equal than ",
+                required, " for degree_to_use=", degree, has_dc ? " (zero-degree coeffs passed separately)" : "");
+    if (has_dc) {
+        const auto dc_dim = coeffs_dc->dim();
+        TORCH_CHECK(dc_dim == 2 || dc_dim == 3, "coeffs_dc must be 2D or 3D");
+        const int64_t ch_axis = layout_3kn ? 0 : dc_dim - 1;
+        const int64_t n_axis = layout_3kn ? dc_dim - 1 : 0;
+        TORCH_CHECK(coeffs_dc->size(ch_axis) == 3 && coeffs_dc->size(n_axis) == N && coeffs_dc->numel() == 3 * N,
+                    "coeffs_dc must hold a single SH band: [N, 3] or [N, 1, 3] if "
+                    "!layout_3kn else [3, N] or [3, 1, N]");
+    }
+}
+
+// spherical_harmonics_fused_fwd (sh_fwd.cu:162-259)
+Tensor spherical_harmonics_fused_fwd(int64_t degree_to_use, const Tensor& origin, const Tensor& positions,
+                                     const Tensor& coeffs, const OptT& mask, bool layout_3kn, const OptT& coeffs_dc,
+                                     const OptT& output) {
+    int64_t N, dim;
+    sh_checks(degree_to_use, origin, positions, coeffs, mask, layout_3kn, coeffs_dc, N, dim);
+    if (output.has_value()) { check_same_device({origin, *output}); all_contiguous({*output}); }
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(positions.device());
+    Tensor out = output.has_value() ? *output : at::zeros({N, 3}, positions.options());
+    check_rc(xsg_sh_fwd((int)degree_to_use, fptr(origin), N, (int)dim, fptr(positions), fptr(coeffs), fptr(coeffs_dc),
+                        mask.has_value() ? (const uint32_t*)mask->data_ptr() : nullptr, layout_3kn ? 1 : 0,
+                        out.data_ptr<float>(), stream_of(positions)));
+    return out;
+}
+
+// spherical_harmonics_fused_bwd (sh_bwd.cu:317-390)
+std::tuple<Tensor, Tensor, Tensor, Tensor> spherical_harmonics_fused_bwd(int64_t degree_to_use, const Tensor& origin,
+                                                                       const Tensor& positions, const Tensor& coeffs,
+                                                                       const OptT& mask, bool layout_3kn,
+                                                                       const Tensor& d_output, const OptT& coeffs_dc) {
+    all_contiguous({d_output});
+    int64_t N, dim;
+    sh_checks(degree_to_use, origin, positions, coeffs, mask, layout_3kn, coeffs_dc, N, dim);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(positions.device());
+    const bool has_dc = coeffs_dc.has_value();
+    Tensor d_coeffs = at::empty_like(coeffs);
+    Tensor d_dc = has_dc ? at::empty_like(*coeffs_dc) : at::empty({0}, coeffs.options());
+    Tensor d_pos = at::empty_like(positions);
+    Tensor d_origin = at::empty({3}, origin.options());
+    Tensor ws = workspace(positions, xsg_sh_bwd_workspace_bytes(N));
+    check_rc(xsg_sh_bwd((int)degree_to_use, fptr(origin), N, (int)dim, fptr(positions), fptr(coeffs),
+                        mask.has_value() ? (const uint32_t*)mask->data_ptr() : nullptr, layout_3kn ? 1 : 0,
+                        fptr(d_output), has_dc ? 1 : 0, d_coeffs.data_ptr<float>(),
+                        has_dc ? d_dc.data_ptr<float>() : nullptr, d_pos.data_ptr<float>(),
+                        d_origin.data_ptr<float>(), ws.data_ptr(), stream_of(positions)));
+    return {d_coeffs, d_dc, d_pos, d_origin};
+}
+
+// ------------------------------------------------------------------ binning
+std::tuple<Tensor, Tensor, Tensor> isect_run(xsg_isect_desc& d, const Tensor& like, bool sort) {
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(like.device());
+    const xsg_stream_t s = stream_of(like);
+    Tensor tiles_per_gauss = at::empty({d.n * d.n_cams}, like.options().dtype(at::kInt));
+    Tensor cws = workspace(like, xsg_isect_count_workspace_bytes(&d));
+    int64_t n_isects = 0, n_visible = 0;
+    check_rc(xsg_isect_count(&d, tiles_per_gauss.data_ptr<int32_t>(), cws.data_ptr(), &n_isects, &n_visible, s));
+    Tensor isect_ids = at::empty({n_isects}, like.options().dtype(at::kLong));
+    Tensor flatten_ids = at::empty({n_isects}, like.options().dtype(at::kInt));
+    if (n_isects > 0) {
+        Tensor fws = workspace(like, sort ? xsg_isect_fill_workspace_bytes(&d, n_isects, n_visible) : 1);
+        check_rc(xsg_isect_fill(&d, n_isects, n_visible, sort ? 1 : 0, cws.data_ptr(), fws.data_ptr(),
+                                isect_ids.data_ptr<int64_t>(), flatten_ids.data_ptr<int32_t>(), s));
+    }
+    return {tiles_per_gauss, isect_ids, flatten_ids};
+}
+
+// isect_regular_tiles (regular_tiling.cu:72-146)
+std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles(const Tensor& means2d, const Tensor& radii, const Tensor& depths,
+                                                       int64_t img_width, int64_t img_height, int64_t tile_size_x,
+                                                       int64_t tile_size_y, bool sort, bool double_buffer) {
+    (void)double_buffer;  // memory strategy only; results are identical
+    check_same_device({means2d, radii, depths});
+    all_contiguous({means2d, radii, depths});
+    xsg_isect_desc d{};
+    d.kind = XSG_TILING_REGULAR;
+    d.n_cams = 1;
+    d.n = means2d.numel() / 2;
+    d.means2d = fptr(means2d); d.radii = fptr(radii); d.depths = fptr(depths);
+    d.img_width = (float)img_width; d.img_height = (float)img_height;
+    d.tile_w = (int)tile_size_x; d.tile_h = (int)tile_size_y;
+    auto r = isect_run(d, depths, sort);
+    std::get<0>(r) = std::get<0>(r).view(depths.sizes());
+    return r;
+}
+
+// isect_regular_tiles over [C, N] projections of C cameras sharing one scene: keys carry the camera id
+// above the tile bits and flatten ids are cam * N + gaussian (extension for batched camera rigs).
+std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles_batched(const Tensor& means2d, const Tensor& radii,
+                                                               const Tensor& depths, int64_t img_width,
+                                                               int64_t img_height, int64_t tile_size_x,
+                                                               int64_t tile_size_y, bool sort) {
+    check_same_device({means2d, radii, depths});
+    all_contiguous({means2d, radii, depths});
+    TORCH_CHECK(depths.dim() == 2, "batched tiling takes [C, N] depths");
+    xsg_isect_desc d{};
+    d.kind = XSG_TILING_REGULAR;
+    d.n_cams = (int)depths.size(0);
+    d.n = depths.size(1);
+    d.means2d = fptr(means2d); d.radii = fptr(radii); d.depths = fptr(depths);
+    d.img_width = (float)img_width; d.img_height = (float)img_height;
+    d.tile_w = (int)tile_size_x; d.tile_h = (int)tile_size_y;
+    auto r = isect_run(d, depths, sort);
+    std::get<0>(r) = std::get<0>(r).view(depths.sizes());
+    return r;
+}
+
+std::tuple<Tensor, Tensor, Tensor> isect_seam_tiles(int kind, const Tensor& camera_pack, const Tensor& points,
+                                                    const OptT& points_velocity, const Tensor& scale, const Tensor& quat,
+                                                    const OptT& opacity, const Tensor& flag, const Tensor& means2d,
+                                                    const Tensor& radii, const Tensor& depths, const OptT& elev,
+                                                    int64_t tile_size_x, int64_t tile_size_y, double img_width,
+                                                    double img_height, double ut_alpha, double ut_beta,
+                                                    double ut_kappa, bool sort) {
+    TORCH_CHECK(camera_pack.is_cuda(), "camera_pack must be CUDA tensor")
+    std::vector<Tensor> ts{camera_pack, points, points_velocity.value_or(points), scale, quat, flag, means2d,
+                           radii, depths};
+    if (elev.has_value()) ts.push_back(*elev);
+    check_same_device(ts);
+    all_contiguous(ts);
+    xsg_isect_desc d{};
+    d.kind = kind;
+    d.n_cams = 1;
+    d.n = means2d.numel() / 2;
+    d.means2d = fptr(means2d); d.radii = fptr(radii); d.depths = fptr(depths);
+    d.flags = flag.data_ptr<uint8_t>();
+    d.camera_pack = fptr(camera_pack);
+    d.points = fptr(points); d.velocity = fptr(points_velocity); d.scales = fptr(scale);
+    d.quats = fptr(quat); d.opacity = fptr(opacity);
+    d.elev_boundaries = elev.has_value() ? fptr(*elev) : nullptr;
+    d.n_elev = elev.has_value() ? (int)elev->size(0) : 0;
+    d.img_width = (float)img_width; d.img_height = (float)img_height;
+    d.tile_w = (int)tile_size_x; d.tile_h = (int)tile_size_y;
+    d.ut_alpha = (float)ut_alpha; d.ut_beta = (float)ut_beta; d.ut_kappa = (float)ut_kappa;
+    auto r = isect_run(d, depths, sort);
+    std::get<0>(r) = std::get<0>(r).view(depths.sizes());
+    return r;
+}
+
+// isect_lidar_tiles (phm_lidar_tiling.cu:239-375)
+std::tuple<Tensor, Tensor, Tensor> isect_lidar_tiles(const Tensor& camera_pack, const Tensor& points,
+                                                     const OptT& points_velocity, const Tensor& scale,
+                                                     const Tensor& quat, const OptT& opacity, const Tensor& flag,
+                                                     const Tensor& means2d, const Tensor& radii, const Tensor& depths,
+                                                     const Tensor& elev_boundaries, int64_t tile_size_x,
+                                                     double img_width, double img_height, double ut_alpha,
+                                                     double ut_beta, double ut_kappa, bool sort, bool double_buffer) {
+    (void)double_buffer;
+    return isect_seam_tiles(XSG_TILING_LIDAR, camera_pack, points, points_velocity, scale, quat, opacity, flag,
+                            means2d, radii, depths, elev_boundaries, tile_size_x, 1, img_width, img_height, ut_alpha,
+                            ut_beta, ut_kappa, sort);
+}
+
+// isect_spherical_tiles (phm_spherical_tiling.cu:179-314)
+std::tuple<Tensor, Tensor, Tensor> isect_spherical_tiles(const Tensor& camera_pack, const Tensor& points,
+                                                         const OptT& points_velocity, const Tensor& scale,
+                                                         const Tensor& quat, const OptT& opacity, const Tensor& flag,
+                                                         const Tensor& means2d, const Tensor& radii,
+                                                         const Tensor& depths, int64_t tile_size_x,
+                                                         int64_t tile_size_y, double img_width, double img_height,
+                                                         double ut_alpha, double ut_beta, double ut_kappa, bool sort,
+                                                         bool double_buffer) {
+    (void)double_buffer;
+    return isect_seam_tiles(XSG_TILING_SPHERICAL, camera_pack, points, points_velocity, scale, quat, opacity, flag,
+                            means2d, radii, depths, std::nullopt, tile_size_x, tile_size_y, img_width, img_height,
+                            ut_alpha, ut_beta, ut_kappa, sort);
+}
+
+// isect_offset_encode (tiling_common.cu:73-99); n_cams > 1 gives [n_cams, th, tw] (batched rigs)
+Tensor isect_offset_encode(const Tensor& isect_ids, int64_t tile_width, int64_t tile_height, int64_t n_cams) {
+    TORCH_CHECK(isect_ids.is_cuda() && isect_ids.is_contiguous(), "isect_ids must be contiguous cuda tensor")
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(isect_ids.device());
+    const int64_t n = isect_ids.size(0);
+    std::vector<int64_t> shape = {tile_height, tile_width};
+    if (n_cams > 1) shape.insert(shape.begin(), n_cams);
+    Tensor offsets = at::empty(shape, isect_ids.options().dtype(at::kInt));
+    check_rc(xsg_isect_offset_encode(isect_ids.data_ptr<int64_t>(), n, (int)tile_width, (int)tile_height, (int)n_cams,
+                                     offsets.data_ptr<int32_t>(), stream_of(isect_ids)));
+    return offsets;
+}
+
+// mask_radii / mask_radii_packed (mask_radii.cu:60-88), in place
+void mask_radii(const Tensor& mask, const Tensor& radii) {
+    if (radii.size(-1) != 2) throw std::runtime_error("radii must be [..., 2] tensor");
+    TORCH_CHECK(mask.dtype() == at::kBool, "Mask must be torch.bool tensor");
+    const int64_t N = radii.numel() / 2;
+    TORCH_CHECK(mask.numel() == N, "Mask size mismatch with radii");
+    check_same_device({mask, radii});
+    all_contiguous({mask, radii});
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(radii.device());
+    check_rc(xsg_mask_radii(N, (const uint8_t*)mask.data_ptr(), radii.data_ptr<float>(), stream_of(radii)));
+}
+
+void mask_radii_packed(const Tensor& packed_mask, const Tensor& radii) {
+    if (radii.size(-1) != 2) throw std::runtime_error("radii must be [..., 2] tensor");
+    TORCH_CHECK(packed_mask.dtype() == at::kUInt32, "Packed mask must be UInt32 tensor");
+    const int64_t N = radii.numel() / 2;
+    TORCH_CHECK(packed_mask.numel() * 32 >= N, "Packed mask size mismatch with radii");
+    check_same_device({packed_mask, radii});
+    all_contiguous({packed_mask, radii});
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(radii.device());
+    check_rc(xsg_mask_radii_packed(N, (const uint32_t*)packed_mask.data_ptr(), radii.data_ptr<float>(),
+                                   stream_of(radii)));
+}
+
+// generic stable radix sort (sort_intersections' cub::DeviceRadixSort::SortPairs)
+std::tuple<Tensor, Tensor> radix_sort_pairs(const Tensor& keys, const Tensor& values, int64_t begin_bit,
+                                            int64_t end_bit) {
+    TORCH_CHECK(keys.scalar_type() == at::kLong && values.scalar_type() == at::kInt, "keys int64, values int32");
+    all_contiguous({keys, values});
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(keys.device());
+    const int64_t n = keys.numel();
+    Tensor k0 = keys.clone(), v0 = values.clone();
+    Tensor k1 = at::empty_like(keys), v1 = at::empty_like(values);
+    Tensor ws = workspace(keys, xsg_radix_sort_workspace_bytes(n));
+    int sel = 0;
+    check_rc(xsg_radix_sort_pairs_u64_i32(k0.data_ptr<int64_t>(), v0.data_ptr<int32_t>(), k1.data_ptr<int64_t>(),
+                                          v1.data_ptr<int32_t>(), n, (int)begin_bit, (int)end_bit, ws.data_ptr(),
+                                          &sel, stream_of(keys)));
+    return sel ? std::make_tuple(k1, v1) : std::make_tuple(k0, v0);
+}
+
+// ------------------------------------------------------------------ cameras
+struct CamSpec {
+    int kind;
+    std::vector<int> impl_dims;
+};
+
+// pack_camera (include/cameras/pack_kernels.h:11-47): validated, then concatenated into the flat
+// layout the kernels read. torch.cat keeps the pack differentiable w.r.t. the camera tensors.
+Tensor camera_pack(const CamSpec& spec, const std::vector<Tensor>& tensors) {
+    static const int base_dims[7] = {4, 3, 3, 3, 2, 1, 1};
+    const size_t expected = 7 + spec.impl_dims.size();
+    if (tensors.size() != expected)
+        throw std::runtime_error("Tensor list size mismatch. Expected " + std::to_string(expected) +
+                                 ", but found: " + std::to_string(tensors.size()));
+    check_same_device(tensors);
+    std::vector<Tensor> flat;
+    for (size_t i = 0; i < tensors.size(); ++i) {
+        TORCH_CHECK(tensors[i].scalar_type() == at::kFloat, "Camera tensors must be float32");
+        const int want = i < 7 ? base_dims[i] : spec.impl_dims[i - 7];
+        TORCH_CHECK(tensors[i].numel() == want, "Only single camera is currently supported (tensor ", i,
+                    " has ", tensors[i].numel(), " elements, expected ", want, ")");
+        flat.push_back(tensors[i].reshape({1, want}));
+    }
+    return at::cat(flat, 1).contiguous();
+}
+
+void validate_pack(const CamSpec& spec, const Tensor& pack) {  // camera.h:56-62
+    TORCH_CHECK(pack.numel() == xsg_camera_pack_elements(spec.kind), "Only single camera is currently supported");
+    TORCH_CHECK(pack.dtype() == at::kFloat, "Camera type must be float32");
+    TORCH_CHECK(pack.is_contiguous(), "Camera pack must be contiguous tensor");
+    TORCH_CHECK(pack.is_cuda(), "Camera pack must be on the GPU");
+}
+
+py::object camera_rays(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool world_space,
+                       bool normalized, bool return_origins, bool return_valid) {
+    validate_pack(spec, pack);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+    auto opt = pack.options();
+    Tensor ray_o = return_origins ? at::empty({height, width, 3}, opt) : Tensor();
+    Tensor ray_d = at::empty({height, width, 3}, opt);
+    Tensor valid = return_valid ? at::empty({height, width}, opt.dtype(at::kBool)) : Tensor();
+    check_rc(xsg_camera_rays(spec.kind, fptr(pack.detach()), (int)width, (int)height, world_space ? 1 : 0,
+                             normalized ? 1 : 0, return_origins ? ray_o.data_ptr<float>() : nullptr,
+                             ray_d.data_ptr<float>(), return_valid ? (uint8_t*)valid.data_ptr() : nullptr,
+                             stream_of(pack)));
+    py::list out;
+    out.append(return_origins ? py::cast(ray_o) : py::none());
+    out.append(py::cast(ray_d));
+    if (return_valid) out.append(py::cast(valid));
+    return out;
+}
+
+Tensor pixel_time(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool delta) {
+    validate_pack(spec, pack);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+    Tensor out = at::empty({height, width}, pack.options());
+    check_rc(xsg_pixel_time(spec.kind, fptr(pack), (int)width, (int)height, nullptr, 0, delta ? 1 : 0,
+                            out.data_ptr<float>(), stream_of(pack)));
+    return out;
+}
+
+Tensor pixel_time_uv(const CamSpec& spec, const Tensor& pack, const Tensor& uv, bool delta) {
+    validate_pack(spec, pack);
+    TORCH_CHECK(uv.size(-1) == 2, "UV coordinates last dimension must be 2")
+    TORCH_CHECK(uv.device() == pack.device(), "Camera and UV-s must be on the same device")
+    TORCH_CHECK(uv.dtype() == at::kFloat, "UV coordinates must be float32 tensor")
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+    auto sizes = uv.sizes().vec();
+    sizes.pop_back();
+    Tensor out = at::empty(sizes, uv.options());
+    Tensor uvc = uv.contiguous();
+    check_rc(xsg_pixel_time(spec.kind, fptr(pack), 0, 0, fptr(uvc), uv.numel() / 2, delta ? 1 : 0,
+                            out.data_ptr<float>(), stream_of(pack)));
+    return out;
+}
+
+std::tuple<Tensor, Tensor> projection(const CamSpec& spec, bool no_jac, const Tensor& pack, const Tensor& points,
+                                      const OptT& points_velocity, double thr, double max_res, double margin,
+                                      int mode) {
+    validate_pack(spec, pack);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+    const int64_t N = points.size(0);
+    Tensor mask = at::empty({N}, pack.options().dtype(at::kBool));
+    Tensor uvdt = at::empty({N, 4}, pack.options());
+    Tensor pts = points.contiguous();
+    OptT vel = points_velocity.has_value() ? OptT(points_velocity->contiguous()) : std::nullopt;
+    check_rc(xsg_project_points(spec.kind, fptr(pack), N, fptr(pts), fptr(vel), (float)thr, (float)max_res,
+                                (float)margin, mode, no_jac ? 1 : 0, uvdt.data_ptr<float>(),
+                                (uint8_t*)mask.data_ptr(), stream_of(pack)));
+    return {uvdt, mask};
+}
+
+// launch_unscented_transform[_phm] (ut_kernels.h:249-305, ut_phm_kernels.h:125-173)
+std::tuple<Tensor, Tensor, Tensor, Tensor> projection_utgs(const CamSpec& spec, bool phm, const Tensor& pack,
+                                                           const Tensor& points, const OptT& points_velocity,
+                                                           const Tensor& scales, const Tensor& quats,
+                                                           const OptT& opacity, double width, double height,
+                                                           double ut_alpha, double ut_beta, double ut_kappa,
+                                                           double thr, double max_res, double margin) {
+    validate_pack(spec, pack);
+    check_same_device({pack, points, scales, quats});
+    std::vector<Tensor> ts{points, scales, quats};
+    if (points_velocity.has_value()) ts.push_back(*points_velocity);
+    if (opacity.has_value()) ts.push_back(*opacity);
+    all_contiguous(ts);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(points.device());
+    const int64_t N = points.size(0);
+    Tensor flags = at::empty({N}, points.options().dtype(at::kByte));
+    Tensor radii = at::empty({N, 2}, points.options());
+    Tensor mean2d = at::empty({N, 2}, points.options());
+    Tensor depths = at::empty({N}, points.options());
+    check_rc(xsg_ut_project(spec.kind, phm ? 1 : 0, fptr(pack), N, fptr(points), fptr(points_velocity),
+                            fptr(scales), fptr(quats), fptr(opacity), (float)width, (float)height, (float)ut_alpha,
+                            (float)ut_beta, (float)ut_kappa, (float)thr, (float)max_res, (float)margin,
+                            flags.data_ptr<uint8_t>(), radii.data_ptr<float>(), mean2d.data_ptr<float>(),
+                            depths.data_ptr<float>(), stream_of(points)));
+    return {flags, radii, mean2d, depths};
+}
+
+template <int I>
+struct CameraTag {};
+
+template <int I>
+void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm, bool available) {
+    auto cls = py::class_<CameraTag<I>>(m, name);
+    if (!available) {
+        auto missing = [name](py::args, py::kwargs) -> py::object {
+            throw std::runtime_error(std::string(name) + " is not provided by this build of xsimgs_amd");
+        };
+        for (const char* meth : {"pack", "camera_rays", "pixel_time", "pixel_time_delta", "pixel_time_from_uv",
+                                 "pixel_time_delta_from_uv", "projection", "projection_nojac", "projection_utgs",
+                                 "undistort_map"})
+            cls.def_static(meth, missing);
+        return;
+    }
+    cls.def_static("pack", [spec](const std::vector<Tensor>& tensors) { return camera_pack(spec, tensors); },
+                   py::arg("tensors"));
+    cls.def_static("camera_rays",
+                   [spec](const Tensor& pack, int64_t width, int64_t height, bool world_space, bool normalized,
+                          bool return_origins, bool return_valid) {
+                       return camera_rays(spec, pack, width, height, world_space, normalized, return_origins,
+                                          return_valid);
+                   },
+                   py::arg("pack"), py::arg("width"), py::arg("height"), py::arg("world_space") = true,
+                   py::arg("normalized") = true, py::arg("return_origins") = true, py::arg("return_valid") = false);
+    cls.def_static("pixel_time",
+                   [spec](const Tensor& pack, int64_t w, int64_t h) { return pixel_time(spec, pack, w, h, false); },
+                   py::arg("pack"), py::arg("width"), py::arg("height"));
+    cls.def_static("pixel_time_delta",
+                   [spec](const Tensor& pack, int64_t w, int64_t h) { return pixel_time(spec, pack, w, h, true); },
+                   py::arg("pack"), py::arg("width"), py::arg("height"));
+    cls.def_static("pixel_time_from_uv",
+                   [spec](const Tensor& pack, const Tensor& uvs) { return pixel_time_uv(spec, pack, uvs, false); },
+                   py::arg("pack"), py::arg("uvs"));
+    cls.def_static("pixel_time_delta_from_uv",
+                   [spec](const Tensor& pack, const Tensor& uvs) { return pixel_time_uv(spec, pack, uvs, true); },
+                   py::arg("pack"), py::arg("uvs"));
+    for (int nojac = 0; nojac < 2; ++nojac) {
+        cls.def_static(nojac ? "projection_nojac" : "projection",
+                       [spec, nojac](const Tensor& pack, const Tensor& points, const OptT& vel, double thr,
+                                     double max_res, double margin, int mode) {
+                           return projection(spec, nojac != 0, pack, points, vel, thr, max_res, margin, mode);
+                       },
+                       py::arg("pack"), py::arg("points"), py::arg("points_velocity") = py::none(),
+                       py::arg("residual_thr_early_stop") = 1e-4f, py::arg("max_residual") = 0.002f,
+                       py::arg("max_margin") = 1.0f, py::arg("projection_mode") = XSG_MODE_CENTRAL);
+    }
+    for (int with_phm = 0; with_phm < (phm ? 2 : 1); ++with_phm) {
+        cls.def_static(with_phm ? "projection_utgs_phm" : "projection_utgs",
+                       [spec, with_phm](const Tensor& pack, const Tensor& points, const OptT& vel, const Tensor& scales,
+                                        const Tensor& quats, const OptT& opacity, double width, double height,
+                                        double a, double b, double k, double thr, double max_res, double margin) {
+                           return projection_utgs(spec, with_phm != 0, pack, points, vel, scales, quats, opacity,
+                                                  width, height, a, b, k, thr, max_res, margin);
+                       },
+                       py::arg("pack"), py::arg("points"), py::arg("points_velocity"), py::arg("scales"),
+                       py::arg("quats"), py::arg("opacity"), py::arg("width"), py::arg("height"),
+                       py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f, py::arg("ut_kappa") = 0.0f,
+                       py::arg("residual_thr_early_stop") = 1e-4f, py::arg("max_residual") = 0.002f,
+                       py::arg("max_margin") = 1.0f);
+    }
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.doc() = "xsimgs_amd: MI355X (gfx950) kernels for the xsimgs Gaussian-splatting hot path";
+    m.def("abi_version", &xsg_abi_version);
+
+    // rasterization (csrc/rasterization/*_bind)
+    m.def("rasterize_eval3d_fwd", &rasterize_eval3d_fwd, py::arg("means"), py::arg("quats"), py::arg("scales"),
+          py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
+          py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"), py::arg("ray_dirs"),
+          py::arg("tile_offsets"), py::arg("flatten_ids"));
+    m.def("rasterize_eval3d_bwd", &rasterize_eval3d_bwd);
+    m.def("rasterize_eval3d_dynamic_fwd", &rasterize_eval3d_dynamic_fwd, py::arg("means"), py::arg("velocity"),
+          py::arg("quats"), py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"),
+          py::arg("image_height"), py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"),
+          py::arg("ray_dirs"), py::arg("ray_time_delta"), py::arg("tile_offsets"), py::arg("flatten_ids"));
+    m.def("rasterize_eval3d_dynamic_bwd", &rasterize_eval3d_dynamic_bwd);
+    m.def("eval3d_supported_ndims", &eval3d_supported_ndims);
+
+    // color (csrc/color/sh_bind.cpp)
+    m.def("spherical_harmonics_fused_fwd", &spherical_harmonics_fused_fwd, py::arg("degree_to_use"),
+          py::arg("origin"), py::arg("positions"), py::arg("coeffs"), py::arg("mask"), py::arg("layout_3kn"),
+          py::arg("coeffs_dc") = py::none(), py::arg("output") = py::none());
+    m.def("spherical_harmonics_fused_bwd", &spherical_harmonics_fused_bwd, py::arg("degree_to_use"),
+          py::arg("origin"), py::arg("positions"), py::arg("coeffs"), py::arg("mask"), py::arg("layout_3kn"),
+          py::arg("d_output"), py::arg("coeffs_dc") = py::none());
+
+    // tiling (csrc/tiling/bind_tiling.cpp)
+    m.def("isect_offset_encode", &isect_offset_encode, py::arg("isect_ids"), py::arg("tile_width"),
+          py::arg("tile_height"), py::arg("n_cams") = 1);
+    m.def("isect_regular_tiles", &isect_regular_tiles, py::arg("means2d"), py::arg("radii"), py::arg("depth"),
+          py::arg("img_width"), py::arg("img_height"), py::arg("tile_size_x"), py::arg("tile_size_y"),
+          py::arg("sort") = true, py::arg("double_buffer") = true);
+    m.def("isect_regular_tiles_batched", &isect_regular_tiles_batched, py::arg("means2d"), py::arg("radii"),
+          py::arg("depth"), py::arg("img_width"), py::arg("img_height"), py::arg("tile_size_x"),
+          py::arg("tile_size_y"), py::arg("sort") = true);
+    m.def("isect_lidar_tiles", &isect_lidar_tiles, py::arg("camera_pack"), py::arg("points"),
+          py::arg("points_velocity"), py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("flag"),
+          py::arg("means2d"), py::arg("radii"), py::arg("depths"), py::arg("elev_boundaries"),
+          py::arg("tile_size_x"), py::arg("img_width"), py::arg("img_height"), py::arg("ut_alpha") = 0.1f,
+          py::arg("ut_beta") = 2.0f, py::arg("ut_kappa") = 0.0f, py::arg("sort") = true,
+          py::arg("double_buffer") = true);
+    m.def("isect_spherical_tiles", &isect_spherical_tiles, py::arg("camera_pack"), py::arg("points"),
+          py::arg("points_velocity"), py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("flag"),
+          py::arg("means2d"), py::arg("radii"), py::arg("depths"), py::arg("tile_size_x"), py::arg("tile_size_y"),
+          py::arg("img_width"), py::arg("img_height"), py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f,
+          py::arg("ut_kappa") = 0.0f, py::arg("sort") = true, py::arg("double_buffer") = true);
+    m.def("mask_radii_packed", &mask_radii_packed, py::arg("packed_mask"), py::arg("radii"));
+    m.def("mask_radii", &mask_radii, py::arg("mask"), py::arg("radii"));
+    m.def("radix_sort_pairs", &radix_sort_pairs, py::arg("keys"), py::arg("values"), py::arg("begin_bit"),
+          py::arg("end_bit"));
+
+    // cameras (csrc/cameras/cameras_bind.h)
+    py::module_ enum_mod = py::module_::import("enum");
+    m.attr("ProjectionMode") = enum_mod.attr("IntEnum")(
+        "ProjectionMode", py::dict(py::arg("Central") = (int)XSG_MODE_CENTRAL,
+                                   py::arg("NegativeDelta") = (int)XSG_MODE_NEGATIVE,
+                                   py::arg("PositiveDelta") = (int)XSG_MODE_POSITIVE));
+    bind_camera<0>(m, "PerspectiveCamera", CamSpec{XSG_CAM_PINHOLE, {4}}, false, true);
+    bind_camera<1>(m, "SphericalCamera", CamSpec{XSG_CAM_SPHERICAL, {4}}, true, true);
+    bind_camera<2>(m, "LidarCamera", CamSpec{XSG_CAM_LIDAR, {4, 2}}, true, true);
+    bind_camera<3>(m, "DistortedPerspectiveCamera", CamSpec{-1, {}}, false, false);
+    bind_camera<4>(m, "OpenCVFisheyeCamera", CamSpec{-1, {}}, false, false);
+}

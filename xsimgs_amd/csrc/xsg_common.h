@@ -1,0 +1,313 @@
+// Shared device helpers for the xsimgs_amd HIP kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/xsimgs_amd.h"
+
+#define XSG_DEV __device__ __forceinline__
+#define XSG_HD __host__ __device__ __forceinline__
+
+// Error reporting shared by every C-ABI entry point (defined in capi.hip).
+int xsg_fail(int code, const char* fmt, ...);
+int xsg_launch_status(const char* what);
+
+#define XSG_TRY_LAUNCH(what)                                  \
+    do {                                                      \
+        int _rc = xsg_launch_status(what);                    \
+        if (_rc != XSG_OK) return _rc;                        \
+    } while (0)
+
+static inline unsigned xsg_blocks(long n, int block) { return (unsigned)((n + block - 1) / block); }
+
+// --------------------------------------------------------------------------
+// small vector types (plain structs: no reliance on HIP vector operators)
+// --------------------------------------------------------------------------
+struct f2 { float x, y; };
+struct f3 { float x, y, z; };
+
+XSG_HD f2 mk2(float x, float y) { return f2{x, y}; }
+XSG_HD f3 mk3(float x, float y, float z) { return f3{x, y, z}; }
+XSG_HD f3 operator+(f3 a, f3 b) { return mk3(a.x + b.x, a.y + b.y, a.z + b.z); }
+XSG_HD f3 operator-(f3 a, f3 b) { return mk3(a.x - b.x, a.y - b.y, a.z - b.z); }
+XSG_HD f3 operator-(f3 a) { return mk3(-a.x, -a.y, -a.z); }
+XSG_HD f3 operator*(f3 a, float s) { return mk3(a.x * s, a.y * s, a.z * s); }
+XSG_HD f3 operator*(float s, f3 a) { return mk3(a.x * s, a.y * s, a.z * s); }
+XSG_HD float dot(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+XSG_HD f3 cross(f3 a, f3 b) {
+    return mk3(a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x);
+}
+XSG_DEV f3 ld3(const float* p) { return mk3(p[0], p[1], p[2]); }
+XSG_DEV void st3(float* p, f3 v) { p[0] = v.x; p[1] = v.y; p[2] = v.z; }
+
+// --------------------------------------------------------------------------
+// Camera pack. Flat float layout (elements):
+//   [0..3] q0 (w,x,y,z) camera-to-world   [4..6] t0   [7..9] v   [10..12] w
+//   [13..14] rolling duration (u, v)  [15] trigger time  [16] pose time
+//   [17..20] impl: pinhole f.x f.y c.x c.y | spherical phi_min phi_range theta_min theta_range
+//   [21..22] lidar only: device address of beam_v (two 32-bit words, low first)
+// Mirrors Camera<Impl> (reference include/cameras/camera.h:67-79) field by field.
+// --------------------------------------------------------------------------
+struct Camera {
+    float qw; f3 qv;
+    f3 t0, v, w;
+    float roll_u, roll_v;
+    float trigger_time, pose_time;
+    float i0, i1, i2, i3;
+    const float* beam_v;
+};
+
+XSG_DEV Camera load_camera(const float* __restrict__ p, int kind) {
+    Camera c;
+    c.qw = p[0]; c.qv = mk3(p[1], p[2], p[3]);
+    c.t0 = mk3(p[4], p[5], p[6]);
+    c.v = mk3(p[7], p[8], p[9]);
+    c.w = mk3(p[10], p[11], p[12]);
+    c.roll_u = p[13]; c.roll_v = p[14];
+    c.trigger_time = p[15]; c.pose_time = p[16];
+    c.i0 = p[17]; c.i1 = p[18]; c.i2 = p[19]; c.i3 = p[20];
+    c.beam_v = nullptr;
+    if (kind == XSG_CAM_LIDAR) {
+        const uint32_t lo = __float_as_uint(p[21]), hi = __float_as_uint(p[22]);
+        c.beam_v = reinterpret_cast<const float*>(((uint64_t)hi << 32) | lo);
+    }
+    return c;
+}
+
+XSG_DEV float pixel_time(const Camera& c, float u, float v) {  // camera.h:89-91
+    return c.trigger_time + (u * c.roll_u + v * c.roll_v);
+}
+
+XSG_DEV float u_pose_of(const Camera& c) {  // spherical.h:113-114
+    return (fabsf(c.roll_u) > 0.0f) ? (c.pose_time - c.trigger_time) / c.roll_u : 0.5f;
+}
+
+// --------------------------------------------------------------------------
+// Rolling-shutter projection (reference include/cameras/projection_kernels.h)
+// --------------------------------------------------------------------------
+XSG_DEV void jac_quat_from_axis_angle(f3 w, float t, float& qw, f3& qxyz, float& dqw, f3& dqxyz) {
+    // projection_kernels.h:12-36. sin/cos of an exactly-zero angle are 0 and 1, so the
+    // common t == 0 / w == 0 case skips sincosf with bit-identical results.
+    const float w_norm = sqrtf(dot(w, w));
+    const float theta = w_norm * fabsf(t);
+    float s = 0.0f, c = 1.0f;
+    if (theta != 0.0f) sincosf(0.5f * theta, &s, &c);
+    const float scale = (theta < 1e-2f) ? 0.5f - theta * theta * (1.0f / 48.0f) : s / theta;
+    qw = c;
+    qxyz = (w * scale) * t;
+    dqw = -0.5f * copysignf(1.0f, t) * s * w_norm;
+    dqxyz = w * (0.5f * c);
+}
+
+XSG_DEV f3 quat_apply(float w, f3 xyz, f3 p) {  // projection_kernels.h:67-71
+    const f3 uv = cross(xyz, p);
+    const f3 uuv = cross(xyz, uv);
+    return p + 2.0f * (w * uv + uuv);
+}
+
+XSG_DEV void world_to_camera_jac(const Camera& c, f3 point, f3 pvel, float time, f3& res, f3& dres) {
+    // projection_kernels.h:74-113
+    float w1, dw1; f3 xyz1, dxyz1;
+    jac_quat_from_axis_angle(c.w, time, w1, xyz1, dw1, dxyz1);
+    const float w2 = c.qw; const f3 xyz2 = c.qv;
+    const float w = w1 * w2 - dot(xyz1, xyz2);
+    f3 xyz = w2 * xyz1 + w1 * xyz2 + cross(xyz1, xyz2);
+    const float dw = dw1 * w2 - dot(dxyz1, xyz2);
+    f3 dxyz = dw1 * xyz2 + w2 * dxyz1 + cross(dxyz1, xyz2);
+    xyz = -xyz; dxyz = -dxyz;
+    const f3 vdiff = pvel - c.v;
+    const f3 p = point - c.t0 + vdiff * time;
+    const f3 uv = cross(xyz, p);
+    const f3 uuv = cross(xyz, uv);
+    res = p + 2.0f * (w * uv + uuv);
+    const f3 duv = cross(dxyz, p);
+    const f3 dp = 2.0f * (dw * uv + w * duv + cross(dxyz, uv) + cross(xyz, duv));
+    dres = dp + quat_apply(w, xyz, vdiff);
+}
+
+// angles_to_uv with the phase unwrapping of SphericalCamera (csrc/cameras/spherical.h:109-125)
+XSG_DEV f2 angles_to_uv(const Camera& c, int mode, float phi, float theta) {
+    float u = (phi - c.i0) / c.i1;
+    const float u_pose = u_pose_of(c);
+    const float u_offset = (2.0f * float(M_PI) / fabsf(c.i1));
+    if (c.roll_u > 0) {
+        if ((mode == XSG_MODE_NEGATIVE) && (u > u_pose)) u = u - u_offset;
+        if ((mode == XSG_MODE_POSITIVE) && (u < u_pose)) u = u + u_offset;
+    } else {
+        if ((mode == XSG_MODE_NEGATIVE) && (u < u_pose)) u = u + u_offset;
+        if ((mode == XSG_MODE_POSITIVE) && (u > u_pose)) u = u - u_offset;
+    }
+    const float v = (theta - c.i2) / c.i3;
+    return mk2(u, v);
+}
+
+template <int KIND>
+XSG_DEV f3 point_to_uvd(const Camera& c, int mode, f3 p) {
+    if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:36-42
+        return mk3(p.x * c.i0 / p.z + c.i2, p.y * c.i1 / p.z + c.i3, p.z);
+    } else {  // spherical.h:133-142
+        const float x2y2 = p.x * p.x + p.y * p.y;
+        const float r = sqrtf(x2y2 + p.z * p.z);
+        const float phi = atan2f(-p.x, -p.y) + float(M_PI);
+        const float theta = asinf(p.z / r);
+        const f2 uv = angles_to_uv(c, mode, phi, theta);
+        return mk3(uv.x, uv.y, r);
+    }
+}
+
+template <int KIND>
+XSG_DEV void point_to_uvd_jacob(const Camera& c, int mode, f3 p, f3 dp, f3& uvd, f2& du_dv) {
+    if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:44-52
+        uvd = point_to_uvd<KIND>(c, mode, p);
+        du_dv.x = c.i0 * (dp.x - uvd.x * dp.z) / uvd.z;
+        du_dv.y = c.i1 * (dp.y - uvd.y * dp.z) / uvd.z;
+    } else {  // spherical.h:133-153
+        const float x2y2 = p.x * p.x + p.y * p.y;
+        const float r = sqrtf(x2y2 + p.z * p.z);
+        const float phi = atan2f(-p.x, -p.y) + float(M_PI);
+        const float theta = asinf(p.z / r);
+        const f2 uv = angles_to_uv(c, mode, phi, theta);
+        uvd = mk3(uv.x, uv.y, r);
+        const float x2y2_sqrt = sqrtf(x2y2);
+        const float r2 = r * r;
+        const float mul = p.z / (r2 * x2y2_sqrt);
+        du_dv.x = ((-p.x * dp.y + p.y * dp.x) / x2y2) / c.i1;
+        du_dv.y = ((x2y2_sqrt * dp.z) / r2 - mul * (p.x * dp.x + p.y * dp.y)) / c.i3;
+    }
+}
+
+struct ProjParams {
+    float thr, max_res, margin;
+};
+
+// camera_projection: projection_kernels.h:201-256 (Newton solve of the pixel time).
+// `is_static` (no camera motion, no point velocity) lets the camera-space point be computed
+// once: the pose is then independent of the time, so every iteration sees the same point.
+template <int KIND>
+XSG_DEV void camera_projection(const Camera& c, f3 pw, f3 pv, const ProjParams& pp, int mode,
+                               bool is_static, float4& uvdt, bool& valid) {
+    f3 uvd = mk3(0.f, 0.f, 0.f);
+    float p_time = 0.0f;
+    if (mode == XSG_MODE_NEGATIVE) p_time = -fabsf(c.roll_u) * 0.5f;
+    else if (mode == XSG_MODE_POSITIVE) p_time = fabsf(c.roll_u) * 0.5f;
+    float residual = 0.0f;
+    f3 pc = mk3(0.f, 0.f, 0.f), jpc = mk3(0.f, 0.f, 0.f);
+    f2 du_dv = mk2(0.f, 0.f);
+    if (is_static) {
+        // static pose: world_to_camera(p, t) == quat_apply(q0.w, -q0.xyz, p - t0) for every t
+        f3 r, dr;
+        world_to_camera_jac(c, pw, pv, p_time, r, dr);
+        pc = r; jpc = dr;
+        point_to_uvd_jacob<KIND>(c, mode, pc, jpc, uvd, du_dv);
+    }
+#pragma unroll 1
+    for (int i = 0; i < 5; ++i) {
+        if (!is_static) {
+            world_to_camera_jac(c, pw, pv, p_time, pc, jpc);
+            point_to_uvd_jacob<KIND>(c, mode, pc, jpc, uvd, du_dv);
+        }
+        const float assumed = c.pose_time + p_time;
+        const float real_time = pixel_time(c, uvd.x, uvd.y);
+        residual = assumed - real_time;
+        const float d_res = 1.0f - (du_dv.x * c.roll_u + du_dv.y * c.roll_v);
+        p_time -= residual / d_res;
+        if ((uvd.z <= 0.0f) || (uvd.x < -pp.margin) || (uvd.x > 1.0f + pp.margin) ||
+            (uvd.y < -pp.margin) || (uvd.y > 1.0f + pp.margin)) {
+            valid = false;
+            uvdt = make_float4(0.f, 0.f, 0.f, 0.f);
+            return;
+        }
+        if (fabsf(residual) < pp.thr) break;
+    }
+    uvdt = make_float4(uvd.x, uvd.y, uvd.z, p_time);
+    valid = valid && (fabsf(residual) < pp.max_res) && (uvd.z > 0.0f);
+}
+
+XSG_DEV bool camera_is_static(const Camera& c, bool has_vel) {
+    return !has_vel && c.w.x == 0.f && c.w.y == 0.f && c.w.z == 0.f && c.v.x == 0.f &&
+           c.v.y == 0.f && c.v.z == 0.f;
+}
+
+// unscented_transform_deltas (ut_kernels.h:38-49): columns of R(q) scaled by s_i * sqrt(3+lambda),
+// from the normalised quaternion (w, x, y, z).
+XSG_DEV void ut_deltas(float sqrt_dl, float4 q, f3 s, f3 d[3]) {
+    float w = q.x, x = q.y, y = q.z, z = q.w;
+    const float inv = 1.0f / sqrtf(w * w + x * x + y * y + z * z);
+    w *= inv; x *= inv; y *= inv; z *= inv;
+    d[0] = mk3(1.f - 2.f * (y * y + z * z), 2.f * (x * y + w * z), 2.f * (x * z - w * y)) * (s.x * sqrt_dl);
+    d[1] = mk3(2.f * (x * y - w * z), 1.f - 2.f * (x * x + z * z), 2.f * (y * z + w * x)) * (s.y * sqrt_dl);
+    d[2] = mk3(2.f * (x * z + w * y), 2.f * (y * z - w * x), 1.f - 2.f * (x * x + y * y)) * (s.z * sqrt_dl);
+}
+
+struct UtWeights { float wm0, wc0, wi, sqrt_dl; };
+
+// unscented_transform (ut_kernels.h:52-137) + the radii / on-screen test of
+// unscented_transform_projection (ut_kernels.h:140-184). On failure mean2d / depth keep what the
+// reference leaves in them (untouched if the centre point fails, the accumulated mean if a sigma
+// point fails) and radii come from a zero covariance, because the phase-modelled selection
+// (ut_phm_kernels.h:417-421) can pick a failed side.
+template <int KIND>
+XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 img, const ProjParams& pp,
+                           f3 pw, f3 pv, float opac, const f3 d[3], bool is_static, f2& mean2d,
+                           f2& radii, float& depth, float& u_distance) {
+    float4 uvdt;
+    bool valid = true;
+    f2 pts[7];
+    bool result = true;
+    camera_projection<KIND>(c, pw, pv, pp, mode, is_static, uvdt, valid);
+    f2 cov_xx_xy = mk2(0.f, 0.f);
+    float cov_yy = 0.f;
+    if (!valid) {
+        result = false;
+    } else {
+        pts[0] = mk2(uvdt.x * img.x, uvdt.y * img.y);
+        mean2d = mk2(ut.wm0 * pts[0].x, ut.wm0 * pts[0].y);
+        depth = uvdt.z;
+        float u_min = pts[0].x, u_max = pts[0].x;
+        float sign = 1.0f;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            camera_projection<KIND>(c, pw + sign * d[i / 2], pv, pp, mode, is_static, uvdt, valid);
+            pts[i + 1] = mk2(uvdt.x * img.x, uvdt.y * img.y);
+            mean2d.x += ut.wi * pts[i + 1].x;
+            mean2d.y += ut.wi * pts[i + 1].y;
+            u_min = fminf(u_min, pts[i + 1].x);
+            u_max = fmaxf(u_max, pts[i + 1].x);
+            sign *= -1.0f;
+        }
+        if (!valid) {
+            result = false;
+        } else {
+            u_distance = u_max - u_min;
+            float vx = pts[0].x - mean2d.x, vy = pts[0].y - mean2d.y;
+            float cx = ut.wc0 * (vx * vx), cxy = ut.wc0 * (vx * vy), cy = ut.wc0 * (vy * vy);
+#pragma unroll
+            for (int i = 1; i < 7; ++i) {
+                vx = pts[i].x - mean2d.x; vy = pts[i].y - mean2d.y;
+                cx += ut.wi * (vx * vx); cxy += ut.wi * (vx * vy); cy += ut.wi * (vy * vy);
+            }
+            const float det = cx * cy - cxy * cxy;
+            if (det <= 0.0f || cx < 0 || cy < 0) result = false;
+            cov_xx_xy = mk2(cx, cxy);
+            cov_yy = cy;
+        }
+    }
+    const float extend = fminf(3.33f, sqrtf(2.0f * logf(opac / (1.0f / 255.0f))));
+    radii = mk2(extend * sqrtf(fmaxf(0.0f, cov_xx_xy.x)), extend * sqrtf(fmaxf(0.0f, cov_yy)));
+    const bool ix = !(((mean2d.x + radii.x) < 0) || (img.x < (mean2d.x - radii.x)));
+    const bool iy = !(((mean2d.y + radii.y) < 0) || (img.y < (mean2d.y - radii.y)));
+    return result && ix && iy;
+}
+
+// --------------------------------------------------------------------------
+// wave64 helpers
+// --------------------------------------------------------------------------
+XSG_DEV int lane_id() { return __lane_id(); }
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+XSG_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}

@@ -1,0 +1,134 @@
+// eval3d compositing kernels (reference csrc/rasterization/eval3d_{fwd,bwd}.cu, eval3d_dynamic_*.cu).
+//
+// One workgroup per (camera, tile); one thread per pixel (tile_w * tile_h <= 256 threads, i.e. up
+// to four wave64s). Gaussians of the tile's depth-sorted list are staged in LDS in batches of one
+// per thread. Per staged Gaussian the LDS slot holds M = S^-1 R^T (three rows) and, when every ray
+// of the tile starts at the same origin (decided by a block vote, always true for a static pinhole
+// or spherical camera), gro = M (o - mu): the per-pair work then only maps the ray direction.
+// These are the values the reference computes per pair, so results do not depend on the path.
+#pragma once
+#include "xsg_common.h"
+
+namespace xsg {
+
+constexpr int kTileThreads = 256;
+constexpr int kColorLdsMax = 16;  // colour channels staged in LDS; larger CDIM read from HBM
+
+#define XSG_CDIM_LIST(X) \
+    X(0) X(1) X(2) X(3) X(4) X(5) X(8) X(9) X(16) X(17) X(32) X(33) X(64) X(65) X(128) X(129) \
+    X(256) X(257) X(512) X(513)
+
+struct TileGrid {
+    int width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_cams;
+    int64_t n;          // Gaussians (flatten id = cam * n + gaussian)
+    int64_t n_isects;
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a contiguous run of tiles so
+// that neighbouring tiles, which share most of their Gaussians, share an L2.
+XSG_DEV int xcd_tile(int b, int nblocks) {
+    const int x = b & 7, q = nblocks >> 3, r = nblocks & 7;
+    return x * q + min(x, r) + (b >> 3);
+}
+
+struct PixelCtx {
+    int cam, tile, tr;
+    int i, j;
+    bool inside;
+    int64_t pix;          // index into [n_cams, H, W]
+    int32_t range_start, range_end;
+};
+
+XSG_DEV PixelCtx pixel_ctx(const TileGrid& g, const int32_t* __restrict__ offsets) {
+    PixelCtx c;
+    const int n_tiles = g.n_tiles_w * g.n_tiles_h;
+    const int nblocks = n_tiles * g.n_cams;
+    const int logical = xcd_tile((int)blockIdx.x, nblocks);
+    c.cam = logical / n_tiles;
+    c.tile = logical - c.cam * n_tiles;
+    c.tr = threadIdx.x;
+    const int ty = c.tr / g.tile_w, tx = c.tr - ty * g.tile_w;
+    const int trow = c.tile / g.n_tiles_w, tcol = c.tile - trow * g.n_tiles_w;
+    c.i = trow * g.tile_h + ty;  // utils.h:32-44
+    c.j = tcol * g.tile_w + tx;
+    c.inside = c.i < g.height && c.j < g.width;
+    const int64_t hw = (int64_t)g.width * g.height;
+    c.pix = (int64_t)c.cam * hw + min((int64_t)c.i * g.width + c.j, hw - 1);
+    const int gt = c.cam * n_tiles + c.tile;  // utils.h:48-58
+    c.range_start = offsets[gt];
+    c.range_end = (gt == nblocks - 1) ? (int32_t)g.n_isects : offsets[gt + 1];
+    return c;
+}
+
+// Rows of M = S^-1 R^T from the raw quaternion (w, x, y, z) and activated scales: row i is column i
+// of R / s_i (utils.h:61-83 and eval3d_fwd.cu:92-107).
+XSG_DEV void iscl_rot_rows(float4 q, f3 s, f3& r0, f3& r1, f3& r2) {
+    float w = q.x, x = q.y, y = q.z, z = q.w;
+    const float inv = rsqrtf(x * x + y * y + z * z + w * w);
+    x *= inv; y *= inv; z *= inv; w *= inv;
+    const float x2 = x * x, y2 = y * y, z2 = z * z;
+    const float xy = x * y, xz = x * z, yz = y * z;
+    const float wx = w * x, wy = w * y, wz = w * z;
+    const float i0 = 1.0f / s.x, i1 = 1.0f / s.y, i2 = 1.0f / s.z;
+    r0 = mk3(i0 * (1.f - 2.f * (y2 + z2)), i0 * (2.f * (xy + wz)), i0 * (2.f * (xz - wy)));
+    r1 = mk3(i1 * (2.f * (xy - wz)), i1 * (1.f - 2.f * (x2 + z2)), i1 * (2.f * (yz + wx)));
+    r2 = mk3(i2 * (2.f * (xz + wy)), i2 * (2.f * (yz - wx)), i2 * (1.f - 2.f * (x2 + y2)));
+}
+
+XSG_DEV f3 rows_mul(f3 r0, f3 r1, f3 r2, f3 v) { return mk3(dot(r0, v), dot(r1, v), dot(r2, v)); }
+XSG_DEV f3 rows_tmul(f3 r0, f3 r1, f3 r2, f3 v) {  // M^T v
+    return mk3(r0.x * v.x + r1.x * v.y + r2.x * v.z, r0.y * v.x + r1.y * v.y + r2.y * v.z,
+               r0.z * v.x + r1.z * v.y + r2.z * v.z);
+}
+
+XSG_DEV f3 safe_normalize(f3 v) {  // utils.h:85-88
+    const float l = dot(v, v);
+    return l > 0.0f ? v * rsqrtf(l) : v;
+}
+
+XSG_DEV f3 safe_normalize_bwd(f3 v, f3 d_out) {  // utils.h:198-206
+    const float l = dot(v, v);
+    if (l > 0.0f) {
+        const float il = rsqrtf(l);
+        const float il3 = il * il * il;
+        return il * d_out - (il3 * dot(d_out, v)) * v;
+    }
+    return d_out;
+}
+
+struct Eval3dParams {
+    TileGrid g;
+    const float* means;
+    const float4* quats;
+    const float* scales;
+    const float* colors;
+    const float* opac;
+    const float* velocity;
+    const float* rtd;
+    const float* ray_o;
+    const float* ray_d;
+    const int32_t* offsets;
+    const int32_t* flatten;
+    float* out_rgb;
+    float* out_depth;
+    float* out_alpha;
+    int32_t* out_last;
+    const float* render_alpha;
+    const int32_t* last_ids;
+    const float* v_rgb;
+    const float* v_depth;
+    const float* v_alpha;
+    float* v_means;
+    float* v_opac;
+    float* v_colors;
+    float* v_ray_o;
+    float* v_ray_d;
+    float* v_velocity;
+    float* v_time;
+    float* v_mt;         // workspace [n, 9]: sum of dL/dM^T per Gaussian (row-major of M^T)
+};
+
+int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
+int eval3d_bwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
+
+}  // namespace xsg

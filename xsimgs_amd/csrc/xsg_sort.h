@@ -1,0 +1,194 @@
+// Device-wide scan and stable LSD radix sort building blocks (256-thread blocks = 4 wave64s).
+//
+// Radix sort pass = three kernels:
+//   upsweep   : per-block digit histograms, stored digit-major hist[d * nb + b]
+//   scan_hist : one block per digit, exclusive scan over blocks + digit totals
+//   downsweep : per block, 16 rounds of 256 keys; a key's rank among equal digits inside its
+//               wavefront comes from 64-bit ballots over the digit bits (wave64 match), wave
+//               counts are combined in LDS, and a running per-digit base keeps the pass stable.
+#pragma once
+#include "xsg_common.h"
+
+namespace xsg {
+
+constexpr int kSortBlock = 256;
+constexpr int kSortItems = 16;
+constexpr int kSortTile = kSortBlock * kSortItems;  // keys per block and pass
+constexpr int kRadix = 256;
+constexpr int kWaves = kSortBlock / 64;
+
+inline unsigned sort_blocks(int64_t n) { return (unsigned)((n + kSortTile - 1) / kSortTile); }
+
+template <typename T>
+XSG_DEV T wave_inclusive_scan(T v) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const T t = __shfl_up(v, off, 64);
+        if (lane >= off) v += t;
+    }
+    return v;
+}
+
+// Exclusive scan over the 256 threads of a block; `lds` holds kWaves elements.
+template <typename T>
+XSG_DEV T block_exclusive_scan(T v, T* lds, T& total) {
+    const T inc = wave_inclusive_scan(v);
+    const int wave = threadIdx.x >> 6;
+    if (__lane_id() == 63) lds[wave] = inc;
+    __syncthreads();
+    T before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const T x = lds[w];
+        if (w < wave) before += x;
+        tot += x;
+    }
+    __syncthreads();
+    total = tot;
+    return before + inc - v;
+}
+
+template <typename T>
+XSG_DEV T block_reduce_sum(T v, T* lds) {
+    T total;
+    block_exclusive_scan(v, lds, total);
+    return total;
+}
+
+// ---------------------------------------------------------------- radix sort passes
+template <typename K>
+XSG_DEV uint32_t digit_of(K key, int shift, int bits) {
+    return (uint32_t)((key >> shift) & (K)((1u << bits) - 1u));
+}
+
+template <typename K>
+__global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict__ keys, int64_t n, int shift,
+                                                            int bits, uint32_t* __restrict__ hist, unsigned nb) {
+    __shared__ uint32_t cnt[kWaves][kRadix];
+    const int t = threadIdx.x, wave = t >> 6;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) cnt[w][t] = 0;
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+#pragma unroll 4
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t idx = base + (int64_t)k * kSortBlock + t;
+        if (idx < n) atomicAdd(&cnt[wave][digit_of<K>(keys[idx], shift, bits)], 1u);
+    }
+    __syncthreads();
+    uint32_t s = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += cnt[w][t];
+    hist[(int64_t)t * nb + blockIdx.x] = s;
+}
+
+// one block per digit: exclusive scan of hist[d * nb .. d * nb + nb), total into digit_total[d]
+__global__ __launch_bounds__(kSortBlock) void radix_scan_hist(uint32_t* __restrict__ hist, unsigned nb,
+                                                              uint32_t* __restrict__ digit_total) {
+    __shared__ uint32_t lds[kWaves];
+    uint32_t* h = hist + (int64_t)blockIdx.x * nb;
+    uint32_t carry = 0;
+    for (unsigned start = 0; start < nb; start += kSortBlock) {
+        const unsigned i = start + threadIdx.x;
+        const uint32_t v = i < nb ? h[i] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(v, lds, tot);
+        if (i < nb) h[i] = carry + ex;
+        carry += tot;
+    }
+    if (threadIdx.x == 0) digit_total[blockIdx.x] = carry;
+}
+
+// Output policies for the downsweep scatter.
+template <typename K, typename V>
+struct PlainOut {
+    K* keys;
+    V* vals;
+    XSG_DEV void put(int64_t pos, K k, V v) const { keys[pos] = k; vals[pos] = v; }
+};
+
+template <typename K, typename V, typename Out>
+__global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restrict__ keys_in,
+                                                              const V* __restrict__ vals_in, int64_t n,
+                                                              int shift, int bits,
+                                                              const uint32_t* __restrict__ hist,
+                                                              const uint32_t* __restrict__ digit_total,
+                                                              unsigned nb, Out out) {
+    __shared__ uint32_t base[kRadix];
+    __shared__ uint32_t wcnt[kWaves][kRadix];
+    __shared__ uint32_t scan_lds[kWaves];
+    const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
+    {
+        uint32_t tot;
+        const uint32_t dprefix = block_exclusive_scan<uint32_t>(digit_total[t], scan_lds, tot);
+        base[t] = dprefix + hist[(int64_t)t * nb + blockIdx.x];
+    }
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) wcnt[w][t] = 0;
+    __syncthreads();
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int64_t tile0 = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t idx = tile0 + (int64_t)k * kSortBlock + t;
+        if (tile0 + (int64_t)k * kSortBlock >= n) break;  // block-uniform
+        const bool valid = idx < n;
+        K key = 0;
+        V val = 0;
+        uint32_t d = 0;
+        if (valid) {
+            key = keys_in[idx];
+            val = vals_in[idx];
+            d = digit_of<K>(key, shift, bits);
+        }
+        uint64_t peers = __ballot(valid);
+        for (int b = 0; b < bits; ++b) {
+            const uint64_t m = __ballot((d >> b) & 1u);
+            peers &= ((d >> b) & 1u) ? m : ~m;
+        }
+        const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
+        if (valid && rank == 0) wcnt[wave][d] = (uint32_t)__popcll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t off = base[d] + rank;
+            for (int w = 0; w < wave; ++w) off += wcnt[w][d];
+            out.put(off, key, val);
+        }
+        __syncthreads();
+        uint32_t s = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) { s += wcnt[w][t]; wcnt[w][t] = 0; }
+        base[t] += s;
+        __syncthreads();
+    }
+}
+
+// Runs every pass of a stable LSD sort over bits [begin_bit, end_bit) (8-bit digits, last one
+// narrower) ping-ponging between (k0, v0) and (k1, v1); the last pass goes through `final_out`.
+// Returns the number of passes. hist must hold kRadix * sort_blocks(n) words, dtot kRadix words.
+template <typename K, typename V, typename FinalOut>
+inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
+                             uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s) {
+    const unsigned nb = sort_blocks(n);
+    int passes = 0;
+    K* src_k = k0; V* src_v = v0; K* dst_k = k1; V* dst_v = v1;
+    for (int shift = begin_bit; shift < end_bit; shift += 8) {
+        const int bits = min(8, end_bit - shift);
+        const bool last = shift + 8 >= end_bit;
+        radix_upsweep<K><<<nb, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb);
+        radix_scan_hist<<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot);
+        if (last) {
+            radix_downsweep<K, V, FinalOut><<<nb, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits, hist,
+                                                                      dtot, nb, final_out);
+        } else {
+            radix_downsweep<K, V, PlainOut<K, V>><<<nb, kSortBlock, 0, s>>>(
+                src_k, src_v, n, shift, bits, hist, dtot, nb, PlainOut<K, V>{dst_k, dst_v});
+        }
+        ++passes;
+        K* tk = src_k; src_k = dst_k; dst_k = tk;
+        V* tv = src_v; src_v = dst_v; dst_v = tv;
+    }
+    return passes;
+}
+
+}  // namespace xsg

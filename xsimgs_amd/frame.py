@@ -1,0 +1,91 @@
+"""One training frame of the hot path, as the reference's caller runs it.
+
+activations (exp scales, sigmoid opacity) -> SH colours -> UT projection -> tile binning with
+sort -> per-tile offsets -> camera rays -> eval3d composite forward -> composite backward ->
+SH backward -> activation gradients. The sequence is ut_gs_render's (reference
+src/xsimgs/rendering/render.py:85-187) with the intermediates kept for inspection; the
+activations and the SH call are the caller's, as in the reference.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import cameras as C
+from .rendering.rasterize import ut_gs_rasterize
+from .rendering.render import ut_gs_tiling
+from .rendering.sh import spherical_harmonics_fused
+
+
+@dataclass
+class FrameState:
+    scene: object
+    device: torch.device
+    means: torch.Tensor
+    log_scales: torch.Tensor
+    quats: torch.Tensor
+    opacity_logits: torch.Tensor
+    sh: torch.Tensor | None
+    colors: torch.Tensor | None
+    cams: list = field(default_factory=list)
+
+
+def make_camera(spec, device) -> C.FusedRSCamera:
+    pose = C.CameraPose.make(q=spec.q, t=spec.t, v=spec.v, w=spec.w, duration=spec.rolling,
+                             offset_time=spec.trigger_time, pose_time=spec.pose_time, device=device)
+    if spec.kind == "pinhole":
+        return C.PerspectiveCamera(pose, torch.tensor(spec.impl))
+    if spec.kind == "spherical":
+        return C.SphericalCamera(pose, torch.tensor(spec.impl))
+    return C.LidarCamera(pose, torch.tensor(spec.impl), spec.beam_v)
+
+
+def prepare(scene, device, requires_grad: bool = True) -> FrameState:
+    def leaf(t):
+        if t is None:
+            return None
+        return t.to(device).contiguous().requires_grad_(requires_grad)
+
+    st = FrameState(scene, torch.device(device), leaf(scene.means), leaf(scene.log_scales), leaf(scene.quats),
+                    leaf(scene.opacity_logits), leaf(scene.sh_coeffs), leaf(scene.colors))
+    st.cams = [make_camera(spec, device) for spec in scene.cameras]
+    return st
+
+
+def render_frame(st: FrameState, backward: bool = False, grads=None, cam_index: int = 0) -> dict:
+    sc = st.scene
+    spec = sc.cameras[cam_index]
+    cam = st.cams[cam_index]
+    scales = torch.exp(st.log_scales)
+    opac = torch.sigmoid(st.opacity_logits)
+    if st.sh is not None:
+        origin = cam.pose.t
+        colors = spherical_harmonics_fused(st.sh, st.means, origin, sc.sh_degree)
+    else:
+        colors = st.colors
+    tsx, tsy = sc.tile_size
+    with cam._freeze_ctx():
+        tiles = ut_gs_tiling(cam, st.means, scales, st.quats, spec.width, spec.height, opacity=opac,
+                             tile_size_x=tsx, tile_size_y=tsy, use_phm=sc.use_phm)
+        ray_o, ray_d = cam.camera_rays(spec.width, spec.height, normalized_rays=True, return_origins=True,
+                                       world_space=True)
+        rgb, depth, alpha = ut_gs_rasterize(st.means, st.quats, scales, opac, colors, ray_o, ray_d,
+                                            tiles["isect_offsets"], tiles["flatten_ids"], tsx, tsy)
+    out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d,
+               offsets=tiles["isect_offsets"], flatten_ids=tiles["flatten_ids"], radii=tiles["radii"],
+               means2d=tiles["means2d"], depths=tiles["depth"])
+    if backward:
+        g_rgb, g_depth, g_alpha = [g.to(st.device) for g in grads]
+        torch.autograd.backward([rgb, depth, alpha], [g_rgb, g_depth, g_alpha])
+        out["grads"] = dict(means=st.means.grad, quats=st.quats.grad, log_scales=st.log_scales.grad,
+                            opacity_logits=st.opacity_logits.grad,
+                            sh=st.sh.grad if st.sh is not None else None,
+                            colors=st.colors.grad if st.colors is not None else None)
+    return out
+
+
+def zero_grads(st: FrameState) -> None:
+    for t in (st.means, st.log_scales, st.quats, st.opacity_logits, st.sh, st.colors):
+        if t is not None:
+            t.grad = None
