@@ -8,8 +8,10 @@
 //  * dL/dM (M = S^-1 R^T) is accumulated per Gaussian and turned into quaternion / scale gradients
 //    once per Gaussian by eval3d_bwd_epilogue: quat_scale_to_preci_half_vjp (utils.h:232-263) is
 //    linear in dL/dM, so the sum of per-pair vjps equals the vjp of the sum;
-//  * per-pair gradients are summed over the 64 lanes of a wavefront and one atomic instruction,
-//    with one lane per gradient component, adds the totals.
+//  * per-pair gradients are summed over the 64 lanes of a wavefront by a reduce-scatter that
+//    leaves each component's total on its own lane, and one atomic instruction per 16
+//    components adds them (one lane per component);
+//  * divisions in the per-pair math are reciprocal-multiplies (v_rcp_f32, 1 ulp).
 #include "xsg_eval3d.h"
 
 namespace xsg {
@@ -128,8 +130,11 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
 #pragma unroll
             for (int k = 0; k < K; ++k) acc[k] = 0.f;
             if (valid) {
-                const float last_hit_T = -dot(grd, gro) / dot(grd, grd);
-                const float ra = 1.0f / fmaxf(1e-6f, 1.0f - alpha);
+                const float dd = dot(grd, grd);
+                const float inv_dd = __builtin_amdgcn_rcpf(dd);
+                const float od = dot(gro, grd);
+                const float last_hit_T = -od * inv_dd;
+                const float ra = __builtin_amdgcn_rcpf(fmaxf(1e-6f, 1.0f - alpha));
                 T *= ra;
                 const float fac = alpha * T;
                 float rgb[CS];
@@ -155,13 +160,9 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
                 v_alpha += (last_hit_T * T - depth_buffer * ra) * v_d;
                 v_alpha += T_final * ra * v_a;
 
-                const float dd = dot(grd, grd);
-                const float od = dot(gro, grd);
                 const float dL_dhitT = v_d * fac;
-                f3 v_gro = mk3((-grd.x * dL_dhitT) / dd, (-grd.y * dL_dhitT) / dd, (-grd.z * dL_dhitT) / dd);
-                f3 v_grd = (2.0f * od * grd - dd * gro) * dL_dhitT;
-                const float dd2 = dd * dd;
-                v_grd = mk3(v_grd.x / dd2, v_grd.y / dd2, v_grd.z / dd2);
+                f3 v_gro = grd * (-dL_dhitT * inv_dd);
+                f3 v_grd = (2.0f * od * grd - dd * gro) * (dL_dhitT * inv_dd * inv_dd);
 
                 if (op * vis <= kMaxAlpha) {
                     const float v_vis = op * v_alpha;
@@ -198,25 +199,25 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
                 for (int k = 0; k < CDIM; ++k) buffer[k] += rgb[k] * fac;
                 depth_buffer += fac * last_hit_T;
             }
-            // wave totals, then one atomic per component from lanes 0..K-1
-#pragma unroll
-            for (int k = 0; k < K; ++k) acc[k] = wave_sum(acc[k]);
+            // wave totals by reduce-scatter: lane l ends with component 16 * chunk + (l >> 2); the
+            // first lane of each quad adds it, one atomic instruction per chunk of 16 components
             const int32_t fid = s_id[t];
             const int64_t gid = fid - (int64_t)c.cam * g.n;
 #pragma unroll
-            for (int base = 0; base < K; base += 64) {
-                const int kk = base + lane;
-                float mine = 0.f;
+            for (int base = 0; base < K; base += 16) {
+                float chunk[16];
 #pragma unroll
-                for (int k = base; k < K && k < base + 64; ++k) mine = (kk == k) ? acc[k] : mine;
-                if (kk < K) {
+                for (int k = 0; k < 16; ++k) chunk[k] = (base + k < K) ? acc[base + k] : 0.f;
+                const float tot = wave_reduce_scatter16(chunk);
+                const int kk = base + (lane >> 2);
+                if ((lane & 3) == 0 && kk < K) {
                     float* dst;
                     if (kk < CDIM) dst = p.v_colors + (int64_t)fid * CDIM + kk;
                     else if (kk < CDIM + 3) dst = p.v_means + 3 * gid + (kk - CDIM);
                     else if (kk < CDIM + 12) dst = p.v_mt + 9 * gid + (kk - CDIM - 3);
                     else if (kk == CDIM + 12) dst = p.v_opac + gid;
                     else dst = p.v_velocity + 3 * gid + (kk - CDIM - 13);
-                    unsafeAtomicAdd(dst, mine);
+                    unsafeAtomicAdd(dst, tot);
                 }
             }
         }

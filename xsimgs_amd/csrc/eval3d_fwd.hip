@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
             const float power = -0.5f * dot(gcrod, gcrod);
             const float alpha = fminf(0.999f, op * __expf(power));
             if (alpha < 1.f / 255.f) continue;
-            const float hit_t = -dot(gro, grd) / dot(grd, grd);
+            const float hit_t = -dot(gro, grd) * __builtin_amdgcn_rcpf(dot(grd, grd));
             const float next_T = T * (1.0f - alpha);
             if (next_T <= 1e-4f) {  // exclusive termination (eval3d_fwd.cu:135-139)
                 done = true;

@@ -96,6 +96,64 @@ XSG_DEV f3 safe_normalize_bwd(f3 v, f3 d_out) {  // utils.h:198-206
     return d_out;
 }
 
+// Lane-to-lane moves inside rows of 16 lanes (DPP). `update_dpp` with all rows/banks enabled and
+// in-bounds patterns returns the source lane's value for every lane.
+template <int CTRL>
+XSG_DEV float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppRowMirror = 0x140;   // lane i <-> 15 - i within a row of 16
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each half row of 8
+
+// Reduce-scatter of 16 per-lane values over the 64 lanes of a wavefront by recursive halving:
+// each step pairs every lane with a partner, keeps half of its values and adds the partner's
+// copy of that half. After the four halving steps (partners at distance 32 and 16, then the row
+// and half-row mirrors) and a final quad sum, lane l holds the wave total of value l >> 2.
+// 15 exchanges + 2 instead of 16 x 6 for a butterfly per value.
+XSG_DEV float wave_reduce_scatter16(const float (&v)[16]) {
+    const int lane = __lane_id();
+    float w[8], x[4], y[2];
+    {
+        const bool up = lane & 32;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float send = up ? v[j] : v[j + 8];
+            const float keep = up ? v[j + 8] : v[j];
+            w[j] = keep + __shfl_xor(send, 32, 64);
+        }
+    }
+    {
+        const bool up = lane & 16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float send = up ? w[j] : w[j + 4];
+            const float keep = up ? w[j + 4] : w[j];
+            x[j] = keep + __shfl_xor(send, 16, 64);
+        }
+    }
+    {
+        const bool up = (lane & 15) >= 8;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float send = up ? x[j] : x[j + 2];
+            const float keep = up ? x[j + 2] : x[j];
+            y[j] = keep + dpp_mov<kDppRowMirror>(send);
+        }
+    }
+    float z;
+    {
+        const bool up = (lane & 7) >= 4;
+        const float send = up ? y[0] : y[1];
+        const float keep = up ? y[1] : y[0];
+        z = keep + dpp_mov<kDppHalfMirror>(send);
+    }
+    z += dpp_mov<kDppQuadSwap2>(z);
+    z += dpp_mov<kDppQuadSwap1>(z);
+    return z;
+}
+
 struct Eval3dParams {
     TileGrid g;
     const float* means;
