@@ -148,8 +148,8 @@ def main():
                                                        W, H, tsx, tsy, ro, rd, off, fl),
                        (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * fwd_loaded),
         "eval3d_bwd": (lambda: _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off,
-                                                       fl, alpha, last, g_rgb, g_d, g_a),
-                       (24 + 8 + 4 * cdim + 8 + 24) * W * H + (48 + 4 * cdim) * bwd_loaded + (11 + cdim) * 4 * N),
+                                                       fl, alpha, last, g_rgb, g_d, g_a, False),
+                       (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * bwd_loaded + (11 + cdim) * 4 * N),
         "sh_bwd": (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh, None, False,
                                                             v_colors, None),
                    (36 + 24 * K) * N) if sh is not None else None,

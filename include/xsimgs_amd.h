@@ -199,7 +199,7 @@ typedef struct {
     float* v_scales;
     float* v_opacities;
     float* v_colors;               /* NULL when cdim == 0 */
-    float* v_ray_o;
+    float* v_ray_o;                /* both NULL: per-pixel ray gradients are not computed */
     float* v_ray_d;
     float* v_velocity;             /* dynamic only */
     float* v_time_delta;           /* dynamic only */

@@ -192,3 +192,26 @@ def test_eval3d_fwd_bwd_cfg0(dev, cfg0):
         fc = frac_close(np_(a), b, GRAD_ATOL, GRAD_RTOL)
         print(report(name, np_(a), b), "frac", fc)
         assert fc > 0.999, name
+
+
+def test_eval3d_bwd_without_ray_grads(dev, cfg0):
+    """ray_grads=False (autograd when rays need no gradient) gives the same Gaussian gradients."""
+    sc, st = cfg0
+    spec = sc.cameras[0]
+    cam, off, fl, ro, rd = _binned(st, sc, dev)
+    scales = torch.exp(st.log_scales)
+    opac = torch.sigmoid(st.opacity_logits)
+    colors = _C.spherical_harmonics_fused_fwd(0, cam.pose.t, st.means, st.sh, None, False)
+    _, _, alpha, last = _C.rasterize_eval3d_fwd(st.means, st.quats, scales, colors.unsqueeze(0), opac.view(1, -1),
+                                                spec.width, spec.height, 16, 16, ro, rd, off, fl)
+    g = torch.Generator().manual_seed(12)
+    vr = (torch.randn(spec.height, spec.width, 3, generator=g) * 1e-3).to(dev)
+    vd = (torch.randn(spec.height, spec.width, generator=g) * 1e-3).to(dev)
+    va = (torch.randn(spec.height, spec.width, generator=g) * 1e-3).to(dev)
+    a = _C.rasterize_eval3d_bwd(st.means, scales, st.quats, opac, colors, ro, rd, 16, 16, off, fl, alpha, last,
+                                vr, vd, va)
+    b = _C.rasterize_eval3d_bwd(st.means, scales, st.quats, opac, colors, ro, rd, 16, 16, off, fl, alpha, last,
+                                vr, vd, va, False)
+    assert b[5] is None and b[6] is None
+    for x, y in zip(a[:5], b[:5]):
+        assert frac_close(np_(y), np_(x), GRAD_ATOL, GRAD_RTOL) == 1.0

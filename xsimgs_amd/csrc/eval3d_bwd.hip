@@ -25,7 +25,7 @@ XSG_DEV int wave_max(int v) {
     return v;
 }
 
-template <int CDIM, bool DYN>
+template <int CDIM, bool DYN, bool RG>
 __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p) {
     constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;
     constexpr int CS = CDIM > 0 ? CDIM : 1;
@@ -192,8 +192,10 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
                         acc[CDIM + 15] = -v_omm.z * rt;
                         v_t += -dot(v_omm, vel);
                     }
-                    v_ro = v_ro + v_omm;
-                    v_rd = v_rd + rows_tmul(r0, r1, r2, v_grd);
+                    if constexpr (RG) {
+                        v_ro = v_ro + v_omm;
+                        v_rd = v_rd + rows_tmul(r0, r1, r2, v_grd);
+                    }
                 }
 #pragma unroll
                 for (int k = 0; k < CDIM; ++k) buffer[k] += rgb[k] * fac;
@@ -223,26 +225,39 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
         }
     }
     if (c.inside) {
-        st3(p.v_ray_o + 3 * c.pix, v_ro);
-        st3(p.v_ray_d + 3 * c.pix, v_rd);
+        if constexpr (RG) {
+            st3(p.v_ray_o + 3 * c.pix, v_ro);
+            st3(p.v_ray_d + 3 * c.pix, v_rd);
+        }
         if constexpr (DYN) p.v_time[c.pix] = v_t;
     }
 }
 
+// Variants without per-pixel ray gradients exist for CDIM <= kColorLdsMax; larger CDIMs always
+// compute them (the C-ABI then needs the ray-gradient buffers).
 template <int CDIM>
-int launch_cdim(bool dyn, const Eval3dParams& p, hipStream_t s) {
+int launch_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t s) {
     const int n_blocks = p.g.n_tiles_w * p.g.n_tiles_h * p.g.n_cams;
     const int bs = p.g.tile_w * p.g.tile_h;
-    if (dyn) eval3d_bwd_kernel<CDIM, true><<<n_blocks, bs, 0, s>>>(p);
-    else eval3d_bwd_kernel<CDIM, false><<<n_blocks, bs, 0, s>>>(p);
+    if constexpr (CDIM <= kColorLdsMax) {
+        if (!ray_grads) {
+            if (dyn) eval3d_bwd_kernel<CDIM, true, false><<<n_blocks, bs, 0, s>>>(p);
+            else eval3d_bwd_kernel<CDIM, false, false><<<n_blocks, bs, 0, s>>>(p);
+            return XSG_OK;
+        }
+    }
+    if (!p.v_ray_o || !p.v_ray_d) return xsg_fail(XSG_ERR_INVALID, "ray gradient buffers are required for cdim %d", CDIM);
+    if (dyn) eval3d_bwd_kernel<CDIM, true, true><<<n_blocks, bs, 0, s>>>(p);
+    else eval3d_bwd_kernel<CDIM, false, true><<<n_blocks, bs, 0, s>>>(p);
     return XSG_OK;
 }
 
 }  // namespace
 
 int eval3d_bwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s) {
+    const bool ray_grads = p.v_ray_o != nullptr;
     switch (cdim) {
-#define XSG_CASE(C) case C: return launch_cdim<C>(dyn, p, s);
+#define XSG_CASE(C) case C: return launch_cdim<C>(dyn, ray_grads, p, s);
         XSG_CDIM_LIST(XSG_CASE)
 #undef XSG_CASE
         default: return xsg_fail(XSG_ERR_INVALID, "unsupported feature dimension: %d", cdim);

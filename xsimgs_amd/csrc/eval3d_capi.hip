@@ -155,7 +155,8 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
         return xsg_fail(XSG_ERR_INVALID, "dynamic backward needs both velocity and ray_time_delta");
     if (!a->render_alpha || !a->last_ids || !a->v_depth || !a->v_alpha || (a->cdim > 0 && !a->v_rgb) ||
         !a->v_means || !a->v_quats || !a->v_scales || !a->v_opacities || (a->cdim > 0 && !a->v_colors) ||
-        !a->v_ray_o || !a->v_ray_d || (dyn && (!a->v_velocity || !a->v_time_delta)) || !workspace)
+        ((a->v_ray_o == nullptr) != (a->v_ray_d == nullptr)) ||
+        (dyn && (!a->v_velocity || !a->v_time_delta)) || !workspace)
         return xsg_fail(XSG_ERR_INVALID, "xsg_eval3d_bwd: null buffer");
     const hipStream_t s = (hipStream_t)stream;
     p.render_alpha = a->render_alpha; p.last_ids = a->last_ids; p.v_rgb = a->v_rgb; p.v_depth = a->v_depth;

@@ -159,10 +159,30 @@ XSG_DEV bool mask_ok(const uint32_t* mask, int64_t i) {
 
 constexpr int odd_stride(int n) { return (n % 2 == 0) ? n + 1 : n; }
 
-// Cooperative copy of `rows` rows of `row_len` floats (global row pitch `pitch`) into LDS rows of
-// stride S. Consecutive threads read consecutive addresses of the chunk.
+// Cooperative copy of `rows` rows of ROW_LEN floats (global row pitch `pitch`) into LDS rows of
+// stride S. A full tile of contiguous rows is copied with every thread's 16-byte loads issued
+// before any LDS store, so each wavefront keeps ROW_LEN / 4 loads in flight; other tiles use a
+// plain strided loop.
 template <int ROW_LEN, int S>
 XSG_DEV void stage_rows(float* lds, const float* __restrict__ src, int64_t pitch, int rows) {
+    if constexpr (ROW_LEN % 4 == 0) {
+        if (rows == kBlock && pitch == ROW_LEN && ((uintptr_t)src & 15) == 0) {
+            constexpr int PER = ROW_LEN / 4;  // 16-byte vectors per thread
+            typedef float v4f __attribute__((ext_vector_type(4)));
+            const v4f* src4 = reinterpret_cast<const v4f*>(src);
+            v4f v[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) v[k] = __builtin_nontemporal_load(src4 + k * kBlock + threadIdx.x);
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int e = 4 * (k * kBlock + (int)threadIdx.x);
+                const int r = e / ROW_LEN, j = e - r * ROW_LEN;
+                float* d = lds + r * S + j;
+                d[0] = v[k].x; d[1] = v[k].y; d[2] = v[k].z; d[3] = v[k].w;
+            }
+            return;
+        }
+    }
     const int total = rows * ROW_LEN;
     for (int e = threadIdx.x; e < total; e += kBlock) {
         const int r = e / ROW_LEN, j = e - r * ROW_LEN;

@@ -124,7 +124,8 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_fwd(
 struct BwdOut {
     Tensor v_points, v_velocity, v_quat, v_scale, v_opacity;
     std::optional<Tensor> v_colors;
-    Tensor v_ray_o, v_ray_d, v_time_delta;
+    std::optional<Tensor> v_ray_o, v_ray_d;
+    Tensor v_time_delta;
 };
 
 // rasterize_eval3d_bwd (eval3d_bwd.cu:297-403) / rasterize_eval3d_dynamic_bwd (eval3d_dynamic_bwd.cu:312-427)
@@ -133,7 +134,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
                        const Tensor& ray_directions, const OptT& ray_time_delta, int64_t tile_size_x,
                        int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
                        const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors,
-                       const Tensor& v_render_depth, const Tensor& v_render_alpha) {
+                       const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads) {
     if (v_render_colors.has_value() && !v_render_colors->is_contiguous())
         throw std::runtime_error("v_render_colors must be contiguous");
     all_contiguous({v_render_depth, v_render_alpha, render_alpha, last_ids});
@@ -149,8 +150,12 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
         o.v_colors = at::zeros_like(*colors);
         cdim = (int)colors->size(1);
     }
-    o.v_ray_o = at::empty_like(ray_origins);
-    o.v_ray_d = at::empty_like(ray_directions);
+    // ray gradients are skipped when the caller does not need them (only kernels with CDIM <= 16
+    // have that variant; larger CDIMs always produce them)
+    if (ray_grads || cdim > 16) {
+        o.v_ray_o = at::empty_like(ray_origins);
+        o.v_ray_d = at::empty_like(ray_directions);
+    }
     xsg_eval3d_args a = base_args(points, quat, scale, colors, opacity, cdim, (int)width, (int)height,
                                   (int)tile_size_x, (int)tile_size_y, ray_origins, ray_directions, tile_offsets,
                                   flatten_ids);
@@ -174,33 +179,33 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     a.v_scales = o.v_scale.data_ptr<float>();
     a.v_opacities = o.v_opacity.data_ptr<float>();
     a.v_colors = o.v_colors.has_value() ? o.v_colors->data_ptr<float>() : nullptr;
-    a.v_ray_o = o.v_ray_o.data_ptr<float>();
-    a.v_ray_d = o.v_ray_d.data_ptr<float>();
+    a.v_ray_o = o.v_ray_o.has_value() ? o.v_ray_o->data_ptr<float>() : nullptr;
+    a.v_ray_d = o.v_ray_d.has_value() ? o.v_ray_d->data_ptr<float>() : nullptr;
     Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(a.n, cdim));
     check_rc(xsg_eval3d_bwd(&a, ws.data_ptr(), stream_of(points)));
     return o;
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, Tensor, Tensor> rasterize_eval3d_bwd(
+std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT> rasterize_eval3d_bwd(
     const Tensor& points, const Tensor& scale, const Tensor& quat, const Tensor& opacity, const OptT& colors,
     const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
     const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
-    const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha) {
+    const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads) {
     BwdOut o = eval3d_bwd_impl(points, std::nullopt, scale, quat, opacity, colors, ray_origins, ray_directions,
                                std::nullopt, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
-                               last_ids, v_render_colors, v_render_depth, v_render_alpha);
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads);
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d};
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_bwd(
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, Tensor> rasterize_eval3d_dynamic_bwd(
     const Tensor& points, const Tensor& velocity, const Tensor& scale, const Tensor& quat, const Tensor& opacity,
     const OptT& colors, const Tensor& ray_origins, const Tensor& ray_directions, const Tensor& ray_time_delta,
     int64_t tile_size_x, int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
     const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors, const Tensor& v_render_depth,
-    const Tensor& v_render_alpha) {
+    const Tensor& v_render_alpha, bool ray_grads) {
     BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
                                ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
-                               last_ids, v_render_colors, v_render_depth, v_render_alpha);
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads);
     return {o.v_points, o.v_velocity, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
             o.v_time_delta};
 }
@@ -640,12 +645,23 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
           py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"), py::arg("ray_dirs"),
           py::arg("tile_offsets"), py::arg("flatten_ids"));
-    m.def("rasterize_eval3d_bwd", &rasterize_eval3d_bwd);
+    // positional like the reference (eval3d_bwd.cu:406-408); `ray_grads` (extension, default True)
+    // lets autograd skip the per-pixel ray gradients when the rays do not require grad
+    m.def("rasterize_eval3d_bwd", &rasterize_eval3d_bwd, py::arg("points"), py::arg("scale"), py::arg("quat"),
+          py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"), py::arg("ray_directions"),
+          py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
+          py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
+          py::arg("v_render_alpha"), py::arg("ray_grads") = true);
     m.def("rasterize_eval3d_dynamic_fwd", &rasterize_eval3d_dynamic_fwd, py::arg("means"), py::arg("velocity"),
           py::arg("quats"), py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"),
           py::arg("image_height"), py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"),
           py::arg("ray_dirs"), py::arg("ray_time_delta"), py::arg("tile_offsets"), py::arg("flatten_ids"));
-    m.def("rasterize_eval3d_dynamic_bwd", &rasterize_eval3d_dynamic_bwd);
+    m.def("rasterize_eval3d_dynamic_bwd", &rasterize_eval3d_dynamic_bwd, py::arg("points"), py::arg("velocity"),
+          py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"),
+          py::arg("ray_directions"), py::arg("ray_time_delta"), py::arg("tile_size_x"), py::arg("tile_size_y"),
+          py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("render_alpha"), py::arg("last_ids"),
+          py::arg("v_render_colors"), py::arg("v_render_depth"), py::arg("v_render_alpha"),
+          py::arg("ray_grads") = true);
     m.def("eval3d_supported_ndims", &eval3d_supported_ndims);
 
     // color (csrc/color/sh_bind.cpp)

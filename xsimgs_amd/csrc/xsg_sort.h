@@ -3,9 +3,8 @@
 // Radix sort pass = three kernels:
 //   upsweep   : per-block digit histograms, stored digit-major hist[d * nb + b]
 //   scan_hist : one block per digit, exclusive scan over blocks + digit totals
-//   downsweep : per block, 16 rounds of 256 keys; a key's rank among equal digits inside its
-//               wavefront comes from 64-bit ballots over the digit bits (wave64 match), wave
-//               counts are combined in LDS, and a running per-digit base keeps the pass stable.
+//   downsweep : per block, wave-private ranking of contiguous segments (wave64 ballot match),
+//               then an LDS reorder by digit and coalesced stores of each digit's run.
 #pragma once
 #include "xsg_common.h"
 
@@ -108,6 +107,12 @@ struct PlainOut {
     XSG_DEV void put(int64_t pos, K k, V v) const { keys[pos] = k; vals[pos] = v; }
 };
 
+// Downsweep of one pass. Each wavefront ranks its own contiguous 1024-key segment of the block's
+// tile in 16 steps of 64 keys: equal digits inside a step are found with 64-bit ballots over the
+// digit bits, and a wave-private counter per digit (in LDS, no block barrier) carries the rank
+// across steps. The block then combines the four waves' counts, reorders its keys by digit in
+// LDS and writes them out so that consecutive lanes store consecutive addresses of a digit's run.
+// Segments, steps and lanes are visited in input order, so the pass is stable.
 template <typename K, typename V, typename Out>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restrict__ keys_in,
                                                               const V* __restrict__ vals_in, int64_t n,
@@ -115,51 +120,76 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
                                                               const uint32_t* __restrict__ hist,
                                                               const uint32_t* __restrict__ digit_total,
                                                               unsigned nb, Out out) {
-    __shared__ uint32_t base[kRadix];
+    constexpr int kSeg = kSortTile / kWaves;  // keys per wave
+    constexpr int kSteps = kSeg / 64;
     __shared__ uint32_t wcnt[kWaves][kRadix];
+    __shared__ uint32_t gbase[kRadix];
+    __shared__ uint32_t lpre[kRadix];
     __shared__ uint32_t scan_lds[kWaves];
+    __shared__ K skeys[kSortTile];
+    __shared__ V svals[kSortTile];
     const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
+    const int64_t tile0 = (int64_t)blockIdx.x * kSortTile;
+    const int n_tile = (int)min<int64_t>(kSortTile, n - tile0);
     {
         uint32_t tot;
         const uint32_t dprefix = block_exclusive_scan<uint32_t>(digit_total[t], scan_lds, tot);
-        base[t] = dprefix + hist[(int64_t)t * nb + blockIdx.x];
+        gbase[t] = dprefix + hist[(int64_t)t * nb + blockIdx.x];
     }
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wcnt[w][t] = 0;
     __syncthreads();
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    const int64_t tile0 = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t idx = tile0 + (int64_t)k * kSortBlock + t;
-        if (tile0 + (int64_t)k * kSortBlock >= n) break;  // block-uniform
-        const bool valid = idx < n;
-        K key = 0;
-        V val = 0;
+    K key[kSteps];
+    V val[kSteps];
+    uint32_t rank[kSteps];
+    const int seg0 = wave * kSeg;
+#pragma unroll
+    for (int r = 0; r < kSteps; ++r) {
+        const int li = seg0 + r * 64 + lane;
+        const bool valid = li < n_tile;
+        key[r] = 0;
+        val[r] = 0;
         uint32_t d = 0;
         if (valid) {
-            key = keys_in[idx];
-            val = vals_in[idx];
-            d = digit_of<K>(key, shift, bits);
+            key[r] = keys_in[tile0 + li];
+            val[r] = vals_in[tile0 + li];
+            d = digit_of<K>(key[r], shift, bits);
         }
         uint64_t peers = __ballot(valid);
         for (int b = 0; b < bits; ++b) {
             const uint64_t m = __ballot((d >> b) & 1u);
             peers &= ((d >> b) & 1u) ? m : ~m;
         }
-        const uint32_t rank = (uint32_t)__popcll(peers & lt_mask);
-        if (valid && rank == 0) wcnt[wave][d] = (uint32_t)__popcll(peers);
-        __syncthreads();
-        if (valid) {
-            uint32_t off = base[d] + rank;
-            for (int w = 0; w < wave; ++w) off += wcnt[w][d];
-            out.put(off, key, val);
-        }
-        __syncthreads();
-        uint32_t s = 0;
+        const uint32_t before = (uint32_t)__popcll(peers & lt_mask);
+        const uint32_t base = valid ? wcnt[wave][d] : 0u;
+        rank[r] = base + before;
+        if (valid && before == 0) wcnt[wave][d] = base + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+    {  // per digit: exclusive prefix over the waves, block-local exclusive prefix over digits
+        uint32_t c[kWaves], s = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) { s += wcnt[w][t]; wcnt[w][t] = 0; }
-        base[t] += s;
-        __syncthreads();
+        for (int w = 0; w < kWaves; ++w) { c[w] = wcnt[w][t]; wcnt[w][t] = s; s += c[w]; }
+        uint32_t tot;
+        lpre[t] = block_exclusive_scan<uint32_t>(s, scan_lds, tot);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kSteps; ++r) {
+        const int li = seg0 + r * 64 + lane;
+        if (li < n_tile) {
+            const uint32_t d = digit_of<K>(key[r], shift, bits);
+            const uint32_t pos = lpre[d] + wcnt[wave][d] + rank[r];
+            skeys[pos] = key[r];
+            svals[pos] = val[r];
+        }
+    }
+    __syncthreads();
+    for (int i = t; i < n_tile; i += kSortBlock) {
+        const K k = skeys[i];
+        const uint32_t d = digit_of<K>(k, shift, bits);
+        out.put((int64_t)gbase[d] + (i - lpre[d]), k, svals[i]);
     }
 }
 

@@ -30,7 +30,8 @@ class UTGSDynamicRasterize(torch.autograd.Function):
             positions, velocity, scale, rotation, density, colors, ray_o, ray_d, ray_time_delta,
             ctx.tile_size_x, ctx.tile_size_y, isect_offsets, flatten_ids, out_alpha, last_ids,
             grad_rgb.contiguous() if grad_rgb is not None else None, grad_depth.contiguous(),
-            grad_alpha.contiguous())
+            grad_alpha.contiguous(),
+            ctx.needs_input_grad[6] or ctx.needs_input_grad[7])
         return apply_grad_mask(ctx, list(grads) + [None, None, None, None])
 
 
