@@ -36,7 +36,32 @@ def parse():
     p.add_argument("--stage-reps", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-stages", default="", help="comma list of stages to run alone (for rocprof)")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 256 MiB device copy 5 times (scale of the rocprofv3 byte counters)")
     return p.parse_args()
+
+
+# Algorithmic VALU work of the compositor per (pixel, Gaussian) pair, counted from the kernels'
+# arithmetic (add, mul, fma, compare, exp, rcp and rsqrt each one op; every pair with a fixed tile
+# origin): alpha evaluation 43 (M rd 15, normalise 9, cross 9, squared norm 5, power / exp /
+# opacity / clamp / threshold 5); forward composite 24 more per contributing pair (hit distance 12,
+# transmittance and test 4, depth 2, 2 per colour channel); backward 170 more per contributing pair
+# at 3 colour channels without ray gradients (the eval3d_bwd.cu:172-271 chain).
+FLOPS_EVAL = 43
+FLOPS_FWD_CONTRIB = 18          # + 2 per colour channel
+FLOPS_BWD_CONTRIB = 146         # + 8 per colour channel
+FP32_VALU_PEAK_TFLOPS = 78.6    # non-packed FP32 (packed FP32 ops are disabled in this build)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "eval3d_bwd_cfg2_traffic.json")
+
+
+def calibrate_copy(torch):
+    n = 64 << 20                                   # 64 Mi floats = 256 MiB each way
+    x = torch.ones(n, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 5}))
 
 
 def event_time_ms(fn, reps, torch):
@@ -63,8 +88,12 @@ def main():
     import numpy as np
     import torch
 
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     import xsimgs_amd  # noqa: F401  (fails loudly without the native libraries)
     from xsimgs_amd import _C, frame, synthetic
+    from xsimgs_amd.rendering import rasterize as rz
 
     dev = torch.device("cuda:0")
     sc = synthetic.make(args.config, seed=args.seed)
@@ -80,15 +109,36 @@ def main():
         for ci in range(n_cams):
             frame.render_frame(st, backward=True, grads=grads[ci], cam_index=ci)
 
+    # the compositor calls are bracketed by HIP events on the stream they run on (torch's current
+    # stream), inside the timed steps
+    live = {"eval3d_fwd": [], "eval3d_bwd": []}
+    orig = {"eval3d_fwd": rz.rasterize_eval3d_fwd, "eval3d_bwd": rz.rasterize_eval3d_bwd}
+
+    def timed(name):
+        fn = orig[name]
+
+        def call(*a, **k):
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            out = fn(*a, **k)
+            ev1.record()
+            live[name].append((ev0, ev1))
+            return out
+        return call
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = timed("eval3d_fwd"), timed("eval3d_bwd")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = orig["eval3d_fwd"], orig["eval3d_bwd"]
     ms = (t1 - t0) * 1e3 / args.steps
+    live_ms = {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in live.items() if v}
     mpix = W * H * n_cams / (ms * 1e-3) / 1e6
 
     # ---------------------------------------------------------------- per-stage timing
@@ -112,8 +162,11 @@ def main():
                                           tile_size_x=tsx, tile_size_y=tsy)
         off = _C.isect_offset_encode(ids, ntx, nty)
         ro, rd = cam.camera_rays(W, H)
+        pairs = torch.zeros(2, dtype=torch.int64, device=dev)
         rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0),
-                                                          opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl)
+                                                          opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl,
+                                                          pair_counts=pairs)
+        fwd_evaluated, contributing = (int(x) for x in pairs.cpu())
         g_rgb, g_d, g_a = grads[0]
         bwd_out = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, alpha,
                                           last, g_rgb, g_d, g_a)
@@ -131,6 +184,9 @@ def main():
         bs = tsx * tsy
         fwd_batches = ((tile_max - starts + 2).clamp(min=1) + bs - 1) // bs
         fwd_loaded = int(torch.minimum(rng, fwd_batches * bs).sum())
+        # backward: every pixel evaluates its tile's list from the start up to its last_id
+        tile_of = ((torch.arange(H, device=dev) // tsy)[:, None] * ntx + (torch.arange(W, device=dev) // tsx)[None, :])
+        bwd_evaluated = int((last.long() - starts[tile_of] + 1).clamp(min=0).sum())
         vis = int((tpg > 0).sum())
         key_bits = 32 + int(math.floor(math.log2(ntx * nty))) + 1
 
@@ -165,15 +221,29 @@ def main():
         gbs = nbytes / (t * 1e-3) / 1e9
         stage_rows[name] = {"ms": round(t, 4), "alg_bytes": int(nbytes), "GB/s": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-    dom = max(stage_rows, key=lambda k: stage_rows[k]["ms"]) if stage_rows else None
-    roofline = None
-    if dom is not None:
-        r = stage_rows[dom]
-        roofline = {"kernel": dom, "bound": "hbm", "achieved": r["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": r["hbm_frac"], "traffic": None}
-        if dom.startswith("eval3d"):
-            roofline["note"] = ("compositor is VALU/LDS/atomic-bound (no dense contraction, no MFMA); the HBM "
-                                "fraction of its algorithmic bytes is reported as defined")
+    # ---------------------------------------------------------------- roofline of the dominant kernel
+    flops = {"eval3d_fwd": FLOPS_EVAL * fwd_evaluated + (FLOPS_FWD_CONTRIB + 2 * cdim) * contributing,
+             "eval3d_bwd": FLOPS_EVAL * bwd_evaluated + (FLOPS_BWD_CONTRIB + 8 * cdim) * contributing}
+    dom = max(live_ms, key=live_ms.get)
+    t_dom = live_ms[dom]
+    alg = stages[dom][1]
+    gbs = alg / (t_dom * 1e-3) / 1e9
+    tfl = flops[dom] / (t_dom * 1e-3) / 1e12
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "launch_ms": round(t_dom, 4), "alg_bytes_per_launch": int(alg),
+                "valu": {"achieved": round(tfl, 2), "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tfl / FP32_VALU_PEAK_TFLOPS, 4), "flops_per_launch": int(flops[dom])},
+                "note": ("the compositor has no dense contraction (no MFMA) and is VALU / LDS / atomic bound: "
+                         "the HBM fraction of its algorithmic bytes is reported as defined, the VALU fraction "
+                         "against non-packed FP32 beside it")}
+    if os.path.exists(TRAFFIC_FILE) and args.config == "cfg2" and dom == "eval3d_bwd":
+        with open(TRAFFIC_FILE) as fh:
+            tr = json.load(fh)
+        roofline["traffic"] = int(tr["fetch_kib_per_dispatch"] * 1024 * tr["fetch_scale"] +
+                                  tr["write_kib_per_dispatch"] * 1024 * tr["write_scale"])
+        roofline["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
+    pair_stats = {"fwd_evaluated": fwd_evaluated, "bwd_evaluated": bwd_evaluated, "contributing": contributing}
 
     # ---------------------------------------------------------------- CPU baseline (oracle, same frame)
     cpu = None
@@ -232,6 +302,8 @@ def main():
                    "n_gaussians": N, "width": W, "height": H, "n_cams": n_cams, "tile": [tsx, tsy],
                    "n_isects": n_isects, "visible_gaussians": vis, "parallelism": "single GPU"},
         "stages": stage_rows,
+        "live_ms": {k: round(v, 4) for k, v in live_ms.items()},
+        "pairs": pair_stats,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

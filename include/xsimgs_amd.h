@@ -203,6 +203,9 @@ typedef struct {
     float* v_ray_d;
     float* v_velocity;             /* dynamic only */
     float* v_time_delta;           /* dynamic only */
+    /* forward, optional (NULL: not counted): pair_counts[0] += (pixel, Gaussian) pairs whose alpha
+     * was evaluated, pair_counts[1] += pairs that were composited; the caller initialises them */
+    uint64_t* pair_counts;
 } xsg_eval3d_args;
 
 int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream);

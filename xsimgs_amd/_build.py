@@ -52,12 +52,25 @@ def _run(cmd, cwd=None):
     return out
 
 
-def build_hip(jobs: int | None = None, verbose: bool = False) -> str:
+def _stale(obj: str, src: str) -> bool:
+    """True when obj is missing or older than src or any header beside it."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [src] + [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith(".h")]
+    deps.append(os.path.join(ROOT, "include", "xsimgs_amd.h"))
+    return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
+
+
+def build_hip(jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> str:
+    """Compile every HIP source (only the stale ones when incremental) and link the library."""
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 4)
 
     def compile_one(src):
         obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+        if incremental and not _stale(obj, os.path.join(CSRC, src)):
+            return obj
         _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
         if verbose:
             print("  built", src, flush=True)
@@ -98,13 +111,12 @@ def build_oracle() -> None:
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
 
 
-def build_all(verbose: bool = False) -> None:
-    from concurrent.futures import ThreadPoolExecutor as TPE
-    build_hip(verbose=verbose)
+def build_all(verbose: bool = False, incremental: bool = False) -> None:
+    build_hip(verbose=verbose, incremental=incremental)
     build_ext(verbose=verbose)
 
 
 if __name__ == "__main__":
-    build_all(verbose=True)
+    build_all(verbose=True, incremental="--incremental" in sys.argv)
     if "--oracle" in sys.argv:
         build_oracle()

@@ -134,6 +134,7 @@ extern "C" int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream) {
         return xsg_fail(XSG_ERR_INVALID, "xsg_eval3d_fwd: null output");
     if ((int64_t)a->width * a->height == 0) return XSG_OK;
     p.out_rgb = a->out_rgb; p.out_depth = a->out_depth; p.out_alpha = a->out_alpha; p.out_last = a->out_last_ids;
+    p.pair_counts = (unsigned long long*)a->pair_counts;
     const bool dyn = a->velocity != nullptr || a->ray_time_delta != nullptr;
     rc = eval3d_fwd_launch(a->cdim, dyn, p, (hipStream_t)stream);
     if (rc) return rc;

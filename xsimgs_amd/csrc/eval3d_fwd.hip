@@ -36,6 +36,7 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
 
     float depth = 0.0f, T = 1.0f;
     uint32_t cur_idx = 0;
+    uint32_t n_eval = 0, n_contrib = 0;
     float pix[CS];
 #pragma unroll
     for (int k = 0; k < CS; ++k) pix[k] = 0.f;
@@ -87,6 +88,7 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
             const f3 gcrod = cross(safe_normalize(grd), gro);
             const float power = -0.5f * dot(gcrod, gcrod);
             const float alpha = fminf(0.999f, op * __expf(power));
+            ++n_eval;
             if (alpha < 1.f / 255.f) continue;
             const float hit_t = -dot(gro, grd) * __builtin_amdgcn_rcpf(dot(grd, grd));
             const float next_T = T * (1.0f - alpha);
@@ -108,6 +110,19 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
             }
             cur_idx = batch_start + t;
             T = next_T;
+            ++n_contrib;
+        }
+    }
+    if (p.pair_counts) {  // one atomic per wave and counter
+        unsigned long long e = n_eval, k = n_contrib;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            e += __shfl_xor(e, off, 64);
+            k += __shfl_xor(k, off, 64);
+        }
+        if (__lane_id() == 0) {
+            atomicAdd(p.pair_counts, e);
+            atomicAdd(p.pair_counts + 1, k);
         }
     }
     if (c.inside) {

@@ -96,9 +96,9 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
     int64_t n_total, const float2* __restrict__ means2d, const float2* __restrict__ radii,
     const float* __restrict__ depths, float tsx, float tsy, int ntx, int nty, int32_t* __restrict__ tpg,
     Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
-    uint64_t* __restrict__ partials) {
+    uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
     __shared__ uint64_t lds[kWaves];
-    uint64_t acc = 0;
+    uint64_t acc = 0, acc_c = 0;
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
     for (int k = 0; k < kSortItems; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
@@ -110,10 +110,12 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
             vcnt[j] = c;
             vkey[j] = __float_as_uint(depths[j]);
             acc += pack_count(c);
+            acc_c += c;
         }
     }
     acc = block_reduce_sum<uint64_t>(acc, lds);
-    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+    acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
+    if (threadIdx.x == 0) { partials[blockIdx.x] = acc; cpart[blockIdx.x] = acc_c; }
 }
 
 // isect_lidar_tiles_kernel (phm_lidar_tiling.cu:96-234) / isect_spherical_tiles_kernel
@@ -128,11 +130,11 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     const float2* __restrict__ radii, const float* __restrict__ depths, const float* __restrict__ elev,
     int n_elev, float u_per_tile, float v_per_tile, int n_v, int32_t* __restrict__ tpg,
     Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
-    uint64_t* __restrict__ partials) {
+    uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
     __shared__ uint64_t lds[kWaves];
     const Camera cam = load_camera(pack, KIND);
     const bool is_static = camera_is_static(cam, vel != nullptr);
-    uint64_t acc = 0;
+    uint64_t acc = 0, acc_c = 0;
     const int64_t base = (int64_t)blockIdx.x * (kSortTile / 2);
     for (int k = 0; k < kSortItems / 2; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
@@ -184,16 +186,23 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
         vkey[2 * j] = __float_as_uint(depths[j]);
         vkey[2 * j + 1] = __float_as_uint(dep2);
         acc += pack_count(ca) + pack_count(cb);
+        acc_c += (uint64_t)ca + cb;
     }
     acc = block_reduce_sum<uint64_t>(acc, lds);
-    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+    acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
+    if (threadIdx.x == 0) { partials[blockIdx.x] = acc; cpart[blockIdx.x] = acc_c; }
 }
 
-// single block: exclusive scan of the block partials in place, grand total at partials[nb]
+// single block: exclusive scan of the block partials in place, grand total at partials[nb]; with
+// `cpart`, also the exact 64-bit sum of cpart[0, nb) at partials[nb + 1] (the packed scan's count
+// field is 32 bits wide, so the host checks that total instead)
 template <typename T>
-__global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb) {
+__global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb,
+                                                               const uint64_t* __restrict__ cpart) {
     __shared__ T lds[kWaves];
+    __shared__ uint64_t lds64[kWaves];
     T carry = 0;
+    uint64_t exact = 0;
     for (unsigned start = 0; start < nb; start += kBlock) {
         const unsigned i = start + threadIdx.x;
         const T v = i < nb ? partials[i] : (T)0;
@@ -201,8 +210,12 @@ __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ p
         const T ex = block_exclusive_scan<T>(v, lds, tot);
         if (i < nb) partials[i] = carry + ex;
         carry += tot;
+        if (cpart) exact += block_reduce_sum<uint64_t>(i < nb ? cpart[i] : 0ull, lds64);
     }
-    if (threadIdx.x == 0) partials[nb] = carry;
+    if (threadIdx.x == 0) {
+        partials[nb] = carry;
+        if (cpart) partials[nb + 1] = (T)exact;
+    }
 }
 
 // Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
@@ -444,7 +457,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
 struct CountWs {
-    Rect* rects; uint32_t* vcnt; uint32_t* vkey; uint64_t* partials;
+    Rect* rects; uint32_t* vcnt; uint32_t* vkey; uint64_t* partials; uint64_t* cpart;
     uint32_t* comp_id; uint32_t* comp_off; uint32_t* comp_key;
     int64_t n_virtual; unsigned nb;
     size_t bytes;
@@ -460,7 +473,8 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     w.rects = (Rect*)(p + off); off += align256(sizeof(Rect) * nv);
     w.vcnt = (uint32_t*)(p + off); off += align256(4 * nv);
     w.vkey = (uint32_t*)(p + off); off += align256(4 * nv);
-    w.partials = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * (w.nb + 1));
+    w.partials = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * (w.nb + 2));
+    w.cpart = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * w.nb);
     w.comp_id = (uint32_t*)(p + off); off += align256(4 * nv);
     w.comp_off = (uint32_t*)(p + off); off += align256(4 * nv);
     w.comp_key = (uint32_t*)(p + off); off += align256(4 * nv);
@@ -531,7 +545,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (g.kind == XSG_TILING_REGULAR) {
         count_regular_kernel<<<w.nb, kBlock, 0, s>>>(nt, (const float2*)d->means2d, (const float2*)d->radii,
                                                      d->depths, (float)d->tile_w, (float)d->tile_h, g.ntx,
-                                                     g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials);
+                                                     g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
     } else {
         if (!d->camera_pack || !d->flags || !d->points || !d->scales || !d->quats)
             return xsg_fail(XSG_ERR_INVALID, "lidar / spherical tiling needs camera and Gaussian tensors");
@@ -544,25 +558,28 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
                 nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
                 d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
                 d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey,
-                w.partials);
+                w.partials, w.cpart);
         } else {
             count_spherical_kernel<XSG_CAM_SPHERICAL, false><<<w.nb, kBlock, 0, s>>>(
                 nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
                 d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths, nullptr,
-                0, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials);
+                0, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
         }
     }
-    scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb);
+    scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb, w.cpart);
     compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
                                            w.comp_key);
     XSG_TRY_LAUNCH("isect_count");
-    uint64_t total = 0;
-    if (hipMemcpyAsync(&total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess ||
+    uint64_t total[2] = {0, 0};  // packed (visible << 32 | count) total, exact count total
+    if (hipMemcpyAsync(total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return xsg_launch_status("isect_count readback");
-    const int64_t isects = (int64_t)(total & 0xffffffffull);
-    const int64_t vis = (int64_t)(total >> 32);
-    if (isects >= (1ll << 31)) return xsg_fail(XSG_ERR_INVALID, "intersection count overflows int32");
+    // below 2^31 intersections the packed count field never carried, so its visible count is exact
+    if (total[1] >= (1ull << 31))
+        return xsg_fail(XSG_ERR_INVALID, "%llu intersections exceed the int32 range of flatten ids",
+                        (unsigned long long)total[1]);
+    const int64_t isects = (int64_t)total[1];
+    const int64_t vis = (int64_t)(total[0] >> 32);
     if (n_isects) *n_isects = isects;
     if (n_visible) *n_visible = vis;
     return XSG_OK;
@@ -604,7 +621,7 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     // intersection offsets of the instances in depth order
     const unsigned nb_m = sort_blocks(m);
     gather_reduce_kernel<<<nb_m, kBlock, 0, s>>>(m, cw.comp_id, cw.vcnt, fw.spart);
-    scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(fw.spart, nb_m);
+    scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(fw.spart, nb_m, nullptr);
     gather_scan_kernel<<<nb_m, kBlock, 0, s>>>(m, cw.comp_id, cw.vcnt, fw.spart, fw.soffs);
     // expansion into (tile bits, virtual instance) pairs
     const int bits = g.tnb + g.cam_bits;

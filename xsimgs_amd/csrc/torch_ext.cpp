@@ -81,7 +81,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
     const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tsw, int64_t tsh,
     const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta, const Tensor& tile_offsets,
-    const Tensor& flatten_ids) {
+    const Tensor& flatten_ids, const OptT& pair_counts) {
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(means.device());
     auto opt = means.options();
     const int64_t channels = colors.has_value() ? colors->size(-1) : 0;
@@ -98,6 +98,12 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     a.ray_time_delta = fptr(ray_time_delta);
     a.out_rgb = renders.data_ptr<float>(); a.out_depth = depths.data_ptr<float>();
     a.out_alpha = alphas.data_ptr<float>(); a.out_last_ids = last_ids.data_ptr<int32_t>();
+    if (pair_counts.has_value()) {
+        TORCH_CHECK(pair_counts->scalar_type() == at::kLong && pair_counts->numel() >= 2 &&
+                        pair_counts->is_contiguous() && pair_counts->device() == means.device(),
+                    "pair_counts must be a contiguous int64 tensor of 2 elements on the Gaussians' device");
+        a.pair_counts = reinterpret_cast<uint64_t*>(pair_counts->data_ptr<int64_t>());
+    }
     check_rc(xsg_eval3d_fwd(&a, stream_of(means)));
     return {renders, depths, alphas, last_ids};
 }
@@ -105,20 +111,21 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
 std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_fwd(
     const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors, const Tensor& opacities,
     int64_t image_width, int64_t image_height, int64_t tile_size_width, int64_t tile_size_height,
-    const Tensor& ray_origs, const Tensor& ray_dirs, const Tensor& tile_offsets, const Tensor& flatten_ids) {
+    const Tensor& ray_origs, const Tensor& ray_dirs, const Tensor& tile_offsets, const Tensor& flatten_ids,
+    const OptT& pair_counts) {
     return eval3d_fwd_impl(means, std::nullopt, quats, scales, colors, opacities, image_width, image_height,
                            tile_size_width, tile_size_height, ray_origs, ray_dirs, std::nullopt, tile_offsets,
-                           flatten_ids);
+                           flatten_ids, pair_counts);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_fwd(
     const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
     const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tile_size_width,
     int64_t tile_size_height, const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta,
-    const Tensor& tile_offsets, const Tensor& flatten_ids) {
+    const Tensor& tile_offsets, const Tensor& flatten_ids, const OptT& pair_counts) {
     return eval3d_fwd_impl(means, velocity, quats, scales, colors, opacities, image_width, image_height,
                            tile_size_width, tile_size_height, ray_origs, ray_dirs, ray_time_delta, tile_offsets,
-                           flatten_ids);
+                           flatten_ids, pair_counts);
 }
 
 struct BwdOut {
@@ -141,13 +148,14 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(points.device());
     const int64_t width = ray_origins.size(1), height = ray_origins.size(0);
     BwdOut o;
-    o.v_points = at::zeros_like(points);
+    // every gradient buffer is zero-filled (or fully written) by xsg_eval3d_bwd itself
+    o.v_points = at::empty_like(points);
     o.v_scale = at::empty_like(scale);
     o.v_quat = at::empty_like(quat);
-    o.v_opacity = at::zeros_like(opacity);
+    o.v_opacity = at::empty_like(opacity);
     int cdim = 0;
     if (colors.has_value()) {
-        o.v_colors = at::zeros_like(*colors);
+        o.v_colors = at::empty_like(*colors);
         cdim = (int)colors->size(1);
     }
     // ray gradients are skipped when the caller does not need them (only kernels with CDIM <= 16
@@ -162,7 +170,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     if (velocity.has_value()) {
         check_f32(*velocity, "velocity");
         all_contiguous({*velocity, *ray_time_delta});
-        o.v_velocity = at::zeros_like(*velocity);
+        o.v_velocity = at::empty_like(*velocity);
         o.v_time_delta = at::empty_like(*ray_time_delta);
         a.velocity = fptr(velocity);
         a.ray_time_delta = fptr(ray_time_delta);
@@ -644,7 +652,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("rasterize_eval3d_fwd", &rasterize_eval3d_fwd, py::arg("means"), py::arg("quats"), py::arg("scales"),
           py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
           py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"), py::arg("ray_dirs"),
-          py::arg("tile_offsets"), py::arg("flatten_ids"));
+          py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("pair_counts") = py::none());
     // positional like the reference (eval3d_bwd.cu:406-408); `ray_grads` (extension, default True)
     // lets autograd skip the per-pixel ray gradients when the rays do not require grad
     m.def("rasterize_eval3d_bwd", &rasterize_eval3d_bwd, py::arg("points"), py::arg("scale"), py::arg("quat"),
@@ -655,7 +663,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("rasterize_eval3d_dynamic_fwd", &rasterize_eval3d_dynamic_fwd, py::arg("means"), py::arg("velocity"),
           py::arg("quats"), py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"),
           py::arg("image_height"), py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"),
-          py::arg("ray_dirs"), py::arg("ray_time_delta"), py::arg("tile_offsets"), py::arg("flatten_ids"));
+          py::arg("ray_dirs"), py::arg("ray_time_delta"), py::arg("tile_offsets"), py::arg("flatten_ids"),
+          py::arg("pair_counts") = py::none());
     m.def("rasterize_eval3d_dynamic_bwd", &rasterize_eval3d_dynamic_bwd, py::arg("points"), py::arg("velocity"),
           py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"),
           py::arg("ray_directions"), py::arg("ray_time_delta"), py::arg("tile_size_x"), py::arg("tile_size_y"),

@@ -184,6 +184,7 @@ struct Eval3dParams {
     float* v_velocity;
     float* v_time;
     float* v_mt;         // workspace [n, 9]: sum of dL/dM^T per Gaussian (row-major of M^T)
+    unsigned long long* pair_counts;  // forward, optional: += [evaluated, contributing] pairs
 };
 
 int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
