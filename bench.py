@@ -211,11 +211,12 @@ def main():
                    (36 + 24 * K) * N) if sh is not None else None,
     }
     stages = {k: v for k, v in stages.items() if v is not None}
+    timed_stages = stages
     if args.profile_stages:
         keep = set(args.profile_stages.split(","))
-        stages = {k: v for k, v in stages.items() if k in keep}
+        timed_stages = {k: v for k, v in stages.items() if k in keep}
     stage_rows = {}
-    for name, (fn, nbytes) in stages.items():
+    for name, (fn, nbytes) in timed_stages.items():
         with torch.no_grad():
             t = event_time_ms(fn, args.stage_reps, torch)
         gbs = nbytes / (t * 1e-3) / 1e9

@@ -129,6 +129,8 @@ typedef struct {
     float img_width, img_height;  /* image size (float, as the reference lidar/spherical ops take it) */
     int tile_w, tile_h;
     float ut_alpha, ut_beta, ut_kappa;
+    int sort;                 /* 1 when xsg_isect_fill will sort: xsg_isect_count then also orders the
+                                 spans by depth before its readback; xsg_isect_fill must get the same */
 } xsg_isect_desc;
 
 /* geometry derived from a descriptor: tiles along u / v, tile count, key bits above 32 */
@@ -136,18 +138,20 @@ int xsg_isect_geometry(const xsg_isect_desc* d, int* n_tiles_w, int* n_tiles_h, 
                        int* key_bits_above_32);
 
 size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d);
-/* Pass 1: tiles per Gaussian into tiles_per_gauss [n_cams*n]; *n_isects (host) receives the total
- * and *n_visible the number of non-empty spans, which xsg_isect_fill takes back. Blocks on
- * `stream` for that one device->host copy. `workspace` carries state into xsg_isect_fill. */
+/* Pass 1: tiles per Gaussian into tiles_per_gauss [n_cams*n]; on the host, *n_isects receives the
+ * total, *n_visible the number of non-empty spans and *n_runs the number of (span, tile row) runs,
+ * which xsg_isect_fill takes back. Blocks on `stream` for that one device->host copy.
+ * `workspace` carries state into xsg_isect_fill. */
 int xsg_isect_count(const xsg_isect_desc* d, int32_t* tiles_per_gauss, void* workspace,
-                    int64_t* n_isects, int64_t* n_visible, xsg_stream_t stream);
+                    int64_t* n_isects, int64_t* n_visible, int64_t* n_runs, xsg_stream_t stream);
 
-size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible);
+size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible,
+                                      int64_t n_runs);
 /* Pass 2: intersection keys ((cam | tile) << 32 | depth bits) and flattened Gaussian ids
  * (cam * n + gaussian); sorted by key bits [0, 32 + key_bits_above_32) with ties in fill order
  * when `sort`, else in the reference's fill order. Consumes (overwrites) count_workspace. */
-int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int sort,
-                   void* count_workspace, void* fill_workspace, int64_t* isect_ids,
+int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int64_t n_runs,
+                   int sort, void* count_workspace, void* fill_workspace, int64_t* isect_ids,
                    int32_t* flatten_ids, xsg_stream_t stream);
 
 /* offsets [n_cams, n_tiles_h, n_tiles_w]: first sorted index of every (camera, tile) */

@@ -72,7 +72,10 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
         }
         __syncthreads();
         const int batch_size = min(bs, c.range_end - (int32_t)batch_start);
-        for (int t = 0; t < batch_size && !done; ++t) {
+        // Branch-free per pair: a finished lane keeps evaluating with its results selected away,
+        // and the wave leaves the batch once all its lanes are finished.
+        for (int t = 0; t < batch_size; ++t) {
+            if (__ballot(!done) == 0) break;  // wave-uniform
             const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t];
             const f3 r0 = mk3(a.x, a.y, a.z), r1 = mk3(bq.x, bq.y, bq.z), r2 = mk3(cq.x, cq.y, cq.z);
             const float op = s_xo[t].w;
@@ -85,18 +88,19 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
                 gro = rows_mul(r0, r1, r2, ro - mu);
             }
             const f3 grd = rows_mul(r0, r1, r2, rd);
-            const f3 gcrod = cross(safe_normalize(grd), gro);
+            const float dd = dot(grd, grd);
+            const float il = inv_len(dd);
+            const f3 gcrod = cross(grd * il, gro);
             const float power = -0.5f * dot(gcrod, gcrod);
             const float alpha = fminf(0.999f, op * __expf(power));
-            ++n_eval;
-            if (alpha < 1.f / 255.f) continue;
-            const float hit_t = -dot(gro, grd) * __builtin_amdgcn_rcpf(dot(grd, grd));
+            const bool live = !done;
+            const bool pass = live && alpha >= 1.f / 255.f;
             const float next_T = T * (1.0f - alpha);
-            if (next_T <= 1e-4f) {  // exclusive termination (eval3d_fwd.cu:135-139)
-                done = true;
-                break;
-            }
-            const float vis = alpha * T;
+            const bool term = pass && next_T <= 1e-4f;  // exclusive termination (eval3d_fwd.cu:135-139)
+            const bool take = pass && !term;
+            done = done || term;
+            const float hit_t = -dot(gro, grd) * (il * il);
+            const float vis = take ? alpha * T : 0.0f;
             depth += vis * hit_t;
             if constexpr (CDIM > 0) {
                 if constexpr (CL > 0) {
@@ -108,9 +112,10 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
                     for (int k = 0; k < CDIM; ++k) pix[k] += cp[k] * vis;
                 }
             }
-            cur_idx = batch_start + t;
-            T = next_T;
-            ++n_contrib;
+            cur_idx = take ? batch_start + t : cur_idx;
+            T = take ? next_T : T;
+            n_eval += live ? 1u : 0u;
+            n_contrib += take ? 1u : 0u;
         }
     }
     if (p.pair_counts) {  // one atomic per wave and counter

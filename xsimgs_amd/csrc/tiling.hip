@@ -18,6 +18,8 @@
 //               the last pass writes the 64-bit keys and flattened ids.
 // Stable by (high bits, low bits, Gaussian order) in both cases, so the result is bit-identical
 // to sorting the reference keys; ties keep Gaussian order as the reference's fill does.
+#include <algorithm>
+
 #include "xsg_sort.h"
 
 UtWeights xsg_ut_weights(float a, float b, float k);
@@ -49,7 +51,7 @@ XSG_DEV Rect regular_rect(float2 m, float2 r, float tsx, float tsy, int ntx, int
 // find_bounds_increasing + tile_limits_irregular (phm_lidar_tiling.cu:35-91), inclusive bounds
 // returned as an exclusive rectangle.
 XSG_DEV Rect lidar_rect(float mx, float my, float rx, float ry, float u_min, float u_max, float u_per_tile,
-                        int n_elev, const float* __restrict__ elev) {
+                        int n_elev, const float* __restrict__ elev, int ntx) {
     Rect out = {0, 0, 0, 0};
     const float lo = fmaxf(mx - rx, u_min), hi = fminf(mx + rx, u_max);
     if (hi <= lo) return out;
@@ -61,20 +63,20 @@ XSG_DEV Rect lidar_rect(float mx, float my, float rx, float ry, float u_min, flo
     const int y0 = min(max(i - 1, 0), n_elev - 1);
     while (i < n_elev && elev[i] < vmax) ++i;
     const int y1 = min(max(i - 1, 0), n_elev - 1);
-    out.x0 = (uint16_t)x0; out.x1 = (uint16_t)(x1 + 1);
+    out.x0 = (uint16_t)min(x0, ntx); out.x1 = (uint16_t)min(x1 + 1, ntx);
     out.y0 = (uint16_t)y0; out.y1 = (uint16_t)(y1 + 1);
     return out;
 }
 
 // tile_limits_regular (phm_spherical_tiling.cu:15-45)
 XSG_DEV Rect spherical_rect(float mx, float my, float rx, float ry, float u_min, float u_max, float u_per_tile,
-                            int n_v, float v_per_tile) {
+                            int n_v, float v_per_tile, int ntx) {
     Rect out = {0, 0, 0, 0};
     const float lo = fmaxf(mx - rx, u_min), hi = fminf(mx + rx, u_max);
     if (hi <= lo) return out;
-    out.x0 = (uint16_t)(int)floorf(lo / u_per_tile);
+    out.x0 = (uint16_t)min((int)floorf(lo / u_per_tile), ntx);
     out.y0 = (uint16_t)min(n_v, max(0, (int)floorf((my - ry) / v_per_tile)));
-    out.x1 = (uint16_t)(int)ceilf(hi / u_per_tile);
+    out.x1 = (uint16_t)min((int)ceilf(hi / u_per_tile), ntx);
     out.y1 = (uint16_t)min(n_v, max(0, (int)ceilf((my + ry) / v_per_tile)));
     return out;
 }
@@ -87,6 +89,7 @@ struct Geometry {
     int tnb;            // tile_n_bits
     int cam_bits;
     int spans;          // virtual instances per Gaussian instance: 1 (regular) or 2 (seam split)
+    int sort;           // the fill sorts (the count pass orders the spans by depth)
 };
 
 // Count pass over Gaussian instances. A block covers kSortTile virtual instances (kSortTile /
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
     Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
     uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
     __shared__ uint64_t lds[kWaves];
-    uint64_t acc = 0, acc_c = 0;
+    uint64_t acc = 0, acc_c = 0, acc_r = 0;
     const int64_t base = (int64_t)blockIdx.x * kSortTile;
     for (int k = 0; k < kSortItems; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
@@ -111,11 +114,17 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
             vkey[j] = __float_as_uint(depths[j]);
             acc += pack_count(c);
             acc_c += c;
+            acc_r += c > 0 ? (uint32_t)(r.y1 - r.y0) : 0u;
         }
     }
     acc = block_reduce_sum<uint64_t>(acc, lds);
     acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
-    if (threadIdx.x == 0) { partials[blockIdx.x] = acc; cpart[blockIdx.x] = acc_c; }
+    acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
+    if (threadIdx.x == 0) {
+        partials[blockIdx.x] = acc;
+        cpart[2 * blockIdx.x] = acc_c;
+        cpart[2 * blockIdx.x + 1] = acc_r;
+    }
 }
 
 // isect_lidar_tiles_kernel (phm_lidar_tiling.cu:96-234) / isect_spherical_tiles_kernel
@@ -128,13 +137,13 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     const float* __restrict__ vel, const float* __restrict__ scales, const float4* __restrict__ quats,
     const float* __restrict__ opacity, const uint8_t* __restrict__ flags, const float2* __restrict__ means2d,
     const float2* __restrict__ radii, const float* __restrict__ depths, const float* __restrict__ elev,
-    int n_elev, float u_per_tile, float v_per_tile, int n_v, int32_t* __restrict__ tpg,
+    int n_elev, float u_per_tile, float v_per_tile, int ntx, int n_v, int32_t* __restrict__ tpg,
     Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
     uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
     __shared__ uint64_t lds[kWaves];
     const Camera cam = load_camera(pack, KIND);
     const bool is_static = camera_is_static(cam, vel != nullptr);
-    uint64_t acc = 0, acc_c = 0;
+    uint64_t acc = 0, acc_c = 0, acc_r = 0;
     const int64_t base = (int64_t)blockIdx.x * (kSortTile / 2);
     for (int k = 0; k < kSortItems / 2; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
@@ -151,8 +160,8 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
             }
             const float2 m = means2d[j];
             const float mx = m.x / img.x, my = m.y / img.y, rx = r.x / img.x, ry = r.y / img.y;
-            if (LIDAR) a = lidar_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, elev);
-            else a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile);
+            if (LIDAR) a = lidar_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, elev, ntx);
+            else a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
             if (flag == 2) {
                 f3 d[3];
                 ut_deltas(ut.sqrt_dl, quats[j], ld3(scales + 3 * j), d);
@@ -171,8 +180,8 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
                         u_max = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f;
                     }
                     const float mx2 = m2.x / img.x, my2 = m2.y / img.y, rx2 = r2.x / img.x, ry2 = r2.y / img.y;
-                    if (LIDAR) b = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev);
-                    else b = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile);
+                    if (LIDAR) b = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev, ntx);
+                    else b = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
                     dep2 = dd;
                 }
             }
@@ -187,22 +196,29 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
         vkey[2 * j + 1] = __float_as_uint(dep2);
         acc += pack_count(ca) + pack_count(cb);
         acc_c += (uint64_t)ca + cb;
+        acc_r += (ca > 0 ? (uint32_t)(a.y1 - a.y0) : 0u) + (cb > 0 ? (uint32_t)(b.y1 - b.y0) : 0u);
     }
     acc = block_reduce_sum<uint64_t>(acc, lds);
     acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
-    if (threadIdx.x == 0) { partials[blockIdx.x] = acc; cpart[blockIdx.x] = acc_c; }
+    acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
+    if (threadIdx.x == 0) {
+        partials[blockIdx.x] = acc;
+        cpart[2 * blockIdx.x] = acc_c;
+        cpart[2 * blockIdx.x + 1] = acc_r;
+    }
 }
 
 // single block: exclusive scan of the block partials in place, grand total at partials[nb]; with
-// `cpart`, also the exact 64-bit sum of cpart[0, nb) at partials[nb + 1] (the packed scan's count
-// field is 32 bits wide, so the host checks that total instead)
+// `cpart` (pairs per block), also the exact 64-bit sums of cpart[2b] and cpart[2b + 1] at
+// partials[nb + 1] and partials[nb + 2] (the packed scan's count field is 32 bits wide, so the
+// host checks the exact intersection total instead)
 template <typename T>
 __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb,
                                                                const uint64_t* __restrict__ cpart) {
     __shared__ T lds[kWaves];
     __shared__ uint64_t lds64[kWaves];
     T carry = 0;
-    uint64_t exact = 0;
+    uint64_t exact = 0, exact2 = 0;
     for (unsigned start = 0; start < nb; start += kBlock) {
         const unsigned i = start + threadIdx.x;
         const T v = i < nb ? partials[i] : (T)0;
@@ -210,11 +226,14 @@ __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ p
         const T ex = block_exclusive_scan<T>(v, lds, tot);
         if (i < nb) partials[i] = carry + ex;
         carry += tot;
-        if (cpart) exact += block_reduce_sum<uint64_t>(i < nb ? cpart[i] : 0ull, lds64);
+        if (cpart) {
+            exact += block_reduce_sum<uint64_t>(i < nb ? cpart[2 * i] : 0ull, lds64);
+            exact2 += block_reduce_sum<uint64_t>(i < nb ? cpart[2 * i + 1] : 0ull, lds64);
+        }
     }
     if (threadIdx.x == 0) {
         partials[nb] = carry;
-        if (cpart) partials[nb + 1] = (T)exact;
+        if (cpart) { partials[nb + 1] = (T)exact; partials[nb + 2] = (T)exact2; }
     }
 }
 
@@ -244,54 +263,10 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
     }
 }
 
-// counts of the depth-sorted virtual instances -> exclusive offsets (reduce / scan partials / scan)
-__global__ __launch_bounds__(kBlock) void gather_reduce_kernel(int64_t m, const uint32_t* __restrict__ ids,
-                                                               const uint32_t* __restrict__ vcnt,
-                                                               uint32_t* __restrict__ partials) {
-    __shared__ uint32_t lds[kWaves];
-    uint32_t acc = 0;
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
-        if (p < m) acc += vcnt[ids[p]];
-    }
-    acc = block_reduce_sum<uint32_t>(acc, lds);
-    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
-}
-
-__global__ __launch_bounds__(kBlock) void gather_scan_kernel(int64_t m, const uint32_t* __restrict__ ids,
-                                                             const uint32_t* __restrict__ vcnt,
-                                                             const uint32_t* __restrict__ partials,
-                                                             uint32_t* __restrict__ offs) {
-    __shared__ uint32_t lds[kWaves];
-    uint32_t carry = partials[blockIdx.x];
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
-        if (base + (int64_t)k * kBlock >= m) break;
-        const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
-        const uint32_t c = p < m ? vcnt[ids[p]] : 0u;
-        uint32_t tot;
-        const uint32_t ex = block_exclusive_scan<uint32_t>(c, lds, tot);
-        if (p < m) offs[p] = carry + ex;
-        carry += tot;
-    }
-}
-
 // 64-bit key exactly as tiling_common.cuh:37,68 builds it: (tile << 32) | sign-extended depth bits
 XSG_DEV int64_t make_key(uint32_t tile_hi, uint32_t depth_bits) {
     return (int64_t)(((uint64_t)tile_hi) << 32) | (int64_t)(int32_t)depth_bits;
 }
-
-struct PairsOut {  // key bits >= 32 under the sort mask, and the virtual instance, for the tile sort
-    uint32_t* hi;
-    uint32_t* id;
-    uint32_t mask;
-    XSG_DEV void put(int64_t o, uint32_t tile_hi, uint32_t v, uint32_t dbits, int spans) const {
-        (void)spans;
-        hi[o] = ((int32_t)dbits < 0) ? mask : (tile_hi & mask);
-        id[o] = v;
-    }
-};
 
 struct FinalOut {  // unsorted output in the reference's fill order
     int64_t* keys;
@@ -299,18 +274,6 @@ struct FinalOut {  // unsorted output in the reference's fill order
     XSG_DEV void put(int64_t o, uint32_t tile_hi, uint32_t v, uint32_t dbits, int spans) const {
         keys[o] = make_key(tile_hi, dbits);
         ids[o] = (int32_t)(v / (uint32_t)spans);
-    }
-};
-
-// Last tile-sort pass: 64-bit key with the virtual instance's depth bits, and the instance id.
-struct SortedKeyOut {
-    int64_t* keys;
-    int32_t* ids;
-    const uint32_t* vkey;
-    int spans;
-    XSG_DEV void put(int64_t pos, uint32_t hi, uint32_t v) const {
-        keys[pos] = make_key(hi, vkey[v]);
-        ids[pos] = (int32_t)(v / (uint32_t)spans);
     }
 };
 
@@ -370,6 +333,314 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(
     }
 }
 
+// ---------------------------------------------------------------- sorted fill by tile rows
+// The sorted fill without sorting the intersections themselves. The visible instances are in
+// depth order (stable). Each instance's rectangle is cut into row runs, one per tile row it
+// covers; the runs (about a ninth of the intersections) are sorted stably by row bucket
+// (camera * n_tiles_y + row), so every row's runs are in depth order. A row's runs are then split
+// into segments of kRunSeg; per segment, a difference array over the columns gives how many of
+// its runs cover each column, and one exclusive scan over (row, column, segment) gives every
+// segment the first output position of each of its columns. Finally a wavefront per (segment,
+// group of 8 columns) walks the segment's runs in order and, per column, ballots the runs that
+// cover it: they take consecutive positions, in depth order, so the stores of a column are
+// contiguous. The order is (camera, tile, depth bits, Gaussian order): the reference's stable
+// sort of its 64-bit keys. Entries of instances with a negative depth belong after every tile
+// (their sign-extended keys saturate the tile bits); they form the last row bucket and are written
+// in run order, which is depth order, then rows, then columns, as the reference orders them.
+constexpr int kRunSeg = 2048;         // runs per row segment
+constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of seg_count_kernel)
+constexpr int kColGroup = 8;    // columns per wavefront in write_runs_kernel
+
+// the visible-span count from the packed grand total of the count scan, for device-sized kernels
+__global__ void visible_count_kernel(const uint64_t* __restrict__ packed_total, uint32_t* __restrict__ m_dev) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *m_dev = (uint32_t)(*packed_total >> 32);
+}
+
+// rows covered by each depth-ordered visible instance -> exclusive run offsets (reduce / scan)
+__global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
+                                                             const uint32_t* __restrict__ ids,
+                                                             const Rect* __restrict__ rects,
+                                                             uint32_t* __restrict__ partials) {
+    __shared__ uint32_t lds[kWaves];
+    m = min(m, (int64_t)*m_dev);
+    uint32_t acc = 0;
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
+        if (p < m) {
+            const Rect r = rects[ids[p]];
+            acc += (uint32_t)(r.y1 - r.y0);
+        }
+    }
+    acc = block_reduce_sum<uint32_t>(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
+                                                           const uint32_t* __restrict__ ids,
+                                                           const Rect* __restrict__ rects,
+                                                           const uint32_t* __restrict__ partials,
+                                                           uint32_t* __restrict__ roff) {
+    __shared__ uint32_t lds[kWaves];
+    m = min(m, (int64_t)*m_dev);
+    uint32_t carry = partials[blockIdx.x];
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        if (base + (int64_t)k * kBlock >= m) break;
+        const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
+        uint32_t h = 0;
+        if (p < m) {
+            const Rect r = rects[ids[p]];
+            h = (uint32_t)(r.y1 - r.y0);
+        }
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(h, lds, tot);
+        if (p < m) roff[p] = carry + ex;
+        carry += tot;
+    }
+}
+
+// Merge-path expansion of the depth-ordered instances into row runs: run r gets its row bucket
+// and the depth-order position of its instance.
+__global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, const uint32_t* __restrict__ roff,
+                                                             const uint32_t* __restrict__ ids,
+                                                             const uint32_t* __restrict__ keys, int64_t m,
+                                                             const Rect* __restrict__ rects, int nty,
+                                                             int64_t n_per_cam, int spans, uint32_t neg_row,
+                                                             uint32_t* __restrict__ out_row,
+                                                             uint32_t* __restrict__ out_p) {
+    __shared__ uint32_t s_off[kExpandPerBlock];
+    __shared__ uint32_t s_row[kExpandPerBlock];  // first row bucket of the instance, or neg_row
+    __shared__ int64_t s_range[2];
+    const int64_t o0 = (int64_t)blockIdx.x * kExpandPerBlock;
+    const int64_t o_end = min(n_runs, o0 + kExpandPerBlock);
+    if (threadIdx.x < 2) {
+        const int64_t x = threadIdx.x == 0 ? o0 : o_end - 1;
+        int64_t lo = 0, hi = m - 1;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if ((int64_t)roff[mid] <= x) lo = mid; else hi = mid - 1;
+        }
+        s_range[threadIdx.x] = lo;
+    }
+    __syncthreads();
+    const int64_t p_lo = s_range[0];
+    const int cnt = (int)min<int64_t>(s_range[1] - p_lo + 1, kExpandPerBlock);
+    for (int e = threadIdx.x; e < cnt; e += kBlock) {
+        const int64_t p = p_lo + e;
+        const uint32_t v = ids[p];
+        const uint32_t inst = v / (uint32_t)spans;
+        const uint32_t cid = n_per_cam > 0 ? (uint32_t)(inst / (uint64_t)n_per_cam) : 0u;
+        s_off[e] = roff[p];
+        s_row[e] = ((int32_t)keys[p] < 0) ? neg_row : cid * (uint32_t)nty + rects[v].y0;
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < kExpandPerBlock; q += kBlock) {
+        const int64_t o = o0 + q;
+        if (o >= o_end) break;
+        int lo = 0, hi = cnt - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if ((int64_t)s_off[mid] <= o) lo = mid; else hi = mid - 1;
+        }
+        const uint32_t row0 = s_row[lo];
+        out_row[o] = row0 == neg_row ? neg_row : row0 + (uint32_t)(o - (int64_t)s_off[lo]);
+        out_p[o] = (uint32_t)(p_lo + lo);
+    }
+}
+
+// row_start[r] = first sorted run of row bucket r (lower bound), r in [0, n_rows]
+__global__ __launch_bounds__(kBlock) void row_bounds_kernel(const uint32_t* __restrict__ rows, int64_t n_runs,
+                                                            int n_rows, uint32_t* __restrict__ row_start) {
+    const int r = blockIdx.x * kBlock + threadIdx.x;
+    if (r > n_rows) return;
+    int64_t lo = 0, hi = n_runs;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (rows[mid] < (uint32_t)r) lo = mid + 1; else hi = mid;
+    }
+    row_start[r] = (uint32_t)lo;
+}
+
+// single block: segments of kRunSeg runs per real row; seg_base = exclusive prefix of the segment
+// counts (total at seg_base[n_real]), seg_row[s] = row of segment s
+__global__ __launch_bounds__(kBlock) void seg_table_kernel(const uint32_t* __restrict__ row_start, int n_real,
+                                                           uint32_t* __restrict__ seg_base,
+                                                           uint32_t* __restrict__ seg_row) {
+    __shared__ uint32_t lds[kWaves];
+    const int per = (n_real + kBlock - 1) / kBlock;
+    const int r0 = threadIdx.x * per, r1 = min(n_real, r0 + per);
+    uint32_t sum = 0;
+    for (int r = r0; r < r1; ++r) sum += (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
+    uint32_t tot;
+    uint32_t run = block_exclusive_scan<uint32_t>(sum, lds, tot);
+    for (int r = r0; r < r1; ++r) {
+        const uint32_t ns = (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
+        seg_base[r] = run;
+        for (uint32_t k = 0; k < ns; ++k) seg_row[run + k] = (uint32_t)r;
+        run += ns;
+    }
+    if (threadIdx.x == 0) seg_base[n_real] = tot;
+}
+
+// Per sorted run: the record the writers read (flatten id, depth bits, column range, row bucket).
+__global__ __launch_bounds__(kBlock) void materialize_runs_kernel(
+    int64_t n_runs, const uint32_t* __restrict__ rows, const uint32_t* __restrict__ rp,
+    const uint32_t* __restrict__ ids, const uint32_t* __restrict__ keys, const Rect* __restrict__ rects,
+    int spans, uint4* __restrict__ rec) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n_runs) return;
+    const uint32_t p = rp[i];
+    const uint32_t v = ids[p];
+    const Rect r = rects[v];
+    rec[i] = make_uint4(v / (uint32_t)spans, keys[p], (uint32_t)r.x0 | ((uint32_t)r.x1 << 16), rows[i]);
+}
+
+// One workgroup per segment: how many of its runs cover each column, from a difference array in
+// LDS (+1 at x0, -1 at x1, then a prefix over the columns), stored at slot (row, column, segment).
+__global__ __launch_bounds__(kBlock) void seg_count_kernel(int n_real, const uint4* __restrict__ rec,
+                                                           const uint32_t* __restrict__ row_start,
+                                                           const uint32_t* __restrict__ seg_base,
+                                                           const uint32_t* __restrict__ seg_row, int ntx,
+                                                           uint32_t* __restrict__ slots) {
+    extern __shared__ int32_t s_diff[];  // ntx + 1
+    __shared__ int32_t lds[kWaves];
+    const int64_t sg = blockIdx.x;
+    if (sg >= (int64_t)seg_base[n_real]) return;
+    const uint32_t row = seg_row[sg];
+    const uint32_t sb = seg_base[row], nseg = seg_base[row + 1] - sb;
+    const uint32_t k = (uint32_t)sg - sb;
+    const int64_t b = (int64_t)row_start[row] + (int64_t)k * kRunSeg;
+    const int64_t e = min((int64_t)row_start[row + 1], b + kRunSeg);
+    for (int c = threadIdx.x; c <= ntx; c += kBlock) s_diff[c] = 0;
+    __syncthreads();
+    for (int64_t i = b + threadIdx.x; i < e; i += kBlock) {
+        const uint32_t x01 = rec[i].z;
+        atomicAdd(&s_diff[x01 & 0xffffu], 1);
+        atomicAdd(&s_diff[x01 >> 16], -1);
+    }
+    __syncthreads();
+    // each thread a run of consecutive columns; block scan of the runs' sums
+    const int per = (ntx + kBlock - 1) / kBlock;
+    const int c0 = threadIdx.x * per, c1 = min(ntx, c0 + per);
+    int32_t sum = 0;
+    for (int c = c0; c < c1; ++c) sum += s_diff[c];
+    int32_t tot;
+    int32_t run = block_exclusive_scan<int32_t>(sum, lds, tot);
+    uint32_t* out = slots + (int64_t)sb * ntx + k;
+    for (int c = c0; c < c1; ++c) {
+        run += s_diff[c];
+        out[(int64_t)c * nseg] = (uint32_t)run;
+    }
+}
+
+// exclusive scan of a u32 array: block sums, scan of the sums (scan_partials_kernel), apply
+__global__ __launch_bounds__(kBlock) void array_reduce_kernel(int64_t n, const uint32_t* __restrict__ a,
+                                                              uint32_t* __restrict__ partials) {
+    __shared__ uint32_t lds[kWaves];
+    uint32_t acc = 0;
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        const int64_t i = base + (int64_t)k * kBlock + threadIdx.x;
+        if (i < n) acc += a[i];
+    }
+    acc = block_reduce_sum<uint32_t>(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void array_scan_kernel(int64_t n, uint32_t* __restrict__ a,
+                                                            const uint32_t* __restrict__ partials) {
+    __shared__ uint32_t lds[kWaves];
+    uint32_t carry = partials[blockIdx.x];
+    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    for (int k = 0; k < kSortItems; ++k) {
+        if (base + (int64_t)k * kBlock >= n) break;
+        const int64_t i = base + (int64_t)k * kBlock + threadIdx.x;
+        const uint32_t x = i < n ? a[i] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(x, lds, tot);
+        if (i < n) a[i] = carry + ex;
+        carry += tot;
+    }
+}
+
+// One wavefront per (segment, group of kColGroup columns). Per column, the runs covering it are
+// found by ballot and take consecutive positions from the column's slot, in run (depth) order.
+__global__ __launch_bounds__(kBlock) void write_runs_kernel(
+    int n_real, const uint4* __restrict__ rec, const uint32_t* __restrict__ row_start,
+    const uint32_t* __restrict__ seg_base, const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ slots,
+    int ntx, int nty, int tnb, int n_groups, int64_t n_out, int64_t* __restrict__ out_keys,
+    int32_t* __restrict__ out_ids) {
+    const int64_t sg = blockIdx.x;
+    if (sg >= (int64_t)seg_base[n_real]) return;
+    const int lane = __lane_id();
+    const int cg = blockIdx.y * kWaves + (threadIdx.x >> 6);
+    if (cg >= n_groups) return;
+    const uint32_t row = seg_row[sg];
+    const uint32_t sb = seg_base[row], nseg = seg_base[row + 1] - sb;
+    const uint32_t k = (uint32_t)sg - sb;
+    const int64_t b = (int64_t)row_start[row] + (int64_t)k * kRunSeg;
+    const int64_t e = min((int64_t)row_start[row + 1], b + kRunSeg);
+    const uint32_t cid = row / (uint32_t)nty, y = row - cid * (uint32_t)nty;
+    const int c0 = cg * kColGroup;
+    const int nc = min(kColGroup, ntx - c0);
+    uint32_t base[kColGroup];
+#pragma unroll
+    for (int j = 0; j < kColGroup; ++j)
+        base[j] = j < nc ? slots[(int64_t)sb * ntx + (int64_t)(c0 + j) * nseg + k] : 0u;
+    const uint32_t tile_row = (cid << tnb) | (y * (uint32_t)ntx);
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int64_t i0 = b; i0 < e; i0 += 64) {
+        const int64_t i = i0 + lane;
+        const bool valid = i < e;
+        const uint4 rr = valid ? rec[i] : make_uint4(0, 0, 0, 0);
+        const int x0 = (int)(rr.z & 0xffffu), x1 = (int)(rr.z >> 16);
+#pragma unroll
+        for (int j = 0; j < kColGroup; ++j) {
+            if (j >= nc) break;
+            const int c = c0 + j;
+            const bool cov = valid && x0 <= c && c < x1;
+            const uint64_t mk = __ballot(cov);
+            if (cov) {
+                const uint64_t pos = (uint64_t)base[j] + (uint64_t)__popcll(mk & lt);
+                if (pos < (uint64_t)n_out) {
+                    out_keys[pos] = make_key(tile_row + (uint32_t)c, rr.y);
+                    out_ids[pos] = (int32_t)rr.x;
+                }
+            }
+            base[j] += (uint32_t)__popcll(mk);
+        }
+    }
+}
+
+// single block: the runs of negative-depth instances, after every tile, in run order; each run's
+// entries consecutive (their keys' tile bits are saturated by the sign extension)
+__global__ __launch_bounds__(kBlock) void write_neg_runs_kernel(const uint4* __restrict__ rec,
+                                                                const uint32_t* __restrict__ row_start,
+                                                                int neg_row, int64_t n_runs,
+                                                                const uint32_t* __restrict__ neg_base,
+                                                                int64_t n_out, int64_t* __restrict__ out_keys,
+                                                                int32_t* __restrict__ out_ids) {
+    __shared__ uint32_t lds[kWaves];
+    const int64_t b = row_start[neg_row];
+    uint32_t carry = *neg_base;
+    for (int64_t i0 = b; i0 < n_runs; i0 += kBlock) {
+        const int64_t i = i0 + threadIdx.x;
+        const uint4 rr = i < n_runs ? rec[i] : make_uint4(0, 0, 0, 0);
+        const uint32_t w = i < n_runs ? (rr.z >> 16) - (rr.z & 0xffffu) : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(w, lds, tot);
+        for (uint32_t q = 0; q < w; ++q) {
+            const uint64_t pos = (uint64_t)carry + ex + q;
+            if (pos < (uint64_t)n_out) {
+                out_keys[pos] = make_key(0u, rr.y);
+                out_ids[pos] = (int32_t)rr.x;
+            }
+        }
+        carry += tot;
+    }
+}
+
 // isect_offset_encode_kernel (tiling_common.cu:25-71); writes are clamped to the offsets array.
 __global__ __launch_bounds__(kBlock) void offset_encode_kernel(const int64_t* __restrict__ ids, int64_t n,
                                                                int n_tiles, int tnb, int64_t total,
@@ -416,6 +687,7 @@ int geometry_of(const xsg_isect_desc* d, Geometry& g) {
         return xsg_fail(XSG_ERR_INVALID, "invalid isect descriptor (n=%lld cams=%d tile=%dx%d)",
                         (long long)d->n, d->n_cams, d->tile_w, d->tile_h);
     g.kind = d->kind;
+    g.sort = d->sort ? 1 : 0;
     g.n_cams = d->n_cams;
     g.n = d->n;
     g.spans = 1;
@@ -459,6 +731,9 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct CountWs {
     Rect* rects; uint32_t* vcnt; uint32_t* vkey; uint64_t* partials; uint64_t* cpart;
     uint32_t* comp_id; uint32_t* comp_off; uint32_t* comp_key;
+    // depth pre-order (sorted fills only): ping-pong, histograms, device-side count, run offsets
+    uint32_t* alt_key; uint32_t* alt_id; uint32_t* hist; uint32_t* dtot; uint32_t* m_dev;
+    uint32_t* roff; uint32_t* rpart;
     int64_t n_virtual; unsigned nb;
     size_t bytes;
 };
@@ -473,39 +748,57 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     w.rects = (Rect*)(p + off); off += align256(sizeof(Rect) * nv);
     w.vcnt = (uint32_t*)(p + off); off += align256(4 * nv);
     w.vkey = (uint32_t*)(p + off); off += align256(4 * nv);
-    w.partials = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * (w.nb + 2));
-    w.cpart = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * w.nb);
+    w.partials = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * (w.nb + 3));
+    w.cpart = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * 2 * w.nb);
     w.comp_id = (uint32_t*)(p + off); off += align256(4 * nv);
     w.comp_off = (uint32_t*)(p + off); off += align256(4 * nv);
     w.comp_key = (uint32_t*)(p + off); off += align256(4 * nv);
+    const size_t ns = g.sort ? (size_t)nv : 0;
+    w.alt_key = (uint32_t*)(p + off); off += align256(4 * ns);
+    w.alt_id = (uint32_t*)(p + off); off += align256(4 * ns);
+    w.roff = (uint32_t*)(p + off); off += align256(4 * ns);
+    w.hist = (uint32_t*)(p + off); off += align256(g.sort ? 4 * (size_t)kRadix * w.nb : 0);
+    w.dtot = (uint32_t*)(p + off); off += align256(4 * kRadix);
+    w.rpart = (uint32_t*)(p + off); off += align256(4 * ((size_t)w.nb + 1));
+    w.m_dev = (uint32_t*)(p + off); off += align256(4);
     w.bytes = off;
     return w;
 }
 
 struct FillWs {
-    uint32_t* alt_key; uint32_t* alt_id;                              // depth sort ping-pong [m]
-    uint32_t* soffs; uint32_t* spart;                                 // offsets in depth order
-    uint32_t* hi_a; uint32_t* id_a; uint32_t* hi_b; uint32_t* id_b;  // tile sort [n_isects]
+    uint32_t* row_a; uint32_t* p_a; uint32_t* row_b; uint32_t* p_b;  // runs and ping-pong [n_runs]
+    uint4* rec;                                     // run records [n_runs]
+    uint32_t* row_start; uint32_t* seg_base; uint32_t* seg_row;
+    uint32_t* slots; uint32_t* spart;
     uint32_t* hist; uint32_t* dtot;
+    int n_rows;                                     // row buckets incl. the negative one
+    int64_t s_max;                                  // segment bound
+    int64_t n_slots;
     size_t bytes;
 };
 
-FillWs fill_ws_layout(int64_t m, int64_t n_isects, void* base) {
+FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     char* p = (char*)base;
-    FillWs w;
+    FillWs w{};
     size_t off = 0;
-    const unsigned nb_m = sort_blocks(m > 0 ? m : 1), nb_i = sort_blocks(n_isects > 0 ? n_isects : 1);
-    const unsigned nb_h = max(nb_m, nb_i);
-    w.alt_key = (uint32_t*)(p + off); off += align256(4 * m);
-    w.alt_id = (uint32_t*)(p + off); off += align256(4 * m);
-    w.soffs = (uint32_t*)(p + off); off += align256(4 * m);
-    w.spart = (uint32_t*)(p + off); off += align256(4 * ((size_t)nb_m + 1));
-    w.hi_a = (uint32_t*)(p + off); off += align256(4 * n_isects);
-    w.id_a = (uint32_t*)(p + off); off += align256(4 * n_isects);
-    w.hi_b = (uint32_t*)(p + off); off += align256(4 * n_isects);
-    w.id_b = (uint32_t*)(p + off); off += align256(4 * n_isects);
-    w.hist = (uint32_t*)(p + off); off += align256(4 * (size_t)kRadix * nb_h);
-    w.dtot = (uint32_t*)(p + off); off += align256(4 * kRadix);
+    w.n_rows = g.n_cams * g.nty + 1;
+    w.s_max = n_runs / kRunSeg + w.n_rows;
+    w.n_slots = w.s_max * g.ntx;
+    const unsigned nb_r = sort_blocks(n_runs > 0 ? n_runs : 1);
+    const unsigned nb_s = sort_blocks(w.n_slots > 0 ? w.n_slots : 1);
+    auto take = [&](size_t bytes) { void* q = p + off; off += align256(bytes); return q; };
+    w.row_a = (uint32_t*)take(4 * n_runs);
+    w.p_a = (uint32_t*)take(4 * n_runs);
+    w.row_b = (uint32_t*)take(4 * n_runs);
+    w.p_b = (uint32_t*)take(4 * n_runs);
+    w.rec = (uint4*)take(16 * n_runs);
+    w.row_start = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
+    w.seg_base = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
+    w.seg_row = (uint32_t*)take(4 * (size_t)w.s_max);
+    w.slots = (uint32_t*)take(4 * (size_t)w.n_slots);
+    w.spart = (uint32_t*)take(4 * ((size_t)nb_s + 1));
+    w.hist = (uint32_t*)take(4 * (size_t)kRadix * nb_r);
+    w.dtot = (uint32_t*)take(4 * kRadix);
     w.bytes = off;
     return w;
 }
@@ -530,13 +823,14 @@ extern "C" size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d) {
 }
 
 extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* workspace, int64_t* n_isects,
-                               int64_t* n_visible, xsg_stream_t stream) {
+                               int64_t* n_visible, int64_t* n_runs, xsg_stream_t stream) {
     Geometry g;
     int rc = geometry_of(d, g);
     if (rc) return rc;
     const int64_t nt = g.n * g.n_cams;
     if (n_isects) *n_isects = 0;
     if (n_visible) *n_visible = 0;
+    if (n_runs) *n_runs = 0;
     if (nt == 0) return XSG_OK;
     if (!workspace || !tpg || !d->means2d || !d->radii || !d->depths)
         return xsg_fail(XSG_ERR_INVALID, "xsg_isect_count: null pointer");
@@ -557,20 +851,32 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
             count_spherical_kernel<XSG_CAM_LIDAR, true><<<w.nb, kBlock, 0, s>>>(
                 nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
                 d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
-                d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey,
-                w.partials, w.cpart);
+                d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt,
+                w.vkey, w.partials, w.cpart);
         } else {
             count_spherical_kernel<XSG_CAM_SPHERICAL, false><<<w.nb, kBlock, 0, s>>>(
                 nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
                 d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths, nullptr,
-                0, u_per_tile, v_per_tile, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
+                0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
         }
     }
     scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb, w.cpart);
     compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
                                            w.comp_key);
+    if (g.sort) {
+        // queued ahead of the readback, sized on the device: the visible spans in depth order
+        // (stable, 4 passes, result back in comp_*), then their row-run offsets
+        visible_count_kernel<<<1, 64, 0, s>>>(w.partials + w.nb, w.m_dev);
+        radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>>(
+            w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
+            PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev);
+        rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
+        scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(w.rpart, w.nb, nullptr);
+        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
+    }
     XSG_TRY_LAUNCH("isect_count");
-    uint64_t total[2] = {0, 0};  // packed (visible << 32 | count) total, exact count total
+    // packed (visible << 32 | count) total, exact intersection total, exact row-run total
+    uint64_t total[3] = {0, 0, 0};
     if (hipMemcpyAsync(total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return xsg_launch_status("isect_count readback");
@@ -578,34 +884,36 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (total[1] >= (1ull << 31))
         return xsg_fail(XSG_ERR_INVALID, "%llu intersections exceed the int32 range of flatten ids",
                         (unsigned long long)total[1]);
-    const int64_t isects = (int64_t)total[1];
-    const int64_t vis = (int64_t)(total[0] >> 32);
-    if (n_isects) *n_isects = isects;
-    if (n_visible) *n_visible = vis;
+    if (n_isects) *n_isects = (int64_t)total[1];
+    if (n_visible) *n_visible = (int64_t)(total[0] >> 32);
+    if (n_runs) *n_runs = (int64_t)total[2];
     return XSG_OK;
 }
 
-extern "C" size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible) {
-    (void)d;
-    return fill_ws_layout(n_visible, n_isects, nullptr).bytes;
+extern "C" size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible,
+                                                 int64_t n_runs) {
+    Geometry g;
+    if (geometry_of(d, g) || n_isects < 0 || n_visible < 0 || n_runs < 0) return 0;
+    return fill_ws_layout(g, n_runs, nullptr).bytes;
 }
 
-extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int sort,
-                              void* count_workspace, void* fill_workspace, int64_t* isect_ids,
+extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int64_t n_runs,
+                              int sort, void* count_workspace, void* fill_workspace, int64_t* isect_ids,
                               int32_t* flatten_ids, xsg_stream_t stream) {
     Geometry g;
     int rc = geometry_of(d, g);
     if (rc) return rc;
     if (n_isects == 0) return XSG_OK;
     const CountWs cw = count_ws_layout(g, count_workspace);
-    if (n_isects < 0 || n_visible <= 0 || n_visible > cw.n_virtual || !count_workspace || !isect_ids ||
-        !flatten_ids)
+    if (n_isects < 0 || n_visible <= 0 || n_visible > cw.n_virtual || n_runs <= 0 || n_runs > n_isects ||
+        !count_workspace || !isect_ids || !flatten_ids)
         return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: bad arguments");
     const hipStream_t s = (hipStream_t)stream;
     const int64_t m = n_visible;
     const int64_t n_per_cam = g.n_cams > 1 ? g.n : 0;
-    const unsigned nb_expand = (unsigned)((n_isects + kExpandPerBlock - 1) / kExpandPerBlock);
     if (!sort) {
+        if (g.sort) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: unsorted fill of a descriptor counted with sort = 1");
+        const unsigned nb_expand = (unsigned)((n_isects + kExpandPerBlock - 1) / kExpandPerBlock);
         expand_kernel<FinalOut><<<nb_expand, kBlock, 0, s>>>(n_isects, cw.comp_off, cw.comp_id, cw.comp_key, m,
                                                              cw.rects, g.ntx, g.tnb, n_per_cam, g.spans,
                                                              FinalOut{isect_ids, flatten_ids});
@@ -613,26 +921,46 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
         return XSG_OK;
     }
     if (!fill_workspace) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: null fill workspace");
-    const FillWs fw = fill_ws_layout(m, n_isects, fill_workspace);
-    // depth pre-order of the visible virtual instances: stable, 4 passes, result back in comp_*
+    if (!g.sort) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: sorted fill of a descriptor counted with sort = 0");
+    if (g.ntx > kMaxSortedCols)
+        return xsg_fail(XSG_ERR_UNSUPPORTED, "sorted binning supports at most %d tile columns (got %d)", kMaxSortedCols,
+                        g.ntx);
+    const FillWs fw = fill_ws_layout(g, n_runs, fill_workspace);
+    const uint32_t neg_row = (uint32_t)(fw.n_rows - 1);
+    const int n_real = fw.n_rows - 1;
+    expand_runs_kernel<<<(unsigned)((n_runs + kExpandPerBlock - 1) / kExpandPerBlock), kBlock, 0, s>>>(
+        n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.rects, g.nty, n_per_cam, g.spans, neg_row, fw.row_a,
+        fw.p_a);
+    int row_bits = 1;
+    while ((1u << row_bits) <= neg_row) ++row_bits;
+    // the last pass must not write over its own input: with an odd pass count the sorted runs end
+    // in the second buffer pair
+    const bool odd = ((row_bits + 7) / 8) % 2 == 1;
+    uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
+    uint32_t* p_sorted = odd ? fw.p_b : fw.p_a;
     radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>>(
-        cw.comp_key, cw.comp_id, fw.alt_key, fw.alt_id, m, 0, 32, fw.hist, fw.dtot,
-        PlainOut<uint32_t, uint32_t>{cw.comp_key, cw.comp_id}, s);
-    // intersection offsets of the instances in depth order
-    const unsigned nb_m = sort_blocks(m);
-    gather_reduce_kernel<<<nb_m, kBlock, 0, s>>>(m, cw.comp_id, cw.vcnt, fw.spart);
-    scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(fw.spart, nb_m, nullptr);
-    gather_scan_kernel<<<nb_m, kBlock, 0, s>>>(m, cw.comp_id, cw.vcnt, fw.spart, fw.soffs);
-    // expansion into (tile bits, virtual instance) pairs
-    const int bits = g.tnb + g.cam_bits;
-    const uint32_t mask = (uint32_t)((1ull << bits) - 1);
-    expand_kernel<PairsOut><<<nb_expand, kBlock, 0, s>>>(n_isects, fw.soffs, cw.comp_id, cw.comp_key, m,
-                                                         cw.rects, g.ntx, g.tnb, n_per_cam, g.spans,
-                                                         PairsOut{fw.hi_a, fw.id_a, mask});
-    // stable sort on the tile bits; the last pass writes the final keys and ids
-    radix_sort_passes<uint32_t, uint32_t, SortedKeyOut>(fw.hi_a, fw.id_a, fw.hi_b, fw.id_b, n_isects, 0, bits,
-                                                        fw.hist, fw.dtot,
-                                                        SortedKeyOut{isect_ids, flatten_ids, cw.vkey, g.spans}, s);
+        fw.row_a, fw.p_a, fw.row_b, fw.p_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
+        PlainOut<uint32_t, uint32_t>{rows_sorted, p_sorted}, s);
+    row_bounds_kernel<<<xsg_blocks(fw.n_rows + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
+                                                                           fw.row_start);
+    seg_table_kernel<<<1, kBlock, 0, s>>>(fw.row_start, n_real, fw.seg_base, fw.seg_row);
+    // column counts per segment, and one exclusive scan over (row, column, segment)
+    materialize_runs_kernel<<<xsg_blocks(n_runs, kBlock), kBlock, 0, s>>>(
+        n_runs, rows_sorted, p_sorted, cw.comp_id, cw.comp_key, cw.rects, g.spans, fw.rec);
+    fill_i32_kernel<<<xsg_blocks(fw.n_slots, kBlock), kBlock, 0, s>>>((int32_t*)fw.slots, fw.n_slots, 0);
+    seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
+        n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
+    const unsigned nb_s = sort_blocks(fw.n_slots);
+    array_reduce_kernel<<<nb_s, kBlock, 0, s>>>(fw.n_slots, fw.slots, fw.spart);
+    scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(fw.spart, nb_s, nullptr);
+    array_scan_kernel<<<nb_s, kBlock, 0, s>>>(fw.n_slots, fw.slots, fw.spart);
+    // the writers
+    const int n_groups = (g.ntx + kColGroup - 1) / kColGroup;
+    const dim3 grid_w((unsigned)fw.s_max, (unsigned)((n_groups + kWaves - 1) / kWaves));
+    write_runs_kernel<<<grid_w, kBlock, 0, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, fw.slots,
+                                                g.ntx, g.nty, g.tnb, n_groups, n_isects, isect_ids, flatten_ids);
+    write_neg_runs_kernel<<<1, kBlock, 0, s>>>(fw.rec, fw.row_start, (int)neg_row, n_runs, fw.spart + nb_s,
+                                               n_isects, isect_ids, flatten_ids);
     XSG_TRY_LAUNCH("isect_fill");
     return XSG_OK;
 }

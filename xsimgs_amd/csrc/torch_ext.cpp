@@ -289,16 +289,18 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> spherical_harmonics_fused_bwd(int64_t
 // ------------------------------------------------------------------ binning
 std::tuple<Tensor, Tensor, Tensor> isect_run(xsg_isect_desc& d, const Tensor& like, bool sort) {
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(like.device());
+    d.sort = sort ? 1 : 0;
     const xsg_stream_t s = stream_of(like);
     Tensor tiles_per_gauss = at::empty({d.n * d.n_cams}, like.options().dtype(at::kInt));
     Tensor cws = workspace(like, xsg_isect_count_workspace_bytes(&d));
-    int64_t n_isects = 0, n_visible = 0;
-    check_rc(xsg_isect_count(&d, tiles_per_gauss.data_ptr<int32_t>(), cws.data_ptr(), &n_isects, &n_visible, s));
+    int64_t n_isects = 0, n_visible = 0, n_runs = 0;
+    check_rc(xsg_isect_count(&d, tiles_per_gauss.data_ptr<int32_t>(), cws.data_ptr(), &n_isects, &n_visible,
+                             &n_runs, s));
     Tensor isect_ids = at::empty({n_isects}, like.options().dtype(at::kLong));
     Tensor flatten_ids = at::empty({n_isects}, like.options().dtype(at::kInt));
     if (n_isects > 0) {
-        Tensor fws = workspace(like, sort ? xsg_isect_fill_workspace_bytes(&d, n_isects, n_visible) : 1);
-        check_rc(xsg_isect_fill(&d, n_isects, n_visible, sort ? 1 : 0, cws.data_ptr(), fws.data_ptr(),
+        Tensor fws = workspace(like, sort ? xsg_isect_fill_workspace_bytes(&d, n_isects, n_visible, n_runs) : 1);
+        check_rc(xsg_isect_fill(&d, n_isects, n_visible, n_runs, sort ? 1 : 0, cws.data_ptr(), fws.data_ptr(),
                                 isect_ids.data_ptr<int64_t>(), flatten_ids.data_ptr<int32_t>(), s));
     }
     return {tiles_per_gauss, isect_ids, flatten_ids};

@@ -81,19 +81,15 @@ XSG_DEV f3 rows_tmul(f3 r0, f3 r1, f3 r2, f3 v) {  // M^T v
                r0.z * v.x + r1.z * v.y + r2.z * v.z);
 }
 
-XSG_DEV f3 safe_normalize(f3 v) {  // utils.h:85-88
-    const float l = dot(v, v);
-    return l > 0.0f ? v * rsqrtf(l) : v;
-}
+// 1/sqrt(l) for l > 0, else 1: safe_normalize(v) (utils.h:85-88) is v * inv_len(|v|^2). The raw
+// v_rsq_f32 (1 ulp) replaces rsqrtf, whose denormal-range scaling costs five more instructions.
+XSG_DEV float inv_len(float l) { return l > 0.0f ? __builtin_amdgcn_rsqf(l) : 1.0f; }
 
-XSG_DEV f3 safe_normalize_bwd(f3 v, f3 d_out) {  // utils.h:198-206
-    const float l = dot(v, v);
-    if (l > 0.0f) {
-        const float il = rsqrtf(l);
-        const float il3 = il * il * il;
-        return il * d_out - (il3 * dot(d_out, v)) * v;
-    }
-    return d_out;
+XSG_DEV f3 safe_normalize(f3 v) { return v * inv_len(dot(v, v)); }
+
+// safe_normalize_bwd (utils.h:198-206) with il = inv_len(|v|^2) already known
+XSG_DEV f3 safe_normalize_bwd_il(f3 v, float il, f3 d_out) {
+    return il * d_out - (il * il * il * dot(d_out, v)) * v;
 }
 
 // Lane-to-lane moves inside rows of 16 lanes (DPP). `update_dpp` with all rows/banks enabled and
@@ -107,32 +103,34 @@ constexpr int kDppQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]: lane ^ 2
 constexpr int kDppRowMirror = 0x140;   // lane i <-> 15 - i within a row of 16
 constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each half row of 8
 
+// One halving step with the gfx950 lane-swap instructions. v_permlane32_swap(x, y) exchanges
+// lanes 32-63 of x with lanes 0-31 of y; v_permlane16_swap(x, y) exchanges the odd 16-lane rows
+// of x with the even rows of y. With x = the component a lower lane keeps and y = the one its
+// partner keeps, afterwards x + y is, on every lane, its kept component summed over the pair.
+XSG_DEV float swap_add32(float keep_lo, float keep_hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+XSG_DEV float swap_add16(float keep_lo, float keep_hi) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Reduce-scatter of 16 per-lane values over the 64 lanes of a wavefront by recursive halving:
 // each step pairs every lane with a partner, keeps half of its values and adds the partner's
-// copy of that half. After the four halving steps (partners at distance 32 and 16, then the row
-// and half-row mirrors) and a final quad sum, lane l holds the wave total of value l >> 2.
-// 15 exchanges + 2 instead of 16 x 6 for a butterfly per value.
+// copy of that half. Partners at distance 32 and 16 exchange through lane swaps (lanes 0-31 keep
+// v[0..7], lanes 16-31 of each half keep the upper half of what is left), then the row and
+// half-row mirrors (DPP) and a final quad sum: lane l holds the wave total of value l >> 2.
+// Must be called with all 64 lanes active.
 XSG_DEV float wave_reduce_scatter16(const float (&v)[16]) {
     const int lane = __lane_id();
     float w[8], x[4], y[2];
-    {
-        const bool up = lane & 32;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float send = up ? v[j] : v[j + 8];
-            const float keep = up ? v[j + 8] : v[j];
-            w[j] = keep + __shfl_xor(send, 32, 64);
-        }
-    }
-    {
-        const bool up = lane & 16;
+    for (int j = 0; j < 8; ++j) w[j] = swap_add32(v[j], v[j + 8]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float send = up ? w[j] : w[j + 4];
-            const float keep = up ? w[j + 4] : w[j];
-            x[j] = keep + __shfl_xor(send, 16, 64);
-        }
-    }
+    for (int j = 0; j < 4; ++j) x[j] = swap_add16(w[j], w[j + 4]);
     {
         const bool up = (lane & 15) >= 8;
 #pragma unroll

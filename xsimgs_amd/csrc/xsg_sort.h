@@ -61,9 +61,12 @@ XSG_DEV uint32_t digit_of(K key, int shift, int bits) {
     return (uint32_t)((key >> shift) & (K)((1u << bits) - 1u));
 }
 
+// n_dev (optional): the element count read on the device, at most n; the grid covers n.
 template <typename K>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict__ keys, int64_t n, int shift,
-                                                            int bits, uint32_t* __restrict__ hist, unsigned nb) {
+                                                            int bits, uint32_t* __restrict__ hist, unsigned nb,
+                                                            const uint32_t* __restrict__ n_dev) {
+    if (n_dev) n = min(n, (int64_t)*n_dev);
     __shared__ uint32_t cnt[kWaves][kRadix];
     const int t = threadIdx.x, wave = t >> 6;
 #pragma unroll
@@ -119,7 +122,9 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
                                                               int shift, int bits,
                                                               const uint32_t* __restrict__ hist,
                                                               const uint32_t* __restrict__ digit_total,
-                                                              unsigned nb, Out out) {
+                                                              unsigned nb, Out out,
+                                                              const uint32_t* __restrict__ n_dev) {
+    if (n_dev) n = min(n, (int64_t)*n_dev);
     constexpr int kSeg = kSortTile / kWaves;  // keys per wave
     constexpr int kSteps = kSeg / 64;
     __shared__ uint32_t wcnt[kWaves][kRadix];
@@ -196,23 +201,25 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
 // Runs every pass of a stable LSD sort over bits [begin_bit, end_bit) (8-bit digits, last one
 // narrower) ping-ponging between (k0, v0) and (k1, v1); the last pass goes through `final_out`.
 // Returns the number of passes. hist must hold kRadix * sort_blocks(n) words, dtot kRadix words.
+// With n_dev, the device-side count (at most n) is sorted; n only sizes the grid.
 template <typename K, typename V, typename FinalOut>
 inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
-                             uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s) {
+                             uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s,
+                             const uint32_t* n_dev = nullptr) {
     const unsigned nb = sort_blocks(n);
     int passes = 0;
     K* src_k = k0; V* src_v = v0; K* dst_k = k1; V* dst_v = v1;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
         const int bits = min(8, end_bit - shift);
         const bool last = shift + 8 >= end_bit;
-        radix_upsweep<K><<<nb, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb);
+        radix_upsweep<K><<<nb, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
         radix_scan_hist<<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot);
         if (last) {
             radix_downsweep<K, V, FinalOut><<<nb, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits, hist,
-                                                                      dtot, nb, final_out);
+                                                                      dtot, nb, final_out, n_dev);
         } else {
             radix_downsweep<K, V, PlainOut<K, V>><<<nb, kSortBlock, 0, s>>>(
-                src_k, src_v, n, shift, bits, hist, dtot, nb, PlainOut<K, V>{dst_k, dst_v});
+                src_k, src_v, n, shift, bits, hist, dtot, nb, PlainOut<K, V>{dst_k, dst_v}, n_dev);
         }
         ++passes;
         K* tk = src_k; src_k = dst_k; dst_k = tk;
