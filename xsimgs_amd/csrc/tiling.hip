@@ -449,25 +449,24 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
     }
 }
 
-// row_start[r] = first sorted run of row bucket r (lower bound), r in [0, n_rows]
-__global__ __launch_bounds__(kBlock) void row_bounds_kernel(const uint32_t* __restrict__ rows, int64_t n_runs,
-                                                            int n_rows, uint32_t* __restrict__ row_start) {
-    const int r = blockIdx.x * kBlock + threadIdx.x;
-    if (r > n_rows) return;
-    int64_t lo = 0, hi = n_runs;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (rows[mid] < (uint32_t)r) lo = mid + 1; else hi = mid;
-    }
-    row_start[r] = (uint32_t)lo;
-}
-
-// single block: segments of kRunSeg runs per real row; seg_base = exclusive prefix of the segment
-// counts (total at seg_base[n_real]), seg_row[s] = row of segment s
-__global__ __launch_bounds__(kBlock) void seg_table_kernel(const uint32_t* __restrict__ row_start, int n_real,
-                                                           uint32_t* __restrict__ seg_base,
-                                                           uint32_t* __restrict__ seg_row) {
+// single block: row_start[r] = first sorted run of row bucket r (lower bound, r in [0, n_rows]),
+// then segments of kRunSeg runs per real row: seg_base = exclusive prefix of the segment counts
+// (total at seg_base[n_real]) and seg_row[s] = row of segment s
+__global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __restrict__ rows, int64_t n_runs,
+                                                              int n_rows, uint32_t* __restrict__ row_start,
+                                                              uint32_t* __restrict__ seg_base,
+                                                              uint32_t* __restrict__ seg_row) {
     __shared__ uint32_t lds[kWaves];
+    for (int r = threadIdx.x; r <= n_rows; r += kBlock) {
+        int64_t lo = 0, hi = n_runs;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (rows[mid] < (uint32_t)r) lo = mid + 1; else hi = mid;
+        }
+        row_start[r] = (uint32_t)lo;
+    }
+    __syncthreads();
+    const int n_real = n_rows - 1;
     const int per = (n_real + kBlock - 1) / kBlock;
     const int r0 = threadIdx.x * per, r1 = min(n_real, r0 + per);
     uint32_t sum = 0;
@@ -483,18 +482,22 @@ __global__ __launch_bounds__(kBlock) void seg_table_kernel(const uint32_t* __res
     if (threadIdx.x == 0) seg_base[n_real] = tot;
 }
 
-// Per sorted run: the record the writers read (flatten id, depth bits, column range, row bucket).
-__global__ __launch_bounds__(kBlock) void materialize_runs_kernel(
-    int64_t n_runs, const uint32_t* __restrict__ rows, const uint32_t* __restrict__ rp,
-    const uint32_t* __restrict__ ids, const uint32_t* __restrict__ keys, const Rect* __restrict__ rects,
-    int spans, uint4* __restrict__ rec) {
-    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n_runs) return;
-    const uint32_t p = rp[i];
-    const uint32_t v = ids[p];
-    const Rect r = rects[v];
-    rec[i] = make_uint4(v / (uint32_t)spans, keys[p], (uint32_t)r.x0 | ((uint32_t)r.x1 << 16), rows[i]);
-}
+// Last pass of the row sort: every run lands with its record for the writers (flatten id, depth
+// bits, column range, row bucket) beside its row bucket.
+struct RunRecOut {
+    uint32_t* rows;
+    uint4* rec;
+    const uint32_t* ids;
+    const uint32_t* keys;
+    const Rect* rects;
+    int spans;
+    XSG_DEV void put(int64_t pos, uint32_t row, uint32_t p) const {
+        const uint32_t v = ids[p];
+        const Rect r = rects[v];
+        rows[pos] = row;
+        rec[pos] = make_uint4(v / (uint32_t)spans, keys[p], (uint32_t)r.x0 | ((uint32_t)r.x1 << 16), row);
+    }
+};
 
 // One workgroup per segment: how many of its runs cover each column, from a difference array in
 // LDS (+1 at x0, -1 at x1, then a prefix over the columns), stored at slot (row, column, segment).
@@ -534,44 +537,90 @@ __global__ __launch_bounds__(kBlock) void seg_count_kernel(int n_real, const uin
     }
 }
 
-// exclusive scan of a u32 array: block sums, scan of the sums (scan_partials_kernel), apply
-__global__ __launch_bounds__(kBlock) void array_reduce_kernel(int64_t n, const uint32_t* __restrict__ a,
-                                                              uint32_t* __restrict__ partials) {
-    __shared__ uint32_t lds[kWaves];
-    uint32_t acc = 0;
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
-        const int64_t i = base + (int64_t)k * kBlock + threadIdx.x;
-        if (i < n) acc += a[i];
+// Per tile (real row, column): exclusive prefix of its segments' counts in place (the slots of a
+// tile are consecutive), and the tile's total into tile_tot.
+__global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restrict__ slots,
+                                                             const uint32_t* __restrict__ seg_base, int n_real,
+                                                             int ntx, uint32_t* __restrict__ tile_tot) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= (int64_t)n_real * ntx) return;
+    const int row = (int)(t / ntx), c = (int)(t - (int64_t)row * ntx);
+    const uint32_t sb = seg_base[row], nseg = seg_base[row + 1] - sb;
+    uint32_t* sl = slots + (int64_t)sb * ntx + (int64_t)c * nseg;
+    uint32_t run = 0;
+    for (uint32_t k = 0; k < nseg; ++k) {
+        const uint32_t x = sl[k];
+        sl[k] = run;
+        run += x;
     }
-    acc = block_reduce_sum<uint32_t>(acc, lds);
-    if (threadIdx.x == 0) partials[blockIdx.x] = acc;
+    tile_tot[t] = run;
 }
 
-__global__ __launch_bounds__(kBlock) void array_scan_kernel(int64_t n, uint32_t* __restrict__ a,
-                                                            const uint32_t* __restrict__ partials) {
+// single block of 1024 threads: exclusive scan of tile_tot[0, n) in place (the first position of
+// every tile of the real rows), the total -- where the negative-depth entries start -- at tile_tot[n]
+constexpr int kScanThreads = 1024;
+__global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n) {
+    __shared__ uint32_t lds[kScanThreads / 64];
+    const int64_t per = (n + kScanThreads - 1) / kScanThreads;
+    const int64_t i0 = (int64_t)threadIdx.x * per, i1 = min(n, i0 + per);
+    uint32_t sum = 0;
+    for (int64_t i = i0; i < i1; ++i) sum += a[i];
+    const uint32_t inc = wave_inclusive_scan(sum);
+    const int wave = threadIdx.x >> 6;
+    if (__lane_id() == 63) lds[wave] = inc;
+    __syncthreads();
+    uint32_t before = 0, tot = 0;
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+        const uint32_t x = lds[w];
+        if (w < wave) before += x;
+        tot += x;
+    }
+    uint32_t run = before + inc - sum;
+    for (int64_t i = i0; i < i1; ++i) {
+        const uint32_t x = a[i];
+        a[i] = run;
+        run += x;
+    }
+    if (threadIdx.x == 0) a[n] = tot;
+}
+
+// Runs of negative-depth instances, after every tile, in run order; each run's entries consecutive
+// (their keys' tile bits are saturated by the sign extension). One workgroup.
+XSG_DEV void write_neg_runs(const uint4* __restrict__ rec, int64_t b, int64_t n_runs, uint32_t base, int64_t n_out,
+                            int64_t* __restrict__ out_keys, int32_t* __restrict__ out_ids) {
     __shared__ uint32_t lds[kWaves];
-    uint32_t carry = partials[blockIdx.x];
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
-        if (base + (int64_t)k * kBlock >= n) break;
-        const int64_t i = base + (int64_t)k * kBlock + threadIdx.x;
-        const uint32_t x = i < n ? a[i] : 0u;
+    uint32_t carry = base;
+    for (int64_t i0 = b; i0 < n_runs; i0 += kBlock) {
+        const int64_t i = i0 + threadIdx.x;
+        const uint4 rr = i < n_runs ? rec[i] : make_uint4(0, 0, 0, 0);
+        const uint32_t w = i < n_runs ? (rr.z >> 16) - (rr.z & 0xffffu) : 0u;
         uint32_t tot;
-        const uint32_t ex = block_exclusive_scan<uint32_t>(x, lds, tot);
-        if (i < n) a[i] = carry + ex;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(w, lds, tot);
+        for (uint32_t q = 0; q < w; ++q) {
+            const uint64_t pos = (uint64_t)carry + ex + q;
+            if (pos < (uint64_t)n_out) {
+                out_keys[pos] = make_key(0u, rr.y);
+                out_ids[pos] = (int32_t)rr.x;
+            }
+        }
         carry += tot;
     }
 }
 
 // One wavefront per (segment, group of kColGroup columns). Per column, the runs covering it are
 // found by ballot and take consecutive positions from the column's slot, in run (depth) order.
+// Workgroup (s_max, 0) writes the negative-depth runs instead.
 __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     int n_real, const uint4* __restrict__ rec, const uint32_t* __restrict__ row_start,
     const uint32_t* __restrict__ seg_base, const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ slots,
-    int ntx, int nty, int tnb, int n_groups, int64_t n_out, int64_t* __restrict__ out_keys,
-    int32_t* __restrict__ out_ids) {
+    const uint32_t* __restrict__ tile_base, int64_t s_max, int64_t n_runs, int ntx, int nty, int tnb, int n_groups,
+    int64_t n_out, int64_t* __restrict__ out_keys, int32_t* __restrict__ out_ids) {
     const int64_t sg = blockIdx.x;
+    if (sg == s_max) {
+        if (blockIdx.y == 0)
+            write_neg_runs(rec, row_start[n_real], n_runs, tile_base[(int64_t)n_real * ntx], n_out, out_keys, out_ids);
+        return;
+    }
     if (sg >= (int64_t)seg_base[n_real]) return;
     const int lane = __lane_id();
     const int cg = blockIdx.y * kWaves + (threadIdx.x >> 6);
@@ -587,7 +636,8 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     uint32_t base[kColGroup];
 #pragma unroll
     for (int j = 0; j < kColGroup; ++j)
-        base[j] = j < nc ? slots[(int64_t)sb * ntx + (int64_t)(c0 + j) * nseg + k] : 0u;
+        base[j] = j < nc ? tile_base[(int64_t)row * ntx + c0 + j] + slots[(int64_t)sb * ntx + (int64_t)(c0 + j) * nseg + k]
+                         : 0u;
     const uint32_t tile_row = (cid << tnb) | (y * (uint32_t)ntx);
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int64_t i0 = b; i0 < e; i0 += 64) {
@@ -613,53 +663,22 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     }
 }
 
-// single block: the runs of negative-depth instances, after every tile, in run order; each run's
-// entries consecutive (their keys' tile bits are saturated by the sign extension)
-__global__ __launch_bounds__(kBlock) void write_neg_runs_kernel(const uint4* __restrict__ rec,
-                                                                const uint32_t* __restrict__ row_start,
-                                                                int neg_row, int64_t n_runs,
-                                                                const uint32_t* __restrict__ neg_base,
-                                                                int64_t n_out, int64_t* __restrict__ out_keys,
-                                                                int32_t* __restrict__ out_ids) {
-    __shared__ uint32_t lds[kWaves];
-    const int64_t b = row_start[neg_row];
-    uint32_t carry = *neg_base;
-    for (int64_t i0 = b; i0 < n_runs; i0 += kBlock) {
-        const int64_t i = i0 + threadIdx.x;
-        const uint4 rr = i < n_runs ? rec[i] : make_uint4(0, 0, 0, 0);
-        const uint32_t w = i < n_runs ? (rr.z >> 16) - (rr.z & 0xffffu) : 0u;
-        uint32_t tot;
-        const uint32_t ex = block_exclusive_scan<uint32_t>(w, lds, tot);
-        for (uint32_t q = 0; q < w; ++q) {
-            const uint64_t pos = (uint64_t)carry + ex + q;
-            if (pos < (uint64_t)n_out) {
-                out_keys[pos] = make_key(0u, rr.y);
-                out_ids[pos] = (int32_t)rr.x;
-            }
-        }
-        carry += tot;
-    }
-}
-
-// isect_offset_encode_kernel (tiling_common.cu:25-71); writes are clamped to the offsets array.
-__global__ __launch_bounds__(kBlock) void offset_encode_kernel(const int64_t* __restrict__ ids, int64_t n,
+// Tile offsets of sorted keys by binary search: offsets[t] = first index whose key bits above 32,
+// read as unsigned, are >= t's (camera, tile) id -- for sorted keys what the reference's encoder
+// (tiling_common.cu:25-71) writes, negative-depth keys included (their saturated bits sort last).
+__global__ __launch_bounds__(kBlock) void offset_search_kernel(const int64_t* __restrict__ ids, int64_t n,
                                                                int n_tiles, int tnb, int64_t total,
                                                                int32_t* __restrict__ offsets) {
-    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
-    const int64_t tmask = (1ll << tnb) - 1;
-    const int64_t cur = ids[i] >> 32;
-    const int64_t id_cur = (cur >> tnb) * n_tiles + (cur & tmask);
-    if (i == 0)
-        for (int64_t t = 0; t < id_cur + 1 && t < total; ++t) offsets[t] = 0;
-    if (i == n - 1)
-        for (int64_t t = max<int64_t>(id_cur + 1, 0); t < total; ++t) offsets[t] = (int32_t)n;
-    if (i > 0) {
-        const int64_t prev = ids[i - 1] >> 32;
-        if (prev == cur) return;
-        const int64_t id_prev = (prev >> tnb) * n_tiles + (prev & tmask);
-        for (int64_t t = max<int64_t>(id_prev + 1, 0); t < id_cur + 1 && t < total; ++t) offsets[t] = (int32_t)i;
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= total) return;
+    const uint32_t cam = (uint32_t)(t / n_tiles), tile = (uint32_t)(t - (int64_t)cam * n_tiles);
+    const uint32_t target = (cam << tnb) | tile;
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((uint32_t)((uint64_t)ids[mid] >> 32) < target) lo = mid + 1; else hi = mid;
     }
+    offsets[t] = (int32_t)lo;
 }
 
 __global__ __launch_bounds__(kBlock) void fill_i32_kernel(int32_t* __restrict__ p, int64_t n, int32_t v) {
@@ -769,7 +788,7 @@ struct FillWs {
     uint32_t* row_a; uint32_t* p_a; uint32_t* row_b; uint32_t* p_b;  // runs and ping-pong [n_runs]
     uint4* rec;                                     // run records [n_runs]
     uint32_t* row_start; uint32_t* seg_base; uint32_t* seg_row;
-    uint32_t* slots; uint32_t* spart;
+    uint32_t* slots; uint32_t* tile_tot;
     uint32_t* hist; uint32_t* dtot;
     int n_rows;                                     // row buckets incl. the negative one
     int64_t s_max;                                  // segment bound
@@ -785,7 +804,6 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     w.s_max = n_runs / kRunSeg + w.n_rows;
     w.n_slots = w.s_max * g.ntx;
     const unsigned nb_r = sort_blocks(n_runs > 0 ? n_runs : 1);
-    const unsigned nb_s = sort_blocks(w.n_slots > 0 ? w.n_slots : 1);
     auto take = [&](size_t bytes) { void* q = p + off; off += align256(bytes); return q; };
     w.row_a = (uint32_t*)take(4 * n_runs);
     w.p_a = (uint32_t*)take(4 * n_runs);
@@ -796,7 +814,7 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     w.seg_base = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
     w.seg_row = (uint32_t*)take(4 * (size_t)w.s_max);
     w.slots = (uint32_t*)take(4 * (size_t)w.n_slots);
-    w.spart = (uint32_t*)take(4 * ((size_t)nb_s + 1));
+    w.tile_tot = (uint32_t*)take(4 * ((size_t)(w.n_rows - 1) * g.ntx + 1));
     w.hist = (uint32_t*)take(4 * (size_t)kRadix * nb_r);
     w.dtot = (uint32_t*)take(4 * kRadix);
     w.bytes = off;
@@ -877,9 +895,14 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     XSG_TRY_LAUNCH("isect_count");
     // packed (visible << 32 | count) total, exact intersection total, exact row-run total
     uint64_t total[3] = {0, 0, 0};
-    if (hipMemcpyAsync(total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
+    if (hipMemcpyAsync(total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess)
         return xsg_launch_status("isect_count readback");
+    // poll rather than block: the readback ends a short queue, and waking from a blocking wait
+    // costs more than the wait itself
+    hipError_t q;
+    while ((q = hipStreamQuery(s)) == hipErrorNotReady) {
+    }
+    if (q != hipSuccess) return xsg_launch_status("isect_count readback");
     // below 2^31 intersections the packed count field never carried, so its visible count is exact
     if (total[1] >= (1ull << 31))
         return xsg_fail(XSG_ERR_INVALID, "%llu intersections exceed the int32 range of flatten ids",
@@ -933,34 +956,28 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
         fw.p_a);
     int row_bits = 1;
     while ((1u << row_bits) <= neg_row) ++row_bits;
-    // the last pass must not write over its own input: with an odd pass count the sorted runs end
-    // in the second buffer pair
+    // stable sort of the runs by row bucket; the last pass writes the sorted row buckets (to the
+    // buffer pair the last pass does not read) and the run records
     const bool odd = ((row_bits + 7) / 8) % 2 == 1;
     uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
-    uint32_t* p_sorted = odd ? fw.p_b : fw.p_a;
-    radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>>(
+    radix_sort_passes<uint32_t, uint32_t, RunRecOut>(
         fw.row_a, fw.p_a, fw.row_b, fw.p_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
-        PlainOut<uint32_t, uint32_t>{rows_sorted, p_sorted}, s);
-    row_bounds_kernel<<<xsg_blocks(fw.n_rows + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
-                                                                           fw.row_start);
-    seg_table_kernel<<<1, kBlock, 0, s>>>(fw.row_start, n_real, fw.seg_base, fw.seg_row);
-    // column counts per segment, and one exclusive scan over (row, column, segment)
-    materialize_runs_kernel<<<xsg_blocks(n_runs, kBlock), kBlock, 0, s>>>(
-        n_runs, rows_sorted, p_sorted, cw.comp_id, cw.comp_key, cw.rects, g.spans, fw.rec);
-    fill_i32_kernel<<<xsg_blocks(fw.n_slots, kBlock), kBlock, 0, s>>>((int32_t*)fw.slots, fw.n_slots, 0);
+        RunRecOut{rows_sorted, fw.rec, cw.comp_id, cw.comp_key, cw.rects, g.spans}, s);
+    row_segments_kernel<<<1, kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows, fw.row_start, fw.seg_base, fw.seg_row);
+    // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
+    // one exclusive scan over the tile totals
     seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
         n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
-    const unsigned nb_s = sort_blocks(fw.n_slots);
-    array_reduce_kernel<<<nb_s, kBlock, 0, s>>>(fw.n_slots, fw.slots, fw.spart);
-    scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(fw.spart, nb_s, nullptr);
-    array_scan_kernel<<<nb_s, kBlock, 0, s>>>(fw.n_slots, fw.slots, fw.spart);
-    // the writers
+    const int64_t n_tile_slots = (int64_t)n_real * g.ntx;
+    tile_prefix_kernel<<<xsg_blocks(n_tile_slots, kBlock), kBlock, 0, s>>>(fw.slots, fw.seg_base, n_real, g.ntx,
+                                                                          fw.tile_tot);
+    tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots);
+    // the writers (one extra workgroup for the negative-depth runs)
     const int n_groups = (g.ntx + kColGroup - 1) / kColGroup;
-    const dim3 grid_w((unsigned)fw.s_max, (unsigned)((n_groups + kWaves - 1) / kWaves));
+    const dim3 grid_w((unsigned)fw.s_max + 1, (unsigned)((n_groups + kWaves - 1) / kWaves));
     write_runs_kernel<<<grid_w, kBlock, 0, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, fw.slots,
-                                                g.ntx, g.nty, g.tnb, n_groups, n_isects, isect_ids, flatten_ids);
-    write_neg_runs_kernel<<<1, kBlock, 0, s>>>(fw.rec, fw.row_start, (int)neg_row, n_runs, fw.spart + nb_s,
-                                               n_isects, isect_ids, flatten_ids);
+                                                fw.tile_tot, fw.s_max, n_runs, g.ntx, g.nty, g.tnb, n_groups,
+                                                n_isects, isect_ids, flatten_ids);
     XSG_TRY_LAUNCH("isect_fill");
     return XSG_OK;
 }
@@ -975,9 +992,8 @@ extern "C" int xsg_isect_offset_encode(const int64_t* isect_ids, int64_t n_isect
     if (n_isects == 0) {  // tiling_common.cu:86-88
         fill_i32_kernel<<<xsg_blocks(total, kBlock), kBlock, 0, s>>>(offsets, total, 0);
     } else {
-        offset_encode_kernel<<<xsg_blocks(n_isects, kBlock), kBlock, 0, s>>>(isect_ids, n_isects, n_tiles,
-                                                                            tile_n_bits_of(n_tiles), total,
-                                                                            offsets);
+        offset_search_kernel<<<xsg_blocks(total, kBlock), kBlock, 0, s>>>(isect_ids, n_isects, n_tiles,
+                                                                          tile_n_bits_of(n_tiles), total, offsets);
     }
     XSG_TRY_LAUNCH("isect_offset_encode");
     return XSG_OK;

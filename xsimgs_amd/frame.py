@@ -66,10 +66,10 @@ def render_frame(st: FrameState, backward: bool = False, grads=None, cam_index: 
         colors = st.colors
     tsx, tsy = sc.tile_size
     with cam._freeze_ctx():
-        tiles = ut_gs_tiling(cam, st.means, scales, st.quats, spec.width, spec.height, opacity=opac,
-                             tile_size_x=tsx, tile_size_y=tsy, use_phm=sc.use_phm)
         ray_o, ray_d = cam.camera_rays(spec.width, spec.height, normalized_rays=True, return_origins=True,
                                        world_space=True)
+        tiles = ut_gs_tiling(cam, st.means, scales, st.quats, spec.width, spec.height, opacity=opac,
+                             tile_size_x=tsx, tile_size_y=tsy, use_phm=sc.use_phm)
         rgb, depth, alpha = ut_gs_rasterize(st.means, st.quats, scales, opac, colors, ray_o, ray_d,
                                             tiles["isect_offsets"], tiles["flatten_ids"], tsx, tsy)
     out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d,

@@ -49,15 +49,17 @@ def ut_gs_render(camera, points, scale, rotation, opacity, width: int, height: i
         opacity = opacity.contiguous()
         colors = colors.contiguous() if colors is not None else None
         points_velocity = points_velocity.contiguous() if points_velocity is not None else None
+        # rays first (independent of the tiling): they run on the GPU ahead of the tiling's one
+        # host readback instead of after it
+        if ray_o is None or ray_d is None:
+            ray_o, ray_d = camera.camera_rays(width=width, height=height, normalized_rays=True, return_origins=True,
+                                              world_space=True)
         tile_data = ut_gs_tiling(camera=camera, points=points, scale=scale, rotation=rotation, width=width,
                                  height=height, points_velocity=points_velocity, opacity=opacity,
                                  packed_particle_mask=packed_particle_mask, tile_size_x=tile_size_x,
                                  tile_size_y=tile_size_y, ut_alpha=ut_alpha, ut_beta=ut_beta, ut_kappa=ut_kappa,
                                  use_phm=use_phm)
         is_scene_static = points_velocity is None
-        if ray_o is None or ray_d is None:
-            ray_o, ray_d = camera.camera_rays(width=width, height=height, normalized_rays=True, return_origins=True,
-                                              world_space=True)
         kwargs = dict(positions=points, rotation=rotation, scale=scale, density=opacity, colors=colors, ray_o=ray_o,
                       ray_d=ray_d, isect_offsets=tile_data['isect_offsets'], flatten_ids=tile_data['flatten_ids'],
                       tile_size_x=tile_size_x, tile_size_y=tile_size_y)
