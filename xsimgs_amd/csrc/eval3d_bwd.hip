@@ -11,6 +11,8 @@
 //  * per-pair gradients are summed over the 64 lanes of a wavefront by a reduce-scatter that
 //    leaves each component's total on its own lane, and one atomic instruction per 16
 //    components adds them (one lane per component);
+//  * each thread owns two pixels, so the staged Gaussian's LDS reads, the reduction and the atomics
+//    serve both;
 //  * divisions in the per-pair math are reciprocal-multiplies (v_rcp_f32, 1 ulp) and 1/|grd|^2 is
 //    the square of the normalisation's reciprocal square root;
 //  * with a shared ray origin, the staged Gaussian carries o - mu instead of mu.
@@ -27,51 +29,198 @@ XSG_DEV int wave_max(int v) {
     return v;
 }
 
+// Per-pixel state of the backward sweep.
+template <int CS>
+struct BwdPixel {
+    f3 ro, rd;
+    float rt;
+    float T, T_final, depth_buffer, v_t;
+    float buffer[CS], v_c[CS];
+    float v_d, v_a;
+    int32_t bin_final;
+    bool inside;
+    int64_t pix;
+    f3 v_ro, v_rd;
+};
+
+// The staged Gaussian of one loop step.
+struct BwdGauss {
+    f3 r0, r1, r2;   // rows of M
+    f3 xo;           // o - mu (shared origin) or mu
+    f3 gro_fixed;    // M (o - mu) (shared origin)
+    f3 vel;
+    float op;
+};
+
+// alpha evaluation of one (pixel, Gaussian) pair (eval3d_bwd.cu:172-205)
+struct BwdEval {
+    f3 omm, gro, grd, grd_n, gcrod;
+    float dd, il, vis, alpha;
+    bool valid;
+};
+
+template <bool DYN>
+XSG_DEV BwdEval bwd_eval(const BwdGauss& gs, const f3 ro, const f3 rd, float rt, bool fixed, bool in_range) {
+    BwdEval e;
+    if (fixed) {
+        e.omm = gs.xo;
+        e.gro = gs.gro_fixed;
+    } else {
+        f3 mu = gs.xo;
+        if constexpr (DYN) mu = mu + rt * gs.vel;
+        e.omm = ro - mu;
+        e.gro = rows_mul(gs.r0, gs.r1, gs.r2, e.omm);
+    }
+    e.grd = rows_mul(gs.r0, gs.r1, gs.r2, rd);
+    e.dd = dot(e.grd, e.grd);
+    e.il = inv_len(e.dd);
+    e.grd_n = e.grd * e.il;
+    e.gcrod = cross(e.grd_n, e.gro);
+    const float power = -0.5f * dot(e.gcrod, e.gcrod);
+    e.vis = __expf(power);
+    e.alpha = fminf(kMaxAlpha, gs.op * e.vis);
+    e.valid = in_range && e.alpha >= 1.f / 255.f;
+    return e;
+}
+
+// Gradient contribution of one pair, added to acc (eval3d_bwd.cu:206-271). A pair that is not
+// valid adds exact zeros (its fac and gated upstream gradients are selected to 0, and every
+// gradient is linear in them) and leaves the pixel's transmittance and buffers unchanged.
+template <int CDIM, int CS, int K, bool DYN, bool RG>
+XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, const float (&rgb)[CS],
+                      float (&acc)[K]) {
+    const float inv_dd = e.il * e.il;
+    const float od = dot(e.gro, e.grd);
+    const float last_hit_T = -od * inv_dd;
+    const float ra = __builtin_amdgcn_rcpf(fmaxf(1e-6f, 1.0f - e.alpha));
+    px.T = e.valid ? px.T * ra : px.T;
+    const float T = px.T;
+    const float fac = e.valid ? e.alpha * T : 0.0f;
+    // grad_alpha (eval3d_bwd.cu:42-63)
+    float v_alpha = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CDIM; ++k) {
+        acc[k] += px.v_c[k] * fac;
+        v_alpha += (rgb[k] * T - px.buffer[k] * ra) * px.v_c[k];
+    }
+    v_alpha += (last_hit_T * T - px.depth_buffer * ra) * px.v_d;
+    v_alpha += px.T_final * ra * px.v_a;
+    // geometry and opacity only below the clamp (eval3d_bwd.cu:243)
+    const bool geo = e.valid && gs.op * e.vis <= kMaxAlpha;
+    const float v_alpha_g = geo ? v_alpha : 0.0f;
+    const float dL_dhitT = geo ? px.v_d * fac : 0.0f;
+
+    f3 v_gro = e.grd * (-dL_dhitT * inv_dd);
+    f3 v_grd = (2.0f * od * e.grd - e.dd * e.gro) * (dL_dhitT * inv_dd * inv_dd);
+    const float v_gd = -0.5f * e.vis * (gs.op * v_alpha_g);
+    const f3 v_gcrod = (2.0f * v_gd) * e.gcrod;
+    const f3 v_grd_n = -cross(v_gcrod, e.gro);
+    v_gro = v_gro + cross(v_gcrod, e.grd_n);
+    v_grd = v_grd + safe_normalize_bwd_il(e.grd, e.il, v_grd_n);
+    const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
+    acc[CDIM + 0] -= v_omm.x;
+    acc[CDIM + 1] -= v_omm.y;
+    acc[CDIM + 2] -= v_omm.z;
+    // dL/dM^T (math rows): v_grd (x) ray_d + v_gro (x) (o - mu)
+    const f3 rd = px.rd, omm = e.omm;
+    acc[CDIM + 3] += v_grd.x * rd.x + v_gro.x * omm.x;
+    acc[CDIM + 4] += v_grd.x * rd.y + v_gro.x * omm.y;
+    acc[CDIM + 5] += v_grd.x * rd.z + v_gro.x * omm.z;
+    acc[CDIM + 6] += v_grd.y * rd.x + v_gro.y * omm.x;
+    acc[CDIM + 7] += v_grd.y * rd.y + v_gro.y * omm.y;
+    acc[CDIM + 8] += v_grd.y * rd.z + v_gro.y * omm.z;
+    acc[CDIM + 9] += v_grd.z * rd.x + v_gro.z * omm.x;
+    acc[CDIM + 10] += v_grd.z * rd.y + v_gro.z * omm.y;
+    acc[CDIM + 11] += v_grd.z * rd.z + v_gro.z * omm.z;
+    acc[CDIM + 12] += e.vis * v_alpha_g;
+    if constexpr (DYN) {
+        acc[CDIM + 13] -= v_omm.x * px.rt;
+        acc[CDIM + 14] -= v_omm.y * px.rt;
+        acc[CDIM + 15] -= v_omm.z * px.rt;
+        px.v_t += -dot(v_omm, gs.vel);
+    }
+    if constexpr (RG) {
+        px.v_ro = px.v_ro + v_omm;
+        px.v_rd = px.v_rd + rows_tmul(gs.r0, gs.r1, gs.r2, v_grd);
+    }
+#pragma unroll
+    for (int k = 0; k < CDIM; ++k) px.buffer[k] += rgb[k] * fac;
+    px.depth_buffer += fac * last_hit_T;
+}
+
+// Two pixels per thread: a workgroup of ceil(tile/2) threads (rounded up to whole wavefronts) per
+// tile, thread tr owning the pixels 2 tr and 2 tr + 1 of the tile in row-major order. The staged Gaussian's LDS reads,
+// the wavefront reduction and the atomic adds are shared by both pixels.
 template <int CDIM, bool DYN, bool RG>
-__global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p) {
+__global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dParams p) {
+    constexpr int NT = kTileThreads / 2;  // threads (and staged Gaussians per batch) at most
     constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;
     constexpr int CS = CDIM > 0 ? CDIM : 1;
     constexpr int K = CDIM + 3 + 9 + 1 + (DYN ? 3 : 0);  // colours, mean, M, opacity, velocity
-    __shared__ int32_t s_id[kTileThreads];
-    __shared__ float4 s_m0[kTileThreads], s_m1[kTileThreads], s_m2[kTileThreads];  // M rows | M (o - mu)
-    __shared__ float4 s_xo[kTileThreads];  // o - mu (fixed origin) or mu, and opacity
-    __shared__ float4 s_vel[DYN ? kTileThreads : 1];
-    __shared__ float s_col[CL > 0 ? kTileThreads * CL : 1];
+    __shared__ int32_t s_id[NT];
+    __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | M (o - mu)
+    __shared__ float4 s_xo[NT];                      // o - mu (shared origin) or mu, and opacity
+    __shared__ float4 s_vel[DYN ? NT : 1];
+    __shared__ float s_col[CL > 0 ? NT * CL : 1];
     __shared__ float s_origin[3];
     __shared__ int s_max;
 
     const TileGrid& g = p.g;
-    const PixelCtx c = pixel_ctx(g, p.offsets);
+    const int n_tiles = g.n_tiles_w * g.n_tiles_h;
+    const int nblocks = n_tiles * g.n_cams;
+    const int logical = xcd_tile((int)blockIdx.x, nblocks);
+    const int cam = logical / n_tiles, tile = logical - cam * n_tiles;
     const int bs = g.tile_w * g.tile_h;
+    const int nthr = (bs + 1) >> 1;
+    const int tr = threadIdx.x;
     const int lane = __lane_id();
-    const f3 rd = c.inside ? ld3(p.ray_d + 3 * c.pix) : mk3(0.f, 0.f, 0.f);
-    const f3 ro = c.inside ? ld3(p.ray_o + 3 * c.pix) : mk3(0.f, 0.f, 0.f);
-    float rt = 0.f;
-    if constexpr (DYN) rt = c.inside ? p.rtd[c.pix] : 0.0f;
+    const int trow = tile / g.n_tiles_w, tcol = tile - trow * g.n_tiles_w;
+    const int gt = cam * n_tiles + tile;  // utils.h:48-58
+    const int32_t range_start = p.offsets[gt];
+    const int32_t range_end = (gt == nblocks - 1) ? (int32_t)g.n_isects : p.offsets[gt + 1];
+    const int64_t hw = (int64_t)g.width * g.height;
 
-    if (c.tr == 0) { s_origin[0] = ro.x; s_origin[1] = ro.y; s_origin[2] = ro.z; s_max = -1; }
+    BwdPixel<CS> px[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        BwdPixel<CS>& q = px[h];
+        const int qi = 2 * tr + h;
+        const int ty = qi / g.tile_w, tx = qi - ty * g.tile_w;
+        const int i = trow * g.tile_h + ty, j = tcol * g.tile_w + tx;  // utils.h:32-44
+        q.inside = qi < bs && i < g.height && j < g.width;
+        q.pix = (int64_t)cam * hw + min((int64_t)i * g.width + j, hw - 1);
+        q.rd = q.inside ? ld3(p.ray_d + 3 * q.pix) : mk3(0.f, 0.f, 0.f);
+        q.ro = q.inside ? ld3(p.ray_o + 3 * q.pix) : mk3(0.f, 0.f, 0.f);
+        q.rt = 0.f;
+        if constexpr (DYN) q.rt = q.inside ? p.rtd[q.pix] : 0.0f;
+        q.T_final = 1.0f - p.render_alpha[q.pix];
+        q.T = q.T_final;
+#pragma unroll
+        for (int k = 0; k < CS; ++k) { q.buffer[k] = 0.f; q.v_c[k] = 0.f; }
+#pragma unroll
+        for (int k = 0; k < CDIM; ++k) q.v_c[k] = q.inside ? p.v_rgb[q.pix * CDIM + k] : 0.0f;
+        q.v_d = q.inside ? p.v_depth[q.pix] : 0.0f;
+        q.v_a = q.inside ? p.v_alpha[q.pix] : 0.0f;
+        q.bin_final = q.inside ? p.last_ids[q.pix] : 0;
+        q.depth_buffer = 0.f;
+        q.v_t = 0.f;
+        q.v_ro = mk3(0.f, 0.f, 0.f);
+        q.v_rd = mk3(0.f, 0.f, 0.f);
+    }
+
+    if (tr == 0) { s_origin[0] = px[0].ro.x; s_origin[1] = px[0].ro.y; s_origin[2] = px[0].ro.z; s_max = -1; }
     __syncthreads();
     const f3 o0 = mk3(s_origin[0], s_origin[1], s_origin[2]);
-    const bool same = !c.inside || (__float_as_uint(ro.x) == __float_as_uint(o0.x) &&
-                                    __float_as_uint(ro.y) == __float_as_uint(o0.y) &&
-                                    __float_as_uint(ro.z) == __float_as_uint(o0.z));
+    bool same = true;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        same = same && (!px[h].inside || (__float_as_uint(px[h].ro.x) == __float_as_uint(o0.x) &&
+                                          __float_as_uint(px[h].ro.y) == __float_as_uint(o0.y) &&
+                                          __float_as_uint(px[h].ro.z) == __float_as_uint(o0.z)));
     const bool fixed = !DYN && __syncthreads_and(same);
 
-    const float T_final = 1.0f - p.render_alpha[c.pix];
-    float T = T_final;
-    float buffer[CS];
-    float v_c[CS];
-#pragma unroll
-    for (int k = 0; k < CS; ++k) { buffer[k] = 0.f; v_c[k] = 0.f; }
-#pragma unroll
-    for (int k = 0; k < CDIM; ++k) v_c[k] = c.inside ? p.v_rgb[c.pix * CDIM + k] : 0.0f;
-    const float v_d = c.inside ? p.v_depth[c.pix] : 0.0f;
-    const float v_a = c.inside ? p.v_alpha[c.pix] : 0.0f;
-    const int32_t bin_final = c.inside ? p.last_ids[c.pix] : 0;
-    const int32_t wave_bin_final = wave_max(bin_final);
+    const int32_t wave_bin_final = wave_max(max(px[0].bin_final, px[1].bin_final));
     if (lane == 0) atomicMax(&s_max, wave_bin_final);
-    f3 v_ro = mk3(0.f, 0.f, 0.f), v_rd = mk3(0.f, 0.f, 0.f);
-    float depth_buffer = 0.0f, v_t = 0.0f;
     // The lane that adds component k of a chunk (k = lane / 4, lanes 4k) writes to
     // dst_base[chunk] + gid * dst_stride[chunk]; both are fixed per lane.
     constexpr int kChunks = (K + 15) / 16;
@@ -81,7 +230,7 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
     for (int ch = 0; ch < kChunks; ++ch) {
         const int kk = 16 * ch + (lane >> 2);
         if (kk < CDIM) {  // colours are [n_cams, n, CDIM]: flatten id = cam * n + gid
-            dst_base[ch] = p.v_colors + ((int64_t)c.cam * g.n) * CDIM + kk;
+            dst_base[ch] = p.v_colors + ((int64_t)cam * g.n) * CDIM + kk;
             dst_stride[ch] = CDIM;
         } else if (kk < CDIM + 3) {
             dst_base[ch] = p.v_means + (kk - CDIM); dst_stride[ch] = 3;
@@ -96,19 +245,19 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
         }
     }
     __syncthreads();
-    const int32_t eff_end = min(c.range_end - 1, s_max);
-    const int32_t n_eff = eff_end - c.range_start + 1;
-    const int num_batches = n_eff > 0 ? (n_eff + bs - 1) / bs : 0;
+    const int32_t eff_end = min(range_end - 1, s_max);
+    const int32_t n_eff = eff_end - range_start + 1;
+    const int num_batches = n_eff > 0 ? (n_eff + nthr - 1) / nthr : 0;
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
-        const int32_t batch_end = eff_end - bs * b;
-        const int32_t batch_size = min(bs, batch_end + 1 - c.range_start);
-        const int32_t idx = batch_end - c.tr;
-        if (idx >= c.range_start) {
+        const int32_t batch_end = eff_end - nthr * b;
+        const int32_t batch_size = min(nthr, batch_end + 1 - range_start);
+        const int32_t idx = batch_end - tr;
+        if (tr < nthr && idx >= range_start) {
             const int32_t fid = p.flatten[idx];
-            const int64_t gid = fid - (int64_t)c.cam * g.n;
-            s_id[c.tr] = fid;
+            const int64_t gid = fid - (int64_t)cam * g.n;
+            s_id[tr] = fid;
             const f3 mu = ld3(p.means + 3 * gid);
             f3 r0, r1, r2;
             iscl_rot_rows(p.quats[gid], ld3(p.scales + 3 * gid), r0, r1, r2);
@@ -117,59 +266,40 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
                 xo = o0 - mu;
                 gro = rows_mul(r0, r1, r2, xo);
             }
-            s_m0[c.tr] = make_float4(r0.x, r0.y, r0.z, gro.x);
-            s_m1[c.tr] = make_float4(r1.x, r1.y, r1.z, gro.y);
-            s_m2[c.tr] = make_float4(r2.x, r2.y, r2.z, gro.z);
-            s_xo[c.tr] = make_float4(xo.x, xo.y, xo.z, p.opac[gid]);
+            s_m0[tr] = make_float4(r0.x, r0.y, r0.z, gro.x);
+            s_m1[tr] = make_float4(r1.x, r1.y, r1.z, gro.y);
+            s_m2[tr] = make_float4(r2.x, r2.y, r2.z, gro.z);
+            s_xo[tr] = make_float4(xo.x, xo.y, xo.z, p.opac[gid]);
             if constexpr (DYN) {
                 const f3 v = ld3(p.velocity + 3 * gid);
-                s_vel[c.tr] = make_float4(v.x, v.y, v.z, 0.f);
+                s_vel[tr] = make_float4(v.x, v.y, v.z, 0.f);
             }
             if constexpr (CL > 0) {
 #pragma unroll
-                for (int k = 0; k < CL; ++k) s_col[c.tr * CL + k] = p.colors[(int64_t)fid * CDIM + k];
+                for (int k = 0; k < CL; ++k) s_col[tr * CL + k] = p.colors[(int64_t)fid * CDIM + k];
             }
         }
         __syncthreads();
         for (int t = max(0, batch_end - wave_bin_final); t < batch_size; ++t) {
-            const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t];
-            const f3 r0 = mk3(a.x, a.y, a.z), r1 = mk3(bq.x, bq.y, bq.z), r2 = mk3(cq.x, cq.y, cq.z);
-            const float4 xo = s_xo[t];
-            const float op = xo.w;
-            f3 vel = mk3(0.f, 0.f, 0.f);
-            f3 omm, gro;  // o - mu and M (o - mu)
-            if (fixed) {
-                omm = mk3(xo.x, xo.y, xo.z);
-                gro = mk3(a.w, bq.w, cq.w);
-            } else {
-                f3 mu = mk3(xo.x, xo.y, xo.z);
-                if constexpr (DYN) {
-                    vel = mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
-                    mu = mu + rt * vel;
-                }
-                omm = ro - mu;
-                gro = rows_mul(r0, r1, r2, omm);
+            BwdGauss gs;
+            {
+                const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t], xo = s_xo[t];
+                gs.r0 = mk3(a.x, a.y, a.z);
+                gs.r1 = mk3(bq.x, bq.y, bq.z);
+                gs.r2 = mk3(cq.x, cq.y, cq.z);
+                gs.gro_fixed = mk3(a.w, bq.w, cq.w);
+                gs.xo = mk3(xo.x, xo.y, xo.z);
+                gs.op = xo.w;
+                gs.vel = mk3(0.f, 0.f, 0.f);
+                if constexpr (DYN) gs.vel = mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
             }
-            const f3 grd = rows_mul(r0, r1, r2, rd);
-            const float dd = dot(grd, grd);
-            const float il = inv_len(dd);
-            const f3 grd_n = grd * il;
-            const f3 gcrod = cross(grd_n, gro);
-            const float power = -0.5f * dot(gcrod, gcrod);
-            const float vis = __expf(power);
-            const float alpha = fminf(kMaxAlpha, op * vis);
-            const bool valid = c.inside && (batch_end - t <= bin_final) && alpha >= 1.f / 255.f;
-            if (__ballot(valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
+            const int32_t gidx = batch_end - t;
+            const BwdEval e0 = bwd_eval<DYN>(gs, px[0].ro, px[0].rd, px[0].rt, fixed,
+                                             px[0].inside && gidx <= px[0].bin_final);
+            const BwdEval e1 = bwd_eval<DYN>(gs, px[1].ro, px[1].rd, px[1].rt, fixed,
+                                             px[1].inside && gidx <= px[1].bin_final);
+            if (__ballot(e0.valid || e1.valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
 
-            // Every lane runs the same instructions; a lane whose pair is not valid contributes
-            // exact zeros (its fac and gated upstream gradients are selected to 0, and every
-            // gradient below is linear in them) and keeps its transmittance and buffers.
-            const float inv_dd = il * il;
-            const float od = dot(gro, grd);
-            const float last_hit_T = -od * inv_dd;
-            const float ra = __builtin_amdgcn_rcpf(fmaxf(1e-6f, 1.0f - alpha));
-            T = valid ? T * ra : T;
-            const float fac = valid ? alpha * T : 0.0f;
             float rgb[CS];
 #pragma unroll
             for (int k = 0; k < CS; ++k) rgb[k] = 0.f;
@@ -184,59 +314,14 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
                 }
             }
             float acc[K];
-            // grad_alpha (eval3d_bwd.cu:42-63)
-            float v_alpha = 0.0f;
 #pragma unroll
-            for (int k = 0; k < CDIM; ++k) {
-                acc[k] = v_c[k] * fac;
-                v_alpha += (rgb[k] * T - buffer[k] * ra) * v_c[k];
-            }
-            v_alpha += (last_hit_T * T - depth_buffer * ra) * v_d;
-            v_alpha += T_final * ra * v_a;
-            // geometry and opacity only below the clamp (eval3d_bwd.cu:243)
-            const bool geo = valid && op * vis <= kMaxAlpha;
-            const float v_alpha_g = geo ? v_alpha : 0.0f;
-            const float dL_dhitT = geo ? v_d * fac : 0.0f;
-
-            f3 v_gro = grd * (-dL_dhitT * inv_dd);
-            f3 v_grd = (2.0f * od * grd - dd * gro) * (dL_dhitT * inv_dd * inv_dd);
-            const float v_gd = -0.5f * vis * (op * v_alpha_g);
-            const f3 v_gcrod = (2.0f * v_gd) * gcrod;
-            const f3 v_grd_n = -cross(v_gcrod, gro);
-            v_gro = v_gro + cross(v_gcrod, grd_n);
-            v_grd = v_grd + safe_normalize_bwd_il(grd, il, v_grd_n);
-            const f3 v_omm = rows_tmul(r0, r1, r2, v_gro);
-            acc[CDIM + 0] = -v_omm.x;
-            acc[CDIM + 1] = -v_omm.y;
-            acc[CDIM + 2] = -v_omm.z;
-            // dL/dM^T (math rows): v_grd (x) ray_d + v_gro (x) (o - mu)
-            acc[CDIM + 3] = v_grd.x * rd.x + v_gro.x * omm.x;
-            acc[CDIM + 4] = v_grd.x * rd.y + v_gro.x * omm.y;
-            acc[CDIM + 5] = v_grd.x * rd.z + v_gro.x * omm.z;
-            acc[CDIM + 6] = v_grd.y * rd.x + v_gro.y * omm.x;
-            acc[CDIM + 7] = v_grd.y * rd.y + v_gro.y * omm.y;
-            acc[CDIM + 8] = v_grd.y * rd.z + v_gro.y * omm.z;
-            acc[CDIM + 9] = v_grd.z * rd.x + v_gro.z * omm.x;
-            acc[CDIM + 10] = v_grd.z * rd.y + v_gro.z * omm.y;
-            acc[CDIM + 11] = v_grd.z * rd.z + v_gro.z * omm.z;
-            acc[CDIM + 12] = vis * v_alpha_g;
-            if constexpr (DYN) {
-                acc[CDIM + 13] = -v_omm.x * rt;
-                acc[CDIM + 14] = -v_omm.y * rt;
-                acc[CDIM + 15] = -v_omm.z * rt;
-                v_t += -dot(v_omm, vel);
-            }
-            if constexpr (RG) {
-                v_ro = v_ro + v_omm;
-                v_rd = v_rd + rows_tmul(r0, r1, r2, v_grd);
-            }
-#pragma unroll
-            for (int k = 0; k < CDIM; ++k) buffer[k] += rgb[k] * fac;
-            depth_buffer += fac * last_hit_T;
+            for (int k = 0; k < K; ++k) acc[k] = 0.f;
+            bwd_pair<CDIM, CS, K, DYN, RG>(px[0], gs, e0, rgb, acc);
+            bwd_pair<CDIM, CS, K, DYN, RG>(px[1], gs, e1, rgb, acc);
 
             // wave totals by reduce-scatter: lane l ends with component 16 * chunk + (l >> 2); the
             // first lane of each quad adds it, one atomic instruction per chunk of 16 components
-            const int64_t gid = s_id[t] - (int64_t)c.cam * g.n;
+            const int64_t gid = s_id[t] - (int64_t)cam * g.n;
 #pragma unroll
             for (int ch = 0; ch < kChunks; ++ch) {
                 float chunk[16];
@@ -248,12 +333,15 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
             }
         }
     }
-    if (c.inside) {
-        if constexpr (RG) {
-            st3(p.v_ray_o + 3 * c.pix, v_ro);
-            st3(p.v_ray_d + 3 * c.pix, v_rd);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (px[h].inside) {
+            if constexpr (RG) {
+                st3(p.v_ray_o + 3 * px[h].pix, px[h].v_ro);
+                st3(p.v_ray_d + 3 * px[h].pix, px[h].v_rd);
+            }
+            if constexpr (DYN) p.v_time[px[h].pix] = px[h].v_t;
         }
-        if constexpr (DYN) p.v_time[c.pix] = v_t;
     }
 }
 
@@ -262,7 +350,8 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_bwd_kernel(Eval3dParams p
 template <int CDIM>
 int launch_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t s) {
     const int n_blocks = p.g.n_tiles_w * p.g.n_tiles_h * p.g.n_cams;
-    const int bs = p.g.tile_w * p.g.tile_h;
+    // two pixels per thread, whole wavefronts (the reduction uses every lane)
+    const int bs = ((p.g.tile_w * p.g.tile_h + 1) / 2 + 63) / 64 * 64;
     if constexpr (CDIM <= kColorLdsMax) {
         if (!ray_grads) {
             if (dyn) eval3d_bwd_kernel<CDIM, true, false><<<n_blocks, bs, 0, s>>>(p);
