@@ -34,8 +34,8 @@ template <int CS>
 struct BwdPixel {
     f3 ro, rd;
     float rt;
-    float T, T_final, depth_buffer, v_t;
-    float buffer[CS], v_c[CS];
+    float T, T_final, depth_buffer, buf_v, v_t;
+    float v_c[CS];
     float v_d, v_a;
     int32_t bin_final;
     bool inside;
@@ -86,6 +86,13 @@ XSG_DEV BwdEval bwd_eval(const BwdGauss& gs, const f3 ro, const f3 rd, float rt,
 // Gradient contribution of one pair, added to acc (eval3d_bwd.cu:206-271). A pair that is not
 // valid adds exact zeros (its fac and gated upstream gradients are selected to 0, and every
 // gradient is linear in them) and leaves the pixel's transmittance and buffers unchanged.
+//
+// The reference's chain from dL/dalpha through gcrod = n x gro (n = grd / |grd|) and
+// safe_normalize_bwd collapses to one vector: with s = n . gro, w = gro - s n (= gcrod x n) and
+// A = 2 dL/d|gcrod|^2 = -vis * opac * dL/dalpha, it adds A w to dL/dgro and -A s / |grd| w to
+// dL/dgrd (expand (n x gro) x n, (n x gro) x gro and the projection in safe_normalize_bwd). The
+// colour terms of dL/dalpha use running sums: sum_k buffer_k v_k is kept per pixel instead of
+// the buffer.
 template <int CDIM, int CS, int K, bool DYN, bool RG>
 XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, const float (&rgb)[CS],
                       float (&acc)[K]) {
@@ -96,13 +103,14 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     px.T = e.valid ? px.T * ra : px.T;
     const float T = px.T;
     const float fac = e.valid ? e.alpha * T : 0.0f;
-    // grad_alpha (eval3d_bwd.cu:42-63)
-    float v_alpha = 0.0f;
+    // grad_alpha (eval3d_bwd.cu:42-63) with rv = sum_k rgb_k v_k and buf_v = sum_k buffer_k v_k
+    float rv = 0.0f;
 #pragma unroll
     for (int k = 0; k < CDIM; ++k) {
         acc[k] += px.v_c[k] * fac;
-        v_alpha += (rgb[k] * T - px.buffer[k] * ra) * px.v_c[k];
+        rv += rgb[k] * px.v_c[k];
     }
+    float v_alpha = rv * T - px.buf_v * ra;
     v_alpha += (last_hit_T * T - px.depth_buffer * ra) * px.v_d;
     v_alpha += px.T_final * ra * px.v_a;
     // geometry and opacity only below the clamp (eval3d_bwd.cu:243)
@@ -110,13 +118,15 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     const float v_alpha_g = geo ? v_alpha : 0.0f;
     const float dL_dhitT = geo ? px.v_d * fac : 0.0f;
 
+    // hit-distance terms as the reference writes them (eval3d_bwd.cu:236-241)
     f3 v_gro = e.grd * (-dL_dhitT * inv_dd);
     f3 v_grd = (2.0f * od * e.grd - e.dd * e.gro) * (dL_dhitT * inv_dd * inv_dd);
-    const float v_gd = -0.5f * e.vis * (gs.op * v_alpha_g);
-    const f3 v_gcrod = (2.0f * v_gd) * e.gcrod;
-    const f3 v_grd_n = -cross(v_gcrod, e.gro);
-    v_gro = v_gro + cross(v_gcrod, e.grd_n);
-    v_grd = v_grd + safe_normalize_bwd_il(e.grd, e.il, v_grd_n);
+    // the alpha terms through gcrod, normalisation and M, collapsed (see above)
+    const float sn = e.il * od;               // n . gro
+    const f3 w = cross(e.gcrod, e.grd_n);     // gro - (n . gro) n, without its cancellation
+    const float A = -(e.vis * gs.op) * v_alpha_g;
+    v_gro = v_gro + A * w;
+    v_grd = v_grd + (-A * sn * e.il) * w;
     const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
     acc[CDIM + 0] -= v_omm.x;
     acc[CDIM + 1] -= v_omm.y;
@@ -143,8 +153,7 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
         px.v_ro = px.v_ro + v_omm;
         px.v_rd = px.v_rd + rows_tmul(gs.r0, gs.r1, gs.r2, v_grd);
     }
-#pragma unroll
-    for (int k = 0; k < CDIM; ++k) px.buffer[k] += rgb[k] * fac;
+    px.buf_v += fac * rv;
     px.depth_buffer += fac * last_hit_T;
 }
 
@@ -196,7 +205,8 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
         q.T_final = 1.0f - p.render_alpha[q.pix];
         q.T = q.T_final;
 #pragma unroll
-        for (int k = 0; k < CS; ++k) { q.buffer[k] = 0.f; q.v_c[k] = 0.f; }
+        for (int k = 0; k < CS; ++k) q.v_c[k] = 0.f;
+        q.buf_v = 0.f;
 #pragma unroll
         for (int k = 0; k < CDIM; ++k) q.v_c[k] = q.inside ? p.v_rgb[q.pix * CDIM + k] : 0.0f;
         q.v_d = q.inside ? p.v_depth[q.pix] : 0.0f;
