@@ -5,9 +5,11 @@
 //  * batches start at the largest last_id of the tile instead of the end of the tile's list; the
 //    reference loads and skips those trailing batches (every index there exceeds every pixel's
 //    last_id, eval3d_bwd.cu:155-159);
-//  * dL/dM (M = S^-1 R^T) is accumulated per Gaussian and turned into quaternion / scale gradients
-//    once per Gaussian by eval3d_bwd_epilogue: quat_scale_to_preci_half_vjp (utils.h:232-263) is
-//    linear in dL/dM, so the sum of per-pair vjps equals the vjp of the sum;
+//  * the gradient of M = S^-1 R^T is accumulated per Gaussian, as Q = sum of v_grd (x) grd +
+//    v_gro (x) gro (dL/dM = Q S R^T), and turned into quaternion / scale gradients once per
+//    Gaussian by the epilogue: quat_scale_to_preci_half_vjp (utils.h:232-263) is linear in dL/dM,
+//    so the sum of per-pair vjps equals the vjp of the sum, and the scale gradient -Q_ii / s_i
+//    sums the same per-pair products as the reference;
 //  * per-pair gradients are summed over the 64 lanes of a wavefront by a reduce-scatter that
 //    leaves each component's total on its own lane, and one atomic instruction per 16
 //    components adds them (one lane per component);
@@ -131,17 +133,18 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     acc[CDIM + 0] -= v_omm.x;
     acc[CDIM + 1] -= v_omm.y;
     acc[CDIM + 2] -= v_omm.z;
-    // dL/dM^T (math rows): v_grd (x) ray_d + v_gro (x) (o - mu)
-    const f3 rd = px.rd, omm = e.omm;
-    acc[CDIM + 3] += v_grd.x * rd.x + v_gro.x * omm.x;
-    acc[CDIM + 4] += v_grd.x * rd.y + v_gro.x * omm.y;
-    acc[CDIM + 5] += v_grd.x * rd.z + v_gro.x * omm.z;
-    acc[CDIM + 6] += v_grd.y * rd.x + v_gro.y * omm.x;
-    acc[CDIM + 7] += v_grd.y * rd.y + v_gro.y * omm.y;
-    acc[CDIM + 8] += v_grd.y * rd.z + v_gro.y * omm.z;
-    acc[CDIM + 9] += v_grd.z * rd.x + v_gro.z * omm.x;
-    acc[CDIM + 10] += v_grd.z * rd.y + v_gro.z * omm.y;
-    acc[CDIM + 11] += v_grd.z * rd.z + v_gro.z * omm.z;
+    // Q = v_grd (x) grd + v_gro (x) gro; dL/dM = Q S R^T, and the scale gradient -Q_ii / s_i is
+    // the reference's per-pair product of the pair's own values
+    const f3 gd = e.grd, go = e.gro;
+    acc[CDIM + 3] += v_grd.x * gd.x + v_gro.x * go.x;
+    acc[CDIM + 4] += v_grd.x * gd.y + v_gro.x * go.y;
+    acc[CDIM + 5] += v_grd.x * gd.z + v_gro.x * go.z;
+    acc[CDIM + 6] += v_grd.y * gd.x + v_gro.y * go.x;
+    acc[CDIM + 7] += v_grd.y * gd.y + v_gro.y * go.y;
+    acc[CDIM + 8] += v_grd.y * gd.z + v_gro.y * go.z;
+    acc[CDIM + 9] += v_grd.z * gd.x + v_gro.z * go.x;
+    acc[CDIM + 10] += v_grd.z * gd.y + v_gro.z * go.y;
+    acc[CDIM + 11] += v_grd.z * gd.z + v_gro.z * go.z;
     acc[CDIM + 12] += e.vis * v_alpha_g;
     if constexpr (DYN) {
         acc[CDIM + 13] -= v_omm.x * px.rt;
@@ -173,6 +176,10 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     __shared__ float s_col[CL > 0 ? NT * CL : 1];
     __shared__ float s_origin[3];
     __shared__ int s_max;
+    constexpr int NWB = NT / 64;
+    __shared__ RayBundle s_bundle[NWB];
+    __shared__ int32_t s_wbf[NWB];       // largest last id of each wavefront's pixels
+    __shared__ uint64_t s_mask[NWB][NWB];  // [wavefront][staging wavefront]: Gaussians it evaluates
 
     const TileGrid& g = p.g;
     const int n_tiles = g.n_tiles_w * g.n_tiles_h;
@@ -230,6 +237,18 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     const bool fixed = !DYN && __syncthreads_and(same);
 
     const int32_t wave_bin_final = wave_max(max(px[0].bin_final, px[1].bin_final));
+    const int wave = tr >> 6;
+    const int nwb = (int)(blockDim.x >> 6);
+    {
+        const bool in2[2] = {px[0].inside, px[1].inside};
+        const f3 ro2[2] = {px[0].ro, px[1].ro}, rd2[2] = {px[0].rd, px[1].rd};
+        const float rt2[2] = {px[0].rt, px[1].rt};
+        const RayBundle bun = wave_bundle<2>(in2, ro2, rd2, rt2);
+        if (lane == 0) {
+            s_bundle[wave] = bun;
+            s_wbf[wave] = wave_bin_final;
+        }
+    }
     if (lane == 0) atomicMax(&s_max, wave_bin_final);
     // The lane that adds component k of a chunk (k = lane / 4, lanes 4k) writes to
     // dst_base[chunk] + gid * dst_stride[chunk]; both are fixed per lane.
@@ -264,13 +283,18 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
         const int32_t batch_end = eff_end - nthr * b;
         const int32_t batch_size = min(nthr, batch_end + 1 - range_start);
         const int32_t idx = batch_end - tr;
+        bool staged = false;
+        CullGauss cg;
         if (tr < nthr && idx >= range_start) {
+            staged = true;
             const int32_t fid = p.flatten[idx];
             const int64_t gid = fid - (int64_t)cam * g.n;
             s_id[tr] = fid;
             const f3 mu = ld3(p.means + 3 * gid);
+            const float4 q = p.quats[gid];
+            const f3 sc = ld3(p.scales + 3 * gid);
             f3 r0, r1, r2;
-            iscl_rot_rows(p.quats[gid], ld3(p.scales + 3 * gid), r0, r1, r2);
+            iscl_rot_rows(q, sc, r0, r1, r2);
             f3 gro = mk3(0.f, 0.f, 0.f), xo = mu;
             if (fixed) {
                 xo = o0 - mu;
@@ -279,18 +303,30 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
             s_m0[tr] = make_float4(r0.x, r0.y, r0.z, gro.x);
             s_m1[tr] = make_float4(r1.x, r1.y, r1.z, gro.y);
             s_m2[tr] = make_float4(r2.x, r2.y, r2.z, gro.z);
-            s_xo[tr] = make_float4(xo.x, xo.y, xo.z, p.opac[gid]);
+            const float op = p.opac[gid];
+            s_xo[tr] = make_float4(xo.x, xo.y, xo.z, op);
+            f3 vel = mk3(0.f, 0.f, 0.f);
             if constexpr (DYN) {
-                const f3 v = ld3(p.velocity + 3 * gid);
-                s_vel[tr] = make_float4(v.x, v.y, v.z, 0.f);
+                vel = ld3(p.velocity + 3 * gid);
+                s_vel[tr] = make_float4(vel.x, vel.y, vel.z, 0.f);
             }
             if constexpr (CL > 0) {
 #pragma unroll
                 for (int k = 0; k < CL; ++k) s_col[tr * CL + k] = p.colors[(int64_t)fid * CDIM + k];
             }
+            cg = cull_gauss(mu, r0, r1, r2, sc, q, op, vel);
+        }
+        // which wavefronts evaluate this Gaussian: those with a pixel at or past it (last ids)
+        // that the Gaussian can reach; one ballot per wavefront
+        for (int k = 0; k < nwb; ++k) {
+            const bool keep = staged && idx <= s_wbf[k] && cull_keep<DYN>(s_bundle[k], cg);
+            const uint64_t m = __ballot(keep);
+            if (lane == 0) s_mask[k][wave] = m;
         }
         __syncthreads();
-        for (int t = max(0, batch_end - wave_bin_final); t < batch_size; ++t) {
+        for (int w2 = 0; w2 < nwb; ++w2)
+        for (uint64_t m = uniform_u64(s_mask[wave][w2]); m != 0; m &= m - 1) {
+            const int t = (w2 << 6) + (int)__builtin_ctzll(m);
             BwdGauss gs;
             {
                 const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t], xo = s_xo[t];

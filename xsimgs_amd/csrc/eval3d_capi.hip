@@ -28,11 +28,12 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float* __restrict__ a, int
 }
 
 // quat_scale_to_preci_half_vjp + quat_to_rotmat_vjp (utils.h:208-263) applied once per Gaussian to
-// the accumulated dL/dM^T. vmt holds M^T gradients row-major: vmt[c*3 + r] is the glm element
-// v_M[c][r] of the reference (v_M = transpose(v_Mt)).
+// the accumulated Q = sum over pairs of v_grd (x) grd + v_gro (x) gro (q[3 i + k] = Q_ik, i the row
+// of M = S^-1 R^T). With rd = R S grd and o - mu = R S gro, dL/dM_ir = sum_k Q_ik s_k R_rk; the
+// scale gradient is -Q_ii / s_i.
 __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const float4* __restrict__ quats,
                                                               const float* __restrict__ scales,
-                                                              const float* __restrict__ vmt,
+                                                              const float* __restrict__ qacc,
                                                               float4* __restrict__ v_quats,
                                                               float* __restrict__ v_scales) {
     const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -41,12 +42,25 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const f
     float w = q.x, x = q.y, y = q.z, z = q.w;
     const float inv_norm = rsqrtf(x * x + y * y + z * z + w * w);
     x *= inv_norm; y *= inv_norm; z *= inv_norm; w *= inv_norm;
-    const float s[3] = {1.0f / scales[3 * i], 1.0f / scales[3 * i + 1], 1.0f / scales[3 * i + 2]};
-    float vm[3][3];  // glm v_M[c][r]
+    const float sc[3] = {scales[3 * i], scales[3 * i + 1], scales[3 * i + 2]};
+    const float s[3] = {1.0f / sc[0], 1.0f / sc[1], 1.0f / sc[2]};
+    // R columns (glm R[c], R[c][r] = R_rc) from quat_to_rotmat (utils.h:61-83)
+    const float x2 = x * x, y2 = y * y, z2 = z * z, xy = x * y, xz = x * z, yz = y * z;
+    const float wx = w * x, wy = w * y, wz = w * z;
+    const float R[3][3] = {{1.f - 2.f * (y2 + z2), 2.f * (xy + wz), 2.f * (xz - wy)},
+                           {2.f * (xy - wz), 1.f - 2.f * (x2 + z2), 2.f * (yz + wx)},
+                           {2.f * (xz + wy), 2.f * (yz - wx), 1.f - 2.f * (x2 + y2)}};
+    float Q[3][3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int k = 0; k < 3; ++k) Q[r][k] = qacc[9 * i + 3 * r + k];
+    float vm[3][3];  // glm v_M[c][r]: dL/dM for row c of M, component r
 #pragma unroll
     for (int cc = 0; cc < 3; ++cc)
 #pragma unroll
-        for (int r = 0; r < 3; ++r) vm[cc][r] = vmt[9 * i + 3 * cc + r];
+        for (int r = 0; r < 3; ++r)
+            vm[cc][r] = Q[cc][0] * sc[0] * R[0][r] + Q[cc][1] * sc[1] * R[1][r] + Q[cc][2] * sc[2] * R[2][r];
     // v_R = v_M * S  -> glm v_R[c][r] = v_M[c][r] * s_c
     float V[3][3];
 #pragma unroll
@@ -65,15 +79,8 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const f
     const float dp = vq[0] * qn[0] + vq[1] * qn[1] + vq[2] * qn[2] + vq[3] * qn[3];
     v_quats[i] = make_float4((vq[0] - dp * qn[0]) * inv_norm, (vq[1] - dp * qn[1]) * inv_norm,
                              (vq[2] - dp * qn[2]) * inv_norm, (vq[3] - dp * qn[3]) * inv_norm);
-    // R columns (glm R[c]) from quat_to_rotmat (utils.h:61-83)
-    const float x2 = x * x, y2 = y * y, z2 = z * z, xy = x * y, xz = x * z, yz = y * z;
-    const float wx = w * x, wy = w * y, wz = w * z;
-    const float R[3][3] = {{1.f - 2.f * (y2 + z2), 2.f * (xy + wz), 2.f * (xz - wy)},
-                           {2.f * (xy - wz), 1.f - 2.f * (x2 + z2), 2.f * (yz + wx)},
-                           {2.f * (xz + wy), 2.f * (yz - wx), 1.f - 2.f * (x2 + y2)}};
 #pragma unroll
-    for (int cc = 0; cc < 3; ++cc)
-        v_scales[3 * i + cc] = -s[cc] * s[cc] * (R[cc][0] * vm[cc][0] + R[cc][1] * vm[cc][1] + R[cc][2] * vm[cc][2]);
+    for (int cc = 0; cc < 3; ++cc) v_scales[3 * i + cc] = -Q[cc][cc] * s[cc];
 }
 
 bool cdim_supported(int c) {

@@ -51,7 +51,7 @@ XSG_DEV PixelCtx pixel_ctx(const TileGrid& g, const int32_t* __restrict__ offset
     const int trow = c.tile / g.n_tiles_w, tcol = c.tile - trow * g.n_tiles_w;
     c.i = trow * g.tile_h + ty;  // utils.h:32-44
     c.j = tcol * g.tile_w + tx;
-    c.inside = c.i < g.height && c.j < g.width;
+    c.inside = c.tr < g.tile_w * g.tile_h && c.i < g.height && c.j < g.width;
     const int64_t hw = (int64_t)g.width * g.height;
     c.pix = (int64_t)c.cam * hw + min((int64_t)c.i * g.width + c.j, hw - 1);
     const int gt = c.cam * n_tiles + c.tile;  // utils.h:48-58
@@ -90,6 +90,179 @@ XSG_DEV f3 safe_normalize(f3 v) { return v * inv_len(dot(v, v)); }
 // safe_normalize_bwd (utils.h:198-206) with il = inv_len(|v|^2) already known
 XSG_DEV f3 safe_normalize_bwd_il(f3 v, float il, f3 d_out) {
     return il * d_out - (il * il * il * dot(d_out, v)) * v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Conservative (wavefront, Gaussian) culling.
+//
+// A pair adds nothing unless alpha = min(0.999, op exp(-d^2 / 2)) >= 1/255, d = |n x gro| being
+// the distance, in the Gaussian's normalised frame (x -> M x, M = S^-1 R^T, centre at 0), from the
+// centre to the pixel's ray line {gro + t n}. For a wavefront, every ray starts within rho of a
+// point c and points within angle theta of a unit axis a. In the normalised frame the origins lie
+// within rho / s_min of g0 = M (c - mu), and each direction M d is within theta' of M a, with
+//   sin theta' <= sin theta |Ma x Mb| / (|Ma| |Md|) <= sin theta (s_max / (s1 s2 s3)) /
+//                 (|Ma| (|Ma| cos theta - sin theta / s_min))
+// (d = cos phi a + sin phi b, (Ma) x (Mb) = det M M^-T (a x b), |M^-T| = s_max, |Mb| <= 1/s_min).
+// So d >= (|g0 x Ma| cos theta' - |g0 . Ma| sin theta') / |Ma| - rho / s_min. Independently, as
+// |M w| >= |w| / s_max, d >= dist(mu, line) / s_max >= (|v x a| cos theta - |v . a| sin theta - rho)
+// / s_max with v = mu - c, which stays tight for very flat Gaussians where theta' is large. When
+// either bound exceeds d_lim = sqrt(2 ln(255 op)) (plus a bound on the f32 error of the per-pair
+// d) no pixel of the wavefront can take the Gaussian: the pair would be evaluated and skipped by the alpha test, and
+// skipping it unevaluated changes no output. Pairs whose per-pair math could overflow or produce
+// NaN (non-finite inputs, degenerate scales or rays) are always kept, so they reach the alpha test
+// as in the reference.
+struct RayBundle {
+    float cx, cy, cz;    // centre of the ray origins
+    float ax, ay, az;    // unit axis
+    float cos_t, sin_t;  // bound on the angle between a ray and the axis
+    float rho;           // bound on |o_i - c|
+    float rt_max;        // bound on |time delta| (dynamic)
+    float rd_max;        // bound on |rd_i|
+    int mode;            // kBundleCull, kBundleKeepAll or kBundleEmpty
+};
+constexpr int kBundleCull = 0, kBundleKeepAll = 1, kBundleEmpty = 2;
+
+XSG_DEV float wave_sum_f(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+XSG_DEV float wave_max_f(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+XSG_DEV float wave_min_f(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+// A wave-uniform 64-bit value read from LDS, moved to scalar registers (readfirstlane is signed:
+// each half goes through uint32_t so that the low half is not sign-extended).
+XSG_DEV uint64_t uniform_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+XSG_DEV bool finite3(f3 v) { return isfinite(v.x) && isfinite(v.y) && isfinite(v.z); }
+XSG_DEV f3 sel3(bool c, f3 a, f3 b) { return mk3(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z); }
+
+// Bundle of the P pixels per lane of a full wavefront (all 64 lanes active). Pixels outside the
+// image do not count; one inside pixel with a degenerate ray turns culling off for the wavefront.
+template <int P>
+XSG_DEV RayBundle wave_bundle(const bool (&inside)[P], const f3 (&ro)[P], const f3 (&rd)[P],
+                              const float (&rt)[P]) {
+    RayBundle b;
+    bool irregular = false, any = false;
+    f3 dn[P], sum = mk3(0.f, 0.f, 0.f), first = mk3(0.f, 0.f, 0.f);
+    bool use[P];
+    float rd2 = 0.f, rtm = 0.f;
+#pragma unroll
+    for (int h = P - 1; h >= 0; --h) {
+        const float l = dot(rd[h], rd[h]);
+        const bool reg = l >= 1e-12f && l <= 1e12f && finite3(ro[h]) && isfinite(rt[h]);
+        irregular = irregular || (inside[h] && !reg);
+        use[h] = inside[h] && reg;
+        any = any || use[h];
+        dn[h] = sel3(use[h], rd[h] * __builtin_amdgcn_rsqf(l), mk3(0.f, 0.f, 0.f));
+        sum = sum + dn[h];
+        rd2 = use[h] ? fmaxf(rd2, l) : rd2;
+        rtm = use[h] ? fmaxf(rtm, fabsf(rt[h])) : rtm;
+        first = sel3(use[h], ro[h], first);  // the lowest usable pixel of the lane
+    }
+    const uint64_t any_mask = __ballot(any);
+    const bool irr = __ballot(irregular) != 0;
+    sum = mk3(wave_sum_f(sum.x), wave_sum_f(sum.y), wave_sum_f(sum.z));
+    const float sl = dot(sum, sum);
+    const f3 a = sum * (sl > 0.f ? __builtin_amdgcn_rsqf(sl) : 0.f);
+    float smax = 0.f, cmin = 1.f;
+#pragma unroll
+    for (int h = 0; h < P; ++h) {
+        const f3 x = cross(dn[h], a);
+        smax = use[h] ? fmaxf(smax, __builtin_amdgcn_sqrtf(dot(x, x))) : smax;
+        cmin = use[h] ? fminf(cmin, dot(dn[h], a)) : cmin;
+    }
+    smax = wave_max_f(smax);
+    cmin = wave_min_f(cmin);
+    const int src = any_mask ? (int)__builtin_ctzll(any_mask) : 0;
+    const f3 c = mk3(__shfl(first.x, src, 64), __shfl(first.y, src, 64), __shfl(first.z, src, 64));
+    float rho = 0.f;
+#pragma unroll
+    for (int h = 0; h < P; ++h) {
+        const f3 u = ro[h] - c;
+        rho = use[h] ? fmaxf(rho, __builtin_amdgcn_sqrtf(dot(u, u))) : rho;
+    }
+    rho = wave_max_f(rho);
+    b.cx = c.x; b.cy = c.y; b.cz = c.z;
+    b.ax = a.x; b.ay = a.y; b.az = a.z;
+    b.sin_t = fminf(1.f, smax * 1.00001f + 1e-6f);
+    b.cos_t = __builtin_amdgcn_sqrtf(fmaxf(0.f, 1.f - b.sin_t * b.sin_t));
+    b.rho = rho * 1.000001f;
+    b.rt_max = wave_max_f(rtm);
+    b.rd_max = __builtin_amdgcn_sqrtf(wave_max_f(rd2)) * 1.000001f;
+    // a bundle wider than 60 degrees is not worth bounding
+    b.mode = any_mask == 0 ? kBundleEmpty : ((irr || !(sl > 0.f) || !(cmin > 0.5f)) ? kBundleKeepAll : kBundleCull);
+    return b;
+}
+
+// Per-Gaussian part of the test, computed once per staged Gaussian.
+struct CullGauss {
+    f3 mu, r0, r1, r2;  // centre and rows of M
+    float inv_smin;     // 1 / s_min
+    float s_max;
+    float cone;         // s_max / (s1 s2 s3) = 1 / (product of the two smaller scales)
+    float s_min, d_lim, vel_len;
+    bool ok;            // finite inputs, scales in [1e-12, 1e9], a quaternion that normalises
+    bool op_low;        // op < 1/255: alpha never reaches the threshold
+};
+
+XSG_DEV CullGauss cull_gauss(f3 mu, f3 r0, f3 r1, f3 r2, f3 s, float4 q, float op, f3 vel) {
+    CullGauss g;
+    g.mu = mu; g.r0 = r0; g.r1 = r1; g.r2 = r2;
+    const float s_max = fmaxf(s.x, fmaxf(s.y, s.z));
+    g.s_max = s_max;
+    g.s_min = fminf(s.x, fminf(s.y, s.z));
+    g.inv_smin = 1.f / g.s_min;
+    g.cone = s_max / (s.x * s.y * s.z);
+    const float q2 = q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w;
+    g.vel_len = __builtin_amdgcn_sqrtf(dot(vel, vel));
+    g.ok = finite3(mu) && g.s_min >= 1e-12f && s_max <= 1e9f && q2 >= 1e-30f && q2 <= 1e30f && isfinite(op) &&
+           isfinite(g.vel_len);
+    g.op_low = op < 1.f / 255.f;
+    // 2 ln(255 op) through log2; + 3e-3 covers the rounding of log, exp, the product and the compare
+    const float l2 = 2.f * 0.69314718f * __builtin_amdgcn_logf(fmaxf(255.f * op, 1.f));
+    g.d_lim = __builtin_amdgcn_sqrtf(fmaxf(0.f, l2)) * 1.0001f + 3e-3f;
+    return g;
+}
+
+// True unless no pixel of the bundle can take the Gaussian.
+template <bool DYN>
+XSG_DEV bool cull_keep(const RayBundle& b, const CullGauss& g) {
+    if (b.mode != kBundleCull) return b.mode == kBundleKeepAll;
+    const f3 v = mk3(b.cx, b.cy, b.cz) - g.mu, a = mk3(b.ax, b.ay, b.az);
+    const f3 g0 = rows_mul(g.r0, g.r1, g.r2, v);  // M (c - mu)
+    const f3 ma = rows_mul(g.r0, g.r1, g.r2, a);  // M a
+    const float ma_len = __builtin_amdgcn_sqrtf(dot(ma, ma));
+    const float shift = b.rho + (DYN ? b.rt_max * g.vel_len : 0.f);  // |o_i - c| + |mu(t) - mu|
+    const float Dr = __builtin_amdgcn_sqrtf(dot(v, v)) + shift;     // bound on |o_i - mu(t)|
+    const float L = Dr * g.inv_smin;                                 // bound on |gro| of every pair
+    // per-pair products stay below 1e18, so the alpha test sees finite values
+    const bool safe = g.s_min * g.s_min * 1e18f >= Dr * b.rd_max;
+    const float mc = ma_len * b.cos_t, ms = b.sin_t * g.inv_smin;
+    const bool narrow = mc - ms > 0.01f * mc;  // the direction bound below holds, to 1% cancellation
+    const float sin_tp = fminf(1.f, b.sin_t * g.cone / (ma_len * (mc - ms)) * 1.00001f + 1e-6f);
+    const float cos_tp = __builtin_amdgcn_sqrtf(fmaxf(0.f, 1.f - sin_tp * sin_tp));
+    const f3 x = cross(g0, ma);
+    const float lhs = (__builtin_amdgcn_sqrtf(dot(x, x)) * cos_tp - fabsf(dot(g0, ma)) * sin_tp) / ma_len;
+    // 2e-5 L bounds the f32 error of the per-pair d (about 17 ulp of |gro|) and of these tests
+    const float d_err = g.d_lim + 2e-5f * L;
+    const bool far_n = narrow && lhs > d_err + shift * g.inv_smin * 1.00001f;
+    // world-space bound (1e-5 Dr: this test's own rounding)
+    const f3 xw = cross(v, a);
+    const float lhs_w = __builtin_amdgcn_sqrtf(dot(xw, xw)) * b.cos_t - fabsf(dot(v, a)) * b.sin_t;
+    const bool far_w = lhs_w > d_err * g.s_max * 1.0001f + shift * 1.00001f + 1e-5f * Dr;
+    const bool skip = g.ok && safe && (g.op_low || far_n || far_w);
+    return !skip;
 }
 
 // Lane-to-lane moves inside rows of 16 lanes (DPP). `update_dpp` with all rows/banks enabled and
@@ -181,7 +354,7 @@ struct Eval3dParams {
     float* v_ray_d;
     float* v_velocity;
     float* v_time;
-    float* v_mt;         // workspace [n, 9]: sum of dL/dM^T per Gaussian (row-major of M^T)
+    float* v_mt;         // workspace [n, 9]: Q = sum of v_grd (x) grd + v_gro (x) gro per Gaussian
     unsigned long long* pair_counts;  // forward, optional: += [evaluated, contributing] pairs
 };
 
