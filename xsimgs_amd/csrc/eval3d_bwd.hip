@@ -15,9 +15,11 @@
 //    components adds them (one lane per component);
 //  * each thread owns two pixels, so the staged Gaussian's LDS reads, the reduction and the atomics
 //    serve both;
-//  * divisions in the per-pair math are reciprocal-multiplies (v_rcp_f32, 1 ulp) and 1/|grd|^2 is
-//    the square of the normalisation's reciprocal square root;
-//  * with a shared ray origin, the staged Gaussian carries o - mu instead of mu.
+//  * divisions in the per-pair math are reciprocal-multiplies (v_rcp_f32, 1 ulp);
+//  * (wavefront, Gaussian) pairs that no pixel of the wavefront can take are skipped unevaluated
+//    (cull_keep); they would add exact zeros.
+#include <type_traits>
+
 #include "xsg_eval3d.h"
 
 namespace xsg {
@@ -36,9 +38,10 @@ template <int CS>
 struct BwdPixel {
     f3 ro, rd;
     float rt;
-    float T, T_final, depth_buffer, buf_v, v_t;
+    float T, v_t;
+    float buf;  // sum over composited pairs of fac (rgb . v_rgb + hit_t v_depth), minus T_final v_alpha
     float v_c[CS];
-    float v_d, v_a;
+    float v_d;
     int32_t bin_final;
     bool inside;
     int64_t pix;
@@ -48,116 +51,119 @@ struct BwdPixel {
 // The staged Gaussian of one loop step.
 struct BwdGauss {
     f3 r0, r1, r2;   // rows of M
-    f3 xo;           // o - mu (shared origin) or mu
+    f3 mu;
     f3 gro_fixed;    // M (o - mu) (shared origin)
     f3 vel;
     float op;
 };
 
-// alpha evaluation of one (pixel, Gaussian) pair (eval3d_bwd.cu:172-205)
+// alpha evaluation of one (pixel, Gaussian) pair (eval3d_bwd.cu:172-205) in the forward kernel's
+// arithmetic: |n x gro|^2 = |grd x gro|^2 / |grd|^2, so that the transmittance this sweep divides
+// out is the one the forward pass multiplied in.
 struct BwdEval {
-    f3 omm, gro, grd, grd_n, gcrod;
-    float dd, il, vis, alpha;
+    f3 gro, grd, c;                  // c = grd x gro
+    float inv_dd, vis, araw, alpha;  // araw = op * vis, before the clamp
     bool valid;
 };
 
-template <bool DYN>
-XSG_DEV BwdEval bwd_eval(const BwdGauss& gs, const f3 ro, const f3 rd, float rt, bool fixed, bool in_range) {
+template <bool DYN, bool FIXED>
+XSG_DEV BwdEval bwd_eval(const BwdGauss& gs, const f3 ro, const f3 rd, float rt, bool in_range) {
     BwdEval e;
-    if (fixed) {
-        e.omm = gs.xo;
+    if constexpr (FIXED) {
         e.gro = gs.gro_fixed;
     } else {
-        f3 mu = gs.xo;
+        f3 mu = gs.mu;
         if constexpr (DYN) mu = mu + rt * gs.vel;
-        e.omm = ro - mu;
-        e.gro = rows_mul(gs.r0, gs.r1, gs.r2, e.omm);
+        e.gro = rows_mul(gs.r0, gs.r1, gs.r2, ro - mu);
     }
     e.grd = rows_mul(gs.r0, gs.r1, gs.r2, rd);
-    e.dd = dot(e.grd, e.grd);
-    e.il = inv_len(e.dd);
-    e.grd_n = e.grd * e.il;
-    e.gcrod = cross(e.grd_n, e.gro);
-    const float power = -0.5f * dot(e.gcrod, e.gcrod);
-    e.vis = __expf(power);
-    e.alpha = fminf(kMaxAlpha, gs.op * e.vis);
+    e.inv_dd = fminf(__builtin_amdgcn_rcpf(dot(e.grd, e.grd)), 3.40282347e38f);
+    e.c = cross(e.grd, e.gro);
+    e.vis = __builtin_amdgcn_exp2f(dot(e.c, e.c) * (e.inv_dd * -0.72134752f));
+    e.araw = gs.op * e.vis;
+    e.alpha = fminf(kMaxAlpha, e.araw);
     e.valid = in_range && e.alpha >= 1.f / 255.f;
     return e;
 }
 
-// Gradient contribution of one pair, added to acc (eval3d_bwd.cu:206-271). A pair that is not
-// valid adds exact zeros (its fac and gated upstream gradients are selected to 0, and every
-// gradient is linear in them) and leaves the pixel's transmittance and buffers unchanged.
+// acc[k] = v for the lane's first pixel, += v for the second (no addition to a zero start)
+template <bool FIRST>
+XSG_DEV void put(float& a, float v) {
+    if constexpr (FIRST) a = v;
+    else a += v;
+}
+
+// Gradient contribution of one pair into acc (eval3d_bwd.cu:206-271). A pair that is not valid
+// adds exact zeros (its fac and gated upstream gradients are selected to 0, and every gradient is
+// linear in them) and leaves the pixel's transmittance and buffer unchanged.
 //
-// The reference's chain from dL/dalpha through gcrod = n x gro (n = grd / |grd|) and
-// safe_normalize_bwd collapses to one vector: with s = n . gro, w = gro - s n (= gcrod x n) and
-// A = 2 dL/d|gcrod|^2 = -vis * opac * dL/dalpha, it adds A w to dL/dgro and -A s / |grd| w to
-// dL/dgrd (expand (n x gro) x n, (n x gro) x gro and the projection in safe_normalize_bwd). The
-// colour terms of dL/dalpha use running sums: sum_k buffer_k v_k is kept per pixel instead of
-// the buffer.
-template <int CDIM, int CS, int K, bool DYN, bool RG>
+// The reference's dL/dalpha sums, per channel, rgb T - buffer / (1 - alpha) and the depth and
+// alpha terms; here one running buffer carries all of them, so dL/dalpha = T u - buf / (1 - alpha)
+// with u = rgb . v_rgb + hit_t v_depth. Its chain through gcrod = n x gro, n = grd / |grd|, and
+// safe_normalize_bwd collapses to one vector w = (grd x gro) x grd (= |grd|^2 (gcrod x n)):
+// with A = -op vis dL/dalpha / |grd|^2 it adds A w to dL/dgro and -A (grd . gro) / |grd|^2 w to
+// dL/dgrd. The hit-distance terms are k1 = dL/dhit_t / |grd|^2 times -grd (gro) and
+// 2 (grd . gro) / |grd|^2 grd - gro (grd). Without per-pixel ray or time gradients the mean
+// gradient -M^T dL/dgro is applied once to the sum over the lane's two pixels (vg_sum).
+template <int CDIM, int CS, int K, bool DYN, bool RG, bool FIRST>
 XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, const float (&rgb)[CS],
-                      float (&acc)[K]) {
-    const float inv_dd = e.il * e.il;
+                      float (&acc)[K], f3& vg_sum) {
     const float od = dot(e.gro, e.grd);
-    const float last_hit_T = -od * inv_dd;
+    const float hit_t = -od * e.inv_dd;
     const float ra = __builtin_amdgcn_rcpf(fmaxf(1e-6f, 1.0f - e.alpha));
     px.T = e.valid ? px.T * ra : px.T;
     const float T = px.T;
     const float fac = e.valid ? e.alpha * T : 0.0f;
-    // grad_alpha (eval3d_bwd.cu:42-63) with rv = sum_k rgb_k v_k and buf_v = sum_k buffer_k v_k
     float rv = 0.0f;
 #pragma unroll
     for (int k = 0; k < CDIM; ++k) {
-        acc[k] += px.v_c[k] * fac;
-        rv += rgb[k] * px.v_c[k];
+        put<FIRST>(acc[k], px.v_c[k] * fac);
+        rv = (k == 0) ? rgb[0] * px.v_c[0] : fmaf(rgb[k], px.v_c[k], rv);
     }
-    float v_alpha = rv * T - px.buf_v * ra;
-    v_alpha += (last_hit_T * T - px.depth_buffer * ra) * px.v_d;
-    v_alpha += px.T_final * ra * px.v_a;
+    const float u = (CDIM > 0) ? fmaf(hit_t, px.v_d, rv) : hit_t * px.v_d;
+    const float v_alpha = T * u - ra * px.buf;
     // geometry and opacity only below the clamp (eval3d_bwd.cu:243)
-    const bool geo = e.valid && gs.op * e.vis <= kMaxAlpha;
+    const bool geo = e.valid && e.araw <= kMaxAlpha;
     const float v_alpha_g = geo ? v_alpha : 0.0f;
-    const float dL_dhitT = geo ? px.v_d * fac : 0.0f;
-
-    // hit-distance terms as the reference writes them (eval3d_bwd.cu:236-241)
-    f3 v_gro = e.grd * (-dL_dhitT * inv_dd);
-    f3 v_grd = (2.0f * od * e.grd - e.dd * e.gro) * (dL_dhitT * inv_dd * inv_dd);
-    // the alpha terms through gcrod, normalisation and M, collapsed (see above)
-    const float sn = e.il * od;               // n . gro
-    const f3 w = cross(e.gcrod, e.grd_n);     // gro - (n . gro) n, without its cancellation
-    const float A = -(e.vis * gs.op) * v_alpha_g;
-    v_gro = v_gro + A * w;
-    v_grd = v_grd + (-A * sn * e.il) * w;
-    const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
-    acc[CDIM + 0] -= v_omm.x;
-    acc[CDIM + 1] -= v_omm.y;
-    acc[CDIM + 2] -= v_omm.z;
+    const float k1 = geo ? px.v_d * fac * e.inv_dd : 0.0f;
+    const float Ap = -e.araw * v_alpha_g * e.inv_dd;
+    const f3 w = cross(e.c, e.grd);
+    const f3 v_gro = Ap * w - k1 * e.grd;
+    const float k2 = 2.0f * od * e.inv_dd * k1;
+    const float Bp = -Ap * od * e.inv_dd;
+    const f3 v_grd = k2 * e.grd - k1 * e.gro + Bp * w;
+    if constexpr (RG || DYN) {
+        const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
+        put<FIRST>(acc[CDIM + 0], -v_omm.x);
+        put<FIRST>(acc[CDIM + 1], -v_omm.y);
+        put<FIRST>(acc[CDIM + 2], -v_omm.z);
+        if constexpr (DYN) {
+            put<FIRST>(acc[CDIM + 13], -v_omm.x * px.rt);
+            put<FIRST>(acc[CDIM + 14], -v_omm.y * px.rt);
+            put<FIRST>(acc[CDIM + 15], -v_omm.z * px.rt);
+            px.v_t -= dot(v_omm, gs.vel);
+        }
+        if constexpr (RG) {
+            px.v_ro = px.v_ro + v_omm;
+            px.v_rd = px.v_rd + rows_tmul(gs.r0, gs.r1, gs.r2, v_grd);
+        }
+    } else {
+        vg_sum = FIRST ? v_gro : vg_sum + v_gro;
+    }
     // Q = v_grd (x) grd + v_gro (x) gro; dL/dM = Q S R^T, and the scale gradient -Q_ii / s_i is
     // the reference's per-pair product of the pair's own values
     const f3 gd = e.grd, go = e.gro;
-    acc[CDIM + 3] += v_grd.x * gd.x + v_gro.x * go.x;
-    acc[CDIM + 4] += v_grd.x * gd.y + v_gro.x * go.y;
-    acc[CDIM + 5] += v_grd.x * gd.z + v_gro.x * go.z;
-    acc[CDIM + 6] += v_grd.y * gd.x + v_gro.y * go.x;
-    acc[CDIM + 7] += v_grd.y * gd.y + v_gro.y * go.y;
-    acc[CDIM + 8] += v_grd.y * gd.z + v_gro.y * go.z;
-    acc[CDIM + 9] += v_grd.z * gd.x + v_gro.z * go.x;
-    acc[CDIM + 10] += v_grd.z * gd.y + v_gro.z * go.y;
-    acc[CDIM + 11] += v_grd.z * gd.z + v_gro.z * go.z;
-    acc[CDIM + 12] += e.vis * v_alpha_g;
-    if constexpr (DYN) {
-        acc[CDIM + 13] -= v_omm.x * px.rt;
-        acc[CDIM + 14] -= v_omm.y * px.rt;
-        acc[CDIM + 15] -= v_omm.z * px.rt;
-        px.v_t += -dot(v_omm, gs.vel);
-    }
-    if constexpr (RG) {
-        px.v_ro = px.v_ro + v_omm;
-        px.v_rd = px.v_rd + rows_tmul(gs.r0, gs.r1, gs.r2, v_grd);
-    }
-    px.buf_v += fac * rv;
-    px.depth_buffer += fac * last_hit_T;
+    put<FIRST>(acc[CDIM + 3], v_grd.x * gd.x + v_gro.x * go.x);
+    put<FIRST>(acc[CDIM + 4], v_grd.x * gd.y + v_gro.x * go.y);
+    put<FIRST>(acc[CDIM + 5], v_grd.x * gd.z + v_gro.x * go.z);
+    put<FIRST>(acc[CDIM + 6], v_grd.y * gd.x + v_gro.y * go.x);
+    put<FIRST>(acc[CDIM + 7], v_grd.y * gd.y + v_gro.y * go.y);
+    put<FIRST>(acc[CDIM + 8], v_grd.y * gd.z + v_gro.y * go.z);
+    put<FIRST>(acc[CDIM + 9], v_grd.z * gd.x + v_gro.z * go.x);
+    put<FIRST>(acc[CDIM + 10], v_grd.z * gd.y + v_gro.z * go.y);
+    put<FIRST>(acc[CDIM + 11], v_grd.z * gd.z + v_gro.z * go.z);
+    put<FIRST>(acc[CDIM + 12], e.vis * v_alpha_g);
+    px.buf = fmaf(fac, u, px.buf);
 }
 
 // Two pixels per thread: a workgroup of ceil(tile/2) threads (rounded up to whole wavefronts) per
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     constexpr int K = CDIM + 3 + 9 + 1 + (DYN ? 3 : 0);  // colours, mean, M, opacity, velocity
     __shared__ int32_t s_id[NT];
     __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | M (o - mu)
-    __shared__ float4 s_xo[NT];                      // o - mu (shared origin) or mu, and opacity
+    __shared__ float4 s_xo[NT];                      // mu and opacity
     __shared__ float4 s_vel[DYN ? NT : 1];
     __shared__ float s_col[CL > 0 ? NT * CL : 1];
     __shared__ float s_origin[3];
@@ -209,17 +215,15 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
         q.ro = q.inside ? ld3(p.ray_o + 3 * q.pix) : mk3(0.f, 0.f, 0.f);
         q.rt = 0.f;
         if constexpr (DYN) q.rt = q.inside ? p.rtd[q.pix] : 0.0f;
-        q.T_final = 1.0f - p.render_alpha[q.pix];
-        q.T = q.T_final;
+        const float T_final = 1.0f - p.render_alpha[q.pix];
+        q.T = T_final;
 #pragma unroll
         for (int k = 0; k < CS; ++k) q.v_c[k] = 0.f;
-        q.buf_v = 0.f;
 #pragma unroll
         for (int k = 0; k < CDIM; ++k) q.v_c[k] = q.inside ? p.v_rgb[q.pix * CDIM + k] : 0.0f;
         q.v_d = q.inside ? p.v_depth[q.pix] : 0.0f;
-        q.v_a = q.inside ? p.v_alpha[q.pix] : 0.0f;
+        q.buf = q.inside ? -T_final * p.v_alpha[q.pix] : 0.0f;
         q.bin_final = q.inside ? p.last_ids[q.pix] : 0;
-        q.depth_buffer = 0.f;
         q.v_t = 0.f;
         q.v_ro = mk3(0.f, 0.f, 0.f);
         q.v_rd = mk3(0.f, 0.f, 0.f);
@@ -295,16 +299,13 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
             const f3 sc = ld3(p.scales + 3 * gid);
             f3 r0, r1, r2;
             iscl_rot_rows(q, sc, r0, r1, r2);
-            f3 gro = mk3(0.f, 0.f, 0.f), xo = mu;
-            if (fixed) {
-                xo = o0 - mu;
-                gro = rows_mul(r0, r1, r2, xo);
-            }
+            f3 gro = mk3(0.f, 0.f, 0.f);
+            if (fixed) gro = rows_mul(r0, r1, r2, o0 - mu);
             s_m0[tr] = make_float4(r0.x, r0.y, r0.z, gro.x);
             s_m1[tr] = make_float4(r1.x, r1.y, r1.z, gro.y);
             s_m2[tr] = make_float4(r2.x, r2.y, r2.z, gro.z);
             const float op = p.opac[gid];
-            s_xo[tr] = make_float4(xo.x, xo.y, xo.z, op);
+            s_xo[tr] = make_float4(mu.x, mu.y, mu.z, op);
             f3 vel = mk3(0.f, 0.f, 0.f);
             if constexpr (DYN) {
                 vel = ld3(p.velocity + 3 * gid);
@@ -324,60 +325,73 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
             if (lane == 0) s_mask[k][wave] = m;
         }
         __syncthreads();
-        for (int w2 = 0; w2 < nwb; ++w2)
-        for (uint64_t m = uniform_u64(s_mask[wave][w2]); m != 0; m &= m - 1) {
-            const int t = (w2 << 6) + (int)__builtin_ctzll(m);
-            BwdGauss gs;
-            {
-                const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t], xo = s_xo[t];
-                gs.r0 = mk3(a.x, a.y, a.z);
-                gs.r1 = mk3(bq.x, bq.y, bq.z);
-                gs.r2 = mk3(cq.x, cq.y, cq.z);
-                gs.gro_fixed = mk3(a.w, bq.w, cq.w);
-                gs.xo = mk3(xo.x, xo.y, xo.z);
-                gs.op = xo.w;
-                gs.vel = mk3(0.f, 0.f, 0.f);
-                if constexpr (DYN) gs.vel = mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
-            }
-            const int32_t gidx = batch_end - t;
-            const BwdEval e0 = bwd_eval<DYN>(gs, px[0].ro, px[0].rd, px[0].rt, fixed,
-                                             px[0].inside && gidx <= px[0].bin_final);
-            const BwdEval e1 = bwd_eval<DYN>(gs, px[1].ro, px[1].rd, px[1].rt, fixed,
-                                             px[1].inside && gidx <= px[1].bin_final);
-            if (__ballot(e0.valid || e1.valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
+        // the pair loop, instantiated for both origin modes so that neither branches per pair
+        auto pairs = [&](auto fixed_c) {
+            constexpr bool FIXED = decltype(fixed_c)::value;
+            for (int w2 = 0; w2 < nwb; ++w2)
+            for (uint64_t m = uniform_u64(s_mask[wave][w2]); m != 0; m &= m - 1) {
+                const int t = (w2 << 6) + (int)__builtin_ctzll(m);
+                BwdGauss gs;
+                {
+                    const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t], xo = s_xo[t];
+                    gs.r0 = mk3(a.x, a.y, a.z);
+                    gs.r1 = mk3(bq.x, bq.y, bq.z);
+                    gs.r2 = mk3(cq.x, cq.y, cq.z);
+                    gs.gro_fixed = mk3(a.w, bq.w, cq.w);
+                    gs.mu = mk3(xo.x, xo.y, xo.z);
+                    gs.op = xo.w;
+                    gs.vel = mk3(0.f, 0.f, 0.f);
+                    if constexpr (DYN) gs.vel = mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
+                }
+                const int32_t gidx = batch_end - t;
+                const BwdEval e0 = bwd_eval<DYN, FIXED>(gs, px[0].ro, px[0].rd, px[0].rt,
+                                                        px[0].inside && gidx <= px[0].bin_final);
+                const BwdEval e1 = bwd_eval<DYN, FIXED>(gs, px[1].ro, px[1].rd, px[1].rt,
+                                                        px[1].inside && gidx <= px[1].bin_final);
+                if (__ballot(e0.valid || e1.valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
 
-            float rgb[CS];
+                float rgb[CS];
 #pragma unroll
-            for (int k = 0; k < CS; ++k) rgb[k] = 0.f;
-            if constexpr (CDIM > 0) {
-                if constexpr (CL > 0) {
+                for (int k = 0; k < CS; ++k) rgb[k] = 0.f;
+                if constexpr (CDIM > 0) {
+                    if constexpr (CL > 0) {
 #pragma unroll
-                    for (int k = 0; k < CDIM; ++k) rgb[k] = s_col[t * CL + k];
-                } else {
-                    const float* cp = p.colors + (int64_t)s_id[t] * CDIM;
+                        for (int k = 0; k < CDIM; ++k) rgb[k] = s_col[t * CL + k];
+                    } else {
+                        const float* cp = p.colors + (int64_t)s_id[t] * CDIM;
 #pragma unroll
-                    for (int k = 0; k < CDIM; ++k) rgb[k] = cp[k];
+                        for (int k = 0; k < CDIM; ++k) rgb[k] = cp[k];
+                    }
+                }
+                float acc[K];
+                f3 vg_sum;
+                bwd_pair<CDIM, CS, K, DYN, RG, true>(px[0], gs, e0, rgb, acc, vg_sum);
+                bwd_pair<CDIM, CS, K, DYN, RG, false>(px[1], gs, e1, rgb, acc, vg_sum);
+                if constexpr (!(RG || DYN)) {
+                    const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, vg_sum);
+                    acc[CDIM + 0] = -v_omm.x;
+                    acc[CDIM + 1] = -v_omm.y;
+                    acc[CDIM + 2] = -v_omm.z;
+                }
+
+                // wave totals by reduce-scatter: lane l ends with component 16 * chunk + (l >> 2);
+                // the first lane of each quad adds it, one atomic instruction per chunk of 16
+                // Gaussian index below 2^31 (flatten ids are int32): one 32 x 32 + 64-bit multiply-add
+                const uint32_t gid = (uint32_t)(__builtin_amdgcn_readfirstlane(s_id[t]) - (int64_t)cam * g.n);
+#pragma unroll
+                for (int ch = 0; ch < kChunks; ++ch) {
+                    float chunk[16];
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) chunk[k] = (16 * ch + k < K) ? acc[16 * ch + k] : 0.f;
+                    const float tot = wave_reduce_scatter16(chunk);
+                    if ((lane & 3) == 0 && 16 * ch + (lane >> 2) < K)
+                        unsafeAtomicAdd((float*)((char*)dst_base[ch] + (uint64_t)gid * (uint32_t)(4 * dst_stride[ch])),
+                                        tot);
                 }
             }
-            float acc[K];
-#pragma unroll
-            for (int k = 0; k < K; ++k) acc[k] = 0.f;
-            bwd_pair<CDIM, CS, K, DYN, RG>(px[0], gs, e0, rgb, acc);
-            bwd_pair<CDIM, CS, K, DYN, RG>(px[1], gs, e1, rgb, acc);
-
-            // wave totals by reduce-scatter: lane l ends with component 16 * chunk + (l >> 2); the
-            // first lane of each quad adds it, one atomic instruction per chunk of 16 components
-            const int64_t gid = s_id[t] - (int64_t)cam * g.n;
-#pragma unroll
-            for (int ch = 0; ch < kChunks; ++ch) {
-                float chunk[16];
-#pragma unroll
-                for (int k = 0; k < 16; ++k) chunk[k] = (16 * ch + k < K) ? acc[16 * ch + k] : 0.f;
-                const float tot = wave_reduce_scatter16(chunk);
-                if ((lane & 3) == 0 && 16 * ch + (lane >> 2) < K)
-                    unsafeAtomicAdd(dst_base[ch] + gid * dst_stride[ch], tot);
-            }
-        }
+        };
+        if (fixed) pairs(std::true_type{});
+        else pairs(std::false_type{});
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
