@@ -347,9 +347,9 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(
 // sort of its 64-bit keys. Entries of instances with a negative depth belong after every tile
 // (their sign-extended keys saturate the tile bits); they form the last row bucket and are written
 // in run order, which is depth order, then rows, then columns, as the reference orders them.
-constexpr int kRunSeg = 2048;         // runs per row segment
+constexpr int kRunSeg = 512;          // runs per row segment
 constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of seg_count_kernel)
-constexpr int kColGroup = 8;    // columns per wavefront in write_runs_kernel
+constexpr int kColGroup = 4;    // columns per wavefront in write_runs_kernel
 
 // the visible-span count from the packed grand total of the count scan, for device-sized kernels
 __global__ void visible_count_kernel(const uint64_t* __restrict__ packed_total, uint32_t* __restrict__ m_dev) {
@@ -607,58 +607,92 @@ XSG_DEV void write_neg_runs(const uint4* __restrict__ rec, int64_t b, int64_t n_
     }
 }
 
-// One wavefront per (segment, group of kColGroup columns). Per column, the runs covering it are
-// found by ballot and take consecutive positions from the column's slot, in run (depth) order.
-// Workgroup (s_max, 0) writes the negative-depth runs instead.
+// One workgroup per segment: its runs are read once into LDS, and each wavefront takes groups of
+// kColGroup columns in turn. Per column, the runs covering it are found by ballot and take
+// consecutive positions from the column's slot, in run (depth) order. They are staged in a
+// wavefront-private LDS buffer of 64 entries per column and stored 64 at a time, so that every
+// global store of a column is a full, contiguous wavefront (a column gets a few of each 64 runs).
+// Workgroup s_max writes the negative-depth runs instead.
 __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     int n_real, const uint4* __restrict__ rec, const uint32_t* __restrict__ row_start,
     const uint32_t* __restrict__ seg_base, const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ slots,
     const uint32_t* __restrict__ tile_base, int64_t s_max, int64_t n_runs, int ntx, int nty, int tnb, int n_groups,
     int64_t n_out, int64_t* __restrict__ out_keys, int32_t* __restrict__ out_ids) {
+    __shared__ uint4 s_rec[kRunSeg];
+    __shared__ uint32_t s_dep[kWaves][kColGroup][64];  // staged depth bits (low key word)
+    __shared__ int32_t s_gid[kWaves][kColGroup][64];   // staged Gaussian ids
+    extern __shared__ uint32_t s_first[];              // [ntx]: first output position per column
     const int64_t sg = blockIdx.x;
     if (sg == s_max) {
-        if (blockIdx.y == 0)
-            write_neg_runs(rec, row_start[n_real], n_runs, tile_base[(int64_t)n_real * ntx], n_out, out_keys, out_ids);
+        write_neg_runs(rec, row_start[n_real], n_runs, tile_base[(int64_t)n_real * ntx], n_out, out_keys, out_ids);
         return;
     }
     if (sg >= (int64_t)seg_base[n_real]) return;
-    const int lane = __lane_id();
-    const int cg = blockIdx.y * kWaves + (threadIdx.x >> 6);
-    if (cg >= n_groups) return;
+    const int lane = __lane_id(), wave = threadIdx.x >> 6;
     const uint32_t row = seg_row[sg];
     const uint32_t sb = seg_base[row], nseg = seg_base[row + 1] - sb;
     const uint32_t k = (uint32_t)sg - sb;
     const int64_t b = (int64_t)row_start[row] + (int64_t)k * kRunSeg;
-    const int64_t e = min((int64_t)row_start[row + 1], b + kRunSeg);
+    const int n_seg = (int)(min((int64_t)row_start[row + 1], b + kRunSeg) - b);
+    for (int i = threadIdx.x; i < n_seg; i += kBlock) s_rec[i] = rec[b + i];
+    for (int c = threadIdx.x; c < ntx; c += kBlock)
+        s_first[c] = tile_base[(int64_t)row * ntx + c] + slots[(int64_t)sb * ntx + (int64_t)c * nseg + k];
+    __syncthreads();
     const uint32_t cid = row / (uint32_t)nty, y = row - cid * (uint32_t)nty;
-    const int c0 = cg * kColGroup;
-    const int nc = min(kColGroup, ntx - c0);
-    uint32_t base[kColGroup];
-#pragma unroll
-    for (int j = 0; j < kColGroup; ++j)
-        base[j] = j < nc ? tile_base[(int64_t)row * ntx + c0 + j] + slots[(int64_t)sb * ntx + (int64_t)(c0 + j) * nseg + k]
-                         : 0u;
     const uint32_t tile_row = (cid << tnb) | (y * (uint32_t)ntx);
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int64_t i0 = b; i0 < e; i0 += 64) {
-        const int64_t i = i0 + lane;
-        const bool valid = i < e;
-        const uint4 rr = valid ? rec[i] : make_uint4(0, 0, 0, 0);
-        const int x0 = (int)(rr.z & 0xffffu), x1 = (int)(rr.z >> 16);
+    for (int cg = wave; cg < n_groups; cg += kWaves) {
+        const int c0 = cg * kColGroup;
+        const int nc = min(kColGroup, ntx - c0);
+        // per column: global position of the next flushed entry and entries staged in LDS (< 64),
+        // both wave-uniform
+        uint32_t out[kColGroup], fill[kColGroup];
 #pragma unroll
         for (int j = 0; j < kColGroup; ++j) {
-            if (j >= nc) break;
-            const int c = c0 + j;
-            const bool cov = valid && x0 <= c && c < x1;
-            const uint64_t mk = __ballot(cov);
-            if (cov) {
-                const uint64_t pos = (uint64_t)base[j] + (uint64_t)__popcll(mk & lt);
-                if (pos < (uint64_t)n_out) {
-                    out_keys[pos] = make_key(tile_row + (uint32_t)c, rr.y);
-                    out_ids[pos] = (int32_t)rr.x;
+            out[j] = j < nc ? (uint32_t)__builtin_amdgcn_readfirstlane((int)s_first[c0 + j]) : 0u;
+            fill[j] = 0;
+        }
+        for (int i0 = 0; i0 < n_seg; i0 += 64) {
+            const int i = i0 + lane;
+            const uint4 rr = i < n_seg ? s_rec[i] : make_uint4(0, 0, 0, 0);  // width 0 past the end
+            const uint32_t x0 = rr.z & 0xffffu, w = (rr.z >> 16) - x0;
+            const uint32_t d0 = (uint32_t)c0 - x0;  // column offset in the run; covered iff below w
+#pragma unroll
+            for (int j = 0; j < kColGroup; ++j) {
+                if (j >= nc) break;
+                const bool cov = d0 + (uint32_t)j < w;
+                const uint64_t mk = __builtin_amdgcn_ballot_w64(cov);
+                const uint32_t cnt = (uint32_t)__popcll(mk);
+                const uint32_t slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)mk, fill[j]));
+                if (cov && slot < 64) {
+                    s_dep[wave][j][slot] = rr.y;
+                    s_gid[wave][j][slot] = (int32_t)rr.x;
+                }
+                const uint32_t f = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fill[j] + cnt));
+                if (f >= 64) {  // the column's buffer is full: store it, then stage the overflow
+                    const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
+                    if (pos < (uint64_t)n_out) {
+                        out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
+                        out_ids[pos] = s_gid[wave][j][lane];
+                    }
+                    out[j] = (uint32_t)__builtin_amdgcn_readfirstlane((int)(out[j] + 64));
+                    if (cov && slot >= 64) {
+                        s_dep[wave][j][slot - 64] = rr.y;
+                        s_gid[wave][j][slot - 64] = (int32_t)rr.x;
+                    }
+                    fill[j] = f - 64;
+                } else {
+                    fill[j] = f;
                 }
             }
-            base[j] += (uint32_t)__popcll(mk);
+        }
+#pragma unroll
+        for (int j = 0; j < kColGroup; ++j) {
+            const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
+            if (j < nc && (uint32_t)lane < fill[j] && pos < (uint64_t)n_out) {
+                out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
+                out_ids[pos] = s_gid[wave][j][lane];
+            }
         }
     }
 }
@@ -746,6 +780,10 @@ int geometry_of(const xsg_isect_desc* d, Geometry& g) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// The depth pre-order sorts the visible instances, usually a small part of the instances its grid
+// is sized for: 1024 keys per block spread them over four times as many workgroups.
+constexpr int kPresortItems = 4;
+
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
 struct CountWs {
     Rect* rects; uint32_t* vcnt; uint32_t* vkey; uint64_t* partials; uint64_t* cpart;
@@ -776,7 +814,8 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     w.alt_key = (uint32_t*)(p + off); off += align256(4 * ns);
     w.alt_id = (uint32_t*)(p + off); off += align256(4 * ns);
     w.roff = (uint32_t*)(p + off); off += align256(4 * ns);
-    w.hist = (uint32_t*)(p + off); off += align256(g.sort ? 4 * (size_t)kRadix * w.nb : 0);
+    w.hist = (uint32_t*)(p + off);
+    off += align256(g.sort ? 4 * (size_t)kRadix * sort_blocks<kPresortItems>(nv > 0 ? nv : 1) : 0);
     w.dtot = (uint32_t*)(p + off); off += align256(4 * kRadix);
     w.rpart = (uint32_t*)(p + off); off += align256(4 * ((size_t)w.nb + 1));
     w.m_dev = (uint32_t*)(p + off); off += align256(4);
@@ -885,7 +924,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         // queued ahead of the readback, sized on the device: the visible spans in depth order
         // (stable, 4 passes, result back in comp_*), then their row-run offsets
         visible_count_kernel<<<1, 64, 0, s>>>(w.partials + w.nb, w.m_dev);
-        radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>>(
+        radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems>(
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev);
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
@@ -974,10 +1013,10 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots);
     // the writers (one extra workgroup for the negative-depth runs)
     const int n_groups = (g.ntx + kColGroup - 1) / kColGroup;
-    const dim3 grid_w((unsigned)fw.s_max + 1, (unsigned)((n_groups + kWaves - 1) / kWaves));
-    write_runs_kernel<<<grid_w, kBlock, 0, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, fw.slots,
-                                                fw.tile_tot, fw.s_max, n_runs, g.ntx, g.nty, g.tnb, n_groups,
-                                                n_isects, isect_ids, flatten_ids);
+    write_runs_kernel<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base,
+                                                                fw.seg_row, fw.slots, fw.tile_tot, fw.s_max, n_runs,
+                                                                g.ntx, g.nty, g.tnb, n_groups, n_isects, isect_ids,
+                                                                flatten_ids);
     XSG_TRY_LAUNCH("isect_fill");
     return XSG_OK;
 }

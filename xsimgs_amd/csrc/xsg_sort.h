@@ -16,7 +16,10 @@ constexpr int kSortTile = kSortBlock * kSortItems;  // keys per block and pass
 constexpr int kRadix = 256;
 constexpr int kWaves = kSortBlock / 64;
 
-inline unsigned sort_blocks(int64_t n) { return (unsigned)((n + kSortTile - 1) / kSortTile); }
+template <int ITEMS = kSortItems>
+inline unsigned sort_blocks(int64_t n) {
+    return (unsigned)((n + kSortBlock * ITEMS - 1) / (kSortBlock * ITEMS));
+}
 
 template <typename T>
 XSG_DEV T wave_inclusive_scan(T v) {
@@ -61,8 +64,9 @@ XSG_DEV uint32_t digit_of(K key, int shift, int bits) {
     return (uint32_t)((key >> shift) & (K)((1u << bits) - 1u));
 }
 
-// n_dev (optional): the element count read on the device, at most n; the grid covers n.
-template <typename K>
+// n_dev (optional): the element count read on the device, at most n; the grid covers n. A block
+// covers kSortBlock * ITEMS keys.
+template <typename K, int ITEMS = kSortItems>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict__ keys, int64_t n, int shift,
                                                             int bits, uint32_t* __restrict__ hist, unsigned nb,
                                                             const uint32_t* __restrict__ n_dev) {
@@ -72,9 +76,9 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict_
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) cnt[w][t] = 0;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
+    const int64_t base = (int64_t)blockIdx.x * (kSortBlock * ITEMS);
 #pragma unroll 4
-    for (int k = 0; k < kSortItems; ++k) {
+    for (int k = 0; k < ITEMS; ++k) {
         const int64_t idx = base + (int64_t)k * kSortBlock + t;
         if (idx < n) atomicAdd(&cnt[wave][digit_of<K>(keys[idx], shift, bits)], 1u);
     }
@@ -110,13 +114,13 @@ struct PlainOut {
     XSG_DEV void put(int64_t pos, K k, V v) const { keys[pos] = k; vals[pos] = v; }
 };
 
-// Downsweep of one pass. Each wavefront ranks its own contiguous 1024-key segment of the block's
-// tile in 16 steps of 64 keys: equal digits inside a step are found with 64-bit ballots over the
+// Downsweep of one pass. Each wavefront ranks its own contiguous segment (ITEMS * 64 keys) of the
+// block's tile in ITEMS steps of 64 keys: equal digits inside a step are found with 64-bit ballots over the
 // digit bits, and a wave-private counter per digit (in LDS, no block barrier) carries the rank
 // across steps. The block then combines the four waves' counts, reorders its keys by digit in
 // LDS and writes them out so that consecutive lanes store consecutive addresses of a digit's run.
 // Segments, steps and lanes are visited in input order, so the pass is stable.
-template <typename K, typename V, typename Out>
+template <typename K, typename V, typename Out, int ITEMS = kSortItems>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restrict__ keys_in,
                                                               const V* __restrict__ vals_in, int64_t n,
                                                               int shift, int bits,
@@ -125,17 +129,18 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
                                                               unsigned nb, Out out,
                                                               const uint32_t* __restrict__ n_dev) {
     if (n_dev) n = min(n, (int64_t)*n_dev);
-    constexpr int kSeg = kSortTile / kWaves;  // keys per wave
+    constexpr int kTile = kSortBlock * ITEMS;
+    constexpr int kSeg = kTile / kWaves;  // keys per wave
     constexpr int kSteps = kSeg / 64;
     __shared__ uint32_t wcnt[kWaves][kRadix];
     __shared__ uint32_t gbase[kRadix];
     __shared__ uint32_t lpre[kRadix];
     __shared__ uint32_t scan_lds[kWaves];
-    __shared__ K skeys[kSortTile];
-    __shared__ V svals[kSortTile];
+    __shared__ K skeys[kTile];
+    __shared__ V svals[kTile];
     const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
-    const int64_t tile0 = (int64_t)blockIdx.x * kSortTile;
-    const int n_tile = (int)min<int64_t>(kSortTile, n - tile0);
+    const int64_t tile0 = (int64_t)blockIdx.x * kTile;
+    const int n_tile = (int)min<int64_t>(kTile, n - tile0);
     {
         uint32_t tot;
         const uint32_t dprefix = block_exclusive_scan<uint32_t>(digit_total[t], scan_lds, tot);
@@ -200,25 +205,26 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
 
 // Runs every pass of a stable LSD sort over bits [begin_bit, end_bit) (8-bit digits, last one
 // narrower) ping-ponging between (k0, v0) and (k1, v1); the last pass goes through `final_out`.
-// Returns the number of passes. hist must hold kRadix * sort_blocks(n) words, dtot kRadix words.
-// With n_dev, the device-side count (at most n) is sorted; n only sizes the grid.
-template <typename K, typename V, typename FinalOut>
+// Returns the number of passes. hist must hold kRadix * sort_blocks<ITEMS>(n) words, dtot kRadix
+// words. With n_dev, the device-side count (at most n) is sorted; n only sizes the grid, so a sort
+// whose count is usually far below n uses fewer ITEMS per block to spread over more blocks.
+template <typename K, typename V, typename FinalOut, int ITEMS = kSortItems>
 inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
                              uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s,
                              const uint32_t* n_dev = nullptr) {
-    const unsigned nb = sort_blocks(n);
+    const unsigned nb = sort_blocks<ITEMS>(n);
     int passes = 0;
     K* src_k = k0; V* src_v = v0; K* dst_k = k1; V* dst_v = v1;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
         const int bits = min(8, end_bit - shift);
         const bool last = shift + 8 >= end_bit;
-        radix_upsweep<K><<<nb, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
+        radix_upsweep<K, ITEMS><<<nb, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
         radix_scan_hist<<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot);
         if (last) {
-            radix_downsweep<K, V, FinalOut><<<nb, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits, hist,
-                                                                      dtot, nb, final_out, n_dev);
+            radix_downsweep<K, V, FinalOut, ITEMS><<<nb, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits,
+                                                                             hist, dtot, nb, final_out, n_dev);
         } else {
-            radix_downsweep<K, V, PlainOut<K, V>><<<nb, kSortBlock, 0, s>>>(
+            radix_downsweep<K, V, PlainOut<K, V>, ITEMS><<<nb, kSortBlock, 0, s>>>(
                 src_k, src_v, n, shift, bits, hist, dtot, nb, PlainOut<K, V>{dst_k, dst_v}, n_dev);
         }
         ++passes;
