@@ -41,15 +41,18 @@ def parse():
     return p.parse_args()
 
 
-# Algorithmic VALU work of the compositor per (pixel, Gaussian) pair, counted from the kernels'
-# arithmetic (add, mul, fma, compare, exp, rcp and rsqrt each one op; every pair with a fixed tile
-# origin): alpha evaluation 43 (M rd 15, normalise 9, cross 9, squared norm 5, power / exp /
-# opacity / clamp / threshold 5); forward composite 24 more per contributing pair (hit distance 12,
-# transmittance and test 4, depth 2, 2 per colour channel); backward 170 more per contributing pair
-# at 3 colour channels without ray gradients (the eval3d_bwd.cu:172-271 chain).
-FLOPS_EVAL = 43
-FLOPS_FWD_CONTRIB = 18          # + 2 per colour channel
-FLOPS_BWD_CONTRIB = 146         # + 8 per colour channel
+# FP32 work the compositor kernels execute per (pixel, Gaussian) pair, counted from their arithmetic
+# (fma two, add / mul / min / max / compare / exp / rcp one each; fixed tile origin): alpha evaluation
+# 42 for every evaluated pair (M rd 15, |grd|^2 5, capped reciprocal 2, grd x gro 9, its squared norm
+# 5, exponent scale 2, exp / opacity / clamp / threshold 4); forward composite 13 + 2 per colour
+# channel for every composited pair (hit distance 6, depth 2, transmittance and tests 5); backward
+# 98 + 4 per colour channel for every composited pair without ray gradients (hit distance, the
+# 1 / (1 - alpha) transmittance, dL/dalpha, the collapsed alpha and hit vectors 45, mean gradient
+# 9, M gradient 27, opacity and buffer 3). Evaluated and composited counts come from the kernels
+# themselves (pair_counts), so pairs skipped unevaluated by the culling are not counted.
+FLOPS_EVAL = 42
+FLOPS_FWD_CONTRIB = 13          # + 2 per colour channel
+FLOPS_BWD_CONTRIB = 98          # + 4 per colour channel
 FP32_VALU_PEAK_TFLOPS = 78.6    # non-packed FP32 (packed FP32 ops are disabled in this build)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "eval3d_bwd_cfg2_traffic.json")
 
@@ -168,8 +171,10 @@ def main():
                                                           pair_counts=pairs)
         fwd_evaluated, contributing = (int(x) for x in pairs.cpu())
         g_rgb, g_d, g_a = grads[0]
+        bpairs = torch.zeros(2, dtype=torch.int64, device=dev)
         bwd_out = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, alpha,
-                                          last, g_rgb, g_d, g_a)
+                                          last, g_rgb, g_d, g_a, False, pair_counts=bpairs)
+        bwd_evaluated, bwd_composited = (int(x) for x in bpairs.cpu())
         v_colors = bwd_out[4]
         n_isects = int(fl.numel())
         # loaded intersections of the compositor (per tile): forward up to the batch holding the
@@ -184,9 +189,9 @@ def main():
         bs = tsx * tsy
         fwd_batches = ((tile_max - starts + 2).clamp(min=1) + bs - 1) // bs
         fwd_loaded = int(torch.minimum(rng, fwd_batches * bs).sum())
-        # backward: every pixel evaluates its tile's list from the start up to its last_id
+        # the reference's backward evaluates every pair of a pixel's list up to its last_id
         tile_of = ((torch.arange(H, device=dev) // tsy)[:, None] * ntx + (torch.arange(W, device=dev) // tsx)[None, :])
-        bwd_evaluated = int((last.long() - starts[tile_of] + 1).clamp(min=0).sum())
+        bwd_listed = int((last.long() - starts[tile_of] + 1).clamp(min=0).sum())
         vis = int((tpg > 0).sum())
         key_bits = 32 + int(math.floor(math.log2(ntx * nty))) + 1
 
@@ -224,7 +229,7 @@ def main():
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     # ---------------------------------------------------------------- roofline of the dominant kernel
     flops = {"eval3d_fwd": FLOPS_EVAL * fwd_evaluated + (FLOPS_FWD_CONTRIB + 2 * cdim) * contributing,
-             "eval3d_bwd": FLOPS_EVAL * bwd_evaluated + (FLOPS_BWD_CONTRIB + 8 * cdim) * contributing}
+             "eval3d_bwd": FLOPS_EVAL * bwd_evaluated + (FLOPS_BWD_CONTRIB + 4 * cdim) * bwd_composited}
     dom = max(live_ms, key=live_ms.get)
     t_dom = live_ms[dom]
     alg = stages[dom][1]
@@ -244,7 +249,8 @@ def main():
         roofline["traffic"] = int(tr["fetch_kib_per_dispatch"] * 1024 * tr["fetch_scale"] +
                                   tr["write_kib_per_dispatch"] * 1024 * tr["write_scale"])
         roofline["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
-    pair_stats = {"fwd_evaluated": fwd_evaluated, "bwd_evaluated": bwd_evaluated, "contributing": contributing}
+    pair_stats = {"fwd_evaluated": fwd_evaluated, "bwd_evaluated": bwd_evaluated, "contributing": contributing,
+                  "bwd_composited": bwd_composited, "bwd_listed_up_to_last_id": bwd_listed}
 
     # ---------------------------------------------------------------- CPU baseline (oracle, same frame)
     cpu = None

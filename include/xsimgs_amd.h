@@ -207,8 +207,10 @@ typedef struct {
     float* v_ray_d;
     float* v_velocity;             /* dynamic only */
     float* v_time_delta;           /* dynamic only */
-    /* forward, optional (NULL: not counted): pair_counts[0] += (pixel, Gaussian) pairs whose alpha
-     * was evaluated, pair_counts[1] += pairs that were composited; the caller initialises them */
+    /* optional (NULL: not counted): pair_counts[0] += (pixel, Gaussian) pairs whose alpha was
+     * evaluated (backward: pairs at or before the pixel's last id), pair_counts[1] += pairs that were
+     * composited; the caller initialises them. Pairs that no pixel of a wavefront can take are
+     * skipped unevaluated and not counted. */
     uint64_t* pair_counts;
 } xsg_eval3d_args;
 

@@ -278,6 +278,8 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
         }
     }
     __syncthreads();
+    const bool counting = p.pair_counts != nullptr;
+    uint64_t n_eval = 0, n_contrib = 0;  // evaluated / composited pixel-pairs of the wave, when counting
     const int32_t eff_end = min(range_end - 1, s_max);
     const int32_t n_eff = eff_end - range_start + 1;
     const int num_batches = n_eff > 0 ? (n_eff + nthr - 1) / nthr : 0;
@@ -348,6 +350,12 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
                                                         px[0].inside && gidx <= px[0].bin_final);
                 const BwdEval e1 = bwd_eval<DYN, FIXED>(gs, px[1].ro, px[1].rd, px[1].rt,
                                                         px[1].inside && gidx <= px[1].bin_final);
+                if (counting) {  // wave totals, scalar
+                    n_eval += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[0].inside && gidx <= px[0].bin_final)) +
+                              (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[1].inside && gidx <= px[1].bin_final));
+                    n_contrib += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e0.valid)) +
+                                 (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e1.valid));
+                }
                 if (__ballot(e0.valid || e1.valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
 
                 float rgb[CS];
@@ -392,6 +400,10 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
         };
         if (fixed) pairs(std::true_type{});
         else pairs(std::false_type{});
+    }
+    if (counting && lane == 0) {  // one atomic per wave and counter
+        atomicAdd(p.pair_counts, (unsigned long long)n_eval);
+        atomicAdd(p.pair_counts + 1, (unsigned long long)n_contrib);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {

@@ -171,6 +171,7 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
     p.v_alpha = a->v_alpha; p.v_means = a->v_means; p.v_opac = a->v_opacities; p.v_colors = a->v_colors;
     p.v_ray_o = a->v_ray_o; p.v_ray_d = a->v_ray_d; p.v_velocity = a->v_velocity; p.v_time = a->v_time_delta;
     p.v_mt = (float*)workspace;
+    p.pair_counts = (unsigned long long*)a->pair_counts;
     const int64_t n = a->n;
     const int64_t ncol = a->cdim > 0 ? (int64_t)a->n_cams * n * a->cdim : 0;
     const int64_t total = 3 * n + n + ncol + 9 * n + (dyn ? 3 * n : 0);

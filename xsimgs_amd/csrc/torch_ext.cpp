@@ -76,6 +76,15 @@ xsg_eval3d_args base_args(const Tensor& means, const Tensor& quats, const Tensor
     return a;
 }
 
+// optional int64[2] device tensor of evaluated / composited pair counts (an extension of this build)
+uint64_t* counts_ptr(const OptT& pair_counts, const Tensor& like) {
+    if (!pair_counts.has_value()) return nullptr;
+    TORCH_CHECK(pair_counts->scalar_type() == at::kLong && pair_counts->numel() >= 2 && pair_counts->is_contiguous() &&
+                    pair_counts->device() == like.device(),
+                "pair_counts must be a contiguous int64 tensor of 2 elements on the Gaussians' device");
+    return reinterpret_cast<uint64_t*>(pair_counts->data_ptr<int64_t>());
+}
+
 // rasterize_eval3d_fwd (eval3d_fwd.cu:248-316) and its dynamic twin (eval3d_dynamic_fwd.cu:249-332)
 std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
@@ -98,12 +107,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     a.ray_time_delta = fptr(ray_time_delta);
     a.out_rgb = renders.data_ptr<float>(); a.out_depth = depths.data_ptr<float>();
     a.out_alpha = alphas.data_ptr<float>(); a.out_last_ids = last_ids.data_ptr<int32_t>();
-    if (pair_counts.has_value()) {
-        TORCH_CHECK(pair_counts->scalar_type() == at::kLong && pair_counts->numel() >= 2 &&
-                        pair_counts->is_contiguous() && pair_counts->device() == means.device(),
-                    "pair_counts must be a contiguous int64 tensor of 2 elements on the Gaussians' device");
-        a.pair_counts = reinterpret_cast<uint64_t*>(pair_counts->data_ptr<int64_t>());
-    }
+    a.pair_counts = counts_ptr(pair_counts, means);
     check_rc(xsg_eval3d_fwd(&a, stream_of(means)));
     return {renders, depths, alphas, last_ids};
 }
@@ -141,7 +145,8 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
                        const Tensor& ray_directions, const OptT& ray_time_delta, int64_t tile_size_x,
                        int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
                        const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors,
-                       const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads) {
+                       const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
+                       const OptT& pair_counts) {
     if (v_render_colors.has_value() && !v_render_colors->is_contiguous())
         throw std::runtime_error("v_render_colors must be contiguous");
     all_contiguous({v_render_depth, v_render_alpha, render_alpha, last_ids});
@@ -189,6 +194,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     a.v_colors = o.v_colors.has_value() ? o.v_colors->data_ptr<float>() : nullptr;
     a.v_ray_o = o.v_ray_o.has_value() ? o.v_ray_o->data_ptr<float>() : nullptr;
     a.v_ray_d = o.v_ray_d.has_value() ? o.v_ray_d->data_ptr<float>() : nullptr;
+    a.pair_counts = counts_ptr(pair_counts, points);
     Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(a.n, cdim));
     check_rc(xsg_eval3d_bwd(&a, ws.data_ptr(), stream_of(points)));
     return o;
@@ -198,10 +204,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT> rasterize_eval3d_bw
     const Tensor& points, const Tensor& scale, const Tensor& quat, const Tensor& opacity, const OptT& colors,
     const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
     const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
-    const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads) {
+    const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
+    const OptT& pair_counts) {
     BwdOut o = eval3d_bwd_impl(points, std::nullopt, scale, quat, opacity, colors, ray_origins, ray_directions,
                                std::nullopt, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
-                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads);
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts);
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d};
 }
 
@@ -210,10 +217,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, Tensor> ras
     const OptT& colors, const Tensor& ray_origins, const Tensor& ray_directions, const Tensor& ray_time_delta,
     int64_t tile_size_x, int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
     const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors, const Tensor& v_render_depth,
-    const Tensor& v_render_alpha, bool ray_grads) {
+    const Tensor& v_render_alpha, bool ray_grads, const OptT& pair_counts) {
     BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
                                ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
-                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads);
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts);
     return {o.v_points, o.v_velocity, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
             o.v_time_delta};
 }
@@ -661,7 +668,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"), py::arg("ray_directions"),
           py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
           py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
-          py::arg("v_render_alpha"), py::arg("ray_grads") = true);
+          py::arg("v_render_alpha"), py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
     m.def("rasterize_eval3d_dynamic_fwd", &rasterize_eval3d_dynamic_fwd, py::arg("means"), py::arg("velocity"),
           py::arg("quats"), py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"),
           py::arg("image_height"), py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"),
@@ -672,7 +679,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("ray_directions"), py::arg("ray_time_delta"), py::arg("tile_size_x"), py::arg("tile_size_y"),
           py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("render_alpha"), py::arg("last_ids"),
           py::arg("v_render_colors"), py::arg("v_render_depth"), py::arg("v_render_alpha"),
-          py::arg("ray_grads") = true);
+          py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
     m.def("eval3d_supported_ndims", &eval3d_supported_ndims);
 
     // color (csrc/color/sh_bind.cpp)

@@ -355,7 +355,7 @@ struct Eval3dParams {
     float* v_velocity;
     float* v_time;
     float* v_mt;         // workspace [n, 9]: Q = sum of v_grd (x) grd + v_gro (x) gro per Gaussian
-    unsigned long long* pair_counts;  // forward, optional: += [evaluated, contributing] pairs
+    unsigned long long* pair_counts;  // optional: += [evaluated, composited] pixel-pairs
 };
 
 int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
