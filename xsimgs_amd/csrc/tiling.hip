@@ -92,7 +92,12 @@ struct Geometry {
     int sort;           // the fill sorts (the count pass orders the spans by depth)
 };
 
-// Count pass over Gaussian instances. A block covers kSortTile virtual instances (kSortTile /
+// Blocks of the count-phase kernels (count, compaction, row-run offsets): 1024 virtual instances,
+// four per thread, so that a 1 M-Gaussian pass spreads over about a thousand workgroups.
+constexpr int kCountItems = 4;
+constexpr int kCountTile = kBlock * kCountItems;
+
+// Count pass over Gaussian instances. A block covers kCountTile virtual instances (kCountTile /
 // SPANS Gaussians); it writes tiles_per_gauss, the rectangle, count and depth bits of every
 // virtual instance, and the block's packed count sum.
 __global__ __launch_bounds__(kBlock) void count_regular_kernel(
@@ -102,8 +107,8 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
     uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
     __shared__ uint64_t lds[kWaves];
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
+    const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    for (int k = 0; k < kCountItems; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
         if (j < n_total) {
             const Rect r = regular_rect(means2d[j], radii[j], tsx, tsy, ntx, nty);
@@ -144,8 +149,8 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     const Camera cam = load_camera(pack, KIND);
     const bool is_static = camera_is_static(cam, vel != nullptr);
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
-    const int64_t base = (int64_t)blockIdx.x * (kSortTile / 2);
-    for (int k = 0; k < kSortItems / 2; ++k) {
+    const int64_t base = (int64_t)blockIdx.x * (kCountTile / 2);
+    for (int k = 0; k < kCountItems / 2; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
         if (j >= n) continue;
         const float2 r = radii[j];
@@ -244,8 +249,8 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
     uint32_t* __restrict__ comp_key) {
     __shared__ uint64_t lds[kWaves];
     uint64_t carry = partials[blockIdx.x];
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
+    const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= n_virtual) break;  // block-uniform
         const int64_t v = base + (int64_t)k * kBlock + threadIdx.x;
         const uint32_t c = v < n_virtual ? vcnt[v] : 0u;
@@ -364,8 +369,8 @@ __global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const ui
     __shared__ uint32_t lds[kWaves];
     m = min(m, (int64_t)*m_dev);
     uint32_t acc = 0;
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
+    const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    for (int k = 0; k < kCountItems; ++k) {
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
         if (p < m) {
             const Rect r = rects[ids[p]];
@@ -384,8 +389,8 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
     __shared__ uint32_t lds[kWaves];
     m = min(m, (int64_t)*m_dev);
     uint32_t carry = partials[blockIdx.x];
-    const int64_t base = (int64_t)blockIdx.x * kSortTile;
-    for (int k = 0; k < kSortItems; ++k) {
+    const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= m) break;
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
         uint32_t h = 0;
@@ -799,7 +804,7 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     CountWs w;
     w.n_virtual = g.n * g.n_cams * g.spans;
     const int64_t nv = w.n_virtual;
-    w.nb = sort_blocks(nv > 0 ? nv : 1);
+    w.nb = (unsigned)(((nv > 0 ? nv : 1) + kCountTile - 1) / kCountTile);
     char* p = (char*)base;
     size_t off = 0;
     w.rects = (Rect*)(p + off); off += align256(sizeof(Rect) * nv);
