@@ -454,21 +454,32 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
     }
 }
 
-// single block: row_start[r] = first sorted run of row bucket r (lower bound, r in [0, n_rows]),
-// then segments of kRunSeg runs per real row: seg_base = exclusive prefix of the segment counts
-// (total at seg_base[n_real]) and seg_row[s] = row of segment s
+// single block: row_start[r] = first sorted run of row bucket r (r in [0, n_rows]), then segments
+// of kRunSeg runs per real row: seg_base = exclusive prefix of the segment counts (total at
+// seg_base[n_real]) and seg_row[s] = row of segment s. When the row sort was a single pass,
+// `row_count` holds its digit totals -- the runs per row bucket -- and row_start is their exclusive
+// scan; otherwise it is a lower-bound search of the sorted row buckets.
 __global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __restrict__ rows, int64_t n_runs,
-                                                              int n_rows, uint32_t* __restrict__ row_start,
+                                                              int n_rows, const uint32_t* __restrict__ row_count,
+                                                              uint32_t* __restrict__ row_start,
                                                               uint32_t* __restrict__ seg_base,
                                                               uint32_t* __restrict__ seg_row) {
     __shared__ uint32_t lds[kWaves];
-    for (int r = threadIdx.x; r <= n_rows; r += kBlock) {
-        int64_t lo = 0, hi = n_runs;
-        while (lo < hi) {
-            const int64_t mid = (lo + hi) >> 1;
-            if (rows[mid] < (uint32_t)r) lo = mid + 1; else hi = mid;
+    if (row_count) {  // n_rows < kRadix == kBlock
+        const uint32_t c = (int)threadIdx.x < n_rows ? row_count[threadIdx.x] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_exclusive_scan<uint32_t>(c, lds, tot);
+        if ((int)threadIdx.x < n_rows) row_start[threadIdx.x] = ex;
+        if (threadIdx.x == 0) row_start[n_rows] = tot;
+    } else {
+        for (int r = threadIdx.x; r <= n_rows; r += kBlock) {
+            int64_t lo = 0, hi = n_runs;
+            while (lo < hi) {
+                const int64_t mid = (lo + hi) >> 1;
+                if (rows[mid] < (uint32_t)r) lo = mid + 1; else hi = mid;
+            }
+            row_start[r] = (uint32_t)lo;
         }
-        row_start[r] = (uint32_t)lo;
     }
     __syncthreads();
     const int n_real = n_rows - 1;
@@ -543,50 +554,63 @@ __global__ __launch_bounds__(kBlock) void seg_count_kernel(int n_real, const uin
 }
 
 // Per tile (real row, column): exclusive prefix of its segments' counts in place (the slots of a
-// tile are consecutive), and the tile's total into tile_tot.
+// tile are consecutive), and the tile's total into tile_tot. One wavefront per tile, lanes over the
+// tile's segments.
 __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restrict__ slots,
                                                              const uint32_t* __restrict__ seg_base, int n_real,
                                                              int ntx, uint32_t* __restrict__ tile_tot) {
-    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (t >= (int64_t)n_real * ntx) return;
+    const int64_t t = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
+    if (t >= (int64_t)n_real * ntx) return;  // wave-uniform
+    const int lane = __lane_id();
     const int row = (int)(t / ntx), c = (int)(t - (int64_t)row * ntx);
     const uint32_t sb = seg_base[row], nseg = seg_base[row + 1] - sb;
     uint32_t* sl = slots + (int64_t)sb * ntx + (int64_t)c * nseg;
-    uint32_t run = 0;
-    for (uint32_t k = 0; k < nseg; ++k) {
-        const uint32_t x = sl[k];
-        sl[k] = run;
-        run += x;
+    uint32_t carry = 0;
+    for (uint32_t k0 = 0; k0 < nseg; k0 += 64) {
+        const uint32_t k = k0 + (uint32_t)lane;
+        const uint32_t x = k < nseg ? sl[k] : 0u;
+        const uint32_t inc = wave_inclusive_scan(x);
+        if (k < nseg) sl[k] = carry + inc - x;
+        carry += (uint32_t)__shfl((int)inc, 63, 64);
     }
-    tile_tot[t] = run;
+    if (lane == 0) tile_tot[t] = carry;
 }
 
 // single block of 1024 threads: exclusive scan of tile_tot[0, n) in place (the first position of
-// every tile of the real rows), the total -- where the negative-depth entries start -- at tile_tot[n]
+// every tile of the real rows), the total -- where the negative-depth entries start -- at tile_tot[n].
+// Chunks of 1024 consecutive entries, one per thread (coalesced), eight chunks' loads in flight.
 constexpr int kScanThreads = 1024;
+constexpr int kScanChunks = 8;
 __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n) {
     __shared__ uint32_t lds[kScanThreads / 64];
-    const int64_t per = (n + kScanThreads - 1) / kScanThreads;
-    const int64_t i0 = (int64_t)threadIdx.x * per, i1 = min(n, i0 + per);
-    uint32_t sum = 0;
-    for (int64_t i = i0; i < i1; ++i) sum += a[i];
-    const uint32_t inc = wave_inclusive_scan(sum);
     const int wave = threadIdx.x >> 6;
-    if (__lane_id() == 63) lds[wave] = inc;
-    __syncthreads();
-    uint32_t before = 0, tot = 0;
-    for (int w = 0; w < kScanThreads / 64; ++w) {
-        const uint32_t x = lds[w];
-        if (w < wave) before += x;
-        tot += x;
+    uint32_t carry = 0;
+    for (int64_t s0 = 0; s0 < n; s0 += (int64_t)kScanThreads * kScanChunks) {
+        uint32_t x[kScanChunks];
+#pragma unroll
+        for (int j = 0; j < kScanChunks; ++j) {
+            const int64_t i = s0 + (int64_t)j * kScanThreads + threadIdx.x;
+            x[j] = i < n ? a[i] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kScanChunks; ++j) {
+            const int64_t i = s0 + (int64_t)j * kScanThreads + threadIdx.x;
+            const uint32_t inc = wave_inclusive_scan(x[j]);
+            if (__lane_id() == 63) lds[wave] = inc;
+            __syncthreads();
+            uint32_t before = 0, tot = 0;
+#pragma unroll
+            for (int w = 0; w < kScanThreads / 64; ++w) {
+                const uint32_t y = lds[w];
+                if (w < wave) before += y;
+                tot += y;
+            }
+            __syncthreads();
+            if (i < n) a[i] = carry + before + inc - x[j];
+            carry += tot;
+        }
     }
-    uint32_t run = before + inc - sum;
-    for (int64_t i = i0; i < i1; ++i) {
-        const uint32_t x = a[i];
-        a[i] = run;
-        run += x;
-    }
-    if (threadIdx.x == 0) a[n] = tot;
+    if (threadIdx.x == 0) a[n] = carry;
 }
 
 // Runs of negative-depth instances, after every tile, in run order; each run's entries consecutive
@@ -788,6 +812,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // The depth pre-order sorts the visible instances, usually a small part of the instances its grid
 // is sized for: 1024 keys per block spread them over four times as many workgroups.
 constexpr int kPresortItems = 4;
+constexpr int kRunSortItems = 4;  // the run sort (one pass over about a million runs) likewise
 
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
 struct CountWs {
@@ -847,7 +872,7 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     w.n_rows = g.n_cams * g.nty + 1;
     w.s_max = n_runs / kRunSeg + w.n_rows;
     w.n_slots = w.s_max * g.ntx;
-    const unsigned nb_r = sort_blocks(n_runs > 0 ? n_runs : 1);
+    const unsigned nb_r = sort_blocks<kRunSortItems>(n_runs > 0 ? n_runs : 1);
     auto take = [&](size_t bytes) { void* q = p + off; off += align256(bytes); return q; };
     w.row_a = (uint32_t*)take(4 * n_runs);
     w.p_a = (uint32_t*)take(4 * n_runs);
@@ -1004,17 +1029,18 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     // buffer pair the last pass does not read) and the run records
     const bool odd = ((row_bits + 7) / 8) % 2 == 1;
     uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
-    radix_sort_passes<uint32_t, uint32_t, RunRecOut>(
+    radix_sort_passes<uint32_t, uint32_t, RunRecOut, kRunSortItems>(
         fw.row_a, fw.p_a, fw.row_b, fw.p_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
         RunRecOut{rows_sorted, fw.rec, cw.comp_id, cw.comp_key, cw.rects, g.spans}, s);
-    row_segments_kernel<<<1, kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows, fw.row_start, fw.seg_base, fw.seg_row);
+    row_segments_kernel<<<1, kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows, row_bits <= 8 ? fw.dtot : nullptr,
+                                             fw.row_start, fw.seg_base, fw.seg_row);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals
     seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
         n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
     const int64_t n_tile_slots = (int64_t)n_real * g.ntx;
-    tile_prefix_kernel<<<xsg_blocks(n_tile_slots, kBlock), kBlock, 0, s>>>(fw.slots, fw.seg_base, n_real, g.ntx,
-                                                                          fw.tile_tot);
+    tile_prefix_kernel<<<xsg_blocks(n_tile_slots * 64, kBlock), kBlock, 0, s>>>(fw.slots, fw.seg_base, n_real,
+                                                                               g.ntx, fw.tile_tot);
     tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots);
     // the writers (one extra workgroup for the negative-depth runs)
     const int n_groups = (g.ntx + kColGroup - 1) / kColGroup;
