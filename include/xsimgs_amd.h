@@ -14,6 +14,8 @@
  *   xsg_project_points        <Camera>.projection[_nojac]       bind.h:66-81, projection_kernels.h:259-309
  *   xsg_camera_rays           <Camera>.camera_rays (forward)    bind.h:47-53, ray_kernels.h:7-59
  *   xsg_pixel_time*           <Camera>.pixel_time*              bind.h:54-65, time_kernels.h:5-241
+ *   xsg_camera_rays_bwd       camera_ray_backward               ray_kernels.h:61-161
+ *   xsg_pixel_time_bwd        pixel_time*_backward              time_kernels.h:123-330
  *   xsg_sh_fwd / xsg_sh_bwd   spherical_harmonics_fused_{fwd,bwd} csrc/color/sh_fwd.cu:248-259,
  *                             sh_bwd.cu:379-390
  *   xsg_mask_radii[_packed]   mask_radii / mask_radii_packed    csrc/tiling/mask_radii.cu:82-88
@@ -91,6 +93,24 @@ int xsg_camera_rays(int kind, const float* pack, int width, int height, int worl
 /* per-pixel (uv == NULL) or per-uv capture time; `delta` subtracts the pose time */
 int xsg_pixel_time(int kind, const float* pack, int width, int height, const float* uv, int64_t n_uv,
                    int delta, float* out, xsg_stream_t stream);
+
+/* Gradient of sum(d_ray_o * ray_o + d_ray_d * ray_d) w.r.t. the camera pack (camera_ray_backward,
+ * ray_kernels.h:61-161). grad_pack gets all xsg_camera_pack_elements(kind) values in pack order
+ * (q0, t0, v, w, rolling_time, trigger_time, pose_time, intrinsics; 0 for the lidar beam address);
+ * it needs no zero-initialisation. d_ray_o may be NULL (no origin gradient). The sum over pixels
+ * is deterministic: per-block partials in `workspace`, then one fixed-order reduction. */
+size_t xsg_camera_rays_bwd_workspace_bytes(int width, int height);
+int xsg_camera_rays_bwd(int kind, const float* pack, int width, int height, int world_space,
+                        int normalized, const float* d_ray_o, const float* d_ray_d, float* grad_pack,
+                        void* workspace, xsg_stream_t stream);
+
+/* Gradient of sum(grad * time) for xsg_pixel_time's output w.r.t. the pack (rolling_time,
+ * trigger_time and, with `delta`, pose_time; every other element 0) and, when uv is given and
+ * d_uv is not NULL, w.r.t. uv (d_uv[i] = grad[i] * rolling_time). time_kernels.h:123-330. */
+size_t xsg_pixel_time_bwd_workspace_bytes(int64_t n);
+int xsg_pixel_time_bwd(int kind, const float* pack, int width, int height, const float* uv,
+                       int64_t n_uv, int delta, const float* grad, float* grad_pack, float* d_uv,
+                       void* workspace, xsg_stream_t stream);
 
 /* ------------------------------------------------------- spherical harmonics */
 int xsg_sh_fwd(int degree, const float* origin, int64_t n, int dim, const float* positions,

@@ -149,6 +149,56 @@ def camera_rays(spec, width, height, world_space=True, normalized=True, prec="f3
     return ro, rd
 
 
+CAMERA_GRAD_FIELDS = (("q", 4), ("t", 3), ("v", 3), ("w", 3), ("rolling", 2), ("trigger_time", 1),
+                      ("pose_time", 1), ("impl", 4))
+
+
+def camera_rays_bwd(spec, width, height, d_ray_o, d_ray_d, world_space=True, normalized=True, prec="f32"):
+    """camera_ray_backward_kernel_cuda (ray_kernels.h:61-161): the gradient of the rays w.r.t. the
+    camera, summed over pixels, as 21 values in ``CAMERA_GRAD_FIELDS`` order (``d_ray_o`` may be None)."""
+    _, nt = _real(prec)
+    cam = camera(spec, prec)
+    d_ray_o, d_ray_d = _arr(d_ray_o, nt), _arr(d_ray_d, nt)
+    out = np.zeros(21, nt)
+    _lib(prec).orc_camera_rays_bwd(C.byref(cam), C.c_int(width), C.c_int(height), C.c_int(int(world_space)),
+                                   C.c_int(int(normalized)), _p(d_ray_o), _p(d_ray_d), _p(out))
+    return out
+
+
+def pixel_uv(spec, width, height):
+    """Pixel centres' uv (base_camera_impl.h:9-14; lidar v from the beam table, spherical.h:77-82)."""
+    u = (np.arange(width, dtype=np.float64) + 0.5) / width
+    if spec.kind == "lidar":
+        v = np.asarray(spec.beam_v, np.float64)[:height]
+    else:
+        v = (np.arange(height, dtype=np.float64) + 0.5) / height
+    return np.stack(np.broadcast_arrays(u[None, :], v[:, None]), -1)
+
+
+def pixel_time(spec, width=None, height=None, uv=None, delta=False):
+    """pixel_time[_delta][_from_uv] forward (camera.h:89-99), float64."""
+    if uv is None:
+        uv = pixel_uv(spec, width, height)
+    uv = np.asarray(uv, np.float64)
+    t = spec.trigger_time + uv[..., 0] * spec.rolling[0] + uv[..., 1] * spec.rolling[1]
+    return t - spec.pose_time if delta else t
+
+
+def pixel_time_bwd(spec, grad, width=0, height=0, uv=None, delta=False, prec="f32"):
+    """pixel_time[_delta][_from_uv] backward (time_kernels.h:123-330): 21 camera values (as
+    ``camera_rays_bwd``) and, with ``uv``, the uv gradient."""
+    _, nt = _real(prec)
+    cam = camera(spec, prec)
+    grad = _arr(grad, nt)
+    uv = _arr(uv, nt)
+    out = np.zeros(21, nt)
+    d_uv = np.zeros_like(uv) if uv is not None else None
+    n = grad.size
+    _lib(prec).orc_pixel_time_bwd(C.byref(cam), C.c_int(width), C.c_int(height), _p(uv), C.c_long(n),
+                                  C.c_int(int(delta)), _p(grad), _p(out), _p(d_uv))
+    return (out, d_uv) if uv is not None else out
+
+
 def sh_fwd(degree, origin, positions, coeffs, dc=None, mask=None, layout_3kn=False, prec="f32"):
     """spherical_harmonics_fused_fwd (csrc/color/sh_fwd.cu:119-245)."""
     _, nt = _real(prec)

@@ -13,6 +13,9 @@
  *   orc_project_utgs_phm      seam flag cases built by hand; phm seam selection
  *                             end-to-end is "parity unpinned" beyond those cases
  *   orc_camera_rays           closed form pinhole / spherical / lidar rays
+ *   orc_camera_rays_bwd       fp64 central differences of orc_camera_rays w.r.t. every camera
+ *                             parameter (pinhole, spherical, lidar; world / camera space)
+ *   orc_pixel_time_bwd        closed form (pixel time is linear in the camera's timing)
  *   orc_sh_fwd / orc_sh_bwd   scipy.special.sph_harm basis, fp64 finite differences
  *   orc_isect_*               brute-force tile enumeration in Python, numpy stable sort
  *   orc_sort_pairs            numpy argsort(kind="stable")
@@ -416,6 +419,109 @@ void orc_camera_rays(const orc_camera *c, int width, int height, int world_space
         ray_o[3 * idx] = o.x; ray_o[3 * idx + 1] = o.y; ray_o[3 * idx + 2] = o.z;
         ray_d[3 * idx] = ray.x; ray_d[3 * idx + 1] = ray.y; ray_d[3 * idx + 2] = ray.z;
     }
+}
+
+/* Backward of orc_camera_rays w.r.t. the camera: camera_ray_backward_kernel_cuda
+ * (ray_kernels.h:61-161), restated for the pose model of orc_camera_rays. Gradients are summed
+ * over pixels (in double) into out[21] = q(4) t(3) v(3) w(3) rolling(2) trigger_time pose_time
+ * impl(4), the camera's tensor order (camera.h:144, perspective.cu:8, spherical.h:35). d_ray_o may
+ * be NULL. Only the pinhole model has an intrinsics gradient (perspective.cu:19-33); the spherical
+ * and lidar models inherit the empty one (base_camera_impl.h:19-22). */
+void orc_camera_rays_bwd(const orc_camera *c, int width, int height, int world_space, int normalized,
+                         const real *d_ray_o, const real *d_ray_d, real *out) {
+    double acc[21];
+    for (int k = 0; k < 21; ++k) acc[k] = 0.0;
+    for (int idx = 0; idx < width * height; ++idx) {
+        const int px = idx % width, py = idx / width;
+        const real u = ((real)px + K(0.5)) / (real)width;
+        const real v = (c->kind == ORC_LIDAR) ? c->beam_v[py] : ((real)py + K(0.5)) / (real)height;
+        const v3 r = pixel_to_camera_ray(c, u, v);
+        const v3 n = normalized ? normalize3(r) : r;
+        const v3 gd = ld3(d_ray_d + 3 * idx);
+        const v3 go = d_ray_o ? ld3(d_ray_o + 3 * idx) : V3(0, 0, 0);
+        v3 dn = gd;
+        if (world_space) {
+            const real dt = c->trigger_time + (u * c->rolling[0] + v * c->rolling[1]) - c->pose_time;
+            const v3 w = ld3(c->w);
+            real w1, dw1; v3 xyz1, dxyz1;
+            jac_quat_from_axis_angle(w, dt, &w1, &xyz1, &dw1, &dxyz1);
+            const real w2 = c->q[0];
+            const v3 xyz2 = V3(c->q[1], c->q[2], c->q[3]);
+            const real qw = w1 * w2 - dot3(xyz1, xyz2);
+            const v3 qv = add3(add3(scl3(xyz2, w1), scl3(xyz1, w2)), cross3(xyz1, xyz2));
+            /* ray_o = t0 + v dt */
+            real d_dt = dot3(go, ld3(c->v));
+            acc[4] += go.x; acc[5] += go.y; acc[6] += go.z;
+            acc[7] += dt * go.x; acc[8] += dt * go.y; acc[9] += dt * go.z;
+            /* ray_d = n + 2 (qw (qv x n) + qv x (qv x n)) */
+            dn = add3(gd, scl3(add3(scl3(cross3(qv, gd), -qw), cross3(qv, cross3(qv, gd))), K(2.0)));
+            const real d_qw = K(2.0) * dot3(gd, cross3(qv, n));
+            const v3 d_qv = add3(add3(scl3(cross3(n, gd), K(2.0) * qw), scl3(n, K(2.0) * dot3(gd, qv))),
+                                 sub3(scl3(gd, K(2.0) * dot3(qv, n)), scl3(qv, K(4.0) * dot3(gd, n))));
+            /* q = (w1, xyz1) (x) (w2, xyz2) */
+            const real d_w1 = d_qw * w2 + dot3(d_qv, xyz2);
+            const v3 d_xyz1 = add3(add3(scl3(xyz2, -d_qw), scl3(d_qv, w2)), cross3(xyz2, d_qv));
+            const real d_w2 = d_qw * w1 + dot3(d_qv, xyz1);
+            const v3 d_xyz2 = add3(add3(scl3(xyz1, -d_qw), scl3(d_qv, w1)), cross3(d_qv, xyz1));
+            acc[0] += d_w2; acc[1] += d_xyz2.x; acc[2] += d_xyz2.y; acc[3] += d_xyz2.z;
+            /* (w1, xyz1) = (cos(theta/2), w dt sigma), theta = |w| |dt|, sigma = sin(theta/2) / theta */
+            d_dt += d_w1 * dw1 + dot3(d_xyz1, dxyz1);
+            const real wn = SQRT(dot3(w, w));
+            const real theta = wn * FABS(dt);
+            real sigma, kappa;  /* kappa = dt |dt| sigma'(theta) / |w| */
+            if (theta < K(1e-2)) {
+                sigma = K(0.5) - theta * theta * (K(1.0) / K(48.0));
+                kappa = -dt * dt * dt / K(24.0);
+            } else {
+                const real sh = SIN(K(0.5) * theta), ch = COS(K(0.5) * theta);
+                sigma = sh / theta;
+                kappa = dt * FABS(dt) * (K(0.5) * theta * ch - sh) / (theta * theta * wn);
+            }
+            const v3 d_w = add3(add3(scl3(w, -d_w1 * dt * dt * sigma * K(0.5)), scl3(d_xyz1, dt * sigma)),
+                                scl3(w, kappa * dot3(d_xyz1, w)));
+            acc[10] += d_w.x; acc[11] += d_w.y; acc[12] += d_w.z;
+            /* dt = trigger_time + u rolling.x + v rolling.y - pose_time */
+            acc[13] += d_dt * u; acc[14] += d_dt * v;
+            acc[15] += d_dt; acc[16] -= d_dt;
+        }
+        v3 dr = dn;
+        if (normalized) {  /* normalize backward */
+            const real il = K(1.0) / SQRT(dot3(r, r));
+            dr = scl3(sub3(dn, scl3(n, dot3(n, dn))), il);
+        }
+        if (c->kind == ORC_PINHOLE) {  /* perspective.cu:19-33 */
+            const real ifx = K(1.0) / c->impl[0], ify = K(1.0) / c->impl[1];
+            acc[17] += -dr.x * (u - c->impl[2]) * ifx * ifx;
+            acc[18] += -dr.y * (v - c->impl[3]) * ify * ify;
+            acc[19] += -dr.x * ifx;
+            acc[20] += -dr.y * ify;
+        }
+    }
+    for (int k = 0; k < 21; ++k) out[k] = (real)acc[k];
+}
+
+/* pixel_time[_delta][_from_uv] backward (time_kernels.h:123-330): with uv NULL the n = width *
+ * height pixels' own uv. out[21] as orc_camera_rays_bwd: trigger_time += sum g, rolling += sum g uv,
+ * pose_time -= sum g for the delta variants; d_uv[i] = g_i rolling when uv is given. */
+void orc_pixel_time_bwd(const orc_camera *c, int width, int height, const real *uv, long n, int delta,
+                        const real *grad, real *out, real *d_uv) {
+    double g0 = 0.0, gu = 0.0, gv = 0.0;
+    if (!uv) n = (long)width * height;
+    for (long i = 0; i < n; ++i) {
+        real u, v;
+        if (uv) {
+            u = uv[2 * i]; v = uv[2 * i + 1];
+            if (d_uv) { d_uv[2 * i] = grad[i] * c->rolling[0]; d_uv[2 * i + 1] = grad[i] * c->rolling[1]; }
+        } else {
+            const int px = (int)(i % width), py = (int)(i / width);
+            u = ((real)px + K(0.5)) / (real)width;
+            v = (c->kind == ORC_LIDAR) ? c->beam_v[py] : ((real)py + K(0.5)) / (real)height;
+        }
+        g0 += grad[i]; gu += (double)grad[i] * u; gv += (double)grad[i] * v;
+    }
+    for (int k = 0; k < 21; ++k) out[k] = 0;
+    out[13] = (real)gu; out[14] = (real)gv; out[15] = (real)g0;
+    if (delta) out[16] = (real)-g0;
 }
 
 /* ------------------------------------------------------------------------- */

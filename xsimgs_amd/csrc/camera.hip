@@ -211,6 +211,151 @@ __global__ __launch_bounds__(kBlock) void pixel_time_kernel(
     out[idx] = t;
 }
 
+// --------------------------------------------------------------------------------------------
+// Camera gradients. Per thread the gradient w.r.t. the camera's 21 parameters (q0, t0, v, w,
+// rolling_time, trigger_time, pose_time, intrinsics: the camera's tensors in order, camera.h:144),
+// reduced per block into partials; grad_final_kernel sums the partials in a fixed order and writes
+// the whole pack gradient (the lidar beam address gets 0).
+constexpr int kCamGrad = 21;
+
+XSG_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+template <int NV>
+XSG_DEV void block_partials(const float (&g)[NV], float* __restrict__ part) {
+    __shared__ float s_w[kBlock / 64][NV];
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const float t = wave_sum(g[k]);
+        if (__lane_id() == 0) s_w[wave][k] = t;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < NV) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) t += s_w[w][threadIdx.x];
+        part[(int64_t)blockIdx.x * NV + threadIdx.x] = t;
+    }
+}
+
+// camera_ray_backward_kernel_cuda (ray_kernels.h:61-161) for this build's pose model: ray_o =
+// t0 + v dt, ray_d = q (x) n, q = (cos(theta/2), w dt sigma) (x) q0 with theta = |w| |dt| and
+// sigma = sin(theta/2) / theta (jac_quat_from_axis_angle), dt = pixel_time - pose_time.
+template <int KIND>
+__global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __restrict__ pack, int width,
+                                                                 int height, int world_space, int normalized,
+                                                                 const float* __restrict__ d_ray_o,
+                                                                 const float* __restrict__ d_ray_d,
+                                                                 float* __restrict__ part) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const Camera c = load_camera(pack, KIND);
+    float g[kCamGrad];
+#pragma unroll
+    for (int k = 0; k < kCamGrad; ++k) g[k] = 0.f;
+    if (idx < (int64_t)width * height) {  // every thread takes part in the reduction below
+        const f2 uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+        const f3 r = pixel_to_camera_ray<KIND>(c, uv);
+        const float il = 1.0f / sqrtf(dot(r, r));
+        const f3 n = normalized ? r * il : r;
+        const f3 gd = ld3(d_ray_d + 3 * idx);
+        const f3 go = d_ray_o ? ld3(d_ray_o + 3 * idx) : mk3(0.f, 0.f, 0.f);
+        f3 dn = gd;
+        if (world_space) {
+            const float dt = pixel_time(c, uv.x, uv.y) - c.pose_time;
+            float w1, dw1; f3 xyz1, dxyz1;
+            jac_quat_from_axis_angle(c.w, dt, w1, xyz1, dw1, dxyz1);
+            const float w2 = c.qw; const f3 xyz2 = c.qv;
+            const float qw = w1 * w2 - dot(xyz1, xyz2);
+            const f3 qv = w2 * xyz1 + w1 * xyz2 + cross(xyz1, xyz2);
+            float d_dt = dot(go, c.v);  // ray_o = t0 + v dt
+            g[4] = go.x; g[5] = go.y; g[6] = go.z;
+            g[7] = dt * go.x; g[8] = dt * go.y; g[9] = dt * go.z;
+            // ray_d = n + 2 (qw (qv x n) + qv x (qv x n))
+            dn = gd + 2.0f * (cross(qv, cross(qv, gd)) - qw * cross(qv, gd));
+            const float d_qw = 2.0f * dot(gd, cross(qv, n));
+            const f3 d_qv = (2.0f * qw) * cross(n, gd) + (2.0f * dot(gd, qv)) * n + (2.0f * dot(qv, n)) * gd -
+                            (4.0f * dot(gd, n)) * qv;
+            // q = (w1, xyz1) (x) (w2, xyz2)
+            const float d_w1 = d_qw * w2 + dot(d_qv, xyz2);
+            const f3 d_xyz1 = w2 * d_qv - d_qw * xyz2 + cross(xyz2, d_qv);
+            const float d_w2 = d_qw * w1 + dot(d_qv, xyz1);
+            const f3 d_xyz2 = w1 * d_qv - d_qw * xyz1 + cross(d_qv, xyz1);
+            g[0] = d_w2; g[1] = d_xyz2.x; g[2] = d_xyz2.y; g[3] = d_xyz2.z;
+            // (w1, xyz1) = (cos(theta/2), w dt sigma); kappa = dt |dt| sigma'(theta) / |w|
+            d_dt += d_w1 * dw1 + dot(d_xyz1, dxyz1);
+            const float wn = sqrtf(dot(c.w, c.w));
+            const float theta = wn * fabsf(dt);
+            float sigma, kappa;
+            if (theta < 1e-2f) {
+                sigma = 0.5f - theta * theta * (1.0f / 48.0f);
+                kappa = -dt * dt * dt * (1.0f / 24.0f);
+            } else {
+                float sh, ch;
+                sincosf(0.5f * theta, &sh, &ch);
+                sigma = sh / theta;
+                kappa = dt * fabsf(dt) * (0.5f * theta * ch - sh) / (theta * theta * wn);
+            }
+            const f3 d_w = (-d_w1 * dt * dt * sigma * 0.5f + kappa * dot(d_xyz1, c.w)) * c.w + (dt * sigma) * d_xyz1;
+            g[10] = d_w.x; g[11] = d_w.y; g[12] = d_w.z;
+            // dt = trigger_time + uv . rolling_time - pose_time
+            g[13] = d_dt * uv.x; g[14] = d_dt * uv.y; g[15] = d_dt; g[16] = -d_dt;
+        }
+        const f3 dr = normalized ? (dn - dot(n, dn) * n) * il : dn;
+        if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:19-33
+            const float ifx = 1.0f / c.i0, ify = 1.0f / c.i1;
+            g[17] = -dr.x * (uv.x - c.i2) * ifx * ifx;
+            g[18] = -dr.y * (uv.y - c.i3) * ify * ify;
+            g[19] = -dr.x * ifx;
+            g[20] = -dr.y * ify;
+        }  // the spherical and lidar models carry no intrinsics gradient (base_camera_impl.h:19-22)
+    }
+    block_partials<kCamGrad>(g, part);
+}
+
+// pixel_time[_delta][_from_uv]_bwd_kernel (time_kernels.h:123-330): partial sums of g u, g v and g;
+// with uv given, d_uv = g rolling_time
+template <int KIND>
+__global__ __launch_bounds__(kBlock) void pixel_time_bwd_kernel(const float* __restrict__ pack, int width,
+                                                                int height, const float2* __restrict__ uv_in,
+                                                                int64_t n, const float* __restrict__ grad,
+                                                                float2* __restrict__ d_uv, float* __restrict__ part) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const Camera c = load_camera(pack, KIND);
+    float g[3] = {0.f, 0.f, 0.f};
+    if (idx < n) {
+        f2 uv;
+        if (uv_in) {
+            uv = mk2(uv_in[idx].x, uv_in[idx].y);
+        } else {
+            uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+        }
+        const float gr = grad[idx];
+        if (d_uv) d_uv[idx] = make_float2(gr * c.roll_u, gr * c.roll_v);
+        g[0] = gr * uv.x; g[1] = gr * uv.y; g[2] = gr;
+    }
+    block_partials<3>(g, part);
+}
+
+// one workgroup: out[k] = sum over blocks of part[b][k] for the nv partial values, placed at the pack
+// positions: rays (nv = kCamGrad) at 0..20; times (nv = 3) at rolling_time, trigger_time and, for
+// the delta variants, -trigger at pose_time; every other pack element 0.
+__global__ __launch_bounds__(kBlock) void grad_final_kernel(const float* __restrict__ part, int nb, int nv, int delta,
+                                                            int pack_elems, float* __restrict__ out) {
+    const int wave = threadIdx.x >> 6, lane = __lane_id();
+    for (int e = wave; e < pack_elems; e += kBlock / 64) {
+        const int k = (nv == kCamGrad) ? e : (e == 13 ? 0 : e == 14 ? 1 : (e == 15 || (e == 16 && delta)) ? 2 : -1);
+        float t = 0.f;
+        if (k >= 0 && k < nv)
+            for (int b = lane; b < nb; b += 64) t += part[(int64_t)b * nv + k];
+        t = wave_sum(t);
+        if (lane == 0) out[e] = (nv != kCamGrad && delta && e == 16) ? -t : t;
+    }
+}
+
 UtWeights ut_weights(float a, float b, float k) {  // ut_kernels.h:17-36 (host, float32)
     const float lam = a * a * (3 + k) - 3;
     UtWeights w;
@@ -340,5 +485,76 @@ extern "C" int xsg_pixel_time(int kind, const float* pack, int width, int height
         default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
     }
     XSG_TRY_LAUNCH("pixel_time");
+    return XSG_OK;
+}
+
+extern "C" size_t xsg_camera_rays_bwd_workspace_bytes(int width, int height) {
+    const int64_t n = (int64_t)(width > 0 ? width : 0) * (height > 0 ? height : 0);
+    return sizeof(float) * (size_t)kCamGrad * xsg_blocks(n > 0 ? n : 1, kBlock);
+}
+
+extern "C" int xsg_camera_rays_bwd(int kind, const float* pack, int width, int height, int world_space,
+                                   int normalized, const float* d_ray_o, const float* d_ray_d, float* grad_pack,
+                                   void* workspace, xsg_stream_t stream) {
+    const int pe = xsg_camera_pack_elements(kind);
+    if (pe <= 0) return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
+    if (width < 0 || height < 0) return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: negative size");
+    if (!pack || !grad_pack || !workspace || (!d_ray_d && (int64_t)width * height > 0))
+        return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: null pointer");
+    const int64_t n = (int64_t)width * height;
+    const unsigned nb = xsg_blocks(n > 0 ? n : 1, kBlock);
+    float* part = (float*)workspace;
+    const hipStream_t s = (hipStream_t)stream;
+    switch (kind) {
+        case XSG_CAM_PINHOLE:
+            camera_rays_bwd_kernel<XSG_CAM_PINHOLE><<<nb, kBlock, 0, s>>>(pack, width, height, world_space,
+                                                                          normalized, d_ray_o, d_ray_d, part);
+            break;
+        case XSG_CAM_SPHERICAL:
+            camera_rays_bwd_kernel<XSG_CAM_SPHERICAL><<<nb, kBlock, 0, s>>>(pack, width, height, world_space,
+                                                                            normalized, d_ray_o, d_ray_d, part);
+            break;
+        default:
+            camera_rays_bwd_kernel<XSG_CAM_LIDAR><<<nb, kBlock, 0, s>>>(pack, width, height, world_space,
+                                                                        normalized, d_ray_o, d_ray_d, part);
+            break;
+    }
+    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, kCamGrad, 0, pe, grad_pack);
+    XSG_TRY_LAUNCH("camera_rays_bwd");
+    return XSG_OK;
+}
+
+extern "C" size_t xsg_pixel_time_bwd_workspace_bytes(int64_t n) {
+    return sizeof(float) * 3 * (size_t)xsg_blocks(n > 0 ? n : 1, kBlock);
+}
+
+extern "C" int xsg_pixel_time_bwd(int kind, const float* pack, int width, int height, const float* uv,
+                                  int64_t n_uv, int delta, const float* grad, float* grad_pack, float* d_uv,
+                                  void* workspace, xsg_stream_t stream) {
+    const int pe = xsg_camera_pack_elements(kind);
+    if (pe <= 0) return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
+    const int64_t n = uv ? n_uv : (int64_t)width * height;
+    if (n < 0 || (!uv && (width < 0 || height < 0))) return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: bad size");
+    if (!pack || !grad_pack || !workspace || (n > 0 && !grad))
+        return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: null pointer");
+    const unsigned nb = xsg_blocks(n > 0 ? n : 1, kBlock);
+    float* part = (float*)workspace;
+    const hipStream_t s = (hipStream_t)stream;
+    const float2* uv2 = (const float2*)uv;
+    float2* duv2 = uv ? (float2*)d_uv : nullptr;
+    switch (kind) {
+        case XSG_CAM_PINHOLE:
+            pixel_time_bwd_kernel<XSG_CAM_PINHOLE><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2, part);
+            break;
+        case XSG_CAM_SPHERICAL:
+            pixel_time_bwd_kernel<XSG_CAM_SPHERICAL><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2,
+                                                                           part);
+            break;
+        default:
+            pixel_time_bwd_kernel<XSG_CAM_LIDAR><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2, part);
+            break;
+    }
+    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, 3, delta ? 1 : 0, pe, grad_pack);
+    XSG_TRY_LAUNCH("pixel_time_bwd");
     return XSG_OK;
 }

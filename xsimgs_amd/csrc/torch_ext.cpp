@@ -501,32 +501,139 @@ void validate_pack(const CamSpec& spec, const Tensor& pack) {  // camera.h:56-62
     TORCH_CHECK(pack.is_cuda(), "Camera pack must be on the GPU");
 }
 
+// CameraRaysFunction (include/cameras/ray_kernels.h:164-226): forward launch_camera_ray_fwd,
+// backward camera_ray_backward into the pack's gradient. Outputs: [ray_o if return_origins], ray_d,
+// [valid, non-differentiable].
+struct CameraRaysFn : public torch::autograd::Function<CameraRaysFn> {
+    static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx, const Tensor& pack,
+                                                  int64_t kind, int64_t width, int64_t height, bool world_space,
+                                                  bool normalized, bool return_origins, bool return_valid) {
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        auto opt = pack.options();
+        Tensor ray_o = return_origins ? at::empty({height, width, 3}, opt) : Tensor();
+        Tensor ray_d = at::empty({height, width, 3}, opt);
+        Tensor valid = return_valid ? at::empty({height, width}, opt.dtype(at::kBool)) : Tensor();
+        check_rc(xsg_camera_rays((int)kind, fptr(pack), (int)width, (int)height, world_space ? 1 : 0,
+                                 normalized ? 1 : 0, return_origins ? ray_o.data_ptr<float>() : nullptr,
+                                 ray_d.data_ptr<float>(), return_valid ? (uint8_t*)valid.data_ptr() : nullptr,
+                                 stream_of(pack)));
+        ctx->save_for_backward({pack});
+        ctx->saved_data["kind"] = kind;
+        ctx->saved_data["world_space"] = world_space;
+        ctx->saved_data["normalized"] = normalized;
+        ctx->saved_data["return_origins"] = return_origins;
+        torch::autograd::variable_list out;
+        if (return_origins) out.push_back(ray_o);
+        out.push_back(ray_d);
+        if (return_valid) {
+            ctx->mark_non_differentiable({valid});
+            out.push_back(valid);
+        }
+        return out;
+    }
+
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                   torch::autograd::variable_list grads) {
+        const Tensor pack = ctx->get_saved_variables()[0];
+        const bool ro = ctx->saved_data["return_origins"].toBool();
+        const Tensor d_ray_d = grads[ro ? 1 : 0].contiguous();
+        const Tensor d_ray_o = ro ? grads[0].contiguous() : Tensor();
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        const int height = (int)d_ray_d.size(0), width = (int)d_ray_d.size(1);
+        Tensor grad_pack = at::empty_like(pack);
+        Tensor ws = workspace(pack, xsg_camera_rays_bwd_workspace_bytes(width, height));
+        check_rc(xsg_camera_rays_bwd((int)ctx->saved_data["kind"].toInt(), fptr(pack), width, height,
+                                     ctx->saved_data["world_space"].toBool() ? 1 : 0,
+                                     ctx->saved_data["normalized"].toBool() ? 1 : 0,
+                                     d_ray_o.defined() ? fptr(d_ray_o) : nullptr, fptr(d_ray_d),
+                                     grad_pack.data_ptr<float>(), ws.data_ptr(), stream_of(pack)));
+        return {grad_pack, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
 py::object camera_rays(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool world_space,
                        bool normalized, bool return_origins, bool return_valid) {
     validate_pack(spec, pack);
-    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
-    auto opt = pack.options();
-    Tensor ray_o = return_origins ? at::empty({height, width, 3}, opt) : Tensor();
-    Tensor ray_d = at::empty({height, width, 3}, opt);
-    Tensor valid = return_valid ? at::empty({height, width}, opt.dtype(at::kBool)) : Tensor();
-    check_rc(xsg_camera_rays(spec.kind, fptr(pack.detach()), (int)width, (int)height, world_space ? 1 : 0,
-                             normalized ? 1 : 0, return_origins ? ray_o.data_ptr<float>() : nullptr,
-                             ray_d.data_ptr<float>(), return_valid ? (uint8_t*)valid.data_ptr() : nullptr,
-                             stream_of(pack)));
+    auto res = CameraRaysFn::apply(pack, (int64_t)spec.kind, width, height, world_space, normalized,
+                                   return_origins, return_valid);
     py::list out;
-    out.append(return_origins ? py::cast(ray_o) : py::none());
-    out.append(py::cast(ray_d));
-    if (return_valid) out.append(py::cast(valid));
+    size_t i = 0;
+    out.append(return_origins ? py::cast(res[i++]) : py::none());
+    out.append(py::cast(res[i++]));
+    if (return_valid) out.append(py::cast(res[i]));
     return out;
 }
 
+// CameraPixelTime[Delta]Function (include/cameras/time_kernels.h:364-458): the gradient w.r.t. the
+// pack is sum(g u), sum(g v), sum(g) on rolling_time and trigger_time (-sum(g) on pose_time for the
+// delta variant).
+struct PixelTimeFn : public torch::autograd::Function<PixelTimeFn> {
+    static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& pack, int64_t kind, int64_t width,
+                          int64_t height, bool delta) {
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        Tensor out = at::empty({height, width}, pack.options());
+        check_rc(xsg_pixel_time((int)kind, fptr(pack), (int)width, (int)height, nullptr, 0, delta ? 1 : 0,
+                                out.data_ptr<float>(), stream_of(pack)));
+        ctx->save_for_backward({pack});
+        ctx->saved_data["kind"] = kind;
+        ctx->saved_data["delta"] = delta;
+        return out;
+    }
+
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                   torch::autograd::variable_list grads) {
+        const Tensor pack = ctx->get_saved_variables()[0];
+        const Tensor g = grads[0].contiguous();
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        const int height = (int)g.size(0), width = (int)g.size(1);
+        Tensor grad_pack = at::empty_like(pack);
+        Tensor ws = workspace(pack, xsg_pixel_time_bwd_workspace_bytes((int64_t)width * height));
+        check_rc(xsg_pixel_time_bwd((int)ctx->saved_data["kind"].toInt(), fptr(pack), width, height, nullptr, 0,
+                                    ctx->saved_data["delta"].toBool() ? 1 : 0, fptr(g), grad_pack.data_ptr<float>(),
+                                    nullptr, ws.data_ptr(), stream_of(pack)));
+        return {grad_pack, Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// CameraPixelTime[Delta]FromUVFunction (include/cameras/time_kernels.h:398-489): gradients w.r.t. the
+// pack and the uv coordinates (d_uv = g rolling_time).
+struct PixelTimeUvFn : public torch::autograd::Function<PixelTimeUvFn> {
+    static Tensor forward(torch::autograd::AutogradContext* ctx, const Tensor& pack, const Tensor& uv, int64_t kind,
+                          bool delta) {
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        auto sizes = uv.sizes().vec();
+        sizes.pop_back();
+        Tensor out = at::empty(sizes, uv.options());
+        Tensor uvc = uv.contiguous();
+        check_rc(xsg_pixel_time((int)kind, fptr(pack), 0, 0, fptr(uvc), uv.numel() / 2, delta ? 1 : 0,
+                                out.data_ptr<float>(), stream_of(pack)));
+        ctx->save_for_backward({pack, uvc});
+        ctx->saved_data["kind"] = kind;
+        ctx->saved_data["delta"] = delta;
+        return out;
+    }
+
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                   torch::autograd::variable_list grads) {
+        const auto saved = ctx->get_saved_variables();
+        const Tensor pack = saved[0], uvc = saved[1];
+        const Tensor g = grads[0].contiguous();
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        const int64_t n = uvc.numel() / 2;
+        Tensor grad_pack = at::empty_like(pack);
+        Tensor d_uv = ctx->needs_input_grad(1) ? at::empty_like(uvc) : Tensor();
+        Tensor ws = workspace(pack, xsg_pixel_time_bwd_workspace_bytes(n));
+        check_rc(xsg_pixel_time_bwd((int)ctx->saved_data["kind"].toInt(), fptr(pack), 0, 0, fptr(uvc), n,
+                                    ctx->saved_data["delta"].toBool() ? 1 : 0, fptr(g), grad_pack.data_ptr<float>(),
+                                    d_uv.defined() ? d_uv.data_ptr<float>() : nullptr, ws.data_ptr(),
+                                    stream_of(pack)));
+        return {grad_pack, d_uv, Tensor(), Tensor()};
+    }
+};
+
 Tensor pixel_time(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool delta) {
     validate_pack(spec, pack);
-    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
-    Tensor out = at::empty({height, width}, pack.options());
-    check_rc(xsg_pixel_time(spec.kind, fptr(pack), (int)width, (int)height, nullptr, 0, delta ? 1 : 0,
-                            out.data_ptr<float>(), stream_of(pack)));
-    return out;
+    return PixelTimeFn::apply(pack, (int64_t)spec.kind, width, height, delta);
 }
 
 Tensor pixel_time_uv(const CamSpec& spec, const Tensor& pack, const Tensor& uv, bool delta) {
@@ -534,14 +641,7 @@ Tensor pixel_time_uv(const CamSpec& spec, const Tensor& pack, const Tensor& uv, 
     TORCH_CHECK(uv.size(-1) == 2, "UV coordinates last dimension must be 2")
     TORCH_CHECK(uv.device() == pack.device(), "Camera and UV-s must be on the same device")
     TORCH_CHECK(uv.dtype() == at::kFloat, "UV coordinates must be float32 tensor")
-    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
-    auto sizes = uv.sizes().vec();
-    sizes.pop_back();
-    Tensor out = at::empty(sizes, uv.options());
-    Tensor uvc = uv.contiguous();
-    check_rc(xsg_pixel_time(spec.kind, fptr(pack), 0, 0, fptr(uvc), uv.numel() / 2, delta ? 1 : 0,
-                            out.data_ptr<float>(), stream_of(pack)));
-    return out;
+    return PixelTimeUvFn::apply(pack, uv, (int64_t)spec.kind, delta);
 }
 
 std::tuple<Tensor, Tensor> projection(const CamSpec& spec, bool no_jac, const Tensor& pack, const Tensor& points,
