@@ -14,6 +14,7 @@
  *   xsg_project_points        <Camera>.projection[_nojac]       bind.h:66-81, projection_kernels.h:259-309
  *   xsg_camera_rays           <Camera>.camera_rays (forward)    bind.h:47-53, ray_kernels.h:7-59
  *   xsg_pixel_time*           <Camera>.pixel_time*              bind.h:54-65, time_kernels.h:5-241
+ *   xsg_undistort_map         <Camera>.undistort_map            distortion.h:33-56
  *   xsg_camera_rays_bwd       camera_ray_backward               ray_kernels.h:61-161
  *   xsg_pixel_time_bwd        pixel_time*_backward              time_kernels.h:123-330
  *   xsg_sh_fwd / xsg_sh_bwd   spherical_harmonics_fused_{fwd,bwd} csrc/color/sh_fwd.cu:248-259,
@@ -55,6 +56,8 @@ extern "C" {
 #define XSG_CAM_PINHOLE 0
 #define XSG_CAM_SPHERICAL 1
 #define XSG_CAM_LIDAR 2
+#define XSG_CAM_DISTORTED 3
+#define XSG_CAM_FISHEYE 4
 #define XSG_MODE_CENTRAL 0
 #define XSG_MODE_NEGATIVE 1
 #define XSG_MODE_POSITIVE 2
@@ -69,7 +72,8 @@ typedef struct ihipStream_t* xsg_stream_t; /* == hipStream_t */
 const char* xsg_last_error(void);
 int xsg_abi_version(void);
 
-/* Number of float32 elements of a camera pack of `kind` (pinhole/spherical 21, lidar 23).
+/* Number of float32 elements of a camera pack of `kind` (pinhole/spherical 21, lidar 23,
+ * distorted perspective 30, OpenCV fisheye 25).
  * Replaces Camera<Impl>::pack_elements (camera.h:141-143); the layout is documented in
  * xsimgs_amd/csrc/xsg_common.h. */
 int xsg_camera_pack_elements(int kind);
@@ -90,13 +94,20 @@ int xsg_camera_rays(int kind, const float* pack, int width, int height, int worl
                     int normalized, float* ray_o, float* ray_d, uint8_t* valid,
                     xsg_stream_t stream);
 
+/* <Camera>.undistort_map (distortion.h:33-56) of the distorted perspective and fisheye models: per
+ * pixel (float2, row-major [height, width]) the distorted image position of the pixel's undistorted
+ * uv, in [0, 1] with normalized_range, else in [-1, 1] */
+int xsg_undistort_map(int kind, const float* pack, int width, int height, int normalized_range, float* out,
+                      xsg_stream_t stream);
+
 /* per-pixel (uv == NULL) or per-uv capture time; `delta` subtracts the pose time */
 int xsg_pixel_time(int kind, const float* pack, int width, int height, const float* uv, int64_t n_uv,
                    int delta, float* out, xsg_stream_t stream);
 
 /* Gradient of sum(d_ray_o * ray_o + d_ray_d * ray_d) w.r.t. the camera pack (camera_ray_backward,
  * ray_kernels.h:61-161). grad_pack gets all xsg_camera_pack_elements(kind) values in pack order
- * (q0, t0, v, w, rolling_time, trigger_time, pose_time, intrinsics; 0 for the lidar beam address);
+ * (q0, t0, v, w, rolling_time, trigger_time, pose_time, the model's tensors; 0 for the lidar beam
+ * address and the distorted model's max_radius^2);
  * it needs no zero-initialisation. d_ray_o may be NULL (no origin gradient). The sum over pixels
  * is deterministic: per-block partials in `workspace`, then one fixed-order reduction. */
 size_t xsg_camera_rays_bwd_workspace_bytes(int width, int height);

@@ -18,7 +18,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 _LIBS = {}
 
-KIND = {"pinhole": 0, "spherical": 1, "lidar": 2}
+KIND = {"pinhole": 0, "spherical": 1, "lidar": 2, "distorted": 3, "fisheye": 4}
 MODE = {"central": 0, "negative": 1, "positive": 2}
 
 
@@ -48,7 +48,7 @@ def _camera_struct(prec):
     class Cam(C.Structure):
         _fields_ = [("kind", C.c_int), ("q", ct * 4), ("t", ct * 3), ("v", ct * 3), ("w", ct * 3),
                     ("rolling", ct * 2), ("trigger_time", ct), ("pose_time", ct), ("impl", ct * 4),
-                    ("beam_v", C.POINTER(ct)), ("n_beams", C.c_int)]
+                    ("beam_v", C.POINTER(ct)), ("n_beams", C.c_int), ("dist", ct * 8), ("max_radius_sq", ct)]
     return Cam
 
 
@@ -72,6 +72,10 @@ def camera(spec, prec: str = "f32"):
             arr[i] = float(vals[i])
     cam.trigger_time = float(spec.trigger_time)
     cam.pose_time = float(spec.pose_time)
+    if spec.kind in ("distorted", "fisheye"):
+        for i, x in enumerate(spec.dist):
+            cam.dist[i] = float(x)
+        cam.max_radius_sq = float(spec.max_radius) ** 2 if spec.max_radius is not None else 0.0
     cam._beam = None
     if spec.kind == "lidar":
         beam = np.ascontiguousarray(np.asarray(spec.beam_v, dtype=nt))
@@ -125,8 +129,9 @@ def project_utgs(spec, means, scales, quats, opacity, width, height, vel=None, u
     return flags, radii, m2, dep
 
 
-def projection(spec, points, vel=None, thr=1e-4, max_res=0.002, margin=1.0, mode="central", prec="f32"):
-    """<Camera>.projection (projection_kernels.h:259-309): ``uvdt[N,4], mask[N]``."""
+def projection(spec, points, vel=None, thr=1e-4, max_res=0.002, margin=1.0, mode="central", no_jac=False,
+               prec="f32"):
+    """<Camera>.projection[_nojac] (projection_kernels.h:259-309): ``uvdt[N,4], mask[N]``."""
     ct, nt = _real(prec)
     cam = camera(spec, prec)
     points, vel = _arr(points, nt), _arr(vel, nt)
@@ -134,32 +139,58 @@ def projection(spec, points, vel=None, thr=1e-4, max_res=0.002, margin=1.0, mode
     uvdt = np.zeros((n, 4), nt)
     mask = np.zeros(n, np.uint8)
     _lib(prec).orc_projection(C.byref(cam), C.c_int(n), _p(points), _p(vel), ct(thr), ct(max_res),
-                              ct(margin), C.c_int(MODE[mode]), _p(uvdt), _p(mask))
+                              ct(margin), C.c_int(MODE[mode]), C.c_int(int(no_jac)), _p(uvdt), _p(mask))
     return uvdt, mask.astype(bool)
 
 
-def camera_rays(spec, width, height, world_space=True, normalized=True, prec="f32"):
-    """<Camera>.camera_rays forward (ray_kernels.h:7-59): ``ray_o, ray_d`` as [H, W, 3]."""
+def camera_rays(spec, width, height, world_space=True, normalized=True, return_valid=False, prec="f32"):
+    """<Camera>.camera_rays forward (ray_kernels.h:7-59): ``ray_o, ray_d`` as [H, W, 3] (and the
+    per-pixel ``ray_valid`` mask with ``return_valid``)."""
     _, nt = _real(prec)
     cam = camera(spec, prec)
     ro = np.zeros((height, width, 3), nt)
     rd = np.zeros((height, width, 3), nt)
+    valid = np.zeros((height, width), np.uint8)
     _lib(prec).orc_camera_rays(C.byref(cam), C.c_int(width), C.c_int(height), C.c_int(int(world_space)),
-                               C.c_int(int(normalized)), _p(ro), _p(rd))
-    return ro, rd
+                               C.c_int(int(normalized)), _p(ro), _p(rd), _p(valid))
+    return (ro, rd, valid.astype(bool)) if return_valid else (ro, rd)
+
+
+def undistort_map(spec, width, height, normalized_range=False, prec="f32"):
+    """<Camera>.undistort_map (distortion.h:33-56) of the distorted and fisheye models: [H, W, 2]."""
+    _, nt = _real(prec)
+    cam = camera(spec, prec)
+    out = np.zeros((height, width, 2), nt)
+    _lib(prec).orc_undistort_map(C.byref(cam), C.c_int(width), C.c_int(height), C.c_int(int(normalized_range)),
+                                 _p(out))
+    return out
 
 
 CAMERA_GRAD_FIELDS = (("q", 4), ("t", 3), ("v", 3), ("w", 3), ("rolling", 2), ("trigger_time", 1),
                       ("pose_time", 1), ("impl", 4))
 
 
+def camera_grad_fields(kind):
+    """The camera's differentiable tensors in pack order, as (name, size): the model's own tensors
+    follow the pose (distorted: intrinsics, 8 coefficients, max_radius_sq; fisheye: intrinsics, 4)."""
+    if kind == "distorted":
+        return CAMERA_GRAD_FIELDS + (("dist", 8), ("max_radius_sq", 1))
+    if kind == "fisheye":
+        return CAMERA_GRAD_FIELDS + (("dist", 4),)
+    return CAMERA_GRAD_FIELDS
+
+
+def grad_elements(kind):
+    return sum(n for _, n in camera_grad_fields(kind))
+
+
 def camera_rays_bwd(spec, width, height, d_ray_o, d_ray_d, world_space=True, normalized=True, prec="f32"):
     """camera_ray_backward_kernel_cuda (ray_kernels.h:61-161): the gradient of the rays w.r.t. the
-    camera, summed over pixels, as 21 values in ``CAMERA_GRAD_FIELDS`` order (``d_ray_o`` may be None)."""
+    camera, summed over pixels, in ``camera_grad_fields(kind)`` order (``d_ray_o`` may be None)."""
     _, nt = _real(prec)
     cam = camera(spec, prec)
     d_ray_o, d_ray_d = _arr(d_ray_o, nt), _arr(d_ray_d, nt)
-    out = np.zeros(21, nt)
+    out = np.zeros(grad_elements(spec.kind), nt)
     _lib(prec).orc_camera_rays_bwd(C.byref(cam), C.c_int(width), C.c_int(height), C.c_int(int(world_space)),
                                    C.c_int(int(normalized)), _p(d_ray_o), _p(d_ray_d), _p(out))
     return out
@@ -191,7 +222,7 @@ def pixel_time_bwd(spec, grad, width=0, height=0, uv=None, delta=False, prec="f3
     cam = camera(spec, prec)
     grad = _arr(grad, nt)
     uv = _arr(uv, nt)
-    out = np.zeros(21, nt)
+    out = np.zeros(grad_elements(spec.kind), nt)
     d_uv = np.zeros_like(uv) if uv is not None else None
     n = grad.size
     _lib(prec).orc_pixel_time_bwd(C.byref(cam), C.c_int(width), C.c_int(height), _p(uv), C.c_long(n),

@@ -16,6 +16,11 @@
  *   orc_camera_rays_bwd       fp64 central differences of orc_camera_rays w.r.t. every camera
  *                             parameter (pinhole, spherical, lidar; world / camera space)
  *   orc_pixel_time_bwd        closed form (pixel time is linear in the camera's timing)
+ *   distorted / fisheye       rays -> projection round trip, zero-coefficient limits (pinhole,
+ *   models                    equidistant fisheye), the published OpenCV polynomials evaluated
+ *                             independently, undistort map = projection of the pinhole ray,
+ *                             fp64 central differences for their intrinsics / coefficient
+ *                             gradients; projection_nojac: fixed point = landing pixel's time
  *   orc_sh_fwd / orc_sh_bwd   scipy.special.sph_harm basis, fp64 finite differences
  *   orc_isect_*               brute-force tile enumeration in Python, numpy stable sort
  *   orc_sort_pairs            numpy argsort(kind="stable")
@@ -51,6 +56,7 @@
 #define COPYSIGN copysign
 #define FMIN fmin
 #define FMAX fmax
+#define HYPOT hypot
 #define ORC_PI 3.14159265358979323846
 #else
 #define SQRT sqrtf
@@ -66,6 +72,7 @@
 #define COPYSIGN copysignf
 #define FMIN fminf
 #define FMAX fmaxf
+#define HYPOT hypotf
 #define ORC_PI ((float)3.14159265358979323846)
 #endif
 
@@ -176,6 +183,134 @@ static v2 angles_to_uv(const orc_camera *c, int mode, real phi, real theta) {
     return r;
 }
 
+/* ------------------------------------------------------------------------- */
+/* Distorted perspective (OpenCV rational + tangential) and OpenCV fisheye    */
+/* camera models: csrc/cameras/distorted_perspective.cu, fisheye_opencv.cu,   */
+/* include/cameras/distortion.h                                               */
+/* ------------------------------------------------------------------------- */
+#define DIST_MIN_DET K(1e-3)
+
+/* uv_distortion (distortion.h:8-30): radial scale and tangential offset of a camera-space uv */
+static void uv_distortion(const real *k, real u, real v, real *scale, real *du, real *dv) {
+    const real uu = u * u, vv = v * v;
+    const real r2 = uu + vv;
+    const real num = K(1.0) + r2 * (k[0] + r2 * (k[1] + r2 * k[4]));
+    const real den = K(1.0) + r2 * (k[5] + r2 * (k[6] + r2 * k[7]));
+    *scale = num / den;
+    const real uv2 = K(2.0) * u * v;
+    *du = k[2] * uv2 + k[3] * (r2 + K(2.0) * uu);
+    *dv = k[2] * (r2 + K(2.0) * vv) + k[3] * uv2;
+}
+
+/* DistortionState (distorted_perspective.cu:11-36, :44-78): the distortion at uv with its
+ * (symmetric) Jacobian */
+typedef struct { real scale, denom, dx, dy, juu, juv, jvv; } dist_state;
+
+static dist_state distortion_state(const real *k, real u, real v) {
+    const real k1 = k[0], k2 = k[1], p1 = k[2], p2 = k[3], k3 = k[4], k4 = k[5], k5 = k[6], k6 = k[7];
+    const real r2 = u * u + v * v;
+    const real num = K(1.0) + r2 * (k1 + r2 * (k2 + r2 * k3));
+    const real den = K(1.0) + r2 * (k4 + r2 * (k5 + r2 * k6));
+    const real scale = num / den;
+    const real d_num = k1 + r2 * (K(2.0) * k2 + K(3.0) * k3 * r2);
+    const real d_den = k4 + r2 * (K(2.0) * k5 + K(3.0) * k6 * r2);
+    const real d_scale = (d_num * den - num * d_den) / (den * den);
+    dist_state s;
+    s.scale = scale;
+    s.denom = den;
+    s.dx = K(2.0) * p1 * u * v + p2 * (r2 + K(2.0) * u * u);
+    s.dy = p1 * (r2 + K(2.0) * v * v) + K(2.0) * p2 * u * v;
+    s.juu = scale + K(2.0) * u * u * d_scale + K(2.0) * p1 * v + K(6.0) * p2 * u;
+    s.juv = K(2.0) * u * v * d_scale + K(2.0) * p1 * u + K(2.0) * p2 * v;
+    s.jvv = scale + K(2.0) * v * v * d_scale + K(6.0) * p1 * v + K(2.0) * p2 * u;
+    return s;
+}
+
+/* undistort_uv (distorted_perspective.cu:80-98): five Newton steps on uv * scale + delta = uv_d,
+ * a fixed-point step where the Jacobian is nearly singular. `st` keeps the state of the last step
+ * (taken before that step's update). */
+static v2 undistort_uv(const real *k, v2 ud, dist_state *st) {
+    v2 uv = ud;
+    for (int j = 0; j < 5; ++j) {
+        *st = distortion_state(k, uv.x, uv.y);
+        const real rx = uv.x * st->scale + st->dx - ud.x;
+        const real ry = uv.y * st->scale + st->dy - ud.y;
+        const real det = st->juu * st->jvv - st->juv * st->juv;
+        if (FABS(det) > DIST_MIN_DET) {
+            uv.x -= (st->jvv * rx - st->juv * ry) / det;
+            uv.y -= (st->juu * ry - st->juv * rx) / det;
+        } else {
+            uv.x = (ud.x - st->dx) / st->scale;
+            uv.y = (ud.y - st->dy) / st->scale;
+        }
+    }
+    return uv;
+}
+
+/* Kannala-Brandt polynomial and its derivative (fisheye_opencv.cu:14-32) */
+static real fisheye_distortion(const real *k, real theta) {
+    const real t2 = theta * theta;
+    real d = t2 * k[3] + k[2];
+    d = t2 * d + k[1];
+    d = t2 * d + k[0];
+    d = t2 * d + K(1.0);
+    return theta * d;
+}
+
+static real fisheye_distortion_deriv(const real *k, real theta) {
+    const real t2 = theta * theta;
+    real d = t2 * K(9.0) * k[3] + K(7.0) * k[2];
+    d = t2 * d + K(5.0) * k[1];
+    d = t2 * d + K(3.0) * k[0];
+    d = t2 * d + K(1.0);
+    return d;
+}
+
+/* solve_theta (fisheye_opencv.cu:34-46): at most 20 Newton steps with the derivative clamped at 0.1
+ * and theta kept in [0, pi] */
+static real fisheye_solve_theta(const real *k, real delta, real *residual) {
+    real theta = delta;
+    *residual = 0;
+    for (int i = 0; i < 20; ++i) {
+        *residual = fisheye_distortion(k, theta) - delta;
+        theta -= *residual / FMAX(fisheye_distortion_deriv(k, theta), K(0.1));
+        theta = FMIN(FMAX(theta, K(0.0)), ORC_PI);
+        if (FABS(*residual) < K(1e-6)) break;
+    }
+    return theta;
+}
+
+/* camera_point_to_uvd of every camera model (perspective.cu:36-42, spherical.h:133-142,
+ * distorted_perspective.cu:190-197, fisheye_opencv.cu:138-148) */
+static v3 point_to_uvd(const orc_camera *c, int mode, v3 p) {
+    const real fx = c->impl[0], fy = c->impl[1], cx = c->impl[2], cy = c->impl[3];
+    if (c->kind == ORC_PINHOLE) return V3(p.x * fx / p.z + cx, p.y * fy / p.z + cy, p.z);
+    if (c->kind == ORC_DISTORTED) {
+        const real x = p.x / p.z, y = p.y / p.z;
+        real scale, du, dv;
+        uv_distortion(c->dist, x, y, &scale, &du, &dv);
+        const real r2 = x * x + y * y;
+        return V3((x * scale + du) * fx + cx, (y * scale + dv) * fy + cy, (r2 <= c->max_radius_sq) ? p.z : K(0));
+    }
+    if (c->kind == ORC_FISHEYE) {
+        const real norm = FMAX(K(1e-6), HYPOT(p.x, p.y));
+        const real theta = ATAN2(norm, p.z);
+        const int valid = fisheye_distortion_deriv(c->dist, theta) > K(0);
+        const real delta = fisheye_distortion(c->dist, theta) / norm;
+        const real depth = (valid && delta > K(0)) ? SQRT(dot3(p, p)) : K(0);
+        return V3(fx * delta * p.x + cx, fy * delta * p.y + cy, depth);
+    }
+    const real r = SQRT(p.x * p.x + p.y * p.y + p.z * p.z);
+    const real phi = ATAN2(-p.x, -p.y) + ORC_PI;
+    const real theta = ASIN(p.z / r);
+    const v2 uv = angles_to_uv(c, mode, phi, theta);
+    return V3(uv.x, uv.y, r);
+}
+
+static int has_projection_jacobian(const orc_camera *c) {
+    return c->kind == ORC_PINHOLE || c->kind == ORC_SPHERICAL || c->kind == ORC_LIDAR;
+}
+
 static void point_to_uvd_jacob(const orc_camera *c, int mode, v3 p, v3 dp, v3 *uvd, v2 *du_dv) {
     if (c->kind == ORC_PINHOLE) {
         /* csrc/cameras/perspective.cu:36-52 */
@@ -200,22 +335,30 @@ static void point_to_uvd_jacob(const orc_camera *c, int mode, v3 p, v3 dp, v3 *u
 }
 
 static void camera_projection(const orc_camera *c, v3 p_world, v3 p_vel, real thr, real max_res,
-                              real margin, int mode, real uvdt[4], int *valid) {
-    /* projection_kernels.h:201-256 with jac_camera_projection_iteration :116-174 */
+                              real margin, int mode, int no_jac, real uvdt[4], int *valid) {
+    /* projection_kernels.h:201-256 with jac_camera_projection_iteration :116-174 for the models
+     * that have a projection Jacobian, else (and for projection_nojac) the fixed-point
+     * camera_projection_iteration :177-198 */
+    const int newton = has_projection_jacobian(c) && !no_jac;
     v3 uvd = V3(0, 0, 0);
     real p_time = 0;
     if (mode == ORC_MODE_NEG) p_time = -FABS(c->rolling[0]) * K(0.5);
     else if (mode == ORC_MODE_POS) p_time = FABS(c->rolling[0]) * K(0.5);
     real residual = 0;
     for (int i = 0; i < 5; ++i) {
-        v3 pc, jpc; v2 du_dv;
+        v3 pc, jpc; v2 du_dv = {0, 0};
         jac_world_to_camera(c, p_world, p_vel, p_time, &pc, &jpc);
-        point_to_uvd_jacob(c, mode, pc, jpc, &uvd, &du_dv);
+        if (newton) point_to_uvd_jacob(c, mode, pc, jpc, &uvd, &du_dv);
+        else uvd = point_to_uvd(c, mode, pc);
         const real assumed = c->pose_time + p_time;
         const real real_time = c->trigger_time + (uvd.x * c->rolling[0] + uvd.y * c->rolling[1]);
         residual = assumed - real_time;
-        const real d_res = K(1.0) - (du_dv.x * c->rolling[0] + du_dv.y * c->rolling[1]);
-        p_time -= residual / d_res;
+        if (newton) {
+            const real d_res = K(1.0) - (du_dv.x * c->rolling[0] + du_dv.y * c->rolling[1]);
+            p_time -= residual / d_res;
+        } else {
+            p_time -= residual;
+        }
         if ((uvd.z <= K(0)) || (uvd.x < -margin) || (uvd.x > K(1) + margin) ||
             (uvd.y < -margin) || (uvd.y > K(1) + margin)) {
             *valid = 0;
@@ -248,7 +391,7 @@ static int unscented_transform(const orc_camera *c, const real ut[4], v2 img, in
     /* ut_kernels.h:52-137 */
     real uvdt[4]; int valid = 1;
     v2 pts[7];
-    camera_projection(c, p_world, p_vel, thr, max_res, margin, mode, uvdt, &valid);
+    camera_projection(c, p_world, p_vel, thr, max_res, margin, mode, 0, uvdt, &valid);
     if (!valid) return 0;
     pts[0].x = uvdt[0] * img.x; pts[0].y = uvdt[1] * img.y;
     mean2d->x = ut[0] * pts[0].x; mean2d->y = ut[0] * pts[0].y;
@@ -256,7 +399,7 @@ static int unscented_transform(const orc_camera *c, const real ut[4], v2 img, in
     real u_min = pts[0].x, u_max = pts[0].x;
     real sign = K(1.0);
     for (int i = 0; i < 6; ++i) {
-        camera_projection(c, add3(p_world, scl3(d[i / 2], sign)), p_vel, thr, max_res, margin, mode,
+        camera_projection(c, add3(p_world, scl3(d[i / 2], sign)), p_vel, thr, max_res, margin, mode, 0,
                           uvdt, &valid);
         pts[i + 1].x = uvdt[0] * img.x; pts[i + 1].y = uvdt[1] * img.y;
         mean2d->x += ut[2] * pts[i + 1].x; mean2d->y += ut[2] * pts[i + 1].y;
@@ -294,11 +437,11 @@ static int ut_projection(const orc_camera *c, int mode, const real ut[4], v2 img
 
 /* Projection of points (uvdt + mask): projection_kernels.h:259-309 (jacobian variant). */
 void orc_projection(const orc_camera *c, int n, const real *pts, const real *vel, real thr,
-                    real max_res, real margin, int mode, real *uvdt_out, uint8_t *mask_out) {
+                    real max_res, real margin, int mode, int no_jac, real *uvdt_out, uint8_t *mask_out) {
     for (int i = 0; i < n; ++i) {
         int valid = 1; real uvdt[4];
         const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
-        camera_projection(c, ld3(pts + 3 * i), pv, thr, max_res, margin, mode, uvdt, &valid);
+        camera_projection(c, ld3(pts + 3 * i), pv, thr, max_res, margin, mode, no_jac, uvdt, &valid);
         uvdt[3] += c->pose_time;
         memcpy(uvdt_out + 4 * i, uvdt, sizeof(uvdt));
         valid = valid && (uvdt[0] >= 0 && uvdt[1] >= 0) && (uvdt[0] <= 1 && uvdt[1] <= 1);
@@ -388,6 +531,21 @@ static v3 pixel_to_camera_ray(const orc_camera *c, real u, real v) {
     if (c->kind == ORC_PINHOLE) { /* perspective.cu:13-16 */
         return V3((u - c->impl[2]) / c->impl[0], (v - c->impl[3]) / c->impl[1], K(1.0));
     }
+    if (c->kind == ORC_DISTORTED) { /* distorted_perspective.cu:100-105 */
+        dist_state st;
+        const v2 ud = {(u - c->impl[2]) / c->impl[0], (v - c->impl[3]) / c->impl[1]};
+        const v2 uc = undistort_uv(c->dist, ud, &st);
+        return V3(uc.x, uc.y, K(1.0));
+    }
+    if (c->kind == ORC_FISHEYE) { /* fisheye_opencv.cu:48-62 */
+        const real x = (u - c->impl[2]) / c->impl[0], y = (v - c->impl[3]) / c->impl[1];
+        const real delta = SQRT(x * x + y * y);
+        real residual;
+        const real theta = fisheye_solve_theta(c->dist, delta, &residual);
+        if (theta <= K(0)) return V3(0, 0, K(1.0));
+        const real sf = SIN(theta) / delta;
+        return V3(sf * x, sf * y, COS(theta));
+    }
     /* spherical.h:9-22, 121-127 */
     const real az = c->impl[0] + u * c->impl[1];
     const real el = c->impl[2] + v * c->impl[3];
@@ -395,8 +553,58 @@ static v3 pixel_to_camera_ray(const orc_camera *c, real u, real v) {
     return V3(xy * SIN(az), xy * COS(az), K(1.0) * SIN(el));
 }
 
+/* ray_valid (camera.h:114-120): distorted_perspective.cu:107-117 (the undistortion converged
+ * to 1e-5, inside max_radius), fisheye_opencv.cu:64-72 (converged, on the rising branch of the
+ * polynomial); every other model is valid everywhere */
+static int ray_valid(const orc_camera *c, real u, real v) {
+    if (c->kind == ORC_DISTORTED) {
+        dist_state st;
+        const v2 ud = {(u - c->impl[2]) / c->impl[0], (v - c->impl[3]) / c->impl[1]};
+        const v2 uc = undistort_uv(c->dist, ud, &st);
+        const real rx = uc.x * st.scale + st.dx - ud.x, ry = uc.y * st.scale + st.dy - ud.y;
+        const real r2 = uc.x * uc.x + uc.y * uc.y;
+        return (r2 <= c->max_radius_sq) && (FABS(rx) < K(1e-5)) && (FABS(ry) < K(1e-5));
+    }
+    if (c->kind == ORC_FISHEYE) {
+        const real x = (u - c->impl[2]) / c->impl[0], y = (v - c->impl[3]) / c->impl[1];
+        const real delta = SQRT(x * x + y * y);
+        if (delta <= K(1e-8)) return 1;
+        real residual;
+        const real theta = fisheye_solve_theta(c->dist, delta, &residual);
+        return (FABS(residual) < K(1e-5)) && (fisheye_distortion_deriv(c->dist, theta) > K(0));
+    }
+    return 1;
+}
+
+/* undistort_map (distortion.h:33-56) with distort_uv of distorted_perspective.cu:199-203 and
+ * fisheye_opencv.cu:150-156: per pixel, the distorted position of the pixel's undistorted uv, in
+ * [0, 1] with normalized_range set, else mapped to [-1, 1] */
+void orc_undistort_map(const orc_camera *c, int width, int height, int normalized_range, real *out) {
+    const real fx = c->impl[0], fy = c->impl[1], cx = c->impl[2], cy = c->impl[3];
+    for (int idx = 0; idx < width * height; ++idx) {
+        const int px = idx % width, py = idx / width;
+        const real u = ((real)px + K(0.5)) / (real)width;
+        const real v = ((real)py + K(0.5)) / (real)height;
+        const real x = (u - cx) / fx, y = (v - cy) / fy;
+        real ru, rv;
+        if (c->kind == ORC_DISTORTED) {
+            real scale, du, dv;
+            uv_distortion(c->dist, x, y, &scale, &du, &dv);
+            ru = (x * scale + du) * fx + cx;
+            rv = (y * scale + dv) * fy + cy;
+        } else {
+            const real theta = SQRT(x * x + y * y);
+            const real scale = (theta > K(1e-8)) ? fisheye_distortion(c->dist, theta) / theta : K(1.0);
+            ru = x * scale * fx + cx;
+            rv = y * scale * fy + cy;
+        }
+        out[2 * idx] = normalized_range ? ru : ru * K(2.0) - K(1.0);
+        out[2 * idx + 1] = normalized_range ? rv : rv * K(2.0) - K(1.0);
+    }
+}
+
 void orc_camera_rays(const orc_camera *c, int width, int height, int world_space, int normalized,
-                     real *ray_o, real *ray_d) {
+                     real *ray_o, real *ray_d, uint8_t *valid) {
     for (int idx = 0; idx < width * height; ++idx) {
         const int px = idx % width, py = idx / width;
         const real u = ((real)px + K(0.5)) / (real)width;
@@ -418,19 +626,29 @@ void orc_camera_rays(const orc_camera *c, int width, int height, int world_space
         }
         ray_o[3 * idx] = o.x; ray_o[3 * idx + 1] = o.y; ray_o[3 * idx + 2] = o.z;
         ray_d[3 * idx] = ray.x; ray_d[3 * idx + 1] = ray.y; ray_d[3 * idx + 2] = ray.z;
+        if (valid) valid[idx] = (uint8_t)ray_valid(c, u, v);
     }
 }
 
 /* Backward of orc_camera_rays w.r.t. the camera: camera_ray_backward_kernel_cuda
  * (ray_kernels.h:61-161), restated for the pose model of orc_camera_rays. Gradients are summed
- * over pixels (in double) into out[21] = q(4) t(3) v(3) w(3) rolling(2) trigger_time pose_time
- * impl(4), the camera's tensor order (camera.h:144, perspective.cu:8, spherical.h:35). d_ray_o may
+ * over pixels (in double) into out[orc_grad_elements(kind)] = q(4) t(3) v(3) w(3) rolling(2)
+ * trigger_time pose_time, then the model's tensors: impl(4) for pinhole / spherical / lidar,
+ * f c(4) dist(8) max_radius_sq(1) for distorted, f c(4) dist(4) for fisheye -- the camera's tensor
+ * order (camera.h:144, perspective.cu:8, spherical.h:35, distorted_perspective.cu:8,
+ * fisheye_opencv.cu:7). d_ray_o may
  * be NULL. Only the pinhole model has an intrinsics gradient (perspective.cu:19-33); the spherical
  * and lidar models inherit the empty one (base_camera_impl.h:19-22). */
+/* Camera gradient length: the 17 pose / timing values and the model's own tensors
+ * (perspective.cu:8, spherical.h:35, distorted_perspective.cu:8, fisheye_opencv.cu:7) */
+int orc_grad_elements(int kind) {
+    return kind == ORC_DISTORTED ? 30 : kind == ORC_FISHEYE ? 25 : 21;
+}
+
 void orc_camera_rays_bwd(const orc_camera *c, int width, int height, int world_space, int normalized,
                          const real *d_ray_o, const real *d_ray_d, real *out) {
-    double acc[21];
-    for (int k = 0; k < 21; ++k) acc[k] = 0.0;
+    double acc[32];
+    for (int k = 0; k < 32; ++k) acc[k] = 0.0;
     for (int idx = 0; idx < width * height; ++idx) {
         const int px = idx % width, py = idx / width;
         const real u = ((real)px + K(0.5)) / (real)width;
@@ -495,13 +713,73 @@ void orc_camera_rays_bwd(const orc_camera *c, int width, int height, int world_s
             acc[18] += -dr.y * (v - c->impl[3]) * ify * ify;
             acc[19] += -dr.x * ifx;
             acc[20] += -dr.y * ify;
+        } else if (c->kind == ORC_DISTORTED) {
+            /* distorted_perspective.cu:121-188: re-solve, then the implicit-function gradient at the
+             * solution: g_d = J^-T (dr.x, dr.y) (J symmetric; d / scale where J is nearly singular),
+             * dL/dk = -g_d . dD/dk */
+            const real ifx = K(1.0) / c->impl[0], ify = K(1.0) / c->impl[1];
+            const v2 ud = {(u - c->impl[2]) * ifx, (v - c->impl[3]) * ify};
+            dist_state st;
+            const v2 uc = undistort_uv(c->dist, ud, &st);
+            st = distortion_state(c->dist, uc.x, uc.y);
+            const real det = st.juu * st.jvv - st.juv * st.juv;
+            real gx, gy;
+            if (FABS(det) <= DIST_MIN_DET) {
+                gx = dr.x / st.scale; gy = dr.y / st.scale;
+            } else {
+                gx = (st.jvv * dr.x - st.juv * dr.y) / det;
+                gy = (st.juu * dr.y - st.juv * dr.x) / det;
+            }
+            acc[17] += -gx * ud.x * ifx;
+            acc[18] += -gy * ud.y * ify;
+            acc[19] += -gx * ifx;
+            acc[20] += -gy * ify;
+            const real r2 = uc.x * uc.x + uc.y * uc.y, r4 = r2 * r2, r6 = r4 * r2;
+            const real d_rad = -(gx * uc.x + gy * uc.y) / st.denom;
+            const real d_rad_den = -d_rad * st.scale;
+            acc[21] += d_rad * r2;
+            acc[22] += d_rad * r4;
+            acc[23] += -(gx * K(2.0) * uc.x * uc.y + gy * (r2 + K(2.0) * uc.y * uc.y));
+            acc[24] += -(gx * (r2 + K(2.0) * uc.x * uc.x) + gy * K(2.0) * uc.x * uc.y);
+            acc[25] += d_rad * r6;
+            acc[26] += d_rad_den * r2;
+            acc[27] += d_rad_den * r4;
+            acc[28] += d_rad_den * r6;
+        } else if (c->kind == ORC_FISHEYE) {
+            /* fisheye_opencv.cu:74-136: theta(delta, k) implicit through theta_d(theta, k) = delta */
+            const real x = (u - c->impl[2]) / c->impl[0], y = (v - c->impl[3]) / c->impl[1];
+            const real delta = SQRT(x * x + y * y);
+            real residual;
+            const real theta = fisheye_solve_theta(c->dist, delta, &residual);
+            const real deriv = fisheye_distortion_deriv(c->dist, theta);
+            if (theta > K(0) && delta > K(1e-8) && FABS(residual) < K(1e-5) && deriv > K(1e-3)) {
+                const real st = SIN(theta), ct = COS(theta);
+                const real inv_delta = K(1.0) / delta;
+                const real sf = st * inv_delta;
+                const real d_s = dr.x * x + dr.y * y;
+                const real d_theta = d_s * ct * inv_delta - dr.z * st;
+                const real dts = d_theta / deriv;
+                const real t2 = theta * theta, t3 = t2 * theta;
+                acc[21] += -dts * t3;
+                acc[22] += -dts * t3 * t2;
+                acc[23] += -dts * t3 * t2 * t2;
+                acc[24] += -dts * t3 * t2 * t2 * t2;
+                const real d_delta = -d_s * st * inv_delta * inv_delta + dts;
+                const real gx = sf * dr.x + d_delta * x * inv_delta;
+                const real gy = sf * dr.y + d_delta * y * inv_delta;
+                acc[17] += -gx * x / c->impl[0];
+                acc[18] += -gy * y / c->impl[1];
+                acc[19] += -gx / c->impl[0];
+                acc[20] += -gy / c->impl[1];
+            }
         }
     }
-    for (int k = 0; k < 21; ++k) out[k] = (real)acc[k];
+    const int ne = orc_grad_elements(c->kind);
+    for (int k = 0; k < ne; ++k) out[k] = (real)acc[k];
 }
 
 /* pixel_time[_delta][_from_uv] backward (time_kernels.h:123-330): with uv NULL the n = width *
- * height pixels' own uv. out[21] as orc_camera_rays_bwd: trigger_time += sum g, rolling += sum g uv,
+ * height pixels' own uv. out as orc_camera_rays_bwd: trigger_time += sum g, rolling += sum g uv,
  * pose_time -= sum g for the delta variants; d_uv[i] = g_i rolling when uv is given. */
 void orc_pixel_time_bwd(const orc_camera *c, int width, int height, const real *uv, long n, int delta,
                         const real *grad, real *out, real *d_uv) {
@@ -519,7 +797,7 @@ void orc_pixel_time_bwd(const orc_camera *c, int width, int height, const real *
         }
         g0 += grad[i]; gu += (double)grad[i] * u; gv += (double)grad[i] * v;
     }
-    for (int k = 0; k < 21; ++k) out[k] = 0;
+    for (int k = 0; k < orc_grad_elements(c->kind); ++k) out[k] = 0;
     out[13] = (real)gu; out[14] = (real)gv; out[15] = (real)g0;
     if (delta) out[16] = (real)-g0;
 }

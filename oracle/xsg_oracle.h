@@ -20,7 +20,7 @@ typedef float real;
 #endif
 
 /* Camera kinds and the flat camera-pack layout shared with the HIP side. */
-enum { ORC_PINHOLE = 0, ORC_SPHERICAL = 1, ORC_LIDAR = 2 };
+enum { ORC_PINHOLE = 0, ORC_SPHERICAL = 1, ORC_LIDAR = 2, ORC_DISTORTED = 3, ORC_FISHEYE = 4 };
 enum { ORC_MODE_CENTRAL = 0, ORC_MODE_NEG = 1, ORC_MODE_POS = 2 };
 
 typedef struct {
@@ -32,9 +32,12 @@ typedef struct {
     real rolling[2];  /* rolling-shutter duration along u, v */
     real trigger_time;
     real pose_time;
-    real impl[4];     /* pinhole f.x f.y c.x c.y | spherical phi_min phi_range theta_min theta_range */
+    real impl[4];     /* pinhole, distorted, fisheye f.x f.y c.x c.y |
+                         spherical, lidar phi_min phi_range theta_min theta_range */
     const real *beam_v; /* lidar: per-row v coordinate (host memory) */
     int n_beams;
+    real dist[8];       /* distorted: k1 k2 p1 p2 k3 k4 k5 k6 | fisheye: k1 k2 k3 k4 */
+    real max_radius_sq; /* distorted: largest squared camera-space radius |xy / z|^2 projected */
 } orc_camera;
 
 #endif

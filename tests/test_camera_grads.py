@@ -31,16 +31,27 @@ def _spec(kind, w_scale=1.0):
         return CameraSpec("pinhole", W, H, impl=[0.93, 1.41, 0.47, 0.53], **common)
     if kind == "spherical":
         return CameraSpec("spherical", W, H, impl=[0.1, 2.0 * np.pi, -0.6, 1.1], **common)
+    if kind == "distorted":
+        return CameraSpec("distorted", W, H, impl=[0.93, 1.41, 0.47, 0.53],
+                          dist=[-0.28, 0.07, 1e-3, -5e-4, 0.01, 0.02, -0.004, 0.001], max_radius=1.5, **common)
+    if kind == "fisheye":
+        return CameraSpec("fisheye", W, H, impl=[0.35, 0.45, 0.5, 0.48], dist=[0.03, -0.005, 0.001, -0.0001],
+                          **common)
     return CameraSpec("lidar", W, H, impl=[0.0, 2.0 * np.pi, 0.3, -0.7], beam_v=_beam_v(H), **common)
 
 
 def _get(spec, name):
+    if name == "max_radius_sq":
+        return [float(spec.max_radius) ** 2]
     v = getattr(spec, name)
     return [float(v)] if np.isscalar(v) else [float(x) for x in v]
 
 
 def _set(spec, name, vals):
-    setattr(spec, name, vals[0] if name in ("trigger_time", "pose_time") else list(vals))
+    if name == "max_radius_sq":
+        spec.max_radius = float(np.sqrt(vals[0]))
+    else:
+        setattr(spec, name, vals[0] if name in ("trigger_time", "pose_time") else list(vals))
 
 
 def _loss(spec, go, gd, world_space, normalized):
@@ -49,7 +60,8 @@ def _loss(spec, go, gd, world_space, normalized):
 
 
 CASES = [(k, ws, nz, wsc) for k in ("pinhole", "spherical", "lidar") for ws in (True, False) for nz in (True, False)
-         for wsc in (1.0, 1e-4)]
+         for wsc in (1.0, 1e-4)] + [(k, ws, nz, 1.0) for k in ("distorted", "fisheye") for ws in (True, False)
+                                    for nz in (True, False)]
 
 
 @pytest.mark.parametrize("kind,world_space,normalized,w_scale", CASES)
@@ -61,7 +73,7 @@ def test_oracle_ray_bwd_matches_finite_differences(kind, world_space, normalized
     got = O.camera_rays_bwd(spec, W, H, go, gd, world_space, normalized, prec="f64")
     fd = []
     eps = 1e-6
-    for name, n in FIELDS:
+    for name, n in O.camera_grad_fields(kind):
         base = _get(spec, name)
         for i in range(n):
             vals = list(base)
@@ -73,7 +85,7 @@ def test_oracle_ray_bwd_matches_finite_differences(kind, world_space, normalized
             fd.append((_loss(sp, go, gd, world_space, normalized) - _loss(sm, go, gd, world_space, normalized))
                       / (2 * eps))
     fd = np.array(fd)
-    if kind != "pinhole":
+    if kind in ("spherical", "lidar"):
         fd[17:] = 0.0  # the spherical and lidar models carry no intrinsics gradient (base_camera_impl.h:19-22)
     np.testing.assert_allclose(got, fd, rtol=1e-6, atol=1e-6 * max(1.0, np.abs(fd).max()))
     if not world_space:
@@ -111,6 +123,8 @@ def _gpu_cam(spec, dev, requires_grad=False):
             t.requires_grad_(True)
         if spec.kind != "lidar":
             _impl(cam).requires_grad_(True)
+        if spec.kind in ("distorted", "fisheye"):
+            cam.distortion.requires_grad_(True)
     return cam
 
 
@@ -129,8 +143,8 @@ def _close(got, ref, name):
     assert not bad.any(), (name, np.nonzero(bad)[0], got[bad], ref[bad])
 
 
-GPU_RAY_CASES = [(k, ws, nz, ro) for k in ("pinhole", "spherical", "lidar") for ws in (True, False)
-                 for nz in (True, False) for ro in (True, False) if ws or ro]
+GPU_RAY_CASES = [(k, ws, nz, ro) for k in ("pinhole", "spherical", "lidar", "distorted", "fisheye")
+                 for ws in (True, False) for nz in (True, False) for ro in (True, False) if ws or ro]
 
 
 @pytest.mark.gpu
@@ -150,10 +164,11 @@ def test_gpu_camera_rays_bwd(dev, kind, world_space, normalized, return_origins)
         loss = loss + (out[0] * torch.from_numpy(go).to(dev)).sum()
     loss.backward()
     got = pack.grad.detach().cpu().numpy().reshape(-1)
-    assert got.shape[0] == (23 if kind == "lidar" else 21)
+    assert got.shape[0] == {"lidar": 23, "distorted": 30, "fisheye": 25}.get(kind, 21)
     ref = O.camera_rays_bwd(spec, W, H, go if return_origins else None, gd, world_space, normalized, prec="f64")
-    _close(got[:21], ref, f"d_pack {kind}")
-    assert np.all(got[21:] == 0)   # the lidar beam-table address carries no gradient
+    _close(got[:len(ref)], ref, f"d_pack {kind}")
+    # the lidar beam-table address and the distorted model's max_radius^2 carry no gradient
+    assert np.all(got[len(ref):] == 0)
 
 
 @pytest.mark.gpu
@@ -183,7 +198,7 @@ def test_gpu_camera_rays_bwd_full_frame(dev, kind, size):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["pinhole", "spherical", "lidar"])
+@pytest.mark.parametrize("kind", ["pinhole", "spherical", "lidar", "distorted", "fisheye"])
 def test_gpu_camera_grads_reach_pose_tensors(dev, kind):
     """Autograd from the rays to the camera's own tensors: the pack's backward splits the pack
     gradient over q, t, v, w, rolling, trigger, pose time and the intrinsics (pack_kernels.h:85-104)."""
@@ -203,6 +218,9 @@ def test_gpu_camera_grads_reach_pose_tensors(dev, kind):
         got = np.concatenate([got, _impl(cam).grad.detach().cpu().numpy().reshape(-1)])
     else:
         ref = ref[:17]
+    if kind in ("distorted", "fisheye"):
+        got = np.concatenate([got, cam.distortion.grad.detach().cpu().numpy().reshape(-1)])
+        ref = ref[:len(got)]   # max_radius is derived from the coefficients, not a leaf
     _close(got, ref, f"pose grads {kind}")
 
 

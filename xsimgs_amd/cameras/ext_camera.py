@@ -121,6 +121,12 @@ class FusedRSCamera:
     def image_time_delta(self, image):
         return self.ext_cls.pixel_time_delta(self.pack, width=image.shape[1], height=image.shape[0]).unsqueeze(-1)
 
+    def undistort_map(self, width: int, height: int, normalized_range: bool = False):
+        if not hasattr(self.ext_cls, "undistort_map"):
+            raise NotImplementedError(f'Camera extension class "{self.ext_cls.__name__}" does not implement '
+                                      '"undistort_map"')
+        return self.ext_cls.undistort_map(self.pack, width=width, height=height, normalized_range=normalized_range)
+
     def ut_gs_projection(self, points, scale, rotation, width: int, height: int, points_velocity=None,
                          opacity=None, ut_alpha: float = 0.1, ut_beta: float = 2.0, ut_kappa: float = 0.0,
                          use_phm: bool = None):

@@ -154,6 +154,20 @@ template <int KIND>
 XSG_DEV f3 pixel_to_camera_ray(const Camera& c, f2 uv) {
     if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:13-16
         return mk3((uv.x - c.i2) / c.i0, (uv.y - c.i3) / c.i1, 1.0f);
+    } else if constexpr (KIND == XSG_CAM_DISTORTED) {  // distorted_perspective.cu:100-105
+        DistState st;
+        const f2 uc = undistort_uv(c, mk2((uv.x - c.i2) / c.i0, (uv.y - c.i3) / c.i1), st);
+        return mk3(uc.x, uc.y, 1.0f);
+    } else if constexpr (KIND == XSG_CAM_FISHEYE) {  // fisheye_opencv.cu:48-62
+        const float x = (uv.x - c.i2) / c.i0, y = (uv.y - c.i3) / c.i1;
+        const float delta = sqrtf(x * x + y * y);
+        float residual;
+        const float th = fisheye_solve_theta(c, delta, residual);
+        if (th <= 0.0f) return mk3(0.f, 0.f, 1.0f);
+        float st, ct;
+        sincosf(th, &st, &ct);
+        const float sf = st / delta;
+        return mk3(sf * x, sf * y, ct);
     } else {  // spherical.h:9-22, 121-127
         const float az = c.i0 + uv.x * c.i1;
         const float el = c.i2 + uv.y * c.i3;
@@ -162,6 +176,30 @@ XSG_DEV f3 pixel_to_camera_ray(const Camera& c, f2 uv) {
         sincosf(az, &sa, &ca);
         const float xy = 1.0f * ce;
         return mk3(xy * sa, xy * ca, 1.0f * se);
+    }
+}
+
+// ray_valid (camera.h:114-120): the distorted model's undistortion converged to 1e-5 inside
+// max_radius (distorted_perspective.cu:107-117), the fisheye solve converged on the rising branch of
+// the polynomial (fisheye_opencv.cu:64-72); the other models are valid everywhere
+template <int KIND>
+XSG_DEV bool ray_valid(const Camera& c, f2 uv) {
+    if constexpr (KIND == XSG_CAM_DISTORTED) {
+        DistState st;
+        const f2 ud = mk2((uv.x - c.i2) / c.i0, (uv.y - c.i3) / c.i1);
+        const f2 uc = undistort_uv(c, ud, st);
+        const float rx = uc.x * st.scale + st.dx - ud.x, ry = uc.y * st.scale + st.dy - ud.y;
+        const float r2 = uc.x * uc.x + uc.y * uc.y;
+        return (r2 <= c.max_r2) && (fabsf(rx) < 1e-5f) && (fabsf(ry) < 1e-5f);
+    } else if constexpr (KIND == XSG_CAM_FISHEYE) {
+        const float x = (uv.x - c.i2) / c.i0, y = (uv.y - c.i3) / c.i1;
+        const float delta = sqrtf(x * x + y * y);
+        if (delta <= 1e-8f) return true;
+        float residual;
+        const float th = fisheye_solve_theta(c, delta, residual);
+        return (fabsf(residual) < 1e-5f) && (fisheye_distortion_deriv(c, th) > 0.0f);
+    } else {
+        return true;
     }
 }
 
@@ -190,7 +228,7 @@ __global__ __launch_bounds__(kBlock) void camera_rays_kernel(
     }
     if (ray_o) st3(ray_o + 3 * idx, o);
     st3(ray_d + 3 * idx, ray);
-    if (valid) valid[idx] = 1;  // no ray_valid on pinhole / spherical / lidar impls (camera.h:117-123)
+    if (valid) valid[idx] = ray_valid<KIND>(c, uv) ? 1 : 0;
 }
 
 template <int KIND>
@@ -211,18 +249,42 @@ __global__ __launch_bounds__(kBlock) void pixel_time_kernel(
     out[idx] = t;
 }
 
-// --------------------------------------------------------------------------------------------
-// Camera gradients. Per thread the gradient w.r.t. the camera's 21 parameters (q0, t0, v, w,
-// rolling_time, trigger_time, pose_time, intrinsics: the camera's tensors in order, camera.h:144),
-// reduced per block into partials; grad_final_kernel sums the partials in a fixed order and writes
-// the whole pack gradient (the lidar beam address gets 0).
-constexpr int kCamGrad = 21;
-
-XSG_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+// undistort_map (distortion.h:33-56) with distort_uv (distorted_perspective.cu:199-203,
+// fisheye_opencv.cu:150-156): the distorted position of each pixel's undistorted uv, in [0, 1] with
+// normalized_range, else mapped to [-1, 1]
+template <int KIND>
+__global__ __launch_bounds__(kBlock) void undistort_map_kernel(const float* __restrict__ pack, int width, int height,
+                                                               int normalized_range, float2* __restrict__ out) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= (int64_t)width * height) return;
+    const Camera c = load_camera(pack, KIND);
+    const f2 uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+    const float x = (uv.x - c.i2) / c.i0, y = (uv.y - c.i3) / c.i1;
+    float ru, rv;
+    if constexpr (KIND == XSG_CAM_DISTORTED) {
+        float scale, du, dv;
+        uv_distortion(c, x, y, scale, du, dv);
+        ru = (x * scale + du) * c.i0 + c.i2;
+        rv = (y * scale + dv) * c.i1 + c.i3;
+    } else {
+        const float th = sqrtf(x * x + y * y);
+        const float scale = (th > 1e-8f) ? fisheye_distortion(c, th) / th : 1.0f;
+        ru = x * scale * c.i0 + c.i2;
+        rv = y * scale * c.i1 + c.i3;
+    }
+    out[idx] = normalized_range ? make_float2(ru, rv) : make_float2(ru * 2.0f - 1.0f, rv * 2.0f - 1.0f);
 }
+
+// --------------------------------------------------------------------------------------------
+// Camera gradients. Per thread the gradient w.r.t. the camera's parameters in pack order (q0, t0,
+// v, w, rolling_time, trigger_time, pose_time, then the model's tensors, camera.h:144), reduced per
+// block into partials; grad_final_kernel sums the partials in a fixed order and writes the whole
+// pack gradient (0 for the lidar beam address and the distorted model's max_radius^2).
+template <int KIND>
+constexpr int cam_grad_count() {
+    return KIND == XSG_CAM_DISTORTED ? 29 : KIND == XSG_CAM_FISHEYE ? 25 : 21;
+}
+constexpr int kCamGradMax = 29;
 
 template <int NV>
 XSG_DEV void block_partials(const float (&g)[NV], float* __restrict__ part) {
@@ -251,11 +313,12 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
                                                                  const float* __restrict__ d_ray_o,
                                                                  const float* __restrict__ d_ray_d,
                                                                  float* __restrict__ part) {
+    constexpr int NG = cam_grad_count<KIND>();
     const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     const Camera c = load_camera(pack, KIND);
-    float g[kCamGrad];
+    float g[NG];
 #pragma unroll
-    for (int k = 0; k < kCamGrad; ++k) g[k] = 0.f;
+    for (int k = 0; k < NG; ++k) g[k] = 0.f;
     if (idx < (int64_t)width * height) {  // every thread takes part in the reduction below
         const f2 uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
         const f3 r = pixel_to_camera_ray<KIND>(c, uv);
@@ -311,9 +374,68 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
             g[18] = -dr.y * (uv.y - c.i3) * ify * ify;
             g[19] = -dr.x * ifx;
             g[20] = -dr.y * ify;
+        } else if constexpr (KIND == XSG_CAM_DISTORTED) {
+            // distorted_perspective.cu:121-188: re-solve, then at the solution g_d = J^-T dr.xy (J is
+            // symmetric; dr.xy / scale where J is nearly singular) and dL/dk = -g_d . dD/dk
+            const float ifx = 1.0f / c.i0, ify = 1.0f / c.i1;
+            const f2 ud = mk2((uv.x - c.i2) * ifx, (uv.y - c.i3) * ify);
+            DistState st;
+            const f2 uc = undistort_uv(c, ud, st);
+            st = distortion_state(c, uc.x, uc.y);
+            const float det = st.juu * st.jvv - st.juv * st.juv;
+            float gx, gy;
+            if (fabsf(det) <= kDistMinDet) {
+                gx = dr.x / st.scale; gy = dr.y / st.scale;
+            } else {
+                gx = (st.jvv * dr.x - st.juv * dr.y) / det;
+                gy = (st.juu * dr.y - st.juv * dr.x) / det;
+            }
+            g[17] = -gx * ud.x * ifx;
+            g[18] = -gy * ud.y * ify;
+            g[19] = -gx * ifx;
+            g[20] = -gy * ify;
+            const float r2 = uc.x * uc.x + uc.y * uc.y, r4 = r2 * r2, r6 = r4 * r2;
+            const float d_rad = -(gx * uc.x + gy * uc.y) / st.denom;
+            const float d_rad_den = -d_rad * st.scale;
+            g[21] = d_rad * r2;
+            g[22] = d_rad * r4;
+            g[23] = -(gx * 2.0f * uc.x * uc.y + gy * (r2 + 2.0f * uc.y * uc.y));
+            g[24] = -(gx * (r2 + 2.0f * uc.x * uc.x) + gy * 2.0f * uc.x * uc.y);
+            g[25] = d_rad * r6;
+            g[26] = d_rad_den * r2;
+            g[27] = d_rad_den * r4;
+            g[28] = d_rad_den * r6;
+        } else if constexpr (KIND == XSG_CAM_FISHEYE) {
+            // fisheye_opencv.cu:74-136: theta(delta, k) implicit through theta_d(theta, k) = delta
+            const float x = (uv.x - c.i2) / c.i0, y = (uv.y - c.i3) / c.i1;
+            const float delta = sqrtf(x * x + y * y);
+            float residual;
+            const float th = fisheye_solve_theta(c, delta, residual);
+            const float deriv = fisheye_distortion_deriv(c, th);
+            if (th > 0.0f && delta > 1e-8f && fabsf(residual) < 1e-5f && deriv > 1e-3f) {
+                float st, ct;
+                sincosf(th, &st, &ct);
+                const float inv_delta = 1.0f / delta;
+                const float sf = st * inv_delta;
+                const float d_s = dr.x * x + dr.y * y;
+                const float d_th = d_s * ct * inv_delta - dr.z * st;
+                const float dts = d_th / deriv;
+                const float t2 = th * th, t3 = t2 * th;
+                g[21] = -dts * t3;
+                g[22] = -dts * t3 * t2;
+                g[23] = -dts * t3 * t2 * t2;
+                g[24] = -dts * t3 * t2 * t2 * t2;
+                const float d_delta = -d_s * st * inv_delta * inv_delta + dts;
+                const float gx = sf * dr.x + d_delta * x * inv_delta;
+                const float gy = sf * dr.y + d_delta * y * inv_delta;
+                g[17] = -gx * x / c.i0;
+                g[18] = -gy * y / c.i1;
+                g[19] = -gx / c.i0;
+                g[20] = -gy / c.i1;
+            }
         }  // the spherical and lidar models carry no intrinsics gradient (base_camera_impl.h:19-22)
     }
-    block_partials<kCamGrad>(g, part);
+    block_partials<NG>(g, part);
 }
 
 // pixel_time[_delta][_from_uv]_bwd_kernel (time_kernels.h:123-330): partial sums of g u, g v and g;
@@ -340,19 +462,20 @@ __global__ __launch_bounds__(kBlock) void pixel_time_bwd_kernel(const float* __r
     block_partials<3>(g, part);
 }
 
-// one workgroup: out[k] = sum over blocks of part[b][k] for the nv partial values, placed at the pack
-// positions: rays (nv = kCamGrad) at 0..20; times (nv = 3) at rolling_time, trigger_time and, for
-// the delta variants, -trigger at pose_time; every other pack element 0.
-__global__ __launch_bounds__(kBlock) void grad_final_kernel(const float* __restrict__ part, int nb, int nv, int delta,
-                                                            int pack_elems, float* __restrict__ out) {
+// one workgroup: out[e] = sum over blocks of part[b][k] for the nv partial values, placed at the pack
+// positions: rays (`rays`) with k = e for the first nv elements; times (nv = 3) at rolling_time,
+// trigger_time and, for the delta variants, minus the trigger sum at pose_time; every other pack
+// element 0.
+__global__ __launch_bounds__(kBlock) void grad_final_kernel(const float* __restrict__ part, int nb, int nv, int rays,
+                                                            int delta, int pack_elems, float* __restrict__ out) {
     const int wave = threadIdx.x >> 6, lane = __lane_id();
     for (int e = wave; e < pack_elems; e += kBlock / 64) {
-        const int k = (nv == kCamGrad) ? e : (e == 13 ? 0 : e == 14 ? 1 : (e == 15 || (e == 16 && delta)) ? 2 : -1);
+        const int k = rays ? e : (e == 13 ? 0 : e == 14 ? 1 : (e == 15 || (e == 16 && delta)) ? 2 : -1);
         float t = 0.f;
         if (k >= 0 && k < nv)
             for (int b = lane; b < nb; b += 64) t += part[(int64_t)b * nv + k];
         t = wave_sum(t);
-        if (lane == 0) out[e] = (nv != kCamGrad && delta && e == 16) ? -t : t;
+        if (lane == 0) out[e] = (!rays && delta && e == 16) ? -t : t;
     }
 }
 
@@ -378,34 +501,33 @@ extern "C" int xsg_ut_project(int kind, int phm, const float* pack, int64_t n, c
                               float max_margin, uint8_t* flags, float* radii, float* means2d,
                               float* depths, xsg_stream_t stream) {
     if (n < 0 || !pack) return xsg_fail(XSG_ERR_INVALID, "xsg_ut_project: bad arguments");
+    if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
+    if (phm && kind != XSG_CAM_SPHERICAL && kind != XSG_CAM_LIDAR)
+        return xsg_fail(XSG_ERR_UNSUPPORTED, "projection_utgs_phm needs a spherical or lidar camera");
     if (n == 0) return XSG_OK;
     if (!means || !scales || !quats || !flags || !radii || !means2d || !depths)
         return xsg_fail(XSG_ERR_INVALID, "xsg_ut_project: null tensor");
-    if (phm && kind == XSG_CAM_PINHOLE)
-        return xsg_fail(XSG_ERR_UNSUPPORTED, "projection_utgs_phm needs a spherical or lidar camera");
     const ProjParams pp{residual_thr, max_residual, max_margin};
     const UtWeights ut = ut_weights(ut_alpha, ut_beta, ut_kappa);
     const f2 img = mk2(width, height);
     const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const hipStream_t s = (hipStream_t)stream;
     auto q4 = reinterpret_cast<const float4*>(quats);
     auto r2 = reinterpret_cast<float2*>(radii);
     auto m2 = reinterpret_cast<float2*>(means2d);
-#define XSG_UT_ARGS n, pack, pp, ut, img, means, velocity, scales, q4, opacity, flags, r2, m2, depths
-    switch (kind) {
-        case XSG_CAM_PINHOLE:
-            ut_project_kernel<XSG_CAM_PINHOLE><<<grid, block, 0, (hipStream_t)stream>>>(XSG_UT_ARGS);
-            break;
-        case XSG_CAM_SPHERICAL:
-            if (phm) ut_project_phm_kernel<XSG_CAM_SPHERICAL><<<grid, block, 0, (hipStream_t)stream>>>(XSG_UT_ARGS);
-            else ut_project_kernel<XSG_CAM_SPHERICAL><<<grid, block, 0, (hipStream_t)stream>>>(XSG_UT_ARGS);
-            break;
-        case XSG_CAM_LIDAR:
-            if (phm) ut_project_phm_kernel<XSG_CAM_LIDAR><<<grid, block, 0, (hipStream_t)stream>>>(XSG_UT_ARGS);
-            else ut_project_kernel<XSG_CAM_LIDAR><<<grid, block, 0, (hipStream_t)stream>>>(XSG_UT_ARGS);
-            break;
-        default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
-    }
-#undef XSG_UT_ARGS
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        constexpr int KIND = decltype(k)::value;
+        if constexpr (KIND == XSG_CAM_SPHERICAL || KIND == XSG_CAM_LIDAR) {
+            if (phm) {
+                ut_project_phm_kernel<KIND><<<grid, block, 0, s>>>(n, pack, pp, ut, img, means, velocity, scales, q4,
+                                                                   opacity, flags, r2, m2, depths);
+                return;
+            }
+        }
+        ut_project_kernel<KIND><<<grid, block, 0, s>>>(n, pack, pp, ut, img, means, velocity, scales, q4, opacity,
+                                                       flags, r2, m2, depths);
+    });
+    if (rc != XSG_OK) return rc;
     XSG_TRY_LAUNCH("ut_project");
     return XSG_OK;
 }
@@ -415,25 +537,17 @@ extern "C" int xsg_project_points(int kind, const float* pack, int64_t n, const 
                                   float max_margin, int mode, int no_jacobian, float* uvdt,
                                   uint8_t* mask, xsg_stream_t stream) {
     if (n < 0 || !pack) return xsg_fail(XSG_ERR_INVALID, "xsg_project_points: bad arguments");
+    if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
     if (n == 0) return XSG_OK;
     const ProjParams pp{residual_thr, max_residual, max_margin};
     const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const hipStream_t s = (hipStream_t)stream;
     auto u4 = reinterpret_cast<float4*>(uvdt);
-    switch (kind) {
-        case XSG_CAM_PINHOLE:
-            project_points_kernel<XSG_CAM_PINHOLE><<<grid, block, 0, (hipStream_t)stream>>>(
-                n, pack, pp, mode, no_jacobian, points, velocity, u4, mask);
-            break;
-        case XSG_CAM_SPHERICAL:
-            project_points_kernel<XSG_CAM_SPHERICAL><<<grid, block, 0, (hipStream_t)stream>>>(
-                n, pack, pp, mode, no_jacobian, points, velocity, u4, mask);
-            break;
-        case XSG_CAM_LIDAR:
-            project_points_kernel<XSG_CAM_LIDAR><<<grid, block, 0, (hipStream_t)stream>>>(
-                n, pack, pp, mode, no_jacobian, points, velocity, u4, mask);
-            break;
-        default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
-    }
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        project_points_kernel<decltype(k)::value><<<grid, block, 0, s>>>(n, pack, pp, mode, no_jacobian, points,
+                                                                         velocity, u4, mask);
+    });
+    if (rc != XSG_OK) return rc;
     XSG_TRY_LAUNCH("project_points");
     return XSG_OK;
 }
@@ -443,24 +557,16 @@ extern "C" int xsg_camera_rays(int kind, const float* pack, int width, int heigh
                                xsg_stream_t stream) {
     if (width < 0 || height < 0 || !pack || !ray_d)
         return xsg_fail(XSG_ERR_INVALID, "xsg_camera_rays: bad arguments");
+    if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
     const int64_t n = (int64_t)width * height;
     if (n == 0) return XSG_OK;
     const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
-    switch (kind) {
-        case XSG_CAM_PINHOLE:
-            camera_rays_kernel<XSG_CAM_PINHOLE><<<grid, block, 0, (hipStream_t)stream>>>(
-                pack, width, height, world_space, normalized, ray_o, ray_d, valid);
-            break;
-        case XSG_CAM_SPHERICAL:
-            camera_rays_kernel<XSG_CAM_SPHERICAL><<<grid, block, 0, (hipStream_t)stream>>>(
-                pack, width, height, world_space, normalized, ray_o, ray_d, valid);
-            break;
-        case XSG_CAM_LIDAR:
-            camera_rays_kernel<XSG_CAM_LIDAR><<<grid, block, 0, (hipStream_t)stream>>>(
-                pack, width, height, world_space, normalized, ray_o, ray_d, valid);
-            break;
-        default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
-    }
+    const hipStream_t s = (hipStream_t)stream;
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        camera_rays_kernel<decltype(k)::value><<<grid, block, 0, s>>>(pack, width, height, world_space, normalized,
+                                                                      ray_o, ray_d, valid);
+    });
+    if (rc != XSG_OK) return rc;
     XSG_TRY_LAUNCH("camera_rays");
     return XSG_OK;
 }
@@ -469,35 +575,47 @@ extern "C" int xsg_pixel_time(int kind, const float* pack, int width, int height
                               int64_t n_uv, int delta, float* out, xsg_stream_t stream) {
     const int64_t n = uv ? n_uv : (int64_t)width * height;
     if (n < 0 || !pack || !out) return xsg_fail(XSG_ERR_INVALID, "xsg_pixel_time: bad arguments");
+    if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
     if (n == 0) return XSG_OK;
     const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const hipStream_t s = (hipStream_t)stream;
     auto uv2 = reinterpret_cast<const float2*>(uv);
-    switch (kind) {
-        case XSG_CAM_PINHOLE:
-            pixel_time_kernel<XSG_CAM_PINHOLE><<<grid, block, 0, (hipStream_t)stream>>>(pack, width, height, uv2, n, delta, out);
-            break;
-        case XSG_CAM_SPHERICAL:
-            pixel_time_kernel<XSG_CAM_SPHERICAL><<<grid, block, 0, (hipStream_t)stream>>>(pack, width, height, uv2, n, delta, out);
-            break;
-        case XSG_CAM_LIDAR:
-            pixel_time_kernel<XSG_CAM_LIDAR><<<grid, block, 0, (hipStream_t)stream>>>(pack, width, height, uv2, n, delta, out);
-            break;
-        default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
-    }
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        pixel_time_kernel<decltype(k)::value><<<grid, block, 0, s>>>(pack, width, height, uv2, n, delta, out);
+    });
+    if (rc != XSG_OK) return rc;
     XSG_TRY_LAUNCH("pixel_time");
+    return XSG_OK;
+}
+
+extern "C" int xsg_undistort_map(int kind, const float* pack, int width, int height, int normalized_range,
+                                 float* out, xsg_stream_t stream) {
+    if (kind != XSG_CAM_DISTORTED && kind != XSG_CAM_FISHEYE)
+        return xsg_fail(XSG_ERR_INVALID, "undistort_map needs a distorted perspective or fisheye camera");
+    if (width < 0 || height < 0 || !pack || !out) return xsg_fail(XSG_ERR_INVALID, "xsg_undistort_map: bad arguments");
+    const int64_t n = (int64_t)width * height;
+    if (n == 0) return XSG_OK;
+    const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const hipStream_t s = (hipStream_t)stream;
+    auto o2 = reinterpret_cast<float2*>(out);
+    if (kind == XSG_CAM_DISTORTED)
+        undistort_map_kernel<XSG_CAM_DISTORTED><<<grid, block, 0, s>>>(pack, width, height, normalized_range, o2);
+    else
+        undistort_map_kernel<XSG_CAM_FISHEYE><<<grid, block, 0, s>>>(pack, width, height, normalized_range, o2);
+    XSG_TRY_LAUNCH("undistort_map");
     return XSG_OK;
 }
 
 extern "C" size_t xsg_camera_rays_bwd_workspace_bytes(int width, int height) {
     const int64_t n = (int64_t)(width > 0 ? width : 0) * (height > 0 ? height : 0);
-    return sizeof(float) * (size_t)kCamGrad * xsg_blocks(n > 0 ? n : 1, kBlock);
+    return sizeof(float) * (size_t)kCamGradMax * xsg_blocks(n > 0 ? n : 1, kBlock);
 }
 
 extern "C" int xsg_camera_rays_bwd(int kind, const float* pack, int width, int height, int world_space,
                                    int normalized, const float* d_ray_o, const float* d_ray_d, float* grad_pack,
                                    void* workspace, xsg_stream_t stream) {
     const int pe = xsg_camera_pack_elements(kind);
-    if (pe <= 0) return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
+    if (pe <= 0) return XSG_ERR_INVALID;
     if (width < 0 || height < 0) return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: negative size");
     if (!pack || !grad_pack || !workspace || (!d_ray_d && (int64_t)width * height > 0))
         return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: null pointer");
@@ -505,21 +623,15 @@ extern "C" int xsg_camera_rays_bwd(int kind, const float* pack, int width, int h
     const unsigned nb = xsg_blocks(n > 0 ? n : 1, kBlock);
     float* part = (float*)workspace;
     const hipStream_t s = (hipStream_t)stream;
-    switch (kind) {
-        case XSG_CAM_PINHOLE:
-            camera_rays_bwd_kernel<XSG_CAM_PINHOLE><<<nb, kBlock, 0, s>>>(pack, width, height, world_space,
-                                                                          normalized, d_ray_o, d_ray_d, part);
-            break;
-        case XSG_CAM_SPHERICAL:
-            camera_rays_bwd_kernel<XSG_CAM_SPHERICAL><<<nb, kBlock, 0, s>>>(pack, width, height, world_space,
-                                                                            normalized, d_ray_o, d_ray_d, part);
-            break;
-        default:
-            camera_rays_bwd_kernel<XSG_CAM_LIDAR><<<nb, kBlock, 0, s>>>(pack, width, height, world_space,
-                                                                        normalized, d_ray_o, d_ray_d, part);
-            break;
-    }
-    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, kCamGrad, 0, pe, grad_pack);
+    int ng = 0;
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        constexpr int KIND = decltype(k)::value;
+        ng = cam_grad_count<KIND>();
+        camera_rays_bwd_kernel<KIND><<<nb, kBlock, 0, s>>>(pack, width, height, world_space, normalized, d_ray_o,
+                                                           d_ray_d, part);
+    });
+    if (rc != XSG_OK) return rc;
+    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, ng, 1, 0, pe, grad_pack);
     XSG_TRY_LAUNCH("camera_rays_bwd");
     return XSG_OK;
 }
@@ -532,7 +644,7 @@ extern "C" int xsg_pixel_time_bwd(int kind, const float* pack, int width, int he
                                   int64_t n_uv, int delta, const float* grad, float* grad_pack, float* d_uv,
                                   void* workspace, xsg_stream_t stream) {
     const int pe = xsg_camera_pack_elements(kind);
-    if (pe <= 0) return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
+    if (pe <= 0) return XSG_ERR_INVALID;
     const int64_t n = uv ? n_uv : (int64_t)width * height;
     if (n < 0 || (!uv && (width < 0 || height < 0))) return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: bad size");
     if (!pack || !grad_pack || !workspace || (n > 0 && !grad))
@@ -542,19 +654,12 @@ extern "C" int xsg_pixel_time_bwd(int kind, const float* pack, int width, int he
     const hipStream_t s = (hipStream_t)stream;
     const float2* uv2 = (const float2*)uv;
     float2* duv2 = uv ? (float2*)d_uv : nullptr;
-    switch (kind) {
-        case XSG_CAM_PINHOLE:
-            pixel_time_bwd_kernel<XSG_CAM_PINHOLE><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2, part);
-            break;
-        case XSG_CAM_SPHERICAL:
-            pixel_time_bwd_kernel<XSG_CAM_SPHERICAL><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2,
-                                                                           part);
-            break;
-        default:
-            pixel_time_bwd_kernel<XSG_CAM_LIDAR><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2, part);
-            break;
-    }
-    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, 3, delta ? 1 : 0, pe, grad_pack);
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        pixel_time_bwd_kernel<decltype(k)::value><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2,
+                                                                        part);
+    });
+    if (rc != XSG_OK) return rc;
+    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, 3, 0, delta ? 1 : 0, pe, grad_pack);
     XSG_TRY_LAUNCH("pixel_time_bwd");
     return XSG_OK;
 }

@@ -34,6 +34,8 @@ extern "C" int xsg_camera_pack_elements(int kind) {
         case XSG_CAM_PINHOLE:
         case XSG_CAM_SPHERICAL: return 21;
         case XSG_CAM_LIDAR: return 23;
+        case XSG_CAM_DISTORTED: return 30;
+        case XSG_CAM_FISHEYE: return 25;
         default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
     }
 }

@@ -644,6 +644,16 @@ Tensor pixel_time_uv(const CamSpec& spec, const Tensor& pack, const Tensor& uv, 
     return PixelTimeUvFn::apply(pack, uv, (int64_t)spec.kind, delta);
 }
 
+// undistort_map (include/cameras/distortion.h:33-56)
+Tensor undistort_map(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool normalized_range) {
+    validate_pack(spec, pack);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+    Tensor out = at::empty({height, width, 2}, pack.options());
+    check_rc(xsg_undistort_map(spec.kind, fptr(pack), (int)width, (int)height, normalized_range ? 1 : 0,
+                               out.data_ptr<float>(), stream_of(pack)));
+    return out;
+}
+
 std::tuple<Tensor, Tensor> projection(const CamSpec& spec, bool no_jac, const Tensor& pack, const Tensor& points,
                                       const OptT& points_velocity, double thr, double max_res, double margin,
                                       int mode) {
@@ -690,19 +700,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> projection_utgs(const CamSpec& spec, 
 template <int I>
 struct CameraTag {};
 
+// pybind_camera (include/cameras/bind.h:20-126): the same static methods, projection_utgs_phm for
+// the phase-modelled (spherical, lidar) cameras and undistort_map for the models with distort_uv.
 template <int I>
-void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm, bool available) {
+void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm) {
     auto cls = py::class_<CameraTag<I>>(m, name);
-    if (!available) {
-        auto missing = [name](py::args, py::kwargs) -> py::object {
-            throw std::runtime_error(std::string(name) + " is not provided by this build of xsimgs_amd");
-        };
-        for (const char* meth : {"pack", "camera_rays", "pixel_time", "pixel_time_delta", "pixel_time_from_uv",
-                                 "pixel_time_delta_from_uv", "projection", "projection_nojac", "projection_utgs",
-                                 "undistort_map"})
-            cls.def_static(meth, missing);
-        return;
-    }
     cls.def_static("pack", [spec](const std::vector<Tensor>& tensors) { return camera_pack(spec, tensors); },
                    py::arg("tensors"));
     cls.def_static("camera_rays",
@@ -748,6 +750,13 @@ void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm, bool a
                        py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f, py::arg("ut_kappa") = 0.0f,
                        py::arg("residual_thr_early_stop") = 1e-4f, py::arg("max_residual") = 0.002f,
                        py::arg("max_margin") = 1.0f);
+    }
+    if (spec.kind == XSG_CAM_DISTORTED || spec.kind == XSG_CAM_FISHEYE) {
+        cls.def_static("undistort_map",
+                       [spec](const Tensor& pack, int64_t width, int64_t height, bool normalized_range) {
+                           return undistort_map(spec, pack, width, height, normalized_range);
+                       },
+                       py::arg("pack"), py::arg("width"), py::arg("height"), py::arg("normalized_range") = false);
     }
 }
 
@@ -821,9 +830,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "ProjectionMode", py::dict(py::arg("Central") = (int)XSG_MODE_CENTRAL,
                                    py::arg("NegativeDelta") = (int)XSG_MODE_NEGATIVE,
                                    py::arg("PositiveDelta") = (int)XSG_MODE_POSITIVE));
-    bind_camera<0>(m, "PerspectiveCamera", CamSpec{XSG_CAM_PINHOLE, {4}}, false, true);
-    bind_camera<1>(m, "SphericalCamera", CamSpec{XSG_CAM_SPHERICAL, {4}}, true, true);
-    bind_camera<2>(m, "LidarCamera", CamSpec{XSG_CAM_LIDAR, {4, 2}}, true, true);
-    bind_camera<3>(m, "DistortedPerspectiveCamera", CamSpec{-1, {}}, false, false);
-    bind_camera<4>(m, "OpenCVFisheyeCamera", CamSpec{-1, {}}, false, false);
+    bind_camera<0>(m, "PerspectiveCamera", CamSpec{XSG_CAM_PINHOLE, {4}}, false);
+    bind_camera<1>(m, "SphericalCamera", CamSpec{XSG_CAM_SPHERICAL, {4}}, true);
+    bind_camera<2>(m, "LidarCamera", CamSpec{XSG_CAM_LIDAR, {4, 2}}, true);
+    bind_camera<3>(m, "DistortedPerspectiveCamera", CamSpec{XSG_CAM_DISTORTED, {4, 8, 1}}, false);
+    bind_camera<4>(m, "OpenCVFisheyeCamera", CamSpec{XSG_CAM_FISHEYE, {4, 4}}, false);
 }

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
+#include <type_traits>
 
 #include "../../include/xsimgs_amd.h"
 
@@ -11,6 +12,19 @@
 
 // Error reporting shared by every C-ABI entry point (defined in capi.hip).
 int xsg_fail(int code, const char* fmt, ...);
+
+// Host-side dispatch over the camera models: calls f(std::integral_constant<int, KIND>{}).
+template <typename F>
+int xsg_with_camera_kind(int kind, F&& f) {
+    switch (kind) {
+        case XSG_CAM_PINHOLE: f(std::integral_constant<int, XSG_CAM_PINHOLE>{}); return XSG_OK;
+        case XSG_CAM_SPHERICAL: f(std::integral_constant<int, XSG_CAM_SPHERICAL>{}); return XSG_OK;
+        case XSG_CAM_LIDAR: f(std::integral_constant<int, XSG_CAM_LIDAR>{}); return XSG_OK;
+        case XSG_CAM_DISTORTED: f(std::integral_constant<int, XSG_CAM_DISTORTED>{}); return XSG_OK;
+        case XSG_CAM_FISHEYE: f(std::integral_constant<int, XSG_CAM_FISHEYE>{}); return XSG_OK;
+        default: return xsg_fail(XSG_ERR_INVALID, "unknown camera kind %d", kind);
+    }
+}
 int xsg_launch_status(const char* what);
 
 #define XSG_TRY_LAUNCH(what)                                  \
@@ -45,8 +59,11 @@ XSG_DEV void st3(float* p, f3 v) { p[0] = v.x; p[1] = v.y; p[2] = v.z; }
 // Camera pack. Flat float layout (elements):
 //   [0..3] q0 (w,x,y,z) camera-to-world   [4..6] t0   [7..9] v   [10..12] w
 //   [13..14] rolling duration (u, v)  [15] trigger time  [16] pose time
-//   [17..20] impl: pinhole f.x f.y c.x c.y | spherical phi_min phi_range theta_min theta_range
-//   [21..22] lidar only: device address of beam_v (two 32-bit words, low first)
+//   [17..20] impl: pinhole, distorted, fisheye f.x f.y c.x c.y |
+//            spherical, lidar phi_min phi_range theta_min theta_range
+//   [21..22] lidar: device address of beam_v (two 32-bit words, low first)
+//   [21..28] distorted: k1 k2 p1 p2 k3 k4 k5 k6, [29] max_radius^2
+//   [21..24] fisheye: k1 k2 k3 k4
 // Mirrors Camera<Impl> (reference include/cameras/camera.h:67-79) field by field.
 // --------------------------------------------------------------------------
 struct Camera {
@@ -56,6 +73,8 @@ struct Camera {
     float trigger_time, pose_time;
     float i0, i1, i2, i3;
     const float* beam_v;
+    float k[8];   // distortion coefficients (distorted: k1 k2 p1 p2 k3 k4 k5 k6; fisheye: k1..k4)
+    float max_r2; // distorted: largest squared camera-space radius that projects
 };
 
 XSG_DEV Camera load_camera(const float* __restrict__ p, int kind) {
@@ -68,11 +87,118 @@ XSG_DEV Camera load_camera(const float* __restrict__ p, int kind) {
     c.trigger_time = p[15]; c.pose_time = p[16];
     c.i0 = p[17]; c.i1 = p[18]; c.i2 = p[19]; c.i3 = p[20];
     c.beam_v = nullptr;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c.k[i] = 0.f;
+    c.max_r2 = 0.f;
     if (kind == XSG_CAM_LIDAR) {
         const uint32_t lo = __float_as_uint(p[21]), hi = __float_as_uint(p[22]);
         c.beam_v = reinterpret_cast<const float*>(((uint64_t)hi << 32) | lo);
+    } else if (kind == XSG_CAM_DISTORTED) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c.k[i] = p[21 + i];
+        c.max_r2 = p[29];
+    } else if (kind == XSG_CAM_FISHEYE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c.k[i] = p[21 + i];
     }
     return c;
+}
+
+// --------------------------------------------------------------------------
+// Distorted perspective (OpenCV rational radial + tangential) and OpenCV fisheye models
+// (reference csrc/cameras/distorted_perspective.cu, fisheye_opencv.cu, include/cameras/distortion.h)
+// --------------------------------------------------------------------------
+constexpr float kDistMinDet = 1e-3f;  // distorted_perspective.cu:9
+
+// uv_distortion (distortion.h:8-30): radial scale and tangential offset at a camera-space uv
+XSG_DEV void uv_distortion(const Camera& c, float u, float v, float& scale, float& du, float& dv) {
+    const float uu = u * u, vv = v * v;
+    const float r2 = uu + vv;
+    const float num = 1.0f + r2 * (c.k[0] + r2 * (c.k[1] + r2 * c.k[4]));
+    const float den = 1.0f + r2 * (c.k[5] + r2 * (c.k[6] + r2 * c.k[7]));
+    scale = num / den;
+    const float uv2 = 2.0f * u * v;
+    du = c.k[2] * uv2 + c.k[3] * (r2 + 2.0f * uu);
+    dv = c.k[2] * (r2 + 2.0f * vv) + c.k[3] * uv2;
+}
+
+// DistortionState (distorted_perspective.cu:11-36, 44-78): distortion at uv and its symmetric Jacobian
+struct DistState { float scale, denom, dx, dy, juu, juv, jvv; };
+
+XSG_DEV DistState distortion_state(const Camera& c, float u, float v) {
+    const float k1 = c.k[0], k2 = c.k[1], p1 = c.k[2], p2 = c.k[3];
+    const float k3 = c.k[4], k4 = c.k[5], k5 = c.k[6], k6 = c.k[7];
+    const float r2 = u * u + v * v;
+    const float num = 1.0f + r2 * (k1 + r2 * (k2 + r2 * k3));
+    const float den = 1.0f + r2 * (k4 + r2 * (k5 + r2 * k6));
+    const float scale = num / den;
+    const float d_num = k1 + r2 * (2.0f * k2 + 3.0f * k3 * r2);
+    const float d_den = k4 + r2 * (2.0f * k5 + 3.0f * k6 * r2);
+    const float d_scale = (d_num * den - num * d_den) / (den * den);
+    DistState s;
+    s.scale = scale;
+    s.denom = den;
+    s.dx = 2.0f * p1 * u * v + p2 * (r2 + 2.0f * u * u);
+    s.dy = p1 * (r2 + 2.0f * v * v) + 2.0f * p2 * u * v;
+    s.juu = scale + 2.0f * u * u * d_scale + 2.0f * p1 * v + 6.0f * p2 * u;
+    s.juv = 2.0f * u * v * d_scale + 2.0f * p1 * u + 2.0f * p2 * v;
+    s.jvv = scale + 2.0f * v * v * d_scale + 6.0f * p1 * v + 2.0f * p2 * u;
+    return s;
+}
+
+// undistort_uv (distorted_perspective.cu:80-98): five Newton steps on uv * scale + delta = ud, a
+// fixed-point step where the Jacobian is nearly singular; `st` keeps the last step's state (taken
+// before that step's update)
+XSG_DEV f2 undistort_uv(const Camera& c, f2 ud, DistState& st) {
+    f2 uv = ud;
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        st = distortion_state(c, uv.x, uv.y);
+        const float rx = uv.x * st.scale + st.dx - ud.x;
+        const float ry = uv.y * st.scale + st.dy - ud.y;
+        const float det = st.juu * st.jvv - st.juv * st.juv;
+        if (fabsf(det) > kDistMinDet) {
+            uv.x -= (st.jvv * rx - st.juv * ry) / det;
+            uv.y -= (st.juu * ry - st.juv * rx) / det;
+        } else {
+            uv.x = (ud.x - st.dx) / st.scale;
+            uv.y = (ud.y - st.dy) / st.scale;
+        }
+    }
+    return uv;
+}
+
+// Kannala-Brandt polynomial theta_d(theta) and its derivative (fisheye_opencv.cu:14-32)
+XSG_DEV float fisheye_distortion(const Camera& c, float th) {
+    const float t2 = th * th;
+    float d = t2 * c.k[3] + c.k[2];
+    d = t2 * d + c.k[1];
+    d = t2 * d + c.k[0];
+    d = t2 * d + 1.0f;
+    return th * d;
+}
+
+XSG_DEV float fisheye_distortion_deriv(const Camera& c, float th) {
+    const float t2 = th * th;
+    float d = t2 * 9.0f * c.k[3] + 7.0f * c.k[2];
+    d = t2 * d + 5.0f * c.k[1];
+    d = t2 * d + 3.0f * c.k[0];
+    d = t2 * d + 1.0f;
+    return d;
+}
+
+// solve_theta (fisheye_opencv.cu:34-46): at most 20 Newton steps, derivative clamped at 0.1,
+// theta kept in [0, pi]
+XSG_DEV float fisheye_solve_theta(const Camera& c, float delta, float& residual) {
+    float th = delta;
+    residual = 0.0f;
+    for (int i = 0; i < 20; ++i) {
+        residual = fisheye_distortion(c, th) - delta;
+        th -= residual / fmaxf(fisheye_distortion_deriv(c, th), 0.1f);
+        th = fminf(fmaxf(th, 0.0f), float(M_PI));
+        if (fabsf(residual) < 1e-6f) break;
+    }
+    return th;
 }
 
 XSG_DEV float pixel_time(const Camera& c, float u, float v) {  // camera.h:89-91
@@ -142,10 +268,30 @@ XSG_DEV f2 angles_to_uv(const Camera& c, int mode, float phi, float theta) {
     return mk2(u, v);
 }
 
+// Camera models with a projection Jacobian take Newton steps on the pixel time; the others the
+// fixed-point step (projection_kernels.h:116-198, selected at :224-236)
+template <int KIND>
+constexpr bool has_projection_jacobian() {
+    return KIND == XSG_CAM_PINHOLE || KIND == XSG_CAM_SPHERICAL || KIND == XSG_CAM_LIDAR;
+}
+
 template <int KIND>
 XSG_DEV f3 point_to_uvd(const Camera& c, int mode, f3 p) {
     if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:36-42
         return mk3(p.x * c.i0 / p.z + c.i2, p.y * c.i1 / p.z + c.i3, p.z);
+    } else if constexpr (KIND == XSG_CAM_DISTORTED) {  // distorted_perspective.cu:190-197
+        const float x = p.x / p.z, y = p.y / p.z;
+        float scale, du, dv;
+        uv_distortion(c, x, y, scale, du, dv);
+        const float r2 = x * x + y * y;
+        return mk3((x * scale + du) * c.i0 + c.i2, (y * scale + dv) * c.i1 + c.i3, (r2 <= c.max_r2) ? p.z : 0.0f);
+    } else if constexpr (KIND == XSG_CAM_FISHEYE) {  // fisheye_opencv.cu:138-148
+        const float norm = fmaxf(1e-6f, hypotf(p.x, p.y));
+        const float th = atan2f(norm, p.z);
+        const bool valid = fisheye_distortion_deriv(c, th) > 0.0f;
+        const float delta = fisheye_distortion(c, th) / norm;
+        const float depth = (valid && (delta > 0.0f)) ? sqrtf(dot(p, p)) : 0.0f;
+        return mk3(c.i0 * delta * p.x + c.i2, c.i1 * delta * p.y + c.i3, depth);
     } else {  // spherical.h:133-142
         const float x2y2 = p.x * p.x + p.y * p.y;
         const float r = sqrtf(x2y2 + p.z * p.z);
@@ -194,24 +340,31 @@ XSG_DEV void camera_projection(const Camera& c, f3 pw, f3 pv, const ProjParams& 
     float residual = 0.0f;
     f3 pc = mk3(0.f, 0.f, 0.f), jpc = mk3(0.f, 0.f, 0.f);
     f2 du_dv = mk2(0.f, 0.f);
+    constexpr bool newton = has_projection_jacobian<KIND>();
     if (is_static) {
         // static pose: world_to_camera(p, t) == quat_apply(q0.w, -q0.xyz, p - t0) for every t
         f3 r, dr;
         world_to_camera_jac(c, pw, pv, p_time, r, dr);
         pc = r; jpc = dr;
-        point_to_uvd_jacob<KIND>(c, mode, pc, jpc, uvd, du_dv);
+        if constexpr (newton) point_to_uvd_jacob<KIND>(c, mode, pc, jpc, uvd, du_dv);
+        else uvd = point_to_uvd<KIND>(c, mode, pc);
     }
 #pragma unroll 1
     for (int i = 0; i < 5; ++i) {
         if (!is_static) {
             world_to_camera_jac(c, pw, pv, p_time, pc, jpc);
-            point_to_uvd_jacob<KIND>(c, mode, pc, jpc, uvd, du_dv);
+            if constexpr (newton) point_to_uvd_jacob<KIND>(c, mode, pc, jpc, uvd, du_dv);
+            else uvd = point_to_uvd<KIND>(c, mode, pc);
         }
         const float assumed = c.pose_time + p_time;
         const float real_time = pixel_time(c, uvd.x, uvd.y);
         residual = assumed - real_time;
-        const float d_res = 1.0f - (du_dv.x * c.roll_u + du_dv.y * c.roll_v);
-        p_time -= residual / d_res;
+        if constexpr (newton) {
+            const float d_res = 1.0f - (du_dv.x * c.roll_u + du_dv.y * c.roll_v);
+            p_time -= residual / d_res;
+        } else {
+            p_time -= residual;  // camera_projection_iteration (projection_kernels.h:177-198)
+        }
         if ((uvd.z <= 0.0f) || (uvd.x < -pp.margin) || (uvd.x > 1.0f + pp.margin) ||
             (uvd.y < -pp.margin) || (uvd.y > 1.0f + pp.margin)) {
             valid = false;

@@ -38,6 +38,13 @@ def make_camera(spec, device) -> C.FusedRSCamera:
         return C.PerspectiveCamera(pose, torch.tensor(spec.impl))
     if spec.kind == "spherical":
         return C.SphericalCamera(pose, torch.tensor(spec.impl))
+    if spec.kind == "distorted":
+        cam = C.DistortedPerspectiveCamera(pose, torch.tensor(spec.impl), torch.tensor(spec.dist))
+        if spec.max_radius is not None:
+            cam._max_radius = torch.tensor([float(spec.max_radius)], device=device)
+        return cam
+    if spec.kind == "fisheye":
+        return C.FisheyeCamera(pose, torch.tensor(spec.impl), torch.tensor(spec.dist))
     return C.LidarCamera(pose, torch.tensor(spec.impl), spec.beam_v)
 
 

@@ -30,18 +30,20 @@ import torch
 class CameraSpec:
     """Plain description of one camera, independent of any device."""
 
-    kind: str                      # "pinhole" | "spherical" | "lidar"
+    kind: str                      # "pinhole" | "spherical" | "lidar" | "distorted" | "fisheye"
     width: int
     height: int
     q: list                        # camera-to-world rotation (w, x, y, z)
     t: list                        # camera position in world
-    impl: list                     # pinhole: [fx/W, fy/H, cx/W, cy/H]; spherical: limits
+    impl: list                     # pinhole, distorted, fisheye: [fx/W, fy/H, cx/W, cy/H]; spherical: limits
     v: list = field(default_factory=lambda: [0.0, 0.0, 0.0])
     w: list = field(default_factory=lambda: [0.0, 0.0, 0.0])
     rolling: list = field(default_factory=lambda: [0.0, 0.0])
     trigger_time: float = 0.0
     pose_time: float = 0.0
     beam_v: torch.Tensor | None = None   # lidar only: per-row v values
+    dist: list | None = None       # distorted: k1 k2 p1 p2 k3 k4 k5 k6; fisheye: k1 k2 k3 k4
+    max_radius: float | None = None  # distorted: largest camera-space radius |xy / z| projected
 
 
 @dataclass
