@@ -20,6 +20,10 @@
  *   xsg_sh_fwd / xsg_sh_bwd   spherical_harmonics_fused_{fwd,bwd} csrc/color/sh_fwd.cu:248-259,
  *                             sh_bwd.cu:379-390
  *   xsg_mask_radii[_packed]   mask_radii / mask_radii_packed    csrc/tiling/mask_radii.cu:82-88
+ *   xsg_packed_mask_from_instances
+ *                             packed_mask_from_instances        csrc/nodes/gs_masking.cu:8-47
+ *   xsg_rigid_transform_fwd / _bwd
+ *                             copy_gs_rigid_transform_{fwd,bwd} csrc/nodes/container.cu:13-266
  *   xsg_isect_count + xsg_isect_fill
  *                             isect_regular_tiles / isect_lidar_tiles / isect_spherical_tiles
  *                             regular_tiling.cu:138-146, phm_lidar_tiling.cu:354-375,
@@ -135,6 +139,49 @@ int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, const float*
                const float* coeffs, const uint32_t* mask, int layout_3kn, const float* d_output,
                int has_dc, float* d_coeffs, float* d_coeffs_dc, float* d_positions,
                float* d_origin, void* workspace, xsg_stream_t stream);
+
+/* ------------------------------------------------- scene-assembly producers */
+/* packed_mask_from_instances (gs_masking.cu:8-47): out[(n + 31) / 32], bit i % 32 of word i / 32 set
+ * when instance_ids[i] < 0 or instance_mask[instance_ids[i]] != 0. Ids at or past n_instances count
+ * as enabled (the reference reads past the mask there). */
+int xsg_packed_mask_from_instances(int64_t n, const int32_t* instance_ids, const uint8_t* instance_mask,
+                                   int64_t n_instances, uint32_t* out, xsg_stream_t stream);
+
+/* Gaussians and instances of copy_gs_rigid_transform_{fwd,bwd} (container.cu:13-266). Gaussian i of
+ * instance k = instance_ids[i] goes to row buffer_offset + i, or buffer_offset +
+ * per_instance_offsets[k] + gs_inst_offsets[i] when both offset arrays are given; Gaussians of a
+ * disabled instance (inst_mask[k] == 0), with k outside [0, n_instances) or with a row outside
+ * [0, n_out) are skipped. Quaternions are (w, x, y, z), float4-aligned. */
+typedef struct {
+    int64_t n;              /* Gaussians */
+    int64_t n_instances;
+    int64_t n_out;          /* rows of the output buffers */
+    int64_t buffer_offset;
+    const float* positions;       /* [n, 3] */
+    const float* rotations;       /* [n, 4] */
+    const int32_t* instance_ids;  /* [n] */
+    const float* inst_q;          /* [n_instances, 4] */
+    const float* inst_t;          /* [n_instances, 3] (forward only) */
+    const float* inst_v;          /* [n_instances, 3] (forward only) */
+    const float* inst_w;          /* [n_instances, 3] */
+    const uint8_t* inst_mask;     /* [n_instances] */
+    const int32_t* per_instance_offsets;  /* [n_instances] or NULL */
+    const int32_t* gs_inst_offsets;       /* [n] or NULL */
+} xsg_rigid_desc;
+
+/* out_pos = q_k p + t_k, out_rot = q_k (x) q, out_vel = v_k + w_k x (q_k p), out_mask = 1, written
+ * in place at each Gaussian's row; other rows are left untouched. out_velocities and out_mask may be
+ * NULL. */
+int xsg_rigid_transform_fwd(const xsg_rigid_desc* d, float* out_positions, float* out_rotations,
+                            float* out_velocities, uint8_t* out_mask, xsg_stream_t stream);
+
+/* Gradients of the forward: grad_positions [n, 3] and grad_rotations [n, 4] (zeros for skipped
+ * Gaussians) and the per-instance sums grad_q [n_instances, 4], grad_t, grad_v, grad_w
+ * [n_instances, 3]; every output is written (no zero-fill needed). v_velocities may be NULL (then
+ * grad_v and grad_w are 0). The instance sums use float atomics: their summation order varies. */
+int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_positions, const float* v_rotations,
+                            const float* v_velocities, float* grad_positions, float* grad_rotations,
+                            float* grad_q, float* grad_t, float* grad_v, float* grad_w, xsg_stream_t stream);
 
 /* ------------------------------------------------------------------ binning */
 int xsg_mask_radii(int64_t n, const uint8_t* mask, float* radii, xsg_stream_t stream);

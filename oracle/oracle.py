@@ -431,3 +431,60 @@ def num_threads() -> int:
 
 def set_num_threads(n: int) -> None:
     _lib("f32").orc_set_num_threads(C.c_int(n))
+
+
+# ------------------------------------------------------------------ scene-assembly producers
+def packed_mask_from_instances(instance_ids, instance_mask):
+    """packed_mask_from_instances (csrc/nodes/gs_masking.cu:8-47): uint32[(N + 31) // 32]."""
+    ids = _arr(instance_ids, np.int32).reshape(-1)
+    m = _arr(instance_mask, np.uint8).reshape(-1)
+    out = np.zeros((ids.size + 31) // 32, np.uint32)
+    _lib("f32").orc_packed_mask_from_instances(C.c_long(ids.size), _p(ids), _p(m), C.c_long(m.size), _p(out))
+    return out
+
+
+def _offsets(per_instance_offsets, gs_inst_offsets):
+    if (per_instance_offsets is None) != (gs_inst_offsets is None):
+        raise ValueError("per_instance_offsets and gs_inst_offsets go together")
+    return _arr(per_instance_offsets, np.int32), _arr(gs_inst_offsets, np.int32)
+
+
+def rigid_fwd(positions, rotations, instance_id, inst_q, inst_t, inst_v, inst_w, inst_mask, out_positions,
+              out_rotations, out_velocities=None, out_mask=None, buffer_offset=0, per_instance_offsets=None,
+              gs_inst_offsets=None, prec="f32"):
+    """copy_gs_rigid_transform_fwd (csrc/nodes/container.cu:13-75, 171-215) on copies of the output
+    buffers, which are returned: ``out_positions, out_rotations, out_velocities, out_mask``."""
+    _, nt = _real(prec)
+    pos, rot = _arr(positions, nt), _arr(rotations, nt)
+    ids = _arr(instance_id, np.int32)
+    iq, it, iv, iw = (_arr(x, nt) for x in (inst_q, inst_t, inst_v, inst_w))
+    im = _arr(inst_mask, np.uint8)
+    po, go = _offsets(per_instance_offsets, gs_inst_offsets)
+    op, orot = _arr(out_positions, nt).copy(), _arr(out_rotations, nt).copy()
+    ov = _arr(out_velocities, nt).copy() if out_velocities is not None else None
+    om = _arr(out_mask, np.uint8).copy() if out_mask is not None else None
+    _lib(prec).orc_rigid_fwd(C.c_long(pos.shape[0]), _p(pos), _p(rot), _p(ids), _p(iq), _p(it), _p(iv), _p(iw),
+                             _p(im), C.c_long(im.size), C.c_long(buffer_offset), _p(po), _p(go),
+                             C.c_long(op.shape[0]), _p(op), _p(orot), _p(ov), _p(om))
+    return op, orot, ov, (om.astype(bool) if om is not None else None)
+
+
+def rigid_bwd(positions, rotations, instance_id, inst_q, inst_w, inst_mask, buffer_offset, per_instance_offsets,
+              gs_inst_offsets, v_positions, v_rotations, v_velocities, prec="f32"):
+    """copy_gs_rigid_transform_bwd (csrc/nodes/container.cu:78-160, 218-266): ``grad_positions,
+    grad_rotations, grad_q, grad_t, grad_v, grad_w``."""
+    _, nt = _real(prec)
+    pos, rot = _arr(positions, nt), _arr(rotations, nt)
+    ids = _arr(instance_id, np.int32)
+    iq, iw = _arr(inst_q, nt), _arr(inst_w, nt)
+    im = _arr(inst_mask, np.uint8)
+    po, go = _offsets(per_instance_offsets, gs_inst_offsets)
+    vp, vr = _arr(v_positions, nt), _arr(v_rotations, nt)
+    vv = _arr(v_velocities, nt)
+    n, k = pos.shape[0], iq.shape[0]
+    gp, gr = np.zeros((n, 3), nt), np.zeros((n, 4), nt)
+    gq, gt, gv, gw = np.zeros((k, 4), nt), np.zeros((k, 3), nt), np.zeros((k, 3), nt), np.zeros((k, 3), nt)
+    _lib(prec).orc_rigid_bwd(C.c_long(n), _p(pos), _p(rot), _p(ids), _p(iq), _p(iw), _p(im), C.c_long(k),
+                             C.c_long(buffer_offset), _p(po), _p(go), C.c_long(vp.shape[0]), _p(vp), _p(vr), _p(vv),
+                             _p(gp), _p(gr), _p(gq), _p(gt), _p(gv), _p(gw))
+    return gp, gr, gq, gt, gv, gw

@@ -16,6 +16,9 @@
  *   orc_camera_rays_bwd       fp64 central differences of orc_camera_rays w.r.t. every camera
  *                             parameter (pinhole, spherical, lidar; world / camera space)
  *   orc_pixel_time_bwd        closed form (pixel time is linear in the camera's timing)
+ *   orc_packed_mask_from_instances  numpy packbits (little bit order) of the element mask
+ *   orc_rigid_fwd / _bwd      scipy Rotation for the rotations and products; fp64 central
+ *                             differences of orc_rigid_fwd for the backward
  *   distorted / fisheye       rays -> projection round trip, zero-coefficient limits (pinhole,
  *   models                    equidistant fisheye), the published OpenCV polynomials evaluated
  *                             independently, undistort map = projection of the pinhole ray,
@@ -1529,4 +1532,125 @@ void orc_set_num_threads(int n) {
 #else
     (void)n;
 #endif
+}
+
+/* ------------------------------------------------------------------------- */
+/* Scene-assembly producers: csrc/nodes/gs_masking.cu, csrc/nodes/container.cu */
+/* ------------------------------------------------------------------------- */
+
+/* packed_mask_from_instances (gs_masking.cu:8-47): bit i % 32 of word i / 32 is set when element i
+ * belongs to no instance (id < 0) or its instance is enabled (mask byte non-zero). Ids at or past
+ * n_instances count as enabled (the reference reads past the mask there). */
+void orc_packed_mask_from_instances(long n, const int32_t *ids, const uint8_t *inst_mask, long n_inst,
+                                    uint32_t *out) {
+    const long nw = (n + 31) / 32;
+    for (long w = 0; w < nw; ++w) out[w] = 0;
+    for (long i = 0; i < n; ++i) {
+        const int32_t id = ids[i];
+        const int v = (id < 0 || (long)id >= n_inst) ? 1 : (inst_mask[id] != 0);
+        if (v) out[i / 32] |= (uint32_t)1 << (i % 32);
+    }
+}
+
+/* unit-quaternion (w, x, y, z) rotation p + 2 (w (u x p) + u x (u x p)) and Hamilton product a b */
+static v3 qrot(const real *q, v3 p) { return quat_apply(q[0], V3(q[1], q[2], q[3]), p); }
+
+static void qmul(const real *a, const real *b, real *o) {
+    const v3 av = V3(a[1], a[2], a[3]), bv = V3(b[1], b[2], b[3]);
+    const v3 ov = add3(add3(scl3(bv, a[0]), scl3(av, b[0])), cross3(av, bv));
+    o[0] = a[0] * b[0] - dot3(av, bv);
+    o[1] = ov.x; o[2] = ov.y; o[3] = ov.z;
+}
+
+/* output row of particle i, or -1 when it is skipped: instance out of range or disabled, or a row
+ * outside [0, n_out) (the reference writes there unchecked) */
+static long rigid_row(long i, const int32_t *inst_id, const uint8_t *imask, long n_inst, long buffer_offset,
+                      const int32_t *per_inst_off, const int32_t *gs_inst_off, long n_out, long *id_out) {
+    const uint32_t id = (uint32_t)inst_id[i];
+    if ((long)id >= n_inst || !imask[id]) return -1;
+    const long r = buffer_offset + (gs_inst_off ? (long)(uint32_t)per_inst_off[id] + (long)(uint32_t)gs_inst_off[i] : i);
+    if (r < 0 || r >= n_out) return -1;
+    *id_out = (long)id;
+    return r;
+}
+
+/* copy_gs_rigid_transform_fwd_kernel (container.cu:13-75): out_pos = q_k p + t_k, out_rot = q_k q,
+ * out_vel = v_k + w_k x (q_k p), out_mask = 1 at row buffer_offset + i (or + per_instance_offsets[k]
+ * + gs_inst_offsets[i]); rows of disabled instances are left as they are */
+void orc_rigid_fwd(long n, const real *pos, const real *rot, const int32_t *inst_id, const real *iq, const real *it,
+                   const real *iv, const real *iw, const uint8_t *imask, long n_inst, long buffer_offset,
+                   const int32_t *per_inst_off, const int32_t *gs_inst_off, long n_out, real *out_pos,
+                   real *out_rot, real *out_vel, uint8_t *out_mask) {
+    for (long i = 0; i < n; ++i) {
+        long k;
+        const long r = rigid_row(i, inst_id, imask, n_inst, buffer_offset, per_inst_off, gs_inst_off, n_out, &k);
+        if (r < 0) continue;
+        const v3 pr = qrot(iq + 4 * k, ld3(pos + 3 * i));
+        out_pos[3 * r] = pr.x + it[3 * k]; out_pos[3 * r + 1] = pr.y + it[3 * k + 1];
+        out_pos[3 * r + 2] = pr.z + it[3 * k + 2];
+        qmul(iq + 4 * k, rot + 4 * i, out_rot + 4 * r);
+        if (out_vel) {
+            const v3 vel = add3(ld3(iv + 3 * k), cross3(ld3(iw + 3 * k), pr));
+            out_vel[3 * r] = vel.x; out_vel[3 * r + 1] = vel.y; out_vel[3 * r + 2] = vel.z;
+        }
+        if (out_mask) out_mask[r] = 1;
+    }
+}
+
+/* copy_gs_rigid_transform_bwd_kernel (container.cu:78-160): per-particle gradients (0 for skipped
+ * particles) and per-instance sums (in double); v_vel may be NULL */
+void orc_rigid_bwd(long n, const real *pos, const real *rot, const int32_t *inst_id, const real *iq, const real *iw,
+                   const uint8_t *imask, long n_inst, long buffer_offset, const int32_t *per_inst_off,
+                   const int32_t *gs_inst_off, long n_out, const real *v_pos, const real *v_rot, const real *v_vel,
+                   real *g_pos, real *g_rot, real *g_q, real *g_t, real *g_v, real *g_w) {
+    double *acc = (double *)calloc((size_t)n_inst * 13, sizeof(double));
+    for (long i = 0; i < 3 * n; ++i) g_pos[i] = 0;
+    for (long i = 0; i < 4 * n; ++i) g_rot[i] = 0;
+    for (long i = 0; i < n; ++i) {
+        long k;
+        const long r = rigid_row(i, inst_id, imask, n_inst, buffer_offset, per_inst_off, gs_inst_off, n_out, &k);
+        if (r < 0) continue;
+        const real *q = iq + 4 * k;
+        const v3 u = V3(q[1], q[2], q[3]);
+        const v3 p = ld3(pos + 3 * i);
+        const v3 g = ld3(v_pos + 3 * r);
+        double *a = acc + 13 * k;  /* q(4) t(3) v(3) w(3) */
+        a[4] += g.x; a[5] += g.y; a[6] += g.z;
+        v3 gp = g;  /* gradient at q p */
+        if (v_vel) {
+            const v3 gv = ld3(v_vel + 3 * r);
+            const v3 pr = qrot(q, p);
+            const v3 gw = cross3(pr, gv);
+            a[7] += gv.x; a[8] += gv.y; a[9] += gv.z;
+            a[10] += gw.x; a[11] += gw.y; a[12] += gw.z;
+            gp = add3(gp, cross3(gv, ld3(iw + 3 * k)));
+        }
+        /* y = p + 2 (w (u x p) + u x (u x p)) */
+        const v3 dp = add3(sub3(gp, scl3(cross3(u, gp), K(2.0) * q[0])), scl3(cross3(u, cross3(u, gp)), K(2.0)));
+        const real dw = K(2.0) * dot3(gp, cross3(u, p));
+        const v3 du = add3(add3(scl3(cross3(p, gp), K(2.0) * q[0]), scl3(p, K(2.0) * dot3(gp, u))),
+                           sub3(scl3(gp, K(2.0) * dot3(u, p)), scl3(u, K(4.0) * dot3(gp, p))));
+        g_pos[3 * i] = dp.x; g_pos[3 * i + 1] = dp.y; g_pos[3 * i + 2] = dp.z;
+        /* out_rot = q_k (x) rot: Hamilton product backward */
+        const real *b = rot + 4 * i;
+        const v3 bv = V3(b[1], b[2], b[3]);
+        const real dqw = v_rot[4 * r];
+        const v3 dqv = V3(v_rot[4 * r + 1], v_rot[4 * r + 2], v_rot[4 * r + 3]);
+        const real daw = dqw * b[0] + dot3(dqv, bv);
+        const v3 dav = add3(sub3(scl3(dqv, b[0]), scl3(bv, dqw)), cross3(bv, dqv));
+        const real dbw = dqw * q[0] + dot3(dqv, u);
+        const v3 dbv = add3(sub3(scl3(dqv, q[0]), scl3(u, dqw)), cross3(dqv, u));
+        g_rot[4 * i] = dbw; g_rot[4 * i + 1] = dbv.x; g_rot[4 * i + 2] = dbv.y; g_rot[4 * i + 3] = dbv.z;
+        a[0] += dw + daw; a[1] += du.x + dav.x; a[2] += du.y + dav.y; a[3] += du.z + dav.z;
+    }
+    for (long k = 0; k < n_inst; ++k) {
+        const double *a = acc + 13 * k;
+        for (int j = 0; j < 4; ++j) g_q[4 * k + j] = (real)a[j];
+        for (int j = 0; j < 3; ++j) {
+            g_t[3 * k + j] = (real)a[4 + j];
+            g_v[3 * k + j] = (real)a[7 + j];
+            g_w[3 * k + j] = (real)a[10 + j];
+        }
+    }
+    free(acc);
 }

@@ -24,7 +24,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("XSG_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["capi.hip", "camera.hip", "sh.hip", "tiling.hip", "eval3d_fwd.hip", "eval3d_bwd.hip",
-               "eval3d_capi.hip"]
+               "eval3d_capi.hip", "nodes.hip"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-result"]

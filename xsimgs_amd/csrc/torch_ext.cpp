@@ -468,6 +468,124 @@ std::tuple<Tensor, Tensor> radix_sort_pairs(const Tensor& keys, const Tensor& va
     return sel ? std::make_tuple(k1, v1) : std::make_tuple(k0, v0);
 }
 
+// ------------------------------------------------------------------ scene-assembly producers
+// mask_from_instances (csrc/nodes/gs_masking.cu:29-44)
+Tensor packed_mask_from_instances(const Tensor& instance_ids, const Tensor& instance_mask) {
+    check_same_device({instance_ids, instance_mask});
+    all_contiguous({instance_ids, instance_mask});
+    TORCH_CHECK(instance_ids.scalar_type() == at::kInt, "instance_ids must be int32");
+    TORCH_CHECK(instance_mask.element_size() == 1, "instance_mask must be a bool / uint8 tensor");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(instance_ids.device());
+    const int64_t n = instance_ids.numel();
+    Tensor out = at::empty({(n + 31) / 32}, instance_ids.options().dtype(at::kUInt32));
+    check_rc(xsg_packed_mask_from_instances(n, instance_ids.data_ptr<int32_t>(),
+                                            (const uint8_t*)instance_mask.data_ptr(), instance_mask.numel(),
+                                            (uint32_t*)out.data_ptr(), stream_of(instance_ids)));
+    return out;
+}
+
+xsg_rigid_desc rigid_desc(const Tensor& positions, const Tensor& rotations, const Tensor& instance_id,
+                          const Tensor& inst_q, const OptT& inst_t, const OptT& inst_v, const Tensor& inst_w,
+                          const Tensor& inst_mask, int64_t n_out, int64_t buffer_offset, const OptT& per_inst_off,
+                          const OptT& gs_inst_off) {
+    std::vector<Tensor> ts{positions, rotations, instance_id, inst_q, inst_w, inst_mask};
+    for (const OptT* o : {&inst_t, &inst_v, &per_inst_off, &gs_inst_off})
+        if (o->has_value()) ts.push_back(**o);
+    check_same_device(ts);
+    all_contiguous(ts);
+    for (const Tensor* t : {&positions, &rotations, &inst_q, &inst_w}) check_f32(*t, "positions / quaternions");
+    TORCH_CHECK(instance_id.scalar_type() == at::kInt, "instance_id must be int32");
+    TORCH_CHECK(inst_mask.element_size() == 1, "inst_mask must be a bool / uint8 tensor");
+    TORCH_CHECK(per_inst_off.has_value() == gs_inst_off.has_value(),
+                "per_instance_offsets and gs_inst_offsets go together");
+    if (gs_inst_off.has_value())
+        TORCH_CHECK(per_inst_off->scalar_type() == at::kInt && gs_inst_off->scalar_type() == at::kInt,
+                    "instance offsets must be int32");
+    const int64_t n = positions.size(0), k = inst_q.size(0);
+    TORCH_CHECK(positions.numel() == 3 * n && rotations.numel() == 4 * n && instance_id.numel() == n,
+                "positions [N, 3], rotations [N, 4], instance_id [N]");
+    TORCH_CHECK(inst_q.numel() == 4 * k && inst_w.numel() == 3 * k && inst_mask.numel() == k,
+                "inst_q [K, 4], inst_w [K, 3], inst_mask [K]");
+    if (gs_inst_off.has_value())
+        TORCH_CHECK(per_inst_off->numel() == k && gs_inst_off->numel() == n,
+                    "per_instance_offsets [K], gs_inst_offsets [N]");
+    xsg_rigid_desc d{};
+    d.n = n; d.n_instances = k; d.n_out = n_out; d.buffer_offset = buffer_offset;
+    d.positions = fptr(positions); d.rotations = fptr(rotations); d.instance_ids = instance_id.data_ptr<int32_t>();
+    d.inst_q = fptr(inst_q); d.inst_t = fptr(inst_t); d.inst_v = fptr(inst_v); d.inst_w = fptr(inst_w);
+    d.inst_mask = (const uint8_t*)inst_mask.data_ptr();
+    d.per_instance_offsets = per_inst_off.has_value() ? per_inst_off->data_ptr<int32_t>() : nullptr;
+    d.gs_inst_offsets = gs_inst_off.has_value() ? gs_inst_off->data_ptr<int32_t>() : nullptr;
+    return d;
+}
+
+// copy_gs_rigid_transform_fwd (csrc/nodes/container.cu:171-215): writes the output buffers in place
+void copy_gs_rigid_transform_fwd(const Tensor& positions, const Tensor& rotations, const Tensor& instance_id,
+                                 const Tensor& inst_q, const Tensor& inst_t, const Tensor& inst_v,
+                                 const Tensor& inst_w, const Tensor& inst_mask, const Tensor& out_positions,
+                                 const Tensor& out_rotations, const OptT& out_velocities, const OptT& out_mask,
+                                 int64_t buffer_offset, const OptT& per_instance_offsets,
+                                 const OptT& gs_inst_offsets) {
+    TORCH_CHECK(buffer_offset >= 0, "buffer_offset must be non-negative");
+    const int64_t k = inst_q.size(0);
+    TORCH_CHECK(inst_t.numel() == 3 * k && inst_v.numel() == 3 * k, "inst_t, inst_v [K, 3]");
+    check_f32(inst_t, "inst_t");
+    check_f32(inst_v, "inst_v");
+    xsg_rigid_desc d = rigid_desc(positions, rotations, instance_id, inst_q, inst_t, inst_v, inst_w, inst_mask,
+                                  out_positions.size(0), buffer_offset, per_instance_offsets, gs_inst_offsets);
+    std::vector<Tensor> outs{out_positions, out_rotations};
+    if (out_velocities.has_value()) outs.push_back(*out_velocities);
+    if (out_mask.has_value()) outs.push_back(*out_mask);
+    outs.push_back(positions);
+    check_same_device(outs);
+    all_contiguous(outs);
+    const int64_t b = out_positions.size(0);
+    check_f32(out_positions, "out_positions");
+    check_f32(out_rotations, "out_rotations");
+    TORCH_CHECK(out_positions.numel() == 3 * b && out_rotations.numel() == 4 * b, "out buffers [B, 3], [B, 4]");
+    if (out_velocities.has_value()) {
+        check_f32(*out_velocities, "out_velocities");
+        TORCH_CHECK(out_velocities->numel() == 3 * b, "out_velocities [B, 3]");
+    }
+    if (out_mask.has_value())
+        TORCH_CHECK(out_mask->element_size() == 1 && out_mask->numel() == b, "out_mask: bool [B]");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(positions.device());
+    check_rc(xsg_rigid_transform_fwd(&d, out_positions.data_ptr<float>(), out_rotations.data_ptr<float>(),
+                                     out_velocities.has_value() ? out_velocities->data_ptr<float>() : nullptr,
+                                     out_mask.has_value() ? (uint8_t*)out_mask->data_ptr() : nullptr,
+                                     stream_of(positions)));
+}
+
+// copy_gs_rigid_transform_bwd (csrc/nodes/container.cu:218-266)
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> copy_gs_rigid_transform_bwd(
+    const Tensor& positions, const Tensor& rotations, const Tensor& instance_id, const Tensor& inst_q,
+    const Tensor& inst_w, const Tensor& inst_mask, int64_t buffer_offset, const OptT& per_instance_offsets,
+    const OptT& gs_inst_offsets, const Tensor& v_positions, const Tensor& v_rotations, const OptT& v_velocities) {
+    TORCH_CHECK(buffer_offset >= 0, "buffer_offset must be non-negative");
+    xsg_rigid_desc d = rigid_desc(positions, rotations, instance_id, inst_q, std::nullopt, std::nullopt, inst_w,
+                                  inst_mask, v_positions.size(0), buffer_offset, per_instance_offsets,
+                                  gs_inst_offsets);
+    const int64_t b = v_positions.size(0);
+    Tensor vp = v_positions.contiguous(), vr = v_rotations.contiguous();
+    OptT vv = v_velocities.has_value() ? OptT(v_velocities->contiguous()) : std::nullopt;
+    check_f32(vp, "v_positions");
+    check_f32(vr, "v_rotations");
+    TORCH_CHECK(vp.numel() == 3 * b && vr.numel() == 4 * b, "v_positions [B, 3], v_rotations [B, 4]");
+    if (vv.has_value()) {
+        check_f32(*vv, "v_velocities");
+        TORCH_CHECK(vv->numel() == 3 * b, "v_velocities [B, 3]");
+    }
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(positions.device());
+    Tensor g_pos = at::empty_like(positions), g_rot = at::empty_like(rotations);
+    Tensor g_q = at::empty_like(inst_q), g_t = at::empty_like(inst_w), g_v = at::empty_like(inst_w),
+           g_w = at::empty_like(inst_w);
+    check_rc(xsg_rigid_transform_bwd(&d, vp.data_ptr<float>(), vr.data_ptr<float>(), fptr(vv),
+                                     g_pos.data_ptr<float>(), g_rot.data_ptr<float>(), g_q.data_ptr<float>(),
+                                     g_t.data_ptr<float>(), g_v.data_ptr<float>(), g_w.data_ptr<float>(),
+                                     stream_of(positions)));
+    return {g_pos, g_rot, g_q, g_t, g_v, g_w};
+}
+
 // ------------------------------------------------------------------ cameras
 struct CamSpec {
     int kind;
@@ -820,6 +938,18 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("img_width"), py::arg("img_height"), py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f,
           py::arg("ut_kappa") = 0.0f, py::arg("sort") = true, py::arg("double_buffer") = true);
     m.def("mask_radii_packed", &mask_radii_packed, py::arg("packed_mask"), py::arg("radii"));
+    // scene-assembly producers (csrc/nodes/gs_masking.cu:44-47, container.cu:269-303)
+    m.def("packed_mask_from_instances", &packed_mask_from_instances, py::arg("instance_ids"),
+          py::arg("instance_mask"));
+    m.def("copy_gs_rigid_transform_fwd", &copy_gs_rigid_transform_fwd, py::arg("positions"), py::arg("rotations"),
+          py::arg("instance_id"), py::arg("inst_q"), py::arg("inst_t"), py::arg("inst_v"), py::arg("inst_w"),
+          py::arg("inst_mask"), py::arg("out_positions"), py::arg("out_rotations"), py::arg("out_velocities"),
+          py::arg("out_mask"), py::arg("buffer_offset"), py::arg("per_instance_offsets") = py::none(),
+          py::arg("gs_inst_offsets") = py::none());
+    m.def("copy_gs_rigid_transform_bwd", &copy_gs_rigid_transform_bwd, py::arg("positions"), py::arg("rotations"),
+          py::arg("instance_id"), py::arg("inst_q"), py::arg("inst_w"), py::arg("inst_mask"), py::arg("buffer_offset"),
+          py::arg("per_instance_offsets"), py::arg("gs_inst_offsets"), py::arg("v_positions"),
+          py::arg("v_rotations"), py::arg("v_velocities"));
     m.def("mask_radii", &mask_radii, py::arg("mask"), py::arg("radii"));
     m.def("radix_sort_pairs", &radix_sort_pairs, py::arg("keys"), py::arg("values"), py::arg("begin_bit"),
           py::arg("end_bit"));
