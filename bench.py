@@ -82,6 +82,63 @@ def event_time_ms(fn, reps, torch):
     return s.elapsed_time(e) / reps
 
 
+def extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales, quats, opac, W, H, reps, dev):
+    """Timing of the rows that widen the frame: camera-pose gradients of the frame's rays, rays and UT
+    projection through the distorted perspective and fisheye models, and the packed instance mask and
+    rigid per-instance copy (fwd, bwd) over the frame's Gaussians."""
+    N = means.shape[0]
+    rows = {}
+
+    def row(name, fn, nbytes):
+        with torch.no_grad():
+            t = event_time_ms(fn, reps, torch)
+        gbs = nbytes / (t * 1e-3) / 1e9
+        rows[name] = {"ms": round(t, 4), "alg_bytes": int(nbytes), "GB/s": round(gbs, 1),
+                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    # camera-pose gradients: backward of the frame's rays into the pack (24 B of ray gradients per pixel)
+    cam = st.cams[0]
+    pack = cam.pack.detach().clone().requires_grad_(True)
+    with torch.enable_grad():
+        ro, rd = cam.ext_cls.camera_rays(pack, W, H)
+    gro = torch.randn(H, W, 3, device=dev, generator=g)
+    grd = torch.randn(H, W, 3, device=dev, generator=g)
+
+    def rays_bwd():
+        torch.autograd.grad((ro, rd), pack, (gro, grd), retain_graph=True)
+    with torch.enable_grad():
+        row("camera_rays_bwd", rays_bwd, 24 * W * H)
+    # distorted models on the frame's Gaussians and pixels
+    for kind, impl, dist in (("distorted", [0.66, 1.17, 0.5, 0.5], [-0.28, 0.07, 1e-3, -5e-4, 0.01, 0.02, -0.004,
+                                                                    0.001]),
+                             ("fisheye", [0.3, 0.53, 0.5, 0.5], [0.03, -0.005, 0.001, -0.0001])):
+        spec = synthetic.CameraSpec(kind, W, H, q=cam_spec.q, t=cam_spec.t, impl=impl, dist=dist,
+                                    max_radius=1.5 if kind == "distorted" else None)
+        c = frame.make_camera(spec, dev)
+        row(f"ut_projection_{kind}", lambda c=c: c.ut_gs_projection(means, scales, quats, W, H, opacity=opac),
+            65 * N)
+        row(f"rays_{kind}", lambda c=c: c.camera_rays(W, H), 24 * W * H)
+    # upstream producers: instances of 500 Gaussians, stored instance by instance
+    k = max(1, N // 500)
+    ids = (torch.arange(N, device=dev, dtype=torch.int32) * k // N).contiguous()
+    imask = torch.rand(k, device=dev, generator=g) < 0.9
+    row("packed_mask_from_instances", lambda: _C.packed_mask_from_instances(ids, imask), 4 * N + N // 8)
+    rot = torch.nn.functional.normalize(torch.randn(N, 4, device=dev, generator=g), dim=1)
+    iq = torch.nn.functional.normalize(torch.randn(k, 4, device=dev, generator=g), dim=1)
+    it, iv, iw = (torch.randn(k, 3, device=dev, generator=g) for _ in range(3))
+    outs = [torch.zeros(N, 3, device=dev), torch.zeros(N, 4, device=dev), torch.zeros(N, 3, device=dev),
+            torch.zeros(N, dtype=torch.bool, device=dev)]
+    pos = means.contiguous()
+    row("rigid_transform_fwd", lambda: _C.copy_gs_rigid_transform_fwd(pos, rot, ids, iq, it, iv, iw, imask, *outs, 0),
+        (12 + 16 + 4) * N + (12 + 16 + 12 + 1) * N)
+    vp, vr, vv = (torch.randn_like(o, ) for o in outs[:3])
+    row("rigid_transform_bwd", lambda: _C.copy_gs_rigid_transform_bwd(pos, rot, ids, iq, iw, imask, 0, None, None,
+                                                                      vp, vr, vv),
+        (12 + 16 + 4 + 12 + 16 + 12) * N + (12 + 16) * N)
+    return rows
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -227,6 +284,15 @@ def main():
         gbs = nbytes / (t * 1e-3) / 1e9
         stage_rows[name] = {"ms": round(t, 4), "alg_bytes": int(nbytes), "GB/s": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # ---------------------------------------------------------------- rows beyond the frame
+    # camera gradients, the distorted camera models and the upstream producers, each at the frame's
+    # size (its pixels or its Gaussians), timed alone; algorithmic bytes are what each kernel must
+    # read and write once
+    ext_rows = {}
+    if not args.profile_stages and cam_spec.kind == "pinhole":
+        ext_rows = extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales, quats, opac, W, H,
+                                  args.stage_reps, dev)
+
     # ---------------------------------------------------------------- roofline of the dominant kernel
     flops = {"eval3d_fwd": FLOPS_EVAL * fwd_evaluated + (FLOPS_FWD_CONTRIB + 2 * cdim) * contributing,
              "eval3d_bwd": FLOPS_EVAL * bwd_evaluated + (FLOPS_BWD_CONTRIB + 4 * cdim) * bwd_composited}
@@ -309,6 +375,7 @@ def main():
                    "n_gaussians": N, "width": W, "height": H, "n_cams": n_cams, "tile": [tsx, tsy],
                    "n_isects": n_isects, "visible_gaussians": vis, "parallelism": "single GPU"},
         "stages": stage_rows,
+        "extensions": ext_rows,
         "live_ms": {k: round(v, 4) for k, v in live_ms.items()},
         "pairs": pair_stats,
         "roofline": roofline,

@@ -122,7 +122,7 @@ int xsg_camera_rays_bwd(int kind, const float* pack, int width, int height, int 
 /* Gradient of sum(grad * time) for xsg_pixel_time's output w.r.t. the pack (rolling_time,
  * trigger_time and, with `delta`, pose_time; every other element 0) and, when uv is given and
  * d_uv is not NULL, w.r.t. uv (d_uv[i] = grad[i] * rolling_time). time_kernels.h:123-330. */
-size_t xsg_pixel_time_bwd_workspace_bytes(int64_t n);
+size_t xsg_pixel_time_bwd_workspace_bytes(int width, int height, int64_t n_uv);
 int xsg_pixel_time_bwd(int kind, const float* pack, int width, int height, const float* uv,
                        int64_t n_uv, int delta, const float* grad, float* grad_pack, float* d_uv,
                        void* workspace, xsg_stream_t stream);
@@ -178,10 +178,13 @@ int xsg_rigid_transform_fwd(const xsg_rigid_desc* d, float* out_positions, float
 /* Gradients of the forward: grad_positions [n, 3] and grad_rotations [n, 4] (zeros for skipped
  * Gaussians) and the per-instance sums grad_q [n_instances, 4], grad_t, grad_v, grad_w
  * [n_instances, 3]; every output is written (no zero-fill needed). v_velocities may be NULL (then
- * grad_v and grad_w are 0). The instance sums use float atomics: their summation order varies. */
+ * grad_v and grad_w are 0). The instance sums are accumulated with float atomics in `workspace`
+ * (xsg_rigid_transform_bwd_workspace_bytes(n_instances) bytes): their summation order varies. */
+size_t xsg_rigid_transform_bwd_workspace_bytes(int64_t n_instances);
 int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_positions, const float* v_rotations,
                             const float* v_velocities, float* grad_positions, float* grad_rotations,
-                            float* grad_q, float* grad_t, float* grad_v, float* grad_w, xsg_stream_t stream);
+                            float* grad_q, float* grad_t, float* grad_v, float* grad_w, void* workspace,
+                            xsg_stream_t stream);
 
 /* ------------------------------------------------------------------ binning */
 int xsg_mask_radii(int64_t n, const uint8_t* mask, float* radii, xsg_stream_t stream);

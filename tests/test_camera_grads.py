@@ -225,6 +225,43 @@ def test_gpu_camera_grads_reach_pose_tensors(dev, kind):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("size", [(65, 33), (1, 300), (700, 1), (64, 32), (129, 97)])
+def test_gpu_camera_grads_ragged_images(dev, size):
+    """Image sizes around the 64 x 32 pixels each workgroup sums: partial strips and row blocks,
+    single rows and columns, for the ray gradients and the per-pixel time gradients."""
+    w, h = size
+    print("case", size, flush=True)
+    spec = _spec("distorted")
+    spec.width, spec.height = w, h
+    cam = _gpu_cam(spec, dev)
+    g = np.random.default_rng(w * 1000 + h)
+    go = g.standard_normal((h, w, 3)).astype(np.float32)
+    gd = g.standard_normal((h, w, 3)).astype(np.float32)
+    pack = cam.pack.detach().clone().requires_grad_(True)
+    ro, rd = cam.ext_cls.camera_rays(pack, w, h)
+    ((ro * torch.from_numpy(go).to(dev)).sum() + (rd * torch.from_numpy(gd).to(dev)).sum()).backward()
+    ref = O.camera_rays_bwd(spec, w, h, go, gd, True, True, prec="f64")
+    got = pack.grad.detach().cpu().numpy().reshape(-1)
+    _close(got[:len(ref)], ref, f"d_pack {size}")
+    for delta in (False, True):
+        pack = cam.pack.detach().clone().requires_grad_(True)
+        fn = cam.ext_cls.pixel_time_delta if delta else cam.ext_cls.pixel_time
+        gr = g.standard_normal((h, w)).astype(np.float32)
+        (fn(pack, w, h) * torch.from_numpy(gr).to(dev)).sum().backward()
+        ref = O.pixel_time_bwd(spec, gr, w, h, delta=delta, prec="f64")
+        _close(pack.grad.detach().cpu().numpy().reshape(-1)[:len(ref)], ref, f"d_pack time {size}")
+    # many uvs: several 2048-element workgroups and a partial one
+    pack = cam.pack.detach().clone().requires_grad_(True)
+    uv_np = g.uniform(0, 1, (5000, 2)).astype(np.float32)
+    uv = torch.from_numpy(uv_np).to(dev).requires_grad_(True)
+    gr = g.standard_normal(5000).astype(np.float32)
+    (cam.ext_cls.pixel_time_from_uv(pack, uv) * torch.from_numpy(gr).to(dev)).sum().backward()
+    ref, ref_duv = O.pixel_time_bwd(spec, gr, uv=uv_np, prec="f64")
+    _close(pack.grad.detach().cpu().numpy().reshape(-1)[:len(ref)], ref, "d_pack uv")
+    _close(uv.grad.detach().cpu().numpy().reshape(-1), ref_duv.reshape(-1), "d_uv")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("kind", ["pinhole", "lidar"])
 @pytest.mark.parametrize("delta", [False, True])
 @pytest.mark.parametrize("from_uv", [False, True])

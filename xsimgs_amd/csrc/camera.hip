@@ -2,6 +2,8 @@
 // per-pixel rays and pixel times. One thread per Gaussian / point / pixel, 256-thread blocks.
 #include "xsg_common.h"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -150,6 +152,14 @@ XSG_DEV f2 pixel_uv(const Camera& c, int px, int py, int width, int height) {
     return mk2(u, (static_cast<float>(py) + 0.5f) / static_cast<float>(height));
 }
 
+// Image kernels run on 64 x 4 pixel workgroups: lane = column within a 64-wide strip, wavefront =
+// row, grid (ceil(width / 64), ceil(height / 4)); no integer division per pixel.
+constexpr int kStrip = 64, kStripRows = kBlock / 64;
+inline dim3 image_grid(int width, int height, int rows_per_thread = 1) {
+    return dim3((unsigned)((width + kStrip - 1) / kStrip),
+                (unsigned)((height + kStripRows * rows_per_thread - 1) / (kStripRows * rows_per_thread)));
+}
+
 template <int KIND>
 XSG_DEV f3 pixel_to_camera_ray(const Camera& c, f2 uv) {
     if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:13-16
@@ -209,10 +219,11 @@ template <int KIND>
 __global__ __launch_bounds__(kBlock) void camera_rays_kernel(
     const float* __restrict__ pack, int width, int height, int world_space, int normalized,
     float* __restrict__ ray_o, float* __restrict__ ray_d, uint8_t* __restrict__ valid) {
-    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (idx >= (int64_t)width * height) return;
+    const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
+    const int py = (int)blockIdx.y * kStripRows + (int)(threadIdx.x >> 6);
+    if (px >= width || py >= height) return;
+    const int64_t idx = (int64_t)py * width + px;
     const Camera c = load_camera(pack, KIND);
-    const int px = (int)(idx % width), py = (int)(idx / width);
     const f2 uv = pixel_uv<KIND>(c, px, py, width, height);
     f3 ray = pixel_to_camera_ray<KIND>(c, uv);
     if (normalized) ray = ray * (1.0f / sqrtf(dot(ray, ray)));
@@ -231,18 +242,24 @@ __global__ __launch_bounds__(kBlock) void camera_rays_kernel(
     if (valid) valid[idx] = ray_valid<KIND>(c, uv) ? 1 : 0;
 }
 
+// uv_in given: one thread per uv (1D grid); else one thread per pixel (image grid)
 template <int KIND>
 __global__ __launch_bounds__(kBlock) void pixel_time_kernel(
     const float* __restrict__ pack, int width, int height, const float2* __restrict__ uv_in,
     int64_t n, int delta, float* __restrict__ out) {
-    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (idx >= n) return;
     const Camera c = load_camera(pack, KIND);
+    int64_t idx;
     f2 uv;
     if (uv_in) {
+        idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+        if (idx >= n) return;
         uv = mk2(uv_in[idx].x, uv_in[idx].y);
     } else {
-        uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+        const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
+        const int py = (int)blockIdx.y * kStripRows + (int)(threadIdx.x >> 6);
+        if (px >= width || py >= height) return;
+        idx = (int64_t)py * width + px;
+        uv = pixel_uv<KIND>(c, px, py, width, height);
     }
     float t = pixel_time(c, uv.x, uv.y);
     if (delta) t = t - c.pose_time;
@@ -255,10 +272,12 @@ __global__ __launch_bounds__(kBlock) void pixel_time_kernel(
 template <int KIND>
 __global__ __launch_bounds__(kBlock) void undistort_map_kernel(const float* __restrict__ pack, int width, int height,
                                                                int normalized_range, float2* __restrict__ out) {
-    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (idx >= (int64_t)width * height) return;
+    const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
+    const int py = (int)blockIdx.y * kStripRows + (int)(threadIdx.x >> 6);
+    if (px >= width || py >= height) return;
+    const int64_t idx = (int64_t)py * width + px;
     const Camera c = load_camera(pack, KIND);
-    const f2 uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+    const f2 uv = pixel_uv<KIND>(c, px, py, width, height);
     const float x = (uv.x - c.i2) / c.i0, y = (uv.y - c.i3) / c.i1;
     float ru, rv;
     if constexpr (KIND == XSG_CAM_DISTORTED) {
@@ -287,7 +306,7 @@ constexpr int cam_grad_count() {
 constexpr int kCamGradMax = 29;
 
 template <int NV>
-XSG_DEV void block_partials(const float (&g)[NV], float* __restrict__ part) {
+XSG_DEV void block_partials(const float (&g)[NV], float* __restrict__ part, int64_t block) {
     __shared__ float s_w[kBlock / 64][NV];
     const int wave = threadIdx.x >> 6;
 #pragma unroll
@@ -300,13 +319,17 @@ XSG_DEV void block_partials(const float (&g)[NV], float* __restrict__ part) {
         float t = 0.f;
 #pragma unroll
         for (int w = 0; w < kBlock / 64; ++w) t += s_w[w][threadIdx.x];
-        part[(int64_t)blockIdx.x * NV + threadIdx.x] = t;
+        part[block * NV + threadIdx.x] = t;
     }
 }
 
 // camera_ray_backward_kernel_cuda (ray_kernels.h:61-161) for this build's pose model: ray_o =
 // t0 + v dt, ray_d = q (x) n, q = (cos(theta/2), w dt sigma) (x) q0 with theta = |w| |dt| and
 // sigma = sin(theta/2) / theta (jac_quat_from_axis_angle), dt = pixel_time - pose_time.
+// Each thread sums kGradRows pixels of its column (rows wave, wave + 4, ...) in registers before the
+// workgroup reduction, so a 1080p frame leaves about a thousand partial rows.
+constexpr int kGradRows = 8;
+
 template <int KIND>
 __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __restrict__ pack, int width,
                                                                  int height, int world_space, int normalized,
@@ -314,13 +337,17 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
                                                                  const float* __restrict__ d_ray_d,
                                                                  float* __restrict__ part) {
     constexpr int NG = cam_grad_count<KIND>();
-    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     const Camera c = load_camera(pack, KIND);
     float g[NG];
 #pragma unroll
     for (int k = 0; k < NG; ++k) g[k] = 0.f;
-    if (idx < (int64_t)width * height) {  // every thread takes part in the reduction below
-        const f2 uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+    const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
+    const int py0 = (int)blockIdx.y * kStripRows * kGradRows + (int)(threadIdx.x >> 6);
+    for (int rr = 0; rr < kGradRows; ++rr) {
+        const int py = py0 + rr * kStripRows;
+        if (px >= width || py >= height) continue;  // every thread takes part in the reduction below
+        const int64_t idx = (int64_t)py * width + px;
+        const f2 uv = pixel_uv<KIND>(c, px, py, width, height);
         const f3 r = pixel_to_camera_ray<KIND>(c, uv);
         const float il = 1.0f / sqrtf(dot(r, r));
         const f3 n = normalized ? r * il : r;
@@ -335,8 +362,8 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
             const float qw = w1 * w2 - dot(xyz1, xyz2);
             const f3 qv = w2 * xyz1 + w1 * xyz2 + cross(xyz1, xyz2);
             float d_dt = dot(go, c.v);  // ray_o = t0 + v dt
-            g[4] = go.x; g[5] = go.y; g[6] = go.z;
-            g[7] = dt * go.x; g[8] = dt * go.y; g[9] = dt * go.z;
+            g[4] += go.x; g[5] += go.y; g[6] += go.z;
+            g[7] += dt * go.x; g[8] += dt * go.y; g[9] += dt * go.z;
             // ray_d = n + 2 (qw (qv x n) + qv x (qv x n))
             dn = gd + 2.0f * (cross(qv, cross(qv, gd)) - qw * cross(qv, gd));
             const float d_qw = 2.0f * dot(gd, cross(qv, n));
@@ -347,7 +374,7 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
             const f3 d_xyz1 = w2 * d_qv - d_qw * xyz2 + cross(xyz2, d_qv);
             const float d_w2 = d_qw * w1 + dot(d_qv, xyz1);
             const f3 d_xyz2 = w1 * d_qv - d_qw * xyz1 + cross(d_qv, xyz1);
-            g[0] = d_w2; g[1] = d_xyz2.x; g[2] = d_xyz2.y; g[3] = d_xyz2.z;
+            g[0] += d_w2; g[1] += d_xyz2.x; g[2] += d_xyz2.y; g[3] += d_xyz2.z;
             // (w1, xyz1) = (cos(theta/2), w dt sigma); kappa = dt |dt| sigma'(theta) / |w|
             d_dt += d_w1 * dw1 + dot(d_xyz1, dxyz1);
             const float wn = sqrtf(dot(c.w, c.w));
@@ -363,17 +390,17 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
                 kappa = dt * fabsf(dt) * (0.5f * theta * ch - sh) / (theta * theta * wn);
             }
             const f3 d_w = (-d_w1 * dt * dt * sigma * 0.5f + kappa * dot(d_xyz1, c.w)) * c.w + (dt * sigma) * d_xyz1;
-            g[10] = d_w.x; g[11] = d_w.y; g[12] = d_w.z;
+            g[10] += d_w.x; g[11] += d_w.y; g[12] += d_w.z;
             // dt = trigger_time + uv . rolling_time - pose_time
-            g[13] = d_dt * uv.x; g[14] = d_dt * uv.y; g[15] = d_dt; g[16] = -d_dt;
+            g[13] += d_dt * uv.x; g[14] += d_dt * uv.y; g[15] += d_dt; g[16] += -d_dt;
         }
         const f3 dr = normalized ? (dn - dot(n, dn) * n) * il : dn;
         if constexpr (KIND == XSG_CAM_PINHOLE) {  // perspective.cu:19-33
             const float ifx = 1.0f / c.i0, ify = 1.0f / c.i1;
-            g[17] = -dr.x * (uv.x - c.i2) * ifx * ifx;
-            g[18] = -dr.y * (uv.y - c.i3) * ify * ify;
-            g[19] = -dr.x * ifx;
-            g[20] = -dr.y * ify;
+            g[17] += -dr.x * (uv.x - c.i2) * ifx * ifx;
+            g[18] += -dr.y * (uv.y - c.i3) * ify * ify;
+            g[19] += -dr.x * ifx;
+            g[20] += -dr.y * ify;
         } else if constexpr (KIND == XSG_CAM_DISTORTED) {
             // distorted_perspective.cu:121-188: re-solve, then at the solution g_d = J^-T dr.xy (J is
             // symmetric; dr.xy / scale where J is nearly singular) and dL/dk = -g_d . dD/dk
@@ -390,21 +417,21 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
                 gx = (st.jvv * dr.x - st.juv * dr.y) / det;
                 gy = (st.juu * dr.y - st.juv * dr.x) / det;
             }
-            g[17] = -gx * ud.x * ifx;
-            g[18] = -gy * ud.y * ify;
-            g[19] = -gx * ifx;
-            g[20] = -gy * ify;
+            g[17] += -gx * ud.x * ifx;
+            g[18] += -gy * ud.y * ify;
+            g[19] += -gx * ifx;
+            g[20] += -gy * ify;
             const float r2 = uc.x * uc.x + uc.y * uc.y, r4 = r2 * r2, r6 = r4 * r2;
             const float d_rad = -(gx * uc.x + gy * uc.y) / st.denom;
             const float d_rad_den = -d_rad * st.scale;
-            g[21] = d_rad * r2;
-            g[22] = d_rad * r4;
-            g[23] = -(gx * 2.0f * uc.x * uc.y + gy * (r2 + 2.0f * uc.y * uc.y));
-            g[24] = -(gx * (r2 + 2.0f * uc.x * uc.x) + gy * 2.0f * uc.x * uc.y);
-            g[25] = d_rad * r6;
-            g[26] = d_rad_den * r2;
-            g[27] = d_rad_den * r4;
-            g[28] = d_rad_den * r6;
+            g[21] += d_rad * r2;
+            g[22] += d_rad * r4;
+            g[23] += -(gx * 2.0f * uc.x * uc.y + gy * (r2 + 2.0f * uc.y * uc.y));
+            g[24] += -(gx * (r2 + 2.0f * uc.x * uc.x) + gy * 2.0f * uc.x * uc.y);
+            g[25] += d_rad * r6;
+            g[26] += d_rad_den * r2;
+            g[27] += d_rad_den * r4;
+            g[28] += d_rad_den * r6;
         } else if constexpr (KIND == XSG_CAM_FISHEYE) {
             // fisheye_opencv.cu:74-136: theta(delta, k) implicit through theta_d(theta, k) = delta
             const float x = (uv.x - c.i2) / c.i0, y = (uv.y - c.i3) / c.i1;
@@ -421,21 +448,21 @@ __global__ __launch_bounds__(kBlock) void camera_rays_bwd_kernel(const float* __
                 const float d_th = d_s * ct * inv_delta - dr.z * st;
                 const float dts = d_th / deriv;
                 const float t2 = th * th, t3 = t2 * th;
-                g[21] = -dts * t3;
-                g[22] = -dts * t3 * t2;
-                g[23] = -dts * t3 * t2 * t2;
-                g[24] = -dts * t3 * t2 * t2 * t2;
+                g[21] += -dts * t3;
+                g[22] += -dts * t3 * t2;
+                g[23] += -dts * t3 * t2 * t2;
+                g[24] += -dts * t3 * t2 * t2 * t2;
                 const float d_delta = -d_s * st * inv_delta * inv_delta + dts;
                 const float gx = sf * dr.x + d_delta * x * inv_delta;
                 const float gy = sf * dr.y + d_delta * y * inv_delta;
-                g[17] = -gx * x / c.i0;
-                g[18] = -gy * y / c.i1;
-                g[19] = -gx / c.i0;
-                g[20] = -gy / c.i1;
+                g[17] += -gx * x / c.i0;
+                g[18] += -gy * y / c.i1;
+                g[19] += -gx / c.i0;
+                g[20] += -gy / c.i1;
             }
         }  // the spherical and lidar models carry no intrinsics gradient (base_camera_impl.h:19-22)
     }
-    block_partials<NG>(g, part);
+    block_partials<NG>(g, part, (int64_t)blockIdx.y * gridDim.x + blockIdx.x);
 }
 
 // pixel_time[_delta][_from_uv]_bwd_kernel (time_kernels.h:123-330): partial sums of g u, g v and g;
@@ -445,35 +472,51 @@ __global__ __launch_bounds__(kBlock) void pixel_time_bwd_kernel(const float* __r
                                                                 int height, const float2* __restrict__ uv_in,
                                                                 int64_t n, const float* __restrict__ grad,
                                                                 float2* __restrict__ d_uv, float* __restrict__ part) {
-    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     const Camera c = load_camera(pack, KIND);
     float g[3] = {0.f, 0.f, 0.f};
-    if (idx < n) {
+    for (int rr = 0; rr < kGradRows; ++rr) {
+        int64_t idx;
         f2 uv;
-        if (uv_in) {
+        if (uv_in) {  // 1D: element blockIdx.x * kBlock * kGradRows + rr * kBlock + thread
+            idx = ((int64_t)blockIdx.x * kGradRows + rr) * kBlock + threadIdx.x;
+            if (idx >= n) continue;
             uv = mk2(uv_in[idx].x, uv_in[idx].y);
         } else {
-            uv = pixel_uv<KIND>(c, (int)(idx % width), (int)(idx / width), width, height);
+            const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
+            const int py = (int)blockIdx.y * kStripRows * kGradRows + (int)(threadIdx.x >> 6) + rr * kStripRows;
+            if (px >= width || py >= height) continue;
+            idx = (int64_t)py * width + px;
+            uv = pixel_uv<KIND>(c, px, py, width, height);
         }
         const float gr = grad[idx];
         if (d_uv) d_uv[idx] = make_float2(gr * c.roll_u, gr * c.roll_v);
-        g[0] = gr * uv.x; g[1] = gr * uv.y; g[2] = gr;
+        g[0] += gr * uv.x; g[1] += gr * uv.y; g[2] += gr;
     }
-    block_partials<3>(g, part);
+    block_partials<3>(g, part, (int64_t)blockIdx.y * gridDim.x + blockIdx.x);
 }
 
 // one workgroup: out[e] = sum over blocks of part[b][k] for the nv partial values, placed at the pack
 // positions: rays (`rays`) with k = e for the first nv elements; times (nv = 3) at rolling_time,
 // trigger_time and, for the delta variants, minus the trigger sum at pose_time; every other pack
 // element 0.
-__global__ __launch_bounds__(kBlock) void grad_final_kernel(const float* __restrict__ part, int nb, int nv, int rays,
-                                                            int delta, int pack_elems, float* __restrict__ out) {
+constexpr int kFinalBlock = 1024;
+__global__ __launch_bounds__(kFinalBlock) void grad_final_kernel(const float* __restrict__ part, int nb, int nv,
+                                                                 int rays, int delta, int pack_elems,
+                                                                 float* __restrict__ out) {
     const int wave = threadIdx.x >> 6, lane = __lane_id();
-    for (int e = wave; e < pack_elems; e += kBlock / 64) {
+    for (int e = wave; e < pack_elems; e += kFinalBlock / 64) {
         const int k = rays ? e : (e == 13 ? 0 : e == 14 ? 1 : (e == 15 || (e == 16 && delta)) ? 2 : -1);
         float t = 0.f;
-        if (k >= 0 && k < nv)
-            for (int b = lane; b < nb; b += 64) t += part[(int64_t)b * nv + k];
+        if (k >= 0 && k < nv) {
+            float t4[4] = {0.f, 0.f, 0.f, 0.f};  // four independent load chains
+            int b = lane;
+            for (; b + 192 < nb; b += 256) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) t4[u] += part[(int64_t)(b + 64 * u) * nv + k];
+            }
+            for (; b < nb; b += 64) t4[0] += part[(int64_t)b * nv + k];
+            t = (t4[0] + t4[1]) + (t4[2] + t4[3]);
+        }
         t = wave_sum(t);
         if (lane == 0) out[e] = (!rays && delta && e == 16) ? -t : t;
     }
@@ -560,7 +603,7 @@ extern "C" int xsg_camera_rays(int kind, const float* pack, int width, int heigh
     if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
     const int64_t n = (int64_t)width * height;
     if (n == 0) return XSG_OK;
-    const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const dim3 grid = image_grid(width, height), block(kBlock);
     const hipStream_t s = (hipStream_t)stream;
     const int rc = xsg_with_camera_kind(kind, [&](auto k) {
         camera_rays_kernel<decltype(k)::value><<<grid, block, 0, s>>>(pack, width, height, world_space, normalized,
@@ -577,7 +620,7 @@ extern "C" int xsg_pixel_time(int kind, const float* pack, int width, int height
     if (n < 0 || !pack || !out) return xsg_fail(XSG_ERR_INVALID, "xsg_pixel_time: bad arguments");
     if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
     if (n == 0) return XSG_OK;
-    const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const dim3 grid = uv ? dim3(xsg_blocks(n, kBlock)) : image_grid(width, height), block(kBlock);
     const hipStream_t s = (hipStream_t)stream;
     auto uv2 = reinterpret_cast<const float2*>(uv);
     const int rc = xsg_with_camera_kind(kind, [&](auto k) {
@@ -595,7 +638,7 @@ extern "C" int xsg_undistort_map(int kind, const float* pack, int width, int hei
     if (width < 0 || height < 0 || !pack || !out) return xsg_fail(XSG_ERR_INVALID, "xsg_undistort_map: bad arguments");
     const int64_t n = (int64_t)width * height;
     if (n == 0) return XSG_OK;
-    const dim3 grid(xsg_blocks(n, kBlock)), block(kBlock);
+    const dim3 grid = image_grid(width, height), block(kBlock);
     const hipStream_t s = (hipStream_t)stream;
     auto o2 = reinterpret_cast<float2*>(out);
     if (kind == XSG_CAM_DISTORTED)
@@ -607,8 +650,8 @@ extern "C" int xsg_undistort_map(int kind, const float* pack, int width, int hei
 }
 
 extern "C" size_t xsg_camera_rays_bwd_workspace_bytes(int width, int height) {
-    const int64_t n = (int64_t)(width > 0 ? width : 0) * (height > 0 ? height : 0);
-    return sizeof(float) * (size_t)kCamGradMax * xsg_blocks(n > 0 ? n : 1, kBlock);
+    const dim3 g = image_grid(width > 0 ? width : 1, height > 0 ? height : 1, kGradRows);
+    return sizeof(float) * (size_t)kCamGradMax * g.x * g.y;
 }
 
 extern "C" int xsg_camera_rays_bwd(int kind, const float* pack, int width, int height, int world_space,
@@ -619,25 +662,35 @@ extern "C" int xsg_camera_rays_bwd(int kind, const float* pack, int width, int h
     if (width < 0 || height < 0) return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: negative size");
     if (!pack || !grad_pack || !workspace || (!d_ray_d && (int64_t)width * height > 0))
         return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: null pointer");
-    const int64_t n = (int64_t)width * height;
-    const unsigned nb = xsg_blocks(n > 0 ? n : 1, kBlock);
+    const dim3 grid = image_grid(width > 0 ? width : 1, height > 0 ? height : 1, kGradRows);
+    const int nb = (int)(grid.x * grid.y);
     float* part = (float*)workspace;
     const hipStream_t s = (hipStream_t)stream;
     int ng = 0;
     const int rc = xsg_with_camera_kind(kind, [&](auto k) {
         constexpr int KIND = decltype(k)::value;
         ng = cam_grad_count<KIND>();
-        camera_rays_bwd_kernel<KIND><<<nb, kBlock, 0, s>>>(pack, width, height, world_space, normalized, d_ray_o,
-                                                           d_ray_d, part);
+        camera_rays_bwd_kernel<KIND><<<grid, kBlock, 0, s>>>(pack, width, height, world_space, normalized, d_ray_o,
+                                                             d_ray_d, part);
     });
     if (rc != XSG_OK) return rc;
-    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, ng, 1, 0, pe, grad_pack);
+    grad_final_kernel<<<1, kFinalBlock, 0, s>>>(part, nb, ng, 1, 0, pe, grad_pack);
     XSG_TRY_LAUNCH("camera_rays_bwd");
     return XSG_OK;
 }
 
-extern "C" size_t xsg_pixel_time_bwd_workspace_bytes(int64_t n) {
-    return sizeof(float) * 3 * (size_t)xsg_blocks(n > 0 ? n : 1, kBlock);
+// pixel_time_bwd's workgroups: an image grid of kGradRows rows per thread for pixels, else
+// kBlock * kGradRows uvs per workgroup
+inline dim3 time_bwd_grid(int width, int height, bool from_uv, int64_t n) {
+    if (from_uv) return dim3(xsg_blocks(n > 0 ? n : 1, (int64_t)kBlock * kGradRows));
+    return image_grid(width > 0 ? width : 1, height > 0 ? height : 1, kGradRows);
+}
+
+extern "C" size_t xsg_pixel_time_bwd_workspace_bytes(int width, int height, int64_t n_uv) {
+    // enough for either layout: the image grid of width x height and the 1D grid of n_uv
+    const dim3 gi = time_bwd_grid(width, height, false, 0), gu = time_bwd_grid(0, 0, true, n_uv);
+    const size_t nb = std::max<size_t>((size_t)gi.x * gi.y, (size_t)gu.x * gu.y);
+    return sizeof(float) * 3 * nb;
 }
 
 extern "C" int xsg_pixel_time_bwd(int kind, const float* pack, int width, int height, const float* uv,
@@ -649,17 +702,18 @@ extern "C" int xsg_pixel_time_bwd(int kind, const float* pack, int width, int he
     if (n < 0 || (!uv && (width < 0 || height < 0))) return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: bad size");
     if (!pack || !grad_pack || !workspace || (n > 0 && !grad))
         return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: null pointer");
-    const unsigned nb = xsg_blocks(n > 0 ? n : 1, kBlock);
+    const dim3 grid = time_bwd_grid(width, height, uv != nullptr, n);
+    const int nb = (int)(grid.x * grid.y);
     float* part = (float*)workspace;
     const hipStream_t s = (hipStream_t)stream;
     const float2* uv2 = (const float2*)uv;
     float2* duv2 = uv ? (float2*)d_uv : nullptr;
     const int rc = xsg_with_camera_kind(kind, [&](auto k) {
-        pixel_time_bwd_kernel<decltype(k)::value><<<nb, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2,
-                                                                        part);
+        pixel_time_bwd_kernel<decltype(k)::value><<<grid, kBlock, 0, s>>>(pack, width, height, uv2, n, grad, duv2,
+                                                                          part);
     });
     if (rc != XSG_OK) return rc;
-    grad_final_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, 3, 0, delta ? 1 : 0, pe, grad_pack);
+    grad_final_kernel<<<1, kFinalBlock, 0, s>>>(part, nb, 3, 0, delta ? 1 : 0, pe, grad_pack);
     XSG_TRY_LAUNCH("pixel_time_bwd");
     return XSG_OK;
 }

@@ -81,17 +81,22 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float* __restrict__ p, int
     if (i < n) p[i] = 0.f;
 }
 
+// Per-instance gradient sums live in 64-byte slots of a workspace, [n_inst][16] floats: q (4), t, v,
+// w (3 each), 3 unused. One slot per instance keeps an instance's 13 atomics in one cache segment;
+// packing the four sums densely (4 and 3 floats per instance) put many instances on each cache line
+// and made the atomics about ten times slower.
+constexpr int kSlot = 16;
+
 // copy_gs_rigid_transform_bwd_kernel (container.cu:78-160). Per-Gaussian gradients are written for
-// every Gaussian (zeros where skipped); the 13 per-instance sums (q, t, v, w) are summed across the
-// wavefront first when all of its active lanes share one instance (Gaussians are usually stored
-// instance by instance), so such a wavefront issues 13 atomics instead of 13 per lane.
+// every Gaussian (zeros where skipped). The 13 per-instance values are summed across the wavefront
+// per instance (Gaussians are usually stored instance by instance, so a wavefront holds one or two)
+// and added by one 13-lane atomic instruction per instance.
 template <bool OFFSETS>
 __global__ __launch_bounds__(kBlock) void rigid_bwd_kernel(RigidArgs a, const float* __restrict__ v_pos,
                                                            const float4* __restrict__ v_rot,
                                                            const float* __restrict__ v_vel,
                                                            float* __restrict__ g_pos, float4* __restrict__ g_rot,
-                                                           float* __restrict__ g_q, float* __restrict__ g_t,
-                                                           float* __restrict__ g_v, float* __restrict__ g_w) {
+                                                           float* __restrict__ slots) {
     const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     float c[13];
 #pragma unroll
@@ -135,31 +140,46 @@ __global__ __launch_bounds__(kBlock) void rigid_bwd_kernel(RigidArgs a, const fl
         st3(g_pos + 3 * i, dp);
         g_rot[i] = dr;
     }
-    const bool active = r >= 0;
-    const uint64_t act = __ballot(active);
-    if (act == 0) return;
-    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)k, __builtin_ctzll(act));
-    float* dst[4] = {g_q, g_t, g_v, g_w};
-    if (__ballot(active && k == k0) == act) {
-        const int lead = __builtin_ctzll(act);
-#pragma unroll
-        for (int j = 0; j < 13; ++j) c[j] = wave_sum(c[j]);
-        if (__lane_id() == lead) {
-#pragma unroll
-            for (int j = 0; j < 13; ++j) {
-                const int f = j < 4 ? 0 : 1 + (j - 4) / 3;
-                const int o = j < 4 ? 4 * (int)k0 + j : 3 * (int)k0 + (j - 4) % 3;
-                if (j < 7 || v_vel) atomicAdd(dst[f] + o, c[j]);
-            }
-        }
-    } else if (active) {
+    const int lane = __lane_id();
+    const int nv = v_vel ? 13 : 7;  // without velocity gradients v and w stay 0
+    uint64_t rem = __ballot(r >= 0);
+    // one instance at a time: the lanes of the first remaining lane's instance are summed across the
+    // wavefront and added by one 13-lane atomic; after kMaxRuns instances (shuffled Gaussians) the
+    // remaining lanes add their own values
+    constexpr int kMaxRuns = 4;
+    for (int run = 0; run < kMaxRuns && rem != 0; ++run) {
+        const uint32_t kk = (uint32_t)__builtin_amdgcn_readlane((int)k, __builtin_ctzll(rem));
+        const bool in = ((rem >> lane) & 1) && k == kk;
+        rem &= ~__ballot(in);
+        float mine = 0.f;
 #pragma unroll
         for (int j = 0; j < 13; ++j) {
-            const int f = j < 4 ? 0 : 1 + (j - 4) / 3;
-            const int o = j < 4 ? 4 * (int)k + j : 3 * (int)k + (j - 4) % 3;
-            if (j < 7 || v_vel) atomicAdd(dst[f] + o, c[j]);
+            const float t = wave_sum(in ? c[j] : 0.f);
+            mine = (lane == j) ? t : mine;
         }
+        if (lane < nv) atomicAdd(slots + (int64_t)kk * kSlot + lane, mine);
     }
+    if ((rem >> lane) & 1) {
+        float* s = slots + (int64_t)k * kSlot;
+#pragma unroll
+        for (int j = 0; j < 13; ++j)
+            if (j < nv) atomicAdd(s + j, c[j]);
+    }
+}
+
+// the slots into the four per-instance outputs
+__global__ __launch_bounds__(kBlock) void rigid_slots_out_kernel(const float* __restrict__ slots, int64_t n_inst,
+                                                                 float* __restrict__ g_q, float* __restrict__ g_t,
+                                                                 float* __restrict__ g_v, float* __restrict__ g_w) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n_inst * 13) return;
+    const int64_t k = i / 13;
+    const int j = (int)(i - k * 13);
+    const float v = slots[k * kSlot + j];
+    if (j < 4) g_q[4 * k + j] = v;
+    else if (j < 7) g_t[3 * k + (j - 4)] = v;
+    else if (j < 10) g_v[3 * k + (j - 7)] = v;
+    else g_w[3 * k + (j - 10)] = v;
 }
 
 int rigid_args(const xsg_rigid_desc* d, RigidArgs& a, const char* who) {
@@ -215,37 +235,41 @@ extern "C" int xsg_rigid_transform_fwd(const xsg_rigid_desc* d, float* out_posit
     return XSG_OK;
 }
 
+extern "C" size_t xsg_rigid_transform_bwd_workspace_bytes(int64_t n_instances) {
+    return sizeof(float) * kSlot * (size_t)(n_instances > 0 ? n_instances : 1);
+}
+
 extern "C" int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_positions, const float* v_rotations,
                                        const float* v_velocities, float* grad_positions, float* grad_rotations,
-                                       float* grad_q, float* grad_t, float* grad_v, float* grad_w,
+                                       float* grad_q, float* grad_t, float* grad_v, float* grad_w, void* workspace,
                                        xsg_stream_t stream) {
     RigidArgs a;
     const int rc = rigid_args(d, a, "copy_gs_rigid_transform_bwd");
     if (rc != XSG_OK) return rc;
-    if (a.n_inst > 0 && (!grad_q || !grad_t || !grad_v || !grad_w))
-        return xsg_fail(XSG_ERR_INVALID, "copy_gs_rigid_transform_bwd: null instance gradient");
+    if (a.n_inst > 0 && (!grad_q || !grad_t || !grad_v || !grad_w || !workspace))
+        return xsg_fail(XSG_ERR_INVALID, "copy_gs_rigid_transform_bwd: null instance gradient or workspace");
     if (a.n > 0 && (!d->inst_w || !v_positions || !v_rotations || !grad_positions || !grad_rotations))
         return xsg_fail(XSG_ERR_INVALID, "copy_gs_rigid_transform_bwd: null tensor");
     if (reinterpret_cast<uintptr_t>(v_rotations) % 16 || reinterpret_cast<uintptr_t>(grad_rotations) % 16)
         return xsg_fail(XSG_ERR_INVALID, "copy_gs_rigid_transform_bwd: quaternion arrays must be 16-byte aligned");
     const hipStream_t s = (hipStream_t)stream;
     const int64_t ni = a.n_inst;
-    if (ni > 0) {  // instance sums start at zero (a fill kernel, so that the call can be graph-captured)
-        zero_kernel<<<xsg_blocks(4 * ni, kBlock), kBlock, 0, s>>>(grad_q, 4 * ni);
-        zero_kernel<<<xsg_blocks(3 * ni, kBlock), kBlock, 0, s>>>(grad_t, 3 * ni);
-        zero_kernel<<<xsg_blocks(3 * ni, kBlock), kBlock, 0, s>>>(grad_v, 3 * ni);
-        zero_kernel<<<xsg_blocks(3 * ni, kBlock), kBlock, 0, s>>>(grad_w, 3 * ni);
-    }
+    float* slots = static_cast<float*>(workspace);
+    // the slots start at zero (a fill kernel, so that the call can be graph-captured)
+    if (ni > 0) zero_kernel<<<xsg_blocks(kSlot * ni, kBlock), kBlock, 0, s>>>(slots, kSlot * ni);
     if (a.n > 0) {
         auto vr = reinterpret_cast<const float4*>(v_rotations);
         auto gr = reinterpret_cast<float4*>(grad_rotations);
         if (a.gs_inst_off)
-            rigid_bwd_kernel<true><<<xsg_blocks(a.n, kBlock), kBlock, 0, s>>>(
-                a, v_positions, vr, v_velocities, grad_positions, gr, grad_q, grad_t, grad_v, grad_w);
+            rigid_bwd_kernel<true><<<xsg_blocks(a.n, kBlock), kBlock, 0, s>>>(a, v_positions, vr, v_velocities,
+                                                                             grad_positions, gr, slots);
         else
-            rigid_bwd_kernel<false><<<xsg_blocks(a.n, kBlock), kBlock, 0, s>>>(
-                a, v_positions, vr, v_velocities, grad_positions, gr, grad_q, grad_t, grad_v, grad_w);
+            rigid_bwd_kernel<false><<<xsg_blocks(a.n, kBlock), kBlock, 0, s>>>(a, v_positions, vr, v_velocities,
+                                                                              grad_positions, gr, slots);
     }
+    if (ni > 0)
+        rigid_slots_out_kernel<<<xsg_blocks(13 * ni, kBlock), kBlock, 0, s>>>(slots, ni, grad_q, grad_t, grad_v,
+                                                                             grad_w);
     XSG_TRY_LAUNCH("copy_gs_rigid_transform_bwd");
     return XSG_OK;
 }

@@ -579,10 +579,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> copy_gs_rigid_transfo
     Tensor g_pos = at::empty_like(positions), g_rot = at::empty_like(rotations);
     Tensor g_q = at::empty_like(inst_q), g_t = at::empty_like(inst_w), g_v = at::empty_like(inst_w),
            g_w = at::empty_like(inst_w);
+    Tensor ws = workspace(positions, xsg_rigid_transform_bwd_workspace_bytes(d.n_instances));
     check_rc(xsg_rigid_transform_bwd(&d, vp.data_ptr<float>(), vr.data_ptr<float>(), fptr(vv),
                                      g_pos.data_ptr<float>(), g_rot.data_ptr<float>(), g_q.data_ptr<float>(),
                                      g_t.data_ptr<float>(), g_v.data_ptr<float>(), g_w.data_ptr<float>(),
-                                     stream_of(positions)));
+                                     ws.data_ptr(), stream_of(positions)));
     return {g_pos, g_rot, g_q, g_t, g_v, g_w};
 }
 
@@ -705,7 +706,7 @@ struct PixelTimeFn : public torch::autograd::Function<PixelTimeFn> {
         const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
         const int height = (int)g.size(0), width = (int)g.size(1);
         Tensor grad_pack = at::empty_like(pack);
-        Tensor ws = workspace(pack, xsg_pixel_time_bwd_workspace_bytes((int64_t)width * height));
+        Tensor ws = workspace(pack, xsg_pixel_time_bwd_workspace_bytes(width, height, 0));
         check_rc(xsg_pixel_time_bwd((int)ctx->saved_data["kind"].toInt(), fptr(pack), width, height, nullptr, 0,
                                     ctx->saved_data["delta"].toBool() ? 1 : 0, fptr(g), grad_pack.data_ptr<float>(),
                                     nullptr, ws.data_ptr(), stream_of(pack)));
@@ -740,7 +741,7 @@ struct PixelTimeUvFn : public torch::autograd::Function<PixelTimeUvFn> {
         const int64_t n = uvc.numel() / 2;
         Tensor grad_pack = at::empty_like(pack);
         Tensor d_uv = ctx->needs_input_grad(1) ? at::empty_like(uvc) : Tensor();
-        Tensor ws = workspace(pack, xsg_pixel_time_bwd_workspace_bytes(n));
+        Tensor ws = workspace(pack, xsg_pixel_time_bwd_workspace_bytes(0, 0, n));
         check_rc(xsg_pixel_time_bwd((int)ctx->saved_data["kind"].toInt(), fptr(pack), 0, 0, fptr(uvc), n,
                                     ctx->saved_data["delta"].toBool() ? 1 : 0, fptr(g), grad_pack.data_ptr<float>(),
                                     d_uv.defined() ? d_uv.data_ptr<float>() : nullptr, ws.data_ptr(),
