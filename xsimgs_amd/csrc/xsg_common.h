@@ -400,6 +400,57 @@ struct UtWeights { float wm0, wc0, wi, sqrt_dl; };
 // reference leaves in them (untouched if the centre point fails, the accumulated mean if a sigma
 // point fails) and radii come from a zero covariance, because the phase-modelled selection
 // (ut_phm_kernels.h:417-421) can pick a failed side.
+// A camera whose pose does not move maps world to camera space by one linear map: quat_apply with
+// the conjugate of q0 (world_to_camera_jac at any time), p -> p + 2 (w (u x p) + u x (u x p)) with
+// u = -q0.xyz, i.e. M = I + 2 w [u]x + 2 (u u^T - |u|^2 I) (exact for any quaternion).
+struct Mat3 { f3 r0, r1, r2; };
+
+XSG_DEV Mat3 static_world_to_camera(const Camera& c) {
+    const float w = c.qw, x = -c.qv.x, y = -c.qv.y, z = -c.qv.z;
+    Mat3 m;
+    m.r0 = mk3(1.f - 2.f * (y * y + z * z), 2.f * (x * y - w * z), 2.f * (x * z + w * y));
+    m.r1 = mk3(2.f * (x * y + w * z), 1.f - 2.f * (x * x + z * z), 2.f * (y * z - w * x));
+    m.r2 = mk3(2.f * (x * z - w * y), 2.f * (y * z + w * x), 1.f - 2.f * (x * x + y * y));
+    return m;
+}
+
+XSG_DEV f3 mul(const Mat3& m, f3 v) { return mk3(dot(m.r0, v), dot(m.r1, v), dot(m.r2, v)); }
+
+// camera_projection for a static pose from the camera-space point: the point does not depend on the
+// time, so the projection's time Jacobian is 0 and the Newton step of the Jacobian models reduces to
+// the fixed-point step p_time -= residual, as for the other models (projection_kernels.h:116-198).
+// The pinhole projection takes one reciprocal of z.
+template <int KIND>
+XSG_DEV void static_camera_projection(const Camera& c, f3 pc, const ProjParams& pp, int mode, float4& uvdt,
+                                      bool& valid) {
+    f3 uvd;
+    if constexpr (KIND == XSG_CAM_PINHOLE) {
+        const float iz = 1.0f / pc.z;
+        uvd = mk3(pc.x * c.i0 * iz + c.i2, pc.y * c.i1 * iz + c.i3, pc.z);
+    } else {
+        uvd = point_to_uvd<KIND>(c, mode, pc);
+    }
+    float p_time = 0.0f;
+    if (mode == XSG_MODE_NEGATIVE) p_time = -fabsf(c.roll_u) * 0.5f;
+    else if (mode == XSG_MODE_POSITIVE) p_time = fabsf(c.roll_u) * 0.5f;
+    float residual = 0.0f;
+    if ((uvd.z <= 0.0f) || (uvd.x < -pp.margin) || (uvd.x > 1.0f + pp.margin) || (uvd.y < -pp.margin) ||
+        (uvd.y > 1.0f + pp.margin)) {
+        valid = false;
+        uvdt = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const float real_time = pixel_time(c, uvd.x, uvd.y);
+#pragma unroll 1
+    for (int i = 0; i < 5; ++i) {
+        residual = (c.pose_time + p_time) - real_time;
+        p_time -= residual;
+        if (fabsf(residual) < pp.thr) break;
+    }
+    uvdt = make_float4(uvd.x, uvd.y, uvd.z, p_time);
+    valid = valid && (fabsf(residual) < pp.max_res) && (uvd.z > 0.0f);
+}
+
 template <int KIND>
 XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 img, const ProjParams& pp,
                            f3 pw, f3 pv, float opac, const f3 d[3], bool is_static, f2& mean2d,
@@ -408,7 +459,18 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
     bool valid = true;
     f2 pts[7];
     bool result = true;
-    camera_projection<KIND>(c, pw, pv, pp, mode, is_static, uvdt, valid);
+    // static pose: the seven camera-space points are M (pw - t0) +- M d_i
+    Mat3 m;
+    f3 pc0 = mk3(0.f, 0.f, 0.f), e[3];
+    if (is_static) {
+        m = static_world_to_camera(c);
+        pc0 = mul(m, pw - c.t0);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) e[k] = mul(m, d[k]);
+        static_camera_projection<KIND>(c, pc0, pp, mode, uvdt, valid);
+    } else {
+        camera_projection<KIND>(c, pw, pv, pp, mode, false, uvdt, valid);
+    }
     f2 cov_xx_xy = mk2(0.f, 0.f);
     float cov_yy = 0.f;
     if (!valid) {
@@ -421,7 +483,8 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
         float sign = 1.0f;
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
-            camera_projection<KIND>(c, pw + sign * d[i / 2], pv, pp, mode, is_static, uvdt, valid);
+            if (is_static) static_camera_projection<KIND>(c, pc0 + sign * e[i / 2], pp, mode, uvdt, valid);
+            else camera_projection<KIND>(c, pw + sign * d[i / 2], pv, pp, mode, false, uvdt, valid);
             pts[i + 1] = mk2(uvdt.x * img.x, uvdt.y * img.y);
             mean2d.x += ut.wi * pts[i + 1].x;
             mean2d.y += ut.wi * pts[i + 1].y;
