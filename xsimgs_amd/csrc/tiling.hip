@@ -19,6 +19,7 @@
 // Stable by (high bits, low bits, Gaussian order) in both cases, so the result is bit-identical
 // to sorting the reference keys; ties keep Gaussian order as the reference's fill does.
 #include <algorithm>
+#include <vector>
 
 #include "xsg_sort.h"
 
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
 // host checks the exact intersection total instead)
 template <typename T>
 __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb,
-                                                               const uint64_t* __restrict__ cpart) {
+                                                               const uint64_t* __restrict__ cpart,
+                                                               uint64_t* __restrict__ publish = nullptr) {
     __shared__ T lds[kWaves];
     __shared__ uint64_t lds64[kWaves];
     T carry = 0;
@@ -239,6 +241,11 @@ __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ p
     if (threadIdx.x == 0) {
         partials[nb] = carry;
         if (cpart) { partials[nb + 1] = (T)exact; partials[nb + 2] = (T)exact2; }
+        if (publish) {  // the three totals, also into host memory (vector stores)
+            publish[0] = (uint64_t)carry;
+            publish[1] = exact;
+            publish[2] = exact2;
+        }
     }
 }
 
@@ -909,6 +916,38 @@ extern "C" size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d) {
     return count_ws_layout(g, nullptr).bytes;
 }
 
+// Per host thread and device: a mapped pinned host buffer that the count phase writes its totals to,
+// and the event that marks the write. Allocated on a thread's first count on a device and kept for
+// the thread's lifetime (64 bytes of pinned memory and one event).
+struct CountReadback {
+    uint64_t* host = nullptr;  // host view
+    uint64_t* dev = nullptr;   // device view of the same memory
+    hipEvent_t ev = nullptr;
+};
+
+static int count_readback(CountReadback*& out) {
+    thread_local std::vector<CountReadback> per_device;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return xsg_launch_status("isect_count readback device");
+    if ((int)per_device.size() <= dev) per_device.resize(dev + 1);
+    CountReadback& rb = per_device[dev];
+    if (!rb.host) {
+        void* h = nullptr;
+        if (hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+            return xsg_launch_status("isect_count readback buffer");
+        void* d = nullptr;
+        if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) return xsg_launch_status("isect_count readback map");
+        hipEvent_t ev = nullptr;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+            return xsg_launch_status("isect_count readback event");
+        rb.host = static_cast<uint64_t*>(h);
+        rb.dev = static_cast<uint64_t*>(d);
+        rb.ev = ev;
+    }
+    out = &rb;
+    return XSG_OK;
+}
+
 extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* workspace, int64_t* n_isects,
                                int64_t* n_visible, int64_t* n_runs, xsg_stream_t stream) {
     Geometry g;
@@ -947,7 +986,13 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
                 0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
         }
     }
-    scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb, w.cpart);
+    // the totals are final here: published to pinned host memory and marked by an event, so that the
+    // host reads them while the depth pre-order and row offsets below still run
+    CountReadback* rb = nullptr;
+    rc = count_readback(rb);
+    if (rc) return rc;
+    scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb, w.cpart, rb->dev);
+    if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
     compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
                                            w.comp_key);
     if (g.sort) {
@@ -962,16 +1007,14 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
-    // packed (visible << 32 | count) total, exact intersection total, exact row-run total
-    uint64_t total[3] = {0, 0, 0};
-    if (hipMemcpyAsync(total, w.partials + w.nb, sizeof(total), hipMemcpyDeviceToHost, s) != hipSuccess)
-        return xsg_launch_status("isect_count readback");
-    // poll rather than block: the readback ends a short queue, and waking from a blocking wait
-    // costs more than the wait itself
+    // packed (visible << 32 | count) total, exact intersection total, exact row-run total; poll the
+    // event rather than block on it (waking from a blocking wait costs more than the short wait)
     hipError_t q;
-    while ((q = hipStreamQuery(s)) == hipErrorNotReady) {
+    while ((q = hipEventQuery(rb->ev)) == hipErrorNotReady) {
     }
     if (q != hipSuccess) return xsg_launch_status("isect_count readback");
+    const volatile uint64_t* hv = rb->host;
+    const uint64_t total[3] = {hv[0], hv[1], hv[2]};
     // below 2^31 intersections the packed count field never carried, so its visible count is exact
     if (total[1] >= (1ull << 31))
         return xsg_fail(XSG_ERR_INVALID, "%llu intersections exceed the int32 range of flatten ids",
