@@ -670,11 +670,21 @@ struct CameraRaysFn : public torch::autograd::Function<CameraRaysFn> {
     }
 };
 
+// the autograd function only when the pack needs a gradient (its bookkeeping costs host time)
+bool needs_grad(const Tensor& t) { return t.requires_grad() && at::GradMode::is_enabled(); }
+
 py::object camera_rays(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool world_space,
                        bool normalized, bool return_origins, bool return_valid) {
     validate_pack(spec, pack);
-    auto res = CameraRaysFn::apply(pack, (int64_t)spec.kind, width, height, world_space, normalized,
-                                   return_origins, return_valid);
+    torch::autograd::variable_list res;
+    if (needs_grad(pack)) {
+        res = CameraRaysFn::apply(pack, (int64_t)spec.kind, width, height, world_space, normalized, return_origins,
+                                  return_valid);
+    } else {
+        torch::autograd::AutogradContext ctx;
+        res = CameraRaysFn::forward(&ctx, pack, (int64_t)spec.kind, width, height, world_space, normalized,
+                                    return_origins, return_valid);
+    }
     py::list out;
     size_t i = 0;
     out.append(return_origins ? py::cast(res[i++]) : py::none());
@@ -752,7 +762,9 @@ struct PixelTimeUvFn : public torch::autograd::Function<PixelTimeUvFn> {
 
 Tensor pixel_time(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool delta) {
     validate_pack(spec, pack);
-    return PixelTimeFn::apply(pack, (int64_t)spec.kind, width, height, delta);
+    if (needs_grad(pack)) return PixelTimeFn::apply(pack, (int64_t)spec.kind, width, height, delta);
+    torch::autograd::AutogradContext ctx;
+    return PixelTimeFn::forward(&ctx, pack, (int64_t)spec.kind, width, height, delta);
 }
 
 Tensor pixel_time_uv(const CamSpec& spec, const Tensor& pack, const Tensor& uv, bool delta) {
@@ -760,7 +772,9 @@ Tensor pixel_time_uv(const CamSpec& spec, const Tensor& pack, const Tensor& uv, 
     TORCH_CHECK(uv.size(-1) == 2, "UV coordinates last dimension must be 2")
     TORCH_CHECK(uv.device() == pack.device(), "Camera and UV-s must be on the same device")
     TORCH_CHECK(uv.dtype() == at::kFloat, "UV coordinates must be float32 tensor")
-    return PixelTimeUvFn::apply(pack, uv, (int64_t)spec.kind, delta);
+    if (needs_grad(pack) || needs_grad(uv)) return PixelTimeUvFn::apply(pack, uv, (int64_t)spec.kind, delta);
+    torch::autograd::AutogradContext ctx;
+    return PixelTimeUvFn::forward(&ctx, pack, uv, (int64_t)spec.kind, delta);
 }
 
 // undistort_map (include/cameras/distortion.h:33-56)
