@@ -103,9 +103,12 @@ XSG_DEV void put(float& a, float v) {
 // safe_normalize_bwd collapses to one vector w = (grd x gro) x grd (= |grd|^2 (gcrod x n)):
 // with A = -op vis dL/dalpha / |grd|^2 it adds A w to dL/dgro and -A (grd . gro) / |grd|^2 w to
 // dL/dgrd. The hit-distance terms are k1 = dL/dhit_t / |grd|^2 times -grd (gro) and
-// 2 (grd . gro) / |grd|^2 grd - gro (grd). Without per-pixel ray or time gradients the mean
-// gradient -M^T dL/dgro is applied once to the sum over the lane's two pixels (vg_sum).
-template <int CDIM, int CS, int K, bool DYN, bool RG, bool FIRST>
+// 2 (grd . gro) / |grd|^2 grd - gro (grd). With hit_t = -(grd . gro) / |grd|^2 the whole of
+// dL/dgrd is hit_t (dL/dgro - k1 grd) - k1 gro. Without per-pixel ray or time gradients the mean
+// gradient -M^T dL/dgro is applied once to the sum over the lane's two pixels (vg_sum), and when
+// every pixel shares gro (one ray origin, no motion: GS) the gro part of Q is added once per lane
+// as vg_sum (x) gro instead of once per pixel.
+template <int CDIM, int CS, int K, bool DYN, bool RG, bool FIRST, bool GS>
 XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, const float (&rgb)[CS],
                       float (&acc)[K], f3& vg_sum) {
     const float od = dot(e.gro, e.grd);
@@ -129,9 +132,7 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     const float Ap = -e.araw * v_alpha_g * e.inv_dd;
     const f3 w = cross(e.c, e.grd);
     const f3 v_gro = Ap * w - k1 * e.grd;
-    const float k2 = 2.0f * od * e.inv_dd * k1;
-    const float Bp = -Ap * od * e.inv_dd;
-    const f3 v_grd = k2 * e.grd - k1 * e.gro + Bp * w;
+    const f3 v_grd = hit_t * (v_gro - k1 * e.grd) - k1 * e.gro;
     if constexpr (RG || DYN) {
         const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
         put<FIRST>(acc[CDIM + 0], -v_omm.x);
@@ -153,15 +154,27 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     // Q = v_grd (x) grd + v_gro (x) gro; dL/dM = Q S R^T, and the scale gradient -Q_ii / s_i is
     // the reference's per-pair product of the pair's own values
     const f3 gd = e.grd, go = e.gro;
-    put<FIRST>(acc[CDIM + 3], v_grd.x * gd.x + v_gro.x * go.x);
-    put<FIRST>(acc[CDIM + 4], v_grd.x * gd.y + v_gro.x * go.y);
-    put<FIRST>(acc[CDIM + 5], v_grd.x * gd.z + v_gro.x * go.z);
-    put<FIRST>(acc[CDIM + 6], v_grd.y * gd.x + v_gro.y * go.x);
-    put<FIRST>(acc[CDIM + 7], v_grd.y * gd.y + v_gro.y * go.y);
-    put<FIRST>(acc[CDIM + 8], v_grd.y * gd.z + v_gro.y * go.z);
-    put<FIRST>(acc[CDIM + 9], v_grd.z * gd.x + v_gro.z * go.x);
-    put<FIRST>(acc[CDIM + 10], v_grd.z * gd.y + v_gro.z * go.y);
-    put<FIRST>(acc[CDIM + 11], v_grd.z * gd.z + v_gro.z * go.z);
+    if constexpr (GS) {
+        put<FIRST>(acc[CDIM + 3], v_grd.x * gd.x);
+        put<FIRST>(acc[CDIM + 4], v_grd.x * gd.y);
+        put<FIRST>(acc[CDIM + 5], v_grd.x * gd.z);
+        put<FIRST>(acc[CDIM + 6], v_grd.y * gd.x);
+        put<FIRST>(acc[CDIM + 7], v_grd.y * gd.y);
+        put<FIRST>(acc[CDIM + 8], v_grd.y * gd.z);
+        put<FIRST>(acc[CDIM + 9], v_grd.z * gd.x);
+        put<FIRST>(acc[CDIM + 10], v_grd.z * gd.y);
+        put<FIRST>(acc[CDIM + 11], v_grd.z * gd.z);
+    } else {
+        put<FIRST>(acc[CDIM + 3], v_grd.x * gd.x + v_gro.x * go.x);
+        put<FIRST>(acc[CDIM + 4], v_grd.x * gd.y + v_gro.x * go.y);
+        put<FIRST>(acc[CDIM + 5], v_grd.x * gd.z + v_gro.x * go.z);
+        put<FIRST>(acc[CDIM + 6], v_grd.y * gd.x + v_gro.y * go.x);
+        put<FIRST>(acc[CDIM + 7], v_grd.y * gd.y + v_gro.y * go.y);
+        put<FIRST>(acc[CDIM + 8], v_grd.y * gd.z + v_gro.y * go.z);
+        put<FIRST>(acc[CDIM + 9], v_grd.z * gd.x + v_gro.z * go.x);
+        put<FIRST>(acc[CDIM + 10], v_grd.z * gd.y + v_gro.z * go.y);
+        put<FIRST>(acc[CDIM + 11], v_grd.z * gd.z + v_gro.z * go.z);
+    }
     put<FIRST>(acc[CDIM + 12], e.vis * v_alpha_g);
     px.buf = fmaf(fac, u, px.buf);
 }
@@ -373,13 +386,26 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
                 }
                 float acc[K];
                 f3 vg_sum;
-                bwd_pair<CDIM, CS, K, DYN, RG, true>(px[0], gs, e0, rgb, acc, vg_sum);
-                bwd_pair<CDIM, CS, K, DYN, RG, false>(px[1], gs, e1, rgb, acc, vg_sum);
+                constexpr bool GS = FIXED && !(RG || DYN);
+                bwd_pair<CDIM, CS, K, DYN, RG, true, GS>(px[0], gs, e0, rgb, acc, vg_sum);
+                bwd_pair<CDIM, CS, K, DYN, RG, false, GS>(px[1], gs, e1, rgb, acc, vg_sum);
                 if constexpr (!(RG || DYN)) {
                     const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, vg_sum);
                     acc[CDIM + 0] = -v_omm.x;
                     acc[CDIM + 1] = -v_omm.y;
                     acc[CDIM + 2] = -v_omm.z;
+                }
+                if constexpr (GS) {
+                    const f3 go = gs.gro_fixed;
+                    acc[CDIM + 3] = fmaf(vg_sum.x, go.x, acc[CDIM + 3]);
+                    acc[CDIM + 4] = fmaf(vg_sum.x, go.y, acc[CDIM + 4]);
+                    acc[CDIM + 5] = fmaf(vg_sum.x, go.z, acc[CDIM + 5]);
+                    acc[CDIM + 6] = fmaf(vg_sum.y, go.x, acc[CDIM + 6]);
+                    acc[CDIM + 7] = fmaf(vg_sum.y, go.y, acc[CDIM + 7]);
+                    acc[CDIM + 8] = fmaf(vg_sum.y, go.z, acc[CDIM + 8]);
+                    acc[CDIM + 9] = fmaf(vg_sum.z, go.x, acc[CDIM + 9]);
+                    acc[CDIM + 10] = fmaf(vg_sum.z, go.y, acc[CDIM + 10]);
+                    acc[CDIM + 11] = fmaf(vg_sum.z, go.z, acc[CDIM + 11]);
                 }
 
                 // wave totals by reduce-scatter: lane l ends with component 16 * chunk + (l >> 2);
