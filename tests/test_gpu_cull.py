@@ -73,6 +73,8 @@ CASES = [  # tile, shared origin, dynamic, tiny ray
     ((8, 8), True, False, False),
     ((16, 8), False, True, False),
     ((10, 6), True, True, True),
+    ((12, 16), True, False, False),   # 192 pixels: four pixels per lane, 48 lanes
+    ((10, 15), False, True, False),   # 150 pixels: four pixels per lane, a ragged last lane
 ]
 
 
@@ -113,17 +115,27 @@ def test_cull_exact(dev, case):
     va = (g.standard_normal((H, W)) * 1e-3).astype(np.float32)
     vd[~kd] = 0.0
     Tn = lambda a: torch.from_numpy(a).to(dev)
+
+    def backward(ray_grads):
+        if dyn:
+            return _C.rasterize_eval3d_dynamic_bwd(T("means"), T("vel"), T("scales"), T("quats"), T("opac"),
+                                                   T("colors"), T("ro"), T("rd"), T("rtd"), tsx, tsy, T("offsets"),
+                                                   T("flat"), Tn(alpha), Tn(last), Tn(vr), Tn(vd), Tn(va),
+                                                   ray_grads=ray_grads)
+        return _C.rasterize_eval3d_bwd(T("means"), T("scales"), T("quats"), T("opac"), T("colors"), T("ro"),
+                                       T("rd"), tsx, tsy, T("offsets"), T("flat"), Tn(alpha), Tn(last), Tn(vr),
+                                       Tn(vd), Tn(va), ray_grads=ray_grads)
+
     if dyn:
-        grads = _C.rasterize_eval3d_dynamic_bwd(T("means"), T("vel"), T("scales"), T("quats"), T("opac"), T("colors"),
-                                                T("ro"), T("rd"), T("rtd"), tsx, tsy, T("offsets"), T("flat"),
-                                                Tn(alpha), Tn(last), Tn(vr), Tn(vd), Tn(va))
         names = ["v_means", "v_velocity", "v_quats", "v_scales", "v_opacity", "v_colors", "v_ray_o", "v_ray_d",
                  "v_time_delta"]
     else:
-        grads = _C.rasterize_eval3d_bwd(T("means"), T("scales"), T("quats"), T("opac"), T("colors"), T("ro"),
-                                        T("rd"), tsx, tsy, T("offsets"), T("flat"), Tn(alpha), Tn(last), Tn(vr),
-                                        Tn(vd), Tn(va))
         names = ["v_means", "v_quats", "v_scales", "v_opacity", "v_colors", "v_ray_o", "v_ray_d"]
+    # with and without per-pixel ray gradients: the kernels differ (pixels per lane, where the
+    # mean gradient and the shared-origin terms are summed)
+    runs = [(names, backward(True))]
+    runs.append(([n for n in names if n not in ("v_ray_o", "v_ray_d")],
+                 [x for n, x in zip(names, backward(False)) if n not in ("v_ray_o", "v_ray_d")]))
     # Gradients of the 1 mm Gaussians centred on pixel rays are ill-conditioned in f32 (the oracle's
     # f32 run misses its f64 run there by as much as the kernel does): judge against the f64 oracle,
     # on every Gaussian / pixel that f32 arithmetic determines, and overall no worse than the f32
@@ -133,7 +145,7 @@ def test_cull_exact(dev, case):
     okw = dict(velocity=s["vel"], ray_time_delta=s["rtd"])
     rg32, rg64 = O.eval3d_bwd(*oargs, **okw), O.eval3d_bwd(*oargs, prec="f64", **okw)
     close = lambda a, b, f=1.0: np.abs(np.asarray(a, np.float64) - b) <= f * (GRAD_ATOL + GRAD_RTOL * np.abs(b))
-    for name, a in zip(names, grads):
+    for name, a in ((n, x) for nm, gr in runs for n, x in zip(nm, gr)):
         a, b32, b64 = np_(a), rg32[name], rg64[name]
         if name in ("v_ray_o", "v_ray_d"):
             a, b32, b64 = a[kd], b32[kd], b64[kd]

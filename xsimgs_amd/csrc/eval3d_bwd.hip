@@ -5,16 +5,17 @@
 //  * batches start at the largest last_id of the tile instead of the end of the tile's list; the
 //    reference loads and skips those trailing batches (every index there exceeds every pixel's
 //    last_id, eval3d_bwd.cu:155-159);
-//  * the gradient of M = S^-1 R^T is accumulated per Gaussian, as Q = sum of v_grd (x) grd +
-//    v_gro (x) gro (dL/dM = Q S R^T), and turned into quaternion / scale gradients once per
-//    Gaussian by the epilogue: quat_scale_to_preci_half_vjp (utils.h:232-263) is linear in dL/dM,
-//    so the sum of per-pair vjps equals the vjp of the sum, and the scale gradient -Q_ii / s_i
-//    sums the same per-pair products as the reference;
+//  * the gradient of M = S^-1 R^T is accumulated per Gaussian, as the symmetric Q = sum of
+//    v_grd (x) grd + v_gro (x) gro (dL/dM = Q S R^T, six entries), and turned into quaternion /
+//    scale gradients once per Gaussian by the epilogue: quat_scale_to_preci_half_vjp
+//    (utils.h:232-263) is linear in dL/dM, so the sum of per-pair vjps equals the vjp of the sum,
+//    and the scale gradient is -Q_ii / s_i;
 //  * per-pair gradients are summed over the 64 lanes of a wavefront by a reduce-scatter that
 //    leaves each component's total on its own lane, and one atomic instruction per 16
 //    components adds them (one lane per component);
-//  * each thread owns two pixels, so the staged Gaussian's LDS reads, the reduction and the atomics
-//    serve both;
+//  * each thread owns two pixels (four in tiles of more than 128 pixels, which a single wavefront
+//    then covers), so the staged Gaussian's LDS reads, the reduction and the atomics serve all of
+//    them;
 //  * divisions in the per-pair math are reciprocal-multiplies (v_rcp_f32, 1 ulp);
 //  * (wavefront, Gaussian) pairs that no pixel of the wavefront can take are skipped unevaluated
 //    (cull_keep); they would add exact zeros.
@@ -105,10 +106,17 @@ XSG_DEV void put(float& a, float v) {
 // dL/dgrd. The hit-distance terms are k1 = dL/dhit_t / |grd|^2 times -grd (gro) and
 // 2 (grd . gro) / |grd|^2 grd - gro (grd). With hit_t = -(grd . gro) / |grd|^2 the whole of
 // dL/dgrd is hit_t (dL/dgro - k1 grd) - k1 gro. Without per-pixel ray or time gradients the mean
-// gradient -M^T dL/dgro is applied once to the sum over the lane's two pixels (vg_sum), and when
-// every pixel shares gro (one ray origin, no motion: GS) the gro part of Q is added once per lane
-// as vg_sum (x) gro instead of once per pixel.
-template <int CDIM, int CS, int K, bool DYN, bool RG, bool FIRST, bool GS>
+// gradient -M^T dL/dgro is applied once to the sum over the lane's pixels (vg_sum).
+//
+// Q: with p = gro + hit_t grd = w / |grd|^2 (the Gaussian's offset from the ray, perpendicular to
+// it, in the normalised frame), dL/dgrd = hit_t dL/dgro - k1 p and gro = p - hit_t grd, so the
+// hit_t terms of Q = dL/dgrd (x) grd + dL/dgro (x) gro cancel exactly and
+//   Q = dL/dgro (x) p - p (x) k1 grd = A |grd|^2 p (x) p - k1 (grd (x) p + p (x) grd),
+// which is symmetric (the loss depends on M only through rotation invariants of gro and grd).
+// Accumulating it in this form skips the two products of size |hit_t| |grd| that cancel (the
+// far-from-the-Gaussian part of the ray), which in float32 lose the scale gradient of thin
+// Gaussians seen from far away.
+template <int CDIM, int CS, int K, bool DYN, bool RG, bool FIRST>
 XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, const float (&rgb)[CS],
                       float (&acc)[K], f3& vg_sum) {
     const float od = dot(e.gro, e.grd);
@@ -131,63 +139,49 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     const float k1 = geo ? px.v_d * fac * e.inv_dd : 0.0f;
     const float Ap = -e.araw * v_alpha_g * e.inv_dd;
     const f3 w = cross(e.c, e.grd);
-    const f3 v_gro = Ap * w - k1 * e.grd;
-    const f3 v_grd = hit_t * (v_gro - k1 * e.grd) - k1 * e.gro;
+    const f3 kg = k1 * e.grd;
+    const f3 v_gro = Ap * w - kg;
     if constexpr (RG || DYN) {
         const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
         put<FIRST>(acc[CDIM + 0], -v_omm.x);
         put<FIRST>(acc[CDIM + 1], -v_omm.y);
         put<FIRST>(acc[CDIM + 2], -v_omm.z);
         if constexpr (DYN) {
-            put<FIRST>(acc[CDIM + 13], -v_omm.x * px.rt);
-            put<FIRST>(acc[CDIM + 14], -v_omm.y * px.rt);
-            put<FIRST>(acc[CDIM + 15], -v_omm.z * px.rt);
+            put<FIRST>(acc[CDIM + 10], -v_omm.x * px.rt);
+            put<FIRST>(acc[CDIM + 11], -v_omm.y * px.rt);
+            put<FIRST>(acc[CDIM + 12], -v_omm.z * px.rt);
             px.v_t -= dot(v_omm, gs.vel);
         }
         if constexpr (RG) {
+            const f3 v_grd = hit_t * (v_gro - kg) - k1 * e.gro;
             px.v_ro = px.v_ro + v_omm;
             px.v_rd = px.v_rd + rows_tmul(gs.r0, gs.r1, gs.r2, v_grd);
         }
     } else {
         vg_sum = FIRST ? v_gro : vg_sum + v_gro;
     }
-    // Q = v_grd (x) grd + v_gro (x) gro; dL/dM = Q S R^T, and the scale gradient -Q_ii / s_i is
-    // the reference's per-pair product of the pair's own values
-    const f3 gd = e.grd, go = e.gro;
-    if constexpr (GS) {
-        put<FIRST>(acc[CDIM + 3], v_grd.x * gd.x);
-        put<FIRST>(acc[CDIM + 4], v_grd.x * gd.y);
-        put<FIRST>(acc[CDIM + 5], v_grd.x * gd.z);
-        put<FIRST>(acc[CDIM + 6], v_grd.y * gd.x);
-        put<FIRST>(acc[CDIM + 7], v_grd.y * gd.y);
-        put<FIRST>(acc[CDIM + 8], v_grd.y * gd.z);
-        put<FIRST>(acc[CDIM + 9], v_grd.z * gd.x);
-        put<FIRST>(acc[CDIM + 10], v_grd.z * gd.y);
-        put<FIRST>(acc[CDIM + 11], v_grd.z * gd.z);
-    } else {
-        put<FIRST>(acc[CDIM + 3], v_grd.x * gd.x + v_gro.x * go.x);
-        put<FIRST>(acc[CDIM + 4], v_grd.x * gd.y + v_gro.x * go.y);
-        put<FIRST>(acc[CDIM + 5], v_grd.x * gd.z + v_gro.x * go.z);
-        put<FIRST>(acc[CDIM + 6], v_grd.y * gd.x + v_gro.y * go.x);
-        put<FIRST>(acc[CDIM + 7], v_grd.y * gd.y + v_gro.y * go.y);
-        put<FIRST>(acc[CDIM + 8], v_grd.y * gd.z + v_gro.y * go.z);
-        put<FIRST>(acc[CDIM + 9], v_grd.z * gd.x + v_gro.z * go.x);
-        put<FIRST>(acc[CDIM + 10], v_grd.z * gd.y + v_gro.z * go.y);
-        put<FIRST>(acc[CDIM + 11], v_grd.z * gd.z + v_gro.z * go.z);
-    }
-    put<FIRST>(acc[CDIM + 12], e.vis * v_alpha_g);
+    // Q (upper triangle, row-major): Q_ij = dL/dgro_i p_j - p_i k1 grd_j
+    const f3 pp = w * e.inv_dd;
+    put<FIRST>(acc[CDIM + 3], pp.x * (v_gro.x - kg.x));
+    put<FIRST>(acc[CDIM + 4], v_gro.x * pp.y - pp.x * kg.y);
+    put<FIRST>(acc[CDIM + 5], v_gro.x * pp.z - pp.x * kg.z);
+    put<FIRST>(acc[CDIM + 6], pp.y * (v_gro.y - kg.y));
+    put<FIRST>(acc[CDIM + 7], v_gro.y * pp.z - pp.y * kg.z);
+    put<FIRST>(acc[CDIM + 8], pp.z * (v_gro.z - kg.z));
+    put<FIRST>(acc[CDIM + 9], e.vis * v_alpha_g);
     px.buf = fmaf(fac, u, px.buf);
 }
 
-// Two pixels per thread: a workgroup of ceil(tile/2) threads (rounded up to whole wavefronts) per
-// tile, thread tr owning the pixels 2 tr and 2 tr + 1 of the tile in row-major order. The staged Gaussian's LDS reads,
-// the wavefront reduction and the atomic adds are shared by both pixels.
-template <int CDIM, bool DYN, bool RG>
-__global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dParams p) {
-    constexpr int NT = kTileThreads / 2;  // threads (and staged Gaussians per batch) at most
+// PX pixels per thread: a workgroup of ceil(tile / PX) threads (rounded up to whole wavefronts) per
+// tile, thread tr owning the pixels PX tr ... PX tr + PX - 1 of the tile in row-major order. The
+// staged Gaussian's LDS reads, the wavefront reduction and the atomic adds are shared by the
+// thread's pixels.
+template <int CDIM, bool DYN, bool RG, int PX>
+__global__ __launch_bounds__(kTileThreads / PX) void eval3d_bwd_kernel(Eval3dParams p) {
+    constexpr int NT = kTileThreads / PX;  // threads (and staged Gaussians per batch) at most
     constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;
     constexpr int CS = CDIM > 0 ? CDIM : 1;
-    constexpr int K = CDIM + 3 + 9 + 1 + (DYN ? 3 : 0);  // colours, mean, M, opacity, velocity
+    constexpr int K = CDIM + 3 + 6 + 1 + (DYN ? 3 : 0);  // colours, mean, Q, opacity, velocity
     __shared__ int32_t s_id[NT];
     __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | M (o - mu)
     __shared__ float4 s_xo[NT];                      // mu and opacity
@@ -206,7 +200,7 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     const int logical = xcd_tile((int)blockIdx.x, nblocks);
     const int cam = logical / n_tiles, tile = logical - cam * n_tiles;
     const int bs = g.tile_w * g.tile_h;
-    const int nthr = (bs + 1) >> 1;
+    const int nthr = (bs + PX - 1) / PX;
     const int tr = threadIdx.x;
     const int lane = __lane_id();
     const int trow = tile / g.n_tiles_w, tcol = tile - trow * g.n_tiles_w;
@@ -215,11 +209,11 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     const int32_t range_end = (gt == nblocks - 1) ? (int32_t)g.n_isects : p.offsets[gt + 1];
     const int64_t hw = (int64_t)g.width * g.height;
 
-    BwdPixel<CS> px[2];
+    BwdPixel<CS> px[PX];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < PX; ++h) {
         BwdPixel<CS>& q = px[h];
-        const int qi = 2 * tr + h;
+        const int qi = PX * tr + h;
         const int ty = qi / g.tile_w, tx = qi - ty * g.tile_w;
         const int i = trow * g.tile_h + ty, j = tcol * g.tile_w + tx;  // utils.h:32-44
         q.inside = qi < bs && i < g.height && j < g.width;
@@ -247,20 +241,30 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     const f3 o0 = mk3(s_origin[0], s_origin[1], s_origin[2]);
     bool same = true;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < PX; ++h)
         same = same && (!px[h].inside || (__float_as_uint(px[h].ro.x) == __float_as_uint(o0.x) &&
                                           __float_as_uint(px[h].ro.y) == __float_as_uint(o0.y) &&
                                           __float_as_uint(px[h].ro.z) == __float_as_uint(o0.z)));
     const bool fixed = !DYN && __syncthreads_and(same);
 
-    const int32_t wave_bin_final = wave_max(max(px[0].bin_final, px[1].bin_final));
+    int32_t lane_bin_final = px[0].bin_final;
+#pragma unroll
+    for (int h = 1; h < PX; ++h) lane_bin_final = max(lane_bin_final, px[h].bin_final);
+    const int32_t wave_bin_final = wave_max(lane_bin_final);
     const int wave = tr >> 6;
     const int nwb = (int)(blockDim.x >> 6);
     {
-        const bool in2[2] = {px[0].inside, px[1].inside};
-        const f3 ro2[2] = {px[0].ro, px[1].ro}, rd2[2] = {px[0].rd, px[1].rd};
-        const float rt2[2] = {px[0].rt, px[1].rt};
-        const RayBundle bun = wave_bundle<2>(in2, ro2, rd2, rt2);
+        bool in2[PX];
+        f3 ro2[PX], rd2[PX];
+        float rt2[PX];
+#pragma unroll
+        for (int h = 0; h < PX; ++h) {
+            in2[h] = px[h].inside;
+            ro2[h] = px[h].ro;
+            rd2[h] = px[h].rd;
+            rt2[h] = px[h].rt;
+        }
+        const RayBundle bun = wave_bundle<PX>(in2, ro2, rd2, rt2);
         if (lane == 0) {
             s_bundle[wave] = bun;
             s_wbf[wave] = wave_bin_final;
@@ -280,12 +284,12 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
             dst_stride[ch] = CDIM;
         } else if (kk < CDIM + 3) {
             dst_base[ch] = p.v_means + (kk - CDIM); dst_stride[ch] = 3;
-        } else if (kk < CDIM + 12) {
-            dst_base[ch] = p.v_mt + (kk - CDIM - 3); dst_stride[ch] = 9;
-        } else if (kk == CDIM + 12) {
+        } else if (kk < CDIM + 9) {
+            dst_base[ch] = p.v_mt + (kk - CDIM - 3); dst_stride[ch] = 6;
+        } else if (kk == CDIM + 9) {
             dst_base[ch] = p.v_opac; dst_stride[ch] = 1;
         } else if (kk < K) {
-            dst_base[ch] = p.v_velocity + (kk - CDIM - 13); dst_stride[ch] = 3;
+            dst_base[ch] = p.v_velocity + (kk - CDIM - 10); dst_stride[ch] = 3;
         } else {
             dst_base[ch] = nullptr; dst_stride[ch] = 0;
         }
@@ -359,17 +363,22 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
                     if constexpr (DYN) gs.vel = mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
                 }
                 const int32_t gidx = batch_end - t;
-                const BwdEval e0 = bwd_eval<DYN, FIXED>(gs, px[0].ro, px[0].rd, px[0].rt,
-                                                        px[0].inside && gidx <= px[0].bin_final);
-                const BwdEval e1 = bwd_eval<DYN, FIXED>(gs, px[1].ro, px[1].rd, px[1].rt,
-                                                        px[1].inside && gidx <= px[1].bin_final);
-                if (counting) {  // wave totals, scalar
-                    n_eval += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[0].inside && gidx <= px[0].bin_final)) +
-                              (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[1].inside && gidx <= px[1].bin_final));
-                    n_contrib += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e0.valid)) +
-                                 (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e1.valid));
+                BwdEval e[PX];
+                bool any_valid = false;
+#pragma unroll
+                for (int h = 0; h < PX; ++h) {
+                    e[h] = bwd_eval<DYN, FIXED>(gs, px[h].ro, px[h].rd, px[h].rt,
+                                                px[h].inside && gidx <= px[h].bin_final);
+                    any_valid = any_valid || e[h].valid;
                 }
-                if (__ballot(e0.valid || e1.valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
+                if (counting) {  // wave totals, scalar
+#pragma unroll
+                    for (int h = 0; h < PX; ++h) {
+                        n_eval += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[h].inside && gidx <= px[h].bin_final));
+                        n_contrib += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e[h].valid));
+                    }
+                }
+                if (__ballot(any_valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
 
                 float rgb[CS];
 #pragma unroll
@@ -386,26 +395,15 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
                 }
                 float acc[K];
                 f3 vg_sum;
-                constexpr bool GS = FIXED && !(RG || DYN);
-                bwd_pair<CDIM, CS, K, DYN, RG, true, GS>(px[0], gs, e0, rgb, acc, vg_sum);
-                bwd_pair<CDIM, CS, K, DYN, RG, false, GS>(px[1], gs, e1, rgb, acc, vg_sum);
+                bwd_pair<CDIM, CS, K, DYN, RG, true>(px[0], gs, e[0], rgb, acc, vg_sum);
+#pragma unroll
+                for (int h = 1; h < PX; ++h)
+                    bwd_pair<CDIM, CS, K, DYN, RG, false>(px[h], gs, e[h], rgb, acc, vg_sum);
                 if constexpr (!(RG || DYN)) {
                     const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, vg_sum);
                     acc[CDIM + 0] = -v_omm.x;
                     acc[CDIM + 1] = -v_omm.y;
                     acc[CDIM + 2] = -v_omm.z;
-                }
-                if constexpr (GS) {
-                    const f3 go = gs.gro_fixed;
-                    acc[CDIM + 3] = fmaf(vg_sum.x, go.x, acc[CDIM + 3]);
-                    acc[CDIM + 4] = fmaf(vg_sum.x, go.y, acc[CDIM + 4]);
-                    acc[CDIM + 5] = fmaf(vg_sum.x, go.z, acc[CDIM + 5]);
-                    acc[CDIM + 6] = fmaf(vg_sum.y, go.x, acc[CDIM + 6]);
-                    acc[CDIM + 7] = fmaf(vg_sum.y, go.y, acc[CDIM + 7]);
-                    acc[CDIM + 8] = fmaf(vg_sum.y, go.z, acc[CDIM + 8]);
-                    acc[CDIM + 9] = fmaf(vg_sum.z, go.x, acc[CDIM + 9]);
-                    acc[CDIM + 10] = fmaf(vg_sum.z, go.y, acc[CDIM + 10]);
-                    acc[CDIM + 11] = fmaf(vg_sum.z, go.z, acc[CDIM + 11]);
                 }
 
                 // wave totals by reduce-scatter: lane l ends with component 16 * chunk + (l >> 2);
@@ -432,7 +430,7 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
         atomicAdd(p.pair_counts + 1, (unsigned long long)n_contrib);
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < PX; ++h) {
         if (px[h].inside) {
             if constexpr (RG) {
                 st3(p.v_ray_o + 3 * px[h].pix, px[h].v_ro);
@@ -443,23 +441,31 @@ __global__ __launch_bounds__(kTileThreads / 2) void eval3d_bwd_kernel(Eval3dPara
     }
 }
 
-// Variants without per-pixel ray gradients exist for CDIM <= kColorLdsMax; larger CDIMs always
-// compute them (the C-ABI then needs the ray-gradient buffers).
+// Variants without per-pixel ray gradients exist for CDIM <= kColorLdsMax, with two or (tiles of
+// more than 128 pixels) four pixels per thread; larger CDIMs always compute them, two pixels per
+// thread (the C-ABI then needs the ray-gradient buffers).
 template <int CDIM>
 int launch_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t s) {
     const int n_blocks = p.g.n_tiles_w * p.g.n_tiles_h * p.g.n_cams;
-    // two pixels per thread, whole wavefronts (the reduction uses every lane)
-    const int bs = ((p.g.tile_w * p.g.tile_h + 1) / 2 + 63) / 64 * 64;
+    const int tile_px = p.g.tile_w * p.g.tile_h;
+    // whole wavefronts (the reduction uses every lane)
+    const int bs2 = ((tile_px + 1) / 2 + 63) / 64 * 64;
     if constexpr (CDIM <= kColorLdsMax) {
         if (!ray_grads) {
-            if (dyn) eval3d_bwd_kernel<CDIM, true, false><<<n_blocks, bs, 0, s>>>(p);
-            else eval3d_bwd_kernel<CDIM, false, false><<<n_blocks, bs, 0, s>>>(p);
+            if (tile_px > 128) {
+                const int bs4 = ((tile_px + 3) / 4 + 63) / 64 * 64;
+                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 4><<<n_blocks, bs4, 0, s>>>(p);
+                else eval3d_bwd_kernel<CDIM, false, false, 4><<<n_blocks, bs4, 0, s>>>(p);
+            } else {
+                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 2><<<n_blocks, bs2, 0, s>>>(p);
+                else eval3d_bwd_kernel<CDIM, false, false, 2><<<n_blocks, bs2, 0, s>>>(p);
+            }
             return XSG_OK;
         }
     }
     if (!p.v_ray_o || !p.v_ray_d) return xsg_fail(XSG_ERR_INVALID, "ray gradient buffers are required for cdim %d", CDIM);
-    if (dyn) eval3d_bwd_kernel<CDIM, true, true><<<n_blocks, bs, 0, s>>>(p);
-    else eval3d_bwd_kernel<CDIM, false, true><<<n_blocks, bs, 0, s>>>(p);
+    if (dyn) eval3d_bwd_kernel<CDIM, true, true, 2><<<n_blocks, bs2, 0, s>>>(p);
+    else eval3d_bwd_kernel<CDIM, false, true, 2><<<n_blocks, bs2, 0, s>>>(p);
     return XSG_OK;
 }
 

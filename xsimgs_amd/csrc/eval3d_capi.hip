@@ -28,9 +28,10 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(float* __restrict__ a, int
 }
 
 // quat_scale_to_preci_half_vjp + quat_to_rotmat_vjp (utils.h:208-263) applied once per Gaussian to
-// the accumulated Q = sum over pairs of v_grd (x) grd + v_gro (x) gro (q[3 i + k] = Q_ik, i the row
-// of M = S^-1 R^T). With rd = R S grd and o - mu = R S gro, dL/dM_ir = sum_k Q_ik s_k R_rk; the
-// scale gradient is -Q_ii / s_i.
+// the accumulated Q = sum over pairs of v_grd (x) grd + v_gro (x) gro, which is symmetric and kept
+// as its upper triangle (Q_00, Q_01, Q_02, Q_11, Q_12, Q_22; index i is the row of M = S^-1 R^T).
+// With rd = R S grd and o - mu = R S gro, dL/dM_ir = sum_k Q_ik s_k R_rk; the scale gradient is
+// -Q_ii / s_i.
 __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const float4* __restrict__ quats,
                                                               const float* __restrict__ scales,
                                                               const float* __restrict__ qacc,
@@ -50,11 +51,8 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const f
     const float R[3][3] = {{1.f - 2.f * (y2 + z2), 2.f * (xy + wz), 2.f * (xz - wy)},
                            {2.f * (xy - wz), 1.f - 2.f * (x2 + z2), 2.f * (yz + wx)},
                            {2.f * (xz + wy), 2.f * (yz - wx), 1.f - 2.f * (x2 + y2)}};
-    float Q[3][3];
-#pragma unroll
-    for (int r = 0; r < 3; ++r)
-#pragma unroll
-        for (int k = 0; k < 3; ++k) Q[r][k] = qacc[9 * i + 3 * r + k];
+    const float* qa = qacc + 6 * i;
+    const float Q[3][3] = {{qa[0], qa[1], qa[2]}, {qa[1], qa[3], qa[4]}, {qa[2], qa[4], qa[5]}};
     float vm[3][3];  // glm v_M[c][r]: dL/dM for row c of M, component r
 #pragma unroll
     for (int cc = 0; cc < 3; ++cc)
@@ -151,7 +149,7 @@ extern "C" int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream) {
 
 extern "C" size_t xsg_eval3d_bwd_workspace_bytes(int64_t n, int cdim) {
     (void)cdim;
-    return (size_t)(n > 0 ? n : 1) * 9 * sizeof(float);
+    return (size_t)(n > 0 ? n : 1) * 6 * sizeof(float);
 }
 
 extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_stream_t stream) {
@@ -174,10 +172,10 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
     p.pair_counts = (unsigned long long*)a->pair_counts;
     const int64_t n = a->n;
     const int64_t ncol = a->cdim > 0 ? (int64_t)a->n_cams * n * a->cdim : 0;
-    const int64_t total = 3 * n + n + ncol + 9 * n + (dyn ? 3 * n : 0);
+    const int64_t total = 3 * n + n + ncol + 6 * n + (dyn ? 3 * n : 0);
     if (total > 0) {
         const unsigned grid = (unsigned)std::min<int64_t>((total + kBlock - 1) / kBlock, 4096);
-        zero_kernel<<<grid, kBlock, 0, s>>>(a->v_means, 3 * n, a->v_opacities, n, a->v_colors, ncol, p.v_mt, 9 * n,
+        zero_kernel<<<grid, kBlock, 0, s>>>(a->v_means, 3 * n, a->v_opacities, n, a->v_colors, ncol, p.v_mt, 6 * n,
                                             a->v_velocity, dyn ? 3 * n : 0);
     }
     if ((int64_t)a->width * a->height > 0) {

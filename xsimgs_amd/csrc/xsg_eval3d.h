@@ -354,7 +354,7 @@ struct Eval3dParams {
     float* v_ray_d;
     float* v_velocity;
     float* v_time;
-    float* v_mt;         // workspace [n, 9]: Q = sum of v_grd (x) grd + v_gro (x) gro per Gaussian
+    float* v_mt;         // workspace [n, 6]: upper triangle of the symmetric Q = sum of v_grd (x) grd + v_gro (x) gro
     unsigned long long* pair_counts;  // optional: += [evaluated, composited] pixel-pairs
 };
 
