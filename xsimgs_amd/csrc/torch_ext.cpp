@@ -263,7 +263,10 @@ Tensor spherical_harmonics_fused_fwd(int64_t degree_to_use, const Tensor& origin
     sh_checks(degree_to_use, origin, positions, coeffs, mask, layout_3kn, coeffs_dc, N, dim);
     if (output.has_value()) { check_same_device({origin, *output}); all_contiguous({*output}); }
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(positions.device());
-    Tensor out = output.has_value() ? *output : at::zeros({N, 3}, positions.options());
+    // without a mask the kernel writes every row; masked rows keep the output's values (zeros here)
+    Tensor out = output.has_value() ? *output
+                 : mask.has_value()   ? at::zeros({N, 3}, positions.options())
+                                      : at::empty({N, 3}, positions.options());
     check_rc(xsg_sh_fwd((int)degree_to_use, fptr(origin), N, (int)dim, fptr(positions), fptr(coeffs), fptr(coeffs_dc),
                         mask.has_value() ? (const uint32_t*)mask->data_ptr() : nullptr, layout_3kn ? 1 : 0,
                         out.data_ptr<float>(), stream_of(positions)));
