@@ -339,9 +339,26 @@ __global__ __launch_bounds__(kBlock) void sh_bwd_kernel(
         const int row_len = dim * 3;
         float* dst = d_coeffs + g0 * row_len;
         const int total = rows * row_len;
-        for (int e = t; e < total; e += kBlock) {
-            const int r = e / row_len, j = e - r * row_len;
-            dst[e] = (j < RL) ? lds[r * S + j] : 0.f;
+        if ((row_len & 3) == 0 && ((uintptr_t)dst & 15) == 0) {
+            // 16-byte stores (a row holds whole vectors), bypassing the caches: written once, read later
+            typedef float v4f __attribute__((ext_vector_type(4)));
+            v4f* dst4 = reinterpret_cast<v4f*>(dst);
+            for (int e4 = t; e4 < total / 4; e4 += kBlock) {
+                const int e = 4 * e4;
+                const int r = e / row_len, j = e - r * row_len;
+                const float* src = lds + r * S + j;
+                v4f v;
+                v.x = (j < RL) ? src[0] : 0.f;
+                v.y = (j + 1 < RL) ? src[1] : 0.f;
+                v.z = (j + 2 < RL) ? src[2] : 0.f;
+                v.w = (j + 3 < RL) ? src[3] : 0.f;
+                __builtin_nontemporal_store(v, dst4 + e4);
+            }
+        } else {
+            for (int e = t; e < total; e += kBlock) {
+                const int r = e / row_len, j = e - r * row_len;
+                dst[e] = (j < RL) ? lds[r * S + j] : 0.f;
+            }
         }
     }
     // d_origin = -sum(d_positions) (sh_bwd.cu:306-314): wave sums, then one partial per block
