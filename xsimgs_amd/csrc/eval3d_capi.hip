@@ -8,23 +8,26 @@ namespace {
 
 constexpr int kBlock = 256;
 
-__global__ __launch_bounds__(kBlock) void zero_kernel(float* __restrict__ a, int64_t na, float* __restrict__ b,
-                                                      int64_t nb, float* __restrict__ c, int64_t nc,
-                                                      float* __restrict__ d, int64_t nd, float* __restrict__ e,
-                                                      int64_t ne) {
+// Zero fill of up to five float arrays, one per grid row (blockIdx.y): 16-byte stores over the
+// aligned body, single floats before and after it.
+struct ZeroList {
+    float* p[5];
+    int64_t n[5];
+};
+
+__global__ __launch_bounds__(kBlock) void zero_kernel(ZeroList z) {
+    float* __restrict__ p = z.p[blockIdx.y];
+    const int64_t n = z.n[blockIdx.y];
+    if (!p || n <= 0) return;
+    const int64_t head = min<int64_t>(n, (int64_t)(((16 - ((uintptr_t)p & 15)) & 15) / 4));
+    const int64_t n4 = (n - head) / 4;
+    const int64_t tail = head + 4 * n4;
     const int64_t stride = (int64_t)gridDim.x * kBlock;
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < na + nb + nc + nd + ne; i += stride) {
-        int64_t k = i;
-        if (k < na) { a[k] = 0.f; continue; }
-        k -= na;
-        if (k < nb) { b[k] = 0.f; continue; }
-        k -= nb;
-        if (k < nc) { c[k] = 0.f; continue; }
-        k -= nc;
-        if (k < nd) { d[k] = 0.f; continue; }
-        k -= nd;
-        e[k] = 0.f;
-    }
+    const int64_t t0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t0 < head) p[t0] = 0.f;
+    if (t0 < n - tail) p[tail + t0] = 0.f;
+    float4* __restrict__ p4 = reinterpret_cast<float4*>(p + head);
+    for (int64_t i = t0; i < n4; i += stride) p4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 // quat_scale_to_preci_half_vjp + quat_to_rotmat_vjp (utils.h:208-263) applied once per Gaussian to
@@ -172,11 +175,13 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
     p.pair_counts = (unsigned long long*)a->pair_counts;
     const int64_t n = a->n;
     const int64_t ncol = a->cdim > 0 ? (int64_t)a->n_cams * n * a->cdim : 0;
-    const int64_t total = 3 * n + n + ncol + 6 * n + (dyn ? 3 * n : 0);
-    if (total > 0) {
-        const unsigned grid = (unsigned)std::min<int64_t>((total + kBlock - 1) / kBlock, 4096);
-        zero_kernel<<<grid, kBlock, 0, s>>>(a->v_means, 3 * n, a->v_opacities, n, a->v_colors, ncol, p.v_mt, 6 * n,
-                                            a->v_velocity, dyn ? 3 * n : 0);
+    const ZeroList zl{{a->v_means, a->v_opacities, a->v_colors, p.v_mt, dyn ? a->v_velocity : nullptr},
+                      {3 * n, n, ncol, 6 * n, dyn ? 3 * n : 0}};
+    int64_t longest = 0;
+    for (int k = 0; k < 5; ++k) longest = std::max(longest, zl.n[k]);
+    if (longest > 0) {
+        const unsigned gx = (unsigned)std::min<int64_t>((longest / 4 + kBlock - 1) / kBlock + 1, 1024);
+        zero_kernel<<<dim3(gx, 5), kBlock, 0, s>>>(zl);
     }
     if ((int64_t)a->width * a->height > 0) {
         rc = eval3d_bwd_launch(a->cdim, dyn, p, s);
