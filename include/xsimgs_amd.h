@@ -3,7 +3,8 @@
  *
  * Every entry point takes device pointers, explicit sizes and a HIP stream, never allocates
  * device memory (scratch comes in through a `workspace` argument sized by the matching
- * *_workspace_bytes query), and returns XSG_OK or a negative error code; xsg_last_error()
+ * *_workspace_bytes query and aligned to 256 bytes, as hipMalloc returns it; a misaligned one is
+ * rejected with XSG_ERR_INVALID), and returns XSG_OK or a negative error code; xsg_last_error()
  * then holds a message (thread-local). Work is enqueued on `stream`; the only blocking call is
  * xsg_isect_count, which copies the intersection total to the host (as the reference's
  * `.item()` does).

@@ -64,3 +64,18 @@ def test_invalid_arguments_fail_before_launch(lib):
     rc = lib.xsg_sh_fwd(7, None, C.c_int64(1), 64, None, None, None, None, 0, None, None)
     assert rc == -1
     assert b"degree" in lib.xsg_last_error().lower()
+
+
+def test_misaligned_workspace_is_rejected_before_launch(lib):
+    """Workspaces must be 256-byte aligned; the pointers here are placeholders that no call reaches."""
+    lib.xsg_last_error.restype = C.c_char_p
+    fake = C.c_void_p(1 << 20)
+    sel = C.c_int(0)
+    rc = lib.xsg_radix_sort_pairs_u64_i32(fake, fake, fake, fake, C.c_int64(1000), 0, 32,
+                                          C.c_void_p((1 << 20) + 16), C.byref(sel), None)
+    assert rc < 0
+    assert b"aligned" in lib.xsg_last_error()
+    rc = lib.xsg_sh_bwd(3, fake, C.c_int64(10), 16, fake, fake, None, 0, fake, 0, fake, None, fake, fake,
+                        C.c_void_p((1 << 20) + 4), None)
+    assert rc < 0
+    assert b"aligned" in lib.xsg_last_error()

@@ -662,6 +662,7 @@ extern "C" int xsg_camera_rays_bwd(int kind, const float* pack, int width, int h
     if (width < 0 || height < 0) return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: negative size");
     if (!pack || !grad_pack || !workspace || (!d_ray_d && (int64_t)width * height > 0))
         return xsg_fail(XSG_ERR_INVALID, "camera_rays_bwd: null pointer");
+    if (const int rc = xsg_check_workspace(workspace, "camera_rays_bwd")) return rc;
     const dim3 grid = image_grid(width > 0 ? width : 1, height > 0 ? height : 1, kGradRows);
     const int nb = (int)(grid.x * grid.y);
     float* part = (float*)workspace;
@@ -702,6 +703,7 @@ extern "C" int xsg_pixel_time_bwd(int kind, const float* pack, int width, int he
     if (n < 0 || (!uv && (width < 0 || height < 0))) return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: bad size");
     if (!pack || !grad_pack || !workspace || (n > 0 && !grad))
         return xsg_fail(XSG_ERR_INVALID, "pixel_time_bwd: null pointer");
+    if (const int rc = xsg_check_workspace(workspace, "pixel_time_bwd")) return rc;
     const dim3 grid = time_bwd_grid(width, height, uv != nullptr, n);
     const int nb = (int)(grid.x * grid.y);
     float* part = (float*)workspace;

@@ -42,6 +42,15 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const f
                                                               float* __restrict__ v_scales) {
     const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (i >= n) return;
+    const float* qa = qacc + 6 * i;
+    const float2 q01 = *reinterpret_cast<const float2*>(qa), q23 = *reinterpret_cast<const float2*>(qa + 2),
+                 q45 = *reinterpret_cast<const float2*>(qa + 4);
+    if (q01.x == 0.f && q01.y == 0.f && q23.x == 0.f && q23.y == 0.f && q45.x == 0.f && q45.y == 0.f) {
+        // no pair reached this Gaussian (most of them): zero gradients without reading its shape
+        v_quats[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        v_scales[3 * i] = 0.f; v_scales[3 * i + 1] = 0.f; v_scales[3 * i + 2] = 0.f;
+        return;
+    }
     const float4 q = quats[i];
     float w = q.x, x = q.y, y = q.z, z = q.w;
     const float inv_norm = rsqrtf(x * x + y * y + z * z + w * w);
@@ -54,8 +63,7 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const f
     const float R[3][3] = {{1.f - 2.f * (y2 + z2), 2.f * (xy + wz), 2.f * (xz - wy)},
                            {2.f * (xy - wz), 1.f - 2.f * (x2 + z2), 2.f * (yz + wx)},
                            {2.f * (xz + wy), 2.f * (yz - wx), 1.f - 2.f * (x2 + y2)}};
-    const float* qa = qacc + 6 * i;
-    const float Q[3][3] = {{qa[0], qa[1], qa[2]}, {qa[1], qa[3], qa[4]}, {qa[2], qa[4], qa[5]}};
+    const float Q[3][3] = {{q01.x, q01.y, q23.x}, {q01.y, q23.y, q45.x}, {q23.x, q45.x, q45.y}};
     float vm[3][3];  // glm v_M[c][r]: dL/dM for row c of M, component r
 #pragma unroll
     for (int cc = 0; cc < 3; ++cc)
@@ -167,6 +175,7 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
         ((a->v_ray_o == nullptr) != (a->v_ray_d == nullptr)) ||
         (dyn && (!a->v_velocity || !a->v_time_delta)) || !workspace)
         return xsg_fail(XSG_ERR_INVALID, "xsg_eval3d_bwd: null buffer");
+    if ((rc = xsg_check_workspace(workspace, "xsg_eval3d_bwd"))) return rc;
     const hipStream_t s = (hipStream_t)stream;
     p.render_alpha = a->render_alpha; p.last_ids = a->last_ids; p.v_rgb = a->v_rgb; p.v_depth = a->v_depth;
     p.v_alpha = a->v_alpha; p.v_means = a->v_means; p.v_opac = a->v_opacities; p.v_colors = a->v_colors;

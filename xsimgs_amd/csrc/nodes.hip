@@ -248,6 +248,7 @@ extern "C" int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_p
     if (rc != XSG_OK) return rc;
     if (a.n_inst > 0 && (!grad_q || !grad_t || !grad_v || !grad_w || !workspace))
         return xsg_fail(XSG_ERR_INVALID, "copy_gs_rigid_transform_bwd: null instance gradient or workspace");
+    if (const int rc2 = xsg_check_workspace(workspace, "copy_gs_rigid_transform_bwd")) return rc2;
     if (a.n > 0 && (!d->inst_w || !v_positions || !v_rotations || !grad_positions || !grad_rotations))
         return xsg_fail(XSG_ERR_INVALID, "copy_gs_rigid_transform_bwd: null tensor");
     if (reinterpret_cast<uintptr_t>(v_rotations) % 16 || reinterpret_cast<uintptr_t>(grad_rotations) % 16)

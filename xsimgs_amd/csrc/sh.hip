@@ -458,6 +458,7 @@ extern "C" int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, c
         return xsg_fail(XSG_ERR_INVALID, "coeffs hold %d bands, degree %d needs %d", dim, degree,
                         ref_dims[degree] - (has_dc ? 1 : 0));
     if (n < 0 || !workspace) return xsg_fail(XSG_ERR_INVALID, "xsg_sh_bwd: bad arguments");
+    if (const int rc = xsg_check_workspace(workspace, "xsg_sh_bwd")) return rc;
     const hipStream_t s = (hipStream_t)stream;
     if (n == 0) {  // d_origin = 0 without a memset node (callers may capture this in a graph)
         sum_partials_kernel<<<1, kBlock, 0, s>>>((const float*)workspace, 0, d_origin);

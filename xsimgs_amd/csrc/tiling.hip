@@ -960,6 +960,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (nt == 0) return XSG_OK;
     if (!workspace || !tpg || !d->means2d || !d->radii || !d->depths)
         return xsg_fail(XSG_ERR_INVALID, "xsg_isect_count: null pointer");
+    if (const int rc2 = xsg_check_workspace(workspace, "xsg_isect_count")) return rc2;
     const hipStream_t s = (hipStream_t)stream;
     const CountWs w = count_ws_layout(g, workspace);
     if (g.kind == XSG_TILING_REGULAR) {
@@ -1043,6 +1044,7 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     if (n_isects < 0 || n_visible <= 0 || n_visible > cw.n_virtual || n_runs <= 0 || n_runs > n_isects ||
         !count_workspace || !isect_ids || !flatten_ids)
         return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: bad arguments");
+    if (const int rc2 = xsg_check_workspace(count_workspace, "xsg_isect_fill")) return rc2;
     const hipStream_t s = (hipStream_t)stream;
     const int64_t m = n_visible;
     const int64_t n_per_cam = g.n_cams > 1 ? g.n : 0;
@@ -1056,6 +1058,7 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
         return XSG_OK;
     }
     if (!fill_workspace) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: null fill workspace");
+    if (const int rc2 = xsg_check_workspace(fill_workspace, "xsg_isect_fill")) return rc2;
     if (!g.sort) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: sorted fill of a descriptor counted with sort = 0");
     if (g.ntx > kMaxSortedCols)
         return xsg_fail(XSG_ERR_UNSUPPORTED, "sorted binning supports at most %d tile columns (got %d)", kMaxSortedCols,
@@ -1143,6 +1146,7 @@ extern "C" int xsg_radix_sort_pairs_u64_i32(int64_t* keys, int32_t* vals, int64_
     if (n == 0 || begin_bit == end_bit) return XSG_OK;
     if (!workspace || !keys || !vals || !keys_alt || !vals_alt)
         return xsg_fail(XSG_ERR_INVALID, "xsg_radix_sort_pairs_u64_i32: null pointer");
+    if (const int rc = xsg_check_workspace(workspace, "xsg_radix_sort_pairs_u64_i32")) return rc;
     uint32_t* hist = (uint32_t*)workspace;
     uint32_t* dtot = (uint32_t*)((char*)workspace + align256(4 * (size_t)kRadix * sort_blocks(n)));
     using K = uint64_t;

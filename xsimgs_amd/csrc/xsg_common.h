@@ -13,6 +13,15 @@
 // Error reporting shared by every C-ABI entry point (defined in capi.hip).
 int xsg_fail(int code, const char* fmt, ...);
 
+// Workspaces are 256-byte aligned (as hipMalloc and torch's allocator return them): the kernels'
+// vector accesses into them rely on it.
+constexpr uintptr_t kWorkspaceAlign = 256;
+inline int xsg_check_workspace(const void* ws, const char* who) {
+    if (((uintptr_t)ws & (kWorkspaceAlign - 1)) != 0)
+        return xsg_fail(XSG_ERR_INVALID, "%s: workspace must be %d-byte aligned", who, (int)kWorkspaceAlign);
+    return XSG_OK;
+}
+
 // Host-side dispatch over the camera models: calls f(std::integral_constant<int, KIND>{}).
 template <typename F>
 int xsg_with_camera_kind(int kind, F&& f) {
