@@ -64,43 +64,59 @@ XSG_DEV uint32_t digit_of(K key, int shift, int bits) {
     return (uint32_t)((key >> shift) & (K)((1u << bits) - 1u));
 }
 
-// n_dev (optional): the element count read on the device, at most n; the grid covers n. A block
-// covers kSortBlock * ITEMS keys.
+// A tile is kSortBlock * ITEMS keys; the tiles holding keys are [0, ceil(n / tile)). n_dev
+// (optional): the element count read on the device, at most n, with the grid sized on the host for
+// n: the upsweep and downsweep workgroups then loop over the tiles (grid stride), so that a grid
+// smaller than n's tile count can serve a count that is usually far below n.
+template <int ITEMS>
+XSG_DEV unsigned active_tiles(int64_t n, const uint32_t* n_dev) {
+    if (n_dev) n = min(n, (int64_t)*n_dev);
+    return (unsigned)((n + kSortBlock * ITEMS - 1) / (kSortBlock * ITEMS));
+}
+
 template <typename K, int ITEMS = kSortItems>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict__ keys, int64_t n, int shift,
                                                             int bits, uint32_t* __restrict__ hist, unsigned nb,
                                                             const uint32_t* __restrict__ n_dev) {
     if (n_dev) n = min(n, (int64_t)*n_dev);
+    const unsigned nt = active_tiles<ITEMS>(n, nullptr);
     __shared__ uint32_t cnt[kWaves][kRadix];
     const int t = threadIdx.x, wave = t >> 6;
+    for (unsigned tile = blockIdx.x; tile < nt; tile += gridDim.x) {
+        __syncthreads();  // the previous tile's sums are read
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) cnt[w][t] = 0;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * (kSortBlock * ITEMS);
+        for (int w = 0; w < kWaves; ++w) cnt[w][t] = 0;
+        __syncthreads();
+        const int64_t base = (int64_t)tile * (kSortBlock * ITEMS);
 #pragma unroll 4
-    for (int k = 0; k < ITEMS; ++k) {
-        const int64_t idx = base + (int64_t)k * kSortBlock + t;
-        if (idx < n) atomicAdd(&cnt[wave][digit_of<K>(keys[idx], shift, bits)], 1u);
-    }
-    __syncthreads();
-    uint32_t s = 0;
+        for (int k = 0; k < ITEMS; ++k) {
+            const int64_t idx = base + (int64_t)k * kSortBlock + t;
+            if (idx < n) atomicAdd(&cnt[wave][digit_of<K>(keys[idx], shift, bits)], 1u);
+        }
+        __syncthreads();
+        uint32_t s = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) s += cnt[w][t];
-    hist[(int64_t)t * nb + blockIdx.x] = s;
+        for (int w = 0; w < kWaves; ++w) s += cnt[w][t];
+        hist[(int64_t)t * nb + tile] = s;
+    }
 }
 
-// one block per digit: exclusive scan of hist[d * nb .. d * nb + nb), total into digit_total[d]
+// one block per digit: exclusive scan of hist[d * nb .. d * nb + nt) over the nt tiles holding keys,
+// total into digit_total[d]
+template <int ITEMS>
 __global__ __launch_bounds__(kSortBlock) void radix_scan_hist(uint32_t* __restrict__ hist, unsigned nb,
-                                                              uint32_t* __restrict__ digit_total) {
+                                                              uint32_t* __restrict__ digit_total, int64_t n,
+                                                              const uint32_t* __restrict__ n_dev) {
     __shared__ uint32_t lds[kWaves];
+    const unsigned nt = active_tiles<ITEMS>(n, n_dev);
     uint32_t* h = hist + (int64_t)blockIdx.x * nb;
     uint32_t carry = 0;
-    for (unsigned start = 0; start < nb; start += kSortBlock) {
+    for (unsigned start = 0; start < nt; start += kSortBlock) {
         const unsigned i = start + threadIdx.x;
-        const uint32_t v = i < nb ? h[i] : 0u;
+        const uint32_t v = i < nt ? h[i] : 0u;
         uint32_t tot;
         const uint32_t ex = block_exclusive_scan<uint32_t>(v, lds, tot);
-        if (i < nb) h[i] = carry + ex;
+        if (i < nt) h[i] = carry + ex;
         carry += tot;
     }
     if (threadIdx.x == 0) digit_total[blockIdx.x] = carry;
@@ -139,92 +155,101 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
     __shared__ K skeys[kTile];
     __shared__ V svals[kTile];
     const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
-    const int64_t tile0 = (int64_t)blockIdx.x * kTile;
-    const int n_tile = (int)min<int64_t>(kTile, n - tile0);
+    const unsigned nt = active_tiles<ITEMS>(n, nullptr);
+    uint32_t dprefix;
     {
         uint32_t tot;
-        const uint32_t dprefix = block_exclusive_scan<uint32_t>(digit_total[t], scan_lds, tot);
-        gbase[t] = dprefix + hist[(int64_t)t * nb + blockIdx.x];
+        dprefix = block_exclusive_scan<uint32_t>(digit_total[t], scan_lds, tot);
     }
+    for (unsigned tile = blockIdx.x; tile < nt; tile += gridDim.x) {
+        __syncthreads();  // the previous tile's LDS contents are consumed
+        const int64_t tile0 = (int64_t)tile * kTile;
+        const int n_tile = (int)min<int64_t>(kTile, n - tile0);
+        gbase[t] = dprefix + hist[(int64_t)t * nb + tile];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) wcnt[w][t] = 0;
-    __syncthreads();
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    K key[kSteps];
-    V val[kSteps];
-    uint32_t rank[kSteps];
-    const int seg0 = wave * kSeg;
+        for (int w = 0; w < kWaves; ++w) wcnt[w][t] = 0;
+        __syncthreads();
+        const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        K key[kSteps];
+        V val[kSteps];
+        uint32_t rank[kSteps];
+        const int seg0 = wave * kSeg;
 #pragma unroll
-    for (int r = 0; r < kSteps; ++r) {
-        const int li = seg0 + r * 64 + lane;
-        const bool valid = li < n_tile;
-        key[r] = 0;
-        val[r] = 0;
-        uint32_t d = 0;
-        if (valid) {
-            key[r] = keys_in[tile0 + li];
-            val[r] = vals_in[tile0 + li];
-            d = digit_of<K>(key[r], shift, bits);
+        for (int r = 0; r < kSteps; ++r) {
+            const int li = seg0 + r * 64 + lane;
+            const bool valid = li < n_tile;
+            key[r] = 0;
+            val[r] = 0;
+            uint32_t d = 0;
+            if (valid) {
+                key[r] = keys_in[tile0 + li];
+                val[r] = vals_in[tile0 + li];
+                d = digit_of<K>(key[r], shift, bits);
+            }
+            uint64_t peers = __ballot(valid);
+            for (int b = 0; b < bits; ++b) {
+                const uint64_t m = __ballot((d >> b) & 1u);
+                peers &= ((d >> b) & 1u) ? m : ~m;
+            }
+            const uint32_t before = (uint32_t)__popcll(peers & lt_mask);
+            const uint32_t base = valid ? wcnt[wave][d] : 0u;
+            rank[r] = base + before;
+            if (valid && before == 0) wcnt[wave][d] = base + (uint32_t)__popcll(peers);
         }
-        uint64_t peers = __ballot(valid);
-        for (int b = 0; b < bits; ++b) {
-            const uint64_t m = __ballot((d >> b) & 1u);
-            peers &= ((d >> b) & 1u) ? m : ~m;
-        }
-        const uint32_t before = (uint32_t)__popcll(peers & lt_mask);
-        const uint32_t base = valid ? wcnt[wave][d] : 0u;
-        rank[r] = base + before;
-        if (valid && before == 0) wcnt[wave][d] = base + (uint32_t)__popcll(peers);
-    }
-    __syncthreads();
-    {  // per digit: exclusive prefix over the waves, block-local exclusive prefix over digits
-        uint32_t c[kWaves], s = 0;
+        __syncthreads();
+        {  // per digit: exclusive prefix over the waves, block-local exclusive prefix over digits
+            uint32_t c[kWaves], s = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) { c[w] = wcnt[w][t]; wcnt[w][t] = s; s += c[w]; }
-        uint32_t tot;
-        lpre[t] = block_exclusive_scan<uint32_t>(s, scan_lds, tot);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kSteps; ++r) {
-        const int li = seg0 + r * 64 + lane;
-        if (li < n_tile) {
-            const uint32_t d = digit_of<K>(key[r], shift, bits);
-            const uint32_t pos = lpre[d] + wcnt[wave][d] + rank[r];
-            skeys[pos] = key[r];
-            svals[pos] = val[r];
+            for (int w = 0; w < kWaves; ++w) { c[w] = wcnt[w][t]; wcnt[w][t] = s; s += c[w]; }
+            uint32_t tot;
+            lpre[t] = block_exclusive_scan<uint32_t>(s, scan_lds, tot);
         }
-    }
-    __syncthreads();
-    for (int i = t; i < n_tile; i += kSortBlock) {
-        const K k = skeys[i];
-        const uint32_t d = digit_of<K>(k, shift, bits);
-        out.put((int64_t)gbase[d] + (i - lpre[d]), k, svals[i]);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kSteps; ++r) {
+            const int li = seg0 + r * 64 + lane;
+            if (li < n_tile) {
+                const uint32_t d = digit_of<K>(key[r], shift, bits);
+                const uint32_t pos = lpre[d] + wcnt[wave][d] + rank[r];
+                skeys[pos] = key[r];
+                svals[pos] = val[r];
+            }
+        }
+        __syncthreads();
+        for (int i = t; i < n_tile; i += kSortBlock) {
+            const K k = skeys[i];
+            const uint32_t d = digit_of<K>(k, shift, bits);
+            out.put((int64_t)gbase[d] + (i - lpre[d]), k, svals[i]);
+        }
     }
 }
 
 // Runs every pass of a stable LSD sort over bits [begin_bit, end_bit) (8-bit digits, last one
 // narrower) ping-ponging between (k0, v0) and (k1, v1); the last pass goes through `final_out`.
 // Returns the number of passes. hist must hold kRadix * sort_blocks<ITEMS>(n) words, dtot kRadix
-// words. With n_dev, the device-side count (at most n) is sorted; n only sizes the grid, so a sort
-// whose count is usually far below n uses fewer ITEMS per block to spread over more blocks.
+// words. With n_dev, the device-side count (at most n) is sorted; n only bounds it, so a sort whose
+// count is usually far below n uses fewer ITEMS per block to spread over more blocks, and its
+// grids are capped at kDevCountGrid workgroups that loop over the tiles holding keys (dispatching
+// workgroups for empty tiles costs about as much as sorting a full one).
+constexpr unsigned kDevCountGrid = 256;
 template <typename K, typename V, typename FinalOut, int ITEMS = kSortItems>
 inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
                              uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s,
                              const uint32_t* n_dev = nullptr) {
     const unsigned nb = sort_blocks<ITEMS>(n);
+    const unsigned grid = n_dev ? min(nb, kDevCountGrid) : nb;
     int passes = 0;
     K* src_k = k0; V* src_v = v0; K* dst_k = k1; V* dst_v = v1;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
         const int bits = min(8, end_bit - shift);
         const bool last = shift + 8 >= end_bit;
-        radix_upsweep<K, ITEMS><<<nb, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
-        radix_scan_hist<<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot);
+        radix_upsweep<K, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
+        radix_scan_hist<ITEMS><<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot, n, n_dev);
         if (last) {
-            radix_downsweep<K, V, FinalOut, ITEMS><<<nb, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits,
-                                                                             hist, dtot, nb, final_out, n_dev);
+            radix_downsweep<K, V, FinalOut, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits,
+                                                                               hist, dtot, nb, final_out, n_dev);
         } else {
-            radix_downsweep<K, V, PlainOut<K, V>, ITEMS><<<nb, kSortBlock, 0, s>>>(
+            radix_downsweep<K, V, PlainOut<K, V>, ITEMS><<<grid, kSortBlock, 0, s>>>(
                 src_k, src_v, n, shift, bits, hist, dtot, nb, PlainOut<K, V>{dst_k, dst_v}, n_dev);
         }
         ++passes;
