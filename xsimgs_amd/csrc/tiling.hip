@@ -250,11 +250,14 @@ __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ p
 }
 
 // Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
+// With m_dev, the visible count (the packed total after the nb block partials) is stored there for the
+// kernels queued ahead of the count readback.
 __global__ __launch_bounds__(kBlock) void compact_kernel(
     int64_t n_virtual, const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vkey,
     const uint64_t* __restrict__ partials, uint32_t* __restrict__ comp_id, uint32_t* __restrict__ comp_off,
-    uint32_t* __restrict__ comp_key) {
+    uint32_t* __restrict__ comp_key, unsigned nb, uint32_t* __restrict__ m_dev) {
     __shared__ uint64_t lds[kWaves];
+    if (m_dev && blockIdx.x == 0 && threadIdx.x == 0) *m_dev = (uint32_t)(partials[nb] >> 32);
     uint64_t carry = partials[blockIdx.x];
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     for (int k = 0; k < kCountItems; ++k) {
@@ -364,9 +367,6 @@ constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of s
 constexpr int kColGroup = 4;    // columns per wavefront in write_runs_kernel
 
 // the visible-span count from the packed grand total of the count scan, for device-sized kernels
-__global__ void visible_count_kernel(const uint64_t* __restrict__ packed_total, uint32_t* __restrict__ m_dev) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) *m_dev = (uint32_t)(*packed_total >> 32);
-}
 
 // rows covered by each depth-ordered visible instance -> exclusive run offsets (reduce / scan)
 __global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
@@ -995,11 +995,10 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb, w.cpart, rb->dev);
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
     compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
-                                           w.comp_key);
+                                           w.comp_key, w.nb, g.sort ? w.m_dev : nullptr);
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
         // (stable, 4 passes, result back in comp_*), then their row-run offsets
-        visible_count_kernel<<<1, 64, 0, s>>>(w.partials + w.nb, w.m_dev);
         radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems>(
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev);
