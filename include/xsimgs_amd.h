@@ -231,10 +231,14 @@ size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects,
                                       int64_t n_runs);
 /* Pass 2: intersection keys ((cam | tile) << 32 | depth bits) and flattened Gaussian ids
  * (cam * n + gaussian); sorted by key bits [0, 32 + key_bits_above_32) with ties in fill order
- * when `sort`, else in the reference's fill order. Consumes (overwrites) count_workspace. */
+ * when `sort`, else in the reference's fill order. Consumes (overwrites) count_workspace.
+ * tile_offsets (optional, sorted fills only; NULL skips it): the n_tile_offsets =
+ * n_cams * n_tiles_h * n_tiles_w offsets that xsg_isect_offset_encode would compute from the
+ * sorted keys, produced by the fill itself (extension: it saves the search that
+ * isect_offset_encode, tiling_common.cu:25-71, runs over the keys). */
 int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int64_t n_runs,
                    int sort, void* count_workspace, void* fill_workspace, int64_t* isect_ids,
-                   int32_t* flatten_ids, xsg_stream_t stream);
+                   int32_t* flatten_ids, int32_t* tile_offsets, int64_t n_tile_offsets, xsg_stream_t stream);
 
 /* offsets [n_cams, n_tiles_h, n_tiles_w]: first sorted index of every (camera, tile) */
 int xsg_isect_offset_encode(const int64_t* isect_ids, int64_t n_isects, int n_tiles_w, int n_tiles_h,

@@ -165,18 +165,20 @@ def test_hip_path_reproduces_fixture(dev, name):
 
     # binning from the fixture's projections: bit-exact
     m2f, rf, df, ff = T("means2d"), T("radii"), T("depths"), T("ut_flags")
-    if spec.kind == "pinhole":
-        tpg, ids, fl = _C.isect_regular_tiles(m2f, rf, df, W, H, tsx, tsy)
-        if "isect_ids_unsorted" in f:
-            _, ids_u, fl_u = _C.isect_regular_tiles(m2f, rf, df, W, H, tsx, tsy, sort=False)
-            assert np.array_equal(np_(ids_u), f["isect_ids_unsorted"])
-            assert np.array_equal(np_(fl_u), f["flatten_ids_unsorted"])
-    elif spec.kind == "lidar":
-        tpg, ids, fl = _C.isect_lidar_tiles(pack, means, vel, scales, quats, opac, ff, m2f, rf, df, T("elev"), tsx,
-                                            W, H)
-    else:
-        tpg, ids, fl = _C.isect_spherical_tiles(pack, means, vel, scales, quats, opac, ff, m2f, rf, df, tsx, tsy,
-                                                W, H)
+
+    def binning(**kw):
+        if spec.kind == "pinhole":
+            return _C.isect_regular_tiles(m2f, rf, df, W, H, tsx, tsy, **kw)
+        if spec.kind == "lidar":
+            return _C.isect_lidar_tiles(pack, means, vel, scales, quats, opac, ff, m2f, rf, df, T("elev"), tsx, W, H,
+                                        **kw)
+        return _C.isect_spherical_tiles(pack, means, vel, scales, quats, opac, ff, m2f, rf, df, tsx, tsy, W, H, **kw)
+
+    tpg, ids, fl = binning()
+    if spec.kind == "pinhole" and "isect_ids_unsorted" in f:
+        _, ids_u, fl_u = binning(sort=False)
+        assert np.array_equal(np_(ids_u), f["isect_ids_unsorted"])
+        assert np.array_equal(np_(fl_u), f["flatten_ids_unsorted"])
     assert np.array_equal(np_(tpg), f["tiles_per_gauss"])
     nth, ntw = f["offsets"].shape
     if spec.kind == "pinhole":
@@ -186,6 +188,11 @@ def test_hip_path_reproduces_fixture(dev, name):
         _check_seam_keys(np_(ids), np_(fl), f["isect_ids"], f["flatten_ids"], ntw * nth)
     off = _C.isect_offset_encode(ids, ntw, nth)
     assert np.array_equal(np_(off), f["offsets"])
+    # the sorted fill's own tile offsets (extension, what ut_gs_tiling uses) are the encoder's
+    fill_off = torch.full((nth, ntw), -7, dtype=torch.int32, device=dev)
+    _, ids2, _ = binning(tile_offsets=fill_off)
+    assert np.array_equal(np_(ids2), np_(ids))
+    assert np.array_equal(np_(fill_off), f["offsets"])
 
     # rays
     ro, rd = cam.camera_rays(W, H)

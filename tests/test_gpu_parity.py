@@ -114,6 +114,33 @@ def test_isect_regular_bitexact(dev, cfg0, sort):
         assert np.array_equal(np_(off), O.offset_encode(rids, 16, 16))
 
 
+def test_fill_tile_offsets(dev, cfg0):
+    """The sorted fill's tile offsets equal isect_offset_encode on its keys: one camera, a batched rig
+    of three (camera bits in the keys), and no intersections at all (every offset 0)."""
+    sc, st = cfg0
+    spec = sc.cameras[0]
+    _, (flags, radii, m2, dep) = _ut(st, spec, dev)
+    ntx, nty = (spec.width + 15) // 16, (spec.height + 15) // 16
+    off = torch.full((nty, ntx), -7, dtype=torch.int32, device=dev)
+    _, ids, _ = _C.isect_regular_tiles(m2, radii, dep, spec.width, spec.height, 16, 16, tile_offsets=off)
+    assert np.array_equal(np_(off), np_(_C.isect_offset_encode(ids, ntx, nty)))
+    # three cameras: the second sees nothing, the third a shifted copy
+    m2b = torch.stack([m2, m2 + 1e6, m2 + 3.5]).contiguous()
+    rb = torch.stack([radii, radii, radii]).contiguous()
+    db = torch.stack([dep, dep, dep * 1.5]).contiguous()
+    offb = torch.full((3, nty, ntx), -7, dtype=torch.int32, device=dev)
+    _, idsb, _ = _C.isect_regular_tiles_batched(m2b, rb, db, spec.width, spec.height, 16, 16, tile_offsets=offb)
+    assert np.array_equal(np_(offb), np_(_C.isect_offset_encode(idsb, ntx, nty, 3)))
+    off0 = torch.full((nty, ntx), -7, dtype=torch.int32, device=dev)
+    _, ids0, _ = _C.isect_regular_tiles(m2 + 1e6, radii, dep, spec.width, spec.height, 16, 16, tile_offsets=off0)
+    assert ids0.numel() == 0 and int(off0.abs().max()) == 0
+    with pytest.raises(RuntimeError, match="tile offsets"):
+        _C.isect_regular_tiles(m2, radii, dep, spec.width, spec.height, 16, 16,
+                               tile_offsets=torch.empty(ntx * nty + 1, dtype=torch.int32, device=dev))
+    with pytest.raises(RuntimeError, match="sorted fill"):
+        _C.isect_regular_tiles(m2, radii, dep, spec.width, spec.height, 16, 16, sort=False, tile_offsets=off)
+
+
 def test_isect_regular_edge_cases(dev):
     # empty input, all-culled input, Gaussians on tile borders and outside the image, negative depth
     W, H = 100, 70

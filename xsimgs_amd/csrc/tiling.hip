@@ -588,7 +588,8 @@ __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restric
 // Chunks of 1024 consecutive entries, one per thread (coalesced), eight chunks' loads in flight.
 constexpr int kScanThreads = 1024;
 constexpr int kScanChunks = 8;
-__global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n) {
+__global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n,
+                                                                 int32_t* __restrict__ offsets) {
     __shared__ uint32_t lds[kScanThreads / 64];
     const int wave = threadIdx.x >> 6;
     uint32_t carry = 0;
@@ -613,7 +614,10 @@ __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __res
                 tot += y;
             }
             __syncthreads();
-            if (i < n) a[i] = carry + before + inc - x[j];
+            if (i < n) {
+                a[i] = carry + before + inc - x[j];
+                if (offsets) offsets[i] = (int32_t)(carry + before + inc - x[j]);
+            }
             carry += tot;
         }
     }
@@ -1034,11 +1038,24 @@ extern "C" size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_
 
 extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int64_t n_runs,
                               int sort, void* count_workspace, void* fill_workspace, int64_t* isect_ids,
-                              int32_t* flatten_ids, xsg_stream_t stream) {
+                              int32_t* flatten_ids, int32_t* tile_offsets, int64_t n_tile_offsets,
+                              xsg_stream_t stream) {
     Geometry g;
     int rc = geometry_of(d, g);
     if (rc) return rc;
-    if (n_isects == 0) return XSG_OK;
+    if (tile_offsets) {
+        if (!sort) return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: tile offsets come with a sorted fill");
+        if (n_tile_offsets != (int64_t)g.n_cams * g.n_tiles)
+            return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: %lld tile offsets for a grid of %d x %d x %d tiles",
+                            (long long)n_tile_offsets, g.n_cams, g.nty, g.ntx);
+    }
+    if (n_isects == 0) {  // tiling_common.cu:86-88: every offset 0
+        if (tile_offsets)
+            fill_i32_kernel<<<xsg_blocks(n_tile_offsets, kBlock), kBlock, 0, (hipStream_t)stream>>>(tile_offsets,
+                                                                                                   n_tile_offsets, 0);
+        XSG_TRY_LAUNCH("isect_fill");
+        return XSG_OK;
+    }
     const CountWs cw = count_ws_layout(g, count_workspace);
     if (n_isects < 0 || n_visible <= 0 || n_visible > cw.n_virtual || n_runs <= 0 || n_runs > n_isects ||
         !count_workspace || !isect_ids || !flatten_ids)
@@ -1086,7 +1103,9 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     const int64_t n_tile_slots = (int64_t)n_real * g.ntx;
     tile_prefix_kernel<<<xsg_blocks(n_tile_slots * 64, kBlock), kBlock, 0, s>>>(fw.slots, fw.seg_base, n_real,
                                                                                g.ntx, fw.tile_tot);
-    tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots);
+    // the exclusive scan over the tiles is each tile's first output position: the reference's
+    // offsets of the sorted keys (negative-depth runs follow every tile)
+    tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots, tile_offsets);
     // the writers (one extra workgroup for the negative-depth runs)
     const int n_groups = (g.ntx + kColGroup - 1) / kColGroup;
     write_runs_kernel<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base,

@@ -6,7 +6,7 @@ compositor, in the reference's order.
 """
 import torch
 
-from .._C import mask_radii, isect_offset_encode, eval3d_supported_ndims
+from .._C import mask_radii, eval3d_supported_ndims
 from .rasterize import ut_gs_rasterize
 from .rasterize_dynamic import ut_gs_dynamic_rasterize
 
@@ -20,14 +20,15 @@ def ut_gs_tiling(camera, points, scale, rotation, width: int, height: int, point
             width=width, height=height, ut_alpha=ut_alpha, ut_beta=ut_beta, ut_kappa=ut_kappa, use_phm=use_phm)
         if packed_particle_mask is not None:
             mask_radii(packed_particle_mask, radii)
+        n_tiles_width = (width + tile_size_x - 1) // tile_size_x
+        n_tiles_height = (height + tile_size_y - 1) // tile_size_y
+        # the sorted fill writes the tile offsets that isect_offset_encode would compute from its keys
+        tile_gs_offsets = torch.empty((n_tiles_height, n_tiles_width), dtype=torch.int32, device=points.device)
         tiles_per_gs, isect_ids, flatten_ids = camera.isect_gs_tiles(
             points=points, points_velocity=points_velocity, scale=scale, rotation=rotation, opacity=opacity,
             flags=flags, means2d=means2d, radii=radii, depths=depth, width=width, height=height,
             ut_alpha=ut_alpha, ut_beta=ut_beta, ut_kappa=ut_kappa, tile_size_x=tile_size_x,
-            tile_size_y=tile_size_y, sort=True, double_buffer=True)
-        n_tiles_width = (width + tile_size_x - 1) // tile_size_x
-        n_tiles_height = (height + tile_size_y - 1) // tile_size_y
-        tile_gs_offsets = isect_offset_encode(isect_ids, tile_width=n_tiles_width, tile_height=n_tiles_height)
+            tile_size_y=tile_size_y, sort=True, double_buffer=True, tile_offsets=tile_gs_offsets)
     return dict(means2d=means2d, radii=radii, depth=depth, isect_offsets=tile_gs_offsets, flatten_ids=flatten_ids)
 
 
