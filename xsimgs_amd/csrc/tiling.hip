@@ -214,18 +214,11 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     }
 }
 
-// single block: exclusive scan of the block partials in place, grand total at partials[nb]; with
-// `cpart` (pairs per block), also the exact 64-bit sums of cpart[2b] and cpart[2b + 1] at
-// partials[nb + 1] and partials[nb + 2] (the packed scan's count field is 32 bits wide, so the
-// host checks the exact intersection total instead)
+// single block: exclusive scan of the block partials in place, grand total at partials[nb]
 template <typename T>
-__global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb,
-                                                               const uint64_t* __restrict__ cpart,
-                                                               uint64_t* __restrict__ publish = nullptr) {
+__global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb) {
     __shared__ T lds[kWaves];
-    __shared__ uint64_t lds64[kWaves];
     T carry = 0;
-    uint64_t exact = 0, exact2 = 0;
     for (unsigned start = 0; start < nb; start += kBlock) {
         const unsigned i = start + threadIdx.x;
         const T v = i < nb ? partials[i] : (T)0;
@@ -233,32 +226,42 @@ __global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ p
         const T ex = block_exclusive_scan<T>(v, lds, tot);
         if (i < nb) partials[i] = carry + ex;
         carry += tot;
-        if (cpart) {
-            exact += block_reduce_sum<uint64_t>(i < nb ? cpart[2 * i] : 0ull, lds64);
-            exact2 += block_reduce_sum<uint64_t>(i < nb ? cpart[2 * i + 1] : 0ull, lds64);
-        }
     }
-    if (threadIdx.x == 0) {
-        partials[nb] = carry;
-        if (cpart) { partials[nb + 1] = (T)exact; partials[nb + 2] = (T)exact2; }
-        if (publish) {  // the three totals, also into host memory (vector stores)
-            publish[0] = (uint64_t)carry;
+    if (threadIdx.x == 0) partials[nb] = carry;
+}
+
+// Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
+// Each block sums the (packed) partials of the count blocks before it, which places its instances.
+// Block 0 also sums them all: the packed total (visible << 32 | count, whose count field may carry)
+// and the exact 64-bit intersection and row-run totals from cpart go to `publish` (mapped host
+// memory, read by the host after an event) and the visible count to m_dev, for the kernels queued
+// ahead of that readback.
+__global__ __launch_bounds__(kBlock) void compact_kernel(
+    int64_t n_virtual, const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vkey,
+    const uint64_t* __restrict__ partials, const uint64_t* __restrict__ cpart, uint32_t* __restrict__ comp_id,
+    uint32_t* __restrict__ comp_off, uint32_t* __restrict__ comp_key, unsigned nb, uint32_t* __restrict__ m_dev,
+    uint64_t* __restrict__ publish) {
+    __shared__ uint64_t lds[kWaves];
+    uint64_t before = 0;
+    for (unsigned b = threadIdx.x; b < blockIdx.x; b += kBlock) before += partials[b];
+    uint64_t carry = block_reduce_sum<uint64_t>(before, lds);
+    if (blockIdx.x == 0) {  // block-uniform
+        uint64_t tot = 0, exact = 0, exact2 = 0;
+        for (unsigned b = threadIdx.x; b < nb; b += kBlock) {
+            tot += partials[b];
+            exact += cpart[2 * b];
+            exact2 += cpart[2 * b + 1];
+        }
+        tot = block_reduce_sum<uint64_t>(tot, lds);
+        exact = block_reduce_sum<uint64_t>(exact, lds);
+        exact2 = block_reduce_sum<uint64_t>(exact2, lds);
+        if (threadIdx.x == 0) {
+            if (m_dev) *m_dev = (uint32_t)(tot >> 32);
+            publish[0] = tot;
             publish[1] = exact;
             publish[2] = exact2;
         }
     }
-}
-
-// Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
-// With m_dev, the visible count (the packed total after the nb block partials) is stored there for the
-// kernels queued ahead of the count readback.
-__global__ __launch_bounds__(kBlock) void compact_kernel(
-    int64_t n_virtual, const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vkey,
-    const uint64_t* __restrict__ partials, uint32_t* __restrict__ comp_id, uint32_t* __restrict__ comp_off,
-    uint32_t* __restrict__ comp_key, unsigned nb, uint32_t* __restrict__ m_dev) {
-    __shared__ uint64_t lds[kWaves];
-    if (m_dev && blockIdx.x == 0 && threadIdx.x == 0) *m_dev = (uint32_t)(partials[nb] >> 32);
-    uint64_t carry = partials[blockIdx.x];
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= n_virtual) break;  // block-uniform
@@ -991,15 +994,15 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
                 0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
         }
     }
-    // the totals are final here: published to pinned host memory and marked by an event, so that the
-    // host reads them while the depth pre-order and row offsets below still run
+    // the totals are final after the compaction, which publishes them to pinned host memory; an event
+    // marks that write, so that the host reads them while the depth pre-order and row offsets below
+    // still run
     CountReadback* rb = nullptr;
     rc = count_readback(rb);
     if (rc) return rc;
-    scan_partials_kernel<uint64_t><<<1, kBlock, 0, s>>>(w.partials, w.nb, w.cpart, rb->dev);
+    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.cpart, w.comp_id,
+                                           w.comp_off, w.comp_key, w.nb, g.sort ? w.m_dev : nullptr, rb->dev);
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
-    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
-                                           w.comp_key, w.nb, g.sort ? w.m_dev : nullptr);
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
         // (stable, 4 passes, result back in comp_*), then their row-run offsets
@@ -1007,7 +1010,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev);
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
-        scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(w.rpart, w.nb, nullptr);
+        scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(w.rpart, w.nb);
         rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
