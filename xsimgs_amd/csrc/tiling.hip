@@ -214,22 +214,6 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     }
 }
 
-// single block: exclusive scan of the block partials in place, grand total at partials[nb]
-template <typename T>
-__global__ __launch_bounds__(kBlock) void scan_partials_kernel(T* __restrict__ partials, unsigned nb) {
-    __shared__ T lds[kWaves];
-    T carry = 0;
-    for (unsigned start = 0; start < nb; start += kBlock) {
-        const unsigned i = start + threadIdx.x;
-        const T v = i < nb ? partials[i] : (T)0;
-        T tot;
-        const T ex = block_exclusive_scan<T>(v, lds, tot);
-        if (i < nb) partials[i] = carry + ex;
-        carry += tot;
-    }
-    if (threadIdx.x == 0) partials[nb] = carry;
-}
-
 // Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
 // Each block sums the (packed) partials of the count blocks before it, which places its instances.
 // Block 0 also sums them all: the packed total (visible << 32 | count, whose count field may carry)
@@ -398,8 +382,12 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
                                                            uint32_t* __restrict__ roff) {
     __shared__ uint32_t lds[kWaves];
     m = min(m, (int64_t)*m_dev);
-    uint32_t carry = partials[blockIdx.x];
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    if (base >= m) return;  // block-uniform
+    // the block's first offset: the row totals of the blocks before it
+    uint32_t before = 0;
+    for (unsigned b = threadIdx.x; b < blockIdx.x; b += kBlock) before += partials[b];
+    uint32_t carry = block_reduce_sum<uint32_t>(before, lds);
     for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= m) break;
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
@@ -1010,7 +998,6 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev);
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
-        scan_partials_kernel<uint32_t><<<1, kBlock, 0, s>>>(w.rpart, w.nb);
         rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
