@@ -351,7 +351,8 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(
 // in run order, which is depth order, then rows, then columns, as the reference orders them.
 constexpr int kRunSeg = 512;          // runs per row segment
 constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of seg_count_kernel)
-constexpr int kColGroup = 4;    // columns per wavefront in write_runs_kernel
+constexpr int kColGroup = 4;    // columns per wavefront step in write_runs_kernel
+constexpr int kBandCols = 16;   // columns whose runs write_runs_kernel lists together (a multiple of kColGroup)
 
 // the visible-span count from the packed grand total of the count scan, for device-sized kernels
 
@@ -638,18 +639,21 @@ XSG_DEV void write_neg_runs(const uint4* __restrict__ rec, int64_t b, int64_t n_
     }
 }
 
-// One workgroup per segment: its runs are read once into LDS, and each wavefront takes groups of
-// kColGroup columns in turn. Per column, the runs covering it are found by ballot and take
-// consecutive positions from the column's slot, in run (depth) order. They are staged in a
-// wavefront-private LDS buffer of 64 entries per column and stored 64 at a time, so that every
-// global store of a column is a full, contiguous wavefront (a column gets a few of each 64 runs).
-// Workgroup s_max writes the negative-depth runs instead.
+// One workgroup per segment: its runs are read once into LDS, and each wavefront takes bands of
+// kBandCols columns in turn. For a band, the runs touching it are first listed in run (depth) order
+// (a stable ballot compaction into a wavefront-private LDS list: a run covers about a tenth of a
+// row's columns, so most runs touch few bands); then, per group of kColGroup columns, the runs of
+// the list covering each column are found by ballot and take consecutive positions from the
+// column's slot, in run order. They are staged in a wavefront-private LDS buffer of 64 entries per
+// column and stored 64 at a time, so that every global store of a column is a full, contiguous
+// wavefront. Workgroup s_max writes the negative-depth runs instead.
 __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     int n_real, const uint4* __restrict__ rec, const uint32_t* __restrict__ row_start,
     const uint32_t* __restrict__ seg_base, const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ slots,
-    const uint32_t* __restrict__ tile_base, int64_t s_max, int64_t n_runs, int ntx, int nty, int tnb, int n_groups,
+    const uint32_t* __restrict__ tile_base, int64_t s_max, int64_t n_runs, int ntx, int nty, int tnb,
     int64_t n_out, int64_t* __restrict__ out_keys, int32_t* __restrict__ out_ids) {
     __shared__ uint4 s_rec[kRunSeg];
+    __shared__ uint16_t s_list[kWaves][kRunSeg];       // per wavefront: the band's runs, in run order
     __shared__ uint32_t s_dep[kWaves][kColGroup][64];  // staged depth bits (low key word)
     __shared__ int32_t s_gid[kWaves][kColGroup][64];   // staged Gaussian ids
     extern __shared__ uint32_t s_first[];              // [ntx]: first output position per column
@@ -671,58 +675,76 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     __syncthreads();
     const uint32_t cid = row / (uint32_t)nty, y = row - cid * (uint32_t)nty;
     const uint32_t tile_row = (cid << tnb) | (y * (uint32_t)ntx);
-    for (int cg = wave; cg < n_groups; cg += kWaves) {
-        const int c0 = cg * kColGroup;
-        const int nc = min(kColGroup, ntx - c0);
-        // per column: global position of the next flushed entry and entries staged in LDS (< 64),
-        // both wave-uniform
-        uint32_t out[kColGroup], fill[kColGroup];
-#pragma unroll
-        for (int j = 0; j < kColGroup; ++j) {
-            out[j] = j < nc ? (uint32_t)__builtin_amdgcn_readfirstlane((int)s_first[c0 + j]) : 0u;
-            fill[j] = 0;
-        }
+    for (int band = wave; band * kBandCols < ntx; band += kWaves) {
+        const int b0 = band * kBandCols, b1 = min(ntx, b0 + kBandCols);
+        // the segment's runs that cover a column of [b0, b1), in run order (n_list is wave-uniform)
+        int n_list = 0;
         for (int i0 = 0; i0 < n_seg; i0 += 64) {
             const int i = i0 + lane;
-            const uint4 rr = i < n_seg ? s_rec[i] : make_uint4(0, 0, 0, 0);  // width 0 past the end
-            const uint32_t x0 = rr.z & 0xffffu, w = (rr.z >> 16) - x0;
-            const uint32_t d0 = (uint32_t)c0 - x0;  // column offset in the run; covered iff below w
+            bool hit = false;
+            if (i < n_seg) {
+                const uint32_t z = s_rec[i].z;
+                hit = (int)(z & 0xffffu) < b1 && (int)(z >> 16) > b0;
+            }
+            const uint64_t mk = __builtin_amdgcn_ballot_w64(hit);
+            if (hit)
+                s_list[wave][n_list + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u))] =
+                    (uint16_t)i;
+            n_list += __popcll(mk);
+        }
+        for (int c0 = b0; c0 < b1; c0 += kColGroup) {
+            const int nc = min(kColGroup, b1 - c0);
+            // per column: global position of the next flushed entry and entries staged in LDS (< 64),
+            // both wave-uniform
+            uint32_t out[kColGroup], fill[kColGroup];
 #pragma unroll
             for (int j = 0; j < kColGroup; ++j) {
-                if (j >= nc) break;
-                const bool cov = d0 + (uint32_t)j < w;
-                const uint64_t mk = __builtin_amdgcn_ballot_w64(cov);
-                const uint32_t cnt = (uint32_t)__popcll(mk);
-                const uint32_t slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
-                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)mk, fill[j]));
-                if (cov && slot < 64) {
-                    s_dep[wave][j][slot] = rr.y;
-                    s_gid[wave][j][slot] = (int32_t)rr.x;
-                }
-                const uint32_t f = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fill[j] + cnt));
-                if (f >= 64) {  // the column's buffer is full: store it, then stage the overflow
-                    const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
-                    if (pos < (uint64_t)n_out) {
-                        out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
-                        out_ids[pos] = s_gid[wave][j][lane];
+                out[j] = j < nc ? (uint32_t)__builtin_amdgcn_readfirstlane((int)s_first[c0 + j]) : 0u;
+                fill[j] = 0;
+            }
+            for (int i0 = 0; i0 < n_list; i0 += 64) {
+                const int li = i0 + lane;
+                const uint4 rr = li < n_list ? s_rec[s_list[wave][li]] : make_uint4(0, 0, 0, 0);  // width 0 past the end
+                const uint32_t x0 = rr.z & 0xffffu, w = (rr.z >> 16) - x0;
+                const uint32_t d0 = (uint32_t)c0 - x0;  // column offset in the run; covered iff below w
+#pragma unroll
+                for (int j = 0; j < kColGroup; ++j) {
+                    if (j >= nc) break;
+                    const bool cov = d0 + (uint32_t)j < w;
+                    const uint64_t mk = __builtin_amdgcn_ballot_w64(cov);
+                    const uint32_t cnt = (uint32_t)__popcll(mk);
+                    const uint32_t slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mk, fill[j]));
+                    if (cov && slot < 64) {
+                        s_dep[wave][j][slot] = rr.y;
+                        s_gid[wave][j][slot] = (int32_t)rr.x;
                     }
-                    out[j] = (uint32_t)__builtin_amdgcn_readfirstlane((int)(out[j] + 64));
-                    if (cov && slot >= 64) {
-                        s_dep[wave][j][slot - 64] = rr.y;
-                        s_gid[wave][j][slot - 64] = (int32_t)rr.x;
+                    const uint32_t f = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fill[j] + cnt));
+                    if (f >= 64) {  // the column's buffer is full: store it, then stage the overflow
+                        const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
+                        if (pos < (uint64_t)n_out) {
+                            out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
+                            out_ids[pos] = s_gid[wave][j][lane];
+                        }
+                        out[j] = (uint32_t)__builtin_amdgcn_readfirstlane((int)(out[j] + 64));
+                        if (cov && slot >= 64) {
+                            s_dep[wave][j][slot - 64] = rr.y;
+                            s_gid[wave][j][slot - 64] = (int32_t)rr.x;
+                        }
+                        fill[j] = f - 64;
+                    } else {
+                        fill[j] = f;
                     }
-                    fill[j] = f - 64;
-                } else {
-                    fill[j] = f;
                 }
             }
-        }
 #pragma unroll
-        for (int j = 0; j < kColGroup; ++j) {
-            const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
-            if (j < nc && (uint32_t)lane < fill[j] && pos < (uint64_t)n_out) {
-                out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
-                out_ids[pos] = s_gid[wave][j][lane];
+            for (int j = 0; j < kColGroup; ++j) {
+                const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
+                if (j < nc && (uint32_t)lane < fill[j] && pos < (uint64_t)n_out) {
+                    out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
+                    out_ids[pos] = s_gid[wave][j][lane];
+                }
             }
         }
     }
@@ -1097,10 +1119,9 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     // offsets of the sorted keys (negative-depth runs follow every tile)
     tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots, tile_offsets);
     // the writers (one extra workgroup for the negative-depth runs)
-    const int n_groups = (g.ntx + kColGroup - 1) / kColGroup;
     write_runs_kernel<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base,
                                                                 fw.seg_row, fw.slots, fw.tile_tot, fw.s_max, n_runs,
-                                                                g.ntx, g.nty, g.tnb, n_groups, n_isects, isect_ids,
+                                                                g.ntx, g.nty, g.tnb, n_isects, isect_ids,
                                                                 flatten_ids);
     XSG_TRY_LAUNCH("isect_fill");
     return XSG_OK;
