@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(
 constexpr int kRunSeg = 512;          // runs per row segment
 constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of seg_count_kernel)
 constexpr int kColGroup = 4;    // columns per wavefront step in write_runs_kernel
-constexpr int kBandCols = 16;   // columns whose runs write_runs_kernel lists together (a multiple of kColGroup)
+constexpr int kBandCols = 8;    // columns whose runs write_runs_kernel lists together (a multiple of kColGroup)
 
 // the visible-span count from the packed grand total of the count scan, for device-sized kernels
 
