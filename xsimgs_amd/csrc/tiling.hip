@@ -405,17 +405,23 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
 }
 
 // Merge-path expansion of the depth-ordered instances into row runs: run r gets its row bucket
-// and the depth-order position of its instance.
+// and the depth-order position of its instance. A block writes one tile of the run sort
+// (kExpandPerBlock runs), so it also stores the tile's histogram of the sort's first digit (the low
+// 8 bits of the row bucket) into hist, digit-major as radix_upsweep would.
+static_assert(kExpandPerBlock == kSortBlock * 4, "an expansion block is one tile of the run sort");
 __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, const uint32_t* __restrict__ roff,
                                                              const uint32_t* __restrict__ ids,
                                                              const uint32_t* __restrict__ keys, int64_t m,
                                                              const Rect* __restrict__ rects, int nty,
                                                              int64_t n_per_cam, int spans, uint32_t neg_row,
                                                              uint32_t* __restrict__ out_row,
-                                                             uint32_t* __restrict__ out_p) {
+                                                             uint32_t* __restrict__ out_p,
+                                                             uint32_t* __restrict__ hist, unsigned nb) {
     __shared__ uint32_t s_off[kExpandPerBlock];
     __shared__ uint32_t s_row[kExpandPerBlock];  // first row bucket of the instance, or neg_row
+    __shared__ uint32_t s_hist[kRadix];
     __shared__ int64_t s_range[2];
+    s_hist[threadIdx.x] = 0;
     const int64_t o0 = (int64_t)blockIdx.x * kExpandPerBlock;
     const int64_t o_end = min(n_runs, o0 + kExpandPerBlock);
     if (threadIdx.x < 2) {
@@ -448,9 +454,13 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
             if ((int64_t)s_off[mid] <= o) lo = mid; else hi = mid - 1;
         }
         const uint32_t row0 = s_row[lo];
-        out_row[o] = row0 == neg_row ? neg_row : row0 + (uint32_t)(o - (int64_t)s_off[lo]);
+        const uint32_t row = row0 == neg_row ? neg_row : row0 + (uint32_t)(o - (int64_t)s_off[lo]);
+        out_row[o] = row;
         out_p[o] = (uint32_t)(p_lo + lo);
+        atomicAdd(&s_hist[row & (kRadix - 1)], 1u);
     }
+    __syncthreads();
+    hist[(int64_t)threadIdx.x * nb + blockIdx.x] = s_hist[threadIdx.x];
 }
 
 // single block: row_start[r] = first sorted run of row bucket r (r in [0, n_rows]), then segments
@@ -1097,9 +1107,9 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     const FillWs fw = fill_ws_layout(g, n_runs, fill_workspace);
     const uint32_t neg_row = (uint32_t)(fw.n_rows - 1);
     const int n_real = fw.n_rows - 1;
-    expand_runs_kernel<<<(unsigned)((n_runs + kExpandPerBlock - 1) / kExpandPerBlock), kBlock, 0, s>>>(
-        n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.rects, g.nty, n_per_cam, g.spans, neg_row, fw.row_a,
-        fw.p_a);
+    const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
+    expand_runs_kernel<<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.rects, g.nty,
+                                                  n_per_cam, g.spans, neg_row, fw.row_a, fw.p_a, fw.hist, nb_runs);
     int row_bits = 1;
     while ((1u << row_bits) <= neg_row) ++row_bits;
     // stable sort of the runs by row bucket; the last pass writes the sorted row buckets (to the
@@ -1108,7 +1118,8 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
     radix_sort_passes<uint32_t, uint32_t, RunRecOut, kRunSortItems>(
         fw.row_a, fw.p_a, fw.row_b, fw.p_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
-        RunRecOut{rows_sorted, fw.rec, cw.comp_id, cw.comp_key, cw.rects, g.spans}, s);
+        RunRecOut{rows_sorted, fw.rec, cw.comp_id, cw.comp_key, cw.rects, g.spans}, s, nullptr,
+        /*first_hist_ready=*/true);
     row_segments_kernel<<<1, kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows, row_bits <= 8 ? fw.dtot : nullptr,
                                              fw.row_start, fw.seg_base, fw.seg_row);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;

@@ -230,12 +230,14 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
 // words. With n_dev, the device-side count (at most n) is sorted; n only bounds it, so a sort whose
 // count is usually far below n uses fewer ITEMS per block to spread over more blocks, and its
 // grids are capped at kDevCountGrid workgroups that loop over the tiles holding keys (dispatching
-// workgroups for empty tiles costs about as much as sorting a full one).
+// workgroups for empty tiles costs about as much as sorting a full one). With first_hist_ready, the
+// caller has already stored the first pass's per-tile histograms in hist (the kernel that wrote the
+// keys counted them), and the first upsweep is skipped.
 constexpr unsigned kDevCountGrid = 256;
 template <typename K, typename V, typename FinalOut, int ITEMS = kSortItems>
 inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
                              uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s,
-                             const uint32_t* n_dev = nullptr) {
+                             const uint32_t* n_dev = nullptr, bool first_hist_ready = false) {
     const unsigned nb = sort_blocks<ITEMS>(n);
     const unsigned grid = n_dev ? min(nb, kDevCountGrid) : nb;
     int passes = 0;
@@ -243,7 +245,8 @@ inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bi
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
         const int bits = min(8, end_bit - shift);
         const bool last = shift + 8 >= end_bit;
-        radix_upsweep<K, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
+        if (!(first_hist_ready && shift == begin_bit))
+            radix_upsweep<K, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
         radix_scan_hist<ITEMS><<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot, n, n_dev);
         if (last) {
             radix_downsweep<K, V, FinalOut, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits,
