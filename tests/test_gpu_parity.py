@@ -141,6 +141,28 @@ def test_fill_tile_offsets(dev, cfg0):
         _C.isect_regular_tiles(m2, radii, dep, spec.width, spec.height, 16, 16, sort=False, tile_offsets=off)
 
 
+def test_isect_regular_many_visible(dev):
+    """More visible instances than the depth pre-order's capped grid covers in one tile each
+    (256 workgroups x 1024 keys), so its workgroups loop over several tiles; bit-exact against the
+    oracle, with tile offsets."""
+    g = np.random.default_rng(21)
+    n, W, H = 700_000, 1920, 1080
+    m2 = np.stack([g.uniform(0, W, n), g.uniform(0, H, n)], 1).astype(np.float32)
+    r = g.uniform(0.5, 20.0, (n, 2)).astype(np.float32)
+    d = g.uniform(0.3, 90.0, n).astype(np.float32)
+    d[: n // 50] = d[n // 2]  # ties in depth
+    T = lambda a: torch.from_numpy(a).to(dev)
+    off = torch.empty(((H + 15) // 16, (W + 15) // 16), dtype=torch.int32, device=dev)
+    tpg, ids, fl = _C.isect_regular_tiles(T(m2), T(r), T(d), W, H, 16, 16, tile_offsets=off)
+    print("visible", int((tpg > 0).sum()), "isects", ids.numel(), flush=True)
+    assert int((tpg > 0).sum()) > 2 * 256 * 1024
+    rtpg, rids, rfl = O.isect_regular(m2, r, d, W, H, 16, 16)
+    assert np.array_equal(np_(tpg), rtpg)
+    assert np.array_equal(np_(ids), rids)
+    assert np.array_equal(np_(fl), rfl)
+    assert np.array_equal(np_(off), O.offset_encode(rids, (W + 15) // 16, (H + 15) // 16))
+
+
 def test_isect_regular_edge_cases(dev):
     # empty input, all-culled input, Gaussians on tile borders and outside the image, negative depth
     W, H = 100, 70
