@@ -163,6 +163,35 @@ def test_isect_regular_many_visible(dev):
     assert np.array_equal(np_(off), O.offset_encode(rids, (W + 15) // 16, (H + 15) // 16))
 
 
+def test_isect_regular_batched_six_cameras(dev):
+    """Six cameras binned in one call (camera bits above the tile bits) equal each camera's oracle
+    binning in turn, with the camera id in the keys and ids offset by cam * N. 6 x 68 tile rows plus the
+    negative-depth bucket need 9-bit row buckets, so the run sort takes two passes (the first pass's
+    histograms come from the expansion kernel)."""
+    g = np.random.default_rng(23)
+    C_, n, W, H = 6, 60_000, 1920, 1080
+    m2 = np.stack([g.uniform(-40, W + 40, (C_, n)), g.uniform(-40, H + 40, (C_, n))], -1).astype(np.float32)
+    r = g.uniform(0.5, 40.0, (C_, n, 2)).astype(np.float32)
+    d = g.uniform(0.3, 90.0, (C_, n)).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ntx, nty = (W + 15) // 16, (H + 15) // 16
+    off = torch.empty((C_, nty, ntx), dtype=torch.int32, device=dev)
+    tpg, ids, fl = _C.isect_regular_tiles_batched(T(m2), T(r), T(d), W, H, 16, 16, tile_offsets=off)
+    tnb = int(np.floor(np.log2(ntx * nty))) + 1
+    want_ids, want_fl, want_tpg = [], [], []
+    for c in range(C_):
+        rtpg, rids, rfl = O.isect_regular(m2[c], r[c], d[c], W, H, 16, 16)
+        want_tpg.append(rtpg)
+        want_ids.append(rids + (np.int64(c) << np.int64(tnb + 32)))
+        want_fl.append(rfl + np.int32(c * n))
+    want_ids, want_fl = np.concatenate(want_ids), np.concatenate(want_fl)
+    print("isects", ids.numel(), flush=True)
+    assert np.array_equal(np_(tpg), np.stack(want_tpg))
+    assert np.array_equal(np_(ids), want_ids)
+    assert np.array_equal(np_(fl), want_fl)
+    assert np.array_equal(np_(off), O.offset_encode(want_ids, ntx, nty, C_))
+
+
 def test_isect_regular_edge_cases(dev):
     # empty input, all-culled input, Gaussians on tile borders and outside the image, negative depth
     W, H = 100, 70
