@@ -165,7 +165,7 @@ def test_cull_exact(dev, case):
 
 
 @pytest.mark.parametrize("dyn", [False, True])
-@pytest.mark.parametrize("cdim", [1, 5, 9, 16, 17])
+@pytest.mark.parametrize("cdim", [0, 1, 5, 9, 16, 17])
 def test_channel_counts(dev, cdim, dyn):
     """The backward without ray gradients at 16x16 tiles (four pixels per lane; from 17 channels, where
     colours are read from HBM, the ray-gradient kernel) for channel counts that move the gradient
@@ -174,14 +174,16 @@ def test_channel_counts(dev, cdim, dyn):
     tsx = tsy = 16
     s = _scene(300 + cdim, tsx, tsy, True, dyn, False)
     g = np.random.default_rng(cdim)
-    s["colors"] = g.uniform(0.0, 1.0, (s["means"].shape[0], cdim)).astype(np.float32)
-    T = lambda k: torch.from_numpy(s[k]).to(dev)
+    # no colours at all (depth and alpha only) for cdim 0
+    s["colors"] = g.uniform(0.0, 1.0, (s["means"].shape[0], cdim)).astype(np.float32) if cdim else None
+    T = lambda k: None if s[k] is None else torch.from_numpy(s[k]).to(dev)
+    cols = T("colors").unsqueeze(0) if cdim else None
     if dyn:
-        out = _C.rasterize_eval3d_dynamic_fwd(T("means"), T("vel"), T("quats"), T("scales"), T("colors").unsqueeze(0),
+        out = _C.rasterize_eval3d_dynamic_fwd(T("means"), T("vel"), T("quats"), T("scales"), cols,
                                               T("opac").view(1, -1), W, H, tsx, tsy, T("ro"), T("rd"), T("rtd"),
                                               T("offsets"), T("flat"))
     else:
-        out = _C.rasterize_eval3d_fwd(T("means"), T("quats"), T("scales"), T("colors").unsqueeze(0),
+        out = _C.rasterize_eval3d_fwd(T("means"), T("quats"), T("scales"), cols,
                                       T("opac").view(1, -1), W, H, tsx, tsy, T("ro"), T("rd"), T("offsets"), T("flat"))
     rgb, depth, alpha, last = (np_(x) for x in out)
     okw = dict(velocity=s["vel"], ray_time_delta=s["rtd"])
@@ -189,11 +191,12 @@ def test_channel_counts(dev, cdim, dyn):
                        s["flat"], tsx, tsy, **okw)
     bar = 1.0 - 2.0 / (W * H)
     for name, a, b in (("rgb", rgb, ref[0]), ("alpha", alpha, ref[2])):
-        assert frac_close(a, b, RENDER_ATOL) >= bar, name
-    vr = (g.standard_normal((H, W, cdim)) * 1e-3).astype(np.float32)
+        if a is not None and a.size:
+            assert frac_close(a, b, RENDER_ATOL) >= bar, name
+    vr = (g.standard_normal((H, W, cdim)) * 1e-3).astype(np.float32) if cdim else None
     vd = (g.standard_normal((H, W)) * 1e-3).astype(np.float32)
     va = (g.standard_normal((H, W)) * 1e-3).astype(np.float32)
-    Tn = lambda a: torch.from_numpy(a).to(dev)
+    Tn = lambda a: None if a is None else torch.from_numpy(a).to(dev)
     if dyn:
         grads = _C.rasterize_eval3d_dynamic_bwd(T("means"), T("vel"), T("scales"), T("quats"), T("opac"), T("colors"),
                                                 T("ro"), T("rd"), T("rtd"), tsx, tsy, T("offsets"), T("flat"),
@@ -210,8 +213,8 @@ def test_channel_counts(dev, cdim, dyn):
     rg32, rg64 = O.eval3d_bwd(*oargs, **okw), O.eval3d_bwd(*oargs, prec="f64", **okw)
     close = lambda a, b, f=1.0: np.abs(np.asarray(a, np.float64) - b) <= f * (GRAD_ATOL + GRAD_RTOL * np.abs(b))
     for name, a in zip(names, grads):
-        if a is None:  # ray gradients are skipped up to 16 channels
-            assert cdim <= 16 and name in ("v_ray_o", "v_ray_d")
+        if a is None:  # ray gradients are skipped up to 16 channels; no colour gradient without colours
+            assert (cdim <= 16 and name in ("v_ray_o", "v_ray_d")) or (cdim == 0 and name == "v_colors")
             continue
         a, b32, b64 = np_(a), rg32[name], rg64[name]
         ok32, okg = close(b32, b64), close(a, b64)
