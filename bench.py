@@ -46,14 +46,14 @@ def parse():
 # 42 for every evaluated pair (M rd 15, |grd|^2 5, capped reciprocal 2, grd x gro 9, its squared norm
 # 5, exponent scale 2, exp / opacity / clamp / threshold 4); forward composite 13 + 2 per colour
 # channel for every composited pair (hit distance 6, depth 2, transmittance and tests 5); backward
-# 74 + 4 per colour channel for every composited pair without ray gradients (hit distance and the
-# 1 / (1 - alpha) transmittance 11, dL/dalpha 6, the collapsed alpha and hit vectors 22, mean
+# 72 + 4 per colour channel for every composited pair without ray gradients (hit distance and the
+# 1 / (1 - alpha) transmittance 10, dL/dalpha 6, the collapsed alpha and hit vectors 21, mean
 # gradient 7 (the lane's M^T product shared by its four pixels), the symmetric M gradient from the
 # ray offset 24, opacity and buffer 4). Evaluated and composited counts come from the kernels
 # themselves (pair_counts), so pairs skipped unevaluated by the culling are not counted.
 FLOPS_EVAL = 42
 FLOPS_FWD_CONTRIB = 13          # + 2 per colour channel
-FLOPS_BWD_CONTRIB = 74          # + 4 per colour channel
+FLOPS_BWD_CONTRIB = 72          # + 4 per colour channel
 FP32_VALU_PEAK_TFLOPS = 78.6    # non-packed FP32 (packed FP32 ops are disabled in this build)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "eval3d_bwd_cfg2_traffic.json")
 

@@ -121,7 +121,8 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
                       float (&acc)[K], f3& vg_sum) {
     const float od = dot(e.gro, e.grd);
     const float hit_t = -od * e.inv_dd;
-    const float ra = __builtin_amdgcn_rcpf(fmaxf(1e-6f, 1.0f - e.alpha));
+    // 1 / max(1e-6, 1 - alpha) (eval3d_bwd.cu:221): alpha <= kMaxAlpha, so the max never applies
+    const float ra = __builtin_amdgcn_rcpf(1.0f - e.alpha);
     px.T = e.valid ? px.T * ra : px.T;
     const float T = px.T;
     const float fac = e.valid ? e.alpha * T : 0.0f;
@@ -137,10 +138,11 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     const bool geo = e.valid && e.araw <= kMaxAlpha;
     const float v_alpha_g = geo ? v_alpha : 0.0f;
     const float k1 = geo ? px.v_d * fac * e.inv_dd : 0.0f;
-    const float Ap = -e.araw * v_alpha_g * e.inv_dd;
-    const f3 w = cross(e.c, e.grd);
+    // A w = -op vis dL/dalpha p with p = w / |grd|^2 (the offset of the Gaussian from the ray)
+    const float Ap = -e.araw * v_alpha_g;
+    const f3 pp = cross(e.c, e.grd) * e.inv_dd;
     const f3 kg = k1 * e.grd;
-    const f3 v_gro = Ap * w - kg;
+    const f3 v_gro = Ap * pp - kg;
     if constexpr (RG || DYN) {
         const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, v_gro);
         put<FIRST>(acc[CDIM + 0], -v_omm.x);
@@ -161,7 +163,6 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
         vg_sum = FIRST ? v_gro : vg_sum + v_gro;
     }
     // Q (upper triangle, row-major): Q_ij = dL/dgro_i p_j - p_i k1 grd_j
-    const f3 pp = w * e.inv_dd;
     put<FIRST>(acc[CDIM + 3], pp.x * (v_gro.x - kg.x));
     put<FIRST>(acc[CDIM + 4], v_gro.x * pp.y - pp.x * kg.y);
     put<FIRST>(acc[CDIM + 5], v_gro.x * pp.z - pp.x * kg.z);
