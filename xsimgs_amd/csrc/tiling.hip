@@ -587,8 +587,9 @@ __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restric
 
 // single block of 1024 threads: exclusive scan of tile_tot[0, n) in place (the first position of
 // every tile of the real rows), the total -- where the negative-depth entries start -- at tile_tot[n];
-// with `offsets`, the same positions as int32 (the tile offsets). Each thread scans kScanChunks
-// consecutive entries in registers, so one block-wide scan serves kScanThreads * kScanChunks entries.
+// with `offsets`, the same positions as int32 (the tile offsets). Chunks of 1024 consecutive entries,
+// one per thread (coalesced), eight chunks' loads in flight. (Eight consecutive entries per thread
+// with one block-wide scan measured slower: 11.9 against 7.3 us, its strided loads coalesce worse.)
 constexpr int kScanThreads = 1024;
 constexpr int kScanChunks = 8;
 __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n,
@@ -597,34 +598,32 @@ __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __res
     const int wave = threadIdx.x >> 6;
     uint32_t carry = 0;
     for (int64_t s0 = 0; s0 < n; s0 += (int64_t)kScanThreads * kScanChunks) {
-        const int64_t i0 = s0 + (int64_t)threadIdx.x * kScanChunks;
-        uint32_t x[kScanChunks], sum = 0;
+        uint32_t x[kScanChunks];
 #pragma unroll
         for (int j = 0; j < kScanChunks; ++j) {
-            x[j] = i0 + j < n ? a[i0 + j] : 0u;
-            sum += x[j];
+            const int64_t i = s0 + (int64_t)j * kScanThreads + threadIdx.x;
+            x[j] = i < n ? a[i] : 0u;
         }
-        const uint32_t inc = wave_inclusive_scan(sum);
-        if (__lane_id() == 63) lds[wave] = inc;
-        __syncthreads();
-        uint32_t before = 0, tot = 0;
-#pragma unroll
-        for (int w = 0; w < kScanThreads / 64; ++w) {
-            const uint32_t y = lds[w];
-            if (w < wave) before += y;
-            tot += y;
-        }
-        __syncthreads();
-        uint32_t run = carry + before + inc - sum;
 #pragma unroll
         for (int j = 0; j < kScanChunks; ++j) {
-            if (i0 + j < n) {
-                a[i0 + j] = run;
-                if (offsets) offsets[i0 + j] = (int32_t)run;
+            const int64_t i = s0 + (int64_t)j * kScanThreads + threadIdx.x;
+            const uint32_t inc = wave_inclusive_scan(x[j]);
+            if (__lane_id() == 63) lds[wave] = inc;
+            __syncthreads();
+            uint32_t before = 0, tot = 0;
+#pragma unroll
+            for (int w = 0; w < kScanThreads / 64; ++w) {
+                const uint32_t y = lds[w];
+                if (w < wave) before += y;
+                tot += y;
             }
-            run += x[j];
+            __syncthreads();
+            if (i < n) {
+                a[i] = carry + before + inc - x[j];
+                if (offsets) offsets[i] = (int32_t)(carry + before + inc - x[j]);
+            }
+            carry += tot;
         }
-        carry += tot;
     }
     if (threadIdx.x == 0) a[n] = carry;
 }
