@@ -373,11 +373,13 @@ __global__ __launch_bounds__(kBlock) void sh_bwd_kernel(
     }
 }
 
-__global__ __launch_bounds__(kBlock) void sum_partials_kernel(const float* __restrict__ part, int nb,
-                                                              float* __restrict__ out) {
-    __shared__ float red[3][kBlock / 64];
+// One workgroup of kSumThreads sums the per-block d_origin partials in a fixed order.
+constexpr int kSumThreads = 1024;
+__global__ __launch_bounds__(kSumThreads) void sum_partials_kernel(const float* __restrict__ part, int nb,
+                                                                   float* __restrict__ out) {
+    __shared__ float red[3][kSumThreads / 64];
     float s[3] = {0.f, 0.f, 0.f};
-    for (int b = threadIdx.x; b < nb; b += kBlock)
+    for (int b = threadIdx.x; b < nb; b += kSumThreads)
         for (int c = 0; c < 3; ++c) s[c] += part[3 * b + c];
     for (int c = 0; c < 3; ++c) s[c] = wave_sum(s[c]);
     const int w = threadIdx.x >> 6;
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void sum_partials_kernel(const float* __res
     __syncthreads();
     if (threadIdx.x < 3) {
         float r = 0.f;
-        for (int k = 0; k < kBlock / 64; ++k) r += red[threadIdx.x][k];
+        for (int k = 0; k < kSumThreads / 64; ++k) r += red[threadIdx.x][k];
         out[threadIdx.x] = r;
     }
 }
@@ -461,7 +463,7 @@ extern "C" int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, c
     if (const int rc = xsg_check_workspace(workspace, "xsg_sh_bwd")) return rc;
     const hipStream_t s = (hipStream_t)stream;
     if (n == 0) {  // d_origin = 0 without a memset node (callers may capture this in a graph)
-        sum_partials_kernel<<<1, kBlock, 0, s>>>((const float*)workspace, 0, d_origin);
+        sum_partials_kernel<<<1, kSumThreads, 0, s>>>((const float*)workspace, 0, d_origin);
         XSG_TRY_LAUNCH("sh_bwd");
         return XSG_OK;
     }
@@ -480,7 +482,7 @@ extern "C" int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, c
         case 4: XSG_B(4); break;
     }
 #undef XSG_B
-    sum_partials_kernel<<<1, kBlock, 0, s>>>(part, (int)nb, d_origin);
+    sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, (int)nb, d_origin);
     XSG_TRY_LAUNCH("sh_bwd");
     return XSG_OK;
 }
