@@ -305,7 +305,6 @@ __global__ __launch_bounds__(kTileThreads / PX) void eval3d_bwd_kernel(Eval3dPar
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
         const int32_t batch_end = eff_end - nthr * b;
-        const int32_t batch_size = min(nthr, batch_end + 1 - range_start);
         const int32_t idx = batch_end - tr;
         bool staged = false;
         CullGauss cg;
