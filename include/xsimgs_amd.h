@@ -240,7 +240,9 @@ int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible,
                    int sort, void* count_workspace, void* fill_workspace, int64_t* isect_ids,
                    int32_t* flatten_ids, int32_t* tile_offsets, int64_t n_tile_offsets, xsg_stream_t stream);
 
-/* offsets [n_cams, n_tiles_h, n_tiles_w]: first sorted index of every (camera, tile) */
+/* offsets [n_cams, n_tiles_h, n_tiles_w]: first sorted index of every (camera, tile). Keys of a
+ * negative depth (sign-extended bits, all ones above bit 31) sort after every tile and are in no
+ * tile's range; the reference's encoder races on them (tiling_common.cu:41-60). */
 int xsg_isect_offset_encode(const int64_t* isect_ids, int64_t n_isects, int n_tiles_w, int n_tiles_h,
                             int n_cams, int32_t* offsets, xsg_stream_t stream);
 

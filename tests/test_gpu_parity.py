@@ -192,6 +192,62 @@ def test_isect_regular_batched_six_cameras(dev):
     assert np.array_equal(np_(off), O.offset_encode(want_ids, ntx, nty, C_))
 
 
+def _rig_expected(m2, r, d, W, H, tsx, tsy):
+    """Oracle binning of a rig: each camera's sorted keys with the camera id OR-ed in above the tile
+    bits (regular_tiling.cu:37-43; a negative depth's sign-extended bits keep the whole upper half at
+    ones), merged by a stable sort on the keys as unsigned numbers -- the reference's single stable
+    sort of all cameras' keys."""
+    C_, n = d.shape
+    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
+    tnb = int(np.floor(np.log2(ntx * nty))) + 1
+    tpg, ids, fl = [], [], []
+    for c in range(C_):
+        rtpg, rids, rfl = O.isect_regular(m2[c], r[c], d[c], W, H, tsx, tsy)
+        tpg.append(rtpg)
+        ids.append(rids | (np.int64(c) << np.int64(tnb + 32)))
+        fl.append(rfl + np.int32(c * n))
+    ids, fl = np.concatenate(ids), np.concatenate(fl)
+    order = np.argsort(ids.view(np.uint64), kind="stable")
+    return np.stack(tpg), ids[order], fl[order]
+
+
+@pytest.mark.parametrize("n_cams", [1, 3])
+def test_isect_negative_depth(dev, n_cams):
+    """Instances with a negative depth (-0.0 included) and a footprint -- the projection never yields
+    them, a direct caller can -- are binned bit-exactly: their sign-extended depth bits fill the key's
+    tile bits, so their entries sort after every tile of every camera. Tile ranges cover the other keys
+    only: the offsets (from the fill and from isect_offset_encode) equal the reference encoder's on the
+    non-negative keys. On the full key list the reference's encoder maps those keys to tile
+    2^tile_bits - 1 - n_tiles, and its last thread writes n_isects over every later tile while other
+    threads write their starts (tiling_common.cu:41-60): a race, so nothing to compare against there."""
+    g = np.random.default_rng(31 + n_cams)
+    n, W, H = 5000, 773, 1117
+    m2 = np.stack([g.uniform(-30, W + 30, (n_cams, n)), g.uniform(-30, H + 30, (n_cams, n))], -1).astype(np.float32)
+    r = g.uniform(0.0, 30.0, (n_cams, n, 2)).astype(np.float32)
+    d = g.uniform(-5.0, 90.0, (n_cams, n)).astype(np.float32)
+    d[:, :10] = -0.0
+    d[:, 10:60] = d[:, 70:71]  # ties
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ntx, nty = (W + 15) // 16, (H + 15) // 16
+    shape = (nty, ntx) if n_cams == 1 else (n_cams, nty, ntx)
+    off = torch.full(shape, -7, dtype=torch.int32, device=dev)
+    if n_cams == 1:
+        tpg, ids, fl = _C.isect_regular_tiles(T(m2[0]), T(r[0]), T(d[0]), W, H, 16, 16, tile_offsets=off)
+        tpg = tpg.view(1, -1)
+    else:
+        tpg, ids, fl = _C.isect_regular_tiles_batched(T(m2), T(r), T(d), W, H, 16, 16, tile_offsets=off)
+    wtpg, wids, wfl = _rig_expected(m2, r, d, W, H, 16, 16)
+    print("isects", ids.numel(), "negative-depth entries", int((wids < 0).sum()), flush=True)
+    assert int((wids < 0).sum()) > 100
+    assert np.array_equal(np_(tpg), wtpg)
+    assert np.array_equal(np_(ids), wids)
+    assert np.array_equal(np_(fl), wfl)
+    want_off = O.offset_encode(wids[wids >= 0], ntx, nty, n_cams)
+    assert np.array_equal(np_(off), want_off)
+    enc = _C.isect_offset_encode(ids, ntx, nty) if n_cams == 1 else _C.isect_offset_encode(ids, ntx, nty, n_cams)
+    assert np.array_equal(np_(enc), want_off)
+
+
 def test_isect_regular_edge_cases(dev):
     # empty input, all-culled input, Gaussians on tile borders and outside the image, negative depth
     W, H = 100, 70

@@ -763,8 +763,11 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
 }
 
 // Tile offsets of sorted keys by binary search: offsets[t] = first index whose key bits above 32,
-// read as unsigned, are >= t's (camera, tile) id -- for sorted keys what the reference's encoder
-// (tiling_common.cu:25-71) writes, negative-depth keys included (their saturated bits sort last).
+// read as unsigned, are >= t's (camera, tile) id -- what the reference's encoder
+// (tiling_common.cu:25-71) writes for sorted keys of non-negative depth. A negative depth's
+// sign-extended bits set the key's whole upper half, so such entries sort after every tile and lie
+// outside every tile's range here; the reference's encoder races on them (its last thread writes
+// n_isects over the tiles after 2^tile_bits - 1 - n_tiles while other threads write their starts).
 __global__ __launch_bounds__(kBlock) void offset_search_kernel(const int64_t* __restrict__ ids, int64_t n,
                                                                int n_tiles, int tnb, int64_t total,
                                                                int32_t* __restrict__ offsets) {
