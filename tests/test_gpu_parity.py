@@ -248,6 +248,39 @@ def test_isect_negative_depth(dev, n_cams):
     assert np.array_equal(np_(enc), want_off)
 
 
+@pytest.mark.parametrize("n_cams", [1, 2])
+@pytest.mark.parametrize("tile", [(8, 8), (16, 8), (12, 10), (32, 32), (10, 6)])
+def test_isect_regular_tile_shapes(dev, tile, n_cams):
+    """Tiles other than 16x16, on an image that no tile shape divides: keys, ids, counts and offsets
+    bit-exact against the oracle, one camera (sorted and unsorted) and a rig of two."""
+    tsx, tsy = tile
+    g = np.random.default_rng(tsx * 100 + tsy + n_cams)
+    n, W, H = 20_000, 1861, 930
+    m2 = np.stack([g.uniform(-50, W + 50, (n_cams, n)), g.uniform(-50, H + 50, (n_cams, n))], -1).astype(np.float32)
+    r = g.uniform(0.0, 24.0, (n_cams, n, 2)).astype(np.float32)
+    d = g.uniform(0.1, 90.0, (n_cams, n)).astype(np.float32)
+    d[:, : n // 10] = d[:, n // 2 : n // 2 + 1]  # ties
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
+    shape = (nty, ntx) if n_cams == 1 else (n_cams, nty, ntx)
+    off = torch.full(shape, -7, dtype=torch.int32, device=dev)
+    if n_cams == 1:
+        tpg, ids, fl = _C.isect_regular_tiles(T(m2[0]), T(r[0]), T(d[0]), W, H, tsx, tsy, tile_offsets=off)
+        tpg = tpg.view(1, -1)
+        _, ids_u, fl_u = _C.isect_regular_tiles(T(m2[0]), T(r[0]), T(d[0]), W, H, tsx, tsy, sort=False)
+        _, rids_u, rfl_u = O.isect_regular(m2[0], r[0], d[0], W, H, tsx, tsy, sort=False)
+        assert np.array_equal(np_(ids_u), rids_u)
+        assert np.array_equal(np_(fl_u), rfl_u)
+    else:
+        tpg, ids, fl = _C.isect_regular_tiles_batched(T(m2), T(r), T(d), W, H, tsx, tsy, tile_offsets=off)
+    wtpg, wids, wfl = _rig_expected(m2, r, d, W, H, tsx, tsy)
+    print("tile", tile, "cameras", n_cams, "isects", ids.numel(), flush=True)
+    assert np.array_equal(np_(tpg), wtpg)
+    assert np.array_equal(np_(ids), wids)
+    assert np.array_equal(np_(fl), wfl)
+    assert np.array_equal(np_(off), O.offset_encode(wids, ntx, nty, n_cams))
+
+
 def test_isect_regular_edge_cases(dev):
     # empty input, all-culled input, Gaussians on tile borders and outside the image, negative depth
     W, H = 100, 70
