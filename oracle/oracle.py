@@ -106,10 +106,13 @@ def ut_weights(alpha=0.1, beta=2.0, kappa=0.0, prec="f32"):
 
 
 def project_utgs(spec, means, scales, quats, opacity, width, height, vel=None, ut=(0.1, 2.0, 0.0),
-                 thr=1e-4, max_res=0.002, margin=1.0, phm=False, prec="f32"):
+                 thr=1e-4, max_res=0.002, margin=1.0, phm=False, prec="f32", margins=False):
     """<Camera>.projection_utgs[_phm] (ut_kernels.h:187-305, ut_phm_kernels.h:13-173).
 
-    Returns ``flags u8[N], radii[N,2], means2d[N,2], depths[N]``.
+    Returns ``flags u8[N], radii[N,2], means2d[N,2], depths[N]`` (+ with ``margins`` a diagnostic
+    per Gaussian: the smallest ratio of a validity decision's distance to its threshold over a bound
+    on the float32 error of the compared value; below 1, float32 rounding can decide the flag either
+    way. Meaningful in the f64 build).
     """
     ct, nt = _real(prec)
     lib = _lib(prec)
@@ -122,10 +125,13 @@ def project_utgs(spec, means, scales, quats, opacity, width, height, vel=None, u
     radii = np.zeros((n, 2), nt)
     m2 = np.zeros((n, 2), nt)
     dep = np.zeros(n, nt)
+    mg = np.zeros(n, nt) if margins else None
     fn = lib.orc_project_utgs_phm if phm else lib.orc_project_utgs
     fn(C.byref(cam), C.c_int(n), _p(means), _p(vel), _p(scales), _p(quats), _p(opacity),
        ct(width), ct(height), _p(w), ct(thr), ct(max_res), ct(margin),
-       _p(flags), _p(radii), _p(m2), _p(dep))
+       _p(flags), _p(radii), _p(m2), _p(dep), _p(mg))
+    if margins:
+        return flags, radii, m2, dep, mg
     return flags, radii, m2, dep
 
 
@@ -297,32 +303,46 @@ def isect_regular(means2d, radii, depths, width, height, tsx, tsy, sort=True):
 
 
 def isect_spherical_family(kind, spec, points, scale, quat, opacity, flags, means2d, radii, depths,
-                           tsx, tsy, width, height, elev=None, vel=None, ut=(0.1, 2.0, 0.0), sort=True):
+                           tsx, tsy, width, height, elev=None, vel=None, ut=(0.1, 2.0, 0.0), sort=True,
+                           seam_margins=False):
     """isect_lidar_tiles (phm_lidar_tiling.cu:239-351) when kind == "lidar", else
-    isect_spherical_tiles (phm_spherical_tiling.cu:179-291)."""
-    lib = _lib("f32")
-    cam = camera(spec, "f32")
+    isect_spherical_tiles (phm_spherical_tiling.cu:179-291).
+
+    With ``seam_margins`` returns instead, per Gaussian, the diagnostic margin of its second span
+    (flag-2 Gaussians; inf elsewhere), computed by the f64 build: the smallest ratio of a decision of
+    the PositiveDelta re-projection (validity, on-screen extent) or of the span's tile range (tile
+    and elevation boundaries) to a bound on the float32 error of the compared value. Below 1, float32
+    rounding can decide that span's tiles either way.
+    """
+    prec = "f64" if seam_margins else "f32"
+    lib = _lib(prec)
+    cam = camera(spec, prec)
     k = 0 if kind == "lidar" else 1
     f32 = np.float32
-    points, scale, quat = _arr(points, f32), _arr(scale, f32), _arr(quat, f32)
-    opacity, vel = _arr(opacity, f32), _arr(vel, f32)
+    rt = _real(prec)[1]
+    points, scale, quat = _arr(points, rt), _arr(scale, rt), _arr(quat, rt)
+    opacity, vel = _arr(opacity, rt), _arr(vel, rt)
     flags = _arr(flags, np.uint8)
     means2d, radii, depths = _arr(means2d, f32), _arr(radii, f32), _arr(depths, f32)
     elev = _arr(elev, f32) if elev is not None else np.zeros(1, f32)
     n_elev = elev.shape[0] if kind == "lidar" else 0
-    w = ut_weights(*ut)
+    w = ut_weights(*ut, prec=prec)
     n = depths.shape[0]
     tpg = np.zeros(n, np.int32)
     args = [C.c_int(k), C.byref(cam), _p(w), C.c_int(n), _p(points), _p(vel), _p(scale), _p(quat),
             _p(opacity), _p(flags), _p(means2d), _p(radii), _p(depths), _p(elev), C.c_int(n_elev),
             C.c_int(tsx), C.c_int(tsy), C.c_float(width), C.c_float(height)]
-    lib.orc_isect_spherical_family(*args, None, _p(tpg), None, None)
+    if seam_margins:
+        mg = np.full(n, np.inf, rt)
+        lib.orc_isect_spherical_family(*args, None, _p(tpg), None, None, _p(mg))
+        return mg
+    lib.orc_isect_spherical_family(*args, None, _p(tpg), None, None, None)
     cum = np.cumsum(tpg.astype(np.int64))
     n_isects = int(cum[-1]) if n else 0
     ids = np.zeros(n_isects, np.int64)
     fl = np.zeros(n_isects, np.int32)
     if n_isects:
-        lib.orc_isect_spherical_family(*args, _p(cum), None, _p(ids), _p(fl))
+        lib.orc_isect_spherical_family(*args, _p(cum), None, _p(ids), _p(fl), None)
     if kind == "lidar":
         ntw = (int(width) + tsx - 1) // tsx
         ntiles = ntw * n_elev
@@ -357,12 +377,26 @@ def _tiles(width, height, tile_w, tile_h):
     return (width + tile_w - 1) // tile_w, (height + tile_h - 1) // tile_h
 
 
+def _tile_mask(tiles, ntw, nth):
+    """uint8 [n_tiles] selecting the tiles to evaluate (None: every tile)."""
+    if tiles is None:
+        return None
+    m = np.zeros(ntw * nth, np.uint8)
+    m[np.asarray(tiles, np.int64)] = 1
+    return m
+
+
 def eval3d_fwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, flatten_ids, tile_w=16,
-               tile_h=16, velocity=None, ray_time_delta=None, prec="f32", counters=False):
+               tile_h=16, velocity=None, ray_time_delta=None, prec="f32", counters=False, tiles=None,
+               margins=False):
     """rasterize_eval3d_[dynamic_]fwd (eval3d_fwd.cu:34-308; eval3d_dynamic_fwd.cu:37-332).
 
     Returns ``rgb [H,W,C], depth [H,W], alpha [H,W], last_ids i32 [H,W]`` (+ counters
-    ``[evaluated pairs, contributing pairs]`` when requested).
+    ``[evaluated pairs, contributing pairs]`` when requested). ``tiles`` (tile indices) restricts
+    the work to those tiles; pixels of other tiles stay zero. ``margins`` appends a diagnostic
+    ``[H,W]``: per pixel the smallest ratio of a decision's distance to its threshold (alpha at
+    1/255, the transmittance cut-off at 1e-4) over a bound on the float32 error of the compared
+    value; below 1, float32 rounding can take that decision either way (meaningful in the f64 build).
     """
     _, nt = _real(prec)
     means, quats, scales = _arr(means, nt), _arr(quats, nt), _arr(scales, nt)
@@ -379,23 +413,30 @@ def eval3d_fwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, fla
     alp = np.zeros((h, w), nt)
     last = np.zeros((h, w), np.int32)
     cnt = np.zeros(2, np.int64)
+    tmask = _tile_mask(tiles, ntw, nth)   # kept alive across the call
+    mg = np.full((h, w), np.inf, nt) if margins else None
     _lib(prec).orc_eval3d_fwd(C.c_int(cdim), C.c_int(means.shape[0]), _p(means), _p(quats), _p(scales),
                               _p(colors), _p(opacity), _p(velocity), _p(rtd), C.c_int(w), C.c_int(h),
                               C.c_int(tile_w), C.c_int(tile_h), _p(ray_o), _p(ray_d), _p(offsets),
                               C.c_int(ntw), C.c_int(nth), C.c_int64(flatten_ids.shape[0]),
-                              _p(flatten_ids), _p(rgb), _p(dep), _p(alp), _p(last), _p(cnt))
+                              _p(flatten_ids), _p(rgb), _p(dep), _p(alp), _p(last), _p(cnt), _p(tmask), _p(mg))
+    out = (rgb, dep, alp, last)
     if counters:
-        return rgb, dep, alp, last, cnt
-    return rgb, dep, alp, last
+        out = out + (cnt,)
+    if margins:
+        out = out + (mg,)
+    return out
 
 
 def eval3d_bwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, flatten_ids, render_alpha,
                last_ids, v_rgb, v_depth, v_alpha, tile_w=16, tile_h=16, velocity=None,
-               ray_time_delta=None, prec="f32"):
+               ray_time_delta=None, prec="f32", tiles=None):
     """rasterize_eval3d_[dynamic_]bwd (eval3d_bwd.cu:66-403; eval3d_dynamic_bwd.cu:312-432).
 
     Returns a dict with ``v_means, v_quats, v_scales, v_opacity, v_colors, v_ray_o, v_ray_d``
-    (+ ``v_velocity, v_time_delta`` in the dynamic case).
+    (+ ``v_velocity, v_time_delta`` in the dynamic case). ``tiles`` (tile indices) restricts the
+    sum to the pixels of those tiles (the gradients of a loss whose upstream gradients are zero
+    elsewhere).
     """
     _, nt = _real(prec)
     means, quats, scales = _arr(means, nt), _arr(quats, nt), _arr(scales, nt)
@@ -415,13 +456,14 @@ def eval3d_bwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, fla
     if velocity is not None:
         out["v_velocity"] = np.zeros((n, 3), nt)
         out["v_time_delta"] = np.zeros((h, w), nt)
+    tmask = _tile_mask(tiles, ntw, nth)   # kept alive across the call
     _lib(prec).orc_eval3d_bwd(
         C.c_int(cdim), _p(means), _p(quats), _p(scales), _p(colors), _p(opacity), _p(velocity), _p(rtd),
         C.c_int(w), C.c_int(h), C.c_int(tile_w), C.c_int(tile_h), _p(ray_o), _p(ray_d), _p(offsets),
         C.c_int(ntw), C.c_int(nth), C.c_int64(flatten_ids.shape[0]), _p(flatten_ids), _p(render_alpha),
         _p(last_ids), _p(v_rgb), _p(v_depth), _p(v_alpha), _p(out["v_means"]), _p(out["v_quats"]),
         _p(out["v_scales"]), _p(out["v_opacity"]), _p(out["v_colors"]), _p(out["v_ray_o"]),
-        _p(out["v_ray_d"]), _p(out.get("v_velocity")), _p(out.get("v_time_delta")))
+        _p(out["v_ray_d"]), _p(out.get("v_velocity")), _p(out.get("v_time_delta")), _p(tmask))
     return out
 
 

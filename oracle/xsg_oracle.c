@@ -337,6 +337,22 @@ static void point_to_uvd_jacob(const orc_camera *c, int mode, v3 p, v3 dp, v3 *u
     }
 }
 
+/* Float32 decision margins (test diagnostics only; they change no result). While tl_mg is set, the
+ * UT helpers lower *tl_mg to the smallest ratio |x - threshold| / e(x) over the threshold decisions
+ * they take, e(x) being a bound on the error a float32 evaluation of x carries (F32_U = 2^-24, the
+ * float32 unit roundoff, whatever precision this build computes in). A ratio below 1 marks an
+ * outcome that float32 rounding can decide either way. tl_ut_err carries the error bounds of the
+ * last unscented_transform to ut_projection and the phase-modelled selection. */
+#define F32_U K(5.9604644775390625e-8)
+static _Thread_local real *tl_mg;
+typedef struct { real em, erx, ery, ep_max, rx_err, ry_err; } ut_err_t;
+static _Thread_local ut_err_t tl_ut_err;
+static void mg_note(real dist, real bound) {
+    if (!tl_mg) return;
+    const real r = FABS(dist) / (bound > 0 ? bound : (real)1e-30);
+    if (r < *tl_mg) *tl_mg = r;
+}
+
 static void camera_projection(const orc_camera *c, v3 p_world, v3 p_vel, real thr, real max_res,
                               real margin, int mode, int no_jac, real uvdt[4], int *valid) {
     /* projection_kernels.h:201-256 with jac_camera_projection_iteration :116-174 for the models
@@ -361,6 +377,13 @@ static void camera_projection(const orc_camera *c, v3 p_world, v3 p_vel, real th
             p_time -= residual / d_res;
         } else {
             p_time -= residual;
+        }
+        if (tl_mg) {  /* uvd carries a few roundings of the camera point and the projection */
+            const real ez = K(8) * F32_U * (FABS(pc.x) + FABS(pc.y) + FABS(pc.z) + FABS(uvd.z));
+            const real eu = K(16) * F32_U * (FABS(uvd.x) + K(1)), ev = K(16) * F32_U * (FABS(uvd.y) + K(1));
+            mg_note(uvd.z, ez);
+            mg_note(uvd.x + margin, eu); mg_note(uvd.x - K(1) - margin, eu);
+            mg_note(uvd.y + margin, ev); mg_note(uvd.y - K(1) - margin, ev);
         }
         if ((uvd.z <= K(0)) || (uvd.x < -margin) || (uvd.x > K(1) + margin) ||
             (uvd.y < -margin) || (uvd.y > K(1) + margin)) {
@@ -419,6 +442,44 @@ static int unscented_transform(const orc_camera *c, const real ut[4], v2 img, in
         cov2d->x += ut[2] * (vx * vx); cov2d->y += ut[2] * (vx * vy); cov2d->z += ut[2] * (vy * vy);
     }
     const real det = cov2d->x * cov2d->z - cov2d->y * cov2d->y;
+    if (tl_mg) {
+        /* each sigma point in pixels carries a few roundings of its own size (and of the principal
+         * point added to it); the weighted sums cancel terms |w| times larger than the mean
+         * (ut_kernels.h:17-36) */
+        const real u = F32_U;
+        real ep[7], em = 0, epm = 0;
+        for (int i = 0; i < 7; ++i) {
+            ep[i] = u * (K(3) * (FABS(pts[i].x) + FABS(pts[i].y)) + K(0.5) * (img.x + img.y));
+            const real w = FABS(i ? ut[2] : ut[0]);
+            em += w * (ep[i] + K(4) * u * (FABS(pts[i].x) + FABS(pts[i].y)));
+            epm = FMAX(epm, ep[i]);
+        }
+        /* each point's own error enters through 2 w v_i; an error d of the mean shifts every v_i by
+         * the same d and moves the covariance by 2 d sum(w_c v) + d^2 sum(w_c) only: the mean weights
+         * sum to 1, so sum(w_c v) = (w_c0 - w_m0) v_0 */
+        real dcx = 0, dcy = 0, dcz = 0, s1x = 0, s1y = 0, sw = 0;
+        for (int i = 0; i < 7; ++i) {
+            const real wc = i ? ut[2] : ut[1], w = FABS(wc);
+            const real vx = pts[i].x - mean2d->x, vy = pts[i].y - mean2d->y;
+            const real ax = FABS(vx), ay = FABS(vy);
+            dcx += w * (K(2) * ax * ep[i] + K(4) * u * ax * ax);
+            dcz += w * (K(2) * ay * ep[i] + K(4) * u * ay * ay);
+            dcy += w * ((ax + ay) * ep[i] + K(4) * u * ax * ay);
+            s1x += wc * vx; s1y += wc * vy; sw += wc;
+        }
+        dcx += K(2) * FABS(s1x) * em + FABS(sw) * em * em;
+        dcz += K(2) * FABS(s1y) * em + FABS(sw) * em * em;
+        dcy += (FABS(s1x) + FABS(s1y)) * em + FABS(sw) * em * em;
+        const real edet = dcx * FABS(cov2d->z) + dcz * FABS(cov2d->x) + K(2) * FABS(cov2d->y) * dcy +
+                          K(4) * u * (FABS(cov2d->x * cov2d->z) + cov2d->y * cov2d->y);
+        mg_note(det, edet);
+        mg_note(cov2d->x, dcx);
+        mg_note(cov2d->z, dcz);
+        tl_ut_err.em = em;
+        tl_ut_err.erx = cov2d->x > 0 ? dcx / (K(2) * SQRT(cov2d->x)) : K(1e30);
+        tl_ut_err.ery = cov2d->z > 0 ? dcz / (K(2) * SQRT(cov2d->z)) : K(1e30);
+        tl_ut_err.ep_max = epm;
+    }
     if (det <= K(0) || cov2d->x < 0 || cov2d->z < 0) return 0;
     return 1;
 }
@@ -435,6 +496,14 @@ static int ut_projection(const orc_camera *c, int mode, const real ut[4], v2 img
     radii->y = extend * SQRT(FMAX(K(0), cov2d.z));
     const int ix = !(((mean2d->x + radii->x) < 0) || (img.x < (mean2d->x - radii->x)));
     const int iy = !(((mean2d->y + radii->y) < 0) || (img.y < (mean2d->y - radii->y)));
+    if (tl_mg && result) {
+        tl_ut_err.rx_err = extend * tl_ut_err.erx + K(4) * F32_U * radii->x;
+        tl_ut_err.ry_err = extend * tl_ut_err.ery + K(4) * F32_U * radii->y;
+        const real ex = tl_ut_err.em + tl_ut_err.rx_err + K(4) * F32_U * FABS(mean2d->x);
+        const real ey = tl_ut_err.em + tl_ut_err.ry_err + K(4) * F32_U * FABS(mean2d->y);
+        mg_note(mean2d->x + radii->x, ex); mg_note(mean2d->x - radii->x - img.x, ex);
+        mg_note(mean2d->y + radii->y, ey); mg_note(mean2d->y - radii->y - img.y, ey);
+    }
     return result && ix && iy;
 }
 
@@ -457,12 +526,15 @@ void orc_projection(const orc_camera *c, int n, const real *pts, const real *vel
 void orc_project_utgs(const orc_camera *c, int n, const real *means, const real *vel,
                       const real *scales, const real *quats, const real *opacity, real width,
                       real height, const real ut[4], real thr, real max_res, real margin,
-                      uint8_t *flags, real *radii, real *means2d, real *depths) {
+                      uint8_t *flags, real *radii, real *means2d, real *depths, real *fmargin) {
     const v2 img = {width, height};
 #pragma omp parallel for schedule(static)
     for (int i = 0; i < n; ++i) {
+        real mg = K(1e30);
+        tl_mg = fmargin ? &mg : NULL;
         flags[i] = 0; radii[2 * i] = radii[2 * i + 1] = 0;
         means2d[2 * i] = means2d[2 * i + 1] = 0; depths[i] = 0;
+        if (fmargin) fmargin[i] = mg;
         const real op = opacity ? opacity[i] : K(1.0);
         if (op < ALPHA_THR_MIN) continue;
         v3 d[3];
@@ -471,6 +543,8 @@ void orc_project_utgs(const orc_camera *c, int n, const real *means, const real 
         const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
         const int ok = ut_projection(c, ORC_MODE_CENTRAL, ut, img, thr, max_res, margin,
                                      ld3(means + 3 * i), pv, op, d, &m2, &r2, &depth, &udist);
+        if (fmargin) fmargin[i] = mg;
+        tl_mg = NULL;
         if (!ok) continue;
         radii[2 * i] = r2.x; radii[2 * i + 1] = r2.y;
         flags[i] = 1;
@@ -483,30 +557,41 @@ void orc_project_utgs(const orc_camera *c, int n, const real *means, const real 
 void orc_project_utgs_phm(const orc_camera *c, int n, const real *means, const real *vel,
                           const real *scales, const real *quats, const real *opacity, real width,
                           real height, const real ut[4], real thr, real max_res, real margin,
-                          uint8_t *flags, real *radii, real *means2d, real *depths) {
+                          uint8_t *flags, real *radii, real *means2d, real *depths, real *fmargin) {
     const v2 img = {width, height};
 #pragma omp parallel for schedule(static)
     for (int i = 0; i < n; ++i) {
+        real mg = K(1e30);
+        tl_mg = fmargin ? &mg : NULL;
         flags[i] = 0; radii[2 * i] = radii[2 * i + 1] = 0;
         means2d[2 * i] = means2d[2 * i + 1] = 0; depths[i] = 0;
+        if (fmargin) fmargin[i] = mg;
         const real op = opacity ? opacity[i] : K(1.0);
-        if (op < ALPHA_THR_MIN) continue;
+        if (op < ALPHA_THR_MIN) { tl_mg = NULL; continue; }
         v3 d[3];
         ut_deltas(ut[3], quats + 4 * i, scales + 3 * i, d);
         const v3 pw = ld3(means + 3 * i);
         const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
         v2 rc = {0, 0}, rl = {0, 0}, rr = {0, 0}, mc = {0, 0}, ml = {0, 0}, mr = {0, 0};
         real dc = 0, dl = 0, dr = 0, ud = 0;
+        const real u_pi = ORC_PI * img.x / FABS(c->impl[1]);
+        /* u_distance = u_max - u_min over the sigma points: two sigma points' errors */
+#define PHM_NOTE(res_) do { if (tl_mg && (res_)) mg_note(ud - u_pi, K(2) * tl_ut_err.ep_max + K(4) * F32_U * u_pi); } while (0)
         int res = ut_projection(c, ORC_MODE_CENTRAL, ut, img, thr, max_res, margin, pw, pv, op, d,
                                 &mc, &rc, &dc, &ud);
-        if (!res) continue;
-        const real u_pi = ORC_PI * img.x / FABS(c->impl[1]);
+        PHM_NOTE(res);
+        if (!res) { if (fmargin) fmargin[i] = mg; tl_mg = NULL; continue; }
         const int r_c = res * ((ud > u_pi) + 1);
         res = ut_projection(c, ORC_MODE_NEG, ut, img, thr, max_res, margin, pw, pv, op, d, &ml, &rl,
                             &dl, &ud);
+        PHM_NOTE(res);
         const int r_l = res * ((ud > u_pi) + 1);
         res = ut_projection(c, ORC_MODE_POS, ut, img, thr, max_res, margin, pw, pv, op, d, &mr, &rr,
                             &dr, &ud);
+        PHM_NOTE(res);
+#undef PHM_NOTE
+        if (fmargin) fmargin[i] = mg;
+        tl_mg = NULL;
         const int r_r = res * ((ud > u_pi) + 1);
         if (r_l == 1 && r_r == 1) {
             flags[i] = 2; radii[2 * i] = rl.x; radii[2 * i + 1] = rl.y;
@@ -1107,6 +1192,32 @@ static void tile_limits_regular(float mx, float my, float rx, float ry, float u_
     *num += (*tmax_y - *tmin_y) * (*tmax_x - *tmin_x);
 }
 
+/* Float32 decision margins of one span's tile range (test diagnostics): lo / hi against u_min /
+ * u_max and the nearest azimuth tile boundary, the span's emptiness, and the v extent against the
+ * elevation boundaries (lidar) or the nearest v tile boundary. ex / ey bound the float32 error of the
+ * normalised centre plus radius. */
+static void span_margins(float mx, float my, float rx, float ry, float u_min, float u_max, float u_per_tile,
+                         int lidar, int n_el, const float *elev, float v_per_tile, real ex, real ey) {
+    if (!tl_mg) return;
+    const real xs[2] = {(real)mx - rx, (real)mx + rx}, ys[2] = {(real)my - ry, (real)my + ry};
+    const real lo = FMAX(xs[0], u_min), hi = FMIN(xs[1], u_max);
+    mg_note(xs[0] - u_min, ex); mg_note(xs[1] - u_max, ex);
+    mg_note(hi - lo, K(2) * ex);
+    if (hi <= lo) return;
+    for (int k = 0; k < 2; ++k) {
+        /* an end clamped to u_min / u_max is that bound exactly on every implementation */
+        const int clamped = k ? xs[1] >= u_max : xs[0] <= u_min;
+        const real t = (k ? hi : lo) / u_per_tile;
+        if (!clamped) mg_note((t - FLOOR(t + K(0.5))) * u_per_tile, ex);
+        if (lidar) {
+            for (int j = 0; j < n_el; ++j) mg_note(ys[k] - elev[j], ey);
+        } else {
+            const real tv = ys[k] / v_per_tile;
+            mg_note((tv - FLOOR(tv + K(0.5))) * v_per_tile, ey);
+        }
+    }
+}
+
 /* The float32 camera for the seam re-projection inside the lidar/spherical binning. */
 typedef struct {
     orc_camera cam;
@@ -1122,7 +1233,7 @@ void orc_isect_spherical_family(int kind, const orc_camera *cam, const real *ut,
                                 const float *means2d, const float *radii, const float *depths,
                                 const float *elev, int n_elev, int tsx, int tsy, float img_w,
                                 float img_h, const int64_t *cum, int32_t *tiles_per_gauss,
-                                int64_t *isect_ids, int32_t *flatten_ids) {
+                                int64_t *isect_ids, int32_t *flatten_ids, real *seam_margin) {
     const int lidar = kind == 0;
     int n_az, n_el;
     float u_per_tile, v_per_tile = 0;
@@ -1167,8 +1278,21 @@ void orc_isect_spherical_family(int kind, const orc_camera *cam, const real *ut,
             const real op = opacity ? opacity[i] : K(1.0);
             v2 m2, r2; real depth = 0, udist = 0;
             const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
+            real mg = K(1e30);
+            tl_mg = seam_margin ? &mg : NULL;
             const int ok = ut_projection(cam, ORC_MODE_POS, ut, img, K(1e-4), K(0.002), K(1.0),
                                          ld3(points + 3 * i), pv, op, dl, &m2, &r2, &depth, &udist);
+            if (ok && tl_mg) {
+                const real ex = (tl_ut_err.em + tl_ut_err.rx_err) / img_w + K(4) * F32_U * (FABS(m2.x) / img_w + K(1));
+                const real ey = (tl_ut_err.em + tl_ut_err.ry_err) / img_h + K(4) * F32_U * (FABS(m2.y) / img_h + K(1));
+                float ulo, uhi;
+                if (cam->rolling[0] > 0) { ulo = ceilf(u_pose / u_per_tile) * u_per_tile + 1e-6f; uhi = 1.0f; }
+                else { ulo = 0.0f; uhi = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f; }
+                span_margins((float)m2.x / img_w, (float)m2.y / img_h, (float)r2.x / img_w, (float)r2.y / img_h,
+                             ulo, uhi, u_per_tile, lidar, n_el, elev, v_per_tile, ex, ey);
+            }
+            if (seam_margin) seam_margin[i] = mg;
+            tl_mg = NULL;
             if (ok) {
                 if (cam->rolling[0] > 0) {
                     u_min = ceilf(u_pose / u_per_tile) * u_per_tile + 1e-6f;
@@ -1288,13 +1412,15 @@ void orc_eval3d_fwd(int cdim, int n, const real *means, const real *quats, const
                     const real *ray_time_delta, int width, int height, int tile_w, int tile_h,
                     const real *ray_o, const real *ray_d, const int32_t *offsets, int n_tiles_w,
                     int n_tiles_h, int64_t n_isects, const int32_t *flatten_ids, real *out_rgb,
-                    real *out_depth, real *out_alpha, int32_t *last_ids, int64_t *counters) {
+                    real *out_depth, real *out_alpha, int32_t *last_ids, int64_t *counters,
+                    const uint8_t *tile_mask, real *fmargin) {
     (void)n;
     const orc_grid g = {width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_isects};
     const int n_tiles = n_tiles_w * n_tiles_h;
     int64_t evaluated = 0, contributing = 0;
 #pragma omp parallel for schedule(dynamic, 4) reduction(+ : evaluated, contributing)
     for (int tile = 0; tile < n_tiles; ++tile) {
+        if (tile_mask && !tile_mask[tile]) continue;  /* test subset: tiles left out keep their outputs */
         const int ty = tile / n_tiles_w, tx = tile % n_tiles_w;
         int64_t rs, re;
         tile_range(&g, offsets, tile, &rs, &re);
@@ -1314,6 +1440,7 @@ void orc_eval3d_fwd(int cdim, int n, const real *means, const real *quats, const
                 const v3 ro = ld3(ray_o + 3 * pid), rd = ld3(ray_d + 3 * pid);
                 const real dtp = ray_time_delta ? ray_time_delta[pid] : K(0);
                 real T = K(1.0), depth = K(0);
+                real mg = K(1e30), relT = 0;  /* decision margins (fmargin) and T's relative error bound */
                 int32_t cur = 0;
                 for (int k = 0; k < cdim; ++k) pix[k] = 0;
                 for (int64_t k = 0; k < cnt; ++k) {
@@ -1326,9 +1453,35 @@ void orc_eval3d_fwd(int cdim, int n, const real *means, const real *quats, const
                     const real power = K(-0.5) * dot3(gcrod, gcrod);
                     const real alpha = FMIN(K(0.999), opac[gid] * EXP(power));
                     ++evaluated;
+                    real ea = 0;  /* relative error bound of a float32 alpha */
+                    if (fmargin) {
+                        /* |n x gro| is off by the error of gro (|M| = 1 / s_min times a few roundings of
+                         * the ray origin and the mean) plus |gro| times the direction error (~ the
+                         * condition s_max / s_min of M); exp turns the error of the power into a
+                         * relative one */
+                        const real *s = scales + 3 * gid;
+                        const real smin = FMIN(s[0], FMIN(s[1], s[2])), smax = FMAX(s[0], FMAX(s[1], s[2]));
+                        const v3 om = sub3(ro, xyz);
+                        const real lom = SQRT(dot3(om, om));
+                        const real lor = (ro.x != 0 || ro.y != 0 || ro.z != 0) ? SQRT(dot3(ro, ro)) + SQRT(dot3(xyz, xyz)) : 0;
+                        const real dist = SQRT(dot3(gcrod, gcrod)), lg = SQRT(dot3(gro, gro));
+                        const real e_d = F32_U * (K(3) * (lom / smin + (smax / smin) * lg) + lor / smin);
+                        ea = K(4) * F32_U + dist * e_d + K(2) * F32_U * FABS(power);
+                        const real araw = opac[gid] * EXP(power);
+                        if (araw < K(0.999)) {
+                            const real r = FABS(araw - K(1.0) / K(255.0)) / (K(2) * ea * araw + (real)1e-30);
+                            if (r < mg) mg = r;
+                        }
+                    }
                     if (alpha < K(1.0) / K(255.0)) continue;
                     const real hit_t = -dot3(gro, grd) / dot3(grd, grd);
                     const real next_T = T * (K(1.0) - alpha);
+                    if (fmargin) {
+                        const real e1 = (ea * alpha + F32_U) / (K(1.0) - alpha) + K(2) * F32_U;
+                        const real r = FABS(next_T - K(1e-4)) / (K(2) * next_T * (relT + e1) + (real)1e-30);
+                        if (r < mg) mg = r;
+                        relT += e1;
+                    }
                     if (next_T <= K(1e-4)) break;
                     const real vis = alpha * T;
                     depth += vis * hit_t;
@@ -1338,6 +1491,7 @@ void orc_eval3d_fwd(int cdim, int n, const real *means, const real *quats, const
                     ++contributing;
                 }
                 out_alpha[pid] = K(1.0) - T;
+                if (fmargin) fmargin[pid] = mg;
                 out_depth[pid] = depth;
                 for (int c = 0; c < cdim; ++c) out_rgb[pid * cdim + c] = pix[c];
                 last_ids[pid] = cur;
@@ -1397,12 +1551,13 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                     const real *render_alpha, const int32_t *last_ids, const real *v_rgb,
                     const real *v_depth, const real *v_alpha, real *v_means, real *v_quats,
                     real *v_scales, real *v_opac, real *v_colors, real *v_ray_o, real *v_ray_d,
-                    real *v_velocity, real *v_time_delta) {
+                    real *v_velocity, real *v_time_delta, const uint8_t *tile_mask) {
     const orc_grid g = {width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_isects};
     const int n_tiles = n_tiles_w * n_tiles_h;
     const real MAX_ALPHA = K(0.99);
 #pragma omp parallel for schedule(dynamic, 4)
     for (int tile = 0; tile < n_tiles; ++tile) {
+        if (tile_mask && !tile_mask[tile]) continue;  /* test subset: only these tiles' pixels contribute */
         const int ty = tile / n_tiles_w, tx = tile % n_tiles_w;
         int64_t rs, re;
         tile_range(&g, offsets, tile, &rs, &re);

@@ -13,6 +13,7 @@ import torch
 
 from oracle import oracle as O
 from xsimgs_amd import synthetic as S
+from tests import _judge as J
 from tests._util import GRAD_ATOL, GRAD_RTOL, RENDER_ATOL, frac_close, np_, report
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -89,34 +90,6 @@ def _check(name, got, ref, atol, rtol=0.0, min_frac=1.0):
     assert fc >= min_frac, name
 
 
-def _check_seam_keys(ids, fl, ref_ids, ref_fl, n_tiles):
-    """Lidar / spherical binning. Every key is bit-exact except the depth bits of the second span
-    of a seam (flag 2) Gaussian: that depth comes from the UT re-projection inside the binning
-    (phm_lidar_tiling.cu:205-226), float32 arithmetic whose last bits differ between any two
-    implementations. So: the same (Gaussian, tile) entries; identical depth bits where the depth
-    is an input; re-projected depths within 1e-5 relative; and the output sorted stably by its
-    own keys over the reference's bits (so the order can differ from the fixture only between
-    entries whose depths are that close)."""
-    assert ids.shape == ref_ids.shape and fl.shape == ref_fl.shape
-    tile = lambda k: k >> 32
-    got = {(int(f), int(t)): int(k) for f, t, k in zip(fl, tile(ids), ids)}
-    ref = {(int(f), int(t)): int(k) for f, t, k in zip(ref_fl, tile(ref_ids), ref_ids)}
-    assert got.keys() == ref.keys()
-    dbits = lambda k: np.array([k & 0xFFFFFFFF], np.uint32).view(np.float32)[0]
-    n_diff = 0
-    for key, k in got.items():
-        if k != ref[key]:
-            n_diff += 1
-            assert abs(dbits(k) - dbits(ref[key])) <= 1e-5 * abs(dbits(ref[key])), key
-    bits = 32 + int(np.floor(np.log2(np.float32(n_tiles)))) + 1
-    masked = ids.view(np.uint64) & np.uint64((1 << bits) - 1)
-    assert np.all(masked[1:] >= masked[:-1])
-    tie = masked[1:] == masked[:-1]
-    assert np.all(fl[1:][tie] >= fl[:-1][tie])      # stable: ties keep Gaussian order
-    print(f"seam keys: {n_diff} of {ids.shape[0]} differ in re-projected depth bits only", flush=True)
-    assert n_diff <= 0.05 * ids.shape[0]
-
-
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", CASES)
 def test_hip_path_reproduces_fixture(dev, name):
@@ -153,15 +126,14 @@ def test_hip_path_reproduces_fixture(dev, name):
         _check("pixel time delta", rtd, f["ray_time_delta"], 1e-6)
 
     # UT projection
-    proj = cam.ext_cls.projection_utgs_phm if name in ("lidar_phm", "spherical") else cam.ext_cls.projection_utgs
+    phm = name in ("lidar_phm", "spherical")
+    vel_np = f.get("velocity")
+    proj = cam.ext_cls.projection_utgs_phm if phm else cam.ext_cls.projection_utgs
     flags, radii, m2, dep = proj(pack, means, vel, scales, quats, opac, W, H)
     agree = (np_(flags) == f["ut_flags"]).mean()
     print("ut flags agree", agree, flush=True)
-    assert agree > 0.99
-    both = (np_(flags) > 0) & (f["ut_flags"] > 0) & (np_(flags) == f["ut_flags"])
-    _check("ut means2d", np_(m2)[both], f["means2d"][both], 2e-2, 1e-5, 0.99)
-    _check("ut radii", np_(radii)[both], f["radii"][both], 2e-2, 1e-4, 0.99)
-    _check("ut depth", np_(dep)[both], f["depths"][both], 1e-5, 1e-5, 0.99)
+    J.judge_ut((flags, radii, m2, dep), spec, f["means"], f["scales"], f["quats"], f["opacity"], W, H, phm=phm,
+               label=name, vel=vel_np)
 
     # binning from the fixture's projections: bit-exact
     m2f, rf, df, ff = T("means2d"), T("radii"), T("depths"), T("ut_flags")
@@ -179,20 +151,25 @@ def test_hip_path_reproduces_fixture(dev, name):
         _, ids_u, fl_u = binning(sort=False)
         assert np.array_equal(np_(ids_u), f["isect_ids_unsorted"])
         assert np.array_equal(np_(fl_u), f["flatten_ids_unsorted"])
-    assert np.array_equal(np_(tpg), f["tiles_per_gauss"])
     nth, ntw = f["offsets"].shape
-    if spec.kind == "pinhole":
-        assert np.array_equal(np_(ids), f["isect_ids"])
-        assert np.array_equal(np_(fl), f["flatten_ids"])
-    else:
-        _check_seam_keys(np_(ids), np_(fl), f["isect_ids"], f["flatten_ids"], ntw * nth)
+    und = None
+    if spec.kind != "pinhole":
+        und = O.isect_spherical_family(spec.kind, spec, f["means"], f["scales"], f["quats"], f["opacity"],
+                                       f["ut_flags"], f["means2d"], f["radii"], f["depths"], tsx, tsy, W, H,
+                                       elev=f.get("elev"), vel=vel_np, seam_margins=True) < 1.0
+    fs = lambda g, t: J.first_span_member(spec.kind, spec, g, t, f["means2d"], f["radii"], W, H, tsx, tsy,
+                                          f.get("elev"))
+    J.check_binning(spec.kind, (np_(tpg), np_(ids), np_(fl)), (f["tiles_per_gauss"], f["isect_ids"],
+                    f["flatten_ids"]), f["ut_flags"], f["depths"], ntw * nth, name, und, fs)
     off = _C.isect_offset_encode(ids, ntw, nth)
-    assert np.array_equal(np_(off), f["offsets"])
+    assert np.array_equal(np_(off), O.offset_encode(np_(ids), ntw, nth))
+    if np.array_equal(np_(tpg), f["tiles_per_gauss"]):
+        assert np.array_equal(np_(off), f["offsets"])
     # the sorted fill's own tile offsets (extension, what ut_gs_tiling uses) are the encoder's
     fill_off = torch.full((nth, ntw), -7, dtype=torch.int32, device=dev)
     _, ids2, _ = binning(tile_offsets=fill_off)
     assert np.array_equal(np_(ids2), np_(ids))
-    assert np.array_equal(np_(fill_off), f["offsets"])
+    assert np.array_equal(np_(fill_off), np_(off))
 
     # rays
     ro, rd = cam.camera_rays(W, H)
