@@ -141,6 +141,19 @@ int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, const float*
                int has_dc, float* d_coeffs, float* d_coeffs_dc, float* d_positions,
                float* d_origin, void* workspace, xsg_stream_t stream);
 
+/* xsg_sh_bwd without a workspace. No counterpart in the reference: for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). The
+ * per-block d_origin partials live in a file-scope device array of this library instead, one per GPU
+ * (1.5 MiB, held until the process ends), sized for n <= XSG_SH_BWD_NOALLOC_MAX_N Gaussians; a larger
+ * n is rejected with XSG_ERR_INVALID before anything runs. It calls no allocator. Every call on one GPU
+ * shares that array: calls that overlap on a GPU (several streams or host threads) race and must be
+ * serialised by the caller. Outputs as xsg_sh_bwd; the stream must belong to the current device. */
+#define XSG_SH_BWD_NOALLOC_MAX_N (1LL << 25)
+int xsg_sh_bwd_noalloc(int degree, const float* origin, int64_t n, int dim, const float* positions,
+                       const float* coeffs, const uint32_t* mask, int layout_3kn, const float* d_output,
+                       int has_dc, float* d_coeffs, float* d_coeffs_dc, float* d_positions,
+                       float* d_origin, xsg_stream_t stream);
+
 /* ------------------------------------------------- scene-assembly producers */
 /* packed_mask_from_instances (gs_masking.cu:8-47): out[(n + 31) / 32], bit i % 32 of word i / 32 set
  * when instance_ids[i] < 0 or instance_mask[instance_ids[i]] != 0. Ids at or past n_instances count

@@ -56,6 +56,15 @@ def test_host_queries(lib):
     lib.xsg_radix_sort_workspace_bytes.restype = C.c_size_t
     assert lib.xsg_eval3d_bwd_workspace_bytes(C.c_int64(1000), 3) >= 1000 * 6 * 4
     assert lib.xsg_radix_sort_workspace_bytes(C.c_int64(1 << 20)) > 0
+    # the allocation-free SH backward rejects sizes over its scratch limit on the host, before any
+    # pointer is used or any HIP call is made
+    vp = C.c_void_p
+    lib.xsg_sh_bwd_noalloc.argtypes = [C.c_int, vp, C.c_int64, C.c_int, vp, vp, vp, C.c_int, vp, C.c_int, vp, vp,
+                                       vp, vp, vp]
+    lib.xsg_last_error.restype = C.c_char_p
+    assert lib.xsg_sh_bwd_noalloc(3, None, (1 << 25) + 1, 16, None, None, None, 0, None, 0, None, None, None, None,
+                                  None) == -1
+    assert b"scratch limit" in lib.xsg_last_error()
 
 
 def test_invalid_arguments_fail_before_launch(lib):

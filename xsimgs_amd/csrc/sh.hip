@@ -7,6 +7,8 @@
 // coalesced per thread and is read directly. The backward writes every band of d_coeffs (zeros
 // above the used degree), d_positions without atomics, and per-block d_origin partials that a
 // second kernel sums in a fixed order.
+#include <mutex>
+
 #include "xsg_common.h"
 
 namespace {
@@ -449,26 +451,26 @@ extern "C" size_t xsg_sh_bwd_workspace_bytes(int64_t n) {
     return (size_t)(xsg_blocks(n > 0 ? n : 1, kBlock)) * 3 * sizeof(float);
 }
 
-extern "C" int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
-                          const float* coeffs, const uint32_t* mask, int layout_3kn,
-                          const float* d_output, int has_dc, float* d_coeffs, float* d_coeffs_dc,
-                          float* d_positions, float* d_origin, void* workspace, xsg_stream_t stream) {
+namespace {
+
+// d_coeffs, d_coeffs_dc, d_positions and the per-block d_origin partials (`part`, 3 floats per
+// kBlock Gaussians), then their fixed-order sum into d_origin. Shared by both backward entry points.
+int sh_bwd_run(int degree, const float* origin, int64_t n, int dim, const float* positions,
+               const float* coeffs, const uint32_t* mask, int layout_3kn, const float* d_output, int has_dc,
+               float* d_coeffs, float* d_coeffs_dc, float* d_positions, float* d_origin, float* part,
+               hipStream_t s) {
     static const int ref_dims[5] = {1, 4, 9, 16, 25};
     if (degree < 0 || degree > 4)
         return xsg_fail(XSG_ERR_INVALID, "Unsupported spherical harmonics degree: %d", degree);
     if (dim < ref_dims[degree] - (has_dc ? 1 : 0))
         return xsg_fail(XSG_ERR_INVALID, "coeffs hold %d bands, degree %d needs %d", dim, degree,
                         ref_dims[degree] - (has_dc ? 1 : 0));
-    if (n < 0 || !workspace) return xsg_fail(XSG_ERR_INVALID, "xsg_sh_bwd: bad arguments");
-    if (const int rc = xsg_check_workspace(workspace, "xsg_sh_bwd")) return rc;
-    const hipStream_t s = (hipStream_t)stream;
     if (n == 0) {  // d_origin = 0 without a memset node (callers may capture this in a graph)
-        sum_partials_kernel<<<1, kSumThreads, 0, s>>>((const float*)workspace, 0, d_origin);
+        sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, 0, d_origin);
         XSG_TRY_LAUNCH("sh_bwd");
         return XSG_OK;
     }
     const unsigned nb = xsg_blocks(n, kBlock);
-    float* part = (float*)workspace;
     const bool l = layout_3kn != 0;
     const dim3 g(nb);
 #define XSG_B(D) \
@@ -485,4 +487,63 @@ extern "C" int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, c
     sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, (int)nb, d_origin);
     XSG_TRY_LAUNCH("sh_bwd");
     return XSG_OK;
+}
+
+// Scratch of xsg_sh_bwd_noalloc: the d_origin partials of up to XSG_SH_BWD_NOALLOC_MAX_N Gaussians
+// (3 floats per kBlock Gaussians, 1.5 MiB). One copy per GPU, allocated with the code object and held
+// until the process ends; every call on a GPU shares it.
+constexpr int64_t kNoAllocParts = 3 * ((XSG_SH_BWD_NOALLOC_MAX_N + kBlock - 1) / kBlock);
+static __device__ __align__(256) float scratch[kNoAllocParts];
+
+// The device address of `scratch` on each GPU, looked up once per device (on the first call there,
+// with that device current). In host code `scratch` names a host-side stand-in, never memory a
+// kernel may touch: kernels only ever get these addresses.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices];
+
+int scratch_for_current_device(float** out) {
+    int dev = -1;
+    const hipError_t e0 = hipGetDevice(&dev);
+    if (e0 != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return xsg_fail(XSG_ERR_LAUNCH, "xsg_sh_bwd_noalloc: no usable current device (%s, device %d)",
+                        hipGetErrorString(e0), dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return xsg_fail(XSG_ERR_LAUNCH, "xsg_sh_bwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                            dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return XSG_OK;
+}
+
+}  // namespace
+
+extern "C" int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
+                          const float* coeffs, const uint32_t* mask, int layout_3kn,
+                          const float* d_output, int has_dc, float* d_coeffs, float* d_coeffs_dc,
+                          float* d_positions, float* d_origin, void* workspace, xsg_stream_t stream) {
+    if (n < 0 || !workspace) return xsg_fail(XSG_ERR_INVALID, "xsg_sh_bwd: bad arguments");
+    if (const int rc = xsg_check_workspace(workspace, "xsg_sh_bwd")) return rc;
+    return sh_bwd_run(degree, origin, n, dim, positions, coeffs, mask, layout_3kn, d_output, has_dc, d_coeffs,
+                      d_coeffs_dc, d_positions, d_origin, (float*)workspace, (hipStream_t)stream);
+}
+
+extern "C" int xsg_sh_bwd_noalloc(int degree, const float* origin, int64_t n, int dim, const float* positions,
+                                  const float* coeffs, const uint32_t* mask, int layout_3kn,
+                                  const float* d_output, int has_dc, float* d_coeffs, float* d_coeffs_dc,
+                                  float* d_positions, float* d_origin, xsg_stream_t stream) {
+    if (n < 0) return xsg_fail(XSG_ERR_INVALID, "xsg_sh_bwd_noalloc: bad arguments");
+    if (n > XSG_SH_BWD_NOALLOC_MAX_N)
+        return xsg_fail(XSG_ERR_INVALID,
+                        "xsg_sh_bwd_noalloc: %lld Gaussians exceed the scratch limit of %lld; use xsg_sh_bwd with a "
+                        "workspace", (long long)n, (long long)XSG_SH_BWD_NOALLOC_MAX_N);
+    float* part = nullptr;
+    if (const int rc = scratch_for_current_device(&part)) return rc;
+    return sh_bwd_run(degree, origin, n, dim, positions, coeffs, mask, layout_3kn, d_output, has_dc, d_coeffs,
+                      d_coeffs_dc, d_positions, d_origin, part, (hipStream_t)stream);
 }
