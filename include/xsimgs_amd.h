@@ -254,8 +254,10 @@ int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible,
                    int32_t* flatten_ids, int32_t* tile_offsets, int64_t n_tile_offsets, xsg_stream_t stream);
 
 /* offsets [n_cams, n_tiles_h, n_tiles_w]: first sorted index of every (camera, tile). Keys of a
- * negative depth (sign-extended bits, all ones above bit 31) sort after every tile and are in no
- * tile's range; the reference's encoder races on them (tiling_common.cu:41-60). */
+ * negative depth (sign-extended bits, all ones above bit 31) sort after every tile; the offsets are
+ * those of the other keys (the reference's encoder races on them, tiling_common.cu:41-60). The
+ * compositor's last tile runs to n_isects (utils.h:52-57), so it composites those entries after its
+ * own, as the reference's compositor does. */
 int xsg_isect_offset_encode(const int64_t* isect_ids, int64_t n_isects, int n_tiles_w, int n_tiles_h,
                             int n_cams, int32_t* offsets, xsg_stream_t stream);
 

@@ -374,3 +374,132 @@ def test_eval3d_bwd_without_ray_grads(dev, cfg0):
     assert b[5] is None and b[6] is None
     for x, y in zip(a[:5], b[:5]):
         assert frac_close(np_(y), np_(x), GRAD_ATOL, GRAD_RTOL) == 1.0
+
+
+# ------------------------------------------------------------------ scenes built for one rule each
+def _pinhole_scene(dev, seed, n=300, W=52, H=38, f=40.0):
+    """Random Gaussians in front of a small pinhole camera, projected by the GPU's UT."""
+    g = np.random.default_rng(seed)
+    z = np.exp(g.uniform(np.log(2.0), np.log(20.0), n))
+    xy = g.uniform(-0.8, 0.8, (n, 2)) * z[:, None] * np.array([W / 2 / f, H / 2 / f])
+    means = np.concatenate([xy, z[:, None]], 1).astype(np.float32)
+    scales = np.exp(g.uniform(np.log(0.02), np.log(0.3), (n, 3))).astype(np.float32)
+    quats = g.standard_normal((n, 4)).astype(np.float32)
+    opac = g.uniform(0.05, 0.95, n).astype(np.float32)
+    colors = g.uniform(0.0, 1.0, (n, 3)).astype(np.float32)
+    spec = synthetic.pinhole(W, H, f, f, W / 2, H / 2)
+    cam = frame.make_camera(spec, dev)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    flags, radii, m2, dep = cam.ext_cls.projection_utgs(cam.pack, T(means), None, T(scales), T(quats), T(opac), W, H)
+    ro, rd = cam.camera_rays(W, H)
+    return dict(means=means, scales=scales, quats=quats, opac=opac, colors=colors, W=W, H=H, spec=spec,
+                radii=radii, m2=m2, dep=dep, ro=np_(ro), rd=np_(rd))
+
+
+def _render_and_judge(dev, s, off, fl, tsx, tsy, label, g):
+    """GPU forward and backward (with ray gradients) against the oracle on the given binning."""
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    W, H = s["W"], s["H"]
+    means, quats, scales, opac, colors = (T(s[k]) for k in ("means", "quats", "scales", "opac", "colors"))
+    ro, rd = T(s["ro"]), T(s["rd"])
+    rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0), opac.view(1, -1),
+                                                      W, H, tsx, tsy, ro, rd, off, fl)
+    got = [np_(rgb), np_(depth), np_(alpha), np_(last)]
+    inp = dict(means=s["means"], quats=s["quats"], scales=s["scales"], opac=s["opac"], colors=s["colors"],
+               ro=s["ro"], rd=s["rd"])
+    hoff, hfl = np_(off), np_(fl)
+    ref32 = O.eval3d_fwd(s["means"], s["quats"], s["scales"], s["colors"], s["opac"], s["ro"], s["rd"], hoff, hfl,
+                         tsx, tsy)
+    J.judge_renders(got, ref32, inp, hoff, hfl, tsx, tsy, label=label)
+    vr = (g.standard_normal((H, W, 3)) * 1e-3).astype(np.float32)
+    vd = (g.standard_normal((H, W)) * 1e-3).astype(np.float32)
+    va = (g.standard_normal((H, W)) * 1e-3).astype(np.float32)
+    names = ["v_means", "v_quats", "v_scales", "v_opacity", "v_colors"]
+    refs = J.bwd_runs(inp, hoff, hfl, got[2], got[3], vr, vd, va, tsx, tsy, None)
+    rows = np.unique(hfl)
+    for ray_grads in (True, False):
+        out = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, alpha, last,
+                                      T(vr), T(vd), T(va), ray_grads)
+        J.judge_grads(dict(zip(names, out[:5])), refs, rows, label=f"{label} ray_grads={ray_grads}")
+    return got
+
+
+def test_eval3d_negative_depth_last_tile(dev):
+    """Entries keyed with a negative depth sort after every tile (tiling_common.cuh:37); the last tile's
+    range runs to n_isects (utils.h:52-57), so the last tile composites them after its own entries, in
+    the forward and the backward, exactly as the oracle does with the same offsets."""
+    s = _pinhole_scene(dev, 41)
+    W, H = s["W"], s["H"]
+    # Gaussians in front of the last tile's pixels (bottom right), keyed with a negative depth
+    g = np.random.default_rng(42)
+    k = 30
+    px = np.stack([g.uniform(48, 52, k), g.uniform(32, 38, k)], 1)
+    z = g.uniform(3.0, 8.0, k)
+    corner = np.stack([(px[:, 0] - W / 2) / 40.0 * z, (px[:, 1] - H / 2) / 40.0 * z, z], 1).astype(np.float32)
+    s["means"][:k] = corner
+    s["opac"][:k] = 0.6
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    cam = frame.make_camera(s["spec"], dev)
+    flags, radii, m2, dep = cam.ext_cls.projection_utgs(cam.pack, T(s["means"]), None, T(s["scales"]),
+                                                        T(s["quats"]), T(s["opac"]), W, H)
+    dep = dep.clone()
+    dep[:k] = -dep[:k]
+    ntx, nty = (W + 15) // 16, (H + 15) // 16
+    off = torch.full((nty, ntx), -7, dtype=torch.int32, device=dev)
+    tpg, ids, fl = _C.isect_regular_tiles(m2, radii, dep, W, H, 16, 16, tile_offsets=off)
+    hids = np_(ids)
+    first_neg = int(np.argmax(hids < 0)) if (hids < 0).any() else hids.size
+    n_neg = int((hids < 0).sum())
+    print("entries", hids.size, "negative-depth entries", n_neg, "from index", first_neg, flush=True)
+    assert n_neg > 20 and np.all(hids[first_neg:] < 0)
+    got = _render_and_judge(dev, s, off, fl, 16, 16, "negative-depth", np.random.default_rng(43))
+    # the last tile's pixels do composite entries past the last non-negative key
+    assert int((got[3] >= first_neg).sum()) > 0
+
+
+def test_eval3d_bwd_clamp_band(dev):
+    """Pairs with op * vis in (0.99, 0.999): forward alpha unclamped, backward at 0.99 with no geometry
+    or opacity gradient (eval3d_bwd.cu:38, 202, 243). Gaussians centred on pixel rays with opacities
+    in that band make most of their pairs fall there."""
+    s = _pinhole_scene(dev, 51)
+    W, H = s["W"], s["H"]
+    g = np.random.default_rng(52)
+    k = 60
+    pi, pj = g.integers(0, H, k), g.integers(0, W, k)
+    t = g.uniform(3.0, 15.0, k)
+    s["means"][:k] = (s["ro"][pi, pj] + t[:, None] * s["rd"][pi, pj]).astype(np.float32)
+    s["opac"][:k] = g.uniform(0.9905, 0.9989, k).astype(np.float32)
+    s["scales"][:k] = np.exp(g.uniform(np.log(0.03), np.log(0.1), (k, 3))).astype(np.float32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    cam = frame.make_camera(s["spec"], dev)
+    flags, radii, m2, dep = cam.ext_cls.projection_utgs(cam.pack, T(s["means"]), None, T(s["scales"]),
+                                                        T(s["quats"]), T(s["opac"]), W, H)
+    ntx, nty = (W + 15) // 16, (H + 15) // 16
+    off = torch.full((nty, ntx), -7, dtype=torch.int32, device=dev)
+    _, ids, fl = _C.isect_regular_tiles(m2, radii, dep, W, H, 16, 16, tile_offsets=off)
+    got = _render_and_judge(dev, s, off, fl, 16, 16, "clamp-band", np.random.default_rng(53))
+    # the band is exercised: on the pixels the Gaussians are centred on, alpha passes 0.99
+    in_band = int((got[2][pi, pj] > 0.99).sum())
+    print("pixels with alpha above 0.99 at a band Gaussian's centre:", in_band, "of", k, flush=True)
+    assert in_band >= k // 3
+
+
+@pytest.mark.parametrize("timing", ["global", "rolling_pos", "rolling_neg"])
+def test_ut_phm_seam_cases(dev, timing):
+    """The phase-modelled UT on the seam cases pinned on the CPU (tests/test_oracle_phm.py): far from
+    the seams, straddling the image seam, straddling u_pose, a footprint crossing the image edge, and
+    the half-turn camera's one-sided case; flags and the stored side's outputs against the oracle."""
+    from tests.test_oracle_phm import seam_cases
+    for name, spec, mu, q, s, op, flag, side in seam_cases(timing):
+        cam = frame.make_camera(spec, dev)
+        T = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+        got = cam.ext_cls.projection_utgs_phm(cam.pack, T(mu[None]), None, T([s]), T([q]), T([op]), spec.width,
+                                              spec.height)
+        f, r, m2, d = (np_(x) for x in got)
+        rf, rr, rm, rd = O.project_utgs(spec, mu[None].astype(np.float32), np.array([s], np.float32),
+                                        np.array([q], np.float32), np.array([op], np.float32), spec.width,
+                                        spec.height, phm=True)
+        print(timing, name, "gpu", int(f[0]), m2[0], r[0], "| oracle", int(rf[0]), rm[0], rr[0], flush=True)
+        assert int(f[0]) == int(rf[0]) == flag, name
+        assert np.allclose(m2, rm, atol=2e-2) and np.allclose(r, rr, atol=2e-2, rtol=1e-4), name
+        assert np.allclose(d, rd, rtol=1e-6), name
