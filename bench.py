@@ -9,7 +9,12 @@ Also reported: per-stage times (HIP events on the stream the kernels run on) wit
 algorithmic HBM GB/s against the 8 TB/s peak, a `roofline` object for the dominant kernel, and
 a `cpu_baseline` of the same frame run by the CPU oracle on this host's cores.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+The same line carries `configs`: the other benchmark configurations measured the same way (cfg1
+forward only; cfg3 the 2048x128 lidar range image; cfg4 the six-camera rig; cfg2_frustum the cfg2
+scene with every Gaussian inside the field of view), each with ms per frame, Mpix/s, Gaussians/s,
+per-stage times, the roofline of its dominant kernel and a CPU-oracle baseline on a bounded sample.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--configs cfg1,cfg3,...]
 """
 from __future__ import annotations
 
@@ -35,6 +40,9 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--stage-reps", type=int, default=20)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--configs", default="cfg1,cfg3,cfg4,cfg2_frustum",
+                   help="comma list of further configurations reported under `configs` ('' for none)")
+    p.add_argument("--config-steps", type=int, default=5)
     p.add_argument("--profile-stages", default="", help="comma list of stages to run alone (for rocprof)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 256 MiB device copy 5 times (scale of the rocprofv3 byte counters)")
@@ -140,6 +148,264 @@ def extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales,
     return rows
 
 
+def binning_alg_bytes(kind, n, n_isects, n_tiles, n_flag2=0):
+    """Bytes the binning cannot avoid: read each Gaussian's projection once (means2d 8, radii 8, depth 4,
+    + flag 1 for the lidar / spherical kinds), write tiles_per_gauss (4) once, write each intersection's
+    key and id (12) once, write each tile's offset (4) once; a seam Gaussian's re-projection reads its
+    point, scale, quaternion and opacity (44). The depth pre-order, run expansion and scans the
+    implementation adds are not priced, so the fraction is that of the unavoidable traffic."""
+    per_g = 24 + (1 if kind != "pinhole" else 0)
+    return per_g * n + 12 * n_isects + 4 * n_tiles + 44 * n_flag2
+
+
+def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extensions=False):
+    import xsimgs_amd  # noqa: F401  (fails loudly without the native libraries)
+    from xsimgs_amd import _C, frame, synthetic
+    from xsimgs_amd.rendering import rasterize as rz
+    from xsimgs_amd.rendering import rasterize_dynamic as rzd  # noqa: F401
+
+    dev = torch.device("cuda:0")
+    sc = synthetic.make(name, seed=args.seed)
+    cam_spec = sc.cameras[0]
+    W, H = cam_spec.width, cam_spec.height
+    st = frame.prepare(sc, dev)
+    n_cams = len(sc.cameras)
+    backward = sc.backward
+    grads = None
+    if backward:
+        grads = [tuple(g.to(dev) for g in (sc.grad_rgb[i], sc.grad_depth[i], sc.grad_alpha[i]))
+                 for i in range(n_cams)]
+
+    def step():
+        frame.zero_grads(st)
+        for ci in range(n_cams):
+            if backward:
+                frame.render_frame(st, backward=True, grads=grads[ci], cam_index=ci)
+            else:
+                with torch.no_grad():
+                    frame.render_frame(st, backward=False, cam_index=ci)
+
+    # the compositor calls are bracketed by HIP events on the stream they run on (torch's current
+    # stream), inside the timed steps
+    live = {"eval3d_fwd": [], "eval3d_bwd": []}
+    orig = {"eval3d_fwd": rz.rasterize_eval3d_fwd, "eval3d_bwd": rz.rasterize_eval3d_bwd}
+
+    def timed(kname):
+        fn = orig[kname]
+
+        def call(*a, **k):
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            out = fn(*a, **k)
+            ev1.record()
+            live[kname].append((ev0, ev1))
+            return out
+        return call
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = timed("eval3d_fwd"), timed("eval3d_bwd")
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = orig["eval3d_fwd"], orig["eval3d_bwd"]
+    ms = (t1 - t0) * 1e3 / steps
+    live_ms = {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in live.items() if v}
+    mpix = W * H * n_cams / (ms * 1e-3) / 1e6
+
+    # ---------------------------------------------------------------- per-stage timing (per camera)
+    N = sc.n
+    K = sc.sh_coeffs.shape[1] if sc.sh_coeffs is not None else 0
+    tsx, tsy = sc.tile_size
+    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
+    kind = cam_spec.kind
+    stage_rows, info = {}, []
+    with torch.no_grad():
+        means, quats = st.means.detach(), st.quats.detach()
+        scales = torch.exp(st.log_scales.detach())
+        opac = torch.sigmoid(st.opacity_logits.detach())
+        sh = st.sh.detach() if st.sh is not None else None
+        for ci in range(n_cams):   # the compositor's loaded work of every camera (its algorithmic bytes)
+            cam = st.cams[ci]
+            origin = cam.pose.t
+            colors = (_C.spherical_harmonics_fused_fwd(sc.sh_degree, origin, means, sh, None, False)
+                      if sh is not None else st.colors.detach())
+            cdim = colors.shape[-1]
+            flags, radii, m2, dep = cam.ut_gs_projection(means, scales, quats, W, H, opacity=opac,
+                                                         use_phm=sc.use_phm)
+            tpg, ids, fl = cam.isect_gs_tiles(means, scales, quats, W, H, flags, radii, m2, dep, opacity=opac,
+                                              tile_size_x=tsx, tile_size_y=tsy)
+            off = _C.isect_offset_encode(ids, ntx, nty)
+            ro, rd = cam.camera_rays(W, H)
+            pairs = torch.zeros(2, dtype=torch.int64, device=dev)
+            rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0),
+                                                              opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl,
+                                                              pair_counts=pairs)
+            c = dict(cam=cam, origin=origin, colors=colors, cdim=cdim, proj=(flags, radii, m2, dep), ids=ids, fl=fl,
+                     off=off, ro=ro, rd=rd, alpha=alpha, last=last, n_isects=int(fl.numel()),
+                     visible=int((tpg > 0).sum()), n_flag2=int((flags == 2).sum()))
+            c["fwd_evaluated"], c["contributing"] = (int(x) for x in pairs.cpu())
+            n_isects = c["n_isects"]
+            starts = off.view(-1).long()
+            ends = torch.cat([starts[1:], torch.tensor([n_isects], device=dev)])
+            lt = torch.nn.functional.pad(last, (0, ntx * tsx - W, 0, nty * tsy - H)).view(nty, tsy, ntx, tsx)
+            tile_max = lt.amax(dim=(1, 3)).reshape(-1).long()
+            rng = (ends - starts).clamp(min=0)
+            # loaded intersections: the forward up to the batch holding the tile's last contribution and
+            # its terminating element, the backward from the tile's largest last id down to the start
+            c["bwd_loaded"] = int((tile_max - starts + 1).clamp(min=0).minimum(rng).sum())
+            bs = tsx * tsy
+            fwd_batches = ((tile_max - starts + 2).clamp(min=1) + bs - 1) // bs
+            c["fwd_loaded"] = int(torch.minimum(rng, fwd_batches * bs).sum())
+            if backward:
+                g_rgb, g_d, g_a = grads[ci]
+                bpairs = torch.zeros(2, dtype=torch.int64, device=dev)
+                bo = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, alpha,
+                                             last, g_rgb, g_d, g_a, False, pair_counts=bpairs)
+                c["v_colors"] = bo[4]
+                c["bwd_evaluated"], c["bwd_composited"] = (int(x) for x in bpairs.cpu())
+            info.append(c)
+        c0 = info[0]
+        cam, origin, colors, cdim = c0["cam"], c0["origin"], c0["colors"], c0["cdim"]
+        flags, radii, m2, dep = c0["proj"]
+        ids, fl, off, ro, rd, alpha, last = (c0[k] for k in ("ids", "fl", "off", "ro", "rd", "alpha", "last"))
+        n_isects = c0["n_isects"]
+        enc_reads = 8 * int(math.ceil(math.log2(n_isects + 1))) if n_isects else 0
+        stages = {
+            "sh_fwd": (lambda: _C.spherical_harmonics_fused_fwd(sc.sh_degree, origin, means, sh, None, False),
+                       (24 + 12 * K) * N) if sh is not None else None,
+            "ut_projection": (lambda: cam.ut_gs_projection(means, scales, quats, W, H, opacity=opac,
+                                                            use_phm=sc.use_phm), 65 * N),
+            "binning": (lambda: cam.isect_gs_tiles(means, scales, quats, W, H, flags, radii, m2, dep, opacity=opac,
+                                                   tile_size_x=tsx, tile_size_y=tsy,
+                                                   tile_offsets=torch.empty(nty, ntx, dtype=torch.int32,
+                                                                            device=dev)),
+                        binning_alg_bytes(kind, N, n_isects, ntx * nty, c0["n_flag2"])),
+            "offset_encode": (lambda: _C.isect_offset_encode(ids, ntx, nty), (enc_reads + 4) * ntx * nty),
+            "rays": (lambda: cam.camera_rays(W, H), 24 * W * H),
+            "eval3d_fwd": (lambda: _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0),
+                                                           opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl),
+                           (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * c0["fwd_loaded"]),
+        }
+        if backward:
+            g_rgb, g_d, g_a = grads[0]
+            stages["eval3d_bwd"] = (lambda: _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx,
+                                                                    tsy, off, fl, alpha, last, g_rgb, g_d, g_a,
+                                                                    False),
+                                    (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * c0["bwd_loaded"] +
+                                    (11 + cdim) * 4 * N)
+            if sh is not None:
+                v_colors = c0["v_colors"]
+                stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh, None,
+                                                                             False, v_colors, None),
+                                    (36 + 24 * K) * N)
+        stages = {k: v for k, v in stages.items() if v is not None}
+        timed_stages = stages
+        if args.profile_stages:
+            keep = set(args.profile_stages.split(","))
+            timed_stages = {k: v for k, v in stages.items() if k in keep}
+        for sname, (fn, nbytes) in timed_stages.items():
+            t = event_time_ms(fn, reps, torch)
+            gbs = nbytes / (t * 1e-3) / 1e9
+            stage_rows[sname] = {"ms": round(t, 4), "alg_bytes": int(nbytes), "GB/s": round(gbs, 1),
+                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    ext_rows = {}
+    if extensions and not args.profile_stages and kind == "pinhole":
+        ext_rows = extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales, quats, opac, W, H,
+                                  reps, dev)
+
+    # ---------------------------------------------------------------- roofline of the dominant kernel
+    # algorithmic bytes and flops averaged over the cameras, as the live times are
+    cdim = info[0]["cdim"]
+    avg = lambda k: sum(c[k] for c in info) / len(info)
+    alg = {"eval3d_fwd": (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * avg("fwd_loaded")}
+    flops = {"eval3d_fwd": FLOPS_EVAL * avg("fwd_evaluated") + (FLOPS_FWD_CONTRIB + 2 * cdim) * avg("contributing")}
+    if backward:
+        alg["eval3d_bwd"] = (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * avg("bwd_loaded") + (11 + cdim) * 4 * N
+        flops["eval3d_bwd"] = FLOPS_EVAL * avg("bwd_evaluated") + (FLOPS_BWD_CONTRIB + 4 * cdim) * avg("bwd_composited")
+    dom = max(live_ms, key=live_ms.get)
+    t_dom = live_ms[dom]
+    gbs = alg[dom] / (t_dom * 1e-3) / 1e9
+    tfl = flops[dom] / (t_dom * 1e-3) / 1e12
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "launch_ms": round(t_dom, 4), "alg_bytes_per_launch": int(alg[dom]),
+                "valu": {"achieved": round(tfl, 2), "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tfl / FP32_VALU_PEAK_TFLOPS, 4), "flops_per_launch": int(flops[dom])},
+                "note": ("the compositor has no dense contraction (no MFMA) and is VALU / LDS / atomic bound: "
+                         "the HBM fraction of its algorithmic bytes is reported as defined, the VALU fraction "
+                         "against non-packed FP32 beside it")}
+    if os.path.exists(TRAFFIC_FILE) and name == "cfg2" and dom == "eval3d_bwd":
+        with open(TRAFFIC_FILE) as fh:
+            tr = json.load(fh)
+        roofline["traffic"] = int(tr["fetch_kib_per_dispatch"] * 1024 * tr["fetch_scale"] +
+                                  tr["write_kib_per_dispatch"] * 1024 * tr["write_scale"])
+        roofline["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
+    pair_stats = {k: int(avg(k)) for k in ("fwd_evaluated", "contributing") + (
+        ("bwd_evaluated", "bwd_composited") if backward else ())}
+
+    # ---------------------------------------------------------------- CPU baseline (oracle, one camera's frame)
+    cpu_row = None
+    if cpu:
+        cpu_row = cpu_baseline(sc, cam_spec, backward, np)
+    return {
+        "workload": f"{name}: {W}x{H} x{n_cams} cams, {N} Gaussians, "
+                    f"{('SH' + str(sc.sh_degree)) if sc.sh_coeffs is not None else 'CDIM ' + str(cdim)}, "
+                    f"{'fwd+bwd' if backward else 'fwd'}",
+        "n_gaussians": N, "width": W, "height": H, "n_cams": n_cams, "tile": [tsx, tsy],
+        "n_isects": int(avg("n_isects")), "visible_gaussians": int(avg("visible")),
+        "ms_per_frame": round(ms, 4), "Mpix/s": round(mpix, 2),
+        "Gaussians/s": round(N * n_cams / (ms * 1e-3), 1),
+        "stages_per_camera": stage_rows, "extensions": ext_rows,
+        "live_ms": {k: round(v, 4) for k, v in live_ms.items()}, "pairs_per_camera": pair_stats,
+        "roofline": roofline, "cpu_baseline": cpu_row, "notes": sc.notes,
+    }
+
+
+def cpu_baseline(sc, cam_spec, backward, np):
+    """The CPU oracle on one camera's frame (activations and SH colours, UT, binning, tile offsets, rays,
+    composite forward and, for the backward configurations, composite backward and SH backward), timed
+    on this host. Threads: the host's CPUs up to 16 -- a one-GPU box's share of its CPUs."""
+    from oracle import oracle as O
+    host_cpus = os.cpu_count() or 1
+    O.set_num_threads(min(host_cpus, 16))
+    threads = O.num_threads()
+    W, H = cam_spec.width, cam_spec.height
+    tsx, tsy = sc.tile_size
+    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
+    m, q, s, o = sc.means.numpy(), sc.quats.numpy(), sc.scales.numpy(), sc.opacity.numpy()
+    tc0 = time.perf_counter()
+    if sc.sh_coeffs is not None:
+        col = O.sh_fwd(sc.sh_degree, np.asarray(cam_spec.t, np.float32), m, sc.sh_coeffs.numpy())
+    else:
+        col = sc.colors.numpy()
+    f_, r_, m_, d_ = O.project_utgs(cam_spec, m, s, q, o, W, H, phm=sc.use_phm)
+    if cam_spec.kind == "pinhole":
+        _, ids_c, fl_c = O.isect_regular(m_, r_, d_, W, H, tsx, tsy)
+    else:
+        elev = cam_spec.beam_v.numpy()[::tsy] if cam_spec.kind == "lidar" else None
+        _, ids_c, fl_c = O.isect_spherical_family(cam_spec.kind, cam_spec, m, s, q, o, f_, m_, r_, d_, tsx, tsy, W, H,
+                                                  elev=elev)
+    off_c = O.offset_encode(ids_c, ntx, nty)
+    ro_c, rd_c = O.camera_rays(cam_spec, W, H)
+    rgb_c, dep_c, alp_c, last_c = O.eval3d_fwd(m, q, s, col, o, ro_c, rd_c, off_c, fl_c, tsx, tsy)
+    if backward:
+        gc = O.eval3d_bwd(m, q, s, col, o, ro_c, rd_c, off_c, fl_c, alp_c, last_c, sc.grad_rgb[0].numpy(),
+                          sc.grad_depth[0].numpy(), sc.grad_alpha[0].numpy(), tsx, tsy)
+        if sc.sh_coeffs is not None:
+            O.sh_bwd(sc.sh_degree, np.asarray(cam_spec.t, np.float32), m, sc.sh_coeffs.numpy(), gc["v_colors"])
+    cpu_s = time.perf_counter() - tc0
+    return {"value": round(W * H / cpu_s / 1e6, 4), "unit": "Mpix/s", "cores": threads, "host_cpus": host_cpus,
+            "kind": "port",
+            "sample": f"camera 0's frame of {sc.name} ({W}x{H}, {sc.n} Gaussians, {'fwd+bwd' if backward else 'fwd'}) "
+                      f"on {threads} OpenMP threads of {host_cpus} host CPUs (a one-GPU box's share is 16): "
+                      f"{cpu_s:.2f} s"}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -152,235 +418,38 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(torch)
         return
-    import xsimgs_amd  # noqa: F401  (fails loudly without the native libraries)
-    from xsimgs_amd import _C, frame, synthetic
-    from xsimgs_amd.rendering import rasterize as rz
-
-    dev = torch.device("cuda:0")
-    sc = synthetic.make(args.config, seed=args.seed)
-    cam_spec = sc.cameras[0]
-    W, H = cam_spec.width, cam_spec.height
-    st = frame.prepare(sc, dev)
-    grads = [(sc.grad_rgb[i], sc.grad_depth[i], sc.grad_alpha[i]) for i in range(len(sc.cameras))]
-    grads = [tuple(g.to(dev) for g in gg) for gg in grads]
-    n_cams = len(sc.cameras)
-
-    def step():
-        frame.zero_grads(st)
-        for ci in range(n_cams):
-            frame.render_frame(st, backward=True, grads=grads[ci], cam_index=ci)
-
-    # the compositor calls are bracketed by HIP events on the stream they run on (torch's current
-    # stream), inside the timed steps
-    live = {"eval3d_fwd": [], "eval3d_bwd": []}
-    orig = {"eval3d_fwd": rz.rasterize_eval3d_fwd, "eval3d_bwd": rz.rasterize_eval3d_bwd}
-
-    def timed(name):
-        fn = orig[name]
-
-        def call(*a, **k):
-            ev0 = torch.cuda.Event(enable_timing=True)
-            ev1 = torch.cuda.Event(enable_timing=True)
-            ev0.record()
-            out = fn(*a, **k)
-            ev1.record()
-            live[name].append((ev0, ev1))
-            return out
-        return call
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = timed("eval3d_fwd"), timed("eval3d_bwd")
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = orig["eval3d_fwd"], orig["eval3d_bwd"]
-    ms = (t1 - t0) * 1e3 / args.steps
-    live_ms = {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in live.items() if v}
-    mpix = W * H * n_cams / (ms * 1e-3) / 1e6
-
-    # ---------------------------------------------------------------- per-stage timing
-    cam = st.cams[0]
-    N = sc.n
-    K = sc.sh_coeffs.shape[1] if sc.sh_coeffs is not None else 0
-    tsx, tsy = sc.tile_size
-    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
-    with torch.no_grad():
-        means, quats = st.means.detach(), st.quats.detach()
-        scales = torch.exp(st.log_scales.detach())
-        opac = torch.sigmoid(st.opacity_logits.detach())
-        pack = cam.pack
-        origin = cam.pose.t
-        sh = st.sh.detach() if st.sh is not None else None
-        colors = (_C.spherical_harmonics_fused_fwd(sc.sh_degree, origin, means, sh, None, False)
-                  if sh is not None else st.colors.detach())
-        cdim = colors.shape[-1]
-        flags, radii, m2, dep = cam.ut_gs_projection(means, scales, quats, W, H, opacity=opac, use_phm=sc.use_phm)
-        tpg, ids, fl = cam.isect_gs_tiles(means, scales, quats, W, H, flags, radii, m2, dep, opacity=opac,
-                                          tile_size_x=tsx, tile_size_y=tsy)
-        off = _C.isect_offset_encode(ids, ntx, nty)
-        ro, rd = cam.camera_rays(W, H)
-        pairs = torch.zeros(2, dtype=torch.int64, device=dev)
-        rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0),
-                                                          opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl,
-                                                          pair_counts=pairs)
-        fwd_evaluated, contributing = (int(x) for x in pairs.cpu())
-        g_rgb, g_d, g_a = grads[0]
-        bpairs = torch.zeros(2, dtype=torch.int64, device=dev)
-        bwd_out = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, alpha,
-                                          last, g_rgb, g_d, g_a, False, pair_counts=bpairs)
-        bwd_evaluated, bwd_composited = (int(x) for x in bpairs.cpu())
-        v_colors = bwd_out[4]
-        n_isects = int(fl.numel())
-        # loaded intersections of the compositor (per tile): forward up to the batch holding the
-        # tile's last contribution plus its terminating element, backward from the tile's
-        # largest last_id down to the range start
-        starts = off.view(-1).long()
-        ends = torch.cat([starts[1:], torch.tensor([n_isects], device=dev)])
-        lt = torch.nn.functional.pad(last, (0, ntx * tsx - W, 0, nty * tsy - H)).view(nty, tsy, ntx, tsx)
-        tile_max = lt.amax(dim=(1, 3)).reshape(-1).long()
-        rng = (ends - starts).clamp(min=0)
-        bwd_loaded = int((tile_max - starts + 1).clamp(min=0).minimum(rng).sum())
-        bs = tsx * tsy
-        fwd_batches = ((tile_max - starts + 2).clamp(min=1) + bs - 1) // bs
-        fwd_loaded = int(torch.minimum(rng, fwd_batches * bs).sum())
-        # the reference's backward evaluates every pair of a pixel's list up to its last_id
-        tile_of = ((torch.arange(H, device=dev) // tsy)[:, None] * ntx + (torch.arange(W, device=dev) // tsx)[None, :])
-        bwd_listed = int((last.long() - starts[tile_of] + 1).clamp(min=0).sum())
-        vis = int((tpg > 0).sum())
-        key_bits = 32 + int(math.floor(math.log2(ntx * nty))) + 1
-
-    stages = {
-        "sh_fwd": (lambda: _C.spherical_harmonics_fused_fwd(sc.sh_degree, origin, means, sh, None, False),
-                   (24 + 12 * K) * N) if sh is not None else None,
-        "ut_projection": (lambda: cam.ut_gs_projection(means, scales, quats, W, H, opacity=opac,
-                                                        use_phm=sc.use_phm), 65 * N),
-        "binning_sort": (lambda: cam.isect_gs_tiles(means, scales, quats, W, H, flags, radii, m2, dep,
-                                                    opacity=opac, tile_size_x=tsx, tile_size_y=tsy),
-                         (20 + 8 + 24) * N + (12 + 24 * math.ceil(key_bits / 8)) * n_isects),
-        "offset_encode": (lambda: _C.isect_offset_encode(ids, ntx, nty), 8 * n_isects + 4 * ntx * nty),
-        "rays": (lambda: cam.camera_rays(W, H), 24 * W * H),
-        "eval3d_fwd": (lambda: _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0), opac.view(1, -1),
-                                                       W, H, tsx, tsy, ro, rd, off, fl),
-                       (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * fwd_loaded),
-        "eval3d_bwd": (lambda: _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off,
-                                                       fl, alpha, last, g_rgb, g_d, g_a, False),
-                       (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * bwd_loaded + (11 + cdim) * 4 * N),
-        "sh_bwd": (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh, None, False,
-                                                            v_colors, None),
-                   (36 + 24 * K) * N) if sh is not None else None,
-    }
-    stages = {k: v for k, v in stages.items() if v is not None}
-    timed_stages = stages
-    if args.profile_stages:
-        keep = set(args.profile_stages.split(","))
-        timed_stages = {k: v for k, v in stages.items() if k in keep}
-    stage_rows = {}
-    for name, (fn, nbytes) in timed_stages.items():
-        with torch.no_grad():
-            t = event_time_ms(fn, args.stage_reps, torch)
-        gbs = nbytes / (t * 1e-3) / 1e9
-        stage_rows[name] = {"ms": round(t, 4), "alg_bytes": int(nbytes), "GB/s": round(gbs, 1),
-                            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-    # ---------------------------------------------------------------- rows beyond the frame
-    # camera gradients, the distorted camera models and the upstream producers, each at the frame's
-    # size (its pixels or its Gaussians), timed alone; algorithmic bytes are what each kernel must
-    # read and write once
-    ext_rows = {}
-    if not args.profile_stages and cam_spec.kind == "pinhole":
-        ext_rows = extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales, quats, opac, W, H,
-                                  args.stage_reps, dev)
-
-    # ---------------------------------------------------------------- roofline of the dominant kernel
-    flops = {"eval3d_fwd": FLOPS_EVAL * fwd_evaluated + (FLOPS_FWD_CONTRIB + 2 * cdim) * contributing,
-             "eval3d_bwd": FLOPS_EVAL * bwd_evaluated + (FLOPS_BWD_CONTRIB + 4 * cdim) * bwd_composited}
-    dom = max(live_ms, key=live_ms.get)
-    t_dom = live_ms[dom]
-    alg = stages[dom][1]
-    gbs = alg / (t_dom * 1e-3) / 1e9
-    tfl = flops[dom] / (t_dom * 1e-3) / 1e12
-    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "launch_ms": round(t_dom, 4), "alg_bytes_per_launch": int(alg),
-                "valu": {"achieved": round(tfl, 2), "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tfl / FP32_VALU_PEAK_TFLOPS, 4), "flops_per_launch": int(flops[dom])},
-                "note": ("the compositor has no dense contraction (no MFMA) and is VALU / LDS / atomic bound: "
-                         "the HBM fraction of its algorithmic bytes is reported as defined, the VALU fraction "
-                         "against non-packed FP32 beside it")}
-    if os.path.exists(TRAFFIC_FILE) and args.config == "cfg2" and dom == "eval3d_bwd":
-        with open(TRAFFIC_FILE) as fh:
-            tr = json.load(fh)
-        roofline["traffic"] = int(tr["fetch_kib_per_dispatch"] * 1024 * tr["fetch_scale"] +
-                                  tr["write_kib_per_dispatch"] * 1024 * tr["write_scale"])
-        roofline["traffic_source"] = os.path.relpath(TRAFFIC_FILE, ROOT)
-    pair_stats = {"fwd_evaluated": fwd_evaluated, "bwd_evaluated": bwd_evaluated, "contributing": contributing,
-                  "bwd_composited": bwd_composited, "bwd_listed_up_to_last_id": bwd_listed}
-
-    # ---------------------------------------------------------------- CPU baseline (oracle, same frame)
-    cpu = None
-    if not args.no_cpu_baseline:
-        from oracle import oracle as O
-        cores = os.cpu_count() or 1
-        O.set_num_threads(min(cores, 16))
-        threads = O.num_threads()
-        sc_np = dict(means=sc.means.numpy(), quats=sc.quats.numpy(), scales=sc.scales.numpy(),
-                     opac=sc.opacity.numpy())
-        tc0 = time.perf_counter()
-        if sc.sh_coeffs is not None:
-            col = O.sh_fwd(sc.sh_degree, np.asarray(cam_spec.t, np.float32), sc_np["means"], sc.sh_coeffs.numpy())
-        else:
-            col = sc.colors.numpy()
-        f_, r_, m_, d_ = O.project_utgs(cam_spec, sc_np["means"], sc_np["scales"], sc_np["quats"], sc_np["opac"],
-                                        W, H, phm=sc.use_phm)
-        if cam_spec.kind == "pinhole":
-            _, ids_c, fl_c = O.isect_regular(m_, r_, d_, W, H, tsx, tsy)
-        else:
-            elev = cam_spec.beam_v.numpy()[::tsy] if cam_spec.kind == "lidar" else None
-            _, ids_c, fl_c = O.isect_spherical_family(cam_spec.kind, cam_spec, sc_np["means"], sc_np["scales"],
-                                                      sc_np["quats"], sc_np["opac"], f_, m_, r_, d_, tsx, tsy,
-                                                      W, H, elev=elev)
-        off_c = O.offset_encode(ids_c, ntx, nty)
-        ro_c, rd_c = O.camera_rays(cam_spec, W, H)
-        rgb_c, dep_c, alp_c, last_c = O.eval3d_fwd(sc_np["means"], sc_np["quats"], sc_np["scales"], col,
-                                                   sc_np["opac"], ro_c, rd_c, off_c, fl_c, tsx, tsy)
-        gc = O.eval3d_bwd(sc_np["means"], sc_np["quats"], sc_np["scales"], col, sc_np["opac"], ro_c, rd_c, off_c,
-                          fl_c, alp_c, last_c, sc.grad_rgb[0].numpy(), sc.grad_depth[0].numpy(),
-                          sc.grad_alpha[0].numpy(), tsx, tsy)
-        if sc.sh_coeffs is not None:
-            O.sh_bwd(sc.sh_degree, np.asarray(cam_spec.t, np.float32), sc_np["means"], sc.sh_coeffs.numpy(),
-                     gc["v_colors"])
-        tc1 = time.perf_counter()
-        cpu_s = tc1 - tc0
-        cpu = {"value": round(W * H / cpu_s / 1e6, 4), "unit": "Mpix/s", "cores": threads, "kind": "port",
-               "sample": f"one full {args.config} frame (camera 0, {W}x{H}, {N} Gaussians, fwd+bwd) "
-                         f"on {threads} OpenMP threads: {cpu_s:.2f} s"}
-
+    head = bench_config(args.config, args, args.steps, args.warmup, args.stage_reps, torch, np,
+                        cpu=not args.no_cpu_baseline, extensions=True)
+    configs = {}
+    for name in [c for c in args.configs.split(",") if c and c != args.config] if not args.profile_stages else []:
+        torch.cuda.empty_cache()
+        configs[name] = bench_config(name, args, args.config_steps, 2, max(3, args.stage_reps // 4), torch, np,
+                                     cpu=not args.no_cpu_baseline)
     out = {
         "metric": "Mpix/s fwd+bwd @1920x1080, 1M Gaussians SH3; achieved HBM GB/s per kernel",
-        "value": round(mpix, 2),
+        "value": head["Mpix/s"],
         "unit": "Mpix/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": head["ms_per_frame"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded, BASELINE.json config definitions)",
-        "config": {"workload": f"{args.config}: {W}x{H} x{n_cams} cams, {N} Gaussians, "
-                               f"SH{sc.sh_degree if sc.sh_coeffs is not None else '-'}, fwd+bwd",
-                   "n_gaussians": N, "width": W, "height": H, "n_cams": n_cams, "tile": [tsx, tsy],
-                   "n_isects": n_isects, "visible_gaussians": vis, "parallelism": "single GPU"},
-        "stages": stage_rows,
-        "extensions": ext_rows,
-        "live_ms": {k: round(v, 4) for k, v in live_ms.items()},
-        "pairs": pair_stats,
-        "roofline": roofline,
-        "cpu_baseline": cpu,
+        "config": {"workload": head["workload"], "n_gaussians": head["n_gaussians"], "width": head["width"],
+                   "height": head["height"], "n_cams": head["n_cams"], "tile": head["tile"],
+                   "n_isects": head["n_isects"], "visible_gaussians": head["visible_gaussians"],
+                   "parallelism": "single GPU"},
+        "Gaussians/s": head["Gaussians/s"],
+        "stages": head["stages_per_camera"],
+        "extensions": head["extensions"],
+        "live_ms": head["live_ms"],
+        "pairs": head["pairs_per_camera"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+        "configs": configs,
     }
     print(json.dumps(out))
 

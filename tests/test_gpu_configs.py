@@ -1,6 +1,7 @@
 """Parity at the benchmark configurations' full sizes (cfg1 - cfg4 of the benchmark definition).
 
-cfg1 / cfg2: 1M Gaussians, SH3, 1920x1080 pinhole (cfg1 forward, cfg2 forward + backward);
+cfg1 / cfg2: 1M Gaussians, SH3, 1920x1080 pinhole (cfg1 forward, cfg2 forward + backward; cfg2_frustum
+the same with every Gaussian inside the field of view: 86M intersections instead of 12M);
 cfg3: 3M Gaussians on a ring, 2048x128 spinning-lidar range image with phase modelling, 32x8 tiles,
 two colour channels (intensity, ray-drop logit); cfg4: 4M Gaussians in 2000 blobs seen by six
 1600x900 pinhole cameras (the reference's equivalent is six single-camera calls, camera.h:58-59;
@@ -42,7 +43,7 @@ from tests._util import GRAD_ATOL, GRAD_RTOL, RENDER_ATOL, frac_close, np_, repo
 
 pytestmark = pytest.mark.gpu
 
-ITEMS = [("cfg1", 0), ("cfg2", 0), ("cfg3", 0)] + [("cfg4", k) for k in range(6)]
+ITEMS = [("cfg1", 0), ("cfg2", 0), ("cfg2_frustum", 0), ("cfg3", 0)] + [("cfg4", k) for k in range(6)]
 _CACHE = {}
 
 

@@ -132,28 +132,37 @@ def _sh3(g, n):
     return torch.cat([dc, rest], dim=1)
 
 
-def make_cfg1(seed: int = 0, n: int = 1_000_000, backward: bool = False) -> Scene:
+def make_cfg1(seed: int = 0, n: int = 1_000_000, backward: bool = False, frustum: bool = False) -> Scene:
+    """``frustum``: lateral positions confined to the camera's field of view (x, y ~ U(-1, 1) times
+    the half-extent of the image at that depth) instead of U(-1.2, 1.2) * depth, so that every
+    Gaussian is in view."""
     g = torch.Generator("cpu").manual_seed(seed)
     u = torch.rand(n, 3, generator=g)
     z = torch.exp(math.log(2.0) + (math.log(80.0) - math.log(2.0)) * u[:, 2])
-    x = (2.0 * u[:, 0] - 1.0) * 1.2 * z
-    y = (2.0 * u[:, 1] - 1.0) * 1.2 * z
+    sx, sy = (960.0 / 1728.0, 540.0 / 1728.0) if frustum else (1.2, 1.2)
+    x = (2.0 * u[:, 0] - 1.0) * sx * z
+    y = (2.0 * u[:, 1] - 1.0) * sy * z
     means = torch.stack([x, y, z], dim=-1)
     log_s = -3.0 + 0.7 * torch.randn(n, 3, generator=g)
     quats = _unit_quats(g, n)
     op = 1.5 * torch.randn(n, generator=g)
     sh = _sh3(g, n)
     cam = pinhole(1920, 1080, 1728.0, 1728.0, 960.0, 540.0)
-    sc = Scene("cfg2" if backward else "cfg1", means, log_s, quats, op, sh, 3, None, [cam],
-               (16, 16), backward,
-               notes="lateral spread read literally: x, y ~ U(-1.2, 1.2) * depth")
+    sc = Scene(("cfg2" if backward else "cfg1") + ("_frustum" if frustum else ""), means, log_s, quats, op, sh, 3,
+               None, [cam], (16, 16), backward,
+               notes=("lateral spread confined to the field of view" if frustum else
+                      "lateral spread read literally: x, y ~ U(-1.2, 1.2) * depth"))
     if backward:
         sc.grad_rgb, sc.grad_depth, sc.grad_alpha = _grads(g, [cam], 3)
     return sc
 
 
-def make_cfg2(seed: int = 0, n: int = 1_000_000) -> Scene:
-    return make_cfg1(seed, n, backward=True)
+def make_cfg2(seed: int = 0, n: int = 1_000_000, frustum: bool = False) -> Scene:
+    return make_cfg1(seed, n, backward=True, frustum=frustum)
+
+
+def make_cfg2_frustum(seed: int = 0, n: int = 1_000_000) -> Scene:
+    return make_cfg1(seed, n, backward=True, frustum=True)
 
 
 def lidar_beams(n_beams: int = 128, top_deg: float = 15.0, bottom_deg: float = -25.0):
@@ -239,7 +248,7 @@ def make_cfg4(seed: int = 0, n: int = 4_000_000, n_blobs: int = 2000) -> Scene:
 
 
 MAKERS = {"cfg0": make_cfg0, "cfg1": make_cfg1, "cfg2": make_cfg2,
-          "cfg3": make_cfg3, "cfg4": make_cfg4}
+          "cfg3": make_cfg3, "cfg4": make_cfg4, "cfg2_frustum": make_cfg2_frustum}
 
 
 def make(name: str, **kw) -> Scene:
