@@ -134,83 +134,147 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
 }
 
 // isect_lidar_tiles_kernel (phm_lidar_tiling.cu:96-234) / isect_spherical_tiles_kernel
-// (phm_spherical_tiling.cu:47-174), count part. Flag-2 Gaussians are re-projected with
-// PositiveDelta once here; their second span (virtual instance 2j+1) carries the re-projected
-// depth, as the reference's second fill_tiles call does (phm_lidar_tiling.cu:224-226).
+// (phm_spherical_tiling.cu:47-174), count part: every Gaussian's first span (virtual instance 2j).
+// A seam Gaussian (flag 2) is appended to a queue instead of being re-projected here: about one
+// Gaussian in a hundred is one, so re-projecting inline would hold about half of the wavefronts for a
+// whole UT; seam_span_kernel re-projects the queue densely and adds the second spans.
 template <int KIND, bool LIDAR>
 __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
-    int64_t n, const float* __restrict__ pack, UtWeights ut, f2 img, const float* __restrict__ points,
-    const float* __restrict__ vel, const float* __restrict__ scales, const float4* __restrict__ quats,
-    const float* __restrict__ opacity, const uint8_t* __restrict__ flags, const float2* __restrict__ means2d,
-    const float2* __restrict__ radii, const float* __restrict__ depths, const float* __restrict__ elev,
-    int n_elev, float u_per_tile, float v_per_tile, int ntx, int n_v, int32_t* __restrict__ tpg,
-    Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
-    uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
+    int64_t n, const float* __restrict__ pack, f2 img, const uint8_t* __restrict__ flags,
+    const float2* __restrict__ means2d, const float2* __restrict__ radii, const float* __restrict__ depths,
+    const float* __restrict__ elev, int n_elev, float u_per_tile, float v_per_tile, int ntx, int n_v,
+    int32_t* __restrict__ tpg, Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
+    uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart, uint32_t* __restrict__ seam_cnt,
+    uint32_t* __restrict__ seam_ids) {
     __shared__ uint64_t lds[kWaves];
+    __shared__ uint32_t s_seam;
+    if (threadIdx.x == 0) s_seam = 0;
+    __syncthreads();
     const Camera cam = load_camera(pack, KIND);
-    const bool is_static = camera_is_static(cam, vel != nullptr);
+    const int lane = __lane_id();
+    const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
     const int64_t base = (int64_t)blockIdx.x * (kCountTile / 2);
     for (int k = 0; k < kCountItems / 2; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
-        if (j >= n) continue;
-        const float2 r = radii[j];
-        const int flag = flags[j];
-        Rect a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-        float dep2 = 0.f;
-        if (!(r.x <= 0 || r.y <= 0 || flag == 0)) {
-            float u_min = 0.0f, u_max = 1.0f;
-            const float u_pose = u_pose_of(cam);
-            if (flag == 2) {
-                if (cam.roll_u > 0) u_max = u_pose; else u_min = u_pose;
-            }
-            const float2 m = means2d[j];
-            const float mx = m.x / img.x, my = m.y / img.y, rx = r.x / img.x, ry = r.y / img.y;
-            if (LIDAR) a = lidar_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, elev, ntx);
-            else a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
-            if (flag == 2) {
-                f3 d[3];
-                ut_deltas(ut.sqrt_dl, quats[j], ld3(scales + 3 * j), d);
-                const float op = opacity ? opacity[j] : 1.0f;
-                const f3 pv = vel ? ld3(vel + 3 * j) : mk3(0.f, 0.f, 0.f);
-                const ProjParams pp{1e-4f, 0.002f, 1.0f};
-                f2 m2 = mk2(0.f, 0.f), r2 = mk2(0.f, 0.f);
-                float dd = 0.f, ud = 0.f;
-                if (ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, ld3(points + 3 * j), pv, op, d,
-                                        is_static, m2, r2, dd, ud)) {
-                    if (cam.roll_u > 0) {
-                        u_min = ceilf(u_pose / u_per_tile) * u_per_tile + 1e-6f;
-                        u_max = 1.0f;
-                    } else {
-                        u_min = 0.0f;
-                        u_max = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f;
-                    }
-                    const float mx2 = m2.x / img.x, my2 = m2.y / img.y, rx2 = r2.x / img.x, ry2 = r2.y / img.y;
-                    if (LIDAR) b = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev, ntx);
-                    else b = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
-                    dep2 = dd;
+        bool seam = false;
+        if (j < n) {
+            const float2 r = radii[j];
+            const int flag = flags[j];
+            Rect a = {0, 0, 0, 0};
+            if (!(r.x <= 0 || r.y <= 0 || flag == 0)) {
+                float u_min = 0.0f, u_max = 1.0f;
+                if (flag == 2) {
+                    seam = true;
+                    if (cam.roll_u > 0) u_max = u_pose_of(cam); else u_min = u_pose_of(cam);
                 }
+                const float2 m = means2d[j];
+                const float mx = m.x / img.x, my = m.y / img.y, rx = r.x / img.x, ry = r.y / img.y;
+                if (LIDAR) a = lidar_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, elev, ntx);
+                else a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
             }
+            const uint32_t ca = rect_count(a);
+            tpg[j] = (int32_t)ca;
+            rects[2 * j] = a;
+            rects[2 * j + 1] = Rect{0, 0, 0, 0};
+            vcnt[2 * j] = ca;
+            vcnt[2 * j + 1] = 0u;
+            vkey[2 * j] = __float_as_uint(depths[j]);
+            vkey[2 * j + 1] = 0u;
+            acc += pack_count(ca);
+            acc_c += ca;
+            acc_r += ca > 0 ? (uint32_t)(a.y1 - a.y0) : 0u;
         }
-        const uint32_t ca = rect_count(a), cb = rect_count(b);
-        tpg[j] = (int32_t)(ca + cb);
-        rects[2 * j] = a;
-        rects[2 * j + 1] = b;
-        vcnt[2 * j] = ca;
-        vcnt[2 * j + 1] = cb;
-        vkey[2 * j] = __float_as_uint(depths[j]);
-        vkey[2 * j + 1] = __float_as_uint(dep2);
-        acc += pack_count(ca) + pack_count(cb);
-        acc_c += (uint64_t)ca + cb;
-        acc_r += (ca > 0 ? (uint32_t)(a.y1 - a.y0) : 0u) + (cb > 0 ? (uint32_t)(b.y1 - b.y0) : 0u);
+        // the block's seam Gaussians go to its own slice of the queue (one LDS slot reservation per
+        // wavefront; their order there does not matter)
+        const uint64_t sm = __ballot(seam);
+        if (sm) {
+            const int leader = (int)__builtin_ctzll(sm);
+            uint32_t slot = 0;
+            if (lane == leader) slot = atomicAdd(&s_seam, (uint32_t)__popcll(sm));
+            slot = (uint32_t)__shfl((int)slot, leader, 64);
+            if (seam) seam_ids[base + slot + (uint32_t)__popcll(sm & lt_mask)] = (uint32_t)j;
+        }
     }
-    acc = block_reduce_sum<uint64_t>(acc, lds);
+    acc = block_reduce_sum<uint64_t>(acc, lds);  // its barriers also order the LDS reservations
     acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
     acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
     if (threadIdx.x == 0) {
         partials[blockIdx.x] = acc;
         cpart[2 * blockIdx.x] = acc_c;
         cpart[2 * blockIdx.x + 1] = acc_r;
+        seam_cnt[blockIdx.x] = s_seam;
+    }
+}
+
+// Second spans of the queued seam Gaussians (phm_lidar_tiling.cu:183-229): re-projected with
+// PositiveDelta, binned past the tile boundary after u_pose and keyed with the re-projected depth
+// (virtual instance 2j + 1). One wavefront per count block walks that block's slice of the queue;
+// it alone adds the block's second spans to the block's partials, before the compaction reads them.
+template <int KIND, bool LIDAR>
+__global__ __launch_bounds__(kBlock) void seam_span_kernel(
+    unsigned n_count_blocks, const uint32_t* __restrict__ seam_cnt, const uint32_t* __restrict__ seam_ids,
+    const float* __restrict__ pack, UtWeights ut, f2 img, const float* __restrict__ points,
+    const float* __restrict__ vel, const float* __restrict__ scales, const float4* __restrict__ quats,
+    const float* __restrict__ opacity, const float* __restrict__ elev, int n_elev, float u_per_tile,
+    float v_per_tile, int ntx, int n_v, int32_t* __restrict__ tpg, Rect* __restrict__ rects,
+    uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey, uint64_t* __restrict__ partials,
+    uint64_t* __restrict__ cpart) {
+    const unsigned blk = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (blk >= n_count_blocks) return;  // wavefront-uniform
+    const uint32_t count = seam_cnt[blk];
+    if (count == 0) return;
+    const Camera cam = load_camera(pack, KIND);
+    const bool is_static = camera_is_static(cam, vel != nullptr);
+    const int lane = __lane_id();
+    const int64_t base = (int64_t)blk * (kCountTile / 2);
+    uint32_t n_vis = 0, n_cnt = 0, n_rows = 0;
+    for (uint32_t q = lane; q < count; q += 64) {
+        const int64_t j = seam_ids[base + q];
+        f3 d[3];
+        ut_deltas(ut.sqrt_dl, quats[j], ld3(scales + 3 * j), d);
+        const float op = opacity ? opacity[j] : 1.0f;
+        const f3 pv = vel ? ld3(vel + 3 * j) : mk3(0.f, 0.f, 0.f);
+        const ProjParams pp{1e-4f, 0.002f, 1.0f};
+        f2 m2 = mk2(0.f, 0.f), r2 = mk2(0.f, 0.f);
+        float dd = 0.f, ud = 0.f;
+        if (!ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, ld3(points + 3 * j), pv, op, d, is_static,
+                                 m2, r2, dd, ud))
+            continue;
+        const float u_pose = u_pose_of(cam);
+        float u_min, u_max;
+        if (cam.roll_u > 0) {
+            u_min = ceilf(u_pose / u_per_tile) * u_per_tile + 1e-6f;
+            u_max = 1.0f;
+        } else {
+            u_min = 0.0f;
+            u_max = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f;
+        }
+        const float mx2 = m2.x / img.x, my2 = m2.y / img.y, rx2 = r2.x / img.x, ry2 = r2.y / img.y;
+        Rect b;
+        if (LIDAR) b = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev, ntx);
+        else b = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
+        const uint32_t cb = rect_count(b);
+        rects[2 * j + 1] = b;
+        vcnt[2 * j + 1] = cb;
+        vkey[2 * j + 1] = __float_as_uint(dd);
+        if (cb > 0) {
+            tpg[j] += (int32_t)cb;
+            n_vis += 1;
+            n_cnt += cb;
+            n_rows += (uint32_t)(b.y1 - b.y0);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        n_vis += (uint32_t)__shfl_xor((int)n_vis, off, 64);
+        n_cnt += (uint32_t)__shfl_xor((int)n_cnt, off, 64);
+        n_rows += (uint32_t)__shfl_xor((int)n_rows, off, 64);
+    }
+    if (lane == 0 && n_vis > 0) {
+        partials[blk] += ((uint64_t)n_vis << 32) + n_cnt;
+        cpart[2 * blk] += n_cnt;
+        cpart[2 * blk + 1] += n_rows;
     }
 }
 
@@ -852,6 +916,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // is sized for: 1024 keys per block spread them over four times as many workgroups.
 constexpr int kPresortItems = 4;
 constexpr int kRunSortItems = 4;  // the run sort (one pass over about a million runs) likewise
+constexpr unsigned kPresortGrid = 2048;
 
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
 struct CountWs {
@@ -860,6 +925,7 @@ struct CountWs {
     // depth pre-order (sorted fills only): ping-pong, histograms, device-side count, run offsets
     uint32_t* alt_key; uint32_t* alt_id; uint32_t* hist; uint32_t* dtot; uint32_t* m_dev;
     uint32_t* roff; uint32_t* rpart;
+    uint32_t* seam_cnt; uint32_t* seam_ids;  // per count block: its seam Gaussians (two spans only)
     int64_t n_virtual; unsigned nb;
     size_t bytes;
 };
@@ -888,6 +954,8 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     w.dtot = (uint32_t*)(p + off); off += align256(4 * kRadix);
     w.rpart = (uint32_t*)(p + off); off += align256(4 * ((size_t)w.nb + 1));
     w.m_dev = (uint32_t*)(p + off); off += align256(4);
+    w.seam_cnt = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb : 0);
+    w.seam_ids = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb * (kCountTile / 2) : 0);
     w.bytes = off;
     return w;
 }
@@ -1006,17 +1074,25 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         const f2 img = mk2(d->img_width, d->img_height);
         const float u_per_tile = (float)d->tile_w / d->img_width;
         const float v_per_tile = (float)d->tile_h / d->img_height;
+        const unsigned seam_grid = (w.nb + kWaves - 1) / kWaves;
         if (g.kind == XSG_TILING_LIDAR) {
             count_spherical_kernel<XSG_CAM_LIDAR, true><<<w.nb, kBlock, 0, s>>>(
-                nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
-                d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
-                d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt,
-                w.vkey, w.partials, w.cpart);
+                nt, d->camera_pack, img, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
+                d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey,
+                w.partials, w.cpart, w.seam_cnt, w.seam_ids);
+            seam_span_kernel<XSG_CAM_LIDAR, true><<<seam_grid, kBlock, 0, s>>>(
+                w.nb, w.seam_cnt, w.seam_ids, d->camera_pack, ut, img, d->points, d->velocity, d->scales,
+                (const float4*)d->quats, d->opacity, d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.ntx,
+                g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
         } else {
             count_spherical_kernel<XSG_CAM_SPHERICAL, false><<<w.nb, kBlock, 0, s>>>(
-                nt, d->camera_pack, ut, img, d->points, d->velocity, d->scales, (const float4*)d->quats,
-                d->opacity, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths, nullptr,
-                0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
+                nt, d->camera_pack, img, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
+                nullptr, 0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart,
+                w.seam_cnt, w.seam_ids);
+            seam_span_kernel<XSG_CAM_SPHERICAL, false><<<seam_grid, kBlock, 0, s>>>(
+                w.nb, w.seam_cnt, w.seam_ids, d->camera_pack, ut, img, d->points, d->velocity, d->scales,
+                (const float4*)d->quats, d->opacity, nullptr, 0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects,
+                w.vcnt, w.vkey, w.partials, w.cpart);
         }
     }
     // the totals are final after the compaction, which publishes them to pinned host memory; an event
@@ -1033,7 +1109,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         // (stable, 4 passes, result back in comp_*), then their row-run offsets
         radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems>(
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
-            PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev);
+            PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev, false, kPresortGrid);
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
         rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
     }

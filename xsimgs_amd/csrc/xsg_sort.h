@@ -237,9 +237,10 @@ constexpr unsigned kDevCountGrid = 256;
 template <typename K, typename V, typename FinalOut, int ITEMS = kSortItems>
 inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
                              uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s,
-                             const uint32_t* n_dev = nullptr, bool first_hist_ready = false) {
+                             const uint32_t* n_dev = nullptr, bool first_hist_ready = false,
+                             unsigned dev_grid = kDevCountGrid) {
     const unsigned nb = sort_blocks<ITEMS>(n);
-    const unsigned grid = n_dev ? min(nb, kDevCountGrid) : nb;
+    const unsigned grid = n_dev ? min(nb, dev_grid) : nb;
     int passes = 0;
     K* src_k = k0; V* src_v = v0; K* dst_k = k1; V* dst_v = v1;
     for (int shift = begin_bit; shift < end_bit; shift += 8) {
