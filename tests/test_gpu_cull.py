@@ -79,6 +79,10 @@ CASES = [  # tile, shared origin, dynamic, tiny ray
     ((10, 6), True, True, True),
     ((12, 16), True, False, False),   # 192 pixels: four pixels per lane, 48 lanes
     ((10, 15), False, True, False),   # 150 pixels: four pixels per lane, a ragged last lane
+    ((32, 16), False, True, False),   # 512 pixels: 512-thread forward, two backward wavefronts
+    ((32, 32), True, False, False),   # 1024 pixels: the largest tile (1024-thread forward)
+    ((30, 30), False, False, True),   # 900 pixels: ragged wavefronts in both kernels
+    ((20, 40), True, True, False),    # 800 pixels, dynamic
 ]
 
 
@@ -207,11 +211,12 @@ def test_cull_exact(dev, case):
 
 
 @pytest.mark.parametrize("dyn", [False, True])
-@pytest.mark.parametrize("tile", [(16, 16), (12, 16), (10, 15), (16, 8)])
+@pytest.mark.parametrize("tile", [(16, 16), (12, 16), (10, 15), (16, 8), (32, 16), (32, 32)])
 @pytest.mark.parametrize("seed", range(4))
 def test_cull_seeds(dev, seed, tile, dyn):
-    """The culling scenes over further seeds, at tile shapes with one, four and two pixels per lane
-    and a ragged last lane: renders to the render tolerance, gradients of both backward kernels."""
+    """The culling scenes over further seeds, at tile shapes with one, four and two pixels per lane,
+    a ragged last lane and tiles of 512 and 1024 pixels: renders to the render tolerance, gradients of
+    both backward kernels."""
     tsx, tsy = tile
     shared = seed % 2 == 0 and not dyn
     tiny = seed % 3 == 0

@@ -503,3 +503,16 @@ def test_ut_phm_seam_cases(dev, timing):
         assert int(f[0]) == int(rf[0]) == flag, name
         assert np.allclose(m2, rm, atol=2e-2) and np.allclose(r, rr, atol=2e-2, rtol=1e-4), name
         assert np.allclose(d, rd, rtol=1e-6), name
+
+
+def test_eval3d_tile_over_1024_pixels_rejected(dev):
+    """Tiles above the 1024-thread workgroup limit fail as the reference's launch setup does
+    (tile_shared_memory.h:8-26)."""
+    s = _pinhole_scene(dev, 61, n=20)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    W, H = s["W"], s["H"]
+    off = torch.zeros((2, 2), dtype=torch.int32, device=dev)
+    fl = torch.zeros(0, dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="Failed to set maximum shared memory size"):
+        _C.rasterize_eval3d_fwd(T(s["means"]), T(s["quats"]), T(s["scales"]), T(s["colors"]).unsqueeze(0),
+                                T(s["opac"]).view(1, -1), W, H, 33, 32, T(s["ro"]), T(s["rd"]), off, fl)

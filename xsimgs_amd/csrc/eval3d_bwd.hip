@@ -14,8 +14,8 @@
 //    leaves each component's total on its own lane, and one atomic instruction per 16
 //    components adds them (one lane per component);
 //  * each thread owns two pixels (four in tiles of more than 128 pixels, which a single wavefront
-//    then covers), so the staged Gaussian's LDS reads, the reduction and the atomics serve all of
-//    them;
+//    then covers up to 256 pixels; tiles of up to 1024 pixels take up to four wavefronts), so the
+//    staged Gaussian's LDS reads, the reduction and the atomics serve all of them;
 //  * divisions in the per-pair math are reciprocal-multiplies (v_rcp_f32, 1 ulp);
 //  * (wavefront, Gaussian) pairs that no pixel of the wavefront can take are skipped unevaluated
 //    (cull_keep); they would add exact zeros.
@@ -177,9 +177,9 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
 // tile, thread tr owning the pixels PX tr ... PX tr + PX - 1 of the tile in row-major order. The
 // staged Gaussian's LDS reads, the wavefront reduction and the atomic adds are shared by the
 // thread's pixels.
-template <int CDIM, bool DYN, bool RG, int PX>
-__global__ __launch_bounds__(kTileThreads / PX) void eval3d_bwd_kernel(Eval3dParams p) {
-    constexpr int NT = kTileThreads / PX;  // threads (and staged Gaussians per batch) at most
+template <int CDIM, bool DYN, bool RG, int PX, int NT>
+__global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
+    // NT: threads (and staged Gaussians per batch) at most
     constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;
     constexpr int CS = CDIM > 0 ? CDIM : 1;
     constexpr int K = CDIM + 3 + 6 + 1 + (DYN ? 3 : 0);  // colours, mean, Q, opacity, velocity
@@ -443,29 +443,44 @@ __global__ __launch_bounds__(kTileThreads / PX) void eval3d_bwd_kernel(Eval3dPar
 
 // Variants without per-pixel ray gradients exist for CDIM <= kColorLdsMax, with two or (tiles of
 // more than 128 pixels) four pixels per thread; larger CDIMs always compute them, two pixels per
-// thread (the C-ABI then needs the ray-gradient buffers).
+// thread (the C-ABI then needs the ray-gradient buffers). Tiles of more than 256 pixels (up to
+// kMaxTilePixels) take four pixels per thread in workgroups of up to 256 threads, with and without
+// ray gradients.
 template <int CDIM>
 int launch_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t s) {
     const int n_blocks = p.g.n_tiles_w * p.g.n_tiles_h * p.g.n_cams;
     const int tile_px = p.g.tile_w * p.g.tile_h;
     // whole wavefronts (the reduction uses every lane)
     const int bs2 = ((tile_px + 1) / 2 + 63) / 64 * 64;
+    const int bs4 = ((tile_px + 3) / 4 + 63) / 64 * 64;
+    constexpr int T = kTileThreads;
+    if (tile_px > T) {
+        if (ray_grads || CDIM > kColorLdsMax) {
+            if (!p.v_ray_o || !p.v_ray_d)
+                return xsg_fail(XSG_ERR_INVALID, "ray gradient buffers are required for cdim %d", CDIM);
+            if (dyn) eval3d_bwd_kernel<CDIM, true, true, 4, T><<<n_blocks, bs4, 0, s>>>(p);
+            else eval3d_bwd_kernel<CDIM, false, true, 4, T><<<n_blocks, bs4, 0, s>>>(p);
+        } else {
+            if (dyn) eval3d_bwd_kernel<CDIM, true, false, 4, T><<<n_blocks, bs4, 0, s>>>(p);
+            else eval3d_bwd_kernel<CDIM, false, false, 4, T><<<n_blocks, bs4, 0, s>>>(p);
+        }
+        return XSG_OK;
+    }
     if constexpr (CDIM <= kColorLdsMax) {
         if (!ray_grads) {
             if (tile_px > 128) {
-                const int bs4 = ((tile_px + 3) / 4 + 63) / 64 * 64;
-                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 4><<<n_blocks, bs4, 0, s>>>(p);
-                else eval3d_bwd_kernel<CDIM, false, false, 4><<<n_blocks, bs4, 0, s>>>(p);
+                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 4, T / 4><<<n_blocks, bs4, 0, s>>>(p);
+                else eval3d_bwd_kernel<CDIM, false, false, 4, T / 4><<<n_blocks, bs4, 0, s>>>(p);
             } else {
-                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 2><<<n_blocks, bs2, 0, s>>>(p);
-                else eval3d_bwd_kernel<CDIM, false, false, 2><<<n_blocks, bs2, 0, s>>>(p);
+                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
+                else eval3d_bwd_kernel<CDIM, false, false, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
             }
             return XSG_OK;
         }
     }
     if (!p.v_ray_o || !p.v_ray_d) return xsg_fail(XSG_ERR_INVALID, "ray gradient buffers are required for cdim %d", CDIM);
-    if (dyn) eval3d_bwd_kernel<CDIM, true, true, 2><<<n_blocks, bs2, 0, s>>>(p);
-    else eval3d_bwd_kernel<CDIM, false, true, 2><<<n_blocks, bs2, 0, s>>>(p);
+    if (dyn) eval3d_bwd_kernel<CDIM, true, true, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
+    else eval3d_bwd_kernel<CDIM, false, true, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
     return XSG_OK;
 }
 

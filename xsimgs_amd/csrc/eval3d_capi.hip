@@ -107,9 +107,9 @@ int fill_params(const xsg_eval3d_args* a, Eval3dParams& p, const char* who) {
     if (a->tile_w <= 0 || a->tile_h <= 0 || a->width < 0 || a->height < 0 || a->n_cams < 1 || a->n < 0 ||
         a->n_isects < 0 || a->n_tiles_w <= 0 || a->n_tiles_h <= 0)
         return xsg_fail(XSG_ERR_INVALID, "%s: invalid sizes", who);
-    if (a->tile_w * a->tile_h > kTileThreads)
+    if (a->tile_w * a->tile_h > kMaxTilePixels)
         return xsg_fail(XSG_ERR_LDS, "Failed to set maximum shared memory size (tile %dx%d has more than %d pixels), "
-                        "try lowering tile_size.", a->tile_w, a->tile_h, kTileThreads);
+                        "try lowering tile_size.", a->tile_w, a->tile_h, kMaxTilePixels);
     if ((int64_t)a->n_tiles_w * a->tile_w < a->width || (int64_t)a->n_tiles_h * a->tile_h < a->height)
         return xsg_fail(XSG_ERR_INVALID, "%s: tile grid %dx%d of %dx%d tiles does not cover %dx%d pixels", who,
                         a->n_tiles_w, a->n_tiles_h, a->tile_w, a->tile_h, a->width, a->height);

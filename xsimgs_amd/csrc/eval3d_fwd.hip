@@ -7,19 +7,23 @@
 namespace xsg {
 namespace {
 
-template <int CDIM, bool DYN>
-__global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p) {
-    constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;  // channels staged in LDS
+// NT threads per workgroup, one per pixel: 256 for tiles of up to 256 pixels, 1024 for larger ones
+// (the reference launches tile_w * tile_h threads, eval3d_fwd.cu:204-221). The 1024-thread variant
+// stages up to 8 colour channels in LDS, so that its batch of 1024 Gaussians fits.
+template <int CDIM, bool DYN, int NT>
+__global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
+    constexpr int kLdsColors = NT > kTileThreads ? 8 : kColorLdsMax;
+    constexpr int CL = (CDIM > 0 && CDIM <= kLdsColors) ? CDIM : 0;   // channels staged in LDS
     constexpr int C4 = (CL + 3) / 4;                                   // float4 slots of them
     constexpr int CS = CDIM > 0 ? CDIM : 1;
-    constexpr int NW = kTileThreads / 64;
+    constexpr int NW = NT / 64;
     // Every per-Gaussian slot is a float4 indexed by the batch position, so one address register
     // serves all reads of a pair.
-    __shared__ float4 s_m0[kTileThreads], s_m1[kTileThreads], s_m2[kTileThreads];  // M rows | gro
-    __shared__ float4 s_xo[kTileThreads];                                            // mean | opacity
-    __shared__ float4 s_vel[DYN ? kTileThreads : 1];
-    __shared__ float4 s_col[C4 > 0 ? C4 : 1][kTileThreads];
-    __shared__ int32_t s_id[CL > 0 ? 1 : kTileThreads];
+    __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | gro
+    __shared__ float4 s_xo[NT];                      // mean | opacity
+    __shared__ float4 s_vel[DYN ? NT : 1];
+    __shared__ float4 s_col[C4 > 0 ? C4 : 1][NT];
+    __shared__ int32_t s_id[CL > 0 ? 1 : NT];
     __shared__ float s_origin[3];
     __shared__ RayBundle s_bundle[NW];
     __shared__ uint64_t s_mask[NW][NW];  // [wavefront][staging wavefront]: Gaussians it evaluates
@@ -191,9 +195,15 @@ __global__ __launch_bounds__(kTileThreads) void eval3d_fwd_kernel(Eval3dParams p
 template <int CDIM>
 int launch_cdim(bool dyn, const Eval3dParams& p, hipStream_t s) {
     const int n_blocks = p.g.n_tiles_w * p.g.n_tiles_h * p.g.n_cams;
-    const int nt = (p.g.tile_w * p.g.tile_h + 63) / 64 * 64;  // whole wavefronts
-    if (dyn) eval3d_fwd_kernel<CDIM, true><<<n_blocks, nt, 0, s>>>(p);
-    else eval3d_fwd_kernel<CDIM, false><<<n_blocks, nt, 0, s>>>(p);
+    const int tile_px = p.g.tile_w * p.g.tile_h;
+    const int nt = (tile_px + 63) / 64 * 64;  // whole wavefronts
+    if (tile_px <= kTileThreads) {
+        if (dyn) eval3d_fwd_kernel<CDIM, true, kTileThreads><<<n_blocks, nt, 0, s>>>(p);
+        else eval3d_fwd_kernel<CDIM, false, kTileThreads><<<n_blocks, nt, 0, s>>>(p);
+    } else {
+        if (dyn) eval3d_fwd_kernel<CDIM, true, kMaxTilePixels><<<n_blocks, nt, 0, s>>>(p);
+        else eval3d_fwd_kernel<CDIM, false, kMaxTilePixels><<<n_blocks, nt, 0, s>>>(p);
+    }
     return XSG_OK;
 }
 

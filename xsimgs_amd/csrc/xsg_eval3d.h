@@ -1,7 +1,7 @@
 // eval3d compositing kernels (reference csrc/rasterization/eval3d_{fwd,bwd}.cu, eval3d_dynamic_*.cu).
 //
-// One workgroup per (camera, tile); one thread per pixel (tile_w * tile_h <= 256 threads, i.e. up
-// to four wave64s). Gaussians of the tile's depth-sorted list are staged in LDS in batches of one
+// One workgroup per (camera, tile); in the forward one thread per pixel (up to 1024 threads, 16
+// wave64s), in the backward two or four pixels per thread. Gaussians of the tile's depth-sorted list are staged in LDS in batches of one
 // per thread. Per staged Gaussian the LDS slot holds M = S^-1 R^T (three rows) and, when every ray
 // of the tile starts at the same origin (decided by a block vote, always true for a static pinhole
 // or spherical camera), gro = M (o - mu): the per-pair work then only maps the ray direction.
@@ -12,6 +12,7 @@
 namespace xsg {
 
 constexpr int kTileThreads = 256;
+constexpr int kMaxTilePixels = 1024;  // largest tile: the reference's 1024-thread workgroup limit
 constexpr int kColorLdsMax = 16;  // colour channels staged in LDS; larger CDIM read from HBM
 
 #define XSG_CDIM_LIST(X) \
