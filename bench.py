@@ -44,6 +44,8 @@ def parse():
                    help="comma list of further configurations reported under `configs` ('' for none)")
     p.add_argument("--config-steps", type=int, default=5)
     p.add_argument("--profile-stages", default="", help="comma list of stages to run alone (for rocprof)")
+    p.add_argument("--per-camera", action="store_true",
+                   help="render camera rigs one camera per call (the reference caller's loop) instead of batched")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 256 MiB device copy 5 times (scale of the rocprofv3 byte counters)")
     return p.parse_args()
@@ -175,9 +177,20 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
     if backward:
         grads = [tuple(g.to(dev) for g in (sc.grad_rgb[i], sc.grad_depth[i], sc.grad_alpha[i]))
                  for i in range(n_cams)]
+    # a rig of regular-tiling cameras renders batched: one binning and one compositor launch per pass
+    # over every camera (one SH evaluation when they share the origin)
+    rig = frame.rig_batchable(st) and not args.per_camera
+    rig_grads = tuple(torch.stack([g[k] for g in grads]) for k in range(3)) if (rig and backward) else None
 
     def step():
         frame.zero_grads(st)
+        if rig:
+            if backward:
+                frame.render_rig(st, backward=True, grads=rig_grads)
+            else:
+                with torch.no_grad():
+                    frame.render_rig(st)
+            return
         for ci in range(n_cams):
             if backward:
                 frame.render_frame(st, backward=True, grads=grads[ci], cam_index=ci)
@@ -188,7 +201,9 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
     # the compositor calls are bracketed by HIP events on the stream they run on (torch's current
     # stream), inside the timed steps
     live = {"eval3d_fwd": [], "eval3d_bwd": []}
-    orig = {"eval3d_fwd": rz.rasterize_eval3d_fwd, "eval3d_bwd": rz.rasterize_eval3d_bwd}
+    sym = ({"eval3d_fwd": "rasterize_eval3d_fwd_batched", "eval3d_bwd": "rasterize_eval3d_bwd_batched"} if rig else
+           {"eval3d_fwd": "rasterize_eval3d_fwd", "eval3d_bwd": "rasterize_eval3d_bwd"})
+    orig = {k: getattr(rz, v) for k, v in sym.items()}
 
     def timed(kname):
         fn = orig[kname]
@@ -206,13 +221,15 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = timed("eval3d_fwd"), timed("eval3d_bwd")
+    for k, v in sym.items():
+        setattr(rz, v, timed(k))
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    rz.rasterize_eval3d_fwd, rz.rasterize_eval3d_bwd = orig["eval3d_fwd"], orig["eval3d_bwd"]
+    for k, v in sym.items():
+        setattr(rz, v, orig[k])
     ms = (t1 - t0) * 1e3 / steps
     live_ms = {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in live.items() if v}
     mpix = W * H * n_cams / (ms * 1e-3) / 1e6
@@ -303,6 +320,43 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh, None,
                                                                              False, v_colors, None),
                                     (36 + 24 * K) * N)
+        per_frame = {"sh_fwd", "sh_bwd"}   # one call per frame: the scenes with SH have one camera or a rig
+        if rig:
+            # the batched stages over every camera of the rig; their bytes are the cameras' sum
+            tot = lambda k: sum(c[k] for c in info)
+            stk = lambda k: torch.stack([c[k] for c in info])
+            radii_b, m2_b, dep_b = (torch.stack([c["proj"][j] for c in info]) for j in (1, 2, 3))
+            ro_b, rd_b = stk("ro"), stk("rd")
+            off_b = torch.empty((n_cams, nty, ntx), dtype=torch.int32, device=dev)
+            _, _, fl_b = _C.isect_regular_tiles_batched(m2_b, radii_b, dep_b, W, H, tsx, tsy, tile_offsets=off_b)
+            col_b = colors if frame.rig_shares_origin(st) else stk("colors")
+            _, _, alpha_b, last_b = _C.rasterize_eval3d_fwd_batched(means, quats, scales, col_b, opac, W, H, tsx, tsy,
+                                                                    ro_b, rd_b, off_b, fl_b)
+            n_col = 1 if col_b.dim() == 2 else n_cams
+            stages["binning"] = (
+                lambda: _C.isect_regular_tiles_batched(m2_b, radii_b, dep_b, W, H, tsx, tsy,
+                                                       tile_offsets=torch.empty_like(off_b)),
+                sum(binning_alg_bytes(kind, N, c["n_isects"], ntx * nty, c["n_flag2"]) for c in info))
+            stages["eval3d_fwd"] = (
+                lambda: _C.rasterize_eval3d_fwd_batched(means, quats, scales, col_b, opac, W, H, tsx, tsy, ro_b,
+                                                        rd_b, off_b, fl_b),
+                n_cams * (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * tot("fwd_loaded"))
+            per_frame |= {"binning", "eval3d_fwd", "eval3d_bwd"}
+            if backward:
+                gb = rig_grads
+                stages["eval3d_bwd"] = (
+                    lambda: _C.rasterize_eval3d_bwd_batched(means, scales, quats, opac, col_b, ro_b, rd_b, tsx, tsy,
+                                                            off_b, fl_b, alpha_b, last_b, gb[0], gb[1], gb[2],
+                                                            ray_grads=False),
+                    n_cams * (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * tot("bwd_loaded") +
+                    (11 + n_col * cdim) * 4 * N)
+                if sh is not None and n_col == 1:
+                    v_col_b = _C.rasterize_eval3d_bwd_batched(means, scales, quats, opac, col_b, ro_b, rd_b, tsx, tsy,
+                                                              off_b, fl_b, alpha_b, last_b, gb[0], gb[1], gb[2],
+                                                              ray_grads=False)[4]
+                    stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh,
+                                                                                 None, False, v_col_b, None),
+                                        (36 + 24 * K) * N)
         stages = {k: v for k, v in stages.items() if v is not None}
         timed_stages = stages
         if args.profile_stages:
@@ -312,21 +366,29 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             t = event_time_ms(fn, reps, torch)
             gbs = nbytes / (t * 1e-3) / 1e9
             stage_rows[sname] = {"ms": round(t, 4), "alg_bytes": int(nbytes), "GB/s": round(gbs, 1),
-                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                                 "per": "frame" if (sname in per_frame or n_cams == 1) else "camera"}
     ext_rows = {}
     if extensions and not args.profile_stages and kind == "pinhole":
         ext_rows = extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales, quats, opac, W, H,
                                   reps, dev)
 
     # ---------------------------------------------------------------- roofline of the dominant kernel
-    # algorithmic bytes and flops averaged over the cameras, as the live times are
+    # algorithmic bytes and flops per launch: one camera's (averaged over the cameras) when each camera
+    # is one launch, every camera's sum when the rig is one batched launch
     cdim = info[0]["cdim"]
     avg = lambda k: sum(c[k] for c in info) / len(info)
-    alg = {"eval3d_fwd": (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * avg("fwd_loaded")}
-    flops = {"eval3d_fwd": FLOPS_EVAL * avg("fwd_evaluated") + (FLOPS_FWD_CONTRIB + 2 * cdim) * avg("contributing")}
+    per_launch = (lambda k: sum(c[k] for c in info)) if rig else avg
+    npix = (n_cams if rig else 1) * W * H
+    n_col = 1 if (not rig or frame.rig_shares_origin(st) or sh is None) else n_cams
+    alg = {"eval3d_fwd": (24 + 4 * cdim + 12) * npix + (48 + 4 * cdim) * per_launch("fwd_loaded")}
+    flops = {"eval3d_fwd": FLOPS_EVAL * per_launch("fwd_evaluated") +
+             (FLOPS_FWD_CONTRIB + 2 * cdim) * per_launch("contributing")}
     if backward:
-        alg["eval3d_bwd"] = (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * avg("bwd_loaded") + (11 + cdim) * 4 * N
-        flops["eval3d_bwd"] = FLOPS_EVAL * avg("bwd_evaluated") + (FLOPS_BWD_CONTRIB + 4 * cdim) * avg("bwd_composited")
+        alg["eval3d_bwd"] = ((24 + 8 + 4 * cdim + 8) * npix + (48 + 4 * cdim) * per_launch("bwd_loaded") +
+                             (11 + n_col * cdim) * 4 * N)
+        flops["eval3d_bwd"] = (FLOPS_EVAL * per_launch("bwd_evaluated") +
+                               (FLOPS_BWD_CONTRIB + 4 * cdim) * per_launch("bwd_composited"))
     dom = max(live_ms, key=live_ms.get)
     t_dom = live_ms[dom]
     gbs = alg[dom] / (t_dom * 1e-3) / 1e9
@@ -360,7 +422,9 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
         "n_isects": int(avg("n_isects")), "visible_gaussians": int(avg("visible")),
         "ms_per_frame": round(ms, 4), "Mpix/s": round(mpix, 2),
         "Gaussians/s": round(N * n_cams / (ms * 1e-3), 1),
-        "stages_per_camera": stage_rows, "extensions": ext_rows,
+        "rig": ("batched: one binning and one compositor launch per pass over all cameras, one SH evaluation "
+                "for the shared origin") if rig else None,
+        "stages": stage_rows, "extensions": ext_rows,
         "live_ms": {k: round(v, 4) for k, v in live_ms.items()}, "pairs_per_camera": pair_stats,
         "roofline": roofline, "cpu_baseline": cpu_row, "notes": sc.notes,
     }
@@ -443,7 +507,7 @@ def main():
                    "n_isects": head["n_isects"], "visible_gaussians": head["visible_gaussians"],
                    "parallelism": "single GPU"},
         "Gaussians/s": head["Gaussians/s"],
-        "stages": head["stages_per_camera"],
+        "stages": head["stages"],
         "extensions": head["extensions"],
         "live_ms": head["live_ms"],
         "pairs": head["pairs_per_camera"],

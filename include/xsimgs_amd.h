@@ -279,7 +279,7 @@ typedef struct {
     const float* means;            /* [n, 3] */
     const float* quats;            /* [n, 4] (w, x, y, z), normalised inside */
     const float* scales;           /* [n, 3] activated */
-    const float* colors;           /* [n_cams, n, cdim] or NULL */
+    const float* colors;           /* [n_cams, n, cdim] ([n, cdim] if colors_shared) or NULL */
     const float* opacities;        /* [n] activated */
     const float* velocity;         /* dynamic scenes: [n, 3], else NULL */
     const float* ray_time_delta;   /* dynamic scenes: [n_cams, H, W], else NULL */
@@ -315,6 +315,10 @@ typedef struct {
      * composited; the caller initialises them. Pairs that no pixel of a wavefront can take are
      * skipped unevaluated and not counted. */
     uint64_t* pair_counts;
+    /* 0: colors are [n_cams, n, cdim] and v_colors likewise; 1: colors [n, cdim] are shared by every
+     * camera (a rig whose cameras share one origin sees one set of view-dependent colours) and
+     * v_colors [n, cdim] receives the sum over cameras. An extension of this build. */
+    int colors_shared;
 } xsg_eval3d_args;
 
 int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream);

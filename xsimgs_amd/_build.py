@@ -23,7 +23,10 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = os.environ.get("XSG_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["capi.hip", "camera.hip", "sh.hip", "tiling.hip", "eval3d_fwd.hip", "eval3d_bwd.hip",
+# the slowest translation units first, so that the parallel build ends soonest
+HIP_SOURCES = ["eval3d_bwd_g7.hip", "eval3d_bwd_g6.hip", "eval3d_bwd_g5.hip", "eval3d_bwd_g4.hip",
+               "eval3d_bwd_g3.hip", "eval3d_bwd_g2.hip", "eval3d_bwd_g1.hip", "eval3d_bwd_g0.hip",
+               "eval3d_fwd.hip", "tiling.hip", "camera.hip", "sh.hip", "capi.hip", "eval3d_bwd.hip",
                "eval3d_capi.hip", "nodes.hip"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

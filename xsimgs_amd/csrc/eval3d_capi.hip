@@ -1,5 +1,6 @@
 // C-ABI entry points of the eval3d compositor and the per-Gaussian backward epilogue.
 #include <algorithm>
+#include <cstdint>
 
 #include "xsg_eval3d.h"
 
@@ -113,6 +114,9 @@ int fill_params(const xsg_eval3d_args* a, Eval3dParams& p, const char* who) {
     if ((int64_t)a->n_tiles_w * a->tile_w < a->width || (int64_t)a->n_tiles_h * a->tile_h < a->height)
         return xsg_fail(XSG_ERR_INVALID, "%s: tile grid %dx%d of %dx%d tiles does not cover %dx%d pixels", who,
                         a->n_tiles_w, a->n_tiles_h, a->tile_w, a->tile_h, a->width, a->height);
+    if ((int64_t)a->n_cams * a->n > INT32_MAX)
+        return xsg_fail(XSG_ERR_INVALID, "%s: %d cameras x %lld Gaussians exceed the int32 flatten ids", who,
+                        a->n_cams, (long long)a->n);
     if (a->cdim > 0 && !a->colors) return xsg_fail(XSG_ERR_INVALID, "%s: colors missing for cdim %d", who, a->cdim);
     if (!a->means || !a->quats || !a->scales || !a->opacities || !a->ray_o || !a->ray_d || !a->tile_offsets ||
         (a->n_isects > 0 && !a->flatten_ids))
@@ -123,6 +127,7 @@ int fill_params(const xsg_eval3d_args* a, Eval3dParams& p, const char* who) {
     p.means = a->means; p.quats = (const float4*)a->quats; p.scales = a->scales; p.colors = a->colors;
     p.opac = a->opacities; p.velocity = a->velocity; p.rtd = a->ray_time_delta;
     p.ray_o = a->ray_o; p.ray_d = a->ray_d; p.offsets = a->tile_offsets; p.flatten = a->flatten_ids;
+    p.col_shift = a->colors_shared ? a->n * a->cdim : 0;
     return XSG_OK;
 }
 
@@ -183,7 +188,7 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
     p.v_mt = (float*)workspace;
     p.pair_counts = (unsigned long long*)a->pair_counts;
     const int64_t n = a->n;
-    const int64_t ncol = a->cdim > 0 ? (int64_t)a->n_cams * n * a->cdim : 0;
+    const int64_t ncol = a->cdim > 0 ? (a->colors_shared ? 1 : (int64_t)a->n_cams) * n * a->cdim : 0;
     const ZeroList zl{{a->v_means, a->v_opacities, a->v_colors, p.v_mt, dyn ? a->v_velocity : nullptr},
                       {3 * n, n, ncol, 6 * n, dyn ? 3 * n : 0}};
     int64_t longest = 0;

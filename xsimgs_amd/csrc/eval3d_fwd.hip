@@ -93,7 +93,7 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                 s_vel[c.tr] = make_float4(vel.x, vel.y, vel.z, 0.f);
             }
             if constexpr (CL > 0) {
-                const float* cp = p.colors + (int64_t)fid * CDIM;
+                const float* cp = p.colors + ((int64_t)fid * CDIM - (int64_t)c.cam * p.col_shift);
 #pragma unroll
                 for (int k4 = 0; k4 < C4; ++k4) {
                     float v[4];
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                                     if (4 * k4 + j < CDIM) pix[4 * k4 + j] += cc[j] * vis;
                             }
                         } else {
-                            const float* cp = p.colors + (int64_t)s_id[t] * CDIM;
+                            const float* cp = p.colors + ((int64_t)s_id[t] * CDIM - (int64_t)c.cam * p.col_shift);
 #pragma unroll
                             for (int k = 0; k < CDIM; ++k) pix[k] += cp[k] * vis;
                         }

@@ -52,9 +52,45 @@ std::vector<int> eval3d_supported_ndims() {
     return std::vector<int>(dims, dims + n);
 }
 
+// Camera batch of a compositor call: the reference composites one camera per call; the batched ops
+// (an extension of this build) take C cameras over one scene with rays [C, H, W, 3], tile offsets
+// [C, th, tw] and flatten ids cam * N + gaussian (isect_regular_tiles_batched), and colours either
+// per camera [C, N, ch] or shared by every camera [N, ch].
+struct CamBatch {
+    int64_t n_cams = 1;
+    bool batched = false, colors_shared = false;
+};
+
+CamBatch cam_batch(bool batched, const Tensor& means, const OptT& colors, const Tensor& ray_o,
+                   const Tensor& ray_d, const Tensor& offsets, const OptT& ray_time_delta) {
+    CamBatch b;
+    if (!batched) return b;
+    b.batched = true;
+    TORCH_CHECK(ray_o.dim() == 4 && ray_o.size(3) == 3 && ray_d.sizes() == ray_o.sizes(),
+                "batched compositing takes rays [C, H, W, 3]");
+    b.n_cams = ray_o.size(0);
+    TORCH_CHECK(b.n_cams >= 1, "batched compositing needs at least one camera");
+    TORCH_CHECK(offsets.dim() == 3 && offsets.size(0) == b.n_cams, "tile_offsets must be [C, tile_height, tile_width]");
+    if (ray_time_delta.has_value())
+        TORCH_CHECK(ray_time_delta->numel() == ray_o.numel() / 3, "ray_time_delta must be [C, H, W]");
+    const int64_t n = means.numel() / 3;
+    if (colors.has_value()) {
+        const Tensor& c = *colors;
+        if (c.dim() == 2) {
+            TORCH_CHECK(c.size(0) == n, "shared colors must be [N, channels]");
+            b.colors_shared = true;
+        } else {
+            TORCH_CHECK(c.dim() == 3 && c.size(0) == b.n_cams && c.size(1) == n,
+                        "colors must be [C, N, channels] or [N, channels]");
+        }
+    }
+    return b;
+}
+
 xsg_eval3d_args base_args(const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors,
                           const Tensor& opac, int cdim, int width, int height, int tw, int th,
-                          const Tensor& ray_o, const Tensor& ray_d, const Tensor& offsets, const Tensor& flat) {
+                          const Tensor& ray_o, const Tensor& ray_d, const Tensor& offsets, const Tensor& flat,
+                          const CamBatch& cb = CamBatch{}) {
     for (const Tensor* t : {&means, &quats, &scales, &opac, &ray_o, &ray_d}) check_f32(*t, "Gaussian / ray tensors");
     TORCH_CHECK(offsets.scalar_type() == at::kInt && flat.scalar_type() == at::kInt,
                 "tile_offsets and flatten_ids must be int32");
@@ -63,7 +99,8 @@ xsg_eval3d_args base_args(const Tensor& means, const Tensor& quats, const Tensor
     xsg_eval3d_args a{};
     a.cdim = cdim;
     a.n = means.numel() / 3;
-    a.n_cams = 1;
+    a.n_cams = (int)cb.n_cams;
+    a.colors_shared = cb.colors_shared ? 1 : 0;
     a.means = fptr(means); a.quats = fptr(quats); a.scales = fptr(scales);
     a.colors = fptr(colors); a.opacities = fptr(opac);
     a.ray_o = fptr(ray_o); a.ray_d = fptr(ray_d);
@@ -90,17 +127,25 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
     const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tsw, int64_t tsh,
     const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta, const Tensor& tile_offsets,
-    const Tensor& flatten_ids, const OptT& pair_counts) {
+    const Tensor& flatten_ids, const OptT& pair_counts, bool batched = false) {
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(means.device());
     auto opt = means.options();
     const int64_t channels = colors.has_value() ? colors->size(-1) : 0;
-    Tensor renders = at::empty({image_height, image_width, channels}, opt);
-    Tensor depths = at::empty({image_height, image_width}, opt);
-    Tensor alphas = at::empty({image_height, image_width}, opt);
-    Tensor last_ids = at::empty({image_height, image_width}, opt.dtype(at::kInt));
+    const CamBatch cb = cam_batch(batched, means, colors, ray_origs, ray_dirs, tile_offsets, ray_time_delta);
+    if (batched)
+        TORCH_CHECK(ray_origs.size(1) == image_height && ray_origs.size(2) == image_width,
+                    "rays must be [C, image_height, image_width, 3]");
+    std::vector<int64_t> hw{image_height, image_width};
+    if (batched) hw.insert(hw.begin(), cb.n_cams);
+    std::vector<int64_t> hwc = hw;
+    hwc.push_back(channels);
+    Tensor renders = at::empty(hwc, opt);
+    Tensor depths = at::empty(hw, opt);
+    Tensor alphas = at::empty(hw, opt);
+    Tensor last_ids = at::empty(hw, opt.dtype(at::kInt));
     xsg_eval3d_args a = base_args(means, quats, scales, colors, opacities, (int)channels, (int)image_width,
                                   (int)image_height, (int)tsw, (int)tsh, ray_origs, ray_dirs, tile_offsets,
-                                  flatten_ids);
+                                  flatten_ids, cb);
     if (velocity.has_value()) { check_f32(*velocity, "velocity"); all_contiguous({*velocity}); }
     if (ray_time_delta.has_value()) { check_f32(*ray_time_delta, "ray_time_delta"); all_contiguous({*ray_time_delta}); }
     a.velocity = fptr(velocity);
@@ -120,6 +165,19 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_fwd(
     return eval3d_fwd_impl(means, std::nullopt, quats, scales, colors, opacities, image_width, image_height,
                            tile_size_width, tile_size_height, ray_origs, ray_dirs, std::nullopt, tile_offsets,
                            flatten_ids, pair_counts);
+}
+
+// batched cameras (extension): outputs [C, H, W, ch], [C, H, W] x2, last ids [C, H, W]
+std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_fwd_batched(
+    const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors, const Tensor& opacities,
+    int64_t image_width, int64_t image_height, int64_t tile_size_width, int64_t tile_size_height,
+    const Tensor& ray_origs, const Tensor& ray_dirs, const Tensor& tile_offsets, const Tensor& flatten_ids,
+    const OptT& velocity, const OptT& ray_time_delta, const OptT& pair_counts) {
+    TORCH_CHECK(velocity.has_value() == ray_time_delta.has_value(),
+                "dynamic compositing needs both velocity and ray_time_delta");
+    return eval3d_fwd_impl(means, velocity, quats, scales, colors, opacities, image_width, image_height,
+                           tile_size_width, tile_size_height, ray_origs, ray_dirs, ray_time_delta, tile_offsets,
+                           flatten_ids, pair_counts, true);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_fwd(
@@ -146,12 +204,18 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
                        int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
                        const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors,
                        const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
-                       const OptT& pair_counts) {
+                       const OptT& pair_counts, bool batched = false) {
     if (v_render_colors.has_value() && !v_render_colors->is_contiguous())
         throw std::runtime_error("v_render_colors must be contiguous");
     all_contiguous({v_render_depth, v_render_alpha, render_alpha, last_ids});
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(points.device());
-    const int64_t width = ray_origins.size(1), height = ray_origins.size(0);
+    const CamBatch cb = cam_batch(batched, points, colors, ray_origins, ray_directions, tile_offsets,
+                                  ray_time_delta);
+    const int64_t width = ray_origins.size(batched ? 2 : 1), height = ray_origins.size(batched ? 1 : 0);
+    const int64_t n_pix = cb.n_cams * width * height;
+    TORCH_CHECK(render_alpha.numel() == n_pix && last_ids.numel() == n_pix && v_render_depth.numel() == n_pix &&
+                    v_render_alpha.numel() == n_pix,
+                "render_alpha, last_ids and the depth / alpha gradients must hold one value per ray");
     BwdOut o;
     // every gradient buffer is zero-filled (or fully written) by xsg_eval3d_bwd itself
     o.v_points = at::empty_like(points);
@@ -161,7 +225,9 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     int cdim = 0;
     if (colors.has_value()) {
         o.v_colors = at::empty_like(*colors);
-        cdim = (int)colors->size(1);
+        cdim = (int)colors->size(-1);
+        if (v_render_colors.has_value())
+            TORCH_CHECK(v_render_colors->numel() == n_pix * cdim, "v_render_colors must be [.., H, W, channels]");
     }
     // ray gradients are skipped when the caller does not need them (only kernels with CDIM <= 16
     // have that variant; larger CDIMs always produce them)
@@ -171,7 +237,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     }
     xsg_eval3d_args a = base_args(points, quat, scale, colors, opacity, cdim, (int)width, (int)height,
                                   (int)tile_size_x, (int)tile_size_y, ray_origins, ray_directions, tile_offsets,
-                                  flatten_ids);
+                                  flatten_ids, cb);
     if (velocity.has_value()) {
         check_f32(*velocity, "velocity");
         all_contiguous({*velocity, *ray_time_delta});
@@ -210,6 +276,25 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT> rasterize_eval3d_bw
                                std::nullopt, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
                                last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts);
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d};
+}
+
+// batched cameras (extension): (v_points, v_quat, v_scale, v_opacity, v_colors, v_ray_o, v_ray_d,
+// v_velocity, v_time_delta); v_colors has the colours' shape ([N, ch] shared: summed over cameras)
+std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, OptT, OptT> rasterize_eval3d_bwd_batched(
+    const Tensor& points, const Tensor& scale, const Tensor& quat, const Tensor& opacity, const OptT& colors,
+    const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
+    const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
+    const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha,
+    const OptT& velocity, const OptT& ray_time_delta, bool ray_grads, const OptT& pair_counts) {
+    TORCH_CHECK(velocity.has_value() == ray_time_delta.has_value(),
+                "dynamic compositing needs both velocity and ray_time_delta");
+    BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
+                               ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
+                               true);
+    const bool dyn = velocity.has_value();
+    return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
+            dyn ? OptT(o.v_velocity) : std::nullopt, dyn ? OptT(o.v_time_delta) : std::nullopt};
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, Tensor> rasterize_eval3d_dynamic_bwd(
@@ -940,6 +1025,18 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("ray_directions"), py::arg("ray_time_delta"), py::arg("tile_size_x"), py::arg("tile_size_y"),
           py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("render_alpha"), py::arg("last_ids"),
           py::arg("v_render_colors"), py::arg("v_render_depth"), py::arg("v_render_alpha"),
+          py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
+    // batched cameras (extension): C cameras over one scene in one launch per pass
+    m.def("rasterize_eval3d_fwd_batched", &rasterize_eval3d_fwd_batched, py::arg("means"), py::arg("quats"),
+          py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
+          py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"), py::arg("ray_dirs"),
+          py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("velocity") = py::none(),
+          py::arg("ray_time_delta") = py::none(), py::arg("pair_counts") = py::none());
+    m.def("rasterize_eval3d_bwd_batched", &rasterize_eval3d_bwd_batched, py::arg("points"), py::arg("scale"),
+          py::arg("quat"), py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"), py::arg("ray_directions"),
+          py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
+          py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
+          py::arg("v_render_alpha"), py::arg("velocity") = py::none(), py::arg("ray_time_delta") = py::none(),
           py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
     m.def("eval3d_supported_ndims", &eval3d_supported_ndims);
 

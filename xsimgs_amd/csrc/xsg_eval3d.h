@@ -15,9 +15,18 @@ constexpr int kTileThreads = 256;
 constexpr int kMaxTilePixels = 1024;  // largest tile: the reference's 1024-thread workgroup limit
 constexpr int kColorLdsMax = 16;  // colour channels staged in LDS; larger CDIM read from HBM
 
-#define XSG_CDIM_LIST(X) \
-    X(0) X(1) X(2) X(3) X(4) X(5) X(8) X(9) X(16) X(17) X(32) X(33) X(64) X(65) X(128) X(129) \
-    X(256) X(257) X(512) X(513)
+// The backward's variants of one group are compiled in one translation unit (eval3d_bwd_g<k>.hip).
+#define XSG_CDIM_GROUP0(X) X(0) X(1) X(2) X(3) X(4) X(5)
+#define XSG_CDIM_GROUP1(X) X(8) X(9) X(16) X(17)
+#define XSG_CDIM_GROUP2(X) X(32) X(33)
+#define XSG_CDIM_GROUP3(X) X(64) X(65)
+#define XSG_CDIM_GROUP4(X) X(128) X(129)
+#define XSG_CDIM_GROUP5(X) X(256) X(257)
+#define XSG_CDIM_GROUP6(X) X(512)
+#define XSG_CDIM_GROUP7(X) X(513)
+#define XSG_CDIM_LIST(X)                                                                                \
+    XSG_CDIM_GROUP0(X) XSG_CDIM_GROUP1(X) XSG_CDIM_GROUP2(X) XSG_CDIM_GROUP3(X) XSG_CDIM_GROUP4(X) \
+    XSG_CDIM_GROUP5(X) XSG_CDIM_GROUP6(X) XSG_CDIM_GROUP7(X)
 
 struct TileGrid {
     int width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_cams;
@@ -356,10 +365,16 @@ struct Eval3dParams {
     float* v_velocity;
     float* v_time;
     float* v_mt;         // workspace [n, 6]: upper triangle of the symmetric Q = sum of v_grd (x) grd + v_gro (x) gro
+    // colours of flatten id fid in camera cam sit at fid * CDIM - cam * col_shift: 0 for per-camera
+    // colours [n_cams, n, CDIM], n * CDIM for one colour set [n, CDIM] that every camera shares
+    int64_t col_shift;
     unsigned long long* pair_counts;  // optional: += [evaluated, composited] pixel-pairs
 };
 
 int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
 int eval3d_bwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
+// per-CDIM backward launcher, instantiated for each supported CDIM by eval3d_bwd_g<k>.hip
+template <int CDIM>
+int eval3d_bwd_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t s);
 
 }  // namespace xsg

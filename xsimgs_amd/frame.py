@@ -13,7 +13,8 @@ from dataclasses import dataclass, field
 import torch
 
 from . import cameras as C
-from .rendering.rasterize import ut_gs_rasterize
+from ._C import isect_regular_tiles_batched
+from .rendering.rasterize import ut_gs_rasterize, ut_gs_rasterize_batched
 from .rendering.render import ut_gs_tiling
 from .rendering.sh import spherical_harmonics_fused
 
@@ -82,6 +83,74 @@ def render_frame(st: FrameState, backward: bool = False, grads=None, cam_index: 
     out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d,
                offsets=tiles["isect_offsets"], flatten_ids=tiles["flatten_ids"], radii=tiles["radii"],
                means2d=tiles["means2d"], depths=tiles["depth"])
+    if backward:
+        g_rgb, g_depth, g_alpha = [g.to(st.device) for g in grads]
+        torch.autograd.backward([rgb, depth, alpha], [g_rgb, g_depth, g_alpha])
+        out["grads"] = dict(means=st.means.grad, quats=st.quats.grad, log_scales=st.log_scales.grad,
+                            opacity_logits=st.opacity_logits.grad,
+                            sh=st.sh.grad if st.sh is not None else None,
+                            colors=st.colors.grad if st.colors is not None else None)
+    return out
+
+
+REGULAR_TILING = ("pinhole", "distorted", "fisheye")
+
+
+def rig_batchable(st: FrameState) -> bool:
+    """Cameras whose frame can run batched: regular tiling and one image size (the scenes here are
+    static; camera motion only enters the per-camera projections and rays)."""
+    specs = st.scene.cameras
+    return (len(specs) > 1 and all(s.kind in REGULAR_TILING for s in specs)
+            and len({(s.width, s.height) for s in specs}) == 1)
+
+
+def rig_shares_origin(st: FrameState) -> bool:
+    """Every camera at one origin: view-dependent colours are then the same for all of them."""
+    return len({tuple(float(x) for x in s.t) for s in st.scene.cameras}) == 1
+
+
+def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
+    """Every camera of a rig in one batched pass (an extension of this build; the reference's caller
+    renders one camera per call, render.py:85-187). Per camera the UT projection and the rays, as
+    in render_frame; then one batched binning (keys carry the camera above the tile bits), one
+    compositor launch per pass over all cameras' tiles and, when the cameras share their origin,
+    one SH evaluation whose colours every camera uses (its gradient sums over the cameras).
+    grads: ([C, H, W, ch], [C, H, W], [C, H, W]) image gradients."""
+    sc = st.scene
+    specs = sc.cameras
+    if not rig_batchable(st):
+        raise ValueError("render_rig takes a static rig of regular-tiling cameras of one image size")
+    W, H = specs[0].width, specs[0].height
+    scales = torch.exp(st.log_scales)
+    opac = torch.sigmoid(st.opacity_logits)
+    if st.sh is None:
+        colors = st.colors
+    elif rig_shares_origin(st):
+        colors = spherical_harmonics_fused(st.sh, st.means, st.cams[0].pose.t, sc.sh_degree)
+    else:
+        colors = torch.stack([spherical_harmonics_fused(st.sh, st.means, cam.pose.t, sc.sh_degree)
+                              for cam in st.cams])
+    tsx, tsy = sc.tile_size
+    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
+    rays, proj = [], []
+    with torch.no_grad():
+        for cam in st.cams:
+            with cam._freeze_ctx():
+                rays.append(cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True))
+                proj.append(cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac,
+                                                 use_phm=sc.use_phm))
+        ray_o = torch.stack([r[0] for r in rays])
+        ray_d = torch.stack([r[1] for r in rays])
+        radii = torch.stack([p[1] for p in proj])
+        means2d = torch.stack([p[2] for p in proj])
+        depths = torch.stack([p[3] for p in proj])
+        offsets = torch.empty((len(specs), nty, ntx), dtype=torch.int32, device=st.device)
+        _, _, flatten_ids = isect_regular_tiles_batched(means2d, radii, depths, W, H, tsx, tsy, sort=True,
+                                                        tile_offsets=offsets)
+    rgb, depth, alpha = ut_gs_rasterize_batched(st.means, st.quats, scales, opac, colors, ray_o, ray_d, offsets,
+                                                flatten_ids, tsx, tsy)
+    out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d, offsets=offsets,
+               flatten_ids=flatten_ids, radii=radii, means2d=means2d, depths=depths)
     if backward:
         g_rgb, g_depth, g_alpha = [g.to(st.device) for g in grads]
         torch.autograd.backward([rgb, depth, alpha], [g_rgb, g_depth, g_alpha])
