@@ -6,16 +6,17 @@
 // The reference sorts 64-bit keys (tile << 32 | depth bits) over bits [0, 32 + tile_n_bits) with a
 // stable radix sort whose input is in Gaussian order. This build produces the identical arrays
 // with less traffic:
-//   1. count  : one thread per Gaussian instance computes its tile rectangle(s) (the seam
-//               re-projection of lidar / spherical flag-2 Gaussians happens here, once) and
-//               writes tiles_per_gauss plus the rectangles.
+//   1. count  : one thread per Gaussian instance computes its tile rectangle(s) (the seam spans of
+//               lidar / spherical flag-2 Gaussians are re-projected densely by seam_span_kernel)
+//               and writes tiles_per_gauss plus the rectangles; count_scan_kernel turns the block
+//               partials into block offsets and publishes the totals.
 //   2. compact: one packed 64-bit scan ((count > 0) << 32 | count) gives every visible
 //               instance both its intersection offset and its rank among visible instances.
 //   3. depth  : the visible instances are sorted stably by the low 32 key bits (depth bits).
-//   4. expand : a merge-path expansion writes (key bits >= 32, instance) pairs in that order,
-//               coalesced, one output per thread.
-//   5. tile   : a stable sort on the remaining key bits (tile, camera) finishes the order and
-//               the last pass writes the 64-bit keys and flattened ids.
+//   4. runs   : every depth-ordered instance is cut into row runs (one per tile row it covers),
+//               written with their records, and sorted stably by row bucket (camera, row).
+//   5. write  : per row segment, column counts give every (tile, segment) its first output
+//               position; the writers store keys and flattened ids in (camera, tile, depth) order.
 // Stable by (high bits, low bits, Gaussian order) in both cases, so the result is bit-identical
 // to sorting the reference keys; ties keep Gaussian order as the reference's fill does.
 #include <algorithm>
@@ -278,38 +279,65 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
     }
 }
 
+// Single workgroup: the exclusive prefix of the count blocks' packed partials, in place, so that
+// each compaction block reads its first position. The packed total (visible << 32 | count, whose
+// count field may carry) and the exact 64-bit intersection and row-run totals from cpart go to
+// `publish` (mapped host memory, read by the host after an event) and the visible count to m_dev,
+// for the kernels queued ahead of that readback. Each thread scans a contiguous chunk.
+__global__ __launch_bounds__(kBlock) void count_scan_kernel(unsigned nb, uint64_t* __restrict__ partials,
+                                                            const uint64_t* __restrict__ cpart,
+                                                            uint32_t* __restrict__ m_dev,
+                                                            uint64_t* __restrict__ publish) {
+    __shared__ uint64_t lds[kWaves];
+    const unsigned per = (nb + kBlock - 1) / kBlock;
+    const unsigned b0 = min(nb, threadIdx.x * per), b1 = min(nb, b0 + per);
+    uint64_t sum = 0, exact = 0, exact2 = 0;
+    for (unsigned b = b0; b < b1; ++b) {
+        sum += partials[b];
+        exact += cpart[2 * b];
+        exact2 += cpart[2 * b + 1];
+    }
+    uint64_t tot;
+    uint64_t run = block_exclusive_scan<uint64_t>(sum, lds, tot);
+    exact = block_reduce_sum<uint64_t>(exact, lds);
+    exact2 = block_reduce_sum<uint64_t>(exact2, lds);
+    for (unsigned b = b0; b < b1; ++b) {
+        const uint64_t x = partials[b];
+        partials[b] = run;
+        run += x;
+    }
+    if (threadIdx.x == 0) {
+        if (m_dev) *m_dev = (uint32_t)(tot >> 32);
+        publish[0] = tot;
+        publish[1] = exact;
+        publish[2] = exact2;
+    }
+}
+
+// Single workgroup: exclusive prefix of n 32-bit block partials, in place (chunk per thread).
+__global__ __launch_bounds__(kBlock) void partials_scan_kernel(unsigned n, uint32_t* __restrict__ partials) {
+    __shared__ uint32_t lds[kWaves];
+    const unsigned per = (n + kBlock - 1) / kBlock;
+    const unsigned b0 = min(n, threadIdx.x * per), b1 = min(n, b0 + per);
+    uint32_t sum = 0;
+    for (unsigned b = b0; b < b1; ++b) sum += partials[b];
+    uint32_t tot;
+    uint32_t run = block_exclusive_scan<uint32_t>(sum, lds, tot);
+    for (unsigned b = b0; b < b1; ++b) {
+        const uint32_t x = partials[b];
+        partials[b] = run;
+        run += x;
+    }
+}
+
 // Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
-// Each block sums the (packed) partials of the count blocks before it, which places its instances.
-// Block 0 also sums them all: the packed total (visible << 32 | count, whose count field may carry)
-// and the exact 64-bit intersection and row-run totals from cpart go to `publish` (mapped host
-// memory, read by the host after an event) and the visible count to m_dev, for the kernels queued
-// ahead of that readback.
+// `pbase` holds each block's first packed position (count_scan_kernel).
 __global__ __launch_bounds__(kBlock) void compact_kernel(
     int64_t n_virtual, const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vkey,
-    const uint64_t* __restrict__ partials, const uint64_t* __restrict__ cpart, uint32_t* __restrict__ comp_id,
-    uint32_t* __restrict__ comp_off, uint32_t* __restrict__ comp_key, unsigned nb, uint32_t* __restrict__ m_dev,
-    uint64_t* __restrict__ publish) {
+    const uint64_t* __restrict__ pbase, uint32_t* __restrict__ comp_id, uint32_t* __restrict__ comp_off,
+    uint32_t* __restrict__ comp_key) {
     __shared__ uint64_t lds[kWaves];
-    uint64_t before = 0;
-    for (unsigned b = threadIdx.x; b < blockIdx.x; b += kBlock) before += partials[b];
-    uint64_t carry = block_reduce_sum<uint64_t>(before, lds);
-    if (blockIdx.x == 0) {  // block-uniform
-        uint64_t tot = 0, exact = 0, exact2 = 0;
-        for (unsigned b = threadIdx.x; b < nb; b += kBlock) {
-            tot += partials[b];
-            exact += cpart[2 * b];
-            exact2 += cpart[2 * b + 1];
-        }
-        tot = block_reduce_sum<uint64_t>(tot, lds);
-        exact = block_reduce_sum<uint64_t>(exact, lds);
-        exact2 = block_reduce_sum<uint64_t>(exact2, lds);
-        if (threadIdx.x == 0) {
-            if (m_dev) *m_dev = (uint32_t)(tot >> 32);
-            publish[0] = tot;
-            publish[1] = exact;
-            publish[2] = exact2;
-        }
-    }
+    uint64_t carry = pbase[blockIdx.x];
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= n_virtual) break;  // block-uniform
@@ -418,8 +446,6 @@ constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of s
 constexpr int kColGroup = 4;    // columns per wavefront step in write_runs_kernel
 constexpr int kBandCols = 8;    // columns whose runs write_runs_kernel lists together (a multiple of kColGroup)
 
-// the visible-span count from the packed grand total of the count scan, for device-sized kernels
-
 // rows covered by each depth-ordered visible instance -> exclusive run offsets (reduce / scan)
 __global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
                                                              const uint32_t* __restrict__ ids,
@@ -449,10 +475,7 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
     m = min(m, (int64_t)*m_dev);
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     if (base >= m) return;  // block-uniform
-    // the block's first offset: the row totals of the blocks before it
-    uint32_t before = 0;
-    for (unsigned b = threadIdx.x; b < blockIdx.x; b += kBlock) before += partials[b];
-    uint32_t carry = block_reduce_sum<uint32_t>(before, lds);
+    uint32_t carry = partials[blockIdx.x];  // the block's first offset (partials_scan_kernel)
     for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= m) break;
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
@@ -469,9 +492,10 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
 }
 
 // Merge-path expansion of the depth-ordered instances into row runs: run r gets its row bucket
-// and the depth-order position of its instance. A block writes one tile of the run sort
-// (kExpandPerBlock runs), so it also stores the tile's histogram of the sort's first digit (the low
-// 8 bits of the row bucket) into hist, digit-major as radix_upsweep would.
+// and its record for the writers (flatten id, depth bits, column range x0 | x1 << 16, row bucket),
+// which the row sort then carries. A block writes one tile of the run sort (kExpandPerBlock runs),
+// so it also stores the tile's histogram of the sort's first digit (the low 8 bits of the row
+// bucket) into hist, digit-major as radix_upsweep would.
 static_assert(kExpandPerBlock == kSortBlock * 4, "an expansion block is one tile of the run sort");
 __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, const uint32_t* __restrict__ roff,
                                                              const uint32_t* __restrict__ ids,
@@ -479,10 +503,13 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
                                                              const Rect* __restrict__ rects, int nty,
                                                              int64_t n_per_cam, int spans, uint32_t neg_row,
                                                              uint32_t* __restrict__ out_row,
-                                                             uint32_t* __restrict__ out_p,
+                                                             uint4* __restrict__ out_rec,
                                                              uint32_t* __restrict__ hist, unsigned nb) {
     __shared__ uint32_t s_off[kExpandPerBlock];
     __shared__ uint32_t s_row[kExpandPerBlock];  // first row bucket of the instance, or neg_row
+    __shared__ uint32_t s_fid[kExpandPerBlock];
+    __shared__ uint32_t s_key[kExpandPerBlock];
+    __shared__ uint32_t s_cols[kExpandPerBlock];
     __shared__ uint32_t s_hist[kRadix];
     __shared__ int64_t s_range[2];
     s_hist[threadIdx.x] = 0;
@@ -505,8 +532,13 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
         const uint32_t v = ids[p];
         const uint32_t inst = v / (uint32_t)spans;
         const uint32_t cid = n_per_cam > 0 ? (uint32_t)(inst / (uint64_t)n_per_cam) : 0u;
+        const uint32_t key = keys[p];
+        const Rect r = rects[v];
         s_off[e] = roff[p];
-        s_row[e] = ((int32_t)keys[p] < 0) ? neg_row : cid * (uint32_t)nty + rects[v].y0;
+        s_row[e] = ((int32_t)key < 0) ? neg_row : cid * (uint32_t)nty + r.y0;
+        s_fid[e] = inst;
+        s_key[e] = key;
+        s_cols[e] = (uint32_t)r.x0 | ((uint32_t)r.x1 << 16);
     }
     __syncthreads();
     for (int q = threadIdx.x; q < kExpandPerBlock; q += kBlock) {
@@ -520,7 +552,7 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
         const uint32_t row0 = s_row[lo];
         const uint32_t row = row0 == neg_row ? neg_row : row0 + (uint32_t)(o - (int64_t)s_off[lo]);
         out_row[o] = row;
-        out_p[o] = (uint32_t)(p_lo + lo);
+        out_rec[o] = make_uint4(s_fid[lo], s_key[lo], s_cols[lo], row);
         atomicAdd(&s_hist[row & (kRadix - 1)], 1u);
     }
     __syncthreads();
@@ -570,23 +602,6 @@ __global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __
     }
     if (threadIdx.x == 0) seg_base[n_real] = tot;
 }
-
-// Last pass of the row sort: every run lands with its record for the writers (flatten id, depth
-// bits, column range, row bucket) beside its row bucket.
-struct RunRecOut {
-    uint32_t* rows;
-    uint4* rec;
-    const uint32_t* ids;
-    const uint32_t* keys;
-    const Rect* rects;
-    int spans;
-    XSG_DEV void put(int64_t pos, uint32_t row, uint32_t p) const {
-        const uint32_t v = ids[p];
-        const Rect r = rects[v];
-        rows[pos] = row;
-        rec[pos] = make_uint4(v / (uint32_t)spans, keys[p], (uint32_t)r.x0 | ((uint32_t)r.x1 << 16), row);
-    }
-};
 
 // One workgroup per segment: how many of its runs cover each column, from a difference array in
 // LDS (+1 at x0, -1 at x1, then a prefix over the columns), stored at slot (row, column, segment).
@@ -961,8 +976,8 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
 }
 
 struct FillWs {
-    uint32_t* row_a; uint32_t* p_a; uint32_t* row_b; uint32_t* p_b;  // runs and ping-pong [n_runs]
-    uint4* rec;                                     // run records [n_runs]
+    uint32_t* row_a; uint32_t* row_b;               // run row buckets and ping-pong [n_runs]
+    uint4* rec_a; uint4* rec_b;                     // run records and ping-pong [n_runs]
     uint32_t* row_start; uint32_t* seg_base; uint32_t* seg_row;
     uint32_t* slots; uint32_t* tile_tot;
     uint32_t* hist; uint32_t* dtot;
@@ -982,10 +997,9 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     const unsigned nb_r = sort_blocks<kRunSortItems>(n_runs > 0 ? n_runs : 1);
     auto take = [&](size_t bytes) { void* q = p + off; off += align256(bytes); return q; };
     w.row_a = (uint32_t*)take(4 * n_runs);
-    w.p_a = (uint32_t*)take(4 * n_runs);
     w.row_b = (uint32_t*)take(4 * n_runs);
-    w.p_b = (uint32_t*)take(4 * n_runs);
-    w.rec = (uint4*)take(16 * n_runs);
+    w.rec_a = (uint4*)take(16 * n_runs);
+    w.rec_b = (uint4*)take(16 * n_runs);
     w.row_start = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
     w.seg_base = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
     w.seg_row = (uint32_t*)take(4 * (size_t)w.s_max);
@@ -1101,8 +1115,9 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     CountReadback* rb = nullptr;
     rc = count_readback(rb);
     if (rc) return rc;
-    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.cpart, w.comp_id,
-                                           w.comp_off, w.comp_key, w.nb, g.sort ? w.m_dev : nullptr, rb->dev);
+    count_scan_kernel<<<1, kBlock, 0, s>>>(w.nb, w.partials, w.cpart, g.sort ? w.m_dev : nullptr, rb->dev);
+    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
+                                           w.comp_key);
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
@@ -1111,6 +1126,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev, false, kPresortGrid);
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
+        partials_scan_kernel<<<1, kBlock, 0, s>>>(w.nb, w.rpart);
         rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
@@ -1187,23 +1203,24 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     const int n_real = fw.n_rows - 1;
     const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
     expand_runs_kernel<<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.rects, g.nty,
-                                                  n_per_cam, g.spans, neg_row, fw.row_a, fw.p_a, fw.hist, nb_runs);
+                                                  n_per_cam, g.spans, neg_row, fw.row_a, fw.rec_a, fw.hist, nb_runs);
     int row_bits = 1;
     while ((1u << row_bits) <= neg_row) ++row_bits;
-    // stable sort of the runs by row bucket; the last pass writes the sorted row buckets (to the
-    // buffer pair the last pass does not read) and the run records
+    // stable sort of the runs (row bucket, record) by row bucket, ping-ponging between the a and b
+    // buffers: an odd number of passes ends in b
     const bool odd = ((row_bits + 7) / 8) % 2 == 1;
     uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
-    radix_sort_passes<uint32_t, uint32_t, RunRecOut, kRunSortItems>(
-        fw.row_a, fw.p_a, fw.row_b, fw.p_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
-        RunRecOut{rows_sorted, fw.rec, cw.comp_id, cw.comp_key, cw.rects, g.spans}, s, nullptr,
+    const uint4* rec = odd ? fw.rec_b : fw.rec_a;
+    radix_sort_passes<uint32_t, uint4, PlainOut<uint32_t, uint4>, kRunSortItems>(
+        fw.row_a, fw.rec_a, fw.row_b, fw.rec_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
+        PlainOut<uint32_t, uint4>{rows_sorted, odd ? fw.rec_b : fw.rec_a}, s, nullptr,
         /*first_hist_ready=*/true);
     row_segments_kernel<<<1, kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows, row_bits <= 8 ? fw.dtot : nullptr,
                                              fw.row_start, fw.seg_base, fw.seg_row);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals
     seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
-        n_real, fw.rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
+        n_real, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
     const int64_t n_tile_slots = (int64_t)n_real * g.ntx;
     tile_prefix_kernel<<<xsg_blocks(n_tile_slots * 64, kBlock), kBlock, 0, s>>>(fw.slots, fw.seg_base, n_real,
                                                                                g.ntx, fw.tile_tot);
@@ -1211,7 +1228,7 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     // offsets of the sorted keys (negative-depth runs follow every tile)
     tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots, tile_offsets);
     // the writers (one extra workgroup for the negative-depth runs)
-    write_runs_kernel<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, fw.rec, fw.row_start, fw.seg_base,
+    write_runs_kernel<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, rec, fw.row_start, fw.seg_base,
                                                                 fw.seg_row, fw.slots, fw.tile_tot, fw.s_max, n_runs,
                                                                 g.ntx, g.nty, g.tnb, n_isects, isect_ids,
                                                                 flatten_ids);

@@ -178,8 +178,8 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
         for (int r = 0; r < kSteps; ++r) {
             const int li = seg0 + r * 64 + lane;
             const bool valid = li < n_tile;
-            key[r] = 0;
-            val[r] = 0;
+            key[r] = K{};
+            val[r] = V{};
             uint32_t d = 0;
             if (valid) {
                 key[r] = keys_in[tile0 + li];
