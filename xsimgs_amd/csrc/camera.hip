@@ -8,31 +8,115 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// One sigma point of a static pinhole camera (static_camera_projection in central mode) from its
+// camera-space point: perspective divide as one reciprocal (1 ulp), the on-screen test, the
+// fixed-point pixel-time steps, and the pixel position. The steps are those of the loop
+// residual = (pose_time + p) - real_time, p -= residual, at most five, ending below thr: the first
+// residual is pose_time - real_time (p starts at 0), and a static pose usually ends there (no
+// rolling shutter) or after the second; later steps run only for the lanes that need them.
+XSG_DEV bool static_pinhole_point(const Camera& c, const ProjParams& pp, f2 img, f3 pc, f2& px) {
+    const float iz = __builtin_amdgcn_rcpf(pc.z);
+    const float u = pc.x * c.i0 * iz + c.i2;
+    const float v = pc.y * c.i1 * iz + c.i3;
+    px = mk2(u * img.x, v * img.y);
+    const bool on_screen = !((pc.z <= 0.0f) || (u < -pp.margin) || (u > 1.0f + pp.margin) || (v < -pp.margin) ||
+                             (v > 1.0f + pp.margin));
+    const float real_time = pixel_time(c, u, v);
+    float residual = c.pose_time - real_time;
+    if (!(fabsf(residual) < pp.thr)) {
+        float p_time = -residual;
+        residual = (c.pose_time + p_time) - real_time;
+        for (int i = 2; i < 5 && !(fabsf(residual) < pp.thr); ++i) {
+            p_time -= residual;
+            residual = (c.pose_time + p_time) - real_time;
+        }
+    }
+    return on_screen && fabsf(residual) < pp.max_res;
+}
+
+// ut_projection (central mode) for a static pinhole camera: the seven camera-space points are
+// M (pw - t0) +- M d_i with M the pose's rotation, each projected by static_pinhole_point; the
+// mean, covariance, radii and on-screen test as in ut_projection. Outputs as ut_projection's.
+XSG_DEV bool ut_projection_static_pinhole(const Camera& c, const Mat3& m, const UtWeights& ut, f2 img,
+                                          const ProjParams& pp, f3 pw, float opac, const f3 d[3], f2& mean2d,
+                                          f2& radii, float& depth) {
+    const f3 pc0 = mul(m, pw - c.t0);
+    f2 pts[7];
+    bool result = static_pinhole_point(c, pp, img, pc0, pts[0]);
+    f2 cov_xx_xy = mk2(0.f, 0.f);
+    float cov_yy = 0.f;
+    if (result) {
+        mean2d = mk2(ut.wm0 * pts[0].x, ut.wm0 * pts[0].y);
+        depth = pc0.z;
+        bool valid = true;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const f3 e = mul(m, d[k]);
+            valid = static_pinhole_point(c, pp, img, pc0 + e, pts[1 + 2 * k]) && valid;
+            valid = static_pinhole_point(c, pp, img, pc0 - e, pts[2 + 2 * k]) && valid;
+        }
+#pragma unroll
+        for (int i = 1; i < 7; ++i) {
+            mean2d.x += ut.wi * pts[i].x;
+            mean2d.y += ut.wi * pts[i].y;
+        }
+        if (!valid) {
+            result = false;
+        } else {
+            float vx = pts[0].x - mean2d.x, vy = pts[0].y - mean2d.y;
+            float cx = ut.wc0 * (vx * vx), cxy = ut.wc0 * (vx * vy), cy = ut.wc0 * (vy * vy);
+#pragma unroll
+            for (int i = 1; i < 7; ++i) {
+                vx = pts[i].x - mean2d.x; vy = pts[i].y - mean2d.y;
+                cx += ut.wi * (vx * vx); cxy += ut.wi * (vx * vy); cy += ut.wi * (vy * vy);
+            }
+            const float det = cx * cy - cxy * cxy;
+            if (det <= 0.0f || cx < 0 || cy < 0) result = false;
+            cov_xx_xy = mk2(cx, cxy);
+            cov_yy = cy;
+        }
+    }
+    if (!result) return false;  // the caller keeps nothing of a failed projection
+    const float extend = fminf(3.33f, sqrtf(2.0f * logf(opac / (1.0f / 255.0f))));
+    radii = mk2(extend * sqrtf(fmaxf(0.0f, cov_xx_xy.x)), extend * sqrtf(fmaxf(0.0f, cov_yy)));
+    const bool ix = !(((mean2d.x + radii.x) < 0) || (img.x < (mean2d.x - radii.x)));
+    const bool iy = !(((mean2d.y + radii.y) < 0) || (img.y < (mean2d.y - radii.y)));
+    return ix && iy;
+}
+
 // unscented_transform_kernel (include/cameras/ut_kernels.h:187-246). Every output element is
 // written (zeros for culled Gaussians), which replaces the reference's zero-initialised
-// allocations (ut_kernels.h:276-280) with a single pass.
+// allocations (ut_kernels.h:276-280) with a single pass. A static pinhole camera takes the lean
+// path above. One thread per Gaussian (two per thread, sharing the camera set-up, measured slower:
+// half as many wavefronts hide less latency; compacting the Gaussians that pass the centre test
+// before the sigma points, too).
 template <int KIND>
-__global__ __launch_bounds__(kBlock) void ut_project_kernel(
-    int64_t n, const float* __restrict__ pack, ProjParams pp, UtWeights ut, f2 img,
-    const float* __restrict__ means, const float* __restrict__ vel, const float* __restrict__ scales,
-    const float4* __restrict__ quats, const float* __restrict__ opacity, uint8_t* __restrict__ flags,
-    float2* __restrict__ radii, float2* __restrict__ means2d, float* __restrict__ depths) {
-    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
-    const Camera cam = load_camera(pack, KIND);
-    const bool is_static = camera_is_static(cam, vel != nullptr);
+XSG_DEV void ut_project_one(int64_t i, const Camera& cam, bool is_static, const Mat3& m, const ProjParams& pp,
+                            const UtWeights& ut, f2 img, const float* __restrict__ means,
+                            const float* __restrict__ vel, const float* __restrict__ scales,
+                            const float4* __restrict__ quats, const float* __restrict__ opacity,
+                            uint8_t* __restrict__ flags, float2* __restrict__ radii, float2* __restrict__ means2d,
+                            float* __restrict__ depths) {
     const float op = opacity ? opacity[i] : 1.0f;
     uint8_t flag = 0;
     f2 m2 = mk2(0.f, 0.f), r2 = mk2(0.f, 0.f);
     float depth = 0.f;
     if (op >= 1.0f / 255.0f) {
         f3 d[3];
-        ut_deltas(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
-        const f3 pv = vel ? ld3(vel + 3 * i) : mk3(0.f, 0.f, 0.f);
-        float udist = 0.f, dep = 0.f;
+        float dep = 0.f;
         f2 mm = mk2(0.f, 0.f), rr = mk2(0.f, 0.f);
-        if (ut_projection<KIND>(cam, XSG_MODE_CENTRAL, ut, img, pp, ld3(means + 3 * i), pv, op, d,
-                                is_static, mm, rr, dep, udist)) {
+        bool ok;
+        if (KIND == XSG_CAM_PINHOLE && is_static) {
+            ut_deltas_rsq(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
+            ok = ut_projection_static_pinhole(cam, m, ut, img, pp, ld3(means + 3 * i), op, d, mm, rr, dep);
+        } else {
+            ut_deltas(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
+            const f3 pv = vel ? ld3(vel + 3 * i) : mk3(0.f, 0.f, 0.f);
+            float udist = 0.f;
+            ok = ut_projection<KIND>(cam, XSG_MODE_CENTRAL, ut, img, pp, ld3(means + 3 * i), pv, op, d, is_static,
+                                     mm, rr, dep, udist);
+        }
+        if (ok) {
             flag = 1; m2 = mm; r2 = rr; depth = dep;
         }
     }
@@ -40,6 +124,21 @@ __global__ __launch_bounds__(kBlock) void ut_project_kernel(
     radii[i] = make_float2(r2.x, r2.y);
     means2d[i] = make_float2(m2.x, m2.y);
     depths[i] = depth;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kBlock) void ut_project_kernel(
+    int64_t n, const float* __restrict__ pack, ProjParams pp, UtWeights ut, f2 img,
+    const float* __restrict__ means, const float* __restrict__ vel, const float* __restrict__ scales,
+    const float4* __restrict__ quats, const float* __restrict__ opacity, uint8_t* __restrict__ flags,
+    float2* __restrict__ radii, float2* __restrict__ means2d, float* __restrict__ depths) {
+    const Camera cam = load_camera(pack, KIND);
+    const bool is_static = camera_is_static(cam, vel != nullptr);
+    const Mat3 m = static_world_to_camera(cam);
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n) return;
+    ut_project_one<KIND>(i, cam, is_static, m, pp, ut, img, means, vel, scales, quats, opacity, flags, radii, means2d,
+                         depths);
 }
 
 // unscented_transform_phm_kernel (include/cameras/ut_phm_kernels.h:13-114)
@@ -215,15 +314,16 @@ XSG_DEV bool ray_valid(const Camera& c, f2 uv) {
 
 // launch_camera_ray_fwd (include/cameras/ray_kernels.h:7-59) with Camera::camera_ray
 // (camera.h:101-131): pose at the pixel's time delta, q = exp(w dt) * q0, t = t0 + v dt.
+// Each thread covers kRayRows rows of one column. A static pinhole camera (no v, no w) maps every
+// pixel by the one rotation M of q0 (quat_apply as a matrix, exact for any quaternion); its
+// camera-space ray is ((u - cx) / fx, (v - cy) / fy, 1), where x is fixed per thread and y per row.
+constexpr int kRayRows = 4;
+
 template <int KIND>
-__global__ __launch_bounds__(kBlock) void camera_rays_kernel(
-    const float* __restrict__ pack, int width, int height, int world_space, int normalized,
-    float* __restrict__ ray_o, float* __restrict__ ray_d, uint8_t* __restrict__ valid) {
-    const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
-    const int py = (int)blockIdx.y * kStripRows + (int)(threadIdx.x >> 6);
-    if (px >= width || py >= height) return;
+XSG_DEV void camera_ray_pixel(const Camera& c, int px, int py, int width, int height, int world_space,
+                              int normalized, float* __restrict__ ray_o, float* __restrict__ ray_d,
+                              uint8_t* __restrict__ valid) {
     const int64_t idx = (int64_t)py * width + px;
-    const Camera c = load_camera(pack, KIND);
     const f2 uv = pixel_uv<KIND>(c, px, py, width, height);
     f3 ray = pixel_to_camera_ray<KIND>(c, uv);
     if (normalized) ray = ray * (1.0f / sqrtf(dot(ray, ray)));
@@ -240,6 +340,42 @@ __global__ __launch_bounds__(kBlock) void camera_rays_kernel(
     if (ray_o) st3(ray_o + 3 * idx, o);
     st3(ray_d + 3 * idx, ray);
     if (valid) valid[idx] = ray_valid<KIND>(c, uv) ? 1 : 0;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kBlock) void camera_rays_kernel(
+    const float* __restrict__ pack, int width, int height, int world_space, int normalized,
+    float* __restrict__ ray_o, float* __restrict__ ray_d, uint8_t* __restrict__ valid) {
+    const int px = (int)blockIdx.x * kStrip + (int)(threadIdx.x & 63);
+    const int py0 = ((int)blockIdx.y * kStripRows + (int)(threadIdx.x >> 6)) * kRayRows;
+    if (px >= width || py0 >= height) return;
+    const int py1 = min(height, py0 + kRayRows);
+    const Camera c = load_camera(pack, KIND);
+    if (KIND == XSG_CAM_PINHOLE && camera_is_static(c, false)) {
+        Mat3 m;
+        m.r0 = mk3(1.f, 0.f, 0.f); m.r1 = mk3(0.f, 1.f, 0.f); m.r2 = mk3(0.f, 0.f, 1.f);
+        if (world_space) {
+            const float w = c.qw, x = c.qv.x, y = c.qv.y, z = c.qv.z;
+            m.r0 = mk3(1.f - 2.f * (y * y + z * z), 2.f * (x * y - w * z), 2.f * (x * z + w * y));
+            m.r1 = mk3(2.f * (x * y + w * z), 1.f - 2.f * (x * x + z * z), 2.f * (y * z - w * x));
+            m.r2 = mk3(2.f * (x * z - w * y), 2.f * (y * z + w * x), 1.f - 2.f * (x * x + y * y));
+        }
+        const f3 o = world_space ? c.t0 : mk3(0.f, 0.f, 0.f);
+        const float rx = ((static_cast<float>(px) + 0.5f) / static_cast<float>(width) - c.i2) / c.i0;
+        for (int py = py0; py < py1; ++py) {
+            const int64_t idx = (int64_t)py * width + px;
+            const float ry = ((static_cast<float>(py) + 0.5f) / static_cast<float>(height) - c.i3) / c.i1;
+            f3 ray = mk3(rx, ry, 1.0f);
+            if (normalized) ray = ray * __builtin_amdgcn_rsqf(rx * rx + ry * ry + 1.0f);
+            ray = mul(m, ray);
+            if (ray_o) st3(ray_o + 3 * idx, o);
+            st3(ray_d + 3 * idx, ray);
+            if (valid) valid[idx] = 1;
+        }
+        return;
+    }
+    for (int py = py0; py < py1; ++py)
+        camera_ray_pixel<KIND>(c, px, py, width, height, world_space, normalized, ray_o, ray_d, valid);
 }
 
 // uv_in given: one thread per uv (1D grid); else one thread per pixel (image grid)
@@ -603,7 +739,7 @@ extern "C" int xsg_camera_rays(int kind, const float* pack, int width, int heigh
     if (xsg_camera_pack_elements(kind) <= 0) return XSG_ERR_INVALID;
     const int64_t n = (int64_t)width * height;
     if (n == 0) return XSG_OK;
-    const dim3 grid = image_grid(width, height), block(kBlock);
+    const dim3 grid = image_grid(width, height, kRayRows), block(kBlock);
     const hipStream_t s = (hipStream_t)stream;
     const int rc = xsg_with_camera_kind(kind, [&](auto k) {
         camera_rays_kernel<decltype(k)::value><<<grid, block, 0, s>>>(pack, width, height, world_space, normalized,

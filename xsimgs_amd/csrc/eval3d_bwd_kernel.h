@@ -89,6 +89,7 @@ XSG_DEV BwdEval bwd_eval(const BwdGauss& gs, const f3 ro, const f3 rd, float rt,
     e.araw = gs.op * e.vis;
     e.alpha = fminf(kMaxAlpha, e.araw);
     e.valid = in_range && e.alpha >= 1.f / 255.f;
+    e.alpha = e.valid ? e.alpha : 0.0f;  // an invalid pair then leaves T (1 / (1 - 0) is exact) and fac at 0
     return e;
 }
 
@@ -100,8 +101,9 @@ XSG_DEV void put(float& a, float v) {
 }
 
 // Gradient contribution of one pair into acc (eval3d_bwd.cu:206-271). A pair that is not valid
-// adds exact zeros (its fac and gated upstream gradients are selected to 0, and every gradient is
-// linear in them) and leaves the pixel's transmittance and buffer unchanged.
+// adds exact zeros (its alpha is 0, so fac = 0 and T / (1 - 0) = T; its gated upstream gradients
+// are selected to 0, and every gradient is linear in them) and leaves the pixel's transmittance
+// and buffer unchanged.
 //
 // The reference's dL/dalpha sums, per channel, rgb T - buffer / (1 - alpha) and the depth and
 // alpha terms; here one running buffer carries all of them, so dL/dalpha = T u - buf / (1 - alpha)
@@ -128,9 +130,9 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     const float hit_t = -od * e.inv_dd;
     // 1 / max(1e-6, 1 - alpha) (eval3d_bwd.cu:221): alpha <= kMaxAlpha, so the max never applies
     const float ra = __builtin_amdgcn_rcpf(1.0f - e.alpha);
-    px.T = e.valid ? px.T * ra : px.T;
+    px.T = px.T * ra;
     const float T = px.T;
-    const float fac = e.valid ? e.alpha * T : 0.0f;
+    const float fac = e.alpha * T;
     float rv = 0.0f;
 #pragma unroll
     for (int k = 0; k < CDIM; ++k) {
@@ -143,7 +145,9 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     const bool geo = e.valid && e.araw <= kMaxAlpha;
     const float v_alpha_g = geo ? v_alpha : 0.0f;
     const float k1 = geo ? px.v_d * fac * e.inv_dd : 0.0f;
-    // A w = -op vis dL/dalpha p with p = w / |grd|^2 (the offset of the Gaussian from the ray)
+    // A w = -op vis dL/dalpha p with p = w / |grd|^2 (the offset of the Gaussian from the ray).
+    // p = gro + hit_t grd in exact arithmetic; from the cross product its float32 error is smaller
+    // (the direct sum moved per-pixel ray gradients of the golden fixtures beyond tolerance).
     const float Ap = -e.araw * v_alpha_g;
     const f3 pp = cross(e.c, e.grd) * e.inv_dd;
     const f3 kg = k1 * e.grd;

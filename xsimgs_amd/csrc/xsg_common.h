@@ -402,6 +402,16 @@ XSG_DEV void ut_deltas(float sqrt_dl, float4 q, f3 s, f3 d[3]) {
     d[2] = mk3(2.f * (x * z + w * y), 2.f * (y * z - w * x), 1.f - 2.f * (x * x + y * y)) * (s.z * sqrt_dl);
 }
 
+// ut_deltas with the quaternion's inverse norm as one reciprocal square root (1 ulp)
+XSG_DEV void ut_deltas_rsq(float sqrt_dl, float4 q, f3 s, f3 d[3]) {
+    float w = q.x, x = q.y, y = q.z, z = q.w;
+    const float inv = __builtin_amdgcn_rsqf(w * w + x * x + y * y + z * z);
+    w *= inv; x *= inv; y *= inv; z *= inv;
+    d[0] = mk3(1.f - 2.f * (y * y + z * z), 2.f * (x * y + w * z), 2.f * (x * z - w * y)) * (s.x * sqrt_dl);
+    d[1] = mk3(2.f * (x * y - w * z), 1.f - 2.f * (x * x + z * z), 2.f * (y * z + w * x)) * (s.y * sqrt_dl);
+    d[2] = mk3(2.f * (x * z + w * y), 2.f * (y * z - w * x), 1.f - 2.f * (x * x + y * y)) * (s.z * sqrt_dl);
+}
+
 struct UtWeights { float wm0, wc0, wi, sqrt_dl; };
 
 // unscented_transform (ut_kernels.h:52-137) + the radii / on-screen test of
