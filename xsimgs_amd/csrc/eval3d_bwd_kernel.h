@@ -186,7 +186,7 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
 // tile, thread tr owning the pixels PX tr ... PX tr + PX - 1 of the tile in row-major order. The
 // staged Gaussian's LDS reads, the wavefront reduction and the atomic adds are shared by the
 // thread's pixels.
-template <int CDIM, bool DYN, bool RG, int PX, int NT>
+template <int CDIM, bool DYN, bool RG, int PX, int NT, bool COUNT>
 __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
     // NT: threads (and staged Gaussians per batch) at most
     constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
         }
     }
     __syncthreads();
-    const bool counting = p.pair_counts != nullptr;
+    constexpr bool counting = COUNT;  // the pair counters (a variant of its own: their scalar work per pair)
     uint64_t n_eval = 0, n_contrib = 0;  // evaluated / composited pixel-pairs of the wave, when counting
     const int32_t eff_end = min(range_end - 1, s_max);
     const int32_t n_eff = eff_end - range_start + 1;
@@ -456,6 +456,13 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
 // thread (the C-ABI then needs the ray-gradient buffers). Tiles of more than 256 pixels (up to
 // kMaxTilePixels) take four pixels per thread in workgroups of up to 256 threads, with and without
 // ray gradients.
+// one launch, with or without the pair counters
+template <int CDIM, bool DYN, bool RG, int PX, int NT>
+void launch_bwd(int n_blocks, int threads, const Eval3dParams& p, hipStream_t s) {
+    if (p.pair_counts) eval3d_bwd_kernel<CDIM, DYN, RG, PX, NT, true><<<n_blocks, threads, 0, s>>>(p);
+    else eval3d_bwd_kernel<CDIM, DYN, RG, PX, NT, false><<<n_blocks, threads, 0, s>>>(p);
+}
+
 }  // namespace
 
 template <int CDIM>
@@ -470,29 +477,29 @@ int eval3d_bwd_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t
         if (ray_grads || CDIM > kColorLdsMax) {
             if (!p.v_ray_o || !p.v_ray_d)
                 return xsg_fail(XSG_ERR_INVALID, "ray gradient buffers are required for cdim %d", CDIM);
-            if (dyn) eval3d_bwd_kernel<CDIM, true, true, 4, T><<<n_blocks, bs4, 0, s>>>(p);
-            else eval3d_bwd_kernel<CDIM, false, true, 4, T><<<n_blocks, bs4, 0, s>>>(p);
+            if (dyn) launch_bwd<CDIM, true, true, 4, T>(n_blocks, bs4, p, s);
+            else launch_bwd<CDIM, false, true, 4, T>(n_blocks, bs4, p, s);
         } else {
-            if (dyn) eval3d_bwd_kernel<CDIM, true, false, 4, T><<<n_blocks, bs4, 0, s>>>(p);
-            else eval3d_bwd_kernel<CDIM, false, false, 4, T><<<n_blocks, bs4, 0, s>>>(p);
+            if (dyn) launch_bwd<CDIM, true, false, 4, T>(n_blocks, bs4, p, s);
+            else launch_bwd<CDIM, false, false, 4, T>(n_blocks, bs4, p, s);
         }
         return XSG_OK;
     }
     if constexpr (CDIM <= kColorLdsMax) {
         if (!ray_grads) {
             if (tile_px > 128) {
-                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 4, T / 4><<<n_blocks, bs4, 0, s>>>(p);
-                else eval3d_bwd_kernel<CDIM, false, false, 4, T / 4><<<n_blocks, bs4, 0, s>>>(p);
+                if (dyn) launch_bwd<CDIM, true, false, 4, T / 4>(n_blocks, bs4, p, s);
+                else launch_bwd<CDIM, false, false, 4, T / 4>(n_blocks, bs4, p, s);
             } else {
-                if (dyn) eval3d_bwd_kernel<CDIM, true, false, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
-                else eval3d_bwd_kernel<CDIM, false, false, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
+                if (dyn) launch_bwd<CDIM, true, false, 2, T / 2>(n_blocks, bs2, p, s);
+                else launch_bwd<CDIM, false, false, 2, T / 2>(n_blocks, bs2, p, s);
             }
             return XSG_OK;
         }
     }
     if (!p.v_ray_o || !p.v_ray_d) return xsg_fail(XSG_ERR_INVALID, "ray gradient buffers are required for cdim %d", CDIM);
-    if (dyn) eval3d_bwd_kernel<CDIM, true, true, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
-    else eval3d_bwd_kernel<CDIM, false, true, 2, T / 2><<<n_blocks, bs2, 0, s>>>(p);
+    if (dyn) launch_bwd<CDIM, true, true, 2, T / 2>(n_blocks, bs2, p, s);
+    else launch_bwd<CDIM, false, true, 2, T / 2>(n_blocks, bs2, p, s);
     return XSG_OK;
 }
 

@@ -10,7 +10,7 @@ namespace {
 // NT threads per workgroup, one per pixel: 256 for tiles of up to 256 pixels, 1024 for larger ones
 // (the reference launches tile_w * tile_h threads, eval3d_fwd.cu:204-221). The 1024-thread variant
 // stages up to 8 colour channels in LDS, so that its batch of 1024 Gaussians fits.
-template <int CDIM, bool DYN, int NT>
+template <int CDIM, bool DYN, int NT, bool COUNT>
 __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
     constexpr int kLdsColors = NT > kTileThreads ? 8 : kColorLdsMax;
     constexpr int CL = (CDIM > 0 && CDIM <= kLdsColors) ? CDIM : 0;   // channels staged in LDS
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                                     __float_as_uint(ro.y) == __float_as_uint(o0.y) &&
                                     __float_as_uint(ro.z) == __float_as_uint(o0.z));
     const bool fixed = !DYN && __syncthreads_and(same);
-    const bool counting = p.pair_counts != nullptr;
+    constexpr bool counting = COUNT;  // the pair counters (a variant of its own: their scalar work per pair)
 
     float depth = 0.0f, T = 1.0f;
     uint32_t cur_idx = 0;
@@ -197,13 +197,18 @@ int launch_cdim(bool dyn, const Eval3dParams& p, hipStream_t s) {
     const int n_blocks = p.g.n_tiles_w * p.g.n_tiles_h * p.g.n_cams;
     const int tile_px = p.g.tile_w * p.g.tile_h;
     const int nt = (tile_px + 63) / 64 * 64;  // whole wavefronts
-    if (tile_px <= kTileThreads) {
-        if (dyn) eval3d_fwd_kernel<CDIM, true, kTileThreads><<<n_blocks, nt, 0, s>>>(p);
-        else eval3d_fwd_kernel<CDIM, false, kTileThreads><<<n_blocks, nt, 0, s>>>(p);
-    } else {
-        if (dyn) eval3d_fwd_kernel<CDIM, true, kMaxTilePixels><<<n_blocks, nt, 0, s>>>(p);
-        else eval3d_fwd_kernel<CDIM, false, kMaxTilePixels><<<n_blocks, nt, 0, s>>>(p);
-    }
+    auto go = [&](auto count_c) {
+        constexpr bool C = decltype(count_c)::value;
+        if (tile_px <= kTileThreads) {
+            if (dyn) eval3d_fwd_kernel<CDIM, true, kTileThreads, C><<<n_blocks, nt, 0, s>>>(p);
+            else eval3d_fwd_kernel<CDIM, false, kTileThreads, C><<<n_blocks, nt, 0, s>>>(p);
+        } else {
+            if (dyn) eval3d_fwd_kernel<CDIM, true, kMaxTilePixels, C><<<n_blocks, nt, 0, s>>>(p);
+            else eval3d_fwd_kernel<CDIM, false, kMaxTilePixels, C><<<n_blocks, nt, 0, s>>>(p);
+        }
+    };
+    if (p.pair_counts) go(std::true_type{});
+    else go(std::false_type{});
     return XSG_OK;
 }
 
