@@ -39,6 +39,37 @@ XSG_DEV int wave_max(int v) {
     return v;
 }
 
+// Reduce-scatter of the first nv (<= 16) of 16 per-lane values over the 64 lanes of a wavefront through a
+// wavefront-private LDS buffer: lane l stores value k at row k (rows of kRedRow floats, padded so that
+// the four lanes reading one quarter-row each fall in different banks), then lane 4k + q adds lanes
+// 16q .. 16q + 15 of row k with four 16-byte reads and the quad adds its four sums (DPP). Every lane of
+// quad k ends with the wave total of value k. LDS instructions of one wavefront complete in order, so
+// the reads see the stores and the next call's stores follow these reads. All 64 lanes active.
+constexpr int kRedRow = 68;
+XSG_DEV float wave_reduce_scatter16_lds(const float (&v)[16], int nv, float* __restrict__ buf) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        if (k < nv) buf[k * kRedRow + lane] = v[k];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int k = lane >> 2, q = lane & 3;
+    float s = 0.0f;
+    if (k < nv) {
+        const float4* row = reinterpret_cast<const float4*>(buf + k * kRedRow + 16 * q);
+        const float4 a = row[0], b = row[1], c = row[2], d = row[3];
+        s = (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) +
+            (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
+    }
+    s += dpp_mov<kDppQuadSwap2>(s);
+    s += dpp_mov<kDppQuadSwap1>(s);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return s;
+}
+
 // Per-pixel state of the backward sweep.
 template <int CS>
 struct BwdPixel {
@@ -203,6 +234,7 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
     __shared__ RayBundle s_bundle[NWB];
     __shared__ int32_t s_wbf[NWB];       // largest last id of each wavefront's pixels
     __shared__ uint64_t s_mask[NWB][NWB];  // [wavefront][staging wavefront]: Gaussians it evaluates
+    __shared__ __align__(16) float s_red[NWB][16 * kRedRow];  // per wavefront: the gradient reduction
 
     const TileGrid& g = p.g;
     const int n_tiles = g.n_tiles_w * g.n_tiles_h;
@@ -425,7 +457,7 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
                     float chunk[16];
 #pragma unroll
                     for (int k = 0; k < 16; ++k) chunk[k] = (16 * ch + k < K) ? acc[16 * ch + k] : 0.f;
-                    const float tot = wave_reduce_scatter16(chunk);
+                    const float tot = wave_reduce_scatter16_lds(chunk, min(16, K - 16 * ch), s_red[wave]);
                     if ((lane & 3) == 0 && 16 * ch + (lane >> 2) < K)
                         unsafeAtomicAdd((float*)((char*)dst_base[ch] + (uint64_t)gid * (uint32_t)(4 * dst_stride[ch])),
                                         tot);
