@@ -283,57 +283,6 @@ XSG_DEV float dpp_mov(float x) {
 }
 constexpr int kDppQuadSwap1 = 0xB1;    // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kDppQuadSwap2 = 0x4E;    // quad_perm [2,3,0,1]: lane ^ 2
-constexpr int kDppRowMirror = 0x140;   // lane i <-> 15 - i within a row of 16
-constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each half row of 8
-
-// One halving step with the gfx950 lane-swap instructions. v_permlane32_swap(x, y) exchanges
-// lanes 32-63 of x with lanes 0-31 of y; v_permlane16_swap(x, y) exchanges the odd 16-lane rows
-// of x with the even rows of y. With x = the component a lower lane keeps and y = the one its
-// partner keeps, afterwards x + y is, on every lane, its kept component summed over the pair.
-XSG_DEV float swap_add32(float keep_lo, float keep_hi) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false,
-                                                    false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-XSG_DEV float swap_add16(float keep_lo, float keep_hi) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false,
-                                                    false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Reduce-scatter of 16 per-lane values over the 64 lanes of a wavefront by recursive halving:
-// each step pairs every lane with a partner, keeps half of its values and adds the partner's
-// copy of that half. Partners at distance 32 and 16 exchange through lane swaps (lanes 0-31 keep
-// v[0..7], lanes 16-31 of each half keep the upper half of what is left), then the row and
-// half-row mirrors (DPP) and a final quad sum: lane l holds the wave total of value l >> 2.
-// Must be called with all 64 lanes active.
-XSG_DEV float wave_reduce_scatter16(const float (&v)[16]) {
-    const int lane = __lane_id();
-    float w[8], x[4], y[2];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) w[j] = swap_add32(v[j], v[j + 8]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) x[j] = swap_add16(w[j], w[j + 4]);
-    {
-        const bool up = (lane & 15) >= 8;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const float send = up ? x[j] : x[j + 2];
-            const float keep = up ? x[j + 2] : x[j];
-            y[j] = keep + dpp_mov<kDppRowMirror>(send);
-        }
-    }
-    float z;
-    {
-        const bool up = (lane & 7) >= 4;
-        const float send = up ? y[0] : y[1];
-        const float keep = up ? y[1] : y[0];
-        z = keep + dpp_mov<kDppHalfMirror>(send);
-    }
-    z += dpp_mov<kDppQuadSwap2>(z);
-    z += dpp_mov<kDppQuadSwap1>(z);
-    return z;
-}
 
 struct Eval3dParams {
     TileGrid g;
