@@ -8,8 +8,8 @@
 // with less traffic:
 //   1. count  : one thread per Gaussian instance computes its tile rectangle(s) (the seam spans of
 //               lidar / spherical flag-2 Gaussians are re-projected densely by seam_span_kernel)
-//               and writes tiles_per_gauss plus the rectangles; count_scan_kernel turns the block
-//               partials into block offsets and publishes the totals.
+//               and writes tiles_per_gauss plus the rectangles; a two-level scan of the block
+//               partials gives every compaction block its offset, and the totals are published.
 //   2. compact: one packed 64-bit scan ((count > 0) << 32 | count) gives every visible
 //               instance both its intersection offset and its rank among visible instances.
 //   3. depth  : the visible instances are sorted stably by the low 32 key bits (depth bits).
@@ -279,65 +279,74 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
     }
 }
 
-// Single workgroup: the exclusive prefix of the count blocks' packed partials, in place, so that
-// each compaction block reads its first position. The packed total (visible << 32 | count, whose
-// count field may carry) and the exact 64-bit intersection and row-run totals from cpart go to
-// `publish` (mapped host memory, read by the host after an event) and the visible count to m_dev,
-// for the kernels queued ahead of that readback. Each thread scans a contiguous chunk.
-__global__ __launch_bounds__(kBlock) void count_scan_kernel(unsigned nb, uint64_t* __restrict__ partials,
-                                                            const uint64_t* __restrict__ cpart,
-                                                            uint32_t* __restrict__ m_dev,
-                                                            uint64_t* __restrict__ publish) {
-    __shared__ uint64_t lds[kWaves];
-    const unsigned per = (nb + kBlock - 1) / kBlock;
-    const unsigned b0 = min(nb, threadIdx.x * per), b1 = min(nb, b0 + per);
-    uint64_t sum = 0, exact = 0, exact2 = 0;
-    for (unsigned b = b0; b < b1; ++b) {
-        sum += partials[b];
-        exact += cpart[2 * b];
-        exact2 += cpart[2 * b + 1];
-    }
-    uint64_t tot;
-    uint64_t run = block_exclusive_scan<uint64_t>(sum, lds, tot);
-    exact = block_reduce_sum<uint64_t>(exact, lds);
-    exact2 = block_reduce_sum<uint64_t>(exact2, lds);
-    for (unsigned b = b0; b < b1; ++b) {
-        const uint64_t x = partials[b];
-        partials[b] = run;
-        run += x;
-    }
-    if (threadIdx.x == 0) {
-        if (m_dev) *m_dev = (uint32_t)(tot >> 32);
-        publish[0] = tot;
-        publish[1] = exact;
-        publish[2] = exact2;
+// Two-level scans of per-block partials. slice_scan_kernel: workgroup s scans the kSlice partials
+// [kSlice s, kSlice (s + 1)) in place (exclusive within the slice) and stores their total in
+// slice_sum[s]; with `extra` (the count blocks' exact intersection and row-run sums, two per block)
+// it also stores their slice totals. A consumer block b then starts at
+// slice_offset(slice_sum, b / kSlice) + partials[b]: the slices before it are few (kSlice = 256 count
+// blocks of 1024 instances each), so each consumer sums them itself.
+constexpr int kSlice = kBlock;
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void slice_scan_kernel(unsigned n, T* __restrict__ partials,
+                                                            T* __restrict__ slice_sum,
+                                                            const uint64_t* __restrict__ extra,
+                                                            uint64_t* __restrict__ slice_extra) {
+    __shared__ T lds[kWaves];
+    __shared__ uint64_t lds64[kWaves];
+    const unsigned i = blockIdx.x * kSlice + threadIdx.x;
+    const T v = i < n ? partials[i] : T(0);
+    T tot;
+    const T ex = block_exclusive_scan<T>(v, lds, tot);
+    if (i < n) partials[i] = ex;
+    if (threadIdx.x == 0) slice_sum[blockIdx.x] = tot;
+    if (extra) {
+        const uint64_t e0 = block_reduce_sum<uint64_t>(i < n ? extra[2 * i] : 0ull, lds64);
+        const uint64_t e1 = block_reduce_sum<uint64_t>(i < n ? extra[2 * i + 1] : 0ull, lds64);
+        if (threadIdx.x == 0) {
+            slice_extra[2 * blockIdx.x] = e0;
+            slice_extra[2 * blockIdx.x + 1] = e1;
+        }
     }
 }
 
-// Single workgroup: exclusive prefix of n 32-bit block partials, in place (chunk per thread).
-__global__ __launch_bounds__(kBlock) void partials_scan_kernel(unsigned n, uint32_t* __restrict__ partials) {
-    __shared__ uint32_t lds[kWaves];
-    const unsigned per = (n + kBlock - 1) / kBlock;
-    const unsigned b0 = min(n, threadIdx.x * per), b1 = min(n, b0 + per);
-    uint32_t sum = 0;
-    for (unsigned b = b0; b < b1; ++b) sum += partials[b];
-    uint32_t tot;
-    uint32_t run = block_exclusive_scan<uint32_t>(sum, lds, tot);
-    for (unsigned b = b0; b < b1; ++b) {
-        const uint32_t x = partials[b];
-        partials[b] = run;
-        run += x;
-    }
+// sum of slice_sum[0, k), by the whole workgroup (block-uniform result)
+template <typename T>
+XSG_DEV T slice_offset(const T* __restrict__ slice_sum, unsigned k, T* lds) {
+    T acc = 0;
+    for (unsigned j = threadIdx.x; j < k; j += kBlock) acc += slice_sum[j];
+    return block_reduce_sum<T>(acc, lds);
 }
 
 // Compaction of the visible virtual instances in instance order: id, intersection offset, depth bits.
-// `pbase` holds each block's first packed position (count_scan_kernel).
+// Block b starts at the packed prefix of the count blocks before it (slice_scan_kernel's two levels).
+// Block 0 also sums the slices: the packed total (visible << 32 | count, whose count field may carry)
+// and the exact 64-bit intersection and row-run totals go to `publish` (mapped host memory, read by the
+// host after an event) and the visible count to m_dev, for the kernels queued ahead of that readback.
 __global__ __launch_bounds__(kBlock) void compact_kernel(
     int64_t n_virtual, const uint32_t* __restrict__ vcnt, const uint32_t* __restrict__ vkey,
-    const uint64_t* __restrict__ pbase, uint32_t* __restrict__ comp_id, uint32_t* __restrict__ comp_off,
-    uint32_t* __restrict__ comp_key) {
+    const uint64_t* __restrict__ pbase, const uint64_t* __restrict__ slice_sum,
+    const uint64_t* __restrict__ slice_extra, unsigned n_slices, uint32_t* __restrict__ comp_id,
+    uint32_t* __restrict__ comp_off, uint32_t* __restrict__ comp_key, uint32_t* __restrict__ m_dev,
+    uint64_t* __restrict__ publish) {
     __shared__ uint64_t lds[kWaves];
-    uint64_t carry = pbase[blockIdx.x];
+    uint64_t carry = slice_offset<uint64_t>(slice_sum, blockIdx.x / kSlice, lds) + pbase[blockIdx.x];
+    if (blockIdx.x == 0) {  // block-uniform
+        const uint64_t tot = slice_offset<uint64_t>(slice_sum, n_slices, lds);
+        uint64_t e0 = 0, e1 = 0;
+        for (unsigned j = threadIdx.x; j < n_slices; j += kBlock) {
+            e0 += slice_extra[2 * j];
+            e1 += slice_extra[2 * j + 1];
+        }
+        e0 = block_reduce_sum<uint64_t>(e0, lds);
+        e1 = block_reduce_sum<uint64_t>(e1, lds);
+        if (threadIdx.x == 0) {
+            if (m_dev) *m_dev = (uint32_t)(tot >> 32);
+            publish[0] = tot;
+            publish[1] = e0;
+            publish[2] = e1;
+        }
+    }
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= n_virtual) break;  // block-uniform
@@ -470,12 +479,14 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
                                                            const uint32_t* __restrict__ ids,
                                                            const Rect* __restrict__ rects,
                                                            const uint32_t* __restrict__ partials,
+                                                           const uint32_t* __restrict__ slice_sum,
                                                            uint32_t* __restrict__ roff) {
     __shared__ uint32_t lds[kWaves];
     m = min(m, (int64_t)*m_dev);
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     if (base >= m) return;  // block-uniform
-    uint32_t carry = partials[blockIdx.x];  // the block's first offset (partials_scan_kernel)
+    // the block's first offset: the slices before it, then its place in its slice (slice_scan_kernel)
+    uint32_t carry = slice_offset<uint32_t>(slice_sum, blockIdx.x / kSlice, lds) + partials[blockIdx.x];
     for (int k = 0; k < kCountItems; ++k) {
         if (base + (int64_t)k * kBlock >= m) break;
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
@@ -748,7 +759,9 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     __shared__ uint32_t s_dep[kWaves][kColGroup][64];  // staged depth bits (low key word)
     __shared__ int32_t s_gid[kWaves][kColGroup][64];   // staged Gaussian ids
     extern __shared__ uint32_t s_first[];              // [ntx]: first output position per column
-    const int64_t sg = blockIdx.x;
+    // consecutive segments of a row write the two sides of the cache lines at their column
+    // boundaries: on one XCD those partial lines meet in its L2
+    const int64_t sg = xcd_tile((int)blockIdx.x, (int)(s_max + 1));
     if (sg == s_max) {
         write_neg_runs(rec, row_start[n_real], n_runs, tile_base[(int64_t)n_real * ntx], n_out, out_keys, out_ids);
         return;
@@ -941,6 +954,7 @@ struct CountWs {
     uint32_t* alt_key; uint32_t* alt_id; uint32_t* hist; uint32_t* dtot; uint32_t* m_dev;
     uint32_t* roff; uint32_t* rpart;
     uint32_t* seam_cnt; uint32_t* seam_ids;  // per count block: its seam Gaussians (two spans only)
+    uint64_t* slice64; uint64_t* slice_extra; uint32_t* slice32;  // slice totals of the two-level scans
     int64_t n_virtual; unsigned nb;
     size_t bytes;
 };
@@ -971,6 +985,10 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     w.m_dev = (uint32_t*)(p + off); off += align256(4);
     w.seam_cnt = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb : 0);
     w.seam_ids = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb * (kCountTile / 2) : 0);
+    const size_t n_slices = ((size_t)w.nb + kSlice - 1) / kSlice;
+    w.slice64 = (uint64_t*)(p + off); off += align256(8 * n_slices);
+    w.slice_extra = (uint64_t*)(p + off); off += align256(16 * n_slices);
+    w.slice32 = (uint32_t*)(p + off); off += align256(4 * n_slices);
     w.bytes = off;
     return w;
 }
@@ -1115,9 +1133,11 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     CountReadback* rb = nullptr;
     rc = count_readback(rb);
     if (rc) return rc;
-    count_scan_kernel<<<1, kBlock, 0, s>>>(w.nb, w.partials, w.cpart, g.sort ? w.m_dev : nullptr, rb->dev);
-    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.comp_id, w.comp_off,
-                                           w.comp_key);
+    const unsigned n_slices = (w.nb + kSlice - 1) / kSlice;
+    slice_scan_kernel<uint64_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.partials, w.slice64, w.cpart, w.slice_extra);
+    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.slice64, w.slice_extra,
+                                           n_slices, w.comp_id, w.comp_off, w.comp_key,
+                                           g.sort ? w.m_dev : nullptr, rb->dev);
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
@@ -1126,8 +1146,9 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev, false, kPresortGrid);
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
-        partials_scan_kernel<<<1, kBlock, 0, s>>>(w.nb, w.rpart);
-        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.roff);
+        slice_scan_kernel<uint32_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.rpart, w.slice32, nullptr, nullptr);
+        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.slice32,
+                                                 w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
     // packed (visible << 32 | count) total, exact intersection total, exact row-run total; poll the

@@ -535,6 +535,14 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
     return result && ix && iy;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs; xcd_tile gives each XCD a contiguous run of
+// logical blocks, so that neighbouring blocks (tiles that share most of their Gaussians, writer
+// segments that share the cache lines at their boundaries) share an L2.
+XSG_DEV int xcd_tile(int b, int nblocks) {
+    const int x = b & 7, q = nblocks >> 3, r = nblocks & 7;
+    return x * q + min(x, r) + (b >> 3);
+}
+
 // --------------------------------------------------------------------------
 // wave64 helpers
 // --------------------------------------------------------------------------

@@ -34,13 +34,6 @@ struct TileGrid {
     int64_t n_isects;
 };
 
-// Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a contiguous run of tiles so
-// that neighbouring tiles, which share most of their Gaussians, share an L2.
-XSG_DEV int xcd_tile(int b, int nblocks) {
-    const int x = b & 7, q = nblocks >> 3, r = nblocks & 7;
-    return x * q + min(x, r) + (b >> 3);
-}
-
 struct PixelCtx {
     int cam, tile, tr;
     int i, j;
