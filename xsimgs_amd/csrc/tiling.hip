@@ -99,14 +99,13 @@ struct Geometry {
 constexpr int kCountItems = 4;
 constexpr int kCountTile = kBlock * kCountItems;
 
-// Count pass over Gaussian instances. A block covers kCountTile virtual instances (kCountTile /
-// SPANS Gaussians); it writes tiles_per_gauss, the rectangle, count and depth bits of every
-// virtual instance, and the block's packed count sum.
+// Count pass over regular-tiling Gaussian instances (one span each). A block covers kCountTile
+// instances; it writes tiles_per_gauss and the rectangle of every instance, and the block's packed
+// count sum. The compaction takes the counts from tiles_per_gauss and the depth bits from the depths.
 __global__ __launch_bounds__(kBlock) void count_regular_kernel(
-    int64_t n_total, const float2* __restrict__ means2d, const float2* __restrict__ radii,
-    const float* __restrict__ depths, float tsx, float tsy, int ntx, int nty, int32_t* __restrict__ tpg,
-    Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
-    uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart) {
+    int64_t n_total, const float2* __restrict__ means2d, const float2* __restrict__ radii, float tsx, float tsy,
+    int ntx, int nty, int32_t* __restrict__ tpg, Rect* __restrict__ rects, uint64_t* __restrict__ partials,
+    uint64_t* __restrict__ cpart) {
     __shared__ uint64_t lds[kWaves];
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
@@ -115,10 +114,8 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
         if (j < n_total) {
             const Rect r = regular_rect(means2d[j], radii[j], tsx, tsy, ntx, nty);
             const uint32_t c = rect_count(r);
-            tpg[j] = (int32_t)c;
+            tpg[j] = (int32_t)c;  // also the compaction's count (one span per instance)
             rects[j] = r;
-            vcnt[j] = c;
-            vkey[j] = __float_as_uint(depths[j]);
             acc += pack_count(c);
             acc_c += c;
             acc_r += c > 0 ? (uint32_t)(r.y1 - r.y0) : 0u;
@@ -347,22 +344,28 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
             publish[2] = e1;
         }
     }
-    const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    // each thread its kCountItems consecutive instances: one block scan places them all
+    const int64_t v0 = (int64_t)blockIdx.x * kCountTile + (int64_t)threadIdx.x * kCountItems;
+    uint32_t c[kCountItems];
+    uint64_t sum = 0;
+#pragma unroll
     for (int k = 0; k < kCountItems; ++k) {
-        if (base + (int64_t)k * kBlock >= n_virtual) break;  // block-uniform
-        const int64_t v = base + (int64_t)k * kBlock + threadIdx.x;
-        const uint32_t c = v < n_virtual ? vcnt[v] : 0u;
-        uint64_t tot;
-        const uint64_t s = carry + block_exclusive_scan<uint64_t>(pack_count(c), lds, tot);
-        carry += tot;
-        if (c > 0) {
+        c[k] = v0 + k < n_virtual ? vcnt[v0 + k] : 0u;
+        sum += pack_count(c[k]);
+    }
+    uint64_t tot;
+    uint64_t s = carry + block_exclusive_scan<uint64_t>(sum, lds, tot);
+#pragma unroll
+    for (int k = 0; k < kCountItems; ++k) {
+        if (c[k] > 0) {
             const uint64_t p = s >> 32;
             if (p < (uint64_t)n_virtual) {
-                comp_id[p] = (uint32_t)v;
+                comp_id[p] = (uint32_t)(v0 + k);
                 comp_off[p] = (uint32_t)s;
-                comp_key[p] = vkey[v];
+                comp_key[p] = vkey[v0 + k];
             }
         }
+        s += pack_count(c[k]);
     }
 }
 
@@ -967,8 +970,9 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     char* p = (char*)base;
     size_t off = 0;
     w.rects = (Rect*)(p + off); off += align256(sizeof(Rect) * nv);
-    w.vcnt = (uint32_t*)(p + off); off += align256(4 * nv);
-    w.vkey = (uint32_t*)(p + off); off += align256(4 * nv);
+    const size_t nv2 = g.spans == 2 ? (size_t)nv : 0;  // regular tiling compacts from its inputs
+    w.vcnt = (uint32_t*)(p + off); off += align256(4 * nv2);
+    w.vkey = (uint32_t*)(p + off); off += align256(4 * nv2);
     w.partials = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * (w.nb + 3));
     w.cpart = (uint64_t*)(p + off); off += align256(sizeof(uint64_t) * 2 * w.nb);
     w.comp_id = (uint32_t*)(p + off); off += align256(4 * nv);
@@ -1097,8 +1101,8 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     const CountWs w = count_ws_layout(g, workspace);
     if (g.kind == XSG_TILING_REGULAR) {
         count_regular_kernel<<<w.nb, kBlock, 0, s>>>(nt, (const float2*)d->means2d, (const float2*)d->radii,
-                                                     d->depths, (float)d->tile_w, (float)d->tile_h, g.ntx,
-                                                     g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
+                                                     (float)d->tile_w, (float)d->tile_h, g.ntx, g.nty, tpg,
+                                                     w.rects, w.partials, w.cpart);
     } else {
         if (!d->camera_pack || !d->flags || !d->points || !d->scales || !d->quats)
             return xsg_fail(XSG_ERR_INVALID, "lidar / spherical tiling needs camera and Gaussian tensors");
@@ -1135,7 +1139,12 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (rc) return rc;
     const unsigned n_slices = (w.nb + kSlice - 1) / kSlice;
     slice_scan_kernel<uint64_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.partials, w.slice64, w.cpart, w.slice_extra);
-    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.vcnt, w.vkey, w.partials, w.slice64, w.slice_extra,
+    // regular tiling has one span per instance: its counts are tiles_per_gauss and its depth bits the
+    // depths themselves
+    const bool regular = g.kind == XSG_TILING_REGULAR;
+    compact_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, regular ? reinterpret_cast<const uint32_t*>(tpg) : w.vcnt,
+                                           regular ? reinterpret_cast<const uint32_t*>(d->depths) : w.vkey,
+                                           w.partials, w.slice64, w.slice_extra,
                                            n_slices, w.comp_id, w.comp_off, w.comp_key,
                                            g.sort ? w.m_dev : nullptr, rb->dev);
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
