@@ -342,6 +342,10 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
     const int32_t eff_end = min(range_end - 1, s_max);
     const int32_t n_eff = eff_end - range_start + 1;
     const int num_batches = n_eff > 0 ? (n_eff + nthr - 1) / nthr : 0;
+    // the flatten id a thread stages in the next batch, loaded one batch ahead (its latency then
+    // overlaps the pair loop instead of preceding the Gaussian's own loads)
+    int32_t fid_next = 0;
+    if (num_batches > 0 && tr < nthr && eff_end - tr >= range_start) fid_next = p.flatten[eff_end - tr];
 
     for (int b = 0; b < num_batches; ++b) {
         __syncthreads();
@@ -349,9 +353,11 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
         const int32_t idx = batch_end - tr;
         bool staged = false;
         CullGauss cg;
+        const int32_t fid_cur = fid_next;
+        if (tr < nthr && idx - nthr >= range_start) fid_next = p.flatten[idx - nthr];
         if (tr < nthr && idx >= range_start) {
             staged = true;
-            const int32_t fid = p.flatten[idx];
+            const int32_t fid = fid_cur;
             const int64_t gid = fid - (int64_t)cam * g.n;
             s_id[tr] = fid;
             const f3 mu = ld3(p.means + 3 * gid);

@@ -65,15 +65,24 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
 
     const int32_t n_range = c.range_end - c.range_start;
     const int num_batches = n_range > 0 ? (n_range + bs - 1) / bs : 0;
+    // the flatten id a thread stages in the next batch, loaded one batch ahead (its latency then
+    // overlaps the pair loop instead of preceding the Gaussian's own loads)
+    int32_t fid_next = 0;
+    {
+        const uint32_t idx0 = (uint32_t)c.range_start + (uint32_t)c.tr;
+        if (num_batches > 0 && c.tr < bs && idx0 < (uint32_t)c.range_end) fid_next = p.flatten[idx0];
+    }
     for (int b = 0; b < num_batches; ++b) {
         if (__syncthreads_count(done) >= (int)blockDim.x) break;
         const uint32_t batch_start = (uint32_t)c.range_start + (uint32_t)(bs * b);
         const uint32_t idx = batch_start + c.tr;
         bool staged = false;
         CullGauss cg;
+        const int32_t fid_cur = fid_next;
+        if (c.tr < bs && idx + (uint32_t)bs < (uint32_t)c.range_end) fid_next = p.flatten[idx + bs];
         if (c.tr < bs && idx < (uint32_t)c.range_end) {
             staged = true;
-            const int32_t fid = p.flatten[idx];
+            const int32_t fid = fid_cur;
             const int64_t gid = fid - (int64_t)c.cam * g.n;
             const f3 mu = ld3(p.means + 3 * gid);
             const float op = p.opac[gid];
