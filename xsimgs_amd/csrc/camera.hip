@@ -163,16 +163,21 @@ __global__ __launch_bounds__(kBlock) void ut_project_phm_kernel(
         const f3 pv = vel ? ld3(vel + 3 * i) : mk3(0.f, 0.f, 0.f);
         f2 rc = mk2(0.f, 0.f), rl = rc, rr = rc, mc = rc, ml = rc, mr = rc;
         float dc = 0.f, dl = 0.f, dr = 0.f, ud = 0.f;
-        bool res = ut_projection<KIND>(cam, XSG_MODE_CENTRAL, ut, img, pp, pw, pv, op, d, is_static,
-                                       mc, rc, dc, ud);
+        // a static pose projects the seven sigma points to angles once; the three phase modes then
+        // differ only in how they unwrap the azimuth
+        SigmaAngles sa;
+        if (is_static) sigma_angles(cam, pw, d, sa);
+        auto project = [&](int mode, f2& m2, f2& r2, float& dd) {
+            if (is_static) return ut_projection_angles(cam, mode, ut, img, pp, op, sa, m2, r2, dd, ud);
+            return ut_projection<KIND>(cam, mode, ut, img, pp, pw, pv, op, d, false, m2, r2, dd, ud);
+        };
+        bool res = project(XSG_MODE_CENTRAL, mc, rc, dc);
         if (res) {
             const float u_pi = float(M_PI) * img.x / fabsf(cam.i1);
             const int r_c = int(res) * (int(ud > u_pi) + 1);
-            res = ut_projection<KIND>(cam, XSG_MODE_NEGATIVE, ut, img, pp, pw, pv, op, d, is_static,
-                                      ml, rl, dl, ud);
+            res = project(XSG_MODE_NEGATIVE, ml, rl, dl);
             const int r_l = int(res) * (int(ud > u_pi) + 1);
-            res = ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, pw, pv, op, d, is_static,
-                                      mr, rr, dr, ud);
+            res = project(XSG_MODE_POSITIVE, mr, rr, dr);
             const int r_r = int(res) * (int(ud > u_pi) + 1);
             if (r_l == 1 && r_r == 1) {
                 flag = 2; r_out = rl; m_out = ml; d_out = dl;

@@ -414,11 +414,6 @@ XSG_DEV void ut_deltas_rsq(float sqrt_dl, float4 q, f3 s, f3 d[3]) {
 
 struct UtWeights { float wm0, wc0, wi, sqrt_dl; };
 
-// unscented_transform (ut_kernels.h:52-137) + the radii / on-screen test of
-// unscented_transform_projection (ut_kernels.h:140-184). On failure mean2d / depth keep what the
-// reference leaves in them (untouched if the centre point fails, the accumulated mean if a sigma
-// point fails) and radii come from a zero covariance, because the phase-modelled selection
-// (ut_phm_kernels.h:417-421) can pick a failed side.
 // A camera whose pose does not move maps world to camera space by one linear map: quat_apply with
 // the conjugate of q0 (world_to_camera_jac at any time), p -> p + 2 (w (u x p) + u x (u x p)) with
 // u = -q0.xyz, i.e. M = I + 2 w [u]x + 2 (u u^T - |u|^2 I) (exact for any quaternion).
@@ -435,20 +430,12 @@ XSG_DEV Mat3 static_world_to_camera(const Camera& c) {
 
 XSG_DEV f3 mul(const Mat3& m, f3 v) { return mk3(dot(m.r0, v), dot(m.r1, v), dot(m.r2, v)); }
 
-// camera_projection for a static pose from the camera-space point: the point does not depend on the
-// time, so the projection's time Jacobian is 0 and the Newton step of the Jacobian models reduces to
-// the fixed-point step p_time -= residual, as for the other models (projection_kernels.h:116-198).
-// The pinhole projection takes one reciprocal of z.
-template <int KIND>
-XSG_DEV void static_camera_projection(const Camera& c, f3 pc, const ProjParams& pp, int mode, float4& uvdt,
-                                      bool& valid) {
-    f3 uvd;
-    if constexpr (KIND == XSG_CAM_PINHOLE) {
-        const float iz = 1.0f / pc.z;
-        uvd = mk3(pc.x * c.i0 * iz + c.i2, pc.y * c.i1 * iz + c.i3, pc.z);
-    } else {
-        uvd = point_to_uvd<KIND>(c, mode, pc);
-    }
+// The time steps of camera_projection for a static pose, from the projected point: the point does not
+// depend on the time, so the projection's time Jacobian is 0 and the Newton step of the Jacobian
+// models reduces to the fixed-point step p_time -= residual, as for the other models
+// (projection_kernels.h:116-198).
+XSG_DEV void static_projection_tail(const Camera& c, f3 uvd, const ProjParams& pp, int mode, float4& uvdt,
+                                    bool& valid) {
     float p_time = 0.0f;
     if (mode == XSG_MODE_NEGATIVE) p_time = -fabsf(c.roll_u) * 0.5f;
     else if (mode == XSG_MODE_POSITIVE) p_time = fabsf(c.roll_u) * 0.5f;
@@ -470,26 +457,35 @@ XSG_DEV void static_camera_projection(const Camera& c, f3 pc, const ProjParams& 
     valid = valid && (fabsf(residual) < pp.max_res) && (uvd.z > 0.0f);
 }
 
+// camera_projection for a static pose from the camera-space point. The pinhole projection takes one
+// reciprocal of z.
 template <int KIND>
-XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 img, const ProjParams& pp,
-                           f3 pw, f3 pv, float opac, const f3 d[3], bool is_static, f2& mean2d,
-                           f2& radii, float& depth, float& u_distance) {
+XSG_DEV void static_camera_projection(const Camera& c, f3 pc, const ProjParams& pp, int mode, float4& uvdt,
+                                      bool& valid) {
+    f3 uvd;
+    if constexpr (KIND == XSG_CAM_PINHOLE) {
+        const float iz = 1.0f / pc.z;
+        uvd = mk3(pc.x * c.i0 * iz + c.i2, pc.y * c.i1 * iz + c.i3, pc.z);
+    } else {
+        uvd = point_to_uvd<KIND>(c, mode, pc);
+    }
+    static_projection_tail(c, uvd, pp, mode, uvdt, valid);
+}
+
+// unscented_transform (ut_kernels.h:52-137) + the radii / on-screen test of
+// unscented_transform_projection (ut_kernels.h:140-184) over the seven sigma points that
+// proj(i, uvdt, valid) projects (0: the centre; 2k + 1 and 2k + 2: the centre plus and minus delta k).
+// On failure mean2d / depth keep what the reference leaves in them (untouched if the centre point
+// fails, the accumulated mean if a sigma point fails) and radii come from a zero covariance, because the
+// phase-modelled selection (ut_phm_kernels.h:417-421) can pick a failed side.
+template <typename Proj>
+XSG_DEV bool ut_projection_core(const UtWeights& ut, f2 img, float opac, Proj&& proj, f2& mean2d, f2& radii,
+                                float& depth, float& u_distance) {
     float4 uvdt;
     bool valid = true;
     f2 pts[7];
     bool result = true;
-    // static pose: the seven camera-space points are M (pw - t0) +- M d_i
-    Mat3 m;
-    f3 pc0 = mk3(0.f, 0.f, 0.f), e[3];
-    if (is_static) {
-        m = static_world_to_camera(c);
-        pc0 = mul(m, pw - c.t0);
-#pragma unroll
-        for (int k = 0; k < 3; ++k) e[k] = mul(m, d[k]);
-        static_camera_projection<KIND>(c, pc0, pp, mode, uvdt, valid);
-    } else {
-        camera_projection<KIND>(c, pw, pv, pp, mode, false, uvdt, valid);
-    }
+    proj(0, uvdt, valid);
     f2 cov_xx_xy = mk2(0.f, 0.f);
     float cov_yy = 0.f;
     if (!valid) {
@@ -499,17 +495,14 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
         mean2d = mk2(ut.wm0 * pts[0].x, ut.wm0 * pts[0].y);
         depth = uvdt.z;
         float u_min = pts[0].x, u_max = pts[0].x;
-        float sign = 1.0f;
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
-            if (is_static) static_camera_projection<KIND>(c, pc0 + sign * e[i / 2], pp, mode, uvdt, valid);
-            else camera_projection<KIND>(c, pw + sign * d[i / 2], pv, pp, mode, false, uvdt, valid);
+            proj(i + 1, uvdt, valid);
             pts[i + 1] = mk2(uvdt.x * img.x, uvdt.y * img.y);
             mean2d.x += ut.wi * pts[i + 1].x;
             mean2d.y += ut.wi * pts[i + 1].y;
             u_min = fminf(u_min, pts[i + 1].x);
             u_max = fmaxf(u_max, pts[i + 1].x);
-            sign *= -1.0f;
         }
         if (!valid) {
             result = false;
@@ -533,6 +526,65 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
     const bool ix = !(((mean2d.x + radii.x) < 0) || (img.x < (mean2d.x - radii.x)));
     const bool iy = !(((mean2d.y + radii.y) < 0) || (img.y < (mean2d.y - radii.y)));
     return result && ix && iy;
+}
+
+// One Gaussian in one phase mode. A static pose maps world to camera space by one linear map, so the
+// seven camera-space points are M (pw - t0) and that plus and minus M d_k; a moving one solves each
+// point's pixel time (camera_projection).
+template <int KIND>
+XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 img, const ProjParams& pp,
+                           f3 pw, f3 pv, float opac, const f3 d[3], bool is_static, f2& mean2d,
+                           f2& radii, float& depth, float& u_distance) {
+    if (is_static) {
+        const Mat3 m = static_world_to_camera(c);
+        const f3 pc0 = mul(m, pw - c.t0);
+        f3 e[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) e[k] = mul(m, d[k]);
+        auto proj = [&](int i, float4& uvdt, bool& valid) {
+            const f3 pc = i == 0 ? pc0 : ((i & 1) ? pc0 + e[(i - 1) >> 1] : pc0 - e[(i - 1) >> 1]);
+            static_camera_projection<KIND>(c, pc, pp, mode, uvdt, valid);
+        };
+        return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
+    }
+    auto proj = [&](int i, float4& uvdt, bool& valid) {
+        const f3 pw_i = i == 0 ? pw : ((i & 1) ? pw + d[(i - 1) >> 1] : pw - d[(i - 1) >> 1]);
+        camera_projection<KIND>(c, pw_i, pv, pp, mode, false, uvdt, valid);
+    };
+    return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
+}
+
+// A static spherical / lidar camera's sigma points in angle form: each camera-space point's azimuth,
+// elevation and range (point_to_uvd's spherical branch, spherical.h:133-142). They do not depend on
+// the phase mode, which only unwraps u (angles_to_uv), so the three modes of the phase-modelled
+// projection share them; each mode's results equal ut_projection's bit for bit.
+struct SigmaAngles { float phi[7], theta[7], r[7]; };
+
+XSG_DEV void sigma_angles(const Camera& c, f3 pw, const f3 d[3], SigmaAngles& a) {
+    const Mat3 m = static_world_to_camera(c);
+    const f3 pc0 = mul(m, pw - c.t0);
+    f3 e[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) e[k] = mul(m, d[k]);
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+        const f3 p = i == 0 ? pc0 : ((i & 1) ? pc0 + e[(i - 1) >> 1] : pc0 - e[(i - 1) >> 1]);
+        const float x2y2 = p.x * p.x + p.y * p.y;
+        const float r = sqrtf(x2y2 + p.z * p.z);
+        a.phi[i] = atan2f(-p.x, -p.y) + float(M_PI);
+        a.theta[i] = asinf(p.z / r);
+        a.r[i] = r;
+    }
+}
+
+XSG_DEV bool ut_projection_angles(const Camera& c, int mode, const UtWeights& ut, f2 img, const ProjParams& pp,
+                                  float opac, const SigmaAngles& a, f2& mean2d, f2& radii, float& depth,
+                                  float& u_distance) {
+    auto proj = [&](int i, float4& uvdt, bool& valid) {
+        const f2 uv = angles_to_uv(c, mode, a.phi[i], a.theta[i]);
+        static_projection_tail(c, mk3(uv.x, uv.y, a.r[i]), pp, mode, uvdt, valid);
+    };
+    return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs; xcd_tile gives each XCD a contiguous run of
