@@ -48,6 +48,8 @@ def parse():
                    help="render camera rigs one camera per call (the reference caller's loop) instead of batched")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 256 MiB device copy 5 times (scale of the rocprofv3 byte counters)")
+    p.add_argument("--calibrate-valu", action="store_true",
+                   help="only measure the VALU issue ceiling at 1-8 waves per SIMD and the shader clock")
     return p.parse_args()
 
 
@@ -64,7 +66,10 @@ def parse():
 FLOPS_EVAL = 42
 FLOPS_FWD_CONTRIB = 13          # + 2 per colour channel
 FLOPS_BWD_CONTRIB = 72          # + 4 per colour channel
-FP32_VALU_PEAK_TFLOPS = 78.6    # non-packed FP32 (packed FP32 ops are disabled in this build)
+# MI355X's published FP32 peak: 1024 SIMDs issue a wave64 FMA every 2 cycles at 2.4 GHz. The kernels
+# are also priced against the FMA rate this GPU measurably sustains (valu_ceiling), which runs below it
+# because the clock drops under a full VALU load.
+FP32_VALU_PEAK_TFLOPS = 157.3
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "eval3d_bwd_cfg2_traffic.json")
 
 
@@ -76,6 +81,38 @@ def calibrate_copy(torch):
         y.copy_(x)
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": 5}))
+
+
+def valu_ceiling(torch, waves_per_simd, iters=8192):
+    """The VALU issue ceiling measured on this GPU: `xsg_bench_valu_ceiling` puts `waves_per_simd`
+    wavefronts on every SIMD, each issuing 16 * iters independent FP32 FMAs (no packed FP32). Returns
+    the wave64 VALU instructions issued per microsecond per SIMD, the FMA rate in TFLOP/s and the
+    shader clock the launch ran at (s_memtime against the 100 MHz real-time counter)."""
+    from xsimgs_amd import _C
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = cus * waves_per_simd
+    out = torch.empty(blocks * 256, device="cuda:0")
+    stamps = torch.zeros(4 * blocks, dtype=torch.int64, device="cuda:0")
+    _C.bench_valu_ceiling(blocks, iters, out, stamps)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    _C.bench_valu_ceiling(blocks, iters, out, stamps)
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_time(e)
+    st = stamps.view(-1, 4).cpu().double()
+    mhz = float(((st[:, 1] - st[:, 0]) / (st[:, 3] - st[:, 2])).mean()) * 100.0
+    insts = blocks * 4 * iters * 16                      # wave64 VALU instructions of the launch
+    return {"waves_per_simd": waves_per_simd, "ms": round(ms, 4),
+            "inst_per_us_per_simd": round(insts / (4 * cus) / (ms * 1e3), 1),
+            "fma_tflops": round(insts * 64 * 2 / (ms * 1e-3) / 1e12, 1), "clock_mhz": round(mhz)}
+
+
+def calibrate_valu(torch):
+    rows = [valu_ceiling(torch, w) for w in range(1, 9)]
+    print(json.dumps({"calibration": "valu", "rows": rows}))
 
 
 def event_time_ms(fn, reps, torch):
@@ -397,10 +434,13 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                 "launch_ms": round(t_dom, 4), "alg_bytes_per_launch": int(alg[dom]),
                 "valu": {"achieved": round(tfl, 2), "peak": FP32_VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tfl / FP32_VALU_PEAK_TFLOPS, 4), "flops_per_launch": int(flops[dom])},
+                         "frac": round(tfl / FP32_VALU_PEAK_TFLOPS, 4), "flops_per_launch": int(flops[dom]),
+                         "measured_fma_ceiling": args.valu_ceiling["fma_tflops"],
+                         "frac_of_measured": round(tfl / args.valu_ceiling["fma_tflops"], 4)},
                 "note": ("the compositor has no dense contraction (no MFMA) and is VALU / LDS / atomic bound: "
-                         "the HBM fraction of its algorithmic bytes is reported as defined, the VALU fraction "
-                         "against non-packed FP32 beside it")}
+                         "the HBM fraction of its algorithmic bytes is reported as defined, beside it the FP32 "
+                         "work it executes against the published FP32 peak and against the FMA rate measured "
+                         "on this GPU (8 waves per SIMD)")}
     if os.path.exists(TRAFFIC_FILE) and name == "cfg2" and dom == "eval3d_bwd":
         with open(TRAFFIC_FILE) as fh:
             tr = json.load(fh)
@@ -482,6 +522,10 @@ def main():
     if args.calibrate_copy:
         calibrate_copy(torch)
         return
+    if args.calibrate_valu:
+        calibrate_valu(torch)
+        return
+    args.valu_ceiling = valu_ceiling(torch, 8)
     head = bench_config(args.config, args, args.steps, args.warmup, args.stage_reps, torch, np,
                         cpu=not args.no_cpu_baseline, extensions=True)
     configs = {}
@@ -512,6 +556,7 @@ def main():
         "live_ms": head["live_ms"],
         "pairs": head["pairs_per_camera"],
         "roofline": head["roofline"],
+        "valu_ceiling": args.valu_ceiling,
         "cpu_baseline": head["cpu_baseline"],
         "configs": configs,
     }

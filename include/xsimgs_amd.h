@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define XSG_ABI_VERSION 1
+#define XSG_ABI_VERSION 2
 
 /* return codes */
 #define XSG_OK 0
@@ -322,7 +322,10 @@ typedef struct {
 } xsg_eval3d_args;
 
 int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream);
-size_t xsg_eval3d_bwd_workspace_bytes(int64_t n, int cdim);
+/* Workspace of xsg_eval3d_bwd for these arguments (sizes only are read): the per-Gaussian
+ * accumulators of the symmetric M gradient (6 floats per Gaussian) and, per (camera, tile), its work
+ * estimate and the order in which the tiles are launched (two int32). */
+size_t xsg_eval3d_bwd_workspace_bytes(const xsg_eval3d_args* a);
 int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_stream_t stream);
 
 #ifdef __cplusplus

@@ -1,4 +1,4 @@
-"""The C-ABI library loads and exports every entry point that include/xsimgs_amd.h declares.
+"""The C-ABI library loads and exports every entry point that include/*.h declares.
 
 CPU only: the library is loaded with ctypes and only its host-side queries are called (version,
 pack sizes, workspace sizes, argument validation that fails before any launch).
@@ -10,14 +10,28 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "xsimgs_amd.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if h.endswith(".h")]
 LIB = os.path.join(ROOT, "xsimgs_amd", "libxsimgs_hip.so")
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    text = "\n".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(xsg_\w+)\s*\(", text, flags=re.M)))
+
+
+class Eval3dArgs(C.Structure):  # xsg_eval3d_args, field for field
+    _fields_ = [("cdim", C.c_int), ("n", C.c_int64), ("n_cams", C.c_int)] + \
+        [(k, C.c_void_p) for k in ("means", "quats", "scales", "colors", "opacities", "velocity",
+                                   "ray_time_delta", "ray_o", "ray_d")] + \
+        [(k, C.c_int) for k in ("width", "height", "tile_w", "tile_h", "n_tiles_w", "n_tiles_h")] + \
+        [("tile_offsets", C.c_void_p), ("flatten_ids", C.c_void_p), ("n_isects", C.c_int64)] + \
+        [(k, C.c_void_p) for k in ("out_rgb", "out_depth", "out_alpha", "out_last_ids", "render_alpha",
+                                   "last_ids", "v_rgb", "v_depth", "v_alpha", "v_means", "v_quats",
+                                   "v_scales", "v_opacities", "v_colors", "v_ray_o", "v_ray_d",
+                                   "v_velocity", "v_time_delta", "pair_counts")] + \
+        [("colors_shared", C.c_int)]
 
 
 @pytest.fixture(scope="module")
@@ -43,7 +57,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_host_queries(lib):
     lib.xsg_abi_version.restype = C.c_int
-    assert lib.xsg_abi_version() == 1
+    assert lib.xsg_abi_version() == 2
     assert lib.xsg_camera_pack_elements(0) == 21
     assert lib.xsg_camera_pack_elements(1) == 21
     assert lib.xsg_camera_pack_elements(2) == 23
@@ -54,8 +68,13 @@ def test_host_queries(lib):
     lib.xsg_sh_bwd_workspace_bytes.restype = C.c_size_t
     lib.xsg_eval3d_bwd_workspace_bytes.restype = C.c_size_t
     lib.xsg_radix_sort_workspace_bytes.restype = C.c_size_t
-    assert lib.xsg_eval3d_bwd_workspace_bytes(C.c_int64(1000), 3) >= 1000 * 6 * 4
+    # the backward's workspace: 6 floats per Gaussian, then two int32 per (camera, tile)
+    a = Eval3dArgs(cdim=3, n=1000, n_cams=2, n_tiles_w=120, n_tiles_h=68)
+    assert lib.xsg_eval3d_bwd_workspace_bytes(C.byref(a)) >= 1000 * 6 * 4 + 2 * 2 * 120 * 68 * 4
+    assert lib.xsg_eval3d_bwd_workspace_bytes(None) == 0
     assert lib.xsg_radix_sort_workspace_bytes(C.c_int64(1 << 20)) > 0
+    # the measurement launch rejects an empty grid on the host
+    assert lib.xsg_bench_valu_ceiling(0, 1, None, None, None) < 0
     # the allocation-free SH backward rejects sizes over its scratch limit on the host, before any
     # pointer is used or any HIP call is made
     vp = C.c_void_p

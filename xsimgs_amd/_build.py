@@ -1,6 +1,6 @@
 """In-tree build of the xsimgs_amd native libraries.
 
-* ``libxsimgs_hip.so`` -- the C-ABI (include/xsimgs_amd.h) with every HIP kernel, compiled by
+* ``libxsimgs_hip.so`` -- the C-ABI (include/*.h) with every HIP kernel, compiled by
   hipcc for gfx950. Packed-FP32 instruction selection is disabled.
 * ``_C*.so`` -- the torch extension that re-exports the reference's op names over the C-ABI.
 
@@ -27,7 +27,7 @@ ARCH = os.environ.get("XSG_OFFLOAD_ARCH", "gfx950")
 HIP_SOURCES = ["eval3d_bwd_g7.hip", "eval3d_bwd_g6.hip", "eval3d_bwd_g5.hip", "eval3d_bwd_g4.hip",
                "eval3d_bwd_g3.hip", "eval3d_bwd_g2.hip", "eval3d_bwd_g1.hip", "eval3d_bwd_g0.hip",
                "eval3d_fwd.hip", "tiling.hip", "camera.hip", "sh.hip", "capi.hip", "eval3d_bwd.hip",
-               "eval3d_capi.hip", "nodes.hip"]
+               "eval3d_capi.hip", "nodes.hip", "calibrate.hip"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-result"]

@@ -239,7 +239,8 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
     const TileGrid& g = p.g;
     const int n_tiles = g.n_tiles_w * g.n_tiles_h;
     const int nblocks = n_tiles * g.n_cams;
-    const int logical = xcd_tile((int)blockIdx.x, nblocks);
+    const int slot = xcd_tile((int)blockIdx.x, nblocks);
+    const int logical = p.tile_order ? p.tile_order[slot] : slot;
     const int cam = logical / n_tiles, tile = logical - cam * n_tiles;
     const int bs = g.tile_w * g.tile_h;
     const int nthr = (bs + PX - 1) / PX;

@@ -93,6 +93,100 @@ __global__ __launch_bounds__(kBlock) void bwd_epilogue_kernel(int64_t n, const f
     for (int cc = 0; cc < 3; ++cc) v_scales[3 * i + cc] = -Q[cc][cc] * s[cc];
 }
 
+// Launch order of the backward's tiles. A tile's backward work is about the number of its Gaussians
+// from its first intersection up to the largest last id of its pixels (compositing stops there for
+// every pixel), and tiles differ by a factor of two or more; with about three tiles per wave slot,
+// the heavy tiles that happen to start last set the kernel's end. Each XCD keeps the same contiguous
+// run of tiles (xcd_tile: neighbouring tiles share their Gaussians in its L2) and launches it heaviest
+// first.
+//
+// tile_work_kernel: one wavefront per (camera, tile), the largest last id of the tile's pixels.
+__global__ __launch_bounds__(kBlock) void tile_work_kernel(TileGrid g, const int32_t* __restrict__ last_ids,
+                                                           const int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ work) {
+    const int n_tiles = g.n_tiles_w * g.n_tiles_h;
+    const int nblocks = n_tiles * g.n_cams;
+    const int t = blockIdx.x * (kBlock / 64) + (int)(threadIdx.x >> 6);
+    if (t >= nblocks) return;  // wave-uniform
+    const int cam = t / n_tiles, tile = t - cam * n_tiles;
+    const int trow = tile / g.n_tiles_w, tcol = tile - trow * g.n_tiles_w;
+    const int bs = g.tile_w * g.tile_h;
+    const int64_t hw = (int64_t)g.width * g.height;
+    int m = -1;
+    for (int qi = __lane_id(); qi < bs; qi += 64) {
+        const int ty = qi / g.tile_w, tx = qi - ty * g.tile_w;
+        const int i = trow * g.tile_h + ty, j = tcol * g.tile_w + tx;
+        if (i < g.height && j < g.width) m = max(m, last_ids[(int64_t)cam * hw + (int64_t)i * g.width + j]);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, __shfl_xor(m, off, 64));
+    if (__lane_id() == 0) {
+        const int32_t rs = offsets[t];
+        const int32_t re = (t == nblocks - 1) ? (int32_t)g.n_isects : offsets[t + 1];
+        work[t] = max(0, min(re - 1, m) - rs + 1);
+    }
+}
+
+// tile_order_kernel: one workgroup per XCD (8). XCD x runs the logical blocks
+// [x q + min(x, r), + q + (x < r)) of xcd_tile; they are placed heaviest first by a counting sort on
+// the top 8 bits of the work (LDS histogram, scan, scatter; ties in no particular order).
+constexpr int kOrderThreads = 1024;
+__global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(int nblocks, const int32_t* __restrict__ work,
+                                                                   int32_t* __restrict__ order) {
+    __shared__ int hist[256];
+    __shared__ int wmax[kOrderThreads / 64];
+    const int x = blockIdx.x, q = nblocks >> 3, r = nblocks & 7;
+    const int s0 = x * q + min(x, r), cnt = q + (x < r ? 1 : 0);
+    int mx = 0;
+    for (int i = threadIdx.x; i < cnt; i += kOrderThreads) mx = max(mx, work[s0 + i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+    if (__lane_id() == 0) wmax[threadIdx.x >> 6] = mx;
+    if (threadIdx.x < 256) hist[threadIdx.x] = 0;
+    __syncthreads();
+    mx = 0;
+#pragma unroll
+    for (int k = 0; k < kOrderThreads / 64; ++k) mx = max(mx, wmax[k]);
+    const int shift = max(0, 32 - __clz(mx) - 8);  // work >> shift < 256
+    for (int i = threadIdx.x; i < cnt; i += kOrderThreads) atomicAdd(&hist[255 - (work[s0 + i] >> shift)], 1);
+    __syncthreads();
+    if (threadIdx.x < 64) {  // exclusive scan of the 256 bins: four per lane, then across the wavefront
+        const int l = threadIdx.x;
+        const int a0 = hist[4 * l], a1 = hist[4 * l + 1], a2 = hist[4 * l + 2], a3 = hist[4 * l + 3];
+        const int sum = a0 + a1 + a2 + a3;
+        int inc = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(inc, off, 64);
+            if (l >= off) inc += v;
+        }
+        const int ex = inc - sum;
+        hist[4 * l] = ex;
+        hist[4 * l + 1] = ex + a0;
+        hist[4 * l + 2] = ex + a0 + a1;
+        hist[4 * l + 3] = ex + a0 + a1 + a2;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < cnt; i += kOrderThreads) {
+        const int pos = atomicAdd(&hist[255 - (work[s0 + i] >> shift)], 1);
+        order[s0 + pos] = s0 + i;
+    }
+}
+
+struct BwdWorkspace {
+    size_t order_off, work_off, bytes;
+};
+
+constexpr size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+BwdWorkspace bwd_workspace(int64_t n, int64_t nblocks) {
+    BwdWorkspace w;
+    w.work_off = align256((size_t)(n > 0 ? n : 1) * 6 * sizeof(float));
+    w.order_off = w.work_off + align256((size_t)(nblocks > 0 ? nblocks : 1) * sizeof(int32_t));
+    w.bytes = w.order_off + align256((size_t)(nblocks > 0 ? nblocks : 1) * sizeof(int32_t));
+    return w;
+}
+
 bool cdim_supported(int c) {
     switch (c) {
 #define XSG_CASE(C) case C: return true;
@@ -114,6 +208,9 @@ int fill_params(const xsg_eval3d_args* a, Eval3dParams& p, const char* who) {
     if ((int64_t)a->n_tiles_w * a->tile_w < a->width || (int64_t)a->n_tiles_h * a->tile_h < a->height)
         return xsg_fail(XSG_ERR_INVALID, "%s: tile grid %dx%d of %dx%d tiles does not cover %dx%d pixels", who,
                         a->n_tiles_w, a->n_tiles_h, a->tile_w, a->tile_h, a->width, a->height);
+    if ((int64_t)a->n_cams * a->n_tiles_w * a->n_tiles_h > INT32_MAX)
+        return xsg_fail(XSG_ERR_INVALID, "%s: %d cameras x %dx%d tiles exceed the launch grid", who, a->n_cams,
+                        a->n_tiles_w, a->n_tiles_h);
     if ((int64_t)a->n_cams * a->n > INT32_MAX)
         return xsg_fail(XSG_ERR_INVALID, "%s: %d cameras x %lld Gaussians exceed the int32 flatten ids", who,
                         a->n_cams, (long long)a->n);
@@ -163,9 +260,10 @@ extern "C" int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream) {
     return XSG_OK;
 }
 
-extern "C" size_t xsg_eval3d_bwd_workspace_bytes(int64_t n, int cdim) {
-    (void)cdim;
-    return (size_t)(n > 0 ? n : 1) * 6 * sizeof(float);
+extern "C" size_t xsg_eval3d_bwd_workspace_bytes(const xsg_eval3d_args* a) {
+    if (!a) return 0;
+    const int64_t nblocks = (int64_t)std::max(a->n_cams, 0) * std::max(a->n_tiles_w, 0) * std::max(a->n_tiles_h, 0);
+    return bwd_workspace(a->n, nblocks).bytes;
 }
 
 extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_stream_t stream) {
@@ -198,6 +296,14 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
         zero_kernel<<<dim3(gx, 5), kBlock, 0, s>>>(zl);
     }
     if ((int64_t)a->width * a->height > 0) {
+        const int nblocks = a->n_cams * a->n_tiles_w * a->n_tiles_h;
+        const BwdWorkspace w = bwd_workspace(n, nblocks);
+        int32_t* work = reinterpret_cast<int32_t*>((char*)workspace + w.work_off);
+        int32_t* order = reinterpret_cast<int32_t*>((char*)workspace + w.order_off);
+        tile_work_kernel<<<(unsigned)((nblocks + kBlock / 64 - 1) / (kBlock / 64)), kBlock, 0, s>>>(
+            p.g, a->last_ids, a->tile_offsets, work);
+        tile_order_kernel<<<8, kOrderThreads, 0, s>>>(nblocks, work, order);
+        p.tile_order = order;
         rc = eval3d_bwd_launch(a->cdim, dyn, p, s);
         if (rc) return rc;
     }

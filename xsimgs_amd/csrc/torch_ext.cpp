@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/xsimgs_amd.h"
+#include "../../include/xsimgs_amd_bench.h"
 
 namespace {
 
@@ -261,7 +262,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     a.v_ray_o = o.v_ray_o.has_value() ? o.v_ray_o->data_ptr<float>() : nullptr;
     a.v_ray_d = o.v_ray_d.has_value() ? o.v_ray_d->data_ptr<float>() : nullptr;
     a.pair_counts = counts_ptr(pair_counts, points);
-    Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(a.n, cdim));
+    Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(&a));
     check_rc(xsg_eval3d_bwd(&a, ws.data_ptr(), stream_of(points)));
     return o;
 }
@@ -997,11 +998,27 @@ void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm) {
     }
 }
 
+// measurement support for bench.py: the VALU issue ceiling launch, on the current stream
+void bench_valu_ceiling(int64_t blocks, int64_t iters, const Tensor& out, const Tensor& stamps) {
+    TORCH_CHECK(blocks > 0 && blocks <= (1 << 20) && iters > 0 && iters <= (1 << 24), "valu ceiling: blocks ",
+                blocks, " / iters ", iters, " out of range");
+    check_f32(out, "out");
+    TORCH_CHECK(stamps.scalar_type() == at::kLong, "stamps must be an int64 tensor");
+    TORCH_CHECK(out.is_contiguous() && stamps.is_contiguous(), "out and stamps must be contiguous");
+    TORCH_CHECK(out.numel() >= blocks * 256 && stamps.numel() >= 4 * blocks,
+                "out needs blocks * 256 floats and stamps 4 * blocks entries");
+    check_same_device({out, stamps});
+    check_rc(xsg_bench_valu_ceiling((int)blocks, (int)iters, out.data_ptr<float>(),
+                                    reinterpret_cast<uint64_t*>(stamps.data_ptr()), stream_of(out)));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "xsimgs_amd: MI355X (gfx950) kernels for the xsimgs Gaussian-splatting hot path";
     m.def("abi_version", &xsg_abi_version);
+    m.def("bench_valu_ceiling", &bench_valu_ceiling, py::arg("blocks"), py::arg("iters"), py::arg("out"),
+          py::arg("stamps"));
 
     // rasterization (csrc/rasterization/*_bind)
     m.def("rasterize_eval3d_fwd", &rasterize_eval3d_fwd, py::arg("means"), py::arg("quats"), py::arg("scales"),

@@ -311,6 +311,8 @@ struct Eval3dParams {
     // colours [n_cams, n, CDIM], n * CDIM for one colour set [n, CDIM] that every camera shares
     int64_t col_shift;
     unsigned long long* pair_counts;  // optional: += [evaluated, composited] pixel-pairs
+    // optional (backward): logical (camera, tile) block launched at each position of xcd_tile's order
+    const int32_t* tile_order;
 };
 
 int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
