@@ -131,6 +131,17 @@ XSG_DEV void put(float& a, float v) {
     else a += v;
 }
 
+// acc = x y - z w for the first pixel; acc += x y, then acc -= z w (two FMAs) for the others
+template <bool FIRST>
+XSG_DEV void put_diff(float& a, float x, float y, float z, float w) {
+    if constexpr (FIRST) {
+        a = fmaf(x, y, -(z * w));
+    } else {
+        a = fmaf(x, y, a);
+        a = fmaf(-z, w, a);
+    }
+}
+
 // Gradient contribution of one pair into acc (eval3d_bwd.cu:206-271). A pair that is not valid
 // adds exact zeros (its alpha is 0, so fac = 0 and T / (1 - 0) = T; its gated upstream gradients
 // are selected to 0, and every gradient is linear in them) and leaves the pixel's transmittance
@@ -204,10 +215,10 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     }
     // Q (upper triangle, row-major): Q_ij = dL/dgro_i p_j - p_i k1 grd_j
     put<FIRST>(acc[CDIM + 3], pp.x * (v_gro.x - kg.x));
-    put<FIRST>(acc[CDIM + 4], v_gro.x * pp.y - pp.x * kg.y);
-    put<FIRST>(acc[CDIM + 5], v_gro.x * pp.z - pp.x * kg.z);
+    put_diff<FIRST>(acc[CDIM + 4], v_gro.x, pp.y, pp.x, kg.y);
+    put_diff<FIRST>(acc[CDIM + 5], v_gro.x, pp.z, pp.x, kg.z);
     put<FIRST>(acc[CDIM + 6], pp.y * (v_gro.y - kg.y));
-    put<FIRST>(acc[CDIM + 7], v_gro.y * pp.z - pp.y * kg.z);
+    put_diff<FIRST>(acc[CDIM + 7], v_gro.y, pp.z, pp.y, kg.z);
     put<FIRST>(acc[CDIM + 8], pp.z * (v_gro.z - kg.z));
     put<FIRST>(acc[CDIM + 9], e.vis * v_alpha_g);
     px.buf = fmaf(fac, u, px.buf);
