@@ -31,6 +31,7 @@ using namespace xsg;
 
 constexpr int kBlock = 256;
 constexpr int kExpandPerBlock = 1024;
+constexpr int kMaxLdsElev = 1024;  // lidar elevation boundaries staged in LDS by the count pass
 
 struct Rect { uint16_t x0, y0, x1, y1; };  // exclusive [x0, x1) x [y0, y1)
 
@@ -50,8 +51,27 @@ XSG_DEV Rect regular_rect(float2 m, float2 r, float tsx, float tsy, int ntx, int
     return out;
 }
 
+// First index at or after i whose boundary is not below v (n_elev if none), scanning up the table as
+// find_bounds_increasing does (phm_lidar_tiling.cu:35-60).
+XSG_DEV int elev_scan_up(const float* elev, int n_elev, int i, float v) {
+    while (i < n_elev && elev[i] < v) ++i;
+    return i;
+}
+// The same index by bisection, for a table known to be non-decreasing: the first index of [i, n_elev)
+// whose boundary is not below v. (A NaN v stops both at i.)
+XSG_DEV int elev_search_up(const float* elev, int n_elev, int i, float v) {
+    int lo = i, hi = n_elev;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (elev[mid] < v) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
 // find_bounds_increasing + tile_limits_irregular (phm_lidar_tiling.cu:35-91), inclusive bounds
-// returned as an exclusive rectangle.
+// returned as an exclusive rectangle. SORTED: the table is non-decreasing, so its two scans are done
+// by bisection with the same results.
+template <bool SORTED = false>
 XSG_DEV Rect lidar_rect(float mx, float my, float rx, float ry, float u_min, float u_max, float u_per_tile,
                         int n_elev, const float* __restrict__ elev, int ntx) {
     Rect out = {0, 0, 0, 0};
@@ -60,10 +80,9 @@ XSG_DEV Rect lidar_rect(float mx, float my, float rx, float ry, float u_min, flo
     const int x0 = (int)floorf(lo / u_per_tile);
     const int x1 = (int)ceilf(hi / u_per_tile) - 1;
     const float vmin = my - ry, vmax = my + ry;
-    int i = 0;
-    while (i < n_elev && elev[i] < vmin) ++i;
+    int i = SORTED ? elev_search_up(elev, n_elev, 0, vmin) : elev_scan_up(elev, n_elev, 0, vmin);
     const int y0 = min(max(i - 1, 0), n_elev - 1);
-    while (i < n_elev && elev[i] < vmax) ++i;
+    i = SORTED ? elev_search_up(elev, n_elev, i, vmax) : elev_scan_up(elev, n_elev, i, vmax);
     const int y1 = min(max(i - 1, 0), n_elev - 1);
     out.x0 = (uint16_t)min(x0, ntx); out.x1 = (uint16_t)min(x1 + 1, ntx);
     out.y0 = (uint16_t)y0; out.y1 = (uint16_t)(y1 + 1);
@@ -146,8 +165,26 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     uint32_t* __restrict__ seam_ids) {
     __shared__ uint64_t lds[kWaves];
     __shared__ uint32_t s_seam;
+    // lidar: the elevation table in LDS; when it is non-decreasing (as find_bounds_increasing
+    // expects) its scans become bisections (same bounds), else they scan as the reference does
+    __shared__ float s_elev[LIDAR ? kMaxLdsElev : 1];
     if (threadIdx.x == 0) s_seam = 0;
-    __syncthreads();
+    bool sorted_elev = false;
+    const float* tab = elev;
+    if constexpr (LIDAR) {
+        const bool fits = n_elev <= kMaxLdsElev;
+        if (fits) {
+            for (int i = threadIdx.x; i < n_elev; i += kBlock) s_elev[i] = elev[i];
+            tab = s_elev;
+        }
+        __syncthreads();
+        bool ok = fits;
+        if (fits)
+            for (int i = threadIdx.x; i + 1 < n_elev; i += kBlock) ok = ok && (s_elev[i] <= s_elev[i + 1]);
+        sorted_elev = __syncthreads_and(ok) != 0;  // block-uniform
+    } else {
+        __syncthreads();
+    }
     const Camera cam = load_camera(pack, KIND);
     const int lane = __lane_id();
     const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
@@ -168,8 +205,12 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
                 }
                 const float2 m = means2d[j];
                 const float mx = m.x / img.x, my = m.y / img.y, rx = r.x / img.x, ry = r.y / img.y;
-                if (LIDAR) a = lidar_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, elev, ntx);
-                else a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
+                if (LIDAR) {
+                    a = sorted_elev ? lidar_rect<true>(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, tab, ntx)
+                                    : lidar_rect<false>(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, tab, ntx);
+                } else {
+                    a = spherical_rect(mx, my, rx, ry, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
+                }
             }
             const uint32_t ca = rect_count(a);
             tpg[j] = (int32_t)ca;
@@ -458,11 +499,21 @@ constexpr int kMaxSortedCols = 8192;  // tile columns (LDS difference array of s
 constexpr int kColGroup = 4;    // columns per wavefront step in write_runs_kernel
 constexpr int kBandCols = 8;    // columns whose runs write_runs_kernel lists together (a multiple of kColGroup)
 
-// rows covered by each depth-ordered visible instance -> exclusive run offsets (reduce / scan)
+// A rectangle as two words (x0 | y0 << 16, x1 | y1 << 16), for the depth-ordered copy that
+// rows_reduce_kernel gathers once and the later passes read in order.
+XSG_DEV Rect rect_of(uint32_t lo, uint32_t hi) {
+    return Rect{(uint16_t)(lo & 0xffffu), (uint16_t)(lo >> 16), (uint16_t)(hi & 0xffffu), (uint16_t)(hi >> 16)};
+}
+
+// rows covered by each depth-ordered visible instance -> exclusive run offsets (reduce / scan).
+// rows_reduce_kernel gathers each instance's rectangle (a random read per instance) and stores it in
+// depth order (d_lo, d_hi), so that rows_scan_kernel and expand_runs_kernel read it sequentially.
 __global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
                                                              const uint32_t* __restrict__ ids,
                                                              const Rect* __restrict__ rects,
-                                                             uint32_t* __restrict__ partials) {
+                                                             uint32_t* __restrict__ partials,
+                                                             uint32_t* __restrict__ d_lo,
+                                                             uint32_t* __restrict__ d_hi) {
     __shared__ uint32_t lds[kWaves];
     m = min(m, (int64_t)*m_dev);
     uint32_t acc = 0;
@@ -471,6 +522,8 @@ __global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const ui
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
         if (p < m) {
             const Rect r = rects[ids[p]];
+            d_lo[p] = (uint32_t)r.x0 | ((uint32_t)r.y0 << 16);
+            d_hi[p] = (uint32_t)r.x1 | ((uint32_t)r.y1 << 16);
             acc += (uint32_t)(r.y1 - r.y0);
         }
     }
@@ -479,8 +532,8 @@ __global__ __launch_bounds__(kBlock) void rows_reduce_kernel(int64_t m, const ui
 }
 
 __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
-                                                           const uint32_t* __restrict__ ids,
-                                                           const Rect* __restrict__ rects,
+                                                           const uint32_t* __restrict__ d_lo,
+                                                           const uint32_t* __restrict__ d_hi,
                                                            const uint32_t* __restrict__ partials,
                                                            const uint32_t* __restrict__ slice_sum,
                                                            uint32_t* __restrict__ roff) {
@@ -494,10 +547,7 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
         if (base + (int64_t)k * kBlock >= m) break;
         const int64_t p = base + (int64_t)k * kBlock + threadIdx.x;
         uint32_t h = 0;
-        if (p < m) {
-            const Rect r = rects[ids[p]];
-            h = (uint32_t)(r.y1 - r.y0);
-        }
+        if (p < m) h = (d_hi[p] >> 16) - (d_lo[p] >> 16);
         uint32_t tot;
         const uint32_t ex = block_exclusive_scan<uint32_t>(h, lds, tot);
         if (p < m) roff[p] = carry + ex;
@@ -514,7 +564,8 @@ static_assert(kExpandPerBlock == kSortBlock * 4, "an expansion block is one tile
 __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, const uint32_t* __restrict__ roff,
                                                              const uint32_t* __restrict__ ids,
                                                              const uint32_t* __restrict__ keys, int64_t m,
-                                                             const Rect* __restrict__ rects, int nty,
+                                                             const uint32_t* __restrict__ d_lo,
+                                                             const uint32_t* __restrict__ d_hi, int nty,
                                                              int64_t n_per_cam, int spans, uint32_t neg_row,
                                                              uint32_t* __restrict__ out_row,
                                                              uint4* __restrict__ out_rec,
@@ -547,7 +598,7 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
         const uint32_t inst = v / (uint32_t)spans;
         const uint32_t cid = n_per_cam > 0 ? (uint32_t)(inst / (uint64_t)n_per_cam) : 0u;
         const uint32_t key = keys[p];
-        const Rect r = rects[v];
+        const Rect r = rect_of(d_lo[p], d_hi[p]);
         s_off[e] = roff[p];
         s_row[e] = ((int32_t)key < 0) ? neg_row : cid * (uint32_t)nty + r.y0;
         s_fid[e] = inst;
@@ -609,12 +660,21 @@ __global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __
     uint32_t tot;
     uint32_t run = block_exclusive_scan<uint32_t>(sum, lds, tot);
     for (int r = r0; r < r1; ++r) {
-        const uint32_t ns = (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
         seg_base[r] = run;
-        for (uint32_t k = 0; k < ns; ++k) seg_row[run + k] = (uint32_t)r;
-        run += ns;
+        run += (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
     }
     if (threadIdx.x == 0) seg_base[n_real] = tot;
+    __syncthreads();  // seg_base is complete (global stores of this block, read back below)
+    // every thread a share of the segments: its row is the last r with seg_base[r] <= segment (rows
+    // without segments share a base with the next row, and the search takes the later one)
+    for (uint32_t sg = threadIdx.x; sg < tot; sg += kBlock) {
+        int lo = 0, hi = n_real - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (seg_base[mid] <= sg) lo = mid; else hi = mid - 1;
+        }
+        seg_row[sg] = (uint32_t)lo;
+    }
 }
 
 // One workgroup per segment: how many of its runs cover each column, from a difference array in
@@ -1154,9 +1214,11 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems>(
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
             PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev, false, kPresortGrid);
-        rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart);
+        // the depth-ordered rectangles go to the pre-order's ping-pong buffers (free after its four passes)
+        rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.alt_key,
+                                                   w.alt_id);
         slice_scan_kernel<uint32_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.rpart, w.slice32, nullptr, nullptr);
-        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.slice32,
+        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.alt_key, w.alt_id, w.rpart, w.slice32,
                                                  w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
@@ -1232,7 +1294,8 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     const uint32_t neg_row = (uint32_t)(fw.n_rows - 1);
     const int n_real = fw.n_rows - 1;
     const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
-    expand_runs_kernel<<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.rects, g.nty,
+    expand_runs_kernel<<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.alt_key,
+                                                  cw.alt_id, g.nty,
                                                   n_per_cam, g.spans, neg_row, fw.row_a, fw.rec_a, fw.hist, nb_runs);
     int row_bits = 1;
     while ((1u << row_bits) <= neg_row) ++row_bits;
