@@ -32,6 +32,7 @@ using namespace xsg;
 constexpr int kBlock = 256;
 constexpr int kExpandPerBlock = 1024;
 constexpr int kMaxLdsElev = 1024;  // lidar elevation boundaries staged in LDS by the count pass
+constexpr int kMaxLdsRows = 8192;  // row buckets whose segment bases row_segments_kernel searches in LDS
 
 struct Rect { uint16_t x0, y0, x1, y1; };  // exclusive [x0, x1) x [y0, y1)
 
@@ -624,13 +625,23 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
     hist[(int64_t)threadIdx.x * nb + blockIdx.x] = s_hist[threadIdx.x];
 }
 
-// single block: row_start[r] = first sorted run of row bucket r (r in [0, n_rows]), then segments
-// of kRunSeg runs per real row: seg_base = exclusive prefix of the segment counts (total at
-// seg_base[n_real]) and seg_row[s] = row of segment s. When the row sort was a single pass,
-// `row_count` holds its digit totals -- the runs per row bucket -- and row_start is their exclusive
-// scan; otherwise it is a lower-bound search of the sorted row buckets.
-__global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __restrict__ rows, int64_t n_runs,
-                                                              int n_rows, const uint32_t* __restrict__ row_count,
+// row_start[r] = first sorted run of row bucket r (r in [0, n_rows]) from the sorted row buckets, one
+// thread per boundary between runs i - 1 and i: it starts the rows (rows[i - 1], rows[i]] (from row 0
+// before the first run, to n_rows after the last), so every row is written once.
+__global__ __launch_bounds__(kBlock) void row_start_kernel(const uint32_t* __restrict__ rows, int64_t n_runs,
+                                                           int n_rows, uint32_t* __restrict__ row_start) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i > n_runs) return;
+    const int lo = i == 0 ? 0 : (int)rows[i - 1] + 1;
+    const int hi = i == n_runs ? n_rows : min((int)rows[i], n_rows);
+    for (int r = lo; r <= hi; ++r) row_start[r] = (uint32_t)i;
+}
+
+// single block: segments of kRunSeg runs per real row: seg_base = exclusive prefix of the segment
+// counts (total at seg_base[n_real]) and seg_row[s] = row of segment s. When the row sort was a
+// single pass, `row_count` holds its digit totals -- the runs per row bucket -- and row_start is
+// their exclusive scan, written here; otherwise row_start_kernel has written row_start.
+__global__ __launch_bounds__(kBlock) void row_segments_kernel(int n_rows, const uint32_t* __restrict__ row_count,
                                                               uint32_t* __restrict__ row_start,
                                                               uint32_t* __restrict__ seg_base,
                                                               uint32_t* __restrict__ seg_row) {
@@ -641,15 +652,6 @@ __global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __
         const uint32_t ex = block_exclusive_scan<uint32_t>(c, lds, tot);
         if ((int)threadIdx.x < n_rows) row_start[threadIdx.x] = ex;
         if (threadIdx.x == 0) row_start[n_rows] = tot;
-    } else {
-        for (int r = threadIdx.x; r <= n_rows; r += kBlock) {
-            int64_t lo = 0, hi = n_runs;
-            while (lo < hi) {
-                const int64_t mid = (lo + hi) >> 1;
-                if (rows[mid] < (uint32_t)r) lo = mid + 1; else hi = mid;
-            }
-            row_start[r] = (uint32_t)lo;
-        }
     }
     __syncthreads();
     const int n_real = n_rows - 1;
@@ -659,19 +661,24 @@ __global__ __launch_bounds__(kBlock) void row_segments_kernel(const uint32_t* __
     for (int r = r0; r < r1; ++r) sum += (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
     uint32_t tot;
     uint32_t run = block_exclusive_scan<uint32_t>(sum, lds, tot);
+    // the bases also go to LDS when they fit, for the searches below
+    __shared__ uint32_t s_base[kMaxLdsRows];
+    const bool in_lds = n_real <= kMaxLdsRows;  // block-uniform
     for (int r = r0; r < r1; ++r) {
         seg_base[r] = run;
+        if (in_lds) s_base[r] = run;
         run += (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
     }
     if (threadIdx.x == 0) seg_base[n_real] = tot;
-    __syncthreads();  // seg_base is complete (global stores of this block, read back below)
     // every thread a share of the segments: its row is the last r with seg_base[r] <= segment (rows
     // without segments share a base with the next row, and the search takes the later one)
+    __syncthreads();  // s_base, and the global seg_base of this block, are complete
+    const uint32_t* base = in_lds ? s_base : seg_base;
     for (uint32_t sg = threadIdx.x; sg < tot; sg += kBlock) {
         int lo = 0, hi = n_real - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (seg_base[mid] <= sg) lo = mid; else hi = mid - 1;
+            if (base[mid] <= sg) lo = mid; else hi = mid - 1;
         }
         seg_row[sg] = (uint32_t)lo;
     }
@@ -1308,8 +1315,11 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
         fw.row_a, fw.rec_a, fw.row_b, fw.rec_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
         PlainOut<uint32_t, uint4>{rows_sorted, odd ? fw.rec_b : fw.rec_a}, s, nullptr,
         /*first_hist_ready=*/true);
-    row_segments_kernel<<<1, kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows, row_bits <= 8 ? fw.dtot : nullptr,
-                                             fw.row_start, fw.seg_base, fw.seg_row);
+    if (row_bits > 8)
+        row_start_kernel<<<xsg_blocks(n_runs + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
+                                                                         fw.row_start);
+    row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, row_bits <= 8 ? fw.dtot : nullptr, fw.row_start,
+                                             fw.seg_base, fw.seg_row);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals
     seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
