@@ -203,3 +203,41 @@ def test_hip_path_reproduces_fixture(dev, name):
     assert len(grads) == len(keys)
     for k, g in zip(keys, grads):
         _check(k, g, f["g_" + k], GRAD_ATOL, GRAD_RTOL, 0.999)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("table", ["unsorted", "long"])
+def test_lidar_elevation_tables(dev, table):
+    """The lidar count pass finds each Gaussian's elevation rows as find_bounds_increasing scans them
+    (phm_lidar_tiling.cu:35-60): by bisection when the table is non-decreasing and fits in LDS (the
+    golden lidar scene and cfg3 take that path), else by the same linear scan. Two boundaries swapped
+    (not non-decreasing) and a table of 1100 boundaries (more than the 1024 kept in LDS) take the scan;
+    both must bin as the oracle does with the same table."""
+    from xsimgs_amd import _C, frame
+    print("elevation table", table, flush=True)
+    spec, f = load("lidar_phm")
+    W, H = spec.width, spec.height
+    tsx, tsy = (int(x) for x in f["tile"])
+    elev = f["elev"].astype(np.float32).copy()
+    if table == "unsorted":
+        k = elev.size // 2
+        elev[k], elev[k + 1] = elev[k + 1], elev[k]
+        assert np.any(np.diff(elev) < 0)
+    else:
+        x = np.linspace(0.0, elev.size - 1.0, 1100)
+        elev = np.interp(x, np.arange(elev.size), elev.astype(np.float64)).astype(np.float32)
+        assert elev.size > 1024 and np.all(np.diff(elev) >= 0)
+    T = lambda k: _t(f[k], dev) if k in f else None
+    cam = frame.make_camera(spec, dev)
+    vel_np = f.get("velocity")
+    tpg, ids, fl = _C.isect_lidar_tiles(cam.pack, T("means"), T("velocity"), T("scales"), T("quats"), T("opacity"),
+                                        T("ut_flags"), T("means2d"), T("radii"), T("depths"), _t(elev, dev), tsx, W,
+                                        H)
+    args = (spec.kind, spec, f["means"], f["scales"], f["quats"], f["opacity"], f["ut_flags"], f["means2d"],
+            f["radii"], f["depths"], tsx, tsy, W, H)
+    ref = O.isect_spherical_family(*args, elev=elev, vel=vel_np)
+    und = O.isect_spherical_family(*args, elev=elev, vel=vel_np, seam_margins=True) < 1.0
+    ntw = (W + tsx - 1) // tsx
+    fs = lambda g, t: J.first_span_member(spec.kind, spec, g, t, f["means2d"], f["radii"], W, H, tsx, tsy, elev)
+    J.check_binning(spec.kind, (np_(tpg), np_(ids), np_(fl)), ref, f["ut_flags"], f["depths"], ntw * elev.size,
+                    f"lidar_phm {table} elevation table", und, fs)
