@@ -31,6 +31,9 @@ using namespace xsg;
 
 constexpr int kBlock = 256;
 constexpr int kExpandPerBlock = 1024;
+// keys per thread of the run sort (one or two passes over the row runs); an expansion block writes
+// exactly one tile of it, with that tile's first-digit histogram
+constexpr int kRunSortItems = 4;
 constexpr int kMaxLdsElev = 1024;  // lidar elevation boundaries staged in LDS by the count pass
 constexpr int kMaxLdsRows = 8192;  // row buckets whose segment bases row_segments_kernel searches in LDS
 
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
 // which the row sort then carries. A block writes one tile of the run sort (kExpandPerBlock runs),
 // so it also stores the tile's histogram of the sort's first digit (the low 8 bits of the row
 // bucket) into hist, digit-major as radix_upsweep would.
-static_assert(kExpandPerBlock == kSortBlock * 4, "an expansion block is one tile of the run sort");
+static_assert(kExpandPerBlock == kSortBlock * kRunSortItems, "an expansion block is one tile of the run sort");
 __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, const uint32_t* __restrict__ roff,
                                                              const uint32_t* __restrict__ ids,
                                                              const uint32_t* __restrict__ keys, int64_t m,
@@ -1013,7 +1016,6 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // The depth pre-order sorts the visible instances, usually a small part of the instances its grid
 // is sized for: 1024 keys per block spread them over four times as many workgroups.
 constexpr int kPresortItems = 4;
-constexpr int kRunSortItems = 4;  // the run sort (one pass over about a million runs) likewise
 constexpr unsigned kPresortGrid = 2048;
 
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
