@@ -197,6 +197,14 @@ def binning_alg_bytes(kind, n, n_isects, n_tiles, n_flag2=0):
     return per_g * n + 12 * n_isects + 4 * n_tiles + 44 * n_flag2
 
 
+def sh_bwd_alg_bytes(K, n, v_colors):
+    """The SH backward's unavoidable bytes: every Gaussian's position and colour gradient read (24),
+    its position gradient (12) and coefficient gradients (12 K) written; the coefficients (12 K) read
+    only for a Gaussian whose colour gradient is not zero (for the others every output is zero)."""
+    n_need = int((v_colors != 0).any(dim=-1).sum())
+    return (36 + 12 * K) * n + 12 * K * n_need
+
+
 def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extensions=False):
     import xsimgs_amd  # noqa: F401  (fails loudly without the native libraries)
     from xsimgs_amd import _C, frame, synthetic
@@ -356,7 +364,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 v_colors = c0["v_colors"]
                 stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh, None,
                                                                              False, v_colors, None),
-                                    (36 + 24 * K) * N)
+                                    sh_bwd_alg_bytes(K, N, v_colors))
         per_frame = {"sh_fwd", "sh_bwd"}   # one call per frame: the scenes with SH have one camera or a rig
         if rig:
             # the batched stages over every camera of the rig; their bytes are the cameras' sum
@@ -393,7 +401,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                                                               ray_grads=False)[4]
                     stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh,
                                                                                  None, False, v_col_b, None),
-                                        (36 + 24 * K) * N)
+                                        sh_bwd_alg_bytes(K, N, v_col_b))
         stages = {k: v for k, v in stages.items() if v is not None}
         timed_stages = stages
         if args.profile_stages:

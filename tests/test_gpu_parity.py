@@ -28,10 +28,15 @@ def cfg0(dev):
 
 
 # ------------------------------------------------------------------ SH
-@pytest.mark.parametrize("degree,layout_3kn,with_dc,with_mask", [
-    (0, False, False, False), (3, False, False, False), (3, True, False, False), (3, False, True, True),
-    (4, True, True, False), (2, False, False, True), (1, True, False, True)])
-def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask):
+@pytest.mark.parametrize("degree,layout_3kn,with_dc,with_mask,sparse", [
+    (0, False, False, False, False), (3, False, False, False, False), (3, True, False, False, False),
+    (3, False, True, True, False), (4, True, True, False, False), (2, False, False, True, False),
+    (1, True, False, True, False), (3, False, False, False, True), (3, True, False, False, True),
+    (4, False, True, True, True)])
+def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask, sparse):
+    """sparse: the colour gradient is zero for most Gaussians (those no tile composited), as in a
+    frame; the backward then reads coefficients only for the rows that need them, except in blocks
+    of 256 Gaussians where most do (here: the first block dense, the second at about a third)."""
     g = torch.Generator().manual_seed(7 + degree)
     n = 3001
     K = (degree + 1) ** 2 + 2            # extra unused bands must come back zero in d_coeffs
@@ -42,6 +47,12 @@ def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask):
     dc = (torch.randn(3, n, generator=g) if layout_3kn else torch.randn(n, 3, generator=g)) if with_dc else None
     mask = torch.randint(-2**31, 2**31 - 1, ((n + 31) // 32,), generator=g, dtype=torch.int32) if with_mask else None
     d_out = torch.randn(n, 3, generator=g)
+    if sparse:
+        keep = torch.rand(n, generator=g) < 0.12
+        keep[:256] = True
+        keep[256:512] = torch.rand(256, generator=g) < 0.35
+        d_out[~keep] = 0.0
+        d_out[keep.nonzero()[::7, 0], 1:] = 0.0   # a gradient zero in some channels only still needs them
     D = lambda t: None if t is None else t.to(dev)
     out = _C.spherical_harmonics_fused_fwd(degree, D(origin), D(pos), D(coeffs), D(mask), layout_3kn, D(dc))
     m_np = None if mask is None else mask.numpy().view(np.uint32)

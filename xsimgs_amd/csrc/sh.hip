@@ -275,38 +275,53 @@ __global__ __launch_bounds__(kBlock) void sh_bwd_kernel(
     const int rows = (int)min<int64_t>(kBlock, n - g0);
     const int t = threadIdx.x;
     const int64_t i = g0 + t;
+    const bool active = t < rows;
+    const bool valid = active && mask_ok(mask, i);
+    float go[3] = {0.f, 0.f, 0.f};
+    if (valid) { go[0] = d_out[3 * i]; go[1] = d_out[3 * i + 1]; go[2] = d_out[3 * i + 2]; }
+    // The coefficients enter only the position gradient, through their product with the colour
+    // gradient: a Gaussian whose colour gradient is exactly zero (one no tile composited) gets an
+    // exactly zero position gradient without reading them (the reference multiplies them by zero;
+    // the results differ at most in the sign of a zero, or where a coefficient is not finite). A
+    // block whose rows mostly need them stages them all with wide loads; a sparse block reads only
+    // the rows that need them.
+    const bool need = valid && (go[0] != 0.f || go[1] != 0.f || go[2] != 0.f);
+    bool staged = L3KN;
     if constexpr (!L3KN && NB > 0) {
-        stage_rows<RL, S>(lds, coeffs + g0 * dim * 3, (int64_t)dim * 3, rows);
-        __syncthreads();
+        staged = 4 * __syncthreads_count(need) > rows;  // block-uniform
+        if (staged) {
+            stage_rows<RL, S>(lds, coeffs + g0 * dim * 3, (int64_t)dim * 3, rows);
+            __syncthreads();
+        }
     }
     f3 dpos = mk3(0.f, 0.f, 0.f);
     float Y[NY];
-    float go[3] = {0.f, 0.f, 0.f};
-    const bool active = t < rows;
-    const bool valid = active && mask_ok(mask, i);
     if (valid) {
         const f3 diff = ld3(pos + 3 * i) - ld3(origin);
         const float il = 1.0f / sqrtf(dot(diff, diff));
         const f3 dir = diff * il;
         sh_basis<DEG>(dir, Y);
-        go[0] = d_out[3 * i]; go[1] = d_out[3 * i + 1]; go[2] = d_out[3 * i + 2];
-        float g[NY];
+        if (need) {
+            const float* row = coeffs + i * dim * 3;  // [N, K, 3] layout, read directly when not staged
+            float g[NY];
 #pragma unroll
-        for (int k = 0; k < NY; ++k) {
-            float s = 0.f;
+            for (int k = 0; k < NY; ++k) {
+                float s = 0.f;
 #pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                float cv;
-                if (HAS_DC && k == 0) cv = 0.f;  // the DC band has no direction dependence
-                else if constexpr (L3KN) cv = coeffs[((int64_t)c * dim + (k - (HAS_DC ? 1 : 0))) * n + i];
-                else cv = lds[t * S + (k - (HAS_DC ? 1 : 0)) * 3 + c];
-                s += cv * go[c];
+                for (int c = 0; c < 3; ++c) {
+                    float cv;
+                    const int kb = k - (HAS_DC ? 1 : 0);
+                    if (HAS_DC && k == 0) cv = 0.f;  // the DC band has no direction dependence
+                    else if constexpr (L3KN) cv = coeffs[((int64_t)c * dim + kb) * n + i];
+                    else cv = staged ? lds[t * S + kb * 3 + c] : row[kb * 3 + c];
+                    s += cv * go[c];
+                }
+                g[k] = s;
             }
-            g[k] = s;
+            const f3 ddir = sh_dir_grad<DEG>(dir, g);
+            // normalize_bwd: (d - (d . n) n) / |v|
+            dpos = ddir * il - diff * (il * il * il * dot(ddir, diff));
         }
-        const f3 ddir = sh_dir_grad<DEG>(dir, g);
-        // normalize_bwd: (d - (d . n) n) / |v|
-        dpos = ddir * il - diff * (il * il * il * dot(ddir, diff));
     } else {
 #pragma unroll
         for (int k = 0; k < NY; ++k) Y[k] = 0.f;
