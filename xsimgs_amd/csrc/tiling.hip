@@ -34,6 +34,9 @@ constexpr int kExpandPerBlock = 1024;
 // keys per thread of the run sort (one or two passes over the row runs); an expansion block writes
 // exactly one tile of it, with that tile's first-digit histogram
 constexpr int kRunSortItems = 4;
+// Digit width of the run sort: one pass of 8, 9 or 10 bits for up to 1024 row buckets (a rig of several
+// cameras), 8-bit passes beyond.
+inline int run_sort_rb(int row_bits) { return row_bits <= 8 ? 8 : row_bits <= 10 ? row_bits : 8; }
 constexpr int kMaxLdsElev = 1024;  // lidar elevation boundaries staged in LDS by the count pass
 constexpr int kMaxLdsRows = 8192;  // row buckets whose segment bases row_segments_kernel searches in LDS
 
@@ -562,9 +565,10 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
 // Merge-path expansion of the depth-ordered instances into row runs: run r gets its row bucket
 // and its record for the writers (flatten id, depth bits, column range x0 | x1 << 16, row bucket),
 // which the row sort then carries. A block writes one tile of the run sort (kExpandPerBlock runs),
-// so it also stores the tile's histogram of the sort's first digit (the low 8 bits of the row
+// so it also stores the tile's histogram of the sort's first digit (the low RB bits of the row
 // bucket) into hist, digit-major as radix_upsweep would.
 static_assert(kExpandPerBlock == kSortBlock * kRunSortItems, "an expansion block is one tile of the run sort");
+template <int RB>
 __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, const uint32_t* __restrict__ roff,
                                                              const uint32_t* __restrict__ ids,
                                                              const uint32_t* __restrict__ keys, int64_t m,
@@ -579,9 +583,10 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
     __shared__ uint32_t s_fid[kExpandPerBlock];
     __shared__ uint32_t s_key[kExpandPerBlock];
     __shared__ uint32_t s_cols[kExpandPerBlock];
-    __shared__ uint32_t s_hist[kRadix];
+    constexpr int R = 1 << RB;
+    __shared__ uint32_t s_hist[R];
     __shared__ int64_t s_range[2];
-    s_hist[threadIdx.x] = 0;
+    for (int d = threadIdx.x; d < R; d += kBlock) s_hist[d] = 0;
     const int64_t o0 = (int64_t)blockIdx.x * kExpandPerBlock;
     const int64_t o_end = min(n_runs, o0 + kExpandPerBlock);
     if (threadIdx.x < 2) {
@@ -622,10 +627,10 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
         const uint32_t row = row0 == neg_row ? neg_row : row0 + (uint32_t)(o - (int64_t)s_off[lo]);
         out_row[o] = row;
         out_rec[o] = make_uint4(s_fid[lo], s_key[lo], s_cols[lo], row);
-        atomicAdd(&s_hist[row & (kRadix - 1)], 1u);
+        atomicAdd(&s_hist[row & (R - 1)], 1u);
     }
     __syncthreads();
-    hist[(int64_t)threadIdx.x * nb + blockIdx.x] = s_hist[threadIdx.x];
+    for (int d = threadIdx.x; d < R; d += kBlock) hist[(int64_t)d * nb + blockIdx.x] = s_hist[d];
 }
 
 // row_start[r] = first sorted run of row bucket r (r in [0, n_rows]) from the sorted row buckets, one
@@ -649,11 +654,17 @@ __global__ __launch_bounds__(kBlock) void row_segments_kernel(int n_rows, const 
                                                               uint32_t* __restrict__ seg_base,
                                                               uint32_t* __restrict__ seg_row) {
     __shared__ uint32_t lds[kWaves];
-    if (row_count) {  // n_rows < kRadix == kBlock
-        const uint32_t c = (int)threadIdx.x < n_rows ? row_count[threadIdx.x] : 0u;
+    if (row_count) {  // the single pass's digit totals: n_rows <= 1 << RB (at most 1024)
+        const int per = (n_rows + kBlock - 1) / kBlock;  // consecutive rows per thread
+        const int q0 = threadIdx.x * per, q1 = min(n_rows, q0 + per);
+        uint32_t c = 0;
+        for (int r = q0; r < q1; ++r) c += row_count[r];
         uint32_t tot;
-        const uint32_t ex = block_exclusive_scan<uint32_t>(c, lds, tot);
-        if ((int)threadIdx.x < n_rows) row_start[threadIdx.x] = ex;
+        uint32_t run = block_exclusive_scan<uint32_t>(c, lds, tot);
+        for (int r = q0; r < q1; ++r) {
+            row_start[r] = run;
+            run += row_count[r];
+        }
         if (threadIdx.x == 0) row_start[n_rows] = tot;
     }
     __syncthreads();
@@ -1073,6 +1084,7 @@ struct FillWs {
     uint32_t* slots; uint32_t* tile_tot;
     uint32_t* hist; uint32_t* dtot;
     int n_rows;                                     // row buckets incl. the negative one
+    int row_bits, rb, passes;                       // row bucket bits, run sort digit width and passes
     int64_t s_max;                                  // segment bound
     int64_t n_slots;
     size_t bytes;
@@ -1083,6 +1095,10 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     FillWs w{};
     size_t off = 0;
     w.n_rows = g.n_cams * g.nty + 1;
+    w.row_bits = 1;
+    while ((1u << w.row_bits) <= (uint32_t)(w.n_rows - 1)) ++w.row_bits;
+    w.rb = run_sort_rb(w.row_bits);
+    w.passes = (w.row_bits + w.rb - 1) / w.rb;
     w.s_max = n_runs / kRunSeg + w.n_rows;
     w.n_slots = w.s_max * g.ntx;
     const unsigned nb_r = sort_blocks<kRunSortItems>(n_runs > 0 ? n_runs : 1);
@@ -1096,10 +1112,25 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     w.seg_row = (uint32_t*)take(4 * (size_t)w.s_max);
     w.slots = (uint32_t*)take(4 * (size_t)w.n_slots);
     w.tile_tot = (uint32_t*)take(4 * ((size_t)(w.n_rows - 1) * g.ntx + 1));
-    w.hist = (uint32_t*)take(4 * (size_t)kRadix * nb_r);
-    w.dtot = (uint32_t*)take(4 * kRadix);
+    w.hist = (uint32_t*)take(4 * ((size_t)1 << w.rb) * nb_r);
+    w.dtot = (uint32_t*)take(4 * ((size_t)1 << w.rb));
     w.bytes = off;
     return w;
+}
+
+// The runs' expansion (which stores the first digit's per-tile histogram) and their stable sort by
+// row bucket, RB bits per pass; the result ends in (out_row, out_rec), the b buffers for an odd
+// number of passes.
+template <int RB>
+void expand_and_sort_runs(const FillWs& fw, const CountWs& cw, int64_t n_runs, int64_t m, int nty, int64_t n_per_cam,
+                          int spans, uint32_t neg_row, uint32_t* out_row, uint4* out_rec, hipStream_t s) {
+    const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
+    expand_runs_kernel<RB><<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.alt_key,
+                                                      cw.alt_id, nty, n_per_cam, spans, neg_row, fw.row_a, fw.rec_a,
+                                                      fw.hist, nb_runs);
+    radix_sort_passes<uint32_t, uint4, PlainOut<uint32_t, uint4>, kRunSortItems, RB>(
+        fw.row_a, fw.rec_a, fw.row_b, fw.rec_b, n_runs, 0, fw.row_bits, fw.hist, fw.dtot,
+        PlainOut<uint32_t, uint4>{out_row, out_rec}, s, nullptr, /*first_hist_ready=*/true);
 }
 
 }  // namespace
@@ -1302,25 +1333,24 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     const FillWs fw = fill_ws_layout(g, n_runs, fill_workspace);
     const uint32_t neg_row = (uint32_t)(fw.n_rows - 1);
     const int n_real = fw.n_rows - 1;
-    const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
-    expand_runs_kernel<<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.alt_key,
-                                                  cw.alt_id, g.nty,
-                                                  n_per_cam, g.spans, neg_row, fw.row_a, fw.rec_a, fw.hist, nb_runs);
-    int row_bits = 1;
-    while ((1u << row_bits) <= neg_row) ++row_bits;
     // stable sort of the runs (row bucket, record) by row bucket, ping-ponging between the a and b
     // buffers: an odd number of passes ends in b
-    const bool odd = ((row_bits + 7) / 8) % 2 == 1;
+    const bool odd = fw.passes % 2 == 1;
     uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
-    const uint4* rec = odd ? fw.rec_b : fw.rec_a;
-    radix_sort_passes<uint32_t, uint4, PlainOut<uint32_t, uint4>, kRunSortItems>(
-        fw.row_a, fw.rec_a, fw.row_b, fw.rec_b, n_runs, 0, row_bits, fw.hist, fw.dtot,
-        PlainOut<uint32_t, uint4>{rows_sorted, odd ? fw.rec_b : fw.rec_a}, s, nullptr,
-        /*first_hist_ready=*/true);
-    if (row_bits > 8)
+    uint4* rec_sorted = odd ? fw.rec_b : fw.rec_a;
+    const uint4* rec = rec_sorted;
+    switch (fw.rb) {
+        case 9: expand_and_sort_runs<9>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
+                                        rec_sorted, s); break;
+        case 10: expand_and_sort_runs<10>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
+                                          rec_sorted, s); break;
+        default: expand_and_sort_runs<8>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
+                                         rec_sorted, s); break;
+    }
+    if (fw.passes > 1)
         row_start_kernel<<<xsg_blocks(n_runs + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
                                                                          fw.row_start);
-    row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, row_bits <= 8 ? fw.dtot : nullptr, fw.row_start,
+    row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, fw.passes == 1 ? fw.dtot : nullptr, fw.row_start,
                                              fw.seg_base, fw.seg_row);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals

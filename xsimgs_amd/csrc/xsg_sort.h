@@ -74,18 +74,24 @@ XSG_DEV unsigned active_tiles(int64_t n, const uint32_t* n_dev) {
     return (unsigned)((n + kSortBlock * ITEMS - 1) / (kSortBlock * ITEMS));
 }
 
-template <typename K, int ITEMS = kSortItems>
+// RB: bits per digit (8 by default; up to 10 for a single pass over a wider key, the digit-indexed
+// arrays then holding 1 << RB entries, R / kSortBlock per thread).
+template <typename K, int ITEMS = kSortItems, int RB = 8>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict__ keys, int64_t n, int shift,
                                                             int bits, uint32_t* __restrict__ hist, unsigned nb,
                                                             const uint32_t* __restrict__ n_dev) {
+    constexpr int R = 1 << RB, DPT = R / kSortBlock;
+    static_assert(DPT >= 1 && DPT * kSortBlock == R, "a digit count that is a multiple of the block");
     if (n_dev) n = min(n, (int64_t)*n_dev);
     const unsigned nt = active_tiles<ITEMS>(n, nullptr);
-    __shared__ uint32_t cnt[kWaves][kRadix];
+    __shared__ uint32_t cnt[kWaves][R];
     const int t = threadIdx.x, wave = t >> 6;
     for (unsigned tile = blockIdx.x; tile < nt; tile += gridDim.x) {
         __syncthreads();  // the previous tile's sums are read
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) cnt[w][t] = 0;
+        for (int w = 0; w < kWaves; ++w)
+#pragma unroll
+            for (int j = 0; j < DPT; ++j) cnt[w][j * kSortBlock + t] = 0;
         __syncthreads();
         const int64_t base = (int64_t)tile * (kSortBlock * ITEMS);
 #pragma unroll 4
@@ -94,10 +100,14 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict_
             if (idx < n) atomicAdd(&cnt[wave][digit_of<K>(keys[idx], shift, bits)], 1u);
         }
         __syncthreads();
-        uint32_t s = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) s += cnt[w][t];
-        hist[(int64_t)t * nb + tile] = s;
+        for (int j = 0; j < DPT; ++j) {
+            const int d = j * kSortBlock + t;
+            uint32_t s = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) s += cnt[w][d];
+            hist[(int64_t)d * nb + tile] = s;
+        }
     }
 }
 
@@ -136,7 +146,7 @@ struct PlainOut {
 // across steps. The block then combines the four waves' counts, reorders its keys by digit in
 // LDS and writes them out so that consecutive lanes store consecutive addresses of a digit's run.
 // Segments, steps and lanes are visited in input order, so the pass is stable.
-template <typename K, typename V, typename Out, int ITEMS = kSortItems>
+template <typename K, typename V, typename Out, int ITEMS = kSortItems, int RB = 8>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restrict__ keys_in,
                                                               const V* __restrict__ vals_in, int64_t n,
                                                               int shift, int bits,
@@ -145,29 +155,39 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
                                                               unsigned nb, Out out,
                                                               const uint32_t* __restrict__ n_dev) {
     if (n_dev) n = min(n, (int64_t)*n_dev);
+    constexpr int R = 1 << RB, DPT = R / kSortBlock;  // thread t owns digits t * DPT .. t * DPT + DPT - 1
     constexpr int kTile = kSortBlock * ITEMS;
     constexpr int kSeg = kTile / kWaves;  // keys per wave
     constexpr int kSteps = kSeg / 64;
-    __shared__ uint32_t wcnt[kWaves][kRadix];
-    __shared__ uint32_t gbase[kRadix];
-    __shared__ uint32_t lpre[kRadix];
+    __shared__ uint32_t wcnt[kWaves][R];
+    __shared__ uint32_t gbase[R];
+    __shared__ uint32_t lpre[R];
     __shared__ uint32_t scan_lds[kWaves];
     __shared__ K skeys[kTile];
     __shared__ V svals[kTile];
     const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
     const unsigned nt = active_tiles<ITEMS>(n, nullptr);
-    uint32_t dprefix;
+    uint32_t dprefix[DPT];  // first output position of each of the thread's digits
     {
+        uint32_t loc[DPT], s = 0;
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) { loc[j] = s; s += digit_total[t * DPT + j]; }
         uint32_t tot;
-        dprefix = block_exclusive_scan<uint32_t>(digit_total[t], scan_lds, tot);
+        const uint32_t ex = block_exclusive_scan<uint32_t>(s, scan_lds, tot);
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) dprefix[j] = ex + loc[j];
     }
     for (unsigned tile = blockIdx.x; tile < nt; tile += gridDim.x) {
         __syncthreads();  // the previous tile's LDS contents are consumed
         const int64_t tile0 = (int64_t)tile * kTile;
         const int n_tile = (int)min<int64_t>(kTile, n - tile0);
-        gbase[t] = dprefix + hist[(int64_t)t * nb + tile];
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) wcnt[w][t] = 0;
+        for (int j = 0; j < DPT; ++j) {
+            const int d = t * DPT + j;
+            gbase[d] = dprefix[j] + hist[(int64_t)d * nb + tile];
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
+        }
         __syncthreads();
         const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
         K key[kSteps];
@@ -198,11 +218,20 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
         }
         __syncthreads();
         {  // per digit: exclusive prefix over the waves, block-local exclusive prefix over digits
-            uint32_t c[kWaves], s = 0;
+            uint32_t loc[DPT], s = 0;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) { c[w] = wcnt[w][t]; wcnt[w][t] = s; s += c[w]; }
+            for (int j = 0; j < DPT; ++j) {
+                const int d = t * DPT + j;
+                uint32_t sd = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) { const uint32_t c = wcnt[w][d]; wcnt[w][d] = sd; sd += c; }
+                loc[j] = s;
+                s += sd;
+            }
             uint32_t tot;
-            lpre[t] = block_exclusive_scan<uint32_t>(s, scan_lds, tot);
+            const uint32_t ex = block_exclusive_scan<uint32_t>(s, scan_lds, tot);
+#pragma unroll
+            for (int j = 0; j < DPT; ++j) lpre[t * DPT + j] = ex + loc[j];
         }
         __syncthreads();
 #pragma unroll
@@ -224,17 +253,17 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
     }
 }
 
-// Runs every pass of a stable LSD sort over bits [begin_bit, end_bit) (8-bit digits, last one
+// Runs every pass of a stable LSD sort over bits [begin_bit, end_bit) (RB-bit digits, last one
 // narrower) ping-ponging between (k0, v0) and (k1, v1); the last pass goes through `final_out`.
-// Returns the number of passes. hist must hold kRadix * sort_blocks<ITEMS>(n) words, dtot kRadix
-// words. With n_dev, the device-side count (at most n) is sorted; n only bounds it, so a sort whose
+// Returns the number of passes. hist must hold (1 << RB) * sort_blocks<ITEMS>(n) words, dtot
+// 1 << RB words. With n_dev, the device-side count (at most n) is sorted; n only bounds it, so a sort whose
 // count is usually far below n uses fewer ITEMS per block to spread over more blocks, and its
 // grids are capped at kDevCountGrid workgroups that loop over the tiles holding keys (dispatching
 // workgroups for empty tiles costs about as much as sorting a full one). With first_hist_ready, the
 // caller has already stored the first pass's per-tile histograms in hist (the kernel that wrote the
 // keys counted them), and the first upsweep is skipped.
 constexpr unsigned kDevCountGrid = 256;
-template <typename K, typename V, typename FinalOut, int ITEMS = kSortItems>
+template <typename K, typename V, typename FinalOut, int ITEMS = kSortItems, int RB = 8>
 inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bit, int end_bit,
                              uint32_t* hist, uint32_t* dtot, FinalOut final_out, hipStream_t s,
                              const uint32_t* n_dev = nullptr, bool first_hist_ready = false,
@@ -243,17 +272,17 @@ inline int radix_sort_passes(K* k0, V* v0, K* k1, V* v1, int64_t n, int begin_bi
     const unsigned grid = n_dev ? min(nb, dev_grid) : nb;
     int passes = 0;
     K* src_k = k0; V* src_v = v0; K* dst_k = k1; V* dst_v = v1;
-    for (int shift = begin_bit; shift < end_bit; shift += 8) {
-        const int bits = min(8, end_bit - shift);
-        const bool last = shift + 8 >= end_bit;
+    for (int shift = begin_bit; shift < end_bit; shift += RB) {
+        const int bits = min(RB, end_bit - shift);
+        const bool last = shift + RB >= end_bit;
         if (!(first_hist_ready && shift == begin_bit))
-            radix_upsweep<K, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
-        radix_scan_hist<ITEMS><<<kRadix, kSortBlock, 0, s>>>(hist, nb, dtot, n, n_dev);
+            radix_upsweep<K, ITEMS, RB><<<grid, kSortBlock, 0, s>>>(src_k, n, shift, bits, hist, nb, n_dev);
+        radix_scan_hist<ITEMS><<<1u << RB, kSortBlock, 0, s>>>(hist, nb, dtot, n, n_dev);
         if (last) {
-            radix_downsweep<K, V, FinalOut, ITEMS><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits,
-                                                                               hist, dtot, nb, final_out, n_dev);
+            radix_downsweep<K, V, FinalOut, ITEMS, RB><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, bits,
+                                                                                   hist, dtot, nb, final_out, n_dev);
         } else {
-            radix_downsweep<K, V, PlainOut<K, V>, ITEMS><<<grid, kSortBlock, 0, s>>>(
+            radix_downsweep<K, V, PlainOut<K, V>, ITEMS, RB><<<grid, kSortBlock, 0, s>>>(
                 src_k, src_v, n, shift, bits, hist, dtot, nb, PlainOut<K, V>{dst_k, dst_v}, n_dev);
         }
         ++passes;
