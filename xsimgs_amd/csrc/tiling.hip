@@ -1028,6 +1028,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // is sized for: 1024 keys per block spread them over four times as many workgroups.
 constexpr int kPresortItems = 4;
 constexpr unsigned kPresortGrid = 2048;
+constexpr int kPresortRB = 8;                                        // digit bits
+constexpr int kPresortPasses = (32 + kPresortRB - 1) / kPresortRB;  // over the 32 depth bits
 
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
 struct CountWs {
@@ -1035,6 +1037,9 @@ struct CountWs {
     uint32_t* comp_id; uint32_t* comp_off; uint32_t* comp_key;
     // depth pre-order (sorted fills only): ping-pong, histograms, device-side count, run offsets
     uint32_t* alt_key; uint32_t* alt_id; uint32_t* hist; uint32_t* dtot; uint32_t* m_dev;
+    // after the pre-order: the depth-ordered instances (keys, ids) and the depth-ordered rectangles
+    // (two words each), in whichever pair of the two ping-pong pairs the passes left free
+    uint32_t* pre_key; uint32_t* pre_id; uint32_t* drect_lo; uint32_t* drect_hi;
     uint32_t* roff; uint32_t* rpart;
     uint32_t* seam_cnt; uint32_t* seam_ids;  // per count block: its seam Gaussians (two spans only)
     uint64_t* slice64; uint64_t* slice_extra; uint32_t* slice32;  // slice totals of the two-level scans
@@ -1061,10 +1066,15 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     const size_t ns = g.sort ? (size_t)nv : 0;
     w.alt_key = (uint32_t*)(p + off); off += align256(4 * ns);
     w.alt_id = (uint32_t*)(p + off); off += align256(4 * ns);
+    const bool odd = kPresortPasses % 2 == 1;  // an odd number of passes ends in the alt pair
+    w.pre_key = odd ? w.alt_key : w.comp_key;
+    w.pre_id = odd ? w.alt_id : w.comp_id;
+    w.drect_lo = odd ? w.comp_key : w.alt_key;
+    w.drect_hi = odd ? w.comp_id : w.alt_id;
     w.roff = (uint32_t*)(p + off); off += align256(4 * ns);
     w.hist = (uint32_t*)(p + off);
-    off += align256(g.sort ? 4 * (size_t)kRadix * sort_blocks<kPresortItems>(nv > 0 ? nv : 1) : 0);
-    w.dtot = (uint32_t*)(p + off); off += align256(4 * kRadix);
+    off += align256(g.sort ? 4 * ((size_t)1 << kPresortRB) * sort_blocks<kPresortItems>(nv > 0 ? nv : 1) : 0);
+    w.dtot = (uint32_t*)(p + off); off += align256(4 * ((size_t)1 << kPresortRB));
     w.rpart = (uint32_t*)(p + off); off += align256(4 * ((size_t)w.nb + 1));
     w.m_dev = (uint32_t*)(p + off); off += align256(4);
     w.seam_cnt = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb : 0);
@@ -1125,8 +1135,8 @@ template <int RB>
 void expand_and_sort_runs(const FillWs& fw, const CountWs& cw, int64_t n_runs, int64_t m, int nty, int64_t n_per_cam,
                           int spans, uint32_t neg_row, uint32_t* out_row, uint4* out_rec, hipStream_t s) {
     const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
-    expand_runs_kernel<RB><<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.comp_id, cw.comp_key, m, cw.alt_key,
-                                                      cw.alt_id, nty, n_per_cam, spans, neg_row, fw.row_a, fw.rec_a,
+    expand_runs_kernel<RB><<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.pre_id, cw.pre_key, m, cw.drect_lo,
+                                                      cw.drect_hi, nty, n_per_cam, spans, neg_row, fw.row_a, fw.rec_a,
                                                       fw.hist, nb_runs);
     radix_sort_passes<uint32_t, uint4, PlainOut<uint32_t, uint4>, kRunSortItems, RB>(
         fw.row_a, fw.rec_a, fw.row_b, fw.rec_b, n_runs, 0, fw.row_bits, fw.hist, fw.dtot,
@@ -1250,15 +1260,15 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
-        // (stable, 4 passes, result back in comp_*), then their row-run offsets
-        radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems>(
+        // (stable, kPresortPasses passes, result in pre_key / pre_id), then their row-run offsets
+        radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems, kPresortRB>(
             w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
-            PlainOut<uint32_t, uint32_t>{w.comp_key, w.comp_id}, s, w.m_dev, false, kPresortGrid);
+            PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
         // the depth-ordered rectangles go to the pre-order's ping-pong buffers (free after its four passes)
-        rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.comp_id, w.rects, w.rpart, w.alt_key,
-                                                   w.alt_id);
+        rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
+                                                   w.drect_hi);
         slice_scan_kernel<uint32_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.rpart, w.slice32, nullptr, nullptr);
-        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.alt_key, w.alt_id, w.rpart, w.slice32,
+        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.drect_lo, w.drect_hi, w.rpart, w.slice32,
                                                  w.roff);
     }
     XSG_TRY_LAUNCH("isect_count");
