@@ -684,17 +684,23 @@ __global__ __launch_bounds__(kBlock) void row_segments_kernel(int n_rows, const 
         run += (row_start[r + 1] - row_start[r] + kRunSeg - 1) / kRunSeg;
     }
     if (threadIdx.x == 0) seg_base[n_real] = tot;
-    // every thread a share of the segments: its row is the last r with seg_base[r] <= segment (rows
-    // without segments share a base with the next row, and the search takes the later one)
+    // every thread a contiguous share of the segments: the row of its first one is the last r with
+    // seg_base[r] <= segment (rows without segments share a base with the next row, and the search
+    // takes the later one); the following ones advance the row as they pass its segments
     __syncthreads();  // s_base, and the global seg_base of this block, are complete
     const uint32_t* base = in_lds ? s_base : seg_base;
-    for (uint32_t sg = threadIdx.x; sg < tot; sg += kBlock) {
+    const uint32_t share = (tot + kBlock - 1) / kBlock;
+    const uint32_t s0 = threadIdx.x * share, s1 = min(tot, s0 + share);
+    if (s0 < s1) {
         int lo = 0, hi = n_real - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if (base[mid] <= sg) lo = mid; else hi = mid - 1;
+            if (base[mid] <= s0) lo = mid; else hi = mid - 1;
         }
-        seg_row[sg] = (uint32_t)lo;
+        for (uint32_t sg = s0; sg < s1; ++sg) {
+            while (lo + 1 < n_real && base[lo + 1] <= sg) ++lo;
+            seg_row[sg] = (uint32_t)lo;
+        }
     }
 }
 
