@@ -166,6 +166,33 @@ def test_isect_regular_many_visible(dev):
     assert np.array_equal(np_(off), O.offset_encode(rids, (W + 15) // 16, (H + 15) // 16))
 
 
+def test_isect_presort_tile_sizes(dev):
+    """The depth pre-order picks its tile size (1024 or 4096 keys) from the previous call's visible
+    count; both must order the keys identically. A small binning sets the hint low, then the same
+    1.6 M-Gaussian scene is binned twice (the second call with 4096-key tiles); both match the
+    oracle."""
+    g = np.random.default_rng(23)
+    T = lambda a: torch.from_numpy(a).to(dev)
+    W, H = 1920, 1080
+    small = 2000
+    _C.isect_regular_tiles(T(np.full((small, 2), 100.0, np.float32)), T(np.full((small, 2), 3.0, np.float32)),
+                           T(np.linspace(1.0, 2.0, small).astype(np.float32)), W, H, 16, 16)
+    n = 1_600_000
+    m2 = np.stack([g.uniform(0, W, n), g.uniform(0, H, n)], 1).astype(np.float32)
+    r = g.uniform(0.5, 6.0, (n, 2)).astype(np.float32)
+    d = g.uniform(0.3, 90.0, n).astype(np.float32)
+    d[: n // 50] = d[n // 2]  # ties in depth
+    a = _C.isect_regular_tiles(T(m2), T(r), T(d), W, H, 16, 16)
+    b = _C.isect_regular_tiles(T(m2), T(r), T(d), W, H, 16, 16)
+    print("visible", int((a[0] > 0).sum()), "isects", a[1].numel(), flush=True)
+    assert int((a[0] > 0).sum()) >= 1_500_000
+    rtpg, rids, rfl = O.isect_regular(m2, r, d, W, H, 16, 16)
+    for got in (a, b):
+        assert np.array_equal(np_(got[0]), rtpg)
+        assert np.array_equal(np_(got[1]), rids)
+        assert np.array_equal(np_(got[2]), rfl)
+
+
 def test_isect_regular_batched_six_cameras(dev):
     """Six cameras binned in one call (camera bits above the tile bits) equal each camera's oracle
     binning in turn, with the camera id in the keys and ids offset by cam * N. 6 x 68 tile rows plus the

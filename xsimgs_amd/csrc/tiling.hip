@@ -20,6 +20,7 @@
 // Stable by (high bits, low bits, Gaussian order) in both cases, so the result is bit-identical
 // to sorting the reference keys; ties keep Gaussian order as the reference's fill does.
 #include <algorithm>
+#include <atomic>
 #include <vector>
 
 #include "xsg_sort.h"
@@ -1031,9 +1032,15 @@ int geometry_of(const xsg_isect_desc* d, Geometry& g) {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // The depth pre-order sorts the visible instances, usually a small part of the instances its grid
-// is sized for: 1024 keys per block spread them over four times as many workgroups.
+// is sized for: 1024 keys per block spread them over four times as many workgroups. Large counts
+// (millions of visible instances: a lidar frame, a camera rig) run faster in tiles of 4096 keys
+// (longer runs per digit in each tile's scatter). The count is known only on the device when the
+// pre-order is queued, so the previous call's visible count chooses (both sort identically).
 constexpr int kPresortItems = 4;
+constexpr int kPresortItemsLarge = 16;
+constexpr int64_t kPresortLargeAt = 1500000;  // visible instances
 constexpr unsigned kPresortGrid = 2048;
+std::atomic<int64_t> g_visible_hint{0};
 constexpr int kPresortRB = 8;                                        // digit bits
 constexpr int kPresortPasses = (32 + kPresortRB - 1) / kPresortRB;  // over the 32 depth bits
 
@@ -1267,9 +1274,14 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
         // (stable, kPresortPasses passes, result in pre_key / pre_id), then their row-run offsets
-        radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems, kPresortRB>(
-            w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
-            PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
+        if (g_visible_hint.load(std::memory_order_relaxed) >= kPresortLargeAt)
+            radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItemsLarge, kPresortRB>(
+                w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
+                PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
+        else
+            radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems, kPresortRB>(
+                w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
+                PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
         // the depth-ordered rectangles go to the pre-order's ping-pong buffers (free after its four passes)
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
                                                    w.drect_hi);
@@ -1292,6 +1304,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
                         (unsigned long long)total[1]);
     if (n_isects) *n_isects = (int64_t)total[1];
     if (n_visible) *n_visible = (int64_t)(total[0] >> 32);
+    if (g.sort) g_visible_hint.store((int64_t)(total[0] >> 32), std::memory_order_relaxed);
     if (n_runs) *n_runs = (int64_t)total[2];
     return XSG_OK;
 }
