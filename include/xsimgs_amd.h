@@ -319,6 +319,10 @@ typedef struct {
      * camera (a rig whose cameras share one origin sees one set of view-dependent colours) and
      * v_colors [n, cdim] receives the sum over cameras. An extension of this build. */
     int colors_shared;
+    /* backward only, tiles of 129 to 256 pixels without per-pixel ray gradients: pixels per lane, 4 (a
+     * wavefront per 16x16 tile) or 2 (two), or 0 to choose: 4 when the grid fills the GPU's wave slots
+     * (3 x 1024 wavefronts), else 2. The gradients agree to float32 rounding either way. An extension. */
+    int bwd_pixels_per_lane;
 } xsg_eval3d_args;
 
 int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream);

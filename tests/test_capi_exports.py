@@ -31,7 +31,7 @@ class Eval3dArgs(C.Structure):  # xsg_eval3d_args, field for field
                                    "last_ids", "v_rgb", "v_depth", "v_alpha", "v_means", "v_quats",
                                    "v_scales", "v_opacities", "v_colors", "v_ray_o", "v_ray_d",
                                    "v_velocity", "v_time_delta", "pair_counts")] + \
-        [("colors_shared", C.c_int)]
+        [("colors_shared", C.c_int), ("bwd_pixels_per_lane", C.c_int)]
 
 
 @pytest.fixture(scope="module")

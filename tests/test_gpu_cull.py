@@ -100,7 +100,9 @@ def _forward(dev, s, tsx, tsy, dyn, counts=None):
     return [np_(x) for x in out]
 
 
-def _backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads):
+def _backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads, ppl=0):
+    """ppl: the backward's pixels per lane for 129..256-pixel tiles without ray gradients (0 chooses by
+    grid size: these small images take 2; the full-size frames take 4)."""
     T = lambda k: None if s[k] is None else torch.from_numpy(s[k]).to(dev)
     Tn = lambda a: None if a is None else torch.from_numpy(a).to(dev)
     alpha, last = fwd[2], fwd[3]
@@ -108,13 +110,13 @@ def _backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads):
         grads = _C.rasterize_eval3d_dynamic_bwd(T("means"), T("vel"), T("scales"), T("quats"), T("opac"),
                                                 T("colors"), T("ro"), T("rd"), T("rtd"), tsx, tsy, T("offsets"),
                                                 T("flat"), Tn(alpha), Tn(last), Tn(vr), Tn(vd), Tn(va),
-                                                ray_grads=ray_grads)
+                                                ray_grads=ray_grads, pixels_per_lane=ppl)
         names = ["v_means", "v_velocity", "v_quats", "v_scales", "v_opacity", "v_colors", "v_ray_o", "v_ray_d",
                  "v_time_delta"]
     else:
         grads = _C.rasterize_eval3d_bwd(T("means"), T("scales"), T("quats"), T("opac"), T("colors"), T("ro"),
                                         T("rd"), tsx, tsy, T("offsets"), T("flat"), Tn(alpha), Tn(last), Tn(vr),
-                                        Tn(vd), Tn(va), ray_grads=ray_grads)
+                                        Tn(vd), Tn(va), ray_grads=ray_grads, pixels_per_lane=ppl)
         names = ["v_means", "v_quats", "v_scales", "v_opacity", "v_colors", "v_ray_o", "v_ray_d"]
     return dict(zip(names, grads))
 
@@ -206,8 +208,8 @@ def test_cull_exact(dev, case):
     refs = _oracle_grads(s, tsx, tsy, fwd, vr, vd, va)
     # with and without per-pixel ray gradients: the kernels differ (pixels per lane, where the
     # mean gradient and the shared-origin terms are summed)
-    for ray_grads in (True, False):
-        _check_grads(_backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads), refs, kd, 3, ray_grads)
+    for ray_grads, ppl in ((True, 0), (False, 4), (False, 2)):
+        _check_grads(_backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads, ppl), refs, kd, 3, ray_grads)
 
 
 @pytest.mark.parametrize("dyn", [False, True])
@@ -232,15 +234,15 @@ def test_cull_seeds(dev, seed, tile, dyn):
     vr, vd, va = _grad_inputs(np.random.default_rng(seed), 3)
     vd[~kd] = 0.0
     refs = _oracle_grads(s, tsx, tsy, fwd, vr, vd, va)
-    for ray_grads in (True, False):
-        _check_grads(_backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads), refs, kd, 3, ray_grads)
+    for ray_grads, ppl in ((True, 0), (False, 4), (False, 2)):
+        _check_grads(_backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, ray_grads, ppl), refs, kd, 3, ray_grads)
 
 
 @pytest.mark.parametrize("dyn", [False, True])
 @pytest.mark.parametrize("cdim", [0, 1, 5, 9, 16, 17])
 def test_channel_counts(dev, cdim, dyn):
-    """The backward without ray gradients at 16x16 tiles (four pixels per lane; from 17 channels, where
-    colours are read from HBM, the ray-gradient kernel) for channel counts that move the gradient
+    """The backward without ray gradients at 16x16 tiles (four and two pixels per lane; from 17 channels,
+    where colours are read from HBM, the ray-gradient kernel) for channel counts that move the gradient
     components across the 16-lane chunks of the wavefront reduction."""
     print(f"cdim {cdim} dynamic={dyn}", flush=True)
     tsx = tsy = 16
@@ -257,4 +259,6 @@ def test_channel_counts(dev, cdim, dyn):
             assert frac_close(a, b, RENDER_ATOL) >= bar, name
     vr, vd, va = _grad_inputs(g, cdim)
     refs = _oracle_grads(s, tsx, tsy, fwd, vr, vd, va)
-    _check_grads(_backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, False), refs, s["keep_depth"], cdim, False)
+    for ppl in (4, 2):
+        _check_grads(_backward(dev, s, tsx, tsy, dyn, fwd, vr, vd, va, False, ppl), refs, s["keep_depth"], cdim,
+                     False)

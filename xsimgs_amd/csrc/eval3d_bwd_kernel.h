@@ -506,6 +506,8 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
 // thread (the C-ABI then needs the ray-gradient buffers). Tiles of more than 256 pixels (up to
 // kMaxTilePixels) take four pixels per thread in workgroups of up to 256 threads, with and without
 // ray gradients.
+constexpr int64_t kBwdFullGridWaves = 3 * 1024;
+
 // one launch, with or without the pair counters
 template <int CDIM, bool DYN, bool RG, int PX, int NT>
 void launch_bwd(int n_blocks, int threads, const Eval3dParams& p, hipStream_t s) {
@@ -537,7 +539,12 @@ int eval3d_bwd_cdim(bool dyn, bool ray_grads, const Eval3dParams& p, hipStream_t
     }
     if constexpr (CDIM <= kColorLdsMax) {
         if (!ray_grads) {
-            if (tile_px > 128) {
+            // four pixels per lane when the grid still fills the GPU's wave slots (three waves on each
+            // of 1024 SIMDs); a small grid (cfg3's 1024 lidar tiles) runs two per lane on twice the
+            // waves; the caller may fix either
+            const bool px4 = p.px_hint == 4 ||
+                             (p.px_hint == 0 && (int64_t)n_blocks * (bs4 / 64) >= kBwdFullGridWaves);
+            if (tile_px > 128 && px4) {
                 if (dyn) launch_bwd<CDIM, true, false, 4, T / 4>(n_blocks, bs4, p, s);
                 else launch_bwd<CDIM, false, false, 4, T / 4>(n_blocks, bs4, p, s);
             } else {

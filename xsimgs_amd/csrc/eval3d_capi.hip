@@ -225,6 +225,10 @@ int fill_params(const xsg_eval3d_args* a, Eval3dParams& p, const char* who) {
     p.opac = a->opacities; p.velocity = a->velocity; p.rtd = a->ray_time_delta;
     p.ray_o = a->ray_o; p.ray_d = a->ray_d; p.offsets = a->tile_offsets; p.flatten = a->flatten_ids;
     p.col_shift = a->colors_shared ? a->n * a->cdim : 0;
+    if (a->bwd_pixels_per_lane != 0 && a->bwd_pixels_per_lane != 2 && a->bwd_pixels_per_lane != 4)
+        return xsg_fail(XSG_ERR_INVALID, "%s: bwd_pixels_per_lane must be 0, 2 or 4 (got %d)", who,
+                        a->bwd_pixels_per_lane);
+    p.px_hint = a->bwd_pixels_per_lane;
     return XSG_OK;
 }
 

@@ -205,7 +205,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
                        int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
                        const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors,
                        const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
-                       const OptT& pair_counts, bool batched = false) {
+                       const OptT& pair_counts, int64_t pixels_per_lane, bool batched = false) {
     if (v_render_colors.has_value() && !v_render_colors->is_contiguous())
         throw std::runtime_error("v_render_colors must be contiguous");
     all_contiguous({v_render_depth, v_render_alpha, render_alpha, last_ids});
@@ -262,6 +262,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     a.v_ray_o = o.v_ray_o.has_value() ? o.v_ray_o->data_ptr<float>() : nullptr;
     a.v_ray_d = o.v_ray_d.has_value() ? o.v_ray_d->data_ptr<float>() : nullptr;
     a.pair_counts = counts_ptr(pair_counts, points);
+    a.bwd_pixels_per_lane = (int)pixels_per_lane;
     Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(&a));
     check_rc(xsg_eval3d_bwd(&a, ws.data_ptr(), stream_of(points)));
     return o;
@@ -272,10 +273,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT> rasterize_eval3d_bw
     const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
     const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
     const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
-    const OptT& pair_counts) {
+    const OptT& pair_counts, int64_t pixels_per_lane) {
     BwdOut o = eval3d_bwd_impl(points, std::nullopt, scale, quat, opacity, colors, ray_origins, ray_directions,
                                std::nullopt, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
-                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts);
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
+                               pixels_per_lane);
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d};
 }
 
@@ -286,13 +288,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, OptT, OptT> rasteri
     const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
     const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
     const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha,
-    const OptT& velocity, const OptT& ray_time_delta, bool ray_grads, const OptT& pair_counts) {
+    const OptT& velocity, const OptT& ray_time_delta, bool ray_grads, const OptT& pair_counts,
+    int64_t pixels_per_lane) {
     TORCH_CHECK(velocity.has_value() == ray_time_delta.has_value(),
                 "dynamic compositing needs both velocity and ray_time_delta");
     BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
                                ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
                                last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
-                               true);
+                               pixels_per_lane, true);
     const bool dyn = velocity.has_value();
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
             dyn ? OptT(o.v_velocity) : std::nullopt, dyn ? OptT(o.v_time_delta) : std::nullopt};
@@ -303,10 +306,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, Tensor> ras
     const OptT& colors, const Tensor& ray_origins, const Tensor& ray_directions, const Tensor& ray_time_delta,
     int64_t tile_size_x, int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
     const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors, const Tensor& v_render_depth,
-    const Tensor& v_render_alpha, bool ray_grads, const OptT& pair_counts) {
+    const Tensor& v_render_alpha, bool ray_grads, const OptT& pair_counts, int64_t pixels_per_lane) {
     BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
                                ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
-                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts);
+                               last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
+                               pixels_per_lane);
     return {o.v_points, o.v_velocity, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
             o.v_time_delta};
 }
@@ -1031,7 +1035,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"), py::arg("ray_directions"),
           py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
           py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
-          py::arg("v_render_alpha"), py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
+          py::arg("v_render_alpha"), py::arg("ray_grads") = true, py::arg("pair_counts") = py::none(),
+          py::arg("pixels_per_lane") = 0);
     m.def("rasterize_eval3d_dynamic_fwd", &rasterize_eval3d_dynamic_fwd, py::arg("means"), py::arg("velocity"),
           py::arg("quats"), py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"),
           py::arg("image_height"), py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"),
@@ -1042,7 +1047,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("ray_directions"), py::arg("ray_time_delta"), py::arg("tile_size_x"), py::arg("tile_size_y"),
           py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("render_alpha"), py::arg("last_ids"),
           py::arg("v_render_colors"), py::arg("v_render_depth"), py::arg("v_render_alpha"),
-          py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
+          py::arg("ray_grads") = true, py::arg("pair_counts") = py::none(),
+          py::arg("pixels_per_lane") = 0);
     // batched cameras (extension): C cameras over one scene in one launch per pass
     m.def("rasterize_eval3d_fwd_batched", &rasterize_eval3d_fwd_batched, py::arg("means"), py::arg("quats"),
           py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
@@ -1054,7 +1060,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
           py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
           py::arg("v_render_alpha"), py::arg("velocity") = py::none(), py::arg("ray_time_delta") = py::none(),
-          py::arg("ray_grads") = true, py::arg("pair_counts") = py::none());
+          py::arg("ray_grads") = true, py::arg("pair_counts") = py::none(),
+          py::arg("pixels_per_lane") = 0);
     m.def("eval3d_supported_ndims", &eval3d_supported_ndims);
 
     // color (csrc/color/sh_bind.cpp)

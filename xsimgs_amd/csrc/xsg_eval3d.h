@@ -313,6 +313,7 @@ struct Eval3dParams {
     unsigned long long* pair_counts;  // optional: += [evaluated, composited] pixel-pairs
     // optional (backward): logical (camera, tile) block launched at each position of xcd_tile's order
     const int32_t* tile_order;
+    int px_hint;  // backward pixels per lane for 129..256-pixel tiles: 0 (by grid size), 2 or 4
 };
 
 int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);
