@@ -4,6 +4,8 @@ Each stage is fed the same inputs on both sides (the GPU's own upstream results)
 judged on its own: binning, sort and tile ranges must be bit-exact; renders within 1e-4 absolute;
 gradients within 1e-3 relative with a 1e-5 absolute floor.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -541,6 +543,44 @@ def test_ut_phm_seam_cases(dev, timing):
         assert int(f[0]) == int(rf[0]) == flag, name
         assert np.allclose(m2, rm, atol=2e-2) and np.allclose(r, rr, atol=2e-2, rtol=1e-4), name
         assert np.allclose(d, rd, rtol=1e-6), name
+
+
+@pytest.mark.parametrize("case", ["moving_lidar", "moving_spherical", "point_velocity", "static_large"])
+def test_ut_phm_pose_kinds(dev, case):
+    """The phase-modelled UT has one kernel for static poses and one for moving poses or moving points
+    (ut_phm_kernels.h:13-114 for both); the launch runs both and the device's camera picks which one
+    writes. Moving lidar / spherical poses (linear and angular velocity, rolling shutter), per-point
+    velocities under a static pose, and a static cfg3 scene of 300k Gaussians (more than the moving
+    kernel's grid covers in one pass) against the oracle (tests/_judge.py)."""
+    if case == "static_large":
+        sc = synthetic.make_cfg3(n=300_000)
+        spec = sc.cameras[0]
+        means, scales, quats, opac = (sc.means.numpy(), sc.scales.numpy(), sc.quats.numpy(),
+                                      sc.opacity.numpy())
+        vel = None
+    else:
+        z = np.load(os.path.join(os.path.dirname(__file__), "golden",
+                                 "spherical.npz" if case == "moving_spherical" else "lidar_phm.npz"))
+        f = {k: z[k] for k in z.files}
+        w, h = (int(x) for x in f["cam_size"])
+        kind = "spherical" if case == "moving_spherical" else "lidar"
+        moving = case != "point_velocity"
+        spec = synthetic.CameraSpec(kind, w, h, [0.9950042, 0.0, 0.0, 0.0998334], [0.4, -0.3, 0.2],
+                                    f["cam_impl"].tolist(),
+                                    v=[2.5, -1.0, 0.3] if moving else [0.0, 0.0, 0.0],
+                                    w=[0.02, -0.01, 0.6] if moving else [0.0, 0.0, 0.0],
+                                    rolling=[0.1, 0.0], trigger_time=0.0, pose_time=0.05,
+                                    beam_v=torch.from_numpy(f["cam_beam_v"]) if "cam_beam_v" in f else None)
+        means, scales, quats, opac = f["means"], f["scales"], f["quats"], f["opacity"]
+        vel = None
+        if case == "point_velocity":
+            vel = np.random.default_rng(11).normal(0.0, 3.0, means.shape).astype(np.float32)
+    cam = frame.make_camera(spec, dev)
+    T = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+    got = cam.ext_cls.projection_utgs_phm(cam.pack, T(means), T(vel), T(scales), T(quats), T(opac), spec.width,
+                                          spec.height)
+    out = J.judge_ut(got, spec, means, scales, quats, opac, spec.width, spec.height, phm=True, vel=vel, label=case)
+    assert out["visible_gpu"] > out["n"] // 4
 
 
 def test_eval3d_tile_over_1024_pixels_rejected(dev):

@@ -141,63 +141,77 @@ __global__ __launch_bounds__(kBlock) void ut_project_kernel(
                          depths);
 }
 
-// unscented_transform_phm_kernel (include/cameras/ut_phm_kernels.h:13-114)
-template <int KIND>
+// unscented_transform_phm_kernel (include/cameras/ut_phm_kernels.h:13-114), one instantiation per kind
+// of pose. A static pose shares the sigma points' (u, v, range) between the three phase modes and needs
+// about half the registers of a moving one, so it has a kernel of its own; the host launches both (the
+// moving one on a small grid-striding grid) and each returns at once for the other kind of pose,
+// which only the device's copy of the camera tells.
+template <int KIND, bool STATIC_POSE>
 __global__ __launch_bounds__(kBlock) void ut_project_phm_kernel(
     int64_t n, const float* __restrict__ pack, ProjParams pp, UtWeights ut, f2 img,
     const float* __restrict__ means, const float* __restrict__ vel, const float* __restrict__ scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity, uint8_t* __restrict__ flags,
     float2* __restrict__ radii, float2* __restrict__ means2d, float* __restrict__ depths) {
-    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n) return;
     const Camera cam = load_camera(pack, KIND);
-    const bool is_static = camera_is_static(cam, vel != nullptr);
-    const float op = opacity ? opacity[i] : 1.0f;
-    uint8_t flag = 0;
-    f2 m_out = mk2(0.f, 0.f), r_out = mk2(0.f, 0.f);
-    float d_out = 0.f;
-    if (op >= 1.0f / 255.0f) {
-        f3 d[3];
-        ut_deltas(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
-        const f3 pw = ld3(means + 3 * i);
-        const f3 pv = vel ? ld3(vel + 3 * i) : mk3(0.f, 0.f, 0.f);
-        f2 rc = mk2(0.f, 0.f), rl = rc, rr = rc, mc = rc, ml = rc, mr = rc;
-        float dc = 0.f, dl = 0.f, dr = 0.f, ud = 0.f;
-        // a static pose projects the seven sigma points to angles once; the three phase modes then
-        // differ only in how they unwrap the azimuth
-        SigmaAngles sa;
-        if (is_static) sigma_angles(cam, pw, d, sa);
-        auto project = [&](int mode, f2& m2, f2& r2, float& dd) {
-            if (is_static) return ut_projection_angles(cam, mode, ut, img, pp, op, sa, m2, r2, dd, ud);
-            return ut_projection<KIND>(cam, mode, ut, img, pp, pw, pv, op, d, false, m2, r2, dd, ud);
-        };
-        bool res = project(XSG_MODE_CENTRAL, mc, rc, dc);
-        if (res) {
-            const float u_pi = float(M_PI) * img.x / fabsf(cam.i1);
-            const int r_c = int(res) * (int(ud > u_pi) + 1);
-            res = project(XSG_MODE_NEGATIVE, ml, rl, dl);
-            const int r_l = int(res) * (int(ud > u_pi) + 1);
-            res = project(XSG_MODE_POSITIVE, mr, rr, dr);
-            const int r_r = int(res) * (int(ud > u_pi) + 1);
-            if (r_l == 1 && r_r == 1) {
-                flag = 2; r_out = rl; m_out = ml; d_out = dl;
-            } else if (r_c == 1) {
-                flag = 1; r_out = rc; m_out = mc; d_out = dc;
-            } else if (r_l == 1 || r_r == 1) {
-                // ut_phm_kernels.h:417-421 selects the side whose result is *not* 1
-                const bool use_left = r_l != 1;
-                flag = 1;
-                r_out = use_left ? rl : rr;
-                m_out = use_left ? ml : mr;
-                d_out = use_left ? dl : dr;
+    if (camera_is_static(cam, vel != nullptr) != STATIC_POSE) return;
+    const PhaseUnwrap unwrap = phase_unwrap(cam);
+    const float u_pi = float(M_PI) * img.x / fabsf(cam.i1);
+    // the static kernel's grid covers the Gaussians once; a loop there would keep per-lane copies of the
+    // camera terms live across iterations and cost occupancy
+    const int64_t stride = STATIC_POSE ? n : (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        const float op = opacity ? opacity[i] : 1.0f;
+        uint8_t flag = 0;
+        f2 m_out = mk2(0.f, 0.f), r_out = mk2(0.f, 0.f);
+        float d_out = 0.f;
+        if (op >= 1.0f / 255.0f) {
+            f3 d[3];
+            ut_deltas(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
+            const f3 pw = ld3(means + 3 * i);
+            f2 rc = mk2(0.f, 0.f), rl = rc, rr = rc, mc = rc, ml = rc, mr = rc;
+            float dc = 0.f, dl = 0.f, dr = 0.f, ud = 0.f;
+            SigmaUv sa;
+            f3 pv = mk3(0.f, 0.f, 0.f);
+            if constexpr (STATIC_POSE) sigma_uv(cam, pw, d, sa);
+            else if (vel) pv = ld3(vel + 3 * i);
+            auto project = [&](int mode, f2& m2, f2& r2, float& dd) {
+                if constexpr (STATIC_POSE)
+                    return ut_projection_sigma_uv(cam, unwrap, mode, ut, img, pp, op, sa, m2, r2, dd, ud);
+                else
+                    return ut_projection<KIND>(cam, mode, ut, img, pp, pw, pv, op, d, false, m2, r2, dd, ud);
+            };
+            bool res = project(XSG_MODE_CENTRAL, mc, rc, dc);
+            if (res) {
+                const int r_c = int(res) * (int(ud > u_pi) + 1);
+                res = project(XSG_MODE_NEGATIVE, ml, rl, dl);
+                const int r_l = int(res) * (int(ud > u_pi) + 1);
+                res = project(XSG_MODE_POSITIVE, mr, rr, dr);
+                const int r_r = int(res) * (int(ud > u_pi) + 1);
+                if (r_l == 1 && r_r == 1) {
+                    flag = 2; r_out = rl; m_out = ml; d_out = dl;
+                } else if (r_c == 1) {
+                    flag = 1; r_out = rc; m_out = mc; d_out = dc;
+                } else if (r_l == 1 || r_r == 1) {
+                    // ut_phm_kernels.h:417-421 selects the side whose result is *not* 1
+                    const bool use_left = r_l != 1;
+                    flag = 1;
+                    r_out = use_left ? rl : rr;
+                    m_out = use_left ? ml : mr;
+                    d_out = use_left ? dl : dr;
+                }
             }
         }
+        flags[i] = flag;
+        radii[i] = make_float2(r_out.x, r_out.y);
+        means2d[i] = make_float2(m_out.x, m_out.y);
+        depths[i] = d_out;
     }
-    flags[i] = flag;
-    radii[i] = make_float2(r_out.x, r_out.y);
-    means2d[i] = make_float2(m_out.x, m_out.y);
-    depths[i] = d_out;
 }
+
+// Workgroups of the moving-pose phase-modelled kernel: enough to fill every CU at that kernel's
+// occupancy (four waves per SIMD), striding over the Gaussians; a static pose's launch of it returns
+// after one camera load per workgroup.
+constexpr int kPhmMovingBlocks = 1024;
 
 // camera_projection_fwd (include/cameras/projection_kernels.h:259-309)
 template <int KIND>
@@ -703,8 +717,15 @@ extern "C" int xsg_ut_project(int kind, int phm, const float* pack, int64_t n, c
         constexpr int KIND = decltype(k)::value;
         if constexpr (KIND == XSG_CAM_SPHERICAL || KIND == XSG_CAM_LIDAR) {
             if (phm) {
-                ut_project_phm_kernel<KIND><<<grid, block, 0, s>>>(n, pack, pp, ut, img, means, velocity, scales, q4,
-                                                                   opacity, flags, r2, m2, depths);
+                // a point velocity makes every pose a moving one
+                if (!velocity)
+                    ut_project_phm_kernel<KIND, true><<<grid, block, 0, s>>>(n, pack, pp, ut, img, means, velocity,
+                                                                             scales, q4, opacity, flags, r2, m2,
+                                                                             depths);
+                const dim3 grid_m(std::min<unsigned>(grid.x, kPhmMovingBlocks));
+                ut_project_phm_kernel<KIND, false><<<grid_m, block, 0, s>>>(n, pack, pp, ut, img, means, velocity,
+                                                                            scales, q4, opacity, flags, r2, m2,
+                                                                            depths);
                 return;
             }
         }

@@ -261,20 +261,29 @@ XSG_DEV void world_to_camera_jac(const Camera& c, f3 point, f3 pvel, float time,
     dres = dp + quat_apply(w, xyz, vdiff);
 }
 
-// angles_to_uv with the phase unwrapping of SphericalCamera (csrc/cameras/spherical.h:109-125)
-XSG_DEV f2 angles_to_uv(const Camera& c, int mode, float phi, float theta) {
-    float u = (phi - c.i0) / c.i1;
-    const float u_pose = u_pose_of(c);
-    const float u_offset = (2.0f * float(M_PI) / fabsf(c.i1));
-    if (c.roll_u > 0) {
-        if ((mode == XSG_MODE_NEGATIVE) && (u > u_pose)) u = u - u_offset;
-        if ((mode == XSG_MODE_POSITIVE) && (u < u_pose)) u = u + u_offset;
+// The phase unwrapping of SphericalCamera's angles_to_uv (csrc/cameras/spherical.h:109-125): u from the
+// azimuth, shifted by one turn towards the pose's side in the negative / positive modes. The pose's u
+// and the turn depend on the camera only.
+struct PhaseUnwrap { float u_pose, u_offset; bool forward; };
+
+XSG_DEV PhaseUnwrap phase_unwrap(const Camera& c) {
+    return {u_pose_of(c), 2.0f * float(M_PI) / fabsf(c.i1), c.roll_u > 0};
+}
+
+XSG_DEV float unwrap_u(const PhaseUnwrap& w, int mode, float u) {
+    if (w.forward) {
+        if ((mode == XSG_MODE_NEGATIVE) && (u > w.u_pose)) u = u - w.u_offset;
+        if ((mode == XSG_MODE_POSITIVE) && (u < w.u_pose)) u = u + w.u_offset;
     } else {
-        if ((mode == XSG_MODE_NEGATIVE) && (u < u_pose)) u = u + u_offset;
-        if ((mode == XSG_MODE_POSITIVE) && (u > u_pose)) u = u - u_offset;
+        if ((mode == XSG_MODE_NEGATIVE) && (u < w.u_pose)) u = u + w.u_offset;
+        if ((mode == XSG_MODE_POSITIVE) && (u > w.u_pose)) u = u - w.u_offset;
     }
-    const float v = (theta - c.i2) / c.i3;
-    return mk2(u, v);
+    return u;
+}
+
+// angles_to_uv (spherical.h:109-125)
+XSG_DEV f2 angles_to_uv(const Camera& c, int mode, float phi, float theta) {
+    return mk2(unwrap_u(phase_unwrap(c), mode, (phi - c.i0) / c.i1), (theta - c.i2) / c.i3);
 }
 
 // Camera models with a projection Jacobian take Newton steps on the pixel time; the others the
@@ -554,13 +563,13 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
     return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
 }
 
-// A static spherical / lidar camera's sigma points in angle form: each camera-space point's azimuth,
-// elevation and range (point_to_uvd's spherical branch, spherical.h:133-142). They do not depend on
-// the phase mode, which only unwraps u (angles_to_uv), so the three modes of the phase-modelled
-// projection share them; each mode's results equal ut_projection's bit for bit.
-struct SigmaAngles { float phi[7], theta[7], r[7]; };
+// A static spherical / lidar camera's sigma points before phase unwrapping: each camera-space point's
+// u = (azimuth - u0) / du, v and range (point_to_uvd's spherical branch, spherical.h:133-142). None of
+// them depends on the phase mode, which only shifts u by one turn (unwrap_u), so the three modes of
+// the phase-modelled projection share them; each mode's results equal ut_projection's bit for bit.
+struct SigmaUv { float u[7], v[7], r[7]; };
 
-XSG_DEV void sigma_angles(const Camera& c, f3 pw, const f3 d[3], SigmaAngles& a) {
+XSG_DEV void sigma_uv(const Camera& c, f3 pw, const f3 d[3], SigmaUv& a) {
     const Mat3 m = static_world_to_camera(c);
     const f3 pc0 = mul(m, pw - c.t0);
     f3 e[3];
@@ -571,18 +580,19 @@ XSG_DEV void sigma_angles(const Camera& c, f3 pw, const f3 d[3], SigmaAngles& a)
         const f3 p = i == 0 ? pc0 : ((i & 1) ? pc0 + e[(i - 1) >> 1] : pc0 - e[(i - 1) >> 1]);
         const float x2y2 = p.x * p.x + p.y * p.y;
         const float r = sqrtf(x2y2 + p.z * p.z);
-        a.phi[i] = atan2f(-p.x, -p.y) + float(M_PI);
-        a.theta[i] = asinf(p.z / r);
+        const float phi = atan2f(-p.x, -p.y) + float(M_PI);
+        const float theta = asinf(p.z / r);
+        a.u[i] = (phi - c.i0) / c.i1;
+        a.v[i] = (theta - c.i2) / c.i3;
         a.r[i] = r;
     }
 }
 
-XSG_DEV bool ut_projection_angles(const Camera& c, int mode, const UtWeights& ut, f2 img, const ProjParams& pp,
-                                  float opac, const SigmaAngles& a, f2& mean2d, f2& radii, float& depth,
-                                  float& u_distance) {
+XSG_DEV bool ut_projection_sigma_uv(const Camera& c, const PhaseUnwrap& w, int mode, const UtWeights& ut, f2 img,
+                                    const ProjParams& pp, float opac, const SigmaUv& a, f2& mean2d, f2& radii,
+                                    float& depth, float& u_distance) {
     auto proj = [&](int i, float4& uvdt, bool& valid) {
-        const f2 uv = angles_to_uv(c, mode, a.phi[i], a.theta[i]);
-        static_projection_tail(c, mk3(uv.x, uv.y, a.r[i]), pp, mode, uvdt, valid);
+        static_projection_tail(c, mk3(unwrap_u(w, mode, a.u[i]), a.v[i], a.r[i]), pp, mode, uvdt, valid);
     };
     return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
 }
