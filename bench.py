@@ -187,14 +187,15 @@ def extension_rows(torch, _C, frame, synthetic, st, sc, cam_spec, means, scales,
     return rows
 
 
-def binning_alg_bytes(kind, n, n_isects, n_tiles, n_flag2=0):
+def binning_alg_bytes(kind, n, n_isects, n_tiles, n_flag2=0, keys=False):
     """Bytes the binning cannot avoid: read each Gaussian's projection once (means2d 8, radii 8, depth 4,
     + flag 1 for the lidar / spherical kinds), write tiles_per_gauss (4) once, write each intersection's
-    key and id (12) once, write each tile's offset (4) once; a seam Gaussian's re-projection reads its
-    point, scale, quaternion and opacity (44). The depth pre-order, run expansion and scans the
-    implementation adds are not priced, so the fraction is that of the unavoidable traffic."""
+    id (4; and its key, 8 more, when the keys are asked for -- the frame's binning takes the tile offsets
+    instead) once, write each tile's offset (4) once; a seam Gaussian's re-projection reads its point,
+    scale, quaternion and opacity (44). The depth pre-order, run expansion and scans the implementation
+    adds are not priced, so the fraction is that of the unavoidable traffic."""
     per_g = 24 + (1 if kind != "pinhole" else 0)
-    return per_g * n + 12 * n_isects + 4 * n_tiles + 44 * n_flag2
+    return per_g * n + (12 if keys else 4) * n_isects + 4 * n_tiles + 44 * n_flag2
 
 
 def sh_bwd_alg_bytes(K, n, v_colors):
@@ -345,7 +346,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             "binning": (lambda: cam.isect_gs_tiles(means, scales, quats, W, H, flags, radii, m2, dep, opacity=opac,
                                                    tile_size_x=tsx, tile_size_y=tsy,
                                                    tile_offsets=torch.empty(nty, ntx, dtype=torch.int32,
-                                                                            device=dev)),
+                                                                            device=dev), keys=False),
                         binning_alg_bytes(kind, N, n_isects, ntx * nty, c0["n_flag2"])),
             "offset_encode": (lambda: _C.isect_offset_encode(ids, ntx, nty), (enc_reads + 4) * ntx * nty),
             "rays": (lambda: cam.camera_rays(W, H), 24 * W * H),
@@ -380,7 +381,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             n_col = 1 if col_b.dim() == 2 else n_cams
             stages["binning"] = (
                 lambda: _C.isect_regular_tiles_batched(m2_b, radii_b, dep_b, W, H, tsx, tsy,
-                                                       tile_offsets=torch.empty_like(off_b)),
+                                                       tile_offsets=torch.empty_like(off_b), keys=False),
                 sum(binning_alg_bytes(kind, N, c["n_isects"], ntx * nty, c["n_flag2"]) for c in info))
             stages["eval3d_fwd"] = (
                 lambda: _C.rasterize_eval3d_fwd_batched(means, quats, scales, col_b, opac, W, H, tsx, tsy, ro_b,

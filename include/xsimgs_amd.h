@@ -248,7 +248,10 @@ size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects,
  * tile_offsets (optional, sorted fills only; NULL skips it): the n_tile_offsets =
  * n_cams * n_tiles_h * n_tiles_w offsets that xsg_isect_offset_encode would compute from the
  * sorted keys, produced by the fill itself (extension: it saves the search that
- * isect_offset_encode, tiling_common.cu:25-71, runs over the keys). */
+ * isect_offset_encode, tiling_common.cu:25-71, runs over the keys).
+ * isect_ids may be NULL in a sorted fill that writes tile_offsets (extension): the keys are then not
+ * written, as a renderer that takes the offsets never reads them (rendering/render.py:45-81 uses
+ * them only to encode the offsets). */
 int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible, int64_t n_runs,
                    int sort, void* count_workspace, void* fill_workspace, int64_t* isect_ids,
                    int32_t* flatten_ids, int32_t* tile_offsets, int64_t n_tile_offsets, xsg_stream_t stream);

@@ -34,6 +34,15 @@ class Eval3dArgs(C.Structure):  # xsg_eval3d_args, field for field
         [("colors_shared", C.c_int), ("bwd_pixels_per_lane", C.c_int)]
 
 
+class IsectDesc(C.Structure):  # xsg_isect_desc, field for field
+    _fields_ = [("kind", C.c_int), ("n_cams", C.c_int), ("n", C.c_int64)] + \
+        [(k, C.c_void_p) for k in ("means2d", "radii", "depths", "flags", "camera_pack", "points", "velocity",
+                                   "scales", "quats", "opacity", "elev_boundaries")] + \
+        [("n_elev", C.c_int), ("img_width", C.c_float), ("img_height", C.c_float), ("tile_w", C.c_int),
+         ("tile_h", C.c_int), ("ut_alpha", C.c_float), ("ut_beta", C.c_float), ("ut_kappa", C.c_float),
+         ("sort", C.c_int)]
+
+
 @pytest.fixture(scope="module")
 def lib():
     if not os.path.exists(LIB):
@@ -92,6 +101,23 @@ def test_invalid_arguments_fail_before_launch(lib):
     rc = lib.xsg_sh_fwd(7, None, C.c_int64(1), 64, None, None, None, None, 0, None, None)
     assert rc == -1
     assert b"degree" in lib.xsg_last_error().lower()
+
+
+def test_fill_without_keys_needs_tile_offsets(lib):
+    """A sorted fill may leave the keys out (isect_ids NULL) only when it writes the tile offsets; an
+    unsorted one, or one without offsets, fails on the host before any launch."""
+    lib.xsg_last_error.restype = C.c_char_p
+    d = IsectDesc(kind=0, n_cams=1, n=100, img_width=64.0, img_height=32.0, tile_w=16, tile_h=16, sort=1)
+    nw, nh, tb, kb = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+    assert lib.xsg_isect_geometry(C.byref(d), C.byref(nw), C.byref(nh), C.byref(tb), C.byref(kb)) == 0
+    assert (nw.value, nh.value) == (4, 2)
+    fake = C.c_void_p(1 << 20)
+    i64 = C.c_int64
+    for sort, offs in ((1, None), (0, None)):
+        rc = lib.xsg_isect_fill(C.byref(d), i64(10), i64(5), i64(5), sort, fake, fake, None, fake, offs,
+                                i64(0), None)
+        assert rc == -1
+        assert b"keys may be left out" in lib.xsg_last_error()
 
 
 def test_misaligned_workspace_is_rejected_before_launch(lib):

@@ -545,6 +545,71 @@ def test_ut_phm_seam_cases(dev, timing):
         assert np.allclose(d, rd, rtol=1e-6), name
 
 
+@pytest.mark.parametrize("case", ["regular", "batched", "lidar", "spherical", "cfg3"])
+def test_fill_without_keys(dev, cfg0, case):
+    """keys=False (the renderer's binning: it takes the tile offsets) writes the same flatten ids and
+    offsets as a fill that writes the keys, and returns no keys; the offsets equal isect_offset_encode
+    of the written keys."""
+    def run(fn, keys):
+        off = torch.full(shape, -7, dtype=torch.int32, device=dev)
+        tpg, ids, fl = fn(off, keys)
+        torch.cuda.synchronize()
+        return tpg, ids, fl, off
+    if case in ("regular", "batched"):
+        sc, st = cfg0
+        spec = sc.cameras[0]
+        _, (flags, radii, m2, dep) = _ut(st, spec, dev)
+        ntx, nty = (spec.width + 15) // 16, (spec.height + 15) // 16
+        if case == "regular":
+            shape, n_cams = (nty, ntx), 1
+            fn = lambda off, keys: _C.isect_regular_tiles(m2, radii, dep, spec.width, spec.height, 16, 16,
+                                                          tile_offsets=off, keys=keys)
+        else:
+            shape, n_cams = (2, nty, ntx), 2
+            m2b, rb, db = (torch.stack([x, x]).contiguous() for x in (m2, radii, dep))
+            m2b[1] += 9.5
+            fn = lambda off, keys: _C.isect_regular_tiles_batched(m2b, rb, db, spec.width, spec.height, 16, 16,
+                                                                  tile_offsets=off, keys=keys)
+    else:
+        if case == "cfg3":
+            sc = synthetic.make_cfg3(n=200_000)
+            st = frame.prepare(sc, dev, requires_grad=False)
+            spec = sc.cameras[0]
+            cam, (flags, radii, m2, dep) = _ut(st, spec, dev, True)
+            means, scales, quats, opac = st.means, torch.exp(st.log_scales), st.quats, torch.sigmoid(st.opacity_logits)
+            tsx, tsy = sc.tile_size
+        else:
+            z = np.load(os.path.join(os.path.dirname(__file__), "golden", f"{'lidar_phm' if case == 'lidar' else case}.npz"))
+            f = {k: z[k] for k in z.files}
+            w, h = (int(x) for x in f["cam_size"])
+            spec = synthetic.CameraSpec(case, w, h, f["cam_q"].tolist(), f["cam_t"].tolist(), f["cam_impl"].tolist(),
+                                        rolling=f["cam_rolling"].tolist(), trigger_time=float(f["cam_times"][0]),
+                                        pose_time=float(f["cam_times"][1]),
+                                        beam_v=torch.from_numpy(f["cam_beam_v"]) if "cam_beam_v" in f else None)
+            cam = frame.make_camera(spec, dev)
+            T = lambda k: torch.from_numpy(np.ascontiguousarray(f[k], np.float32)).to(dev)
+            means, scales, quats, opac = T("means"), T("scales"), T("quats"), T("opacity")
+            flags, radii, m2, dep = cam.ext_cls.projection_utgs_phm(cam.pack, means, None, scales, quats, opac,
+                                                                    spec.width, spec.height)
+            tsx, tsy = (int(x) for x in f["tile"])
+        ntx, nty = (spec.width + tsx - 1) // tsx, (spec.height + tsy - 1) // tsy
+        shape, n_cams = (nty, ntx), 1
+        fn = lambda off, keys: cam.isect_gs_tiles(means, scales, quats, spec.width, spec.height, flags, radii, m2, dep,
+                                                  opacity=opac, tile_size_x=tsx, tile_size_y=tsy, tile_offsets=off,
+                                                  keys=keys)
+    tpg_k, ids_k, fl_k, off_k = run(fn, True)
+    tpg_n, ids_n, fl_n, off_n = run(fn, False)
+    print(case, "intersections", fl_k.numel(), flush=True)
+    assert fl_k.numel() > 500
+    assert ids_n.numel() == 0 and ids_n.dtype == torch.int64
+    assert torch.equal(tpg_k, tpg_n) and torch.equal(fl_k, fl_n) and torch.equal(off_k, off_n)
+    enc = _C.isect_offset_encode(ids_k, shape[-1], shape[-2], n_cams)
+    assert np.array_equal(np_(enc).reshape(-1), np_(off_k).reshape(-1))
+    with pytest.raises(RuntimeError, match="keys=False needs tile_offsets"):
+        _C.isect_regular_tiles(m2.reshape(-1, 2)[:100].contiguous(), radii.reshape(-1, 2)[:100].contiguous(),
+                               dep.reshape(-1)[:100].contiguous(), 64, 64, 16, 16, keys=False)
+
+
 @pytest.mark.parametrize("case", ["moving_lidar", "moving_spherical", "point_velocity", "static_large"])
 def test_ut_phm_pose_kinds(dev, case):
     """The phase-modelled UT has one kernel for static poses and one for moving poses or moving points

@@ -145,7 +145,7 @@ class FusedRSCamera:
     def isect_gs_tiles(self, points, scale, rotation, width: int, height: int, flags, radii, means2d, depths,
                        points_velocity=None, opacity=None, tile_size_x: int = 16, tile_size_y: int = 16,
                        ut_alpha: float = 0.1, ut_beta: float = 2.0, ut_kappa: float = 0.0, sort: bool = True,
-                       double_buffer: bool = True, tile_offsets=None):
+                       double_buffer: bool = True, tile_offsets=None, keys: bool = True):
         return isect_regular_tiles(means2d, radii, depths, img_width=width, img_height=height,
                                    tile_size_x=tile_size_x, tile_size_y=tile_size_y, sort=sort,
-                                   double_buffer=double_buffer, tile_offsets=tile_offsets)
+                                   double_buffer=double_buffer, tile_offsets=tile_offsets, keys=keys)

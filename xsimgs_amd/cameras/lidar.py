@@ -65,11 +65,11 @@ class LidarCamera(FusedRSCamera):
     def isect_gs_tiles(self, points, scale, rotation, width: int, height: int, flags, radii, means2d, depths,
                        points_velocity=None, opacity=None, tile_size_x: int = 16, tile_size_y: int = 16,
                        ut_alpha: float = 0.1, ut_beta: float = 2.0, ut_kappa: float = 0.0, sort: bool = True,
-                       double_buffer: bool = True, tile_offsets=None):
+                       double_buffer: bool = True, tile_offsets=None, keys: bool = True):
         elev_boundaries = self.beam_v[::tile_size_y].contiguous()
         return isect_lidar_tiles(camera_pack=self.pack, points=points, points_velocity=points_velocity, scale=scale,
                                  quat=rotation, opacity=opacity, flag=flags, means2d=means2d, radii=radii,
                                  depths=depths, elev_boundaries=elev_boundaries, tile_size_x=tile_size_x,
                                  img_width=width, img_height=height, ut_alpha=ut_alpha, ut_beta=ut_beta,
                                  ut_kappa=ut_kappa, sort=sort, double_buffer=double_buffer,
-                                 tile_offsets=tile_offsets)
+                                 tile_offsets=tile_offsets, keys=keys)

@@ -24,10 +24,10 @@ class SphericalCamera(FusedRSCamera):
     def isect_gs_tiles(self, points, scale, rotation, width: int, height: int, flags, radii, means2d, depths,
                        points_velocity=None, opacity=None, tile_size_x: int = 16, tile_size_y: int = 16,
                        ut_alpha: float = 0.1, ut_beta: float = 2.0, ut_kappa: float = 0.0, sort: bool = True,
-                       double_buffer: bool = True, tile_offsets=None):
+                       double_buffer: bool = True, tile_offsets=None, keys: bool = True):
         return isect_spherical_tiles(camera_pack=self.pack, points=points, points_velocity=points_velocity,
                                      scale=scale, quat=rotation, opacity=opacity, flag=flags, means2d=means2d,
                                      radii=radii, depths=depths, tile_size_x=tile_size_x, tile_size_y=tile_size_y,
                                      img_width=width, img_height=height, ut_alpha=ut_alpha, ut_beta=ut_beta,
                                      ut_kappa=ut_kappa, sort=sort, double_buffer=double_buffer,
-                                     tile_offsets=tile_offsets)
+                                     tile_offsets=tile_offsets, keys=keys)

@@ -183,10 +183,42 @@ __global__ __launch_bounds__(kBlock) void ut_project_phm_kernel(
             bool res = project(XSG_MODE_CENTRAL, mc, rc, dc);
             if (res) {
                 const int r_c = int(res) * (int(ud > u_pi) + 1);
-                res = project(XSG_MODE_NEGATIVE, ml, rl, dl);
-                const int r_l = int(res) * (int(ud > u_pi) + 1);
-                res = project(XSG_MODE_POSITIVE, mr, rr, dr);
-                const int r_r = int(res) * (int(ud > u_pi) + 1);
+                int r_l, r_r;
+                if (STATIC_POSE && fabsf(cam.roll_u) == 0.0f) {
+                    // Global shutter: u_pose is 0.5 and every mode starts its time solve at +-0, so a
+                    // side mode whose unwrap shifts none of the seven points repeats the central
+                    // projection bit for bit. With roll_u 0 the negative mode shifts the points left of
+                    // u_pose, the positive mode those right of it; most Gaussians lie on one side, so
+                    // each lane projects the one side mode that differs (its own mode), and only
+                    // Gaussians across u_pose project both.
+                    bool lo = false, hi = false;
+#pragma unroll
+                    for (int k = 0; k < 7; ++k) {
+                        lo |= sa.u[k] < unwrap.u_pose;
+                        hi |= sa.u[k] > unwrap.u_pose;
+                    }
+                    f2 m1 = mk2(0.f, 0.f), r1 = m1, m2 = m1, r2 = m1;
+                    float d1 = 0.f, d2 = 0.f;
+                    int r_1 = r_c, r_2 = r_c;
+                    if (lo || hi) {
+                        res = project(lo ? XSG_MODE_NEGATIVE : XSG_MODE_POSITIVE, m1, r1, d1);
+                        r_1 = int(res) * (int(ud > u_pi) + 1);
+                    }
+                    if (lo && hi) {
+                        res = project(XSG_MODE_POSITIVE, m2, r2, d2);
+                        r_2 = int(res) * (int(ud > u_pi) + 1);
+                    }
+                    ml = lo ? m1 : mc; rl = lo ? r1 : rc; dl = lo ? d1 : dc; r_l = lo ? r_1 : r_c;
+                    mr = hi ? (lo ? m2 : m1) : mc;
+                    rr = hi ? (lo ? r2 : r1) : rc;
+                    dr = hi ? (lo ? d2 : d1) : dc;
+                    r_r = hi ? (lo ? r_2 : r_1) : r_c;
+                } else {
+                    res = project(XSG_MODE_NEGATIVE, ml, rl, dl);
+                    r_l = int(res) * (int(ud > u_pi) + 1);
+                    res = project(XSG_MODE_POSITIVE, mr, rr, dr);
+                    r_r = int(res) * (int(ud > u_pi) + 1);
+                }
                 if (r_l == 1 && r_r == 1) {
                     flag = 2; r_out = rl; m_out = ml; d_out = dl;
                 } else if (r_c == 1) {

@@ -17,6 +17,9 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
     constexpr int C4 = (CL + 3) / 4;                                   // float4 slots of them
     constexpr int CS = CDIM > 0 ? CDIM : 1;
     constexpr int NW = NT / 64;
+    // The opacity rides in the last colour float4's first free component when there is one, so that a
+    // pair of a tile with one ray origin reads four float4s (M rows with gro, colours with opacity)
+    constexpr bool OP_IN_COL = CL > 0 && (CL & 3) != 0;
     // Every per-Gaussian slot is a float4 indexed by the batch position, so one address register
     // serves all reads of a pair.
     __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | gro
@@ -107,7 +110,8 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                 for (int k4 = 0; k4 < C4; ++k4) {
                     float v[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) v[j] = (4 * k4 + j < CL) ? cp[4 * k4 + j] : 0.f;
+                    for (int j = 0; j < 4; ++j)
+                        v[j] = (4 * k4 + j < CL) ? cp[4 * k4 + j] : (OP_IN_COL && 4 * k4 + j == CL) ? op : 0.f;
                     s_col[k4][c.tr] = make_float4(v[0], v[1], v[2], v[3]);
                 }
             } else {
@@ -133,12 +137,23 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                 uint64_t m = uniform_u64(s_mask[wave][w2]);
                 for (; m != 0 && alive != 0; m &= m - 1) {
                     const int t = (w2 << 6) + (int)__builtin_ctzll(m);
-                    const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t], xo = s_xo[t];
+                    const float4 a = s_m0[t], bq = s_m1[t], cq = s_m2[t];
                     const f3 r0 = mk3(a.x, a.y, a.z), r1 = mk3(bq.x, bq.y, bq.z), r2 = mk3(cq.x, cq.y, cq.z);
+                    float4 cl[C4 > 0 ? C4 : 1];
+#pragma unroll
+                    for (int k4 = 0; k4 < C4; ++k4) cl[k4] = s_col[k4][t];
+                    float op;
+                    if constexpr (OP_IN_COL) {
+                        const float4 last = cl[C4 - 1];
+                        op = (CL & 3) == 1 ? last.y : (CL & 3) == 2 ? last.z : last.w;
+                    }
                     f3 gro;
                     if constexpr (FIXED) {
                         gro = mk3(a.w, bq.w, cq.w);
+                        if constexpr (!OP_IN_COL) op = s_xo[t].w;
                     } else {
+                        const float4 xo = s_xo[t];
+                        if constexpr (!OP_IN_COL) op = xo.w;
                         f3 mu = mk3(xo.x, xo.y, xo.z);
                         if constexpr (DYN) mu = mu + rt * mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
                         gro = rows_mul(r0, r1, r2, ro - mu);
@@ -149,7 +164,7 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                     // |n x gro|^2 = |grd x gro|^2 / |grd|^2; exp(-x/2) = exp2(x * -log2(e)/2)
                     const f3 cr = cross(grd, gro);
                     const float e = __builtin_amdgcn_exp2f(dot(cr, cr) * (inv_dd * -0.72134752f));
-                    const float alpha = fminf(0.999f, xo.w * e);
+                    const float alpha = fminf(0.999f, op * e);
                     const float next_T = T * (1.0f - alpha);
                     // lane masks of this pair; termination is exclusive (eval3d_fwd.cu:135-139)
                     const uint64_t pass_m = __ballot(alpha >= 1.f / 255.f) & alive;
@@ -162,7 +177,7 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                         if constexpr (CL > 0) {
 #pragma unroll
                             for (int k4 = 0; k4 < C4; ++k4) {
-                                const float4 cv = s_col[k4][t];
+                                const float4 cv = cl[k4];
                                 const float cc[4] = {cv.x, cv.y, cv.z, cv.w};
 #pragma unroll
                                 for (int j = 0; j < 4; ++j)

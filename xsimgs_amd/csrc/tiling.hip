@@ -810,7 +810,9 @@ __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __res
 }
 
 // Runs of negative-depth instances, after every tile, in run order; each run's entries consecutive
-// (their keys' tile bits are saturated by the sign extension). One workgroup.
+// (their keys' tile bits are saturated by the sign extension). One workgroup. KEYS false writes the
+// flatten ids only (a fill whose caller takes the tile offsets instead of the keys).
+template <bool KEYS>
 XSG_DEV void write_neg_runs(const uint4* __restrict__ rec, int64_t b, int64_t n_runs, uint32_t base, int64_t n_out,
                             int64_t* __restrict__ out_keys, int32_t* __restrict__ out_ids) {
     __shared__ uint32_t lds[kWaves];
@@ -824,7 +826,7 @@ XSG_DEV void write_neg_runs(const uint4* __restrict__ rec, int64_t b, int64_t n_
         for (uint32_t q = 0; q < w; ++q) {
             const uint64_t pos = (uint64_t)carry + ex + q;
             if (pos < (uint64_t)n_out) {
-                out_keys[pos] = make_key(0u, rr.y);
+                if constexpr (KEYS) out_keys[pos] = make_key(0u, rr.y);
                 out_ids[pos] = (int32_t)rr.x;
             }
         }
@@ -840,6 +842,7 @@ XSG_DEV void write_neg_runs(const uint4* __restrict__ rec, int64_t b, int64_t n_
 // column's slot, in run order. They are staged in a wavefront-private LDS buffer of 64 entries per
 // column and stored 64 at a time, so that every global store of a column is a full, contiguous
 // wavefront. Workgroup s_max writes the negative-depth runs instead.
+template <bool KEYS>
 __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     int n_real, const uint4* __restrict__ rec, const uint32_t* __restrict__ row_start,
     const uint32_t* __restrict__ seg_base, const uint32_t* __restrict__ seg_row, const uint32_t* __restrict__ slots,
@@ -854,7 +857,8 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
     // boundaries: on one XCD those partial lines meet in its L2
     const int64_t sg = xcd_tile((int)blockIdx.x, (int)(s_max + 1));
     if (sg == s_max) {
-        write_neg_runs(rec, row_start[n_real], n_runs, tile_base[(int64_t)n_real * ntx], n_out, out_keys, out_ids);
+        write_neg_runs<KEYS>(rec, row_start[n_real], n_runs, tile_base[(int64_t)n_real * ntx], n_out, out_keys,
+                             out_ids);
         return;
     }
     if (sg >= (int64_t)seg_base[n_real]) return;
@@ -912,19 +916,20 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
                     const uint32_t slot = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mk, fill[j]));
                     if (cov && slot < 64) {
-                        s_dep[wave][j][slot] = rr.y;
+                        if constexpr (KEYS) s_dep[wave][j][slot] = rr.y;
                         s_gid[wave][j][slot] = (int32_t)rr.x;
                     }
                     const uint32_t f = (uint32_t)__builtin_amdgcn_readfirstlane((int)(fill[j] + cnt));
                     if (f >= 64) {  // the column's buffer is full: store it, then stage the overflow
                         const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
                         if (pos < (uint64_t)n_out) {
-                            out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
+                            if constexpr (KEYS)
+                                out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
                             out_ids[pos] = s_gid[wave][j][lane];
                         }
                         out[j] = (uint32_t)__builtin_amdgcn_readfirstlane((int)(out[j] + 64));
                         if (cov && slot >= 64) {
-                            s_dep[wave][j][slot - 64] = rr.y;
+                            if constexpr (KEYS) s_dep[wave][j][slot - 64] = rr.y;
                             s_gid[wave][j][slot - 64] = (int32_t)rr.x;
                         }
                         fill[j] = f - 64;
@@ -937,7 +942,7 @@ __global__ __launch_bounds__(kBlock) void write_runs_kernel(
             for (int j = 0; j < kColGroup; ++j) {
                 const uint64_t pos = (uint64_t)out[j] + (uint64_t)lane;
                 if (j < nc && (uint32_t)lane < fill[j] && pos < (uint64_t)n_out) {
-                    out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
+                    if constexpr (KEYS) out_keys[pos] = make_key(tile_row + (uint32_t)(c0 + j), s_dep[wave][j][lane]);
                     out_ids[pos] = s_gid[wave][j][lane];
                 }
             }
@@ -1329,6 +1334,9 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
             return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: %lld tile offsets for a grid of %d x %d x %d tiles",
                             (long long)n_tile_offsets, g.n_cams, g.nty, g.ntx);
     }
+    if (!isect_ids && !(sort && tile_offsets))
+        return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: the keys may be left out only by a sorted fill that writes "
+                                         "the tile offsets");
     if (n_isects == 0) {  // tiling_common.cu:86-88: every offset 0
         if (tile_offsets)
             fill_i32_kernel<<<xsg_blocks(n_tile_offsets, kBlock), kBlock, 0, (hipStream_t)stream>>>(tile_offsets,
@@ -1338,7 +1346,7 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     }
     const CountWs cw = count_ws_layout(g, count_workspace);
     if (n_isects < 0 || n_visible <= 0 || n_visible > cw.n_virtual || n_runs <= 0 || n_runs > n_isects ||
-        !count_workspace || !isect_ids || !flatten_ids)
+        !count_workspace || !flatten_ids)
         return xsg_fail(XSG_ERR_INVALID, "xsg_isect_fill: bad arguments");
     if (const int rc2 = xsg_check_workspace(count_workspace, "xsg_isect_fill")) return rc2;
     const hipStream_t s = (hipStream_t)stream;
@@ -1392,10 +1400,11 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     // offsets of the sorted keys (negative-depth runs follow every tile)
     tile_scan_kernel<<<1, kScanThreads, 0, s>>>(fw.tile_tot, n_tile_slots, tile_offsets);
     // the writers (one extra workgroup for the negative-depth runs)
-    write_runs_kernel<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, rec, fw.row_start, fw.seg_base,
-                                                                fw.seg_row, fw.slots, fw.tile_tot, fw.s_max, n_runs,
-                                                                g.ntx, g.nty, g.tnb, n_isects, isect_ids,
-                                                                flatten_ids);
+    auto writer = isect_ids ? write_runs_kernel<true> : write_runs_kernel<false>;
+    writer<<<(unsigned)fw.s_max + 1, kBlock, sizeof(uint32_t) * g.ntx, s>>>(n_real, rec, fw.row_start, fw.seg_base,
+                                                                         fw.seg_row, fw.slots, fw.tile_tot, fw.s_max,
+                                                                         n_runs, g.ntx, g.nty, g.tnb, n_isects,
+                                                                         isect_ids, flatten_ids);
     XSG_TRY_LAUNCH("isect_fill");
     return XSG_OK;
 }

@@ -388,9 +388,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> spherical_harmonics_fused_bwd(int64_t
 
 // ------------------------------------------------------------------ binning
 // tile_offsets (extension): an int32 tensor that a sorted fill writes the tile offsets into, the values
-// isect_offset_encode would compute from the sorted keys
+// isect_offset_encode would compute from the sorted keys. keys = false (extension, with tile_offsets):
+// the keys are not written and isect_ids comes back empty.
 std::tuple<Tensor, Tensor, Tensor> isect_run(xsg_isect_desc& d, const Tensor& like, bool sort,
-                                             const OptT& tile_offsets) {
+                                             const OptT& tile_offsets, bool keys) {
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(like.device());
     int32_t* offs = nullptr;
     if (tile_offsets.has_value()) {
@@ -400,6 +401,7 @@ std::tuple<Tensor, Tensor, Tensor> isect_run(xsg_isect_desc& d, const Tensor& li
         check_same_device({like, *tile_offsets});
         offs = tile_offsets->data_ptr<int32_t>();
     }
+    TORCH_CHECK(keys || offs, "keys=False needs tile_offsets (a sorted fill that writes the offsets)");
     d.sort = sort ? 1 : 0;
     const xsg_stream_t s = stream_of(like);
     Tensor tiles_per_gauss = at::empty({d.n * d.n_cams}, like.options().dtype(at::kInt));
@@ -407,14 +409,14 @@ std::tuple<Tensor, Tensor, Tensor> isect_run(xsg_isect_desc& d, const Tensor& li
     int64_t n_isects = 0, n_visible = 0, n_runs = 0;
     check_rc(xsg_isect_count(&d, tiles_per_gauss.data_ptr<int32_t>(), cws.data_ptr(), &n_isects, &n_visible,
                              &n_runs, s));
-    Tensor isect_ids = at::empty({n_isects}, like.options().dtype(at::kLong));
+    Tensor isect_ids = at::empty({keys ? n_isects : 0}, like.options().dtype(at::kLong));
     Tensor flatten_ids = at::empty({n_isects}, like.options().dtype(at::kInt));
     if (n_isects > 0 || offs) {
         Tensor fws = workspace(like, sort && n_isects > 0 ? xsg_isect_fill_workspace_bytes(&d, n_isects, n_visible,
                                                                                            n_runs)
                                                           : 1);
         check_rc(xsg_isect_fill(&d, n_isects, n_visible, n_runs, sort ? 1 : 0, cws.data_ptr(), fws.data_ptr(),
-                                isect_ids.data_ptr<int64_t>(), flatten_ids.data_ptr<int32_t>(), offs,
+                                keys ? isect_ids.data_ptr<int64_t>() : nullptr, flatten_ids.data_ptr<int32_t>(), offs,
                                 offs ? tile_offsets->numel() : 0, s));
     }
     return {tiles_per_gauss, isect_ids, flatten_ids};
@@ -424,7 +426,7 @@ std::tuple<Tensor, Tensor, Tensor> isect_run(xsg_isect_desc& d, const Tensor& li
 std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles(const Tensor& means2d, const Tensor& radii, const Tensor& depths,
                                                        int64_t img_width, int64_t img_height, int64_t tile_size_x,
                                                        int64_t tile_size_y, bool sort, bool double_buffer,
-                                                       const OptT& tile_offsets) {
+                                                       const OptT& tile_offsets, bool keys) {
     (void)double_buffer;  // memory strategy only; results are identical
     check_same_device({means2d, radii, depths});
     all_contiguous({means2d, radii, depths});
@@ -435,7 +437,7 @@ std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles(const Tensor& means2d, co
     d.means2d = fptr(means2d); d.radii = fptr(radii); d.depths = fptr(depths);
     d.img_width = (float)img_width; d.img_height = (float)img_height;
     d.tile_w = (int)tile_size_x; d.tile_h = (int)tile_size_y;
-    auto r = isect_run(d, depths, sort, tile_offsets);
+    auto r = isect_run(d, depths, sort, tile_offsets, keys);
     std::get<0>(r) = std::get<0>(r).view(depths.sizes());
     return r;
 }
@@ -445,7 +447,8 @@ std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles(const Tensor& means2d, co
 std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles_batched(const Tensor& means2d, const Tensor& radii,
                                                                const Tensor& depths, int64_t img_width,
                                                                int64_t img_height, int64_t tile_size_x,
-                                                               int64_t tile_size_y, bool sort, const OptT& tile_offsets) {
+                                                               int64_t tile_size_y, bool sort, const OptT& tile_offsets,
+                                                               bool keys) {
     check_same_device({means2d, radii, depths});
     all_contiguous({means2d, radii, depths});
     TORCH_CHECK(depths.dim() == 2, "batched tiling takes [C, N] depths");
@@ -456,7 +459,7 @@ std::tuple<Tensor, Tensor, Tensor> isect_regular_tiles_batched(const Tensor& mea
     d.means2d = fptr(means2d); d.radii = fptr(radii); d.depths = fptr(depths);
     d.img_width = (float)img_width; d.img_height = (float)img_height;
     d.tile_w = (int)tile_size_x; d.tile_h = (int)tile_size_y;
-    auto r = isect_run(d, depths, sort, tile_offsets);
+    auto r = isect_run(d, depths, sort, tile_offsets, keys);
     std::get<0>(r) = std::get<0>(r).view(depths.sizes());
     return r;
 }
@@ -467,7 +470,7 @@ std::tuple<Tensor, Tensor, Tensor> isect_seam_tiles(int kind, const Tensor& came
                                                     const Tensor& radii, const Tensor& depths, const OptT& elev,
                                                     int64_t tile_size_x, int64_t tile_size_y, double img_width,
                                                     double img_height, double ut_alpha, double ut_beta,
-                                                    double ut_kappa, bool sort, const OptT& tile_offsets) {
+                                                    double ut_kappa, bool sort, const OptT& tile_offsets, bool keys) {
     TORCH_CHECK(camera_pack.is_cuda(), "camera_pack must be CUDA tensor")
     std::vector<Tensor> ts{camera_pack, points, points_velocity.value_or(points), scale, quat, flag, means2d,
                            radii, depths};
@@ -488,7 +491,7 @@ std::tuple<Tensor, Tensor, Tensor> isect_seam_tiles(int kind, const Tensor& came
     d.img_width = (float)img_width; d.img_height = (float)img_height;
     d.tile_w = (int)tile_size_x; d.tile_h = (int)tile_size_y;
     d.ut_alpha = (float)ut_alpha; d.ut_beta = (float)ut_beta; d.ut_kappa = (float)ut_kappa;
-    auto r = isect_run(d, depths, sort, tile_offsets);
+    auto r = isect_run(d, depths, sort, tile_offsets, keys);
     std::get<0>(r) = std::get<0>(r).view(depths.sizes());
     return r;
 }
@@ -501,11 +504,11 @@ std::tuple<Tensor, Tensor, Tensor> isect_lidar_tiles(const Tensor& camera_pack, 
                                                      const Tensor& elev_boundaries, int64_t tile_size_x,
                                                      double img_width, double img_height, double ut_alpha,
                                                      double ut_beta, double ut_kappa, bool sort, bool double_buffer,
-                                                     const OptT& tile_offsets) {
+                                                     const OptT& tile_offsets, bool keys) {
     (void)double_buffer;
     return isect_seam_tiles(XSG_TILING_LIDAR, camera_pack, points, points_velocity, scale, quat, opacity, flag,
                             means2d, radii, depths, elev_boundaries, tile_size_x, 1, img_width, img_height, ut_alpha,
-                            ut_beta, ut_kappa, sort, tile_offsets);
+                            ut_beta, ut_kappa, sort, tile_offsets, keys);
 }
 
 // isect_spherical_tiles (phm_spherical_tiling.cu:179-314)
@@ -516,11 +519,11 @@ std::tuple<Tensor, Tensor, Tensor> isect_spherical_tiles(const Tensor& camera_pa
                                                          const Tensor& depths, int64_t tile_size_x,
                                                          int64_t tile_size_y, double img_width, double img_height,
                                                          double ut_alpha, double ut_beta, double ut_kappa, bool sort,
-                                                         bool double_buffer, const OptT& tile_offsets) {
+                                                         bool double_buffer, const OptT& tile_offsets, bool keys) {
     (void)double_buffer;
     return isect_seam_tiles(XSG_TILING_SPHERICAL, camera_pack, points, points_velocity, scale, quat, opacity, flag,
                             means2d, radii, depths, std::nullopt, tile_size_x, tile_size_y, img_width, img_height,
-                            ut_alpha, ut_beta, ut_kappa, sort, tile_offsets);
+                            ut_alpha, ut_beta, ut_kappa, sort, tile_offsets, keys);
 }
 
 // isect_offset_encode (tiling_common.cu:73-99); n_cams > 1 gives [n_cams, th, tw] (batched rigs)
@@ -1077,22 +1080,24 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("tile_height"), py::arg("n_cams") = 1);
     m.def("isect_regular_tiles", &isect_regular_tiles, py::arg("means2d"), py::arg("radii"), py::arg("depth"),
           py::arg("img_width"), py::arg("img_height"), py::arg("tile_size_x"), py::arg("tile_size_y"),
-          py::arg("sort") = true, py::arg("double_buffer") = true, py::arg("tile_offsets") = py::none());
+          py::arg("sort") = true, py::arg("double_buffer") = true, py::arg("tile_offsets") = py::none(),
+          py::arg("keys") = true);
     m.def("isect_regular_tiles_batched", &isect_regular_tiles_batched, py::arg("means2d"), py::arg("radii"),
           py::arg("depth"), py::arg("img_width"), py::arg("img_height"), py::arg("tile_size_x"),
-          py::arg("tile_size_y"), py::arg("sort") = true, py::arg("tile_offsets") = py::none());
+          py::arg("tile_size_y"), py::arg("sort") = true, py::arg("tile_offsets") = py::none(),
+          py::arg("keys") = true);
     m.def("isect_lidar_tiles", &isect_lidar_tiles, py::arg("camera_pack"), py::arg("points"),
           py::arg("points_velocity"), py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("flag"),
           py::arg("means2d"), py::arg("radii"), py::arg("depths"), py::arg("elev_boundaries"),
           py::arg("tile_size_x"), py::arg("img_width"), py::arg("img_height"), py::arg("ut_alpha") = 0.1f,
           py::arg("ut_beta") = 2.0f, py::arg("ut_kappa") = 0.0f, py::arg("sort") = true,
-          py::arg("double_buffer") = true, py::arg("tile_offsets") = py::none());
+          py::arg("double_buffer") = true, py::arg("tile_offsets") = py::none(), py::arg("keys") = true);
     m.def("isect_spherical_tiles", &isect_spherical_tiles, py::arg("camera_pack"), py::arg("points"),
           py::arg("points_velocity"), py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("flag"),
           py::arg("means2d"), py::arg("radii"), py::arg("depths"), py::arg("tile_size_x"), py::arg("tile_size_y"),
           py::arg("img_width"), py::arg("img_height"), py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f,
           py::arg("ut_kappa") = 0.0f, py::arg("sort") = true, py::arg("double_buffer") = true,
-          py::arg("tile_offsets") = py::none());
+          py::arg("tile_offsets") = py::none(), py::arg("keys") = true);
     m.def("mask_radii_packed", &mask_radii_packed, py::arg("packed_mask"), py::arg("radii"));
     // scene-assembly producers (csrc/nodes/gs_masking.cu:44-47, container.cu:269-303)
     m.def("packed_mask_from_instances", &packed_mask_from_instances, py::arg("instance_ids"),

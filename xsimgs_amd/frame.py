@@ -146,7 +146,7 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
         depths = torch.stack([p[3] for p in proj])
         offsets = torch.empty((len(specs), nty, ntx), dtype=torch.int32, device=st.device)
         _, _, flatten_ids = isect_regular_tiles_batched(means2d, radii, depths, W, H, tsx, tsy, sort=True,
-                                                        tile_offsets=offsets)
+                                                        tile_offsets=offsets, keys=False)
     rgb, depth, alpha = ut_gs_rasterize_batched(st.means, st.quats, scales, opac, colors, ray_o, ray_d, offsets,
                                                 flatten_ids, tsx, tsy)
     out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d, offsets=offsets,

@@ -22,13 +22,14 @@ def ut_gs_tiling(camera, points, scale, rotation, width: int, height: int, point
             mask_radii(packed_particle_mask, radii)
         n_tiles_width = (width + tile_size_x - 1) // tile_size_x
         n_tiles_height = (height + tile_size_y - 1) // tile_size_y
-        # the sorted fill writes the tile offsets that isect_offset_encode would compute from its keys
+        # the sorted fill writes the tile offsets that isect_offset_encode would compute from its keys, so
+        # the keys themselves (read by nothing else here) are not written
         tile_gs_offsets = torch.empty((n_tiles_height, n_tiles_width), dtype=torch.int32, device=points.device)
         tiles_per_gs, isect_ids, flatten_ids = camera.isect_gs_tiles(
             points=points, points_velocity=points_velocity, scale=scale, rotation=rotation, opacity=opacity,
             flags=flags, means2d=means2d, radii=radii, depths=depth, width=width, height=height,
             ut_alpha=ut_alpha, ut_beta=ut_beta, ut_kappa=ut_kappa, tile_size_x=tile_size_x,
-            tile_size_y=tile_size_y, sort=True, double_buffer=True, tile_offsets=tile_gs_offsets)
+            tile_size_y=tile_size_y, sort=True, double_buffer=True, tile_offsets=tile_gs_offsets, keys=False)
     return dict(means2d=means2d, radii=radii, depth=depth, isect_offsets=tile_gs_offsets, flatten_ids=flatten_ids)
 
 
