@@ -18,12 +18,13 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
     constexpr int CS = CDIM > 0 ? CDIM : 1;
     constexpr int NW = NT / 64;
     // The opacity rides in the last colour float4's first free component when there is one, so that a
-    // pair of a tile with one ray origin reads four float4s (M rows with gro, colours with opacity)
+    // pair reads four float4s (M rows with gro or the mean, colours with opacity)
     constexpr bool OP_IN_COL = CL > 0 && (CL & 3) != 0;
     // Every per-Gaussian slot is a float4 indexed by the batch position, so one address register
-    // serves all reads of a pair.
-    __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | gro
-    __shared__ float4 s_xo[NT];                      // mean | opacity
+    // serves all reads of a pair. The M rows' fourth components hold gro = M (o - mu) when the tile's
+    // rays share one origin, else the mean.
+    __shared__ float4 s_m0[NT], s_m1[NT], s_m2[NT];  // M rows | gro or mean
+    __shared__ float s_op[OP_IN_COL ? 1 : NT];       // opacity, when no colour slot has room
     __shared__ float4 s_vel[DYN ? NT : 1];
     __shared__ float4 s_col[C4 > 0 ? C4 : 1][NT];
     __shared__ int32_t s_id[CL > 0 ? 1 : NT];
@@ -93,12 +94,11 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
             const f3 sc = ld3(p.scales + 3 * gid);
             f3 r0, r1, r2;
             iscl_rot_rows(q, sc, r0, r1, r2);
-            f3 gro = mk3(0.f, 0.f, 0.f);
-            if (fixed) gro = rows_mul(r0, r1, r2, o0 - mu);
-            s_m0[c.tr] = make_float4(r0.x, r0.y, r0.z, gro.x);
-            s_m1[c.tr] = make_float4(r1.x, r1.y, r1.z, gro.y);
-            s_m2[c.tr] = make_float4(r2.x, r2.y, r2.z, gro.z);
-            s_xo[c.tr] = make_float4(mu.x, mu.y, mu.z, op);
+            const f3 fourth = fixed ? rows_mul(r0, r1, r2, o0 - mu) : mu;
+            s_m0[c.tr] = make_float4(r0.x, r0.y, r0.z, fourth.x);
+            s_m1[c.tr] = make_float4(r1.x, r1.y, r1.z, fourth.y);
+            s_m2[c.tr] = make_float4(r2.x, r2.y, r2.z, fourth.z);
+            if constexpr (!OP_IN_COL) s_op[c.tr] = op;
             f3 vel = mk3(0.f, 0.f, 0.f);
             if constexpr (DYN) {
                 if (p.velocity) vel = ld3(p.velocity + 3 * gid);
@@ -146,15 +146,14 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
                     if constexpr (OP_IN_COL) {
                         const float4 last = cl[C4 - 1];
                         op = (CL & 3) == 1 ? last.y : (CL & 3) == 2 ? last.z : last.w;
+                    } else {
+                        op = s_op[t];
                     }
                     f3 gro;
                     if constexpr (FIXED) {
                         gro = mk3(a.w, bq.w, cq.w);
-                        if constexpr (!OP_IN_COL) op = s_xo[t].w;
                     } else {
-                        const float4 xo = s_xo[t];
-                        if constexpr (!OP_IN_COL) op = xo.w;
-                        f3 mu = mk3(xo.x, xo.y, xo.z);
+                        f3 mu = mk3(a.w, bq.w, cq.w);
                         if constexpr (DYN) mu = mu + rt * mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
                         gro = rows_mul(r0, r1, r2, ro - mu);
                     }
