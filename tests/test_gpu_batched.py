@@ -211,3 +211,39 @@ def test_render_rig_matches_camera_loop(dev):
     assert set(got) == set(want) == {"means", "quats", "log_scales", "opacity_logits", "sh"}
     for k in want:
         _close(f"rig {k}", got[k], want[k])
+
+
+def test_projection_and_rays_into_preallocated_slices(dev):
+    """out= of the UT projection and of camera_rays (extension): one camera's results written into its
+    slice of a rig's [C, ...] buffers equal the op's own outputs bit for bit; wrong shapes or dtypes,
+    and a pack that needs a gradient, are rejected."""
+    sc = S.make_cfg4(seed=5, n=50_000, n_blobs=100)
+    st = frame.prepare(sc, dev, requires_grad=False)
+    W, H = sc.cameras[0].width, sc.cameras[0].height
+    N = sc.means.shape[0]
+    scales, opac = torch.exp(st.log_scales), torch.sigmoid(st.opacity_logits)
+    C = 2
+    fl = torch.full((C, N), 7, dtype=torch.uint8, device=dev)
+    ra, m2, de = (torch.full(s, -3.0, device=dev) for s in ((C, N, 2), (C, N, 2), (C, N)))
+    ro, rd = torch.full((C, H, W, 3), -3.0, device=dev), torch.full((C, H, W, 3), -3.0, device=dev)
+    for c in range(C):
+        cam = st.cams[c + 1]
+        want = cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac)
+        cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac, out=(fl[c], ra[c], m2[c], de[c]))
+        for a, b in zip((fl[c], ra[c], m2[c], de[c]), want):
+            assert torch.equal(a, b)
+        wo, wd = cam.camera_rays(W, H)
+        go, gd = cam.camera_rays(W, H, out=(ro[c], rd[c]))
+        assert go.data_ptr() == ro[c].data_ptr() and gd.data_ptr() == rd[c].data_ptr()
+        assert torch.equal(ro[c], wo) and torch.equal(rd[c], wd)
+    cam = st.cams[0]
+    with pytest.raises(RuntimeError, match="out: flags must be uint8"):
+        cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac, out=(ra[0], ra[0], m2[0], de[0]))
+    with pytest.raises(RuntimeError, match="out: tensors for"):
+        cam.ut_gs_projection(st.means[:100].contiguous(), scales[:100].contiguous(), st.quats[:100].contiguous(), W,
+                             H, opacity=opac[:100].contiguous(), out=(fl[0], ra[0], m2[0], de[0]))
+    with pytest.raises(RuntimeError, match="height x width x 3"):
+        cam.camera_rays(W, H + 1, out=(ro[0], rd[0]))
+    pack = cam.pack.detach().clone().requires_grad_(True)
+    with pytest.raises(RuntimeError, match="needs no gradient"):
+        cam.ext_cls.camera_rays(pack, W, H, out=(ro[0], rd[0]))

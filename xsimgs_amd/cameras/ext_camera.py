@@ -101,9 +101,11 @@ class FusedRSCamera:
             max_margin=self.max_margin)
 
     def camera_rays(self, width: int, height: int, normalized_rays: bool = True, world_space: bool = True,
-                    return_origins: bool = True, return_valid: bool = False):
+                    return_origins: bool = True, return_valid: bool = False, out=None):
+        """out (extension): preallocated (ray_o, ray_d) tensors of [height, width, 3] to write into."""
         out = self.ext_cls.camera_rays(self.pack, width=width, height=height, world_space=world_space,
-                                       normalized=normalized_rays, return_valid=return_valid)
+                                       normalized=normalized_rays, return_origins=return_origins,
+                                       return_valid=return_valid, out=out)
         ray_o = out[0] if return_origins else None
         if return_valid:
             return ray_o, out[1], out[2]
@@ -129,7 +131,8 @@ class FusedRSCamera:
 
     def ut_gs_projection(self, points, scale, rotation, width: int, height: int, points_velocity=None,
                          opacity=None, ut_alpha: float = 0.1, ut_beta: float = 2.0, ut_kappa: float = 0.0,
-                         use_phm: bool = None):
+                         use_phm: bool = None, out=None):
+        """out (extension): preallocated (flags, radii, means2d, depths) tensors to write into."""
         if use_phm is None:
             use_phm = self.use_phm
         proj_fn = (self.ext_cls.projection_utgs_phm if use_phm and self.supports_phm()
@@ -140,7 +143,7 @@ class FusedRSCamera:
                        opacity.contiguous() if opacity is not None else None, width=width, height=height,
                        ut_alpha=ut_alpha, ut_beta=ut_beta, ut_kappa=ut_kappa,
                        residual_thr_early_stop=self.residual_thr_early_stop, max_residual=self.residual_max_valid,
-                       max_margin=self.max_margin)
+                       max_margin=self.max_margin, out=out)
 
     def isect_gs_tiles(self, points, scale, rotation, width: int, height: int, flags, radii, means2d, depths,
                        points_velocity=None, opacity=None, tile_size_x: int = 16, tile_size_y: int = 16,

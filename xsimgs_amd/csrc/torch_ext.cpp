@@ -785,10 +785,34 @@ struct CameraRaysFn : public torch::autograd::Function<CameraRaysFn> {
 // the autograd function only when the pack needs a gradient (its bookkeeping costs host time)
 bool needs_grad(const Tensor& t) { return t.requires_grad() && at::GradMode::is_enabled(); }
 
+// out (extension): preallocated contiguous float32 (ray_o, ray_d) of [height, width, 3] each (ray_o
+// ignored without return_origins), e.g. one camera's slices of a rig's [C, H, W, 3] buffers; not with
+// a pack that needs a gradient
 py::object camera_rays(const CamSpec& spec, const Tensor& pack, int64_t width, int64_t height, bool world_space,
-                       bool normalized, bool return_origins, bool return_valid) {
+                       bool normalized, bool return_origins, bool return_valid,
+                       const std::optional<std::tuple<Tensor, Tensor>>& out_rays) {
     validate_pack(spec, pack);
     torch::autograd::variable_list res;
+    if (out_rays.has_value()) {
+        TORCH_CHECK(!needs_grad(pack), "camera_rays: out= takes a pack that needs no gradient");
+        TORCH_CHECK(!return_valid, "camera_rays: out= comes without return_valid");
+        const auto& [ro, rd] = *out_rays;
+        std::vector<Tensor> ts{pack, rd};
+        if (return_origins) ts.push_back(ro);
+        check_same_device(ts);
+        for (size_t i = 1; i < ts.size(); ++i)
+            TORCH_CHECK(ts[i].scalar_type() == at::kFloat && ts[i].is_contiguous() &&
+                            ts[i].numel() == height * width * 3,
+                        "camera_rays: out tensors must be contiguous float32 of height x width x 3");
+        const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(pack.device());
+        check_rc(xsg_camera_rays(spec.kind, fptr(pack), (int)width, (int)height, world_space ? 1 : 0,
+                                 normalized ? 1 : 0, return_origins ? ro.data_ptr<float>() : nullptr,
+                                 rd.data_ptr<float>(), nullptr, stream_of(pack)));
+        py::list o;
+        o.append(return_origins ? py::cast(ro) : py::none());
+        o.append(py::cast(rd));
+        return std::move(o);
+    }
     if (needs_grad(pack)) {
         res = CameraRaysFn::apply(pack, (int64_t)spec.kind, width, height, world_space, normalized, return_origins,
                                   return_valid);
@@ -916,12 +940,18 @@ std::tuple<Tensor, Tensor> projection(const CamSpec& spec, bool no_jac, const Te
 }
 
 // launch_unscented_transform[_phm] (ut_kernels.h:249-305, ut_phm_kernels.h:125-173)
+// out (extension): four preallocated contiguous tensors (flags u8 [N], radii [N, 2], means2d [N, 2],
+// depths [N], float32) that receive the results, e.g. one camera's slices of a rig's [C, N, ...]
+// buffers, which then need no stacking
+using UtOut = std::optional<std::tuple<Tensor, Tensor, Tensor, Tensor>>;
+
 std::tuple<Tensor, Tensor, Tensor, Tensor> projection_utgs(const CamSpec& spec, bool phm, const Tensor& pack,
                                                            const Tensor& points, const OptT& points_velocity,
                                                            const Tensor& scales, const Tensor& quats,
                                                            const OptT& opacity, double width, double height,
                                                            double ut_alpha, double ut_beta, double ut_kappa,
-                                                           double thr, double max_res, double margin) {
+                                                           double thr, double max_res, double margin,
+                                                           const UtOut& out) {
     validate_pack(spec, pack);
     check_same_device({pack, points, scales, quats});
     std::vector<Tensor> ts{points, scales, quats};
@@ -930,10 +960,22 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> projection_utgs(const CamSpec& spec, 
     all_contiguous(ts);
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(points.device());
     const int64_t N = points.size(0);
-    Tensor flags = at::empty({N}, points.options().dtype(at::kByte));
-    Tensor radii = at::empty({N, 2}, points.options());
-    Tensor mean2d = at::empty({N, 2}, points.options());
-    Tensor depths = at::empty({N}, points.options());
+    Tensor flags, radii, mean2d, depths;
+    if (out.has_value()) {
+        std::tie(flags, radii, mean2d, depths) = *out;
+        check_same_device({points, flags, radii, mean2d, depths});
+        TORCH_CHECK(flags.scalar_type() == at::kByte && radii.scalar_type() == at::kFloat &&
+                        mean2d.scalar_type() == at::kFloat && depths.scalar_type() == at::kFloat,
+                    "out: flags must be uint8, radii / means2d / depths float32");
+        TORCH_CHECK(flags.numel() == N && radii.numel() == 2 * N && mean2d.numel() == 2 * N && depths.numel() == N,
+                    "out: tensors for ", N, " points expected");
+        all_contiguous({flags, radii, mean2d, depths});
+    } else {
+        flags = at::empty({N}, points.options().dtype(at::kByte));
+        radii = at::empty({N, 2}, points.options());
+        mean2d = at::empty({N, 2}, points.options());
+        depths = at::empty({N}, points.options());
+    }
     check_rc(xsg_ut_project(spec.kind, phm ? 1 : 0, fptr(pack), N, fptr(points), fptr(points_velocity),
                             fptr(scales), fptr(quats), fptr(opacity), (float)width, (float)height, (float)ut_alpha,
                             (float)ut_beta, (float)ut_kappa, (float)thr, (float)max_res, (float)margin,
@@ -954,12 +996,14 @@ void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm) {
                    py::arg("tensors"));
     cls.def_static("camera_rays",
                    [spec](const Tensor& pack, int64_t width, int64_t height, bool world_space, bool normalized,
-                          bool return_origins, bool return_valid) {
+                          bool return_origins, bool return_valid,
+                          const std::optional<std::tuple<Tensor, Tensor>>& out) {
                        return camera_rays(spec, pack, width, height, world_space, normalized, return_origins,
-                                          return_valid);
+                                          return_valid, out);
                    },
                    py::arg("pack"), py::arg("width"), py::arg("height"), py::arg("world_space") = true,
-                   py::arg("normalized") = true, py::arg("return_origins") = true, py::arg("return_valid") = false);
+                   py::arg("normalized") = true, py::arg("return_origins") = true, py::arg("return_valid") = false,
+                   py::arg("out") = py::none());
     cls.def_static("pixel_time",
                    [spec](const Tensor& pack, int64_t w, int64_t h) { return pixel_time(spec, pack, w, h, false); },
                    py::arg("pack"), py::arg("width"), py::arg("height"));
@@ -986,15 +1030,16 @@ void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm) {
         cls.def_static(with_phm ? "projection_utgs_phm" : "projection_utgs",
                        [spec, with_phm](const Tensor& pack, const Tensor& points, const OptT& vel, const Tensor& scales,
                                         const Tensor& quats, const OptT& opacity, double width, double height,
-                                        double a, double b, double k, double thr, double max_res, double margin) {
+                                        double a, double b, double k, double thr, double max_res, double margin,
+                                        const UtOut& out) {
                            return projection_utgs(spec, with_phm != 0, pack, points, vel, scales, quats, opacity,
-                                                  width, height, a, b, k, thr, max_res, margin);
+                                                  width, height, a, b, k, thr, max_res, margin, out);
                        },
                        py::arg("pack"), py::arg("points"), py::arg("points_velocity"), py::arg("scales"),
                        py::arg("quats"), py::arg("opacity"), py::arg("width"), py::arg("height"),
                        py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f, py::arg("ut_kappa") = 0.0f,
                        py::arg("residual_thr_early_stop") = 1e-4f, py::arg("max_residual") = 0.002f,
-                       py::arg("max_margin") = 1.0f);
+                       py::arg("max_margin") = 1.0f, py::arg("out") = py::none());
     }
     if (spec.kind == XSG_CAM_DISTORTED || spec.kind == XSG_CAM_FISHEYE) {
         cls.def_static("undistort_map",

@@ -132,18 +132,22 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
                               for cam in st.cams])
     tsx, tsy = sc.tile_size
     ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
-    rays, proj = [], []
+    C, N = len(specs), st.means.shape[0]
+    dev = st.device
+    # every camera's rays and projections go straight into its slice of the rig's buffers
+    ray_o = torch.empty((C, H, W, 3), device=dev)
+    ray_d = torch.empty((C, H, W, 3), device=dev)
+    flags = torch.empty((C, N), dtype=torch.uint8, device=dev)
+    radii = torch.empty((C, N, 2), device=dev)
+    means2d = torch.empty((C, N, 2), device=dev)
+    depths = torch.empty((C, N), device=dev)
     with torch.no_grad():
-        for cam in st.cams:
+        for c, cam in enumerate(st.cams):
             with cam._freeze_ctx():
-                rays.append(cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True))
-                proj.append(cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac,
-                                                 use_phm=sc.use_phm))
-        ray_o = torch.stack([r[0] for r in rays])
-        ray_d = torch.stack([r[1] for r in rays])
-        radii = torch.stack([p[1] for p in proj])
-        means2d = torch.stack([p[2] for p in proj])
-        depths = torch.stack([p[3] for p in proj])
+                cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True,
+                                out=(ray_o[c], ray_d[c]))
+                cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac, use_phm=sc.use_phm,
+                                     out=(flags[c], radii[c], means2d[c], depths[c]))
         offsets = torch.empty((len(specs), nty, ntx), dtype=torch.int32, device=st.device)
         _, _, flatten_ids = isect_regular_tiles_batched(means2d, radii, depths, W, H, tsx, tsy, sort=True,
                                                         tile_offsets=offsets, keys=False)
