@@ -1038,11 +1038,11 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // The depth pre-order sorts the visible instances, usually a small part of the instances its grid
 // is sized for: 1024 keys per block spread them over four times as many workgroups. Large counts
-// (millions of visible instances: a lidar frame, a camera rig) run faster in tiles of 4096 keys
+// (millions of visible instances: a lidar frame, a camera rig) run faster in tiles of 2048 keys
 // (longer runs per digit in each tile's scatter). The count is known only on the device when the
 // pre-order is queued, so the previous call's visible count chooses (both sort identically).
 constexpr int kPresortItems = 4;
-constexpr int kPresortItemsLarge = 16;
+constexpr int kPresortItemsLarge = 8;
 constexpr int64_t kPresortLargeAt = 1500000;  // visible instances
 constexpr unsigned kPresortGrid = 2048;
 std::atomic<int64_t> g_visible_hint{0};
