@@ -90,6 +90,16 @@ int xsg_ut_project(int kind, int phm, const float* pack, int64_t n, const float*
                    float ut_kappa, float residual_thr, float max_residual, float max_margin,
                    uint8_t* flags, float* radii, float* means2d, float* depths, xsg_stream_t stream);
 
+/* Extension, no reference counterpart (the reference projects one camera per call,
+ * ut_kernels.h:249-305): the UT projection of one scene by n_cams cameras of one kind (pinhole,
+ * distorted or fisheye), packs [n_cams] at a stride of pack_stride floats; each Gaussian is read once
+ * and projected with every camera as xsg_ut_project does. Outputs are [n_cams, n] camera-major. */
+int xsg_ut_project_rig(int kind, int n_cams, const float* packs, int64_t pack_stride, int64_t n,
+                       const float* means, const float* velocity, const float* scales, const float* quats,
+                       const float* opacity, float width, float height, float ut_alpha, float ut_beta,
+                       float ut_kappa, float residual_thr, float max_residual, float max_margin,
+                       uint8_t* flags, float* radii, float* means2d, float* depths, xsg_stream_t stream);
+
 int xsg_project_points(int kind, const float* pack, int64_t n, const float* points,
                        const float* velocity, float residual_thr, float max_residual,
                        float max_margin, int mode, int no_jacobian, float* uvdt, uint8_t* mask,

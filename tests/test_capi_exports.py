@@ -120,6 +120,21 @@ def test_fill_without_keys_needs_tile_offsets(lib):
         assert b"keys may be left out" in lib.xsg_last_error()
 
 
+def test_rig_projection_rejects_before_launch(lib):
+    """xsg_ut_project_rig: phase-modelled kinds and a pack stride below the kind's pack size fail on
+    the host; placeholder pointers are never dereferenced."""
+    lib.xsg_last_error.restype = C.c_char_p
+    fake = C.c_void_p(1 << 20)
+    f = C.c_float
+    args = lambda kind, stride: (kind, 2, fake, C.c_int64(stride), C.c_int64(10), fake, None, fake, fake, None,
+                                 f(64), f(32), f(0.1), f(2.0), f(0.0), f(1e-4), f(2e-3), f(1.0), fake, fake, fake,
+                                 fake, None)
+    assert lib.xsg_ut_project_rig(*args(2, 23)) < 0
+    assert b"pinhole, distorted or fisheye" in lib.xsg_last_error()
+    assert lib.xsg_ut_project_rig(*args(0, 20)) == -1
+    assert b"pack stride" in lib.xsg_last_error()
+
+
 def test_misaligned_workspace_is_rejected_before_launch(lib):
     """Workspaces must be 256-byte aligned; the pointers here are placeholders that no call reaches."""
     lib.xsg_last_error.restype = C.c_char_p

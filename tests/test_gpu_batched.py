@@ -247,3 +247,44 @@ def test_projection_and_rays_into_preallocated_slices(dev):
     pack = cam.pack.detach().clone().requires_grad_(True)
     with pytest.raises(RuntimeError, match="needs no gradient"):
         cam.ext_cls.camera_rays(pack, W, H, out=(ro[0], rd[0]))
+
+
+@pytest.mark.parametrize("case", ["static_pinhole", "moving_pinhole", "distorted"])
+def test_rig_projection_matches_per_camera(dev, case):
+    """projection_utgs_rig (extension: one launch for a rig's cameras of one kind, each Gaussian read
+    once) equals projection_utgs per camera bit for bit: the cfg4 rig (static pinholes), the same rig
+    with moving poses and moving points, and a distorted-lens rig."""
+    sc = S.make_cfg4(seed=7, n=60_000, n_blobs=120)
+    specs = sc.cameras
+    if case != "static_pinhole":
+        specs = [S.CameraSpec(s.kind, s.width, s.height, s.q, s.t, s.impl, v=[1.5, -0.5, 0.1],
+                              w=[0.0, 0.02, 0.3], rolling=[0.02, 0.01], trigger_time=0.0, pose_time=0.01)
+                 for s in specs]
+    if case == "distorted":
+        specs = [S.CameraSpec("distorted", s.width, s.height, s.q, s.t, s.impl, v=s.v, w=s.w, rolling=s.rolling,
+                              trigger_time=s.trigger_time, pose_time=s.pose_time,
+                              dist=[-0.05, 0.01, 0.001, -0.001, 0.0, 0.0, 0.0, 0.0], max_radius=1.5)
+                 for s in specs]
+    cams = [frame.make_camera(s, dev) for s in specs]
+    T = lambda t: t.to(dev).contiguous()
+    means, scales, quats, opac = T(sc.means), T(sc.scales), T(sc.quats), T(sc.opacity)
+    vel = T(0.5 * torch.randn(sc.means.shape, generator=torch.Generator().manual_seed(3))) \
+        if case == "moving_pinhole" else None
+    W, H = specs[0].width, specs[0].height
+    c0 = cams[0]
+    kw = dict(residual_thr_early_stop=c0.residual_thr_early_stop, max_residual=c0.residual_max_valid,
+              max_margin=c0.max_margin)
+    got = c0.ext_cls.projection_utgs_rig(torch.cat([c.pack for c in cams]), means, vel, scales, quats, opac,
+                                         W, H, **kw)
+    assert [tuple(x.shape) for x in got] == [(6, 60_000), (6, 60_000, 2), (6, 60_000, 2), (6, 60_000)]
+    visible = 0
+    for ci, cam in enumerate(cams):
+        want = cam.ext_cls.projection_utgs(cam.pack, means, vel, scales, quats, opac, W, H, **kw)
+        for name, a, b in zip(("flags", "radii", "means2d", "depths"), got, want):
+            assert torch.equal(a[ci], b), (case, ci, name)
+        visible += int((want[0] > 0).sum())
+    print(case, "visible (camera, Gaussian) pairs", visible, flush=True)
+    assert visible > 60_000 // 2
+    with pytest.raises(RuntimeError, match="packs must be"):
+        c0.ext_cls.projection_utgs_rig(torch.cat([c.pack for c in cams])[:, :5].contiguous(), means, vel, scales,
+                                       quats, opac, W, H)

@@ -84,61 +84,84 @@ XSG_DEV bool ut_projection_static_pinhole(const Camera& c, const Mat3& m, const 
     return ix && iy;
 }
 
-// unscented_transform_kernel (include/cameras/ut_kernels.h:187-246). Every output element is
-// written (zeros for culled Gaussians), which replaces the reference's zero-initialised
-// allocations (ut_kernels.h:276-280) with a single pass. A static pinhole camera takes the lean
-// path above. One thread per Gaussian (two per thread, sharing the camera set-up, measured slower:
-// half as many wavefronts hide less latency; compacting the Gaussians that pass the centre test
-// before the sigma points, too).
+// One Gaussian's inputs, read once (a rig's projection reuses them for every camera).
+struct UtIn {
+    f3 pw, pv, sc;
+    float4 q;
+    float op;
+};
+
+XSG_DEV UtIn load_ut_in(int64_t i, const float* __restrict__ means, const float* __restrict__ vel,
+                        const float* __restrict__ scales, const float4* __restrict__ quats,
+                        const float* __restrict__ opacity) {
+    UtIn in;
+    in.op = opacity ? opacity[i] : 1.0f;
+    in.q = quats[i];
+    in.sc = ld3(scales + 3 * i);
+    in.pw = ld3(means + 3 * i);
+    in.pv = vel ? ld3(vel + 3 * i) : mk3(0.f, 0.f, 0.f);
+    return in;
+}
+
 template <int KIND>
-XSG_DEV void ut_project_one(int64_t i, const Camera& cam, bool is_static, const Mat3& m, const ProjParams& pp,
-                            const UtWeights& ut, f2 img, const float* __restrict__ means,
-                            const float* __restrict__ vel, const float* __restrict__ scales,
-                            const float4* __restrict__ quats, const float* __restrict__ opacity,
-                            uint8_t* __restrict__ flags, float2* __restrict__ radii, float2* __restrict__ means2d,
-                            float* __restrict__ depths) {
-    const float op = opacity ? opacity[i] : 1.0f;
-    uint8_t flag = 0;
-    f2 m2 = mk2(0.f, 0.f), r2 = mk2(0.f, 0.f);
-    float depth = 0.f;
-    if (op >= 1.0f / 255.0f) {
+XSG_DEV void ut_project_in(const UtIn& in, const Camera& cam, bool is_static, const Mat3& m, const ProjParams& pp,
+                           const UtWeights& ut, f2 img, uint8_t& flag, f2& m2, f2& r2, float& depth) {
+    flag = 0;
+    m2 = mk2(0.f, 0.f);
+    r2 = mk2(0.f, 0.f);
+    depth = 0.f;
+    if (in.op >= 1.0f / 255.0f) {
         f3 d[3];
         float dep = 0.f;
         f2 mm = mk2(0.f, 0.f), rr = mk2(0.f, 0.f);
         bool ok;
         if (KIND == XSG_CAM_PINHOLE && is_static) {
-            ut_deltas_rsq(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
-            ok = ut_projection_static_pinhole(cam, m, ut, img, pp, ld3(means + 3 * i), op, d, mm, rr, dep);
+            ut_deltas_rsq(ut.sqrt_dl, in.q, in.sc, d);
+            ok = ut_projection_static_pinhole(cam, m, ut, img, pp, in.pw, in.op, d, mm, rr, dep);
         } else {
-            ut_deltas(ut.sqrt_dl, quats[i], ld3(scales + 3 * i), d);
-            const f3 pv = vel ? ld3(vel + 3 * i) : mk3(0.f, 0.f, 0.f);
+            ut_deltas(ut.sqrt_dl, in.q, in.sc, d);
             float udist = 0.f;
-            ok = ut_projection<KIND>(cam, XSG_MODE_CENTRAL, ut, img, pp, ld3(means + 3 * i), pv, op, d, is_static,
-                                     mm, rr, dep, udist);
+            ok = ut_projection<KIND>(cam, XSG_MODE_CENTRAL, ut, img, pp, in.pw, in.pv, in.op, d, is_static, mm, rr,
+                                     dep, udist);
         }
         if (ok) {
             flag = 1; m2 = mm; r2 = rr; depth = dep;
         }
     }
-    flags[i] = flag;
-    radii[i] = make_float2(r2.x, r2.y);
-    means2d[i] = make_float2(m2.x, m2.y);
-    depths[i] = depth;
 }
 
+// unscented_transform_kernel (include/cameras/ut_kernels.h:187-246) over n_cams cameras of one kind
+// (one for projection_utgs; a rig's cameras, an extension, for projection_utgs_rig): each thread reads
+// its Gaussian once and projects it with every camera in camera order, so that a rig's projections
+// equal the single-camera ones bit for bit (one compiled path). Outputs are [n_cams, n]
+// camera-major; every element is written (zeros for culled Gaussians), which replaces the
+// reference's zero-initialised allocations (ut_kernels.h:276-280) with a single pass. A static
+// pinhole camera takes the lean path above. One thread per Gaussian (two per thread, sharing the
+// camera set-up, measured slower: half as many wavefronts hide less latency; compacting the Gaussians
+// that pass the centre test before the sigma points, too).
 template <int KIND>
 __global__ __launch_bounds__(kBlock) void ut_project_kernel(
-    int64_t n, const float* __restrict__ pack, ProjParams pp, UtWeights ut, f2 img,
+    int n_cams, int64_t n, const float* __restrict__ packs, int64_t pack_stride, ProjParams pp, UtWeights ut, f2 img,
     const float* __restrict__ means, const float* __restrict__ vel, const float* __restrict__ scales,
     const float4* __restrict__ quats, const float* __restrict__ opacity, uint8_t* __restrict__ flags,
     float2* __restrict__ radii, float2* __restrict__ means2d, float* __restrict__ depths) {
-    const Camera cam = load_camera(pack, KIND);
-    const bool is_static = camera_is_static(cam, vel != nullptr);
-    const Mat3 m = static_world_to_camera(cam);
     const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (i >= n) return;
-    ut_project_one<KIND>(i, cam, is_static, m, pp, ut, img, means, vel, scales, quats, opacity, flags, radii, means2d,
-                         depths);
+    const UtIn in = load_ut_in(i, means, vel, scales, quats, opacity);
+    for (int c = 0; c < n_cams; ++c) {  // uniform
+        const Camera cam = load_camera(packs + (int64_t)c * pack_stride, KIND);
+        const bool is_static = camera_is_static(cam, vel != nullptr);
+        const Mat3 m = static_world_to_camera(cam);
+        uint8_t flag;
+        f2 m2, r2;
+        float depth;
+        ut_project_in<KIND>(in, cam, is_static, m, pp, ut, img, flag, m2, r2, depth);
+        const int64_t o = (int64_t)c * n + i;
+        flags[o] = flag;
+        radii[o] = make_float2(r2.x, r2.y);
+        means2d[o] = make_float2(m2.x, m2.y);
+        depths[o] = depth;
+    }
 }
 
 // unscented_transform_phm_kernel (include/cameras/ut_phm_kernels.h:13-114), one instantiation per kind
@@ -761,11 +784,43 @@ extern "C" int xsg_ut_project(int kind, int phm, const float* pack, int64_t n, c
                 return;
             }
         }
-        ut_project_kernel<KIND><<<grid, block, 0, s>>>(n, pack, pp, ut, img, means, velocity, scales, q4, opacity,
-                                                       flags, r2, m2, depths);
+        ut_project_kernel<KIND><<<grid, block, 0, s>>>(1, n, pack, xsg_camera_pack_elements(kind), pp, ut, img, means,
+                                                       velocity, scales, q4, opacity, flags, r2, m2, depths);
     });
     if (rc != XSG_OK) return rc;
     XSG_TRY_LAUNCH("ut_project");
+    return XSG_OK;
+}
+
+extern "C" int xsg_ut_project_rig(int kind, int n_cams, const float* packs, int64_t pack_stride, int64_t n,
+                                  const float* means, const float* velocity, const float* scales, const float* quats,
+                                  const float* opacity, float width, float height, float ut_alpha, float ut_beta,
+                                  float ut_kappa, float residual_thr, float max_residual, float max_margin,
+                                  uint8_t* flags, float* radii, float* means2d, float* depths, xsg_stream_t stream) {
+    const int pe = xsg_camera_pack_elements(kind);
+    if (pe <= 0) return XSG_ERR_INVALID;
+    if (kind == XSG_CAM_SPHERICAL || kind == XSG_CAM_LIDAR)
+        return xsg_fail(XSG_ERR_UNSUPPORTED, "xsg_ut_project_rig takes pinhole, distorted or fisheye cameras");
+    if (n < 0 || n_cams < 0 || pack_stride < pe)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_ut_project_rig: bad arguments (pack stride %lld for %d elements)",
+                        (long long)pack_stride, pe);
+    if (n == 0 || n_cams == 0) return XSG_OK;
+    if (!packs || !means || !scales || !quats || !flags || !radii || !means2d || !depths)
+        return xsg_fail(XSG_ERR_INVALID, "xsg_ut_project_rig: null tensor");
+    const ProjParams pp{residual_thr, max_residual, max_margin};
+    const UtWeights ut = ut_weights(ut_alpha, ut_beta, ut_kappa);
+    const f2 img = mk2(width, height);
+    const hipStream_t s = (hipStream_t)stream;
+    const int rc = xsg_with_camera_kind(kind, [&](auto k) {
+        constexpr int KIND = decltype(k)::value;
+        if constexpr (KIND != XSG_CAM_SPHERICAL && KIND != XSG_CAM_LIDAR)
+            ut_project_kernel<KIND><<<xsg_blocks(n, kBlock), kBlock, 0, s>>>(
+                n_cams, n, packs, pack_stride, pp, ut, img, means, velocity, scales,
+                reinterpret_cast<const float4*>(quats), opacity, flags, reinterpret_cast<float2*>(radii),
+                reinterpret_cast<float2*>(means2d), depths);
+    });
+    if (rc != XSG_OK) return rc;
+    XSG_TRY_LAUNCH("ut_project_rig");
     return XSG_OK;
 }
 

@@ -984,6 +984,37 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> projection_utgs(const CamSpec& spec, 
     return {flags, radii, mean2d, depths};
 }
 
+// projection_utgs over a rig (extension): packs [C, pack elements] of C cameras of this kind, one
+// launch; returns flags [C, N], radii [C, N, 2], means2d [C, N, 2], depths [C, N]
+std::tuple<Tensor, Tensor, Tensor, Tensor> projection_utgs_rig(const CamSpec& spec, const Tensor& packs,
+                                                               const Tensor& points, const OptT& points_velocity,
+                                                               const Tensor& scales, const Tensor& quats,
+                                                               const OptT& opacity, double width, double height,
+                                                               double ut_alpha, double ut_beta, double ut_kappa,
+                                                               double thr, double max_res, double margin) {
+    TORCH_CHECK(packs.is_cuda() && packs.dtype() == at::kFloat && packs.is_contiguous() && packs.dim() == 2 &&
+                    packs.size(1) == xsg_camera_pack_elements(spec.kind),
+                "packs must be a contiguous float32 CUDA tensor of [cameras, ", xsg_camera_pack_elements(spec.kind),
+                "]");
+    check_same_device({packs, points, scales, quats});
+    std::vector<Tensor> ts{points, scales, quats};
+    if (points_velocity.has_value()) ts.push_back(*points_velocity);
+    if (opacity.has_value()) ts.push_back(*opacity);
+    all_contiguous(ts);
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(points.device());
+    const int64_t C = packs.size(0), N = points.size(0);
+    Tensor flags = at::empty({C, N}, points.options().dtype(at::kByte));
+    Tensor radii = at::empty({C, N, 2}, points.options());
+    Tensor mean2d = at::empty({C, N, 2}, points.options());
+    Tensor depths = at::empty({C, N}, points.options());
+    check_rc(xsg_ut_project_rig(spec.kind, (int)C, fptr(packs), packs.size(1), N, fptr(points),
+                                fptr(points_velocity), fptr(scales), fptr(quats), fptr(opacity), (float)width,
+                                (float)height, (float)ut_alpha, (float)ut_beta, (float)ut_kappa, (float)thr,
+                                (float)max_res, (float)margin, flags.data_ptr<uint8_t>(), radii.data_ptr<float>(),
+                                mean2d.data_ptr<float>(), depths.data_ptr<float>(), stream_of(points)));
+    return {flags, radii, mean2d, depths};
+}
+
 template <int I>
 struct CameraTag {};
 
@@ -1041,6 +1072,19 @@ void bind_camera(py::module& m, const char* name, CamSpec spec, bool phm) {
                        py::arg("residual_thr_early_stop") = 1e-4f, py::arg("max_residual") = 0.002f,
                        py::arg("max_margin") = 1.0f, py::arg("out") = py::none());
     }
+    if (!phm)
+        cls.def_static("projection_utgs_rig",
+                       [spec](const Tensor& packs, const Tensor& points, const OptT& vel, const Tensor& scales,
+                              const Tensor& quats, const OptT& opacity, double width, double height, double a,
+                              double b, double k, double thr, double max_res, double margin) {
+                           return projection_utgs_rig(spec, packs, points, vel, scales, quats, opacity, width,
+                                                      height, a, b, k, thr, max_res, margin);
+                       },
+                       py::arg("packs"), py::arg("points"), py::arg("points_velocity"), py::arg("scales"),
+                       py::arg("quats"), py::arg("opacity"), py::arg("width"), py::arg("height"),
+                       py::arg("ut_alpha") = 0.1f, py::arg("ut_beta") = 2.0f, py::arg("ut_kappa") = 0.0f,
+                       py::arg("residual_thr_early_stop") = 1e-4f, py::arg("max_residual") = 0.002f,
+                       py::arg("max_margin") = 1.0f);
     if (spec.kind == XSG_CAM_DISTORTED || spec.kind == XSG_CAM_FISHEYE) {
         cls.def_static("undistort_map",
                        [spec](const Tensor& pack, int64_t width, int64_t height, bool normalized_range) {

@@ -8,6 +8,7 @@ activations and the SH call are the caller's, as in the reference.
 """
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass, field
 
 import torch
@@ -134,18 +135,30 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
     ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
     C, N = len(specs), st.means.shape[0]
     dev = st.device
-    # every camera's rays and projections go straight into its slice of the rig's buffers
+    # every camera's rays go straight into its slice of the rig's buffers; cameras of one kind project
+    # in one launch that reads each Gaussian once, others one camera at a time into their slices
     ray_o = torch.empty((C, H, W, 3), device=dev)
     ray_d = torch.empty((C, H, W, 3), device=dev)
-    flags = torch.empty((C, N), dtype=torch.uint8, device=dev)
-    radii = torch.empty((C, N, 2), device=dev)
-    means2d = torch.empty((C, N, 2), device=dev)
-    depths = torch.empty((C, N), device=dev)
-    with torch.no_grad():
+    one_kind = len({type(cam) for cam in st.cams}) == 1
+    with torch.no_grad(), contextlib.ExitStack() as frozen:
+        for cam in st.cams:
+            frozen.enter_context(cam._freeze_ctx())
         for c, cam in enumerate(st.cams):
-            with cam._freeze_ctx():
-                cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True,
-                                out=(ray_o[c], ray_d[c]))
+            cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True,
+                            out=(ray_o[c], ray_d[c]))
+        if one_kind:
+            cam0 = st.cams[0]
+            flags, radii, means2d, depths = cam0.ext_cls.projection_utgs_rig(
+                torch.cat([cam.pack for cam in st.cams]), st.means.contiguous(), None, scales.contiguous(),
+                st.quats.contiguous(), opac.contiguous(), width=W, height=H,
+                residual_thr_early_stop=cam0.residual_thr_early_stop, max_residual=cam0.residual_max_valid,
+                max_margin=cam0.max_margin)
+        else:
+            flags = torch.empty((C, N), dtype=torch.uint8, device=dev)
+            radii = torch.empty((C, N, 2), device=dev)
+            means2d = torch.empty((C, N, 2), device=dev)
+            depths = torch.empty((C, N), device=dev)
+            for c, cam in enumerate(st.cams):
                 cam.ut_gs_projection(st.means, scales, st.quats, W, H, opacity=opac, use_phm=sc.use_phm,
                                      out=(flags[c], radii[c], means2d[c], depths[c]))
         offsets = torch.empty((len(specs), nty, ntx), dtype=torch.int32, device=st.device)
