@@ -379,6 +379,15 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             _, _, alpha_b, last_b = _C.rasterize_eval3d_fwd_batched(means, quats, scales, col_b, opac, W, H, tsx, tsy,
                                                                     ro_b, rd_b, off_b, fl_b)
             n_col = 1 if col_b.dim() == 2 else n_cams
+            if len({type(c["cam"]) for c in info}) == 1:
+                # the rig's cameras of one kind project in one launch, each Gaussian read once: its inputs
+                # (44 B) once, every camera's outputs (21 B)
+                packs_b = torch.cat([c["cam"].pack for c in info])
+                cam0 = info[0]["cam"]
+                stages["ut_projection"] = (
+                    lambda: cam0.ext_cls.projection_utgs_rig(packs_b, means, None, scales, quats, opac, W, H),
+                    44 * N + 21 * N * n_cams)
+                per_frame |= {"ut_projection"}
             stages["binning"] = (
                 lambda: _C.isect_regular_tiles_batched(m2_b, radii_b, dep_b, W, H, tsx, tsy,
                                                        tile_offsets=torch.empty_like(off_b), keys=False),
