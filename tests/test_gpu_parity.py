@@ -169,9 +169,9 @@ def test_isect_regular_many_visible(dev):
 
 
 def test_isect_presort_tile_sizes(dev):
-    """The depth pre-order picks its tile size (1024 or 4096 keys) from the previous call's visible
+    """The depth pre-order picks its tile size (1024 or 2048 keys) from the previous call's visible
     count; both must order the keys identically. A small binning sets the hint low, then the same
-    1.6 M-Gaussian scene is binned twice (the second call with 4096-key tiles); both match the
+    1.6 M-Gaussian scene is binned twice (the second call with 2048-key tiles); both match the
     oracle."""
     g = np.random.default_rng(23)
     T = lambda a: torch.from_numpy(a).to(dev)
