@@ -605,6 +605,12 @@ def test_fill_without_keys(dev, cfg0, case):
     assert torch.equal(tpg_k, tpg_n) and torch.equal(fl_k, fl_n) and torch.equal(off_k, off_n)
     enc = _C.isect_offset_encode(ids_k, shape[-1], shape[-2], n_cams)
     assert np.array_equal(np_(enc).reshape(-1), np_(off_k).reshape(-1))
+    if case == "regular":  # nothing visible: no keys, no ids, every offset 0
+        off0 = torch.full(shape, -7, dtype=torch.int32, device=dev)
+        tpg0, ids0, fl0 = _C.isect_regular_tiles(m2 + 1e6, radii, dep, spec.width, spec.height, 16, 16,
+                                                 tile_offsets=off0, keys=False)
+        assert ids0.numel() == 0 and fl0.numel() == 0 and int(tpg0.abs().max()) == 0
+        assert int(off0.abs().max()) == 0
     with pytest.raises(RuntimeError, match="keys=False needs tile_offsets"):
         _C.isect_regular_tiles(m2.reshape(-1, 2)[:100].contiguous(), radii.reshape(-1, 2)[:100].contiguous(),
                                dep.reshape(-1)[:100].contiguous(), 64, 64, 16, 16, keys=False)
