@@ -256,8 +256,12 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
 
 // Second spans of the queued seam Gaussians (phm_lidar_tiling.cu:183-229): re-projected with
 // PositiveDelta, binned past the tile boundary after u_pose and keyed with the re-projected depth
-// (virtual instance 2j + 1). One wavefront per count block walks that block's slice of the queue;
-// it alone adds the block's second spans to the block's partials, before the compaction reads them.
+// (virtual instance 2j + 1). A workgroup takes the queues of kSeamBlocks consecutive count blocks (a
+// few seam Gaussians each) and spreads them over its threads, one Gaussian per thread, so that the
+// re-projections run on mostly full wavefronts; it alone adds those blocks' second spans to their
+// partials, before the compaction reads them.
+constexpr int kSeamBlocks = 16;
+
 template <int KIND, bool LIDAR>
 __global__ __launch_bounds__(kBlock) void seam_span_kernel(
     unsigned n_count_blocks, const uint32_t* __restrict__ seam_cnt, const uint32_t* __restrict__ seam_ids,
@@ -267,17 +271,25 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
     float v_per_tile, int ntx, int n_v, int32_t* __restrict__ tpg, Rect* __restrict__ rects,
     uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey, uint64_t* __restrict__ partials,
     uint64_t* __restrict__ cpart) {
-    const unsigned blk = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    if (blk >= n_count_blocks) return;  // wavefront-uniform
-    const uint32_t count = seam_cnt[blk];
-    if (count == 0) return;
+    __shared__ uint32_t s_off[kSeamBlocks + 1];
+    __shared__ uint32_t s_vis[kSeamBlocks], s_cnt[kSeamBlocks], s_rows[kSeamBlocks];
+    const unsigned blk0 = blockIdx.x * kSeamBlocks;
+    const int nb = (int)min<unsigned>(kSeamBlocks, n_count_blocks - blk0);
+    if (threadIdx.x == 0) {
+        uint32_t o = 0;
+        for (int b = 0; b < nb; ++b) { s_off[b] = o; o += seam_cnt[blk0 + b]; }
+        s_off[nb] = o;
+    }
+    if (threadIdx.x < kSeamBlocks) { s_vis[threadIdx.x] = 0; s_cnt[threadIdx.x] = 0; s_rows[threadIdx.x] = 0; }
+    __syncthreads();
+    const uint32_t total = s_off[nb];
+    if (total == 0) return;  // workgroup-uniform
     const Camera cam = load_camera(pack, KIND);
     const bool is_static = camera_is_static(cam, vel != nullptr);
-    const int lane = __lane_id();
-    const int64_t base = (int64_t)blk * (kCountTile / 2);
-    uint32_t n_vis = 0, n_cnt = 0, n_rows = 0;
-    for (uint32_t q = lane; q < count; q += 64) {
-        const int64_t j = seam_ids[base + q];
+    for (uint32_t q = threadIdx.x; q < total; q += kBlock) {
+        int b = 0;
+        while (b + 1 < nb && s_off[b + 1] <= q) ++b;
+        const int64_t j = seam_ids[(int64_t)(blk0 + b) * (kCountTile / 2) + (q - s_off[b])];
         f3 d[3];
         ut_deltas(ut.sqrt_dl, quats[j], ld3(scales + 3 * j), d);
         const float op = opacity ? opacity[j] : 1.0f;
@@ -298,30 +310,26 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
             u_max = floorf(u_pose / u_per_tile) * u_per_tile - 1e-6f;
         }
         const float mx2 = m2.x / img.x, my2 = m2.y / img.y, rx2 = r2.x / img.x, ry2 = r2.y / img.y;
-        Rect b;
-        if (LIDAR) b = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev, ntx);
-        else b = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
-        const uint32_t cb = rect_count(b);
-        rects[2 * j + 1] = b;
+        Rect r;
+        if (LIDAR) r = lidar_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_elev, elev, ntx);
+        else r = spherical_rect(mx2, my2, rx2, ry2, u_min, u_max, u_per_tile, n_v, v_per_tile, ntx);
+        const uint32_t cb = rect_count(r);
+        rects[2 * j + 1] = r;
         vcnt[2 * j + 1] = cb;
         vkey[2 * j + 1] = __float_as_uint(dd);
         if (cb > 0) {
             tpg[j] += (int32_t)cb;
-            n_vis += 1;
-            n_cnt += cb;
-            n_rows += (uint32_t)(b.y1 - b.y0);
+            atomicAdd(&s_vis[b], 1u);
+            atomicAdd(&s_cnt[b], cb);
+            atomicAdd(&s_rows[b], (uint32_t)(r.y1 - r.y0));
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        n_vis += (uint32_t)__shfl_xor((int)n_vis, off, 64);
-        n_cnt += (uint32_t)__shfl_xor((int)n_cnt, off, 64);
-        n_rows += (uint32_t)__shfl_xor((int)n_rows, off, 64);
-    }
-    if (lane == 0 && n_vis > 0) {
-        partials[blk] += ((uint64_t)n_vis << 32) + n_cnt;
-        cpart[2 * blk] += n_cnt;
-        cpart[2 * blk + 1] += n_rows;
+    __syncthreads();
+    if ((int)threadIdx.x < nb && s_vis[threadIdx.x] > 0) {
+        const unsigned blk = blk0 + threadIdx.x;
+        partials[blk] += ((uint64_t)s_vis[threadIdx.x] << 32) + s_cnt[threadIdx.x];
+        cpart[2 * blk] += s_cnt[threadIdx.x];
+        cpart[2 * blk + 1] += s_rows[threadIdx.x];
     }
 }
 
@@ -1238,7 +1246,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         const f2 img = mk2(d->img_width, d->img_height);
         const float u_per_tile = (float)d->tile_w / d->img_width;
         const float v_per_tile = (float)d->tile_h / d->img_height;
-        const unsigned seam_grid = (w.nb + kWaves - 1) / kWaves;
+        const unsigned seam_grid = (w.nb + kSeamBlocks - 1) / kSeamBlocks;
         if (g.kind == XSG_TILING_LIDAR) {
             count_spherical_kernel<XSG_CAM_LIDAR, true><<<w.nb, kBlock, 0, s>>>(
                 nt, d->camera_pack, img, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
