@@ -288,3 +288,22 @@ def test_rig_projection_matches_per_camera(dev, case):
     with pytest.raises(RuntimeError, match="packs must be"):
         c0.ext_cls.projection_utgs_rig(torch.cat([c.pack for c in cams])[:, :5].contiguous(), means, vel, scales,
                                        quats, opac, W, H)
+
+
+def test_render_rig_mixed_kinds_matches_camera_loop(dev):
+    """A rig of two camera kinds (pinholes and distorted-lens cameras of one image size) projects
+    camera by camera into its slices instead of in one launch; its images equal render_frame per camera."""
+    sc = S.make_cfg4(seed=9, n=60_000, n_blobs=120)
+    sc.cameras = [s if i % 2 == 0 else
+                  S.CameraSpec("distorted", s.width, s.height, s.q, s.t, s.impl,
+                               dist=[-0.04, 0.01, 0.0005, -0.0005, 0.0, 0.0, 0.0, 0.0], max_radius=1.5)
+                  for i, s in enumerate(sc.cameras)]
+    st = frame.prepare(sc, dev, requires_grad=False)
+    assert frame.rig_batchable(st) and len({type(c) for c in st.cams}) == 2
+    with torch.no_grad():
+        rig = frame.render_rig(st)
+        for ci in range(len(sc.cameras)):
+            o = frame.render_frame(st, cam_index=ci)
+            for k in ("rgb", "depth", "alpha"):
+                assert torch.equal(rig[k][ci], o[k]), (ci, k)
+            assert torch.equal(rig["radii"][ci], o["radii"]) and torch.equal(rig["depths"][ci], o["depths"])
