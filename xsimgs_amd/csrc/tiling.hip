@@ -751,6 +751,99 @@ __global__ __launch_bounds__(kBlock) void seg_count_kernel(int n_real, const uin
     }
 }
 
+// seg_count_kernel with row_segments_kernel's work done by every workgroup, for up to kFusedRows row
+// buckets: each derives the row starts (from the run sort's digit totals when given, else from
+// row_start) and the segment bases, finds its own segment's row, and counts as seg_count_kernel does;
+// workgroup 0 stores the row starts and bases and each workgroup its segment's row, for the kernels
+// after it. One launch fewer per fill.
+constexpr int kFusedRows = 1024;
+
+__global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, const uint32_t* __restrict__ row_count,
+                                                                const uint4* __restrict__ rec,
+                                                                uint32_t* __restrict__ row_start,
+                                                                uint32_t* __restrict__ seg_base,
+                                                                uint32_t* __restrict__ seg_row, int ntx,
+                                                                uint32_t* __restrict__ slots) {
+    extern __shared__ int32_t s_diff[];  // ntx + 1
+    __shared__ int32_t lds[kWaves];
+    __shared__ uint32_t s_rs[kFusedRows + 1], s_sb[kFusedRows + 1];
+    __shared__ uint32_t s_lds[kWaves];
+    const int n_real = n_rows - 1;
+    {
+        // row starts: consecutive rows per thread, one block scan
+        const int per = (n_rows + kBlock - 1) / kBlock;
+        const int q0 = threadIdx.x * per, q1 = min(n_rows, q0 + per);
+        if (row_count) {
+            uint32_t c = 0;
+            for (int r = q0; r < q1; ++r) c += row_count[r];
+            uint32_t tot;
+            uint32_t run = block_exclusive_scan<uint32_t>(c, s_lds, tot);
+            for (int r = q0; r < q1; ++r) {
+                s_rs[r] = run;
+                run += row_count[r];
+            }
+            if (threadIdx.x == 0) s_rs[n_rows] = tot;
+        } else {
+            for (int r = threadIdx.x; r <= n_rows; r += kBlock) s_rs[r] = row_start[r];
+        }
+    }
+    __syncthreads();
+    {
+        // segments per real row, one block scan
+        const int per = (n_real + kBlock - 1) / kBlock;
+        const int r0 = threadIdx.x * per, r1 = min(n_real, r0 + per);
+        uint32_t sum = 0;
+        for (int r = r0; r < r1; ++r) sum += (s_rs[r + 1] - s_rs[r] + kRunSeg - 1) / kRunSeg;
+        uint32_t tot;
+        uint32_t run = block_exclusive_scan<uint32_t>(sum, s_lds, tot);
+        for (int r = r0; r < r1; ++r) {
+            s_sb[r] = run;
+            run += (s_rs[r + 1] - s_rs[r] + kRunSeg - 1) / kRunSeg;
+        }
+        if (threadIdx.x == 0) s_sb[n_real] = tot;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (row_count)
+            for (int r = threadIdx.x; r <= n_rows; r += kBlock) row_start[r] = s_rs[r];
+        for (int r = threadIdx.x; r <= n_real; r += kBlock) seg_base[r] = s_sb[r];
+    }
+    const uint32_t sg = blockIdx.x;
+    if (sg >= s_sb[n_real]) return;  // workgroup-uniform
+    // the segment's row: the last r with s_sb[r] <= sg (rows without segments share a base with the
+    // next row, and the search takes the later one)
+    int lo = 0, hi = n_real - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_sb[mid] <= sg) lo = mid; else hi = mid - 1;
+    }
+    const uint32_t row = (uint32_t)lo;
+    if (threadIdx.x == 0) seg_row[sg] = row;
+    const uint32_t sb = s_sb[row], nseg = s_sb[row + 1] - sb;
+    const uint32_t k = sg - sb;
+    const int64_t b = (int64_t)s_rs[row] + (int64_t)k * kRunSeg;
+    const int64_t e = min((int64_t)s_rs[row + 1], b + kRunSeg);
+    for (int c = threadIdx.x; c <= ntx; c += kBlock) s_diff[c] = 0;
+    __syncthreads();
+    for (int64_t i = b + threadIdx.x; i < e; i += kBlock) {
+        const uint32_t x01 = rec[i].z;
+        atomicAdd(&s_diff[x01 & 0xffffu], 1);
+        atomicAdd(&s_diff[x01 >> 16], -1);
+    }
+    __syncthreads();
+    const int per = (ntx + kBlock - 1) / kBlock;
+    const int c0 = threadIdx.x * per, c1 = min(ntx, c0 + per);
+    int32_t sum = 0;
+    for (int c = c0; c < c1; ++c) sum += s_diff[c];
+    int32_t tot;
+    int32_t run = block_exclusive_scan<int32_t>(sum, lds, tot);
+    uint32_t* out = slots + (int64_t)sb * ntx + k;
+    for (int c = c0; c < c1; ++c) {
+        run += s_diff[c];
+        out[(int64_t)c * nseg] = (uint32_t)run;
+    }
+}
+
 // Per tile (real row, column): exclusive prefix of its segments' counts in place (the slots of a
 // tile are consecutive), and the tile's total into tile_tot. One wavefront per tile, lanes over the
 // tile's segments.
@@ -1395,12 +1488,18 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     if (fw.passes > 1)
         row_start_kernel<<<xsg_blocks(n_runs + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
                                                                          fw.row_start);
-    row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, fw.passes == 1 ? fw.dtot : nullptr, fw.row_start,
-                                             fw.seg_base, fw.seg_row);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals
-    seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
-        n_real, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
+    if (fw.n_rows <= kFusedRows) {
+        seg_count_rows_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
+            fw.n_rows, fw.passes == 1 ? fw.dtot : nullptr, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx,
+            fw.slots);
+    } else {
+        row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, fw.passes == 1 ? fw.dtot : nullptr, fw.row_start,
+                                                 fw.seg_base, fw.seg_row);
+        seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
+            n_real, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
+    }
     const int64_t n_tile_slots = (int64_t)n_real * g.ntx;
     tile_prefix_kernel<<<xsg_blocks(n_tile_slots * 64, kBlock), kBlock, 0, s>>>(fw.slots, fw.seg_base, n_real,
                                                                                g.ntx, fw.tile_tot);
