@@ -869,45 +869,44 @@ __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restric
 
 // single block of 1024 threads: exclusive scan of tile_tot[0, n) in place (the first position of
 // every tile of the real rows), the total -- where the negative-depth entries start -- at tile_tot[n];
-// with `offsets`, the same positions as int32 (the tile offsets). Chunks of 1024 consecutive entries,
-// one per thread (coalesced), eight chunks' loads in flight. (Eight consecutive entries per thread
-// with one block-wide scan measured slower: 11.9 against 7.3 us, its strided loads coalesce worse.)
+// with `offsets`, the same positions as int32 (the tile offsets). Each wavefront owns a contiguous
+// range: it sums its range (coalesced 64-entry chunks, all loads in flight), one barrier gives every
+// wavefront the sum of the ranges before it, and it then scans its range chunk by chunk (the second
+// read hits the cache): 7.7 µs at cfg2's 8160 tiles and 21 µs at the six-camera rig's 34 k. (Chunks of
+// 1024 entries across the block, two barriers per chunk, took 9 and 23-31 µs; eight consecutive entries
+// per thread, 11.9 µs at cfg2.)
 constexpr int kScanThreads = 1024;
-constexpr int kScanChunks = 8;
 __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n,
                                                                  int32_t* __restrict__ offsets) {
-    __shared__ uint32_t lds[kScanThreads / 64];
-    const int wave = threadIdx.x >> 6;
-    uint32_t carry = 0;
-    for (int64_t s0 = 0; s0 < n; s0 += (int64_t)kScanThreads * kScanChunks) {
-        uint32_t x[kScanChunks];
+    constexpr int NW = kScanThreads / 64;
+    __shared__ uint32_t s_tot[NW];
+    const int wave = threadIdx.x >> 6, lane = __lane_id();
+    const int64_t per = ((n + NW - 1) / NW + 63) / 64 * 64;  // whole chunks per wavefront
+    const int64_t w0 = min(n, (int64_t)wave * per), w1 = min(n, w0 + per);
+    uint32_t sum = 0;
+    for (int64_t i = w0 + lane; i < w1; i += 64) sum += a[i];
 #pragma unroll
-        for (int j = 0; j < kScanChunks; ++j) {
-            const int64_t i = s0 + (int64_t)j * kScanThreads + threadIdx.x;
-            x[j] = i < n ? a[i] : 0u;
-        }
+    for (int off = 32; off >= 1; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, 64);
+    if (lane == 0) s_tot[wave] = sum;
+    __syncthreads();
+    uint32_t carry = 0, total = 0;
 #pragma unroll
-        for (int j = 0; j < kScanChunks; ++j) {
-            const int64_t i = s0 + (int64_t)j * kScanThreads + threadIdx.x;
-            const uint32_t inc = wave_inclusive_scan(x[j]);
-            if (__lane_id() == 63) lds[wave] = inc;
-            __syncthreads();
-            uint32_t before = 0, tot = 0;
-#pragma unroll
-            for (int w = 0; w < kScanThreads / 64; ++w) {
-                const uint32_t y = lds[w];
-                if (w < wave) before += y;
-                tot += y;
-            }
-            __syncthreads();
-            if (i < n) {
-                a[i] = carry + before + inc - x[j];
-                if (offsets) offsets[i] = (int32_t)(carry + before + inc - x[j]);
-            }
-            carry += tot;
-        }
+    for (int w = 0; w < NW; ++w) {
+        const uint32_t t = s_tot[w];
+        if (w < wave) carry += t;
+        total += t;
     }
-    if (threadIdx.x == 0) a[n] = carry;
+    for (int64_t c0 = w0; c0 < w1; c0 += 64) {
+        const int64_t i = c0 + lane;
+        const uint32_t x = i < w1 ? a[i] : 0u;
+        const uint32_t inc = wave_inclusive_scan(x);
+        if (i < w1) {
+            a[i] = carry + inc - x;
+            if (offsets) offsets[i] = (int32_t)(carry + inc - x);
+        }
+        carry += (uint32_t)__shfl((int)inc, 63, 64);
+    }
+    if (threadIdx.x == 0) a[n] = total;
 }
 
 // Runs of negative-depth instances, after every tile, in run order; each run's entries consecutive
