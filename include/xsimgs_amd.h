@@ -7,7 +7,8 @@
  * rejected with XSG_ERR_INVALID), and returns XSG_OK or a negative error code; xsg_last_error()
  * then holds a message (thread-local). Work is enqueued on `stream`; the only blocking call is
  * xsg_isect_count, which copies the intersection total to the host (as the reference's
- * `.item()` does).
+ * `.item()` does); the pinned host buffer it reads that through is the C-ABI's one host allocation
+ * (per host thread and device, freed by xsg_release_thread_resources).
  *
  * Reference interfaces replaced (whesense/xsimgs, pybind module xsimgs._C):
  *   xsg_ut_project            <Camera>.projection_utgs[_phm]   include/cameras/bind.h:82-114,
@@ -246,9 +247,19 @@ size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d);
 /* Pass 1: tiles per Gaussian into tiles_per_gauss [n_cams*n]; on the host, *n_isects receives the
  * total, *n_visible the number of non-empty spans and *n_runs the number of (span, tile row) runs,
  * which xsg_isect_fill takes back. Blocks on `stream` for that one device->host copy.
- * `workspace` carries state into xsg_isect_fill. */
+ * `workspace` carries state into xsg_isect_fill.
+ * Host resources: the totals arrive in a 64-byte mapped pinned host buffer (hipHostMalloc) with one
+ * event, created on a host thread's first call on a device and reused by that thread's later calls
+ * on it; they stay allocated until that thread calls xsg_release_thread_resources. */
 int xsg_isect_count(const xsg_isect_desc* d, int32_t* tiles_per_gauss, void* workspace,
                     int64_t* n_isects, int64_t* n_visible, int64_t* n_runs, xsg_stream_t stream);
+
+/* Frees the calling host thread's xsg_isect_count readback buffers and events (every device it used;
+ * a later count allocates them again). A caller whose binding threads end, or that wants the pinned
+ * memory back, calls it from each such thread once its counts have returned. No reference
+ * counterpart: the reference reads its totals with `.item()` through torch's allocator
+ * (regular_tiling.cu:112, phm_lidar_tiling.cu:316). */
+int xsg_release_thread_resources(void);
 
 size_t xsg_isect_fill_workspace_bytes(const xsg_isect_desc* d, int64_t n_isects, int64_t n_visible,
                                       int64_t n_runs);

@@ -430,13 +430,16 @@ def eval3d_fwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, fla
 
 def eval3d_bwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, flatten_ids, render_alpha,
                last_ids, v_rgb, v_depth, v_alpha, tile_w=16, tile_h=16, velocity=None,
-               ray_time_delta=None, prec="f32", tiles=None):
+               ray_time_delta=None, prec="f32", tiles=None, abs_sums=False, und_mode=0):
     """rasterize_eval3d_[dynamic_]bwd (eval3d_bwd.cu:66-403; eval3d_dynamic_bwd.cu:312-432).
 
     Returns a dict with ``v_means, v_quats, v_scales, v_opacity, v_colors, v_ray_o, v_ray_d``
     (+ ``v_velocity, v_time_delta`` in the dynamic case). ``tiles`` (tile indices) restricts the
     sum to the pixels of those tiles (the gradients of a loss whose upstream gradients are zero
-    elsewhere).
+    elsewhere). With ``abs_sums`` also ``abs``: for each of those names, the sum of the magnitudes
+    of the per-pair contributions to each element (the conditioning of its float sum).
+    ``und_mode`` 1 / 2 takes / drops every pair whose alpha test (1/255) or geometry gate (0.99)
+    float32 rounding can decide either way (the forward's alpha error bound; f64 diagnostics).
     """
     _, nt = _real(prec)
     means, quats, scales = _arr(means, nt), _arr(quats, nt), _arr(scales, nt)
@@ -457,14 +460,31 @@ def eval3d_bwd(means, quats, scales, colors, opacity, ray_o, ray_d, offsets, fla
         out["v_velocity"] = np.zeros((n, 3), nt)
         out["v_time_delta"] = np.zeros((h, w), nt)
     tmask = _tile_mask(tiles, ntw, nth)   # kept alive across the call
+    ag = 11 + cdim + (3 if velocity is not None else 0)
+    abs_g = np.zeros((n, ag), nt) if abs_sums else None
+    abs_px = np.zeros((h, w, 7), nt) if abs_sums else None
     _lib(prec).orc_eval3d_bwd(
         C.c_int(cdim), _p(means), _p(quats), _p(scales), _p(colors), _p(opacity), _p(velocity), _p(rtd),
         C.c_int(w), C.c_int(h), C.c_int(tile_w), C.c_int(tile_h), _p(ray_o), _p(ray_d), _p(offsets),
         C.c_int(ntw), C.c_int(nth), C.c_int64(flatten_ids.shape[0]), _p(flatten_ids), _p(render_alpha),
         _p(last_ids), _p(v_rgb), _p(v_depth), _p(v_alpha), _p(out["v_means"]), _p(out["v_quats"]),
         _p(out["v_scales"]), _p(out["v_opacity"]), _p(out["v_colors"]), _p(out["v_ray_o"]),
-        _p(out["v_ray_d"]), _p(out.get("v_velocity")), _p(out.get("v_time_delta")), _p(tmask))
+        _p(out["v_ray_d"]), _p(out.get("v_velocity")), _p(out.get("v_time_delta")), _p(tmask), _p(abs_g),
+        _p(abs_px), C.c_int(und_mode))
+    if abs_sums:
+        a = dict(v_means=abs_g[:, 0:3], v_quats=abs_g[:, 3:7], v_scales=abs_g[:, 7:10], v_opacity=abs_g[:, 10],
+                 v_colors=abs_g[:, 11:11 + cdim] if cdim else None, v_ray_o=abs_px[..., 0:3],
+                 v_ray_d=abs_px[..., 3:6])
+        if velocity is not None:
+            a["v_velocity"] = abs_g[:, 11 + cdim:14 + cdim]
+            a["v_time_delta"] = abs_px[..., 6]
+        out["abs"] = a
     return out
+
+
+def margin_pointer_live(prec: str = "f64") -> bool:
+    """Whether the calling thread still holds a decision-margin pointer (test hook)."""
+    return bool(_lib(prec).orc_margin_pointer_live())
 
 
 def num_threads() -> int:

@@ -10,8 +10,9 @@
  *   orc_ut_weights            closed form (tests/test_oracle_pins.py)
  *   orc_project_utgs          on-axis closed form, EWA small-scale limit,
  *                             rolling-shutter residual invariant
- *   orc_project_utgs_phm      seam flag cases built by hand; phm seam selection
- *                             end-to-end is "parity unpinned" beyond those cases
+ *   orc_project_utgs_phm      a float64 restatement of each phase mode from the geometry on
+ *                             hand-placed Gaussians covering every branch of the seam
+ *                             selection, three shutter timings (tests/test_oracle_phm.py)
  *   orc_camera_rays           closed form pinhole / spherical / lidar rays
  *   orc_camera_rays_bwd       fp64 central differences of orc_camera_rays w.r.t. every camera
  *                             parameter (pinhole, spherical, lidar; world / camera space)
@@ -25,14 +26,18 @@
  *                             fp64 central differences for their intrinsics / coefficient
  *                             gradients; projection_nojac: fixed point = landing pixel's time
  *   orc_sh_fwd / orc_sh_bwd   scipy.special.sph_harm basis, fp64 finite differences
- *   orc_isect_*               brute-force tile enumeration in Python, numpy stable sort
+ *   orc_isect_*               brute-force tile enumeration in Python, numpy stable sort;
+ *                             the seam spans of orc_isect_spherical_family: exact first- and
+ *                             second-span tile sets from a float64 restatement of the
+ *                             re-projection and the span bounds, every shutter branch
+ *                             (tests/test_oracle_seam.py)
  *   orc_sort_pairs            numpy argsort(kind="stable")
  *   orc_offset_encode         numpy searchsorted
  *   orc_eval3d_fwd            one-Gaussian closed form, two-Gaussian analytic
  *                             composite, depth-sorted brute force without tiles
  *   orc_eval3d_bwd            fp64 finite differences of orc_eval3d_fwd (no-clamp
- *                             regime); the 0.99 clamp branch is pinned only by
- *                             code reading ("parity unpinned" inside that band)
+ *                             regime); the 0.99 clamp band by a hand-derived closed
+ *                             form (tests/test_oracle_bwd_band.py)
  */
 #include "xsg_oracle.h"
 
@@ -531,7 +536,6 @@ void orc_project_utgs(const orc_camera *c, int n, const real *means, const real 
 #pragma omp parallel for schedule(static)
     for (int i = 0; i < n; ++i) {
         real mg = K(1e30);
-        tl_mg = fmargin ? &mg : NULL;
         flags[i] = 0; radii[2 * i] = radii[2 * i + 1] = 0;
         means2d[2 * i] = means2d[2 * i + 1] = 0; depths[i] = 0;
         if (fmargin) fmargin[i] = mg;
@@ -541,6 +545,8 @@ void orc_project_utgs(const orc_camera *c, int n, const real *means, const real 
         ut_deltas(ut[3], quats + 4 * i, scales + 3 * i, d);
         v2 m2, r2; real depth = 0, udist = 0;
         const v3 pv = vel ? ld3(vel + 3 * i) : V3(0, 0, 0);
+        /* the margin pointer lives only around the one call that notes into mg */
+        tl_mg = fmargin ? &mg : NULL;
         const int ok = ut_projection(c, ORC_MODE_CENTRAL, ut, img, thr, max_res, margin,
                                      ld3(means + 3 * i), pv, op, d, &m2, &r2, &depth, &udist);
         if (fmargin) fmargin[i] = mg;
@@ -1542,7 +1548,19 @@ static void quat_scale_to_preci_half_vjp(const real *quat, const real *scale, co
 
 /* rasterize_eval3d_bwd_kernel: eval3d_bwd.cu:42-294 (dynamic: eval3d_dynamic_bwd.cu adds
  * v_velocity = -v_(o-mu) * dt and v_dt = -v_(o-mu) . velocity). Gradient outputs must be
- * zero-initialised; v_ray_o / v_ray_d are written for every pixel inside the image. */
+ * zero-initialised; v_ray_o / v_ray_d are written for every pixel inside the image.
+ *
+ * abs_g / abs_px (test diagnostics, NULL or zero-initialised; they change no result): the sum of
+ * the absolute per-pair contributions of each gradient component, per Gaussian [means 3, quats 4,
+ * scales 3, opacity 1, colours cdim, velocity 3 when given] and per pixel [ray_o 3, ray_d 3,
+ * time delta 1]. A component whose contributions cancel (the sum of their magnitudes far above the
+ * magnitude of their sum) is rounded differently by every float32 summation order.
+ *
+ * und_mode (test diagnostics): 0 computes the reference's backward. 1 and 2 force the outcome of
+ * every decision float32 rounding can take either way: a pair's alpha against 1/255 and its
+ * opacity-times-visibility against the 0.99 gate, judged with the forward's bound on the float32
+ * error of alpha (orc_eval3d_fwd's margins); 1 takes every such pair (and its geometry gradients),
+ * 2 drops them. A gradient that differs between the two is decided by float32 rounding. */
 void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *scales,
                     const real *colors, const real *opac, const real *velocity,
                     const real *ray_time_delta, int width, int height, int tile_w, int tile_h,
@@ -1551,10 +1569,14 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                     const real *render_alpha, const int32_t *last_ids, const real *v_rgb,
                     const real *v_depth, const real *v_alpha, real *v_means, real *v_quats,
                     real *v_scales, real *v_opac, real *v_colors, real *v_ray_o, real *v_ray_d,
-                    real *v_velocity, real *v_time_delta, const uint8_t *tile_mask) {
+                    real *v_velocity, real *v_time_delta, const uint8_t *tile_mask, real *abs_g,
+                    real *abs_px, int und_mode) {
     const orc_grid g = {width, height, tile_w, tile_h, n_tiles_w, n_tiles_h, n_isects};
     const int n_tiles = n_tiles_w * n_tiles_h;
     const real MAX_ALPHA = K(0.99);
+    const long ag = 11 + cdim + (velocity ? 3 : 0);   /* abs_g row length */
+#define ACC(ptr, val, k) do { const real v_ = (val); ATOMIC_ADD(ptr, v_); \
+                              if (abs_g) ATOMIC_ADD(&abs_g[(long)gid * ag + (k)], FABS(v_)); } while (0)
 #pragma omp parallel for schedule(dynamic, 4)
     for (int tile = 0; tile < n_tiles; ++tile) {
         if (tile_mask && !tile_mask[tile]) continue;  /* test subset: only these tiles' pixels contribute */
@@ -1575,8 +1597,8 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                 const int64_t bin_final = last_ids[pid];
                 const real vd = v_depth[pid], va = v_alpha[pid];
                 const real *vc = v_rgb ? v_rgb + pid * cdim : NULL;
-                v3 v_ro = V3(0, 0, 0), v_rd = V3(0, 0, 0);
-                real depth_buffer = 0, v_dt = 0;
+                v3 v_ro = V3(0, 0, 0), v_rd = V3(0, 0, 0), a_ro = V3(0, 0, 0), a_rd = V3(0, 0, 0);
+                real depth_buffer = 0, v_dt = 0, a_dt = 0;
                 for (int64_t idx = re - 1; idx >= rs; --idx) {
                     if (idx > bin_final) continue;
                     const int32_t gid = flatten_ids[idx];
@@ -1596,7 +1618,21 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                     const real power = K(-0.5) * dot3(gcrod, gcrod);
                     const real vis = EXP(power);
                     const real alpha = FMIN(MAX_ALPHA, op * vis);
-                    if (alpha < K(1.0) / K(255.0)) continue;
+                    int take = alpha >= K(1.0) / K(255.0), gate = op * vis <= MAX_ALPHA;
+                    if (und_mode) {
+                        /* the forward's float32 error bound of alpha (orc_eval3d_fwd) */
+                        const real *s = scales + 3 * gid;
+                        const real smin = FMIN(s[0], FMIN(s[1], s[2])), smax = FMAX(s[0], FMAX(s[1], s[2]));
+                        const real lom = SQRT(dot3(omm, omm));
+                        const real lor = (ro.x != 0 || ro.y != 0 || ro.z != 0) ? SQRT(dot3(ro, ro)) + SQRT(dot3(xyz, xyz)) : 0;
+                        const real dist = SQRT(dot3(gcrod, gcrod)), lg = SQRT(dot3(gro, gro));
+                        const real e_d = F32_U * (K(3) * (lom / smin + (smax / smin) * lg) + lor / smin);
+                        const real ea = K(4) * F32_U + dist * e_d + K(2) * F32_U * FABS(power);
+                        const real araw = op * vis, eb = K(2) * ea * araw + (real)1e-30;
+                        if (FABS(araw - K(1.0) / K(255.0)) < eb) take = und_mode == 1;
+                        if (FABS(araw - MAX_ALPHA) < eb) gate = und_mode == 1;
+                    }
+                    if (!take) continue;
                     const real last_hit_T = -dot3(grd, gro) / dot3(grd, grd);
                     const real ra = K(1.0) / FMAX(K(1e-6), K(1.0) - alpha);
                     T *= ra;
@@ -1607,12 +1643,12 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                     for (int c = 0; c < cdim; ++c) v_a += (rgb[c] * T - buffer[c] * ra) * vc[c];
                     v_a += (last_hit_T * T - depth_buffer * ra) * vd;
                     v_a += T_final * ra * va;
-                    for (int c = 0; c < cdim; ++c) ATOMIC_ADD(&v_colors[(long)gid * cdim + c], vc[c] * fac);
+                    for (int c = 0; c < cdim; ++c) ACC(&v_colors[(long)gid * cdim + c], vc[c] * fac, 11 + c);
                     const real dd = dot3(grd, grd), od = dot3(gro, grd);
                     const real dL_dhitT = vd * fac;
                     v3 v_gro = scl3(scl3(grd, K(-1)), dL_dhitT / dd);
                     v3 v_grd = scl3(sub3(scl3(grd, K(2.0) * od), scl3(gro, dd)), dL_dhitT / (dd * dd));
-                    if (op * vis <= MAX_ALPHA) {
+                    if (gate) {
                         const real v_vis = op * v_a;
                         const real v_gd = K(-0.5) * vis * v_vis;
                         const v3 v_gcrod = scl3(gcrod, K(2.0) * v_gd);
@@ -1634,23 +1670,27 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                             for (int ri = 0; ri < 3; ++ri) v_Mt.m[cj][ri] = a3[ri] * d3[cj] + b3[ri] * o3[cj];
                         const m3 trMt = transpose3(&Mt);
                         const v3 v_omm = mv(&trMt, v_gro);
-                        ATOMIC_ADD(&v_means[3 * gid], -v_omm.x);
-                        ATOMIC_ADD(&v_means[3 * gid + 1], -v_omm.y);
-                        ATOMIC_ADD(&v_means[3 * gid + 2], -v_omm.z);
+                        ACC(&v_means[3 * gid], -v_omm.x, 0);
+                        ACC(&v_means[3 * gid + 1], -v_omm.y, 1);
+                        ACC(&v_means[3 * gid + 2], -v_omm.z, 2);
                         if (velocity) {
-                            ATOMIC_ADD(&v_velocity[3 * gid], -v_omm.x * dtp);
-                            ATOMIC_ADD(&v_velocity[3 * gid + 1], -v_omm.y * dtp);
-                            ATOMIC_ADD(&v_velocity[3 * gid + 2], -v_omm.z * dtp);
+                            ACC(&v_velocity[3 * gid], -v_omm.x * dtp, 11 + cdim);
+                            ACC(&v_velocity[3 * gid + 1], -v_omm.y * dtp, 12 + cdim);
+                            ACC(&v_velocity[3 * gid + 2], -v_omm.z * dtp, 13 + cdim);
                             v_dt += -dot3(v_omm, vel);
+                            a_dt += FABS(dot3(v_omm, vel));
                         }
+                        const v3 v_rd_i = mv(&trMt, v_grd);
                         v_ro = add3(v_ro, v_omm);
-                        v_rd = add3(v_rd, mv(&trMt, v_grd));
+                        v_rd = add3(v_rd, v_rd_i);
+                        a_ro = add3(a_ro, V3(FABS(v_omm.x), FABS(v_omm.y), FABS(v_omm.z)));
+                        a_rd = add3(a_rd, V3(FABS(v_rd_i.x), FABS(v_rd_i.y), FABS(v_rd_i.z)));
                         const m3 v_M = transpose3(&v_Mt);
                         real vq[4] = {0, 0, 0, 0}, vs[3] = {0, 0, 0};
                         quat_scale_to_preci_half_vjp(quat, scale, &R, &v_M, vq, vs);
-                        for (int k = 0; k < 4; ++k) ATOMIC_ADD(&v_quats[4 * gid + k], vq[k]);
-                        for (int k = 0; k < 3; ++k) ATOMIC_ADD(&v_scales[3 * gid + k], vs[k]);
-                        ATOMIC_ADD(&v_opac[gid], vis * v_a);
+                        for (int k = 0; k < 4; ++k) ACC(&v_quats[4 * gid + k], vq[k], 3 + k);
+                        for (int k = 0; k < 3; ++k) ACC(&v_scales[3 * gid + k], vs[k], 7 + k);
+                        ACC(&v_opac[gid], vis * v_a, 10);
                     }
                     for (int c = 0; c < cdim; ++c) buffer[c] += rgb[c] * fac;
                     depth_buffer += fac * last_hit_T;
@@ -1658,9 +1698,15 @@ void orc_eval3d_bwd(int cdim, const real *means, const real *quats, const real *
                 v_ray_o[3 * pid] = v_ro.x; v_ray_o[3 * pid + 1] = v_ro.y; v_ray_o[3 * pid + 2] = v_ro.z;
                 v_ray_d[3 * pid] = v_rd.x; v_ray_d[3 * pid + 1] = v_rd.y; v_ray_d[3 * pid + 2] = v_rd.z;
                 if (v_time_delta) v_time_delta[pid] = v_dt;
+                if (abs_px) {
+                    real *a = abs_px + 7 * pid;
+                    a[0] = a_ro.x; a[1] = a_ro.y; a[2] = a_ro.z;
+                    a[3] = a_rd.x; a[4] = a_rd.y; a[5] = a_rd.z; a[6] = a_dt;
+                }
             }
         free(buffer);
     }
+#undef ACC
 }
 
 /* Host-side mask_radii: mask_radii.cu:10-58 (bool and packed uint32 masks). */
@@ -1672,6 +1718,10 @@ void orc_mask_radii(int n, const uint8_t *mask, const uint32_t *packed, float *r
 }
 
 int orc_real_bytes(void) { return (int)sizeof(real); }
+
+/* 1 while the calling thread's decision-margin pointer is set: every exported function clears it
+ * before it returns, so that no later call notes a margin through a dead stack slot (test hook). */
+int orc_margin_pointer_live(void) { return tl_mg != NULL; }
 
 int orc_num_threads(void) {
 #ifdef _OPENMP

@@ -119,7 +119,16 @@ def test_hip_path_reproduces_fixture(dev, name):
     if "proj_uvdt" in f:
         uvdt, mask = cam.ext_cls.projection(pack, means, vel)
         m = np_(mask).astype(bool)
-        assert (m == f["proj_mask"]).mean() > 0.99
+        # a validity disagreement only where float32 does not decide it: the f64 landing point within
+        # 1e-5 of the image's [0, 1] bounds (the last test of projection_kernels.h:255 and the caller's
+        # in-image check), else the mask must be f64's
+        dis = np.nonzero(m != f["proj_mask"])[0]
+        if dis.size:
+            u64, m64 = O.projection(spec, f["means"], vel=f.get("velocity"), prec="f64")
+            uv = u64[dis, :2]
+            near = (np.minimum(np.abs(uv), np.abs(uv - 1.0)) < 1e-5).any(-1)
+            print("projection mask disagreements", dis.size, "near the image bounds", int(near.sum()), flush=True)
+            assert np.all(near | (m[dis] == m64[dis].astype(bool))), dis[~near]
         both = m & f["proj_mask"]
         _check("projection uvdt", np_(uvdt)[both], f["proj_uvdt"][both], 1e-5, 1e-5)
         rtd = cam.ext_cls.pixel_time_delta(pack, W, H)
@@ -185,11 +194,13 @@ def test_hip_path_reproduces_fixture(dev, name):
     else:
         rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0), opac.view(1, -1),
                                                           W, H, tsx, tsy, ro, rd, off, fl)
-    _check("rgb", rgb, f["rgb"], RENDER_ATOL, 0.0, 0.999)
-    _check("depth", depth, f["depth"], RENDER_ATOL, 0.0, 0.999)
-    _check("alpha", alpha, f["alpha"], RENDER_ATOL, 0.0, 0.999)
-    print("last_ids agree", (np_(last) == f["last_ids"]).mean(), flush=True)
-    assert (np_(last) == f["last_ids"]).mean() > 0.999
+    # renders against the fixture (the f32 oracle's): every pixel outside 1e-4 or with another last id
+    # undetermined in float32 or right against f64 (tests/_judge.py)
+    rtd_np = f["ray_time_delta"] if vel is not None else None
+    inp = dict(means=f["means"], quats=f["quats"], scales=f["scales"], opac=f["opacity"], colors=f["colors"],
+               ro=f["ray_o"], rd=f["ray_d"], vel=f.get("velocity"), rtd=rtd_np)
+    J.judge_renders([np_(rgb), np_(depth), np_(alpha), np_(last)], (f["rgb"], f["depth"], f["alpha"], f["last_ids"]),
+                    inp, f["offsets"], f["flatten_ids"], tsx, tsy, label=name)
     args = dict(render_alpha=T("alpha"), last_ids=T("last_ids"), v_render_colors=T("v_rgb"),
                 v_render_depth=T("v_depth"), v_render_alpha=T("v_alpha"))
     if vel is not None:
@@ -201,8 +212,16 @@ def test_hip_path_reproduces_fixture(dev, name):
         grads = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, **args)
         keys = GRAD_KEYS
     assert len(grads) == len(keys)
-    for k, g in zip(keys, grads):
-        _check(k, g, f["g_" + k], GRAD_ATOL, GRAD_RTOL, 0.999)
+    got = dict(zip(keys, grads))
+    # gradients judged against f64 on every Gaussian and pixel float32 determines (tests/_judge.py),
+    # from the fixture's alpha and last ids as the kernel was given them; the fixture's own gradients
+    # are the f32 oracle's (test_oracle_reproduces_fixture)
+    refs = J.bwd_runs(inp, f["offsets"], f["flatten_ids"], f["alpha"], f["last_ids"], f["v_rgb"], f["v_depth"],
+                      f["v_alpha"], tsx, tsy, None)
+    gk = [k for k in ("v_means", "v_quats", "v_scales", "v_opacity", "v_colors", "v_velocity") if k in got]
+    J.judge_grads({k: got[k] for k in gk}, refs, np.unique(f["flatten_ids"]), label=name)
+    pk = [k for k in ("v_ray_o", "v_ray_d", "v_time_delta") if k in got]
+    J.judge_pixel_grads({k: got[k] for k in pk}, refs, np.ones(f["alpha"].shape, bool), label=name)
 
 
 @pytest.mark.gpu

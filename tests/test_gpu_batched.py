@@ -190,10 +190,17 @@ def test_batched_compositor_rejects_bad_shapes(dev):
                                         off[0], fl)
 
 
-def test_render_rig_matches_camera_loop(dev):
-    """The cfg4 rig (six co-located cameras) with 200k Gaussians: render_rig against render_frame per
-    camera, forward and every leaf's gradient."""
-    sc = S.make_cfg4(seed=3, n=200_000, n_blobs=300)
+@pytest.mark.parametrize("size", ["200k", "full"])
+def test_render_rig_matches_camera_loop(dev, size):
+    """The cfg4 rig (six co-located cameras): render_rig (the frame the cfg4 benchmark line times) against
+    render_frame per camera (the reference caller's loop, camera.h:58-59), forward and every leaf's
+    gradient, with 200k Gaussians and at the benchmark's full size (4M Gaussians in 2000 blobs: 24M
+    camera instances and ~33M intersections in one batched binning, which takes the size-dependent
+    paths: the large pre-order tiles and the single-pass rig row sort). Each camera's slice of the
+    batched binning (its tile offsets, its flatten ids less the camera's first row) equals that camera's
+    own binning bit for bit."""
+    sc = S.make_cfg4(seed=3, n=200_000, n_blobs=300) if size == "200k" else S.make_cfg4()
+    print("rig", size, sc.n, "Gaussians", flush=True)
     st = frame.prepare(sc, dev)
     assert frame.rig_batchable(st) and frame.rig_shares_origin(st)
     C = len(sc.cameras)
@@ -201,12 +208,26 @@ def test_render_rig_matches_camera_loop(dev):
     grads = [torch.stack([getattr(sc, k)[i] for i in range(C)]) for k in ("grad_rgb", "grad_depth", "grad_alpha")]
     rig = frame.render_rig(st, backward=True, grads=grads)
     got = {k: np_(v).astype(np.float64) for k, v in rig["grads"].items() if v is not None}
+    r_off = np_(rig["offsets"]).astype(np.int64)
+    r_fl = np_(rig["flatten_ids"])
+    n_rig = r_fl.size
     frame.zero_grads(st)
+    total = 0
     for ci in range(C):
         o = frame.render_frame(st, backward=True, cam_index=ci,
                                grads=(sc.grad_rgb[ci], sc.grad_depth[ci], sc.grad_alpha[ci]))
         for k in ("rgb", "depth", "alpha"):
             assert torch.equal(rig[k][ci].detach(), o[k].detach()), (ci, k)
+        off1, fl1 = np_(o["offsets"]).astype(np.int64), np_(o["flatten_ids"])
+        first = int(r_off[ci].reshape(-1)[0])
+        end = int(r_off[ci + 1].reshape(-1)[0]) if ci + 1 < C else n_rig
+        assert first == total, (ci, first, total)
+        assert np.array_equal(r_off[ci] - first, off1), ci
+        # the batched ids index the camera-major [C, N] projections: camera ci's are ci * N + Gaussian
+        assert np.array_equal(r_fl[first:end].astype(np.int64) - ci * sc.n, fl1), ci
+        total += fl1.size
+    assert total == n_rig
+    print("rig", size, "intersections", n_rig, flush=True)
     want = {k: np_(v).astype(np.float64) for k, v in o["grads"].items() if v is not None}
     assert set(got) == set(want) == {"means", "quats", "log_scales", "opacity_logits", "sh"}
     for k in want:

@@ -126,11 +126,16 @@ def test_config_full_size(dev, name, ci):
                                           tile_size_x=tsx, tile_size_y=tsy, tile_offsets=off_fill)
         off = _C.isect_offset_encode(ids, ntx, nty)
     elev = spec.beam_v.numpy()[::tsy] if spec.kind == "lidar" else None
+    ref_in = None
     if spec.kind == "pinhole":
         ref_bin = O.isect_regular(hm2, hr, hd, W, H, tsx, tsy)
     else:
-        ref_bin = O.isect_spherical_family(spec.kind, spec, hm, hs, hq, ho, hf, hm2, hr, hd, tsx, tsy, W, H,
-                                           elev=elev)
+        unsorted = O.isect_spherical_family(spec.kind, spec, hm, hs, hq, ho, hf, hm2, hr, hd, tsx, tsy, W, H,
+                                            elev=elev, sort=False)
+        ref_bin = (unsorted[0],) + O.sort_pairs(unsorted[1], unsorted[2], 32 + O.tile_n_bits(n_tiles))
+        if not any(spec.v) and not any(spec.w):
+            # a static camera: both spans of a seam Gaussian carry its input depth in the reference
+            ref_in = J.with_input_depths(unsorted, hd, n_tiles)
     hfl, hids = np_(fl), np_(ids)
     und = None
     if spec.kind != "pinhole":
@@ -138,7 +143,8 @@ def test_config_full_size(dev, name, ci):
                                        seam_margins=True) < 1.0
     with S.check("binning"):
         fs = lambda g, t: J.first_span_member(spec.kind, spec, g, t, hm2, hr, W, H, tsx, tsy, elev)
-        J.check_binning(spec.kind, (np_(tpg), hids, hfl), ref_bin, hf, hd, n_tiles, label, und, fs)
+        J.check_binning(spec.kind, (np_(tpg), hids, hfl), ref_bin, hf, hd, n_tiles, label, und, fs,
+                        ref_input_depths=ref_in)
     hoff = np_(off)
     with S.check("tile_offsets"):
         # the encoder and the fill's offsets on the GPU's keys; the oracle's where the keys agree

@@ -286,6 +286,7 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
     if (total == 0) return;  // workgroup-uniform
     const Camera cam = load_camera(pack, KIND);
     const bool is_static = camera_is_static(cam, vel != nullptr);
+    const PhaseUnwrap unwrap = phase_unwrap(cam);
     for (uint32_t q = threadIdx.x; q < total; q += kBlock) {
         int b = 0;
         while (b + 1 < nb && s_off[b + 1] <= q) ++b;
@@ -293,13 +294,23 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
         f3 d[3];
         ut_deltas(ut.sqrt_dl, quats[j], ld3(scales + 3 * j), d);
         const float op = opacity ? opacity[j] : 1.0f;
-        const f3 pv = vel ? ld3(vel + 3 * j) : mk3(0.f, 0.f, 0.f);
         const ProjParams pp{1e-4f, 0.002f, 1.0f};
+        const f3 pw = ld3(points + 3 * j);
         f2 m2 = mk2(0.f, 0.f), r2 = mk2(0.f, 0.f);
         float dd = 0.f, ud = 0.f;
-        if (!ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, ld3(points + 3 * j), pv, op, d, is_static,
-                                 m2, r2, dd, ud))
-            continue;
+        bool ok;
+        if (is_static) {
+            // the phase-modelled projection's own static-pose path (ut_project_phm_kernel), so that
+            // the re-projected depth -- the centre point's range, which no phase mode changes -- is
+            // the stored depth bit for bit, as both spans' keys carry one depth in the reference
+            SigmaUv sa;
+            sigma_uv(cam, pw, d, sa);
+            ok = ut_projection_sigma_uv(cam, unwrap, XSG_MODE_POSITIVE, ut, img, pp, op, sa, m2, r2, dd, ud);
+        } else {
+            const f3 pv = vel ? ld3(vel + 3 * j) : mk3(0.f, 0.f, 0.f);
+            ok = ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, pw, pv, op, d, false, m2, r2, dd, ud);
+        }
+        if (!ok) continue;
         const float u_pose = u_pose_of(cam);
         float u_min, u_max;
         if (cam.roll_u > 0) {
@@ -1139,13 +1150,13 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // The depth pre-order sorts the visible instances, usually a small part of the instances its grid
 // is sized for: 1024 keys per block spread them over four times as many workgroups. Large counts
 // (millions of visible instances: a lidar frame, a camera rig) run faster in tiles of 2048 keys
-// (longer runs per digit in each tile's scatter). The count is known only on the device when the
-// pre-order is queued, so the previous call's visible count chooses (both sort identically).
+// (longer runs per digit in each tile's scatter). The visible count is known only on the device when
+// the pre-order is queued, so the number of virtual instances, known to the host, chooses: one call's
+// launches depend on its own arguments only (both tile sizes sort identically).
 constexpr int kPresortItems = 4;
 constexpr int kPresortItemsLarge = 8;
-constexpr int64_t kPresortLargeAt = 1500000;  // visible instances
+constexpr int64_t kPresortLargeAt = 3000000;  // virtual instances (Gaussians x cameras x spans)
 constexpr unsigned kPresortGrid = 2048;
-std::atomic<int64_t> g_visible_hint{0};
 constexpr int kPresortRB = 8;                                        // digit bits
 constexpr int kPresortPasses = (32 + kPresortRB - 1) / kPresortRB;  // over the 32 depth bits
 
@@ -1281,16 +1292,36 @@ extern "C" size_t xsg_isect_count_workspace_bytes(const xsg_isect_desc* d) {
 }
 
 // Per host thread and device: a mapped pinned host buffer that the count phase writes its totals to,
-// and the event that marks the write. Allocated on a thread's first count on a device and kept for
-// the thread's lifetime (64 bytes of pinned memory and one event).
+// and the event that marks the write. Allocated on a thread's first count on a device and kept until
+// the thread calls xsg_release_thread_resources (64 bytes of pinned memory and one event per device).
 struct CountReadback {
     uint64_t* host = nullptr;  // host view
     uint64_t* dev = nullptr;   // device view of the same memory
     hipEvent_t ev = nullptr;
 };
 
+static thread_local std::vector<CountReadback> tl_readbacks;
+
+extern "C" int xsg_release_thread_resources(void) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return xsg_launch_status("release_thread_resources device");
+    int rc = XSG_OK;
+    for (size_t d = 0; d < tl_readbacks.size(); ++d) {
+        CountReadback& rb = tl_readbacks[d];
+        if (!rb.host) continue;
+        // xsg_isect_count waited for the event before it returned, so no queued work still writes here
+        if (hipSetDevice((int)d) != hipSuccess || hipEventDestroy(rb.ev) != hipSuccess ||
+            hipHostFree(rb.host) != hipSuccess)
+            rc = xsg_launch_status("release_thread_resources");
+        rb = CountReadback{};
+    }
+    tl_readbacks.clear();
+    if (hipSetDevice(cur) != hipSuccess && rc == XSG_OK) rc = xsg_launch_status("release_thread_resources device");
+    return rc;
+}
+
 static int count_readback(CountReadback*& out) {
-    thread_local std::vector<CountReadback> per_device;
+    std::vector<CountReadback>& per_device = tl_readbacks;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return xsg_launch_status("isect_count readback device");
     if ((int)per_device.size() <= dev) per_device.resize(dev + 1);
@@ -1379,7 +1410,7 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
         // (stable, kPresortPasses passes, result in pre_key / pre_id), then their row-run offsets
-        if (g_visible_hint.load(std::memory_order_relaxed) >= kPresortLargeAt)
+        if (w.n_virtual >= kPresortLargeAt)
             radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItemsLarge, kPresortRB>(
                 w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
                 PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
@@ -1409,7 +1440,6 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
                         (unsigned long long)total[1]);
     if (n_isects) *n_isects = (int64_t)total[1];
     if (n_visible) *n_visible = (int64_t)(total[0] >> 32);
-    if (g.sort) g_visible_hint.store((int64_t)(total[0] >> 32), std::memory_order_relaxed);
     if (n_runs) *n_runs = (int64_t)total[2];
     return XSG_OK;
 }

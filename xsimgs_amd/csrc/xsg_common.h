@@ -566,7 +566,8 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
 // A static spherical / lidar camera's sigma points before phase unwrapping: each camera-space point's
 // u = (azimuth - u0) / du, v and range (point_to_uvd's spherical branch, spherical.h:133-142). None of
 // them depends on the phase mode, which only shifts u by one turn (unwrap_u), so the three modes of
-// the phase-modelled projection share them; each mode's results equal ut_projection's bit for bit.
+// the phase-modelled projection share them, and the binning's seam re-projection of a static pose
+// computes them the same way (its depth, the centre's range, is then the stored depth bit for bit).
 struct SigmaUv { float u[7], v[7], r[7]; };
 
 XSG_DEV void sigma_uv(const Camera& c, f3 pw, const f3 d[3], SigmaUv& a) {
