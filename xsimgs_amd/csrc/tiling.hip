@@ -126,15 +126,34 @@ struct Geometry {
 constexpr int kCountItems = 4;
 constexpr int kCountTile = kBlock * kCountItems;
 
+// Smallest and largest of the threads' (lo, hi) over a 256-thread block, on thread 0 (the block's
+// range of visible depth keys, which the depth pre-order's first digit is taken from).
+XSG_DEV void block_key_range(uint32_t& lo, uint32_t& hi, uint32_t* s_lo, uint32_t* s_hi) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        lo = min(lo, (uint32_t)__shfl_xor((int)lo, off, 64));
+        hi = max(hi, (uint32_t)__shfl_xor((int)hi, off, 64));
+    }
+    if (__lane_id() == 0) { s_lo[threadIdx.x >> 6] = lo; s_hi[threadIdx.x >> 6] = hi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) { lo = min(lo, s_lo[w]); hi = max(hi, s_hi[w]); }
+    }
+}
+
 // Count pass over regular-tiling Gaussian instances (one span each). A block covers kCountTile
 // instances; it writes tiles_per_gauss and the rectangle of every instance, and the block's packed
 // count sum. The compaction takes the counts from tiles_per_gauss and the depth bits from the depths.
+// With key_range (the bucketed depth pre-order), also the block's range of visible depth keys.
 __global__ __launch_bounds__(kBlock) void count_regular_kernel(
     int64_t n_total, const float2* __restrict__ means2d, const float2* __restrict__ radii, float tsx, float tsy,
     int ntx, int nty, int32_t* __restrict__ tpg, Rect* __restrict__ rects, uint64_t* __restrict__ partials,
-    uint64_t* __restrict__ cpart) {
+    uint64_t* __restrict__ cpart, const float* __restrict__ depths, uint32_t* __restrict__ key_range) {
     __shared__ uint64_t lds[kWaves];
+    __shared__ uint32_t s_lo[kWaves], s_hi[kWaves];
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
+    uint32_t lo = 0xffffffffu, hi = 0u;
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
     for (int k = 0; k < kCountItems; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
@@ -146,15 +165,22 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
             acc += pack_count(c);
             acc_c += c;
             acc_r += c > 0 ? (uint32_t)(r.y1 - r.y0) : 0u;
+            if (key_range && c > 0) {
+                const uint32_t key = __float_as_uint(depths[j]);
+                lo = min(lo, key);
+                hi = max(hi, key);
+            }
         }
     }
     acc = block_reduce_sum<uint64_t>(acc, lds);
     acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
     acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
+    if (key_range) block_key_range(lo, hi, s_lo, s_hi);  // block-uniform
     if (threadIdx.x == 0) {
         partials[blockIdx.x] = acc;
         cpart[2 * blockIdx.x] = acc_c;
         cpart[2 * blockIdx.x + 1] = acc_r;
+        if (key_range) { key_range[2 * blockIdx.x] = lo; key_range[2 * blockIdx.x + 1] = hi; }
     }
 }
 
@@ -170,8 +196,9 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     const float* __restrict__ elev, int n_elev, float u_per_tile, float v_per_tile, int ntx, int n_v,
     int32_t* __restrict__ tpg, Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
     uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart, uint32_t* __restrict__ seam_cnt,
-    uint32_t* __restrict__ seam_ids) {
+    uint32_t* __restrict__ seam_ids, uint32_t* __restrict__ key_range) {
     __shared__ uint64_t lds[kWaves];
+    __shared__ uint32_t s_lo[kWaves], s_hi[kWaves];
     __shared__ uint32_t s_seam;
     // lidar: the elevation table in LDS; when it is non-decreasing (as find_bounds_increasing
     // expects) its scans become bisections (same bounds), else they scan as the reference does
@@ -197,6 +224,7 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     const int lane = __lane_id();
     const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
+    uint32_t lo = 0xffffffffu, hi = 0u;
     const int64_t base = (int64_t)blockIdx.x * (kCountTile / 2);
     for (int k = 0; k < kCountItems / 2; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
@@ -228,6 +256,10 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
             vcnt[2 * j + 1] = 0u;
             vkey[2 * j] = __float_as_uint(depths[j]);
             vkey[2 * j + 1] = 0u;
+            if (ca > 0) {
+                lo = min(lo, __float_as_uint(depths[j]));
+                hi = max(hi, __float_as_uint(depths[j]));
+            }
             acc += pack_count(ca);
             acc_c += ca;
             acc_r += ca > 0 ? (uint32_t)(a.y1 - a.y0) : 0u;
@@ -246,11 +278,13 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     acc = block_reduce_sum<uint64_t>(acc, lds);  // its barriers also order the LDS reservations
     acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
     acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
+    if (key_range) block_key_range(lo, hi, s_lo, s_hi);  // block-uniform
     if (threadIdx.x == 0) {
         partials[blockIdx.x] = acc;
         cpart[2 * blockIdx.x] = acc_c;
         cpart[2 * blockIdx.x + 1] = acc_r;
         seam_cnt[blockIdx.x] = s_seam;
+        if (key_range) { key_range[2 * blockIdx.x] = lo; key_range[2 * blockIdx.x + 1] = hi; }
     }
 }
 
@@ -270,9 +304,10 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
     const float* __restrict__ opacity, const float* __restrict__ elev, int n_elev, float u_per_tile,
     float v_per_tile, int ntx, int n_v, int32_t* __restrict__ tpg, Rect* __restrict__ rects,
     uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey, uint64_t* __restrict__ partials,
-    uint64_t* __restrict__ cpart) {
+    uint64_t* __restrict__ cpart, uint32_t* __restrict__ key_range) {
     __shared__ uint32_t s_off[kSeamBlocks + 1];
     __shared__ uint32_t s_vis[kSeamBlocks], s_cnt[kSeamBlocks], s_rows[kSeamBlocks];
+    __shared__ uint32_t s_klo[kSeamBlocks], s_khi[kSeamBlocks];
     const unsigned blk0 = blockIdx.x * kSeamBlocks;
     const int nb = (int)min<unsigned>(kSeamBlocks, n_count_blocks - blk0);
     if (threadIdx.x == 0) {
@@ -280,7 +315,10 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
         for (int b = 0; b < nb; ++b) { s_off[b] = o; o += seam_cnt[blk0 + b]; }
         s_off[nb] = o;
     }
-    if (threadIdx.x < kSeamBlocks) { s_vis[threadIdx.x] = 0; s_cnt[threadIdx.x] = 0; s_rows[threadIdx.x] = 0; }
+    if (threadIdx.x < kSeamBlocks) {
+        s_vis[threadIdx.x] = 0; s_cnt[threadIdx.x] = 0; s_rows[threadIdx.x] = 0;
+        s_klo[threadIdx.x] = 0xffffffffu; s_khi[threadIdx.x] = 0u;
+    }
     __syncthreads();
     const uint32_t total = s_off[nb];
     if (total == 0) return;  // workgroup-uniform
@@ -333,6 +371,10 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
             atomicAdd(&s_vis[b], 1u);
             atomicAdd(&s_cnt[b], cb);
             atomicAdd(&s_rows[b], (uint32_t)(r.y1 - r.y0));
+            if (key_range) {  // LDS atomics: the block's second spans join its key range
+                atomicMin(&s_klo[b], __float_as_uint(dd));
+                atomicMax(&s_khi[b], __float_as_uint(dd));
+            }
         }
     }
     __syncthreads();
@@ -341,6 +383,10 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
         partials[blk] += ((uint64_t)s_vis[threadIdx.x] << 32) + s_cnt[threadIdx.x];
         cpart[2 * blk] += s_cnt[threadIdx.x];
         cpart[2 * blk + 1] += s_rows[threadIdx.x];
+        if (key_range) {
+            key_range[2 * blk] = min(key_range[2 * blk], s_klo[threadIdx.x]);
+            key_range[2 * blk + 1] = max(key_range[2 * blk + 1], s_khi[threadIdx.x]);
+        }
     }
 }
 
@@ -356,10 +402,18 @@ template <typename T>
 __global__ __launch_bounds__(kBlock) void slice_scan_kernel(unsigned n, T* __restrict__ partials,
                                                             T* __restrict__ slice_sum,
                                                             const uint64_t* __restrict__ extra,
-                                                            uint64_t* __restrict__ slice_extra) {
+                                                            uint64_t* __restrict__ slice_extra,
+                                                            const uint32_t* __restrict__ block_range = nullptr,
+                                                            uint32_t* __restrict__ slice_range = nullptr) {
     __shared__ T lds[kWaves];
     __shared__ uint64_t lds64[kWaves];
+    __shared__ uint32_t s_lo[kWaves], s_hi[kWaves];
     const unsigned i = blockIdx.x * kSlice + threadIdx.x;
+    if (block_range) {  // the slice's range of visible depth keys from its blocks' (block-uniform)
+        uint32_t lo = i < n ? block_range[2 * i] : 0xffffffffu, hi = i < n ? block_range[2 * i + 1] : 0u;
+        block_key_range(lo, hi, s_lo, s_hi);
+        if (threadIdx.x == 0) { slice_range[2 * blockIdx.x] = lo; slice_range[2 * blockIdx.x + 1] = hi; }
+    }
     const T v = i < n ? partials[i] : T(0);
     T tot;
     const T ex = block_exclusive_scan<T>(v, lds, tot);
@@ -434,6 +488,187 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
             }
         }
         s += pack_count(c[k]);
+    }
+}
+
+// Depth pre-order, second stage. A most-significant-digit pass (the top RB bits of each key's offset
+// from the smallest visible key, stable) has split the visible instances into buckets of consecutive
+// key values, each in instance order. One workgroup per bucket sorts it stably by the key bits below
+// that digit, 8 bits per pass: in LDS when it holds at most kBucketCap keys, else chunk by chunk
+// through global memory (ping-ponging between the bucket's ranges of the two arrays). The result is
+// the stable order of the keys, which is what LSD passes over all 32 bits give.
+constexpr int kBucketThreads = 512;
+constexpr int kBucketWaves = kBucketThreads / 64;
+constexpr int kBucketCap = 8192;
+constexpr int kBucketSteps = kBucketCap / kBucketThreads;  // steps of 64 keys per wavefront, at most
+
+struct BucketLds {
+    uint32_t key[2][kBucketCap];
+    uint32_t id[2][kBucketCap];
+    uint32_t wcnt[kBucketWaves][256];  // per wavefront and digit: count, then the wavefront's prefix
+    uint32_t dpre[256];                // per digit: first position in the chunk
+    uint32_t dcnt[256];                // per digit: keys of the chunk
+    uint32_t gbase[256];               // global path: per digit, next position in the bucket
+    uint32_t scan[kBucketWaves];
+};
+
+XSG_DEV uint32_t block_exclusive_scan_bucket(uint32_t v, uint32_t* lds, uint32_t& total) {
+    const uint32_t inc = wave_inclusive_scan(v);
+    const int wave = threadIdx.x >> 6;
+    if (__lane_id() == 63) lds[wave] = inc;
+    __syncthreads();
+    uint32_t before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kBucketWaves; ++w) {
+        const uint32_t x = lds[w];
+        if (w < wave) before += x;
+        tot += x;
+    }
+    __syncthreads();
+    total = tot;
+    return before + inc - v;
+}
+
+// Stable ranking of the chunk's n keys in L.key[src][0, n): wavefront w takes the contiguous segment
+// [w seg, (w + 1) seg) in steps of 64 keys (seg a multiple of 64, at most kBucketSteps steps), equal
+// digits inside a step are found with ballots over the digit bits and a wavefront counter per digit
+// carries the rank across steps. pos[r] receives the step's key's position in the digit-sorted chunk,
+// L.dpre / L.dcnt each digit's first position and count. Ends with a barrier.
+XSG_DEV void bucket_rank(BucketLds& L, int src, int n, int seg, uint32_t kmin, int sh, int bits,
+                         uint32_t (&dig)[kBucketSteps], uint32_t (&pos)[kBucketSteps]) {
+    const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
+    for (int i = t; i < kBucketWaves * 256; i += kBucketThreads) (&L.wcnt[0][0])[i] = 0u;
+    __syncthreads();
+    const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int steps = seg >> 6;
+#pragma unroll
+    for (int r = 0; r < kBucketSteps; ++r) {
+        dig[r] = 0u;
+        pos[r] = 0u;
+        if (r < steps) {  // uniform
+            const int li = wave * seg + r * 64 + lane;
+            const bool valid = li < n;
+            const uint32_t d = valid ? ((L.key[src][li] - kmin) >> sh) & ((1u << bits) - 1u) : 0u;
+            uint64_t peers = __ballot(valid);
+            for (int b = 0; b < bits; ++b) {
+                const uint64_t m = __ballot((d >> b) & 1u);
+                peers &= ((d >> b) & 1u) ? m : ~m;
+            }
+            const uint32_t before = (uint32_t)__popcll(peers & lt_mask);
+            const uint32_t base = valid ? L.wcnt[wave][d] : 0u;
+            pos[r] = base + before;
+            dig[r] = d;
+            if (valid && before == 0) L.wcnt[wave][d] = base + (uint32_t)__popcll(peers);
+        }
+    }
+    __syncthreads();
+    uint32_t tot_d = 0;
+    if (t < 256) {
+#pragma unroll
+        for (int w = 0; w < kBucketWaves; ++w) {
+            const uint32_t c = L.wcnt[w][t];
+            L.wcnt[w][t] = tot_d;
+            tot_d += c;
+        }
+    }
+    uint32_t total;
+    const uint32_t ex = block_exclusive_scan_bucket(t < 256 ? tot_d : 0u, L.scan, total);
+    if (t < 256) { L.dpre[t] = ex; L.dcnt[t] = tot_d; }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kBucketSteps; ++r)
+        if (r < steps && wave * seg + r * 64 + lane < n) pos[r] += L.dpre[dig[r]] + L.wcnt[wave][dig[r]];
+}
+
+// segment per wavefront for n keys: a multiple of 64, the wavefronts covering n in order
+XSG_DEV int bucket_seg(int n) { return min(kBucketCap / kBucketWaves, ((n + kBucketWaves * 64 - 1) / (kBucketWaves * 64)) * 64); }
+
+template <int RB>
+__global__ __launch_bounds__(kBucketThreads) void bucket_sort_kernel(
+    const uint32_t* __restrict__ digit_total, const uint32_t* __restrict__ range, int range_parts,
+    uint32_t* __restrict__ a_key, uint32_t* __restrict__ a_id, uint32_t* __restrict__ out_key,
+    uint32_t* __restrict__ out_id) {
+    __shared__ BucketLds L;
+    const int t = threadIdx.x;
+    const int b = blockIdx.x;
+    // the bucket's first position: the counts of the buckets before it
+    uint32_t acc = 0;
+    for (int j = t; j < b; j += kBucketThreads) acc += digit_total[j];
+    uint32_t start;
+    block_exclusive_scan_bucket(acc, L.scan, start);
+    const int n = (int)digit_total[b];
+    if (n == 0) return;  // uniform
+    const KeyRange kr = key_range(range, range_parts, RB);
+    const int low = kr.shift;  // the key bits below the bucket digit
+    if (low == 0 || n == 1) {  // equal keys (or one): already in order
+        for (int i = t; i < n; i += kBucketThreads) { out_key[start + i] = a_key[start + i]; out_id[start + i] = a_id[start + i]; }
+        return;
+    }
+    uint32_t dig[kBucketSteps], pos[kBucketSteps];
+    if (n <= kBucketCap) {
+        for (int i = t; i < n; i += kBucketThreads) { L.key[0][i] = a_key[start + i]; L.id[0][i] = a_id[start + i]; }
+        __syncthreads();
+        const int seg = bucket_seg(n);
+        const int wave = t >> 6, lane = __lane_id();
+        int cur = 0;
+        for (int sh = 0; sh < low; sh += 8) {
+            bucket_rank(L, cur, n, seg, kr.kmin, sh, min(8, low - sh), dig, pos);
+#pragma unroll
+            for (int r = 0; r < kBucketSteps; ++r) {
+                const int li = wave * seg + r * 64 + lane;
+                if (r < (seg >> 6) && li < n) {
+                    L.key[cur ^ 1][pos[r]] = L.key[cur][li];
+                    L.id[cur ^ 1][pos[r]] = L.id[cur][li];
+                }
+            }
+            __syncthreads();
+            cur ^= 1;
+        }
+        for (int i = t; i < n; i += kBucketThreads) { out_key[start + i] = L.key[cur][i]; out_id[start + i] = L.id[cur][i]; }
+        return;
+    }
+    // larger than LDS: each pass counts the bucket's digits, then ranks it chunk by chunk in order and
+    // writes every key to its place; the passes alternate between the bucket's ranges of the two arrays
+    uint32_t* src_k = a_key; uint32_t* src_i = a_id;
+    uint32_t* dst_k = out_key; uint32_t* dst_i = out_id;
+    for (int sh = 0; sh < low; sh += 8) {
+        const int bits = min(8, low - sh);
+        if (t < 256) L.gbase[t] = 0u;
+        __syncthreads();
+        for (int i = t; i < n; i += kBucketThreads)
+            atomicAdd(&L.gbase[((src_k[start + i] - kr.kmin) >> sh) & ((1u << bits) - 1u)], 1u);
+        __syncthreads();
+        uint32_t total;
+        const uint32_t g = t < 256 ? L.gbase[t] : 0u;
+        const uint32_t ex = block_exclusive_scan_bucket(g, L.scan, total);
+        if (t < 256) L.gbase[t] = ex;
+        __syncthreads();
+        for (int c0 = 0; c0 < n; c0 += kBucketCap) {
+            const int nc = min(kBucketCap, n - c0);
+            for (int i = t; i < nc; i += kBucketThreads) { L.key[0][i] = src_k[start + c0 + i]; L.id[0][i] = src_i[start + c0 + i]; }
+            __syncthreads();
+            const int seg = bucket_seg(nc);
+            bucket_rank(L, 0, nc, seg, kr.kmin, sh, bits, dig, pos);
+            const int wave = t >> 6, lane = __lane_id();
+#pragma unroll
+            for (int r = 0; r < kBucketSteps; ++r) {
+                const int li = wave * seg + r * 64 + lane;
+                if (r < (seg >> 6) && li < nc) {
+                    const uint32_t d = dig[r];
+                    const uint32_t gp = L.gbase[d] + (pos[r] - L.dpre[d]);
+                    dst_k[start + gp] = L.key[0][li];
+                    dst_i[start + gp] = L.id[0][li];
+                }
+            }
+            __syncthreads();
+            if (t < 256) L.gbase[t] += L.dcnt[t];
+            __syncthreads();
+        }
+        uint32_t* tk = src_k; src_k = dst_k; dst_k = tk;
+        uint32_t* ti = src_i; src_i = dst_i; dst_i = ti;
+    }
+    if (src_k != out_key) {  // an even number of passes ends in the input arrays
+        for (int i = t; i < n; i += kBucketThreads) { out_key[start + i] = src_k[start + i]; out_id[start + i] = src_i[start + i]; }
     }
 }
 
@@ -1147,18 +1382,21 @@ int geometry_of(const xsg_isect_desc* d, Geometry& g) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// The depth pre-order sorts the visible instances, usually a small part of the instances its grid
-// is sized for: 1024 keys per block spread them over four times as many workgroups. Large counts
-// (millions of visible instances: a lidar frame, a camera rig) run faster in tiles of 2048 keys
-// (longer runs per digit in each tile's scatter). The visible count is known only on the device when
-// the pre-order is queued, so the number of virtual instances, known to the host, chooses: one call's
-// launches depend on its own arguments only (both tile sizes sort identically).
+// The depth pre-order sorts the visible instances' depth bits. Below kPresortLargeAt virtual
+// instances (the count sizes the launches on the host; the visible count is known only on the
+// device when they are queued), in two stages: a stable most-significant-digit pass over the top 8
+// bits of each key's offset from the smallest visible key (the compaction finds the key range)
+// splits them into buckets of consecutive key values, and bucket_sort_kernel sorts each bucket by its
+// remaining bits: four launches, where four LSD passes over 32 bits take twelve, whose fixed cost
+// dominates at these counts; the same stable order. From kPresortLargeAt on (a lidar frame, a camera
+// rig: millions of visible instances), four LSD passes in tiles of 2048 keys, where buckets would
+// outgrow the LDS or need a wider first digit whose scatter coalesces poorly. One call's launches
+// depend on its own arguments only.
 constexpr int kPresortItems = 4;
 constexpr int kPresortItemsLarge = 8;
+constexpr int kPresortRB = 8;  // digit bits of both schemes
 constexpr int64_t kPresortLargeAt = 3000000;  // virtual instances (Gaussians x cameras x spans)
 constexpr unsigned kPresortGrid = 2048;
-constexpr int kPresortRB = 8;                                        // digit bits
-constexpr int kPresortPasses = (32 + kPresortRB - 1) / kPresortRB;  // over the 32 depth bits
 
 // count workspace: per virtual instance rectangle / count / depth bits, block partials, compaction
 struct CountWs {
@@ -1166,6 +1404,8 @@ struct CountWs {
     uint32_t* comp_id; uint32_t* comp_off; uint32_t* comp_key;
     // depth pre-order (sorted fills only): ping-pong, histograms, device-side count, run offsets
     uint32_t* alt_key; uint32_t* alt_id; uint32_t* hist; uint32_t* dtot; uint32_t* m_dev;
+    uint32_t* key_range;  // per count block, then per slice of them: smallest and largest visible depth key
+    uint32_t* slice_range;
     // after the pre-order: the depth-ordered instances (keys, ids) and the depth-ordered rectangles
     // (two words each), in whichever pair of the two ping-pong pairs the passes left free
     uint32_t* pre_key; uint32_t* pre_id; uint32_t* drect_lo; uint32_t* drect_hi;
@@ -1195,20 +1435,25 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     const size_t ns = g.sort ? (size_t)nv : 0;
     w.alt_key = (uint32_t*)(p + off); off += align256(4 * ns);
     w.alt_id = (uint32_t*)(p + off); off += align256(4 * ns);
-    const bool odd = kPresortPasses % 2 == 1;  // an odd number of passes ends in the alt pair
-    w.pre_key = odd ? w.alt_key : w.comp_key;
-    w.pre_id = odd ? w.alt_id : w.comp_id;
-    w.drect_lo = odd ? w.comp_key : w.alt_key;
-    w.drect_hi = odd ? w.comp_id : w.alt_id;
+    // the bucket pass scatters the compacted pairs into the alt pair and the bucket sort writes them
+    // back in order; the rectangles in depth order then go to the alt pair
+    w.pre_key = w.comp_key;
+    w.pre_id = w.comp_id;
+    w.drect_lo = w.alt_key;
+    w.drect_hi = w.alt_id;
     w.roff = (uint32_t*)(p + off); off += align256(4 * ns);
     w.hist = (uint32_t*)(p + off);
-    off += align256(g.sort ? 4 * ((size_t)1 << kPresortRB) * sort_blocks<kPresortItems>(nv > 0 ? nv : 1) : 0);
+    const size_t nv1 = nv > 0 ? (size_t)nv : 1;
+    const size_t hist_words = ((size_t)1 << kPresortRB) * sort_blocks<kPresortItems>(nv1);
+    off += align256(g.sort ? 4 * hist_words : 0);
     w.dtot = (uint32_t*)(p + off); off += align256(4 * ((size_t)1 << kPresortRB));
     w.rpart = (uint32_t*)(p + off); off += align256(4 * ((size_t)w.nb + 1));
     w.m_dev = (uint32_t*)(p + off); off += align256(4);
+    const size_t n_slices = ((size_t)w.nb + kSlice - 1) / kSlice;
+    w.key_range = (uint32_t*)(p + off); off += align256(8 * (size_t)w.nb);
+    w.slice_range = (uint32_t*)(p + off); off += align256(8 * n_slices);
     w.seam_cnt = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb : 0);
     w.seam_ids = (uint32_t*)(p + off); off += align256(g.spans == 2 ? 4 * (size_t)w.nb * (kCountTile / 2) : 0);
-    const size_t n_slices = ((size_t)w.nb + kSlice - 1) / kSlice;
     w.slice64 = (uint64_t*)(p + off); off += align256(8 * n_slices);
     w.slice_extra = (uint64_t*)(p + off); off += align256(16 * n_slices);
     w.slice32 = (uint32_t*)(p + off); off += align256(4 * n_slices);
@@ -1343,6 +1588,22 @@ static int count_readback(CountReadback*& out) {
     return XSG_OK;
 }
 
+// The depth pre-order: the bucket pass (compacted pairs -> alt pair, by the top RB bits of each key's
+// offset in the visible key range) and the per-bucket sort (alt pair -> pre pair).
+template <int ITEMS, int RB>
+void presort_buckets(const CountWs& w, int range_parts, hipStream_t s) {
+    const unsigned nb = sort_blocks<ITEMS>(w.n_virtual);
+    const unsigned grid = min(nb, kPresortGrid);
+    radix_upsweep<uint32_t, ITEMS, RB, true><<<grid, kSortBlock, 0, s>>>(w.comp_key, w.n_virtual, 0, RB, w.hist, nb,
+                                                                        w.m_dev, w.slice_range, range_parts);
+    radix_scan_hist<ITEMS><<<1u << RB, kSortBlock, 0, s>>>(w.hist, nb, w.dtot, w.n_virtual, w.m_dev);
+    radix_downsweep<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, ITEMS, RB, true><<<grid, kSortBlock, 0, s>>>(
+        w.comp_key, w.comp_id, w.n_virtual, 0, RB, w.hist, w.dtot, nb, PlainOut<uint32_t, uint32_t>{w.alt_key, w.alt_id},
+        w.m_dev, w.slice_range, range_parts);
+    bucket_sort_kernel<RB><<<1u << RB, kBucketThreads, 0, s>>>(w.dtot, w.slice_range, range_parts, w.alt_key, w.alt_id,
+                                                               w.pre_key, w.pre_id);
+}
+
 extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* workspace, int64_t* n_isects,
                                int64_t* n_visible, int64_t* n_runs, xsg_stream_t stream) {
     Geometry g;
@@ -1358,10 +1619,14 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (const int rc2 = xsg_check_workspace(workspace, "xsg_isect_count")) return rc2;
     const hipStream_t s = (hipStream_t)stream;
     const CountWs w = count_ws_layout(g, workspace);
+    // the bucketed depth pre-order takes its first digit from the visible keys' range: every count
+    // block records its own, each slice scan workgroup reduces its blocks' (no atomics)
+    const bool large_presort = w.n_virtual >= kPresortLargeAt;
+    uint32_t* key_range = g.sort && !large_presort ? w.key_range : nullptr;
     if (g.kind == XSG_TILING_REGULAR) {
         count_regular_kernel<<<w.nb, kBlock, 0, s>>>(nt, (const float2*)d->means2d, (const float2*)d->radii,
                                                      (float)d->tile_w, (float)d->tile_h, g.ntx, g.nty, tpg,
-                                                     w.rects, w.partials, w.cpart);
+                                                     w.rects, w.partials, w.cpart, d->depths, key_range);
     } else {
         if (!d->camera_pack || !d->flags || !d->points || !d->scales || !d->quats)
             return xsg_fail(XSG_ERR_INVALID, "lidar / spherical tiling needs camera and Gaussian tensors");
@@ -1374,20 +1639,20 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
             count_spherical_kernel<XSG_CAM_LIDAR, true><<<w.nb, kBlock, 0, s>>>(
                 nt, d->camera_pack, img, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
                 d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey,
-                w.partials, w.cpart, w.seam_cnt, w.seam_ids);
+                w.partials, w.cpart, w.seam_cnt, w.seam_ids, key_range);
             seam_span_kernel<XSG_CAM_LIDAR, true><<<seam_grid, kBlock, 0, s>>>(
                 w.nb, w.seam_cnt, w.seam_ids, d->camera_pack, ut, img, d->points, d->velocity, d->scales,
                 (const float4*)d->quats, d->opacity, d->elev_boundaries, d->n_elev, u_per_tile, v_per_tile, g.ntx,
-                g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart);
+                g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart, key_range);
         } else {
             count_spherical_kernel<XSG_CAM_SPHERICAL, false><<<w.nb, kBlock, 0, s>>>(
                 nt, d->camera_pack, img, d->flags, (const float2*)d->means2d, (const float2*)d->radii, d->depths,
                 nullptr, 0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects, w.vcnt, w.vkey, w.partials, w.cpart,
-                w.seam_cnt, w.seam_ids);
+                w.seam_cnt, w.seam_ids, key_range);
             seam_span_kernel<XSG_CAM_SPHERICAL, false><<<seam_grid, kBlock, 0, s>>>(
                 w.nb, w.seam_cnt, w.seam_ids, d->camera_pack, ut, img, d->points, d->velocity, d->scales,
                 (const float4*)d->quats, d->opacity, nullptr, 0, u_per_tile, v_per_tile, g.ntx, g.nty, tpg, w.rects,
-                w.vcnt, w.vkey, w.partials, w.cpart);
+                w.vcnt, w.vkey, w.partials, w.cpart, key_range);
         }
     }
     // the totals are final after the compaction, which publishes them to pinned host memory; an event
@@ -1397,7 +1662,8 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     rc = count_readback(rb);
     if (rc) return rc;
     const unsigned n_slices = (w.nb + kSlice - 1) / kSlice;
-    slice_scan_kernel<uint64_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.partials, w.slice64, w.cpart, w.slice_extra);
+    slice_scan_kernel<uint64_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.partials, w.slice64, w.cpart, w.slice_extra,
+                                                            key_range, w.slice_range);
     // regular tiling has one span per instance: its counts are tiles_per_gauss and its depth bits the
     // depths themselves
     const bool regular = g.kind == XSG_TILING_REGULAR;
@@ -1409,16 +1675,14 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
     if (hipEventRecord(rb->ev, s) != hipSuccess) return xsg_launch_status("isect_count readback event");
     if (g.sort) {
         // queued ahead of the readback, sized on the device: the visible spans in depth order
-        // (stable, kPresortPasses passes, result in pre_key / pre_id), then their row-run offsets
-        if (w.n_virtual >= kPresortLargeAt)
+        // (stable; result in pre_key / pre_id), then their row-run offsets
+        if (large_presort)  // four LSD passes over the 32 depth bits (an even count: the result is back in pre)
             radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItemsLarge, kPresortRB>(
                 w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
                 PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
         else
-            radix_sort_passes<uint32_t, uint32_t, PlainOut<uint32_t, uint32_t>, kPresortItems, kPresortRB>(
-                w.comp_key, w.comp_id, w.alt_key, w.alt_id, w.n_virtual, 0, 32, w.hist, w.dtot,
-                PlainOut<uint32_t, uint32_t>{w.pre_key, w.pre_id}, s, w.m_dev, false, kPresortGrid);
-        // the depth-ordered rectangles go to the pre-order's ping-pong buffers (free after its four passes)
+            presort_buckets<kPresortItems, kPresortRB>(w, (int)n_slices, s);
+        // the depth-ordered rectangles go to the bucket pass's output pair (free after the bucket sort)
         rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
                                                    w.drect_hi);
         slice_scan_kernel<uint32_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.rpart, w.slice32, nullptr, nullptr);

@@ -570,21 +570,68 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
 // computes them the same way (its depth, the centre's range, is then the stored depth bit for bit).
 struct SigmaUv { float u[7], v[7], r[7]; };
 
+// atan(y / x) for 0 <= |y| <= x / 4: the Taylor series of atan t to t^11 (the first term left out,
+// t^13 / 13, is below 2^-27 of atan t for |t| <= 1/4).
+XSG_DEV float atan_small(float y, float x) {
+    const float t = y * __builtin_amdgcn_rcpf(x);
+    const float t2 = t * t;
+    float q = -1.0f / 11.0f;
+    q = fmaf(q, t2, 1.0f / 9.0f);
+    q = fmaf(q, t2, -1.0f / 7.0f);
+    q = fmaf(q, t2, 1.0f / 5.0f);
+    q = fmaf(q, t2, -1.0f / 3.0f);
+    return fmaf(q * t2, t, t);
+}
+
+// The sigma points p = p0 +- e_k lie close to the centre p0 (0.17 of the Gaussian's scale), so their
+// azimuth and elevation are the centre's plus a small angle: the azimuth difference is
+// atan2(y0 ex - x0 ey, rho0^2 + x0 ex + y0 ey) (times the sign of the delta), the elevation difference
+// atan2(dz rho0 - z0 drho, rho rho0 + z z0) with rho - rho0 = (rho^2 - rho0^2) / (rho + rho0), both
+// formed from the deltas without cancellation and evaluated by atan_small; only the centre takes
+// atan2 / asin. A point whose angle difference is not small (a Gaussian near the camera or a pole), or
+// whose azimuth lands within 1e-4 of the image seam (where atan2's branch decides between 0 and 2 pi),
+// takes atan2 / asin of its own coordinates, as the centre does.
 XSG_DEV void sigma_uv(const Camera& c, f3 pw, const f3 d[3], SigmaUv& a) {
     const Mat3 m = static_world_to_camera(c);
-    const f3 pc0 = mul(m, pw - c.t0);
+    const f3 p0 = mul(m, pw - c.t0);
     f3 e[3];
 #pragma unroll
     for (int k = 0; k < 3; ++k) e[k] = mul(m, d[k]);
+    const float rho0_sq = p0.x * p0.x + p0.y * p0.y;
+    const float r0 = sqrtf(rho0_sq + p0.z * p0.z);
+    const float phi0 = atan2f(-p0.x, -p0.y) + float(M_PI);
+    const float theta0 = asinf(p0.z / r0);
+    const float rho0 = sqrtf(rho0_sq);
+    const float two_pi = 2.0f * float(M_PI);
+    // u and v by reciprocal multiplies (1 ulp): far below the float32 noise of the UT's weighted sums
+    const float inv_du = __builtin_amdgcn_rcpf(c.i1), inv_dv = __builtin_amdgcn_rcpf(c.i3);
+    a.u[0] = (phi0 - c.i0) * inv_du;
+    a.v[0] = (theta0 - c.i2) * inv_dv;
+    a.r[0] = r0;
 #pragma unroll
-    for (int i = 0; i < 7; ++i) {
-        const f3 p = i == 0 ? pc0 : ((i & 1) ? pc0 + e[(i - 1) >> 1] : pc0 - e[(i - 1) >> 1]);
-        const float x2y2 = p.x * p.x + p.y * p.y;
-        const float r = sqrtf(x2y2 + p.z * p.z);
-        const float phi = atan2f(-p.x, -p.y) + float(M_PI);
-        const float theta = asinf(p.z / r);
-        a.u[i] = (phi - c.i0) / c.i1;
-        a.v[i] = (theta - c.i2) / c.i3;
+    for (int i = 1; i < 7; ++i) {
+        const f3 ek = e[(i - 1) >> 1];
+        const float sg = (i & 1) ? 1.0f : -1.0f;
+        const f3 p = (i & 1) ? p0 + ek : p0 - ek;
+        const float cross_xy = sg * (p0.y * ek.x - p0.x * ek.y);   // y0 x - x0 y
+        const float dot_xy = rho0_sq + sg * (p0.x * ek.x + p0.y * ek.y);  // x0 x + y0 y
+        const float drho_sq = sg * 2.0f * (p0.x * ek.x + p0.y * ek.y) + (ek.x * ek.x + ek.y * ek.y);
+        const float rho_sq = p.x * p.x + p.y * p.y;
+        const float rho = sqrtf(rho_sq);
+        const float r = sqrtf(rho_sq + p.z * p.z);
+        float phi = phi0 + atan_small(cross_xy, dot_xy);
+        phi = phi <= 0.0f ? phi + two_pi : (phi > two_pi ? phi - two_pi : phi);
+        const bool phi_small = dot_xy > 0.0f && fabsf(cross_xy) <= 0.25f * dot_xy && phi > 1e-4f &&
+                               phi < two_pi - 1e-4f;
+        if (!phi_small) phi = atan2f(-p.x, -p.y) + float(M_PI);
+        const float drho = drho_sq * __builtin_amdgcn_rcpf(rho + rho0);
+        const float num = sg * ek.z * rho0 - p0.z * drho;
+        const float den = rho * rho0 + p.z * p0.z;
+        float theta;
+        if (den > 0.0f && fabsf(num) <= 0.25f * den) theta = theta0 + atan_small(num, den);
+        else theta = asinf(p.z / r);
+        a.u[i] = (phi - c.i0) * inv_du;
+        a.v[i] = (theta - c.i2) * inv_dv;
         a.r[i] = r;
     }
 }

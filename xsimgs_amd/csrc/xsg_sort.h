@@ -64,6 +64,33 @@ XSG_DEV uint32_t digit_of(K key, int shift, int bits) {
     return (uint32_t)((key >> shift) & (K)((1u << bits) - 1u));
 }
 
+// The most significant RB bits of a 32-bit key's offset from the smallest key: the digit of a
+// most-significant-digit pass that splits the keys into 1 << RB buckets of consecutive key values.
+// The key range comes from the device as n_part partial ranges (smallest, largest) in `range`, each
+// (~0, 0) when it saw no key. shift: the bits below the digit.
+struct KeyRange {
+    uint32_t kmin;
+    int shift;
+};
+XSG_DEV KeyRange key_range(const uint32_t* __restrict__ range, int n_part, int rb) {
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    for (int i = 0; i < n_part; ++i) {
+        kmin = min(kmin, range[2 * i]);
+        kmax = max(kmax, range[2 * i + 1]);
+    }
+    const uint32_t span = kmax > kmin ? kmax - kmin : 0u;  // kmin > kmax: no keys
+    const int width = span ? 32 - __clz(span) : 0;
+    return KeyRange{kmin, max(0, width - rb)};
+}
+
+// a pass's digit: bits [shift, shift + bits) of the key, or with a key range the top digit of the
+// key's offset in the range
+template <typename K, bool RANGE>
+XSG_DEV uint32_t pass_digit(K key, int shift, int bits, const KeyRange& kr) {
+    if constexpr (RANGE) return (uint32_t)(((uint32_t)key - kr.kmin) >> kr.shift) & ((1u << bits) - 1u);
+    else return digit_of<K>(key, shift, bits);
+}
+
 // A tile is kSortBlock * ITEMS keys; the tiles holding keys are [0, ceil(n / tile)). n_dev
 // (optional): the element count read on the device, at most n, with the grid sized on the host for
 // n: the upsweep and downsweep workgroups then loop over the tiles (grid stride), so that a grid
@@ -76,13 +103,17 @@ XSG_DEV unsigned active_tiles(int64_t n, const uint32_t* n_dev) {
 
 // RB: bits per digit (8 by default; up to 10 for a single pass over a wider key, the digit-indexed
 // arrays then holding 1 << RB entries, R / kSortBlock per thread).
-template <typename K, int ITEMS = kSortItems, int RB = 8>
+template <typename K, int ITEMS = kSortItems, int RB = 8, bool RANGE = false>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict__ keys, int64_t n, int shift,
                                                             int bits, uint32_t* __restrict__ hist, unsigned nb,
-                                                            const uint32_t* __restrict__ n_dev) {
+                                                            const uint32_t* __restrict__ n_dev,
+                                                            const uint32_t* __restrict__ range = nullptr,
+                                                            int range_parts = 0) {
     constexpr int R = 1 << RB, DPT = R / kSortBlock;
     static_assert(DPT >= 1 && DPT * kSortBlock == R, "a digit count that is a multiple of the block");
     if (n_dev) n = min(n, (int64_t)*n_dev);
+    KeyRange kr{0u, 0};
+    if constexpr (RANGE) kr = key_range(range, range_parts, RB);
     const unsigned nt = active_tiles<ITEMS>(n, nullptr);
     __shared__ uint32_t cnt[kWaves][R];
     const int t = threadIdx.x, wave = t >> 6;
@@ -97,7 +128,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict_
 #pragma unroll 4
         for (int k = 0; k < ITEMS; ++k) {
             const int64_t idx = base + (int64_t)k * kSortBlock + t;
-            if (idx < n) atomicAdd(&cnt[wave][digit_of<K>(keys[idx], shift, bits)], 1u);
+            if (idx < n) atomicAdd(&cnt[wave][pass_digit<K, RANGE>(keys[idx], shift, bits, kr)], 1u);
         }
         __syncthreads();
 #pragma unroll
@@ -146,15 +177,19 @@ struct PlainOut {
 // across steps. The block then combines the four waves' counts, reorders its keys by digit in
 // LDS and writes them out so that consecutive lanes store consecutive addresses of a digit's run.
 // Segments, steps and lanes are visited in input order, so the pass is stable.
-template <typename K, typename V, typename Out, int ITEMS = kSortItems, int RB = 8>
+template <typename K, typename V, typename Out, int ITEMS = kSortItems, int RB = 8, bool RANGE = false>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restrict__ keys_in,
                                                               const V* __restrict__ vals_in, int64_t n,
                                                               int shift, int bits,
                                                               const uint32_t* __restrict__ hist,
                                                               const uint32_t* __restrict__ digit_total,
                                                               unsigned nb, Out out,
-                                                              const uint32_t* __restrict__ n_dev) {
+                                                              const uint32_t* __restrict__ n_dev,
+                                                              const uint32_t* __restrict__ range = nullptr,
+                                                              int range_parts = 0) {
     if (n_dev) n = min(n, (int64_t)*n_dev);
+    KeyRange kr{0u, 0};
+    if constexpr (RANGE) kr = key_range(range, range_parts, RB);
     constexpr int R = 1 << RB, DPT = R / kSortBlock;  // thread t owns digits t * DPT .. t * DPT + DPT - 1
     constexpr int kTile = kSortBlock * ITEMS;
     constexpr int kSeg = kTile / kWaves;  // keys per wave
@@ -204,7 +239,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
             if (valid) {
                 key[r] = keys_in[tile0 + li];
                 val[r] = vals_in[tile0 + li];
-                d = digit_of<K>(key[r], shift, bits);
+                d = pass_digit<K, RANGE>(key[r], shift, bits, kr);
             }
             uint64_t peers = __ballot(valid);
             for (int b = 0; b < bits; ++b) {
@@ -238,7 +273,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
         for (int r = 0; r < kSteps; ++r) {
             const int li = seg0 + r * 64 + lane;
             if (li < n_tile) {
-                const uint32_t d = digit_of<K>(key[r], shift, bits);
+                const uint32_t d = pass_digit<K, RANGE>(key[r], shift, bits, kr);
                 const uint32_t pos = lpre[d] + wcnt[wave][d] + rank[r];
                 skeys[pos] = key[r];
                 svals[pos] = val[r];
@@ -247,7 +282,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
         __syncthreads();
         for (int i = t; i < n_tile; i += kSortBlock) {
             const K k = skeys[i];
-            const uint32_t d = digit_of<K>(k, shift, bits);
+            const uint32_t d = pass_digit<K, RANGE>(k, shift, bits, kr);
             out.put((int64_t)gbase[d] + (i - lpre[d]), k, svals[i]);
         }
     }
