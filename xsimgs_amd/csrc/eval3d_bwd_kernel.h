@@ -70,10 +70,12 @@ XSG_DEV float wave_reduce_scatter16_lds(const float (&v)[16], int nv, float* __r
     return s;
 }
 
-// Per-pixel state of the backward sweep.
+// Per-pixel state of the backward sweep. The ray origin is not kept: the tiles whose rays share one
+// origin never read it per pair, the others reload it (keeping it live would cost the registers
+// that decide the kernel's occupancy).
 template <int CS>
 struct BwdPixel {
-    f3 ro, rd;
+    f3 rd;
     float rt;
     float T, v_t;
     float buf;  // sum over composited pairs of fac (rgb . v_rgb + hit_t v_depth), minus T_final v_alpha
@@ -81,7 +83,6 @@ struct BwdPixel {
     float v_d;
     int32_t bin_final;
     bool inside;
-    int64_t pix;
     f3 v_ro, v_rd;
 };
 
@@ -224,12 +225,19 @@ XSG_DEV void bwd_pair(BwdPixel<CS>& px, const BwdGauss& gs, const BwdEval& e, co
     px.buf = fmaf(fac, u, px.buf);
 }
 
+// Waves per SIMD the compiler is asked to fit: four for the one-wavefront tiles of up to three colour
+// channels without per-pixel ray or time gradients (evaluating and compositing one pixel slot at a
+// time, they need about 139 registers; at 128 the few that do not fit are set-up values spilled
+// outside the pair loop), else whatever the registers allow.
+template <int CDIM, bool DYN, bool RG, int PX, int NT>
+constexpr int kBwdWaves = (NT == 64 && PX == 4 && !RG && !DYN && CDIM <= 3) ? 4 : 1;
+
 // PX pixels per thread: a workgroup of ceil(tile / PX) threads (rounded up to whole wavefronts) per
 // tile, thread tr owning the pixels PX tr ... PX tr + PX - 1 of the tile in row-major order. The
 // staged Gaussian's LDS reads, the wavefront reduction and the atomic adds are shared by the
 // thread's pixels.
 template <int CDIM, bool DYN, bool RG, int PX, int NT, bool COUNT>
-__global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(kBwdWaves<CDIM, DYN, RG, PX, NT>))) void eval3d_bwd_kernel(Eval3dParams p) {
     // NT: threads (and staged Gaussians per batch) at most
     constexpr int CL = (CDIM > 0 && CDIM <= kColorLdsMax) ? CDIM : 0;
     constexpr int CS = CDIM > 0 ? CDIM : 1;
@@ -263,7 +271,16 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
     const int32_t range_end = (gt == nblocks - 1) ? (int32_t)g.n_isects : p.offsets[gt + 1];
     const int64_t hw = (int64_t)g.width * g.height;
 
+    // a pixel's index in the [cams, H, W] images (utils.h:32-44), recomputed where needed rather than
+    // kept in registers
+    auto pixel_of = [&](int h) {
+        const int qi = PX * tr + h;
+        const int ty = qi / g.tile_w, tx = qi - ty * g.tile_w;
+        const int i = trow * g.tile_h + ty, j = tcol * g.tile_w + tx;
+        return (int64_t)cam * hw + min((int64_t)i * g.width + j, hw - 1);
+    };
     BwdPixel<CS> px[PX];
+    f3 ro0[PX];  // the pixels' ray origins, for the set-up only
 #pragma unroll
     for (int h = 0; h < PX; ++h) {
         BwdPixel<CS>& q = px[h];
@@ -271,34 +288,34 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
         const int ty = qi / g.tile_w, tx = qi - ty * g.tile_w;
         const int i = trow * g.tile_h + ty, j = tcol * g.tile_w + tx;  // utils.h:32-44
         q.inside = qi < bs && i < g.height && j < g.width;
-        q.pix = (int64_t)cam * hw + min((int64_t)i * g.width + j, hw - 1);
-        q.rd = q.inside ? ld3(p.ray_d + 3 * q.pix) : mk3(0.f, 0.f, 0.f);
-        q.ro = q.inside ? ld3(p.ray_o + 3 * q.pix) : mk3(0.f, 0.f, 0.f);
+        const int64_t pix = pixel_of(h);
+        q.rd = q.inside ? ld3(p.ray_d + 3 * pix) : mk3(0.f, 0.f, 0.f);
+        ro0[h] = q.inside ? ld3(p.ray_o + 3 * pix) : mk3(0.f, 0.f, 0.f);
         q.rt = 0.f;
-        if constexpr (DYN) q.rt = q.inside ? p.rtd[q.pix] : 0.0f;
-        const float T_final = 1.0f - p.render_alpha[q.pix];
+        if constexpr (DYN) q.rt = q.inside ? p.rtd[pix] : 0.0f;
+        const float T_final = 1.0f - p.render_alpha[pix];
         q.T = T_final;
 #pragma unroll
         for (int k = 0; k < CS; ++k) q.v_c[k] = 0.f;
 #pragma unroll
-        for (int k = 0; k < CDIM; ++k) q.v_c[k] = q.inside ? p.v_rgb[q.pix * CDIM + k] : 0.0f;
-        q.v_d = q.inside ? p.v_depth[q.pix] : 0.0f;
-        q.buf = q.inside ? -T_final * p.v_alpha[q.pix] : 0.0f;
-        q.bin_final = q.inside ? p.last_ids[q.pix] : 0;
+        for (int k = 0; k < CDIM; ++k) q.v_c[k] = q.inside ? p.v_rgb[pix * CDIM + k] : 0.0f;
+        q.v_d = q.inside ? p.v_depth[pix] : 0.0f;
+        q.buf = q.inside ? -T_final * p.v_alpha[pix] : 0.0f;
+        q.bin_final = q.inside ? p.last_ids[pix] : 0;
         q.v_t = 0.f;
         q.v_ro = mk3(0.f, 0.f, 0.f);
         q.v_rd = mk3(0.f, 0.f, 0.f);
     }
 
-    if (tr == 0) { s_origin[0] = px[0].ro.x; s_origin[1] = px[0].ro.y; s_origin[2] = px[0].ro.z; s_max = -1; }
+    if (tr == 0) { s_origin[0] = ro0[0].x; s_origin[1] = ro0[0].y; s_origin[2] = ro0[0].z; s_max = -1; }
     __syncthreads();
     const f3 o0 = mk3(s_origin[0], s_origin[1], s_origin[2]);
     bool same = true;
 #pragma unroll
     for (int h = 0; h < PX; ++h)
-        same = same && (!px[h].inside || (__float_as_uint(px[h].ro.x) == __float_as_uint(o0.x) &&
-                                          __float_as_uint(px[h].ro.y) == __float_as_uint(o0.y) &&
-                                          __float_as_uint(px[h].ro.z) == __float_as_uint(o0.z)));
+        same = same && (!px[h].inside || (__float_as_uint(ro0[h].x) == __float_as_uint(o0.x) &&
+                                          __float_as_uint(ro0[h].y) == __float_as_uint(o0.y) &&
+                                          __float_as_uint(ro0[h].z) == __float_as_uint(o0.z)));
     const bool fixed = !DYN && __syncthreads_and(same);
 
     int32_t lane_bin_final = px[0].bin_final;
@@ -314,7 +331,7 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
 #pragma unroll
         for (int h = 0; h < PX; ++h) {
             in2[h] = px[h].inside;
-            ro2[h] = px[h].ro;
+            ro2[h] = ro0[h];
             rd2[h] = px[h].rd;
             rt2[h] = px[h].rt;
         }
@@ -423,23 +440,6 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
                     if constexpr (DYN) gs.vel = mk3(s_vel[t].x, s_vel[t].y, s_vel[t].z);
                 }
                 const int32_t gidx = batch_end - t;
-                BwdEval e[PX];
-                bool any_valid = false;
-#pragma unroll
-                for (int h = 0; h < PX; ++h) {
-                    e[h] = bwd_eval<DYN, FIXED>(gs, px[h].ro, px[h].rd, px[h].rt,
-                                                px[h].inside && gidx <= px[h].bin_final);
-                    any_valid = any_valid || e[h].valid;
-                }
-                if (counting) {  // wave totals, scalar
-#pragma unroll
-                    for (int h = 0; h < PX; ++h) {
-                        n_eval += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[h].inside && gidx <= px[h].bin_final));
-                        n_contrib += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e[h].valid));
-                    }
-                }
-                if (__ballot(any_valid) == 0) continue;  // wave-uniform (eval3d_bwd.cu:209-212)
-
                 float rgb[CS];
 #pragma unroll
                 for (int k = 0; k < CS; ++k) rgb[k] = 0.f;
@@ -453,12 +453,38 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
                         for (int k = 0; k < CDIM; ++k) rgb[k] = cp[k];
                     }
                 }
+                // each pixel slot evaluated, then composited, in turn (one evaluation live at a time): the
+                // first slot always (its gradients initialise the accumulators), the others only when a
+                // lane of the wave takes the pair (eval3d_bwd.cu:209-212 skips pairs below the alpha
+                // threshold; an invalid pair adds exact zeros, so skipping whole slots changes nothing)
+                auto eval = [&](int h) {
+                    f3 ro = mk3(0.f, 0.f, 0.f);
+                    if constexpr (!FIXED) ro = px[h].inside ? ld3(p.ray_o + 3 * pixel_of(h)) : ro;
+                    const BwdEval e = bwd_eval<DYN, FIXED>(gs, ro, px[h].rd, px[h].rt,
+                                                           px[h].inside && gidx <= px[h].bin_final);
+                    if (counting) {  // wave totals, scalar
+                        n_eval += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(px[h].inside && gidx <= px[h].bin_final));
+                        n_contrib += (uint64_t)__popcll(__builtin_amdgcn_ballot_w64(e.valid));
+                    }
+                    return e;
+                };
                 float acc[K];
                 f3 vg_sum;
-                bwd_pair<CDIM, CS, K, DYN, RG, true>(px[0], gs, e[0], rgb, acc, vg_sum);
+                bool any_valid;
+                {
+                    const BwdEval e = eval(0);
+                    any_valid = __builtin_amdgcn_ballot_w64(e.valid) != 0;
+                    bwd_pair<CDIM, CS, K, DYN, RG, true>(px[0], gs, e, rgb, acc, vg_sum);
+                }
 #pragma unroll
-                for (int h = 1; h < PX; ++h)
-                    bwd_pair<CDIM, CS, K, DYN, RG, false>(px[h], gs, e[h], rgb, acc, vg_sum);
+                for (int h = 1; h < PX; ++h) {
+                    const BwdEval e = eval(h);
+                    if (__builtin_amdgcn_ballot_w64(e.valid) != 0) {  // wave-uniform
+                        any_valid = true;
+                        bwd_pair<CDIM, CS, K, DYN, RG, false>(px[h], gs, e, rgb, acc, vg_sum);
+                    }
+                }
+                if (!any_valid) continue;  // nothing to reduce (wave-uniform)
                 if constexpr (!(RG || DYN)) {
                     const f3 v_omm = rows_tmul(gs.r0, gs.r1, gs.r2, vg_sum);
                     acc[CDIM + 0] = -v_omm.x;
@@ -492,11 +518,12 @@ __global__ __launch_bounds__(NT) void eval3d_bwd_kernel(Eval3dParams p) {
 #pragma unroll
     for (int h = 0; h < PX; ++h) {
         if (px[h].inside) {
+            const int64_t pix = pixel_of(h);
             if constexpr (RG) {
-                st3(p.v_ray_o + 3 * px[h].pix, px[h].v_ro);
-                st3(p.v_ray_d + 3 * px[h].pix, px[h].v_rd);
+                st3(p.v_ray_o + 3 * pix, px[h].v_ro);
+                st3(p.v_ray_d + 3 * pix, px[h].v_rd);
             }
-            if constexpr (DYN) p.v_time[px[h].pix] = px[h].v_t;
+            if constexpr (DYN) p.v_time[pix] = px[h].v_t;
         }
     }
 }
