@@ -888,6 +888,194 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
     for (int d = threadIdx.x; d < R; d += kBlock) hist[(int64_t)d * nb + blockIdx.x] = s_hist[d];
 }
 
+// Scan of the per-group counts of every bucket over its first ceil(m / 64) groups, in slices of
+// kGroupSlice groups, grid (buckets, slices): group_slice_sum_kernel sums each slice, then
+// group_slice_scan_kernel scans each slice in place (exclusive) from the sum of the bucket's slices
+// before it; slice 0 also stores the bucket total.
+constexpr int kGroupSlice = kBlock * 16;
+
+__global__ __launch_bounds__(kBlock) void group_slice_sum_kernel(const uint32_t* __restrict__ hist, int64_t n_groups,
+                                                                 const uint32_t* __restrict__ m_dev,
+                                                                 uint32_t* __restrict__ part) {
+    __shared__ uint32_t lds[kWaves];
+    const int64_t ng = min(n_groups, ((int64_t)*m_dev + 63) / 64);
+    const int64_t s0 = (int64_t)blockIdx.y * kGroupSlice;
+    if (s0 >= ng) return;  // block-uniform
+    const uint32_t* h = hist + (int64_t)blockIdx.x * n_groups;
+    uint32_t sum = 0;
+    for (int64_t i = s0 + threadIdx.x; i < min(ng, s0 + kGroupSlice); i += kBlock) sum += h[i];
+    sum = block_reduce_sum<uint32_t>(sum, lds);
+    if (threadIdx.x == 0) part[(int64_t)blockIdx.x * gridDim.y + blockIdx.y] = sum;
+}
+
+__global__ __launch_bounds__(kBlock) void group_slice_scan_kernel(uint32_t* __restrict__ hist, int64_t n_groups,
+                                                                  const uint32_t* __restrict__ m_dev,
+                                                                  const uint32_t* __restrict__ part,
+                                                                  uint32_t* __restrict__ total) {
+    __shared__ uint32_t lds[kWaves];
+    const int64_t ng = min(n_groups, ((int64_t)*m_dev + 63) / 64);
+    const unsigned n_slices = (unsigned)((ng + kGroupSlice - 1) / kGroupSlice);
+    const unsigned k = blockIdx.y;
+    const uint32_t* pr = part + (int64_t)blockIdx.x * gridDim.y;
+    if (k == 0) {  // block-uniform
+        uint32_t acc = 0;
+        for (unsigned j = threadIdx.x; j < n_slices; j += kBlock) acc += pr[j];
+        acc = block_reduce_sum<uint32_t>(acc, lds);
+        if (threadIdx.x == 0) total[blockIdx.x] = acc;
+    }
+    if (k >= n_slices) return;  // block-uniform
+    uint32_t acc = 0;
+    for (unsigned j = threadIdx.x; j < k; j += kBlock) acc += pr[j];
+    uint32_t run = block_reduce_sum<uint32_t>(acc, lds);
+    uint32_t* h = hist + (int64_t)blockIdx.x * n_groups;
+    const int64_t s0 = (int64_t)k * kGroupSlice;
+    const int64_t i0 = s0 + (int64_t)threadIdx.x * 16;
+    uint32_t v[16], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        v[j] = i0 + j < ng ? h[i0 + j] : 0u;
+        sum += v[j];
+    }
+    uint32_t tot;
+    run += block_exclusive_scan<uint32_t>(sum, lds, tot);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (i0 + j < ng) h[i0 + j] = run;
+        run += v[j];
+    }
+}
+
+// Direct placement of the row runs, for at most kDirectRows row buckets (camera rows plus the
+// negative-depth bucket): instead of expanding the runs in depth order and sorting them stably by row
+// bucket, every group of 64 depth-ordered instances (one wavefront step) counts its runs per row
+// bucket (rows_hist_kernel, which also gathers the rectangles in depth order), one scan per bucket
+// over the groups gives each (bucket, group) its first position (radix_scan_hist), and
+// place_runs_kernel, one wavefront per group, writes each run straight to its place, bucket by bucket
+// in lane order. Every bucket thus holds its runs in depth order: the order the stable sort gave.
+constexpr int kDirectRows = 256;
+constexpr int kGroupsPerCountBlock = kCountTile / 64;
+
+XSG_DEV void run_rows(uint32_t key, Rect r, uint32_t v, int spans, int64_t n_per_cam, int nty, uint32_t& lo,
+                      uint32_t& hi, uint32_t& n_neg) {
+    // non-negative keys: buckets [lo, hi), one run each; a negative key: n_neg runs in the last bucket
+    if ((int32_t)key < 0) {
+        lo = hi = 0u;
+        n_neg = (uint32_t)(r.y1 - r.y0);
+        return;
+    }
+    const uint32_t inst = v / (uint32_t)spans;
+    const uint32_t cid = n_per_cam > 0 ? (uint32_t)(inst / (uint64_t)n_per_cam) : 0u;
+    lo = cid * (uint32_t)nty + r.y0;
+    hi = cid * (uint32_t)nty + r.y1;
+    n_neg = 0u;
+}
+
+// A count block of depth-ordered instances: their rectangles to d_lo / d_hi, and per group of 64
+// (wavefront w, step k: group kGroupsPerCountBlock b + 4 k + w) its runs per bucket,
+// hist[bucket * n_groups + group].
+__global__ __launch_bounds__(kBlock) void rows_hist_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
+                                                           const uint32_t* __restrict__ ids,
+                                                           const uint32_t* __restrict__ keys,
+                                                           const Rect* __restrict__ rects, int nty, int64_t n_per_cam,
+                                                           int spans, int n_rows, int64_t n_groups,
+                                                           uint32_t* __restrict__ hist, uint32_t* __restrict__ d_lo,
+                                                           uint32_t* __restrict__ d_hi) {
+    __shared__ uint32_t s_h[kWaves][kDirectRows];
+    m = min(m, (int64_t)*m_dev);
+    const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    if (base >= m) return;  // block-uniform; the scan reads the active groups only
+    const int wave = threadIdx.x >> 6, lane = __lane_id();
+    uint32_t* h = s_h[wave];
+    const uint32_t neg = (uint32_t)(n_rows - 1);
+    for (int k = 0; k < kCountItems; ++k) {
+        const int64_t grp = (int64_t)blockIdx.x * kGroupsPerCountBlock + k * kWaves + wave;
+        const int64_t p = grp * 64 + lane;
+        if (grp * 64 >= m) break;  // wave-uniform
+        for (int i = lane; i < n_rows; i += 64) h[i] = 0u;
+        if (p < m) {
+            const uint32_t v = ids[p];
+            const Rect r = rects[v];
+            d_lo[p] = (uint32_t)r.x0 | ((uint32_t)r.y0 << 16);
+            d_hi[p] = (uint32_t)r.x1 | ((uint32_t)r.y1 << 16);
+            uint32_t lo, hi, n_neg;
+            run_rows(keys[p], r, v, spans, n_per_cam, nty, lo, hi, n_neg);
+            if (n_neg) atomicAdd(&h[neg], n_neg);
+            for (uint32_t b = lo; b < hi; ++b) atomicAdd(&h[b], 1u);
+        }
+        for (int i = lane; i < n_rows; i += 64) hist[(int64_t)i * n_groups + grp] = h[i];
+    }
+}
+
+XSG_DEV uint32_t wave_min_u32(uint32_t x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x = min(x, (uint32_t)__shfl_xor((int)x, off, 64));
+    return x;
+}
+XSG_DEV uint32_t wave_max_u32(uint32_t x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, off, 64));
+    return x;
+}
+
+// One wavefront per group of 64 instances: each bucket's first position for the group (the bucket's
+// base, an exclusive scan of the bucket totals, plus the group's scanned count), then the runs,
+// bucket by bucket, at consecutive positions in lane order.
+__global__ __launch_bounds__(64) void place_runs_kernel(int64_t m, const uint32_t* __restrict__ ids,
+                                                        const uint32_t* __restrict__ keys,
+                                                        const uint32_t* __restrict__ d_lo,
+                                                        const uint32_t* __restrict__ d_hi, int nty, int64_t n_per_cam,
+                                                        int spans, int n_rows, int64_t n_groups,
+                                                        const uint32_t* __restrict__ hist,
+                                                        const uint32_t* __restrict__ row_tot,
+                                                        uint4* __restrict__ out_rec) {
+    __shared__ uint32_t s_at[kDirectRows];
+    const int lane = __lane_id();
+    const int64_t grp = blockIdx.x;
+    // bucket bases: lane l holds buckets 4 l .. 4 l + 3
+    constexpr int kPer = kDirectRows / 64;
+    uint32_t c[kPer], sum = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int b = lane * kPer + j;
+        c[j] = b < n_rows ? row_tot[b] : 0u;
+        sum += c[j];
+    }
+    uint32_t run = wave_inclusive_scan<uint32_t>(sum) - sum;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int b = lane * kPer + j;
+        if (b < n_rows) s_at[b] = run + hist[(int64_t)b * n_groups + grp];
+        run += c[j];
+    }
+    __syncthreads();
+    const int64_t p = grp * 64 + lane;
+    uint32_t lo = 0u, hi = 0u, n_neg = 0u;
+    uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+    if (p < m) {
+        const uint32_t v = ids[p], key = keys[p];
+        const Rect r = rect_of(d_lo[p], d_hi[p]);
+        run_rows(key, r, v, spans, n_per_cam, nty, lo, hi, n_neg);
+        rec = make_uint4(v / (uint32_t)spans, key, (uint32_t)r.x0 | ((uint32_t)r.x1 << 16), 0u);
+    }
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t b0 = wave_min_u32(lo < hi ? lo : 0xffffffffu);
+    const uint32_t b1 = wave_max_u32(hi);
+    for (uint32_t b = b0; b < b1; ++b) {  // wave-uniform
+        const bool cov = lo <= b && b < hi;
+        const uint64_t mk = __ballot(cov);
+        if (cov) {
+            rec.w = b;
+            out_rec[s_at[b] + (uint32_t)__popcll(mk & lt)] = rec;
+        }
+    }
+    if (__ballot(n_neg > 0)) {  // negative keys: n_neg identical runs each, in lane order
+        const uint32_t neg = (uint32_t)(n_rows - 1);
+        const uint32_t at = s_at[neg] + wave_inclusive_scan<uint32_t>(n_neg) - n_neg;
+        rec.w = neg;
+        for (uint32_t q = 0; q < n_neg; ++q) out_rec[at + q] = rec;
+    }
+}
+
 // row_start[r] = first sorted run of row bucket r (r in [0, n_rows]) from the sorted row buckets, one
 // thread per boundary between runs i - 1 and i: it starts the rows (rows[i - 1], rows[i]] (from row 0
 // before the first run, to n_rows after the last), so every row is written once.
@@ -1412,9 +1600,15 @@ struct CountWs {
     uint32_t* roff; uint32_t* rpart;
     uint32_t* seam_cnt; uint32_t* seam_ids;  // per count block: its seam Gaussians (two spans only)
     uint64_t* slice64; uint64_t* slice_extra; uint32_t* slice32;  // slice totals of the two-level scans
+    // direct run placement (sorted fills of at most kDirectRows row buckets): per count block and
+    // bucket the block's runs (scanned in place), and the bucket totals
+    bool direct; int n_rows;
+    uint32_t* row_hist; uint32_t* row_part; uint32_t* row_tot;
     int64_t n_virtual; unsigned nb;
     size_t bytes;
 };
+
+int row_buckets(const Geometry& g) { return g.n_cams * g.nty + 1; }  // camera rows + the negative bucket
 
 CountWs count_ws_layout(const Geometry& g, void* base) {
     CountWs w;
@@ -1457,6 +1651,13 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     w.slice64 = (uint64_t*)(p + off); off += align256(8 * n_slices);
     w.slice_extra = (uint64_t*)(p + off); off += align256(16 * n_slices);
     w.slice32 = (uint32_t*)(p + off); off += align256(4 * n_slices);
+    w.n_rows = row_buckets(g);
+    w.direct = g.sort && w.n_rows <= kDirectRows;
+    const size_t nr = w.direct ? (size_t)w.n_rows : 0;
+    w.row_hist = (uint32_t*)(p + off); off += align256(4 * nr * w.nb * kGroupsPerCountBlock);
+    w.row_part = (uint32_t*)(p + off);
+    off += align256(4 * nr * (((size_t)w.nb * kGroupsPerCountBlock + kGroupSlice - 1) / kGroupSlice));
+    w.row_tot = (uint32_t*)(p + off); off += align256(4 * nr);
     w.bytes = off;
     return w;
 }
@@ -1478,7 +1679,8 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     char* p = (char*)base;
     FillWs w{};
     size_t off = 0;
-    w.n_rows = g.n_cams * g.nty + 1;
+    w.n_rows = row_buckets(g);
+    const bool direct = w.n_rows <= kDirectRows;  // the runs are placed, not sorted: one record array
     w.row_bits = 1;
     while ((1u << w.row_bits) <= (uint32_t)(w.n_rows - 1)) ++w.row_bits;
     w.rb = run_sort_rb(w.row_bits);
@@ -1487,17 +1689,18 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     w.n_slots = w.s_max * g.ntx;
     const unsigned nb_r = sort_blocks<kRunSortItems>(n_runs > 0 ? n_runs : 1);
     auto take = [&](size_t bytes) { void* q = p + off; off += align256(bytes); return q; };
-    w.row_a = (uint32_t*)take(4 * n_runs);
-    w.row_b = (uint32_t*)take(4 * n_runs);
+    const size_t n_sorted = direct ? 0 : (size_t)n_runs;
+    w.row_a = (uint32_t*)take(4 * n_sorted);
+    w.row_b = (uint32_t*)take(4 * n_sorted);
     w.rec_a = (uint4*)take(16 * n_runs);
-    w.rec_b = (uint4*)take(16 * n_runs);
+    w.rec_b = (uint4*)take(16 * n_sorted);
     w.row_start = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
     w.seg_base = (uint32_t*)take(4 * ((size_t)w.n_rows + 1));
     w.seg_row = (uint32_t*)take(4 * (size_t)w.s_max);
     w.slots = (uint32_t*)take(4 * (size_t)w.n_slots);
     w.tile_tot = (uint32_t*)take(4 * ((size_t)(w.n_rows - 1) * g.ntx + 1));
-    w.hist = (uint32_t*)take(4 * ((size_t)1 << w.rb) * nb_r);
-    w.dtot = (uint32_t*)take(4 * ((size_t)1 << w.rb));
+    w.hist = (uint32_t*)take(direct ? 0 : 4 * ((size_t)1 << w.rb) * nb_r);
+    w.dtot = (uint32_t*)take(direct ? 0 : 4 * ((size_t)1 << w.rb));
     w.bytes = off;
     return w;
 }
@@ -1683,11 +1886,22 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         else
             presort_buckets<kPresortItems, kPresortRB>(w, (int)n_slices, s);
         // the depth-ordered rectangles go to the bucket pass's output pair (free after the bucket sort)
-        rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
-                                                   w.drect_hi);
-        slice_scan_kernel<uint32_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.rpart, w.slice32, nullptr, nullptr);
-        rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.drect_lo, w.drect_hi, w.rpart, w.slice32,
-                                                 w.roff);
+        if (w.direct) {  // per count block and row bucket, the block's runs; their scans
+            const int64_t n_per_cam = g.n_cams > 1 ? g.n : 0;
+            const int64_t n_groups = (int64_t)w.nb * kGroupsPerCountBlock;
+            rows_hist_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.pre_key, w.rects, g.nty,
+                                                     n_per_cam, g.spans, w.n_rows, n_groups, w.row_hist, w.drect_lo,
+                                                     w.drect_hi);
+            const dim3 sgrid((unsigned)w.n_rows, (unsigned)((n_groups + kGroupSlice - 1) / kGroupSlice));
+            group_slice_sum_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev, w.row_part);
+            group_slice_scan_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev, w.row_part, w.row_tot);
+        } else {
+            rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
+                                                       w.drect_hi);
+            slice_scan_kernel<uint32_t><<<n_slices, kBlock, 0, s>>>(w.nb, w.rpart, w.slice32, nullptr, nullptr);
+            rows_scan_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.drect_lo, w.drect_hi, w.rpart,
+                                                     w.slice32, w.roff);
+        }
     }
     XSG_TRY_LAUNCH("isect_count");
     // packed (visible << 32 | count) total, exact intersection total, exact row-run total; poll the
@@ -1764,32 +1978,42 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     const FillWs fw = fill_ws_layout(g, n_runs, fill_workspace);
     const uint32_t neg_row = (uint32_t)(fw.n_rows - 1);
     const int n_real = fw.n_rows - 1;
-    // stable sort of the runs (row bucket, record) by row bucket, ping-ponging between the a and b
-    // buffers: an odd number of passes ends in b
-    const bool odd = fw.passes % 2 == 1;
-    uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
-    uint4* rec_sorted = odd ? fw.rec_b : fw.rec_a;
-    const uint4* rec = rec_sorted;
-    switch (fw.rb) {
-        case 9: expand_and_sort_runs<9>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
-                                        rec_sorted, s); break;
-        case 10: expand_and_sort_runs<10>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
-                                          rec_sorted, s); break;
-        default: expand_and_sort_runs<8>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
-                                         rec_sorted, s); break;
+    const uint4* rec;
+    const uint32_t* row_count;  // with one pass or direct placement: the bucket totals (else row_start)
+    if (cw.direct) {
+        // every run written to its place in (row bucket, depth) order
+        place_runs_kernel<<<(unsigned)((m + 63) / 64), 64, 0, s>>>(
+            m, cw.pre_id, cw.pre_key, cw.drect_lo, cw.drect_hi, g.nty, n_per_cam, g.spans, fw.n_rows,
+            (int64_t)cw.nb * kGroupsPerCountBlock, cw.row_hist, cw.row_tot, fw.rec_a);
+        rec = fw.rec_a;
+        row_count = cw.row_tot;
+    } else {
+        // stable sort of the runs (row bucket, record) by row bucket, ping-ponging between the a and b
+        // buffers: an odd number of passes ends in b
+        const bool odd = fw.passes % 2 == 1;
+        uint32_t* rows_sorted = odd ? fw.row_b : fw.row_a;
+        uint4* rec_sorted = odd ? fw.rec_b : fw.rec_a;
+        rec = rec_sorted;
+        row_count = fw.passes == 1 ? fw.dtot : nullptr;
+        switch (fw.rb) {
+            case 9: expand_and_sort_runs<9>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
+                                            rec_sorted, s); break;
+            case 10: expand_and_sort_runs<10>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
+                                              rec_sorted, s); break;
+            default: expand_and_sort_runs<8>(fw, cw, n_runs, m, g.nty, n_per_cam, g.spans, neg_row, rows_sorted,
+                                             rec_sorted, s); break;
+        }
+        if (fw.passes > 1)
+            row_start_kernel<<<xsg_blocks(n_runs + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
+                                                                             fw.row_start);
     }
-    if (fw.passes > 1)
-        row_start_kernel<<<xsg_blocks(n_runs + 1, kBlock), kBlock, 0, s>>>(rows_sorted, n_runs, fw.n_rows,
-                                                                         fw.row_start);
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals
     if (fw.n_rows <= kFusedRows) {
         seg_count_rows_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
-            fw.n_rows, fw.passes == 1 ? fw.dtot : nullptr, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx,
-            fw.slots);
+            fw.n_rows, row_count, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
     } else {
-        row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, fw.passes == 1 ? fw.dtot : nullptr, fw.row_start,
-                                                 fw.seg_base, fw.seg_row);
+        row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, row_count, fw.row_start, fw.seg_base, fw.seg_row);
         seg_count_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
             n_real, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
     }
