@@ -891,8 +891,10 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
 // Scan of the per-group counts of every bucket over its first ceil(m / 64) groups, in slices of
 // kGroupSlice groups, grid (buckets, slices): group_slice_sum_kernel sums each slice, then
 // group_slice_scan_kernel scans each slice in place (exclusive) from the sum of the bucket's slices
-// before it; slice 0 also stores the bucket total.
-constexpr int kGroupSlice = kBlock * 16;
+// before it, and slice 0 stores the bucket total. When every group fits one slice (the host's bound),
+// the sums are not needed: part is null and slice 0's own total is the bucket's.
+constexpr int kGroupChunk = kBlock * 16;
+constexpr int kGroupSlice = kGroupChunk * 4;
 
 __global__ __launch_bounds__(kBlock) void group_slice_sum_kernel(const uint32_t* __restrict__ hist, int64_t n_groups,
                                                                  const uint32_t* __restrict__ m_dev,
@@ -916,33 +918,40 @@ __global__ __launch_bounds__(kBlock) void group_slice_scan_kernel(uint32_t* __re
     const int64_t ng = min(n_groups, ((int64_t)*m_dev + 63) / 64);
     const unsigned n_slices = (unsigned)((ng + kGroupSlice - 1) / kGroupSlice);
     const unsigned k = blockIdx.y;
-    const uint32_t* pr = part + (int64_t)blockIdx.x * gridDim.y;
-    if (k == 0) {  // block-uniform
+    const uint32_t* pr = part ? part + (int64_t)blockIdx.x * gridDim.y : nullptr;
+    if (k == 0 && pr) {  // block-uniform
         uint32_t acc = 0;
         for (unsigned j = threadIdx.x; j < n_slices; j += kBlock) acc += pr[j];
         acc = block_reduce_sum<uint32_t>(acc, lds);
         if (threadIdx.x == 0) total[blockIdx.x] = acc;
     }
-    if (k >= n_slices) return;  // block-uniform
-    uint32_t acc = 0;
-    for (unsigned j = threadIdx.x; j < k; j += kBlock) acc += pr[j];
-    uint32_t run = block_reduce_sum<uint32_t>(acc, lds);
+    if (k >= max(n_slices, 1u)) return;  // block-uniform
+    uint32_t run = 0;
+    if (pr) {
+        uint32_t acc = 0;
+        for (unsigned j = threadIdx.x; j < k; j += kBlock) acc += pr[j];
+        run = block_reduce_sum<uint32_t>(acc, lds);
+    }
     uint32_t* h = hist + (int64_t)blockIdx.x * n_groups;
-    const int64_t s0 = (int64_t)k * kGroupSlice;
-    const int64_t i0 = s0 + (int64_t)threadIdx.x * 16;
-    uint32_t v[16], sum = 0;
+    for (int c = 0; c < kGroupSlice / kGroupChunk; ++c) {
+        const int64_t i0 = (int64_t)k * kGroupSlice + (int64_t)c * kGroupChunk + (int64_t)threadIdx.x * 16;
+        if (i0 - (int64_t)threadIdx.x * 16 >= ng) break;  // block-uniform
+        uint32_t v[16], sum = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        v[j] = i0 + j < ng ? h[i0 + j] : 0u;
-        sum += v[j];
-    }
-    uint32_t tot;
-    run += block_exclusive_scan<uint32_t>(sum, lds, tot);
+        for (int j = 0; j < 16; ++j) {
+            v[j] = i0 + j < ng ? h[i0 + j] : 0u;
+            sum += v[j];
+        }
+        uint32_t tot;
+        uint32_t at = run + block_exclusive_scan<uint32_t>(sum, lds, tot);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (i0 + j < ng) h[i0 + j] = run;
-        run += v[j];
+        for (int j = 0; j < 16; ++j) {
+            if (i0 + j < ng) h[i0 + j] = at;
+            at += v[j];
+        }
+        run += tot;
     }
+    if (!pr && threadIdx.x == 0) total[blockIdx.x] = run;  // the only slice
 }
 
 // Direct placement of the row runs, for at most kDirectRows row buckets (camera rows plus the
@@ -1893,8 +1902,11 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
                                                      n_per_cam, g.spans, w.n_rows, n_groups, w.row_hist, w.drect_lo,
                                                      w.drect_hi);
             const dim3 sgrid((unsigned)w.n_rows, (unsigned)((n_groups + kGroupSlice - 1) / kGroupSlice));
-            group_slice_sum_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev, w.row_part);
-            group_slice_scan_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev, w.row_part, w.row_tot);
+            const bool one_slice = sgrid.y == 1;
+            if (!one_slice)
+                group_slice_sum_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev, w.row_part);
+            group_slice_scan_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev,
+                                                             one_slice ? nullptr : w.row_part, w.row_tot);
         } else {
             rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
                                                        w.drect_hi);
