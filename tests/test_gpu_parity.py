@@ -207,10 +207,12 @@ def test_isect_regular_many_visible(dev):
 
 
 def test_isect_presort_tile_sizes(dev):
-    """The depth pre-order sorts in tiles of 1024 or 2048 keys, chosen by the call's number of virtual
-    instances (3 M or more: 2048); both must order the keys as the oracle does. A 3.2 M-Gaussian scene
-    (2048-key tiles) and its first half (1024-key tiles), with ties in depth; a call's result does not
-    depend on an earlier call's size (the small scene binned between two identical calls)."""
+    """The depth pre-order takes one of two schemes by the call's number of virtual instances: from 3 M
+    on, four LSD passes in tiles of 2048 keys; below, a most-significant-digit pass over the keys'
+    offsets from the smallest visible key and an LDS sort of each bucket. Both must order the keys as
+    the oracle does. A 3.2 M-Gaussian scene (LSD) and its first half (buckets), with ties in depth; a
+    call's result does not depend on an earlier call's size (the small scene binned between two
+    identical calls)."""
     g = np.random.default_rng(23)
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     W, H = 1920, 1080
