@@ -77,8 +77,8 @@ XSG_DEV bool ut_projection_static_pinhole(const Camera& c, const Mat3& m, const 
         }
     }
     if (!result) return false;  // the caller keeps nothing of a failed projection
-    const float extend = fminf(3.33f, sqrtf(2.0f * logf(opac / (1.0f / 255.0f))));
-    radii = mk2(extend * sqrtf(fmaxf(0.0f, cov_xx_xy.x)), extend * sqrtf(fmaxf(0.0f, cov_yy)));
+    const float extend = ut_extend(opac);
+    radii = mk2(extend * hw_sqrt(fmaxf(0.0f, cov_xx_xy.x)), extend * hw_sqrt(fmaxf(0.0f, cov_yy)));
     const bool ix = !(((mean2d.x + radii.x) < 0) || (img.x < (mean2d.x - radii.x)));
     const bool iy = !(((mean2d.y + radii.y) < 0) || (img.y < (mean2d.y - radii.y)));
     return ix && iy;
@@ -195,11 +195,12 @@ __global__ __launch_bounds__(kBlock) void ut_project_phm_kernel(
             float dc = 0.f, dl = 0.f, dr = 0.f, ud = 0.f;
             SigmaUv sa;
             f3 pv = mk3(0.f, 0.f, 0.f);
+            const float ext = ut_extend(op);
             if constexpr (STATIC_POSE) sigma_uv(cam, pw, d, sa);
             else if (vel) pv = ld3(vel + 3 * i);
             auto project = [&](int mode, f2& m2, f2& r2, float& dd) {
                 if constexpr (STATIC_POSE)
-                    return ut_projection_sigma_uv(cam, unwrap, mode, ut, img, pp, op, sa, m2, r2, dd, ud);
+                    return ut_projection_sigma_uv(cam, unwrap, mode, ut, img, pp, ext, sa, m2, r2, dd, ud);
                 else
                     return ut_projection<KIND>(cam, mode, ut, img, pp, pw, pv, op, d, false, m2, r2, dd, ud);
             };

@@ -343,7 +343,8 @@ __global__ __launch_bounds__(kBlock) void seam_span_kernel(
             // the stored depth bit for bit, as both spans' keys carry one depth in the reference
             SigmaUv sa;
             sigma_uv(cam, pw, d, sa);
-            ok = ut_projection_sigma_uv(cam, unwrap, XSG_MODE_POSITIVE, ut, img, pp, op, sa, m2, r2, dd, ud);
+            ok = ut_projection_sigma_uv(cam, unwrap, XSG_MODE_POSITIVE, ut, img, pp, ut_extend(op), sa, m2, r2, dd,
+                                        ud);
         } else {
             const f3 pv = vel ? ld3(vel + 3 * j) : mk3(0.f, 0.f, 0.f);
             ok = ut_projection<KIND>(cam, XSG_MODE_POSITIVE, ut, img, pp, pw, pv, op, d, false, m2, r2, dd, ud);

@@ -487,8 +487,16 @@ XSG_DEV void static_camera_projection(const Camera& c, f3 pc, const ProjParams& 
 // On failure mean2d / depth keep what the reference leaves in them (untouched if the centre point
 // fails, the accumulated mean if a sigma point fails) and radii come from a zero covariance, because the
 // phase-modelled selection (ut_phm_kernels.h:417-421) can pick a failed side.
+// The opacity-aware extent of the radii (ut_kernels.h:175-177): one per Gaussian, whatever the mode.
+XSG_DEV float ut_extend(float opac) { return fminf(3.33f, sqrtf(2.0f * logf(opac / (1.0f / 255.0f)))); }
+
+// sqrt by the hardware instruction (v_sqrt_f32, within 1 ulp) where the UT's float32 noise is far larger
+// than an ulp: the sigma points' ranges and the radii. sqrtf's correctly rounded expansion costs about
+// fourteen instructions instead of one.
+XSG_DEV float hw_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+
 template <typename Proj>
-XSG_DEV bool ut_projection_core(const UtWeights& ut, f2 img, float opac, Proj&& proj, f2& mean2d, f2& radii,
+XSG_DEV bool ut_projection_core(const UtWeights& ut, f2 img, float extend, Proj&& proj, f2& mean2d, f2& radii,
                                 float& depth, float& u_distance) {
     float4 uvdt;
     bool valid = true;
@@ -530,8 +538,7 @@ XSG_DEV bool ut_projection_core(const UtWeights& ut, f2 img, float opac, Proj&& 
             cov_yy = cy;
         }
     }
-    const float extend = fminf(3.33f, sqrtf(2.0f * logf(opac / (1.0f / 255.0f))));
-    radii = mk2(extend * sqrtf(fmaxf(0.0f, cov_xx_xy.x)), extend * sqrtf(fmaxf(0.0f, cov_yy)));
+    radii = mk2(extend * hw_sqrt(fmaxf(0.0f, cov_xx_xy.x)), extend * hw_sqrt(fmaxf(0.0f, cov_yy)));
     const bool ix = !(((mean2d.x + radii.x) < 0) || (img.x < (mean2d.x - radii.x)));
     const bool iy = !(((mean2d.y + radii.y) < 0) || (img.y < (mean2d.y - radii.y)));
     return result && ix && iy;
@@ -554,13 +561,13 @@ XSG_DEV bool ut_projection(const Camera& c, int mode, const UtWeights& ut, f2 im
             const f3 pc = i == 0 ? pc0 : ((i & 1) ? pc0 + e[(i - 1) >> 1] : pc0 - e[(i - 1) >> 1]);
             static_camera_projection<KIND>(c, pc, pp, mode, uvdt, valid);
         };
-        return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
+        return ut_projection_core(ut, img, ut_extend(opac), proj, mean2d, radii, depth, u_distance);
     }
     auto proj = [&](int i, float4& uvdt, bool& valid) {
         const f3 pw_i = i == 0 ? pw : ((i & 1) ? pw + d[(i - 1) >> 1] : pw - d[(i - 1) >> 1]);
         camera_projection<KIND>(c, pw_i, pv, pp, mode, false, uvdt, valid);
     };
-    return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
+    return ut_projection_core(ut, img, ut_extend(opac), proj, mean2d, radii, depth, u_distance);
 }
 
 // A static spherical / lidar camera's sigma points before phase unwrapping: each camera-space point's
@@ -598,10 +605,10 @@ XSG_DEV void sigma_uv(const Camera& c, f3 pw, const f3 d[3], SigmaUv& a) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) e[k] = mul(m, d[k]);
     const float rho0_sq = p0.x * p0.x + p0.y * p0.y;
-    const float r0 = sqrtf(rho0_sq + p0.z * p0.z);
+    const float r0 = hw_sqrt(rho0_sq + p0.z * p0.z);
     const float phi0 = atan2f(-p0.x, -p0.y) + float(M_PI);
     const float theta0 = asinf(p0.z / r0);
-    const float rho0 = sqrtf(rho0_sq);
+    const float rho0 = hw_sqrt(rho0_sq);
     const float two_pi = 2.0f * float(M_PI);
     // u and v by reciprocal multiplies (1 ulp): far below the float32 noise of the UT's weighted sums
     const float inv_du = __builtin_amdgcn_rcpf(c.i1), inv_dv = __builtin_amdgcn_rcpf(c.i3);
@@ -617,8 +624,8 @@ XSG_DEV void sigma_uv(const Camera& c, f3 pw, const f3 d[3], SigmaUv& a) {
         const float dot_xy = rho0_sq + sg * (p0.x * ek.x + p0.y * ek.y);  // x0 x + y0 y
         const float drho_sq = sg * 2.0f * (p0.x * ek.x + p0.y * ek.y) + (ek.x * ek.x + ek.y * ek.y);
         const float rho_sq = p.x * p.x + p.y * p.y;
-        const float rho = sqrtf(rho_sq);
-        const float r = sqrtf(rho_sq + p.z * p.z);
+        const float rho = hw_sqrt(rho_sq);
+        const float r = hw_sqrt(rho_sq + p.z * p.z);
         float phi = phi0 + atan_small(cross_xy, dot_xy);
         phi = phi <= 0.0f ? phi + two_pi : (phi > two_pi ? phi - two_pi : phi);
         const bool phi_small = dot_xy > 0.0f && fabsf(cross_xy) <= 0.25f * dot_xy && phi > 1e-4f &&
@@ -636,13 +643,14 @@ XSG_DEV void sigma_uv(const Camera& c, f3 pw, const f3 d[3], SigmaUv& a) {
     }
 }
 
+// extend: ut_extend of the Gaussian's opacity (computed once for all its modes)
 XSG_DEV bool ut_projection_sigma_uv(const Camera& c, const PhaseUnwrap& w, int mode, const UtWeights& ut, f2 img,
-                                    const ProjParams& pp, float opac, const SigmaUv& a, f2& mean2d, f2& radii,
+                                    const ProjParams& pp, float extend, const SigmaUv& a, f2& mean2d, f2& radii,
                                     float& depth, float& u_distance) {
     auto proj = [&](int i, float4& uvdt, bool& valid) {
         static_projection_tail(c, mk3(unwrap_u(w, mode, a.u[i]), a.v[i], a.r[i]), pp, mode, uvdt, valid);
     };
-    return ut_projection_core(ut, img, opac, proj, mean2d, radii, depth, u_distance);
+    return ut_projection_core(ut, img, extend, proj, mean2d, radii, depth, u_distance);
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs; xcd_tile gives each XCD a contiguous run of
