@@ -285,6 +285,35 @@ def _rig_expected(m2, r, d, W, H, tsx, tsy):
     return np.stack(tpg), ids[order], fl[order]
 
 
+@pytest.mark.parametrize("C_,n,neg", [(4, 800_000, False), (4, 800_000, True), (3, 1_100_000, False)],
+                         ids=["4cam", "4cam-negative-depth", "3cam"])
+def test_isect_large_rig(dev, C_, n, neg):
+    """Rigs of at least 3 M camera instances, where the depth pre-order takes its four LSD passes: the
+    keys, ids and offsets must equal the oracle's stable sort of every camera's keys. Four 1920x1080
+    cameras have 4 x 68 + 1 = 273 row buckets, past what is placed directly: the runs are expanded and
+    sorted by row bucket (one 9-bit pass); three cameras have 205, and their runs are placed directly
+    from the depth order that interleaves the cameras. Ties in depth across and within cameras, and
+    in one case a negative depth (its entries after every tile of every camera)."""
+    g = np.random.default_rng(31 + C_ + int(neg))
+    W, H = 1920, 1080
+    m2 = np.stack([g.uniform(-20, W + 20, (C_, n)), g.uniform(-20, H + 20, (C_, n))], -1).astype(np.float32)
+    r = g.uniform(0.5, 12.0, (C_, n, 2)).astype(np.float32)
+    d = g.uniform(0.3, 90.0, (C_, n)).astype(np.float32)
+    d[:, : n // 40] = d[0, n // 2]  # ties in depth, within and across cameras
+    if neg:
+        d[1, 7] = -2.5
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    ntx, nty = (W + 15) // 16, (H + 15) // 16
+    off = torch.empty((C_, nty, ntx), dtype=torch.int32, device=dev)
+    tpg, ids, fl = _C.isect_regular_tiles_batched(T(m2), T(r), T(d), W, H, 16, 16, tile_offsets=off)
+    w_tpg, w_ids, w_fl = _rig_expected(m2, r, d, W, H, 16, 16)
+    print("isects", ids.numel(), flush=True)
+    assert np.array_equal(np_(tpg), w_tpg)
+    assert np.array_equal(np_(ids), w_ids)
+    assert np.array_equal(np_(fl), w_fl)
+    assert np.array_equal(np_(off), O.offset_encode(w_ids[w_ids >= 0], ntx, nty, C_))
+
+
 @pytest.mark.parametrize("n_cams", [1, 3])
 def test_isect_negative_depth(dev, n_cams):
     """Instances with a negative depth (-0.0 included) and a footprint -- the projection never yields
