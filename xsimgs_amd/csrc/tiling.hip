@@ -890,34 +890,38 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
 }
 
 // Scan of the per-group counts of every bucket over its first ceil(m / 64) groups, in slices of
-// kGroupSlice groups, grid (buckets, slices): group_slice_sum_kernel sums each slice, then
+// `slice` groups, grid (buckets, slices): group_slice_sum_kernel sums each slice, then
 // group_slice_scan_kernel scans each slice in place (exclusive) from the sum of the bucket's slices
-// before it, and slice 0 stores the bucket total. When every group fits one slice (the host's bound),
-// the sums are not needed: part is null and slice 0's own total is the bucket's.
-constexpr int kGroupChunk = kBlock * 16;
-constexpr int kGroupSlice = kGroupChunk * 4;
+// before it, and slice 0 stores the bucket total. Up to kGroupOneSlice groups (the host's bound) are
+// one slice, whose sums are not needed: part is null and slice 0's own total is the bucket's. More
+// groups take slices of one chunk each, so that the grid has several workgroups per bucket (a lidar
+// frame's 17 buckets and 31 k groups: 272 instead of 34).
+constexpr int kGroupItems = 8;                           // consecutive groups per thread and chunk
+constexpr int kGroupChunk = kBlock * kGroupItems;        // groups per block scan
+constexpr int kGroupOneSlice = kGroupChunk * 8;
+inline int64_t group_slice(int64_t n_groups) { return n_groups <= kGroupOneSlice ? kGroupOneSlice : kGroupChunk; }
 
 __global__ __launch_bounds__(kBlock) void group_slice_sum_kernel(const uint32_t* __restrict__ hist, int64_t n_groups,
-                                                                 const uint32_t* __restrict__ m_dev,
+                                                                 int64_t slice, const uint32_t* __restrict__ m_dev,
                                                                  uint32_t* __restrict__ part) {
     __shared__ uint32_t lds[kWaves];
     const int64_t ng = min(n_groups, ((int64_t)*m_dev + 63) / 64);
-    const int64_t s0 = (int64_t)blockIdx.y * kGroupSlice;
+    const int64_t s0 = (int64_t)blockIdx.y * slice;
     if (s0 >= ng) return;  // block-uniform
     const uint32_t* h = hist + (int64_t)blockIdx.x * n_groups;
     uint32_t sum = 0;
-    for (int64_t i = s0 + threadIdx.x; i < min(ng, s0 + kGroupSlice); i += kBlock) sum += h[i];
+    for (int64_t i = s0 + threadIdx.x; i < min(ng, s0 + slice); i += kBlock) sum += h[i];
     sum = block_reduce_sum<uint32_t>(sum, lds);
     if (threadIdx.x == 0) part[(int64_t)blockIdx.x * gridDim.y + blockIdx.y] = sum;
 }
 
 __global__ __launch_bounds__(kBlock) void group_slice_scan_kernel(uint32_t* __restrict__ hist, int64_t n_groups,
-                                                                  const uint32_t* __restrict__ m_dev,
+                                                                  int64_t slice, const uint32_t* __restrict__ m_dev,
                                                                   const uint32_t* __restrict__ part,
                                                                   uint32_t* __restrict__ total) {
     __shared__ uint32_t lds[kWaves];
     const int64_t ng = min(n_groups, ((int64_t)*m_dev + 63) / 64);
-    const unsigned n_slices = (unsigned)((ng + kGroupSlice - 1) / kGroupSlice);
+    const unsigned n_slices = (unsigned)((ng + slice - 1) / slice);
     const unsigned k = blockIdx.y;
     const uint32_t* pr = part ? part + (int64_t)blockIdx.x * gridDim.y : nullptr;
     if (k == 0 && pr) {  // block-uniform
@@ -934,19 +938,21 @@ __global__ __launch_bounds__(kBlock) void group_slice_scan_kernel(uint32_t* __re
         run = block_reduce_sum<uint32_t>(acc, lds);
     }
     uint32_t* h = hist + (int64_t)blockIdx.x * n_groups;
-    for (int c = 0; c < kGroupSlice / kGroupChunk; ++c) {
-        const int64_t i0 = (int64_t)k * kGroupSlice + (int64_t)c * kGroupChunk + (int64_t)threadIdx.x * 16;
-        if (i0 - (int64_t)threadIdx.x * 16 >= ng) break;  // block-uniform
-        uint32_t v[16], sum = 0;
+    const int n_chunks = (int)(slice / kGroupChunk);
+    for (int c = 0; c < n_chunks; ++c) {
+        const int64_t c0 = (int64_t)k * slice + (int64_t)c * kGroupChunk;
+        if (c0 >= ng) break;  // block-uniform
+        const int64_t i0 = c0 + (int64_t)threadIdx.x * kGroupItems;
+        uint32_t v[kGroupItems], sum = 0;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < kGroupItems; ++j) {
             v[j] = i0 + j < ng ? h[i0 + j] : 0u;
             sum += v[j];
         }
         uint32_t tot;
         uint32_t at = run + block_exclusive_scan<uint32_t>(sum, lds, tot);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < kGroupItems; ++j) {
             if (i0 + j < ng) h[i0 + j] = at;
             at += v[j];
         }
@@ -980,9 +986,9 @@ XSG_DEV void run_rows(uint32_t key, Rect r, uint32_t v, int spans, int64_t n_per
     n_neg = 0u;
 }
 
-// A count block of depth-ordered instances: their rectangles to d_lo / d_hi, and per group of 64
-// (wavefront w, step k: group kGroupsPerCountBlock b + 4 k + w) its runs per bucket,
-// hist[bucket * n_groups + group].
+// Per group of 64 depth-ordered instances (one wavefront, four per workgroup): their rectangles to
+// d_lo / d_hi, and the group's runs per bucket, hist[bucket * n_groups + group]. The group's counts
+// are kept in a wavefront-private LDS row (the LDS instructions of one wavefront complete in order).
 __global__ __launch_bounds__(kBlock) void rows_hist_kernel(int64_t m, const uint32_t* __restrict__ m_dev,
                                                            const uint32_t* __restrict__ ids,
                                                            const uint32_t* __restrict__ keys,
@@ -992,28 +998,24 @@ __global__ __launch_bounds__(kBlock) void rows_hist_kernel(int64_t m, const uint
                                                            uint32_t* __restrict__ d_hi) {
     __shared__ uint32_t s_h[kWaves][kDirectRows];
     m = min(m, (int64_t)*m_dev);
-    const int64_t base = (int64_t)blockIdx.x * kCountTile;
-    if (base >= m) return;  // block-uniform; the scan reads the active groups only
     const int wave = threadIdx.x >> 6, lane = __lane_id();
+    const int64_t grp = (int64_t)blockIdx.x * kWaves + wave;
+    if (grp * 64 >= m) return;  // wave-uniform; the scan reads the active groups only
+    const int64_t p = grp * 64 + lane;
+    uint32_t v = 0u, key = 0u;
+    if (p < m) { v = ids[p]; key = keys[p]; }
     uint32_t* h = s_h[wave];
-    const uint32_t neg = (uint32_t)(n_rows - 1);
-    for (int k = 0; k < kCountItems; ++k) {
-        const int64_t grp = (int64_t)blockIdx.x * kGroupsPerCountBlock + k * kWaves + wave;
-        const int64_t p = grp * 64 + lane;
-        if (grp * 64 >= m) break;  // wave-uniform
-        for (int i = lane; i < n_rows; i += 64) h[i] = 0u;
-        if (p < m) {
-            const uint32_t v = ids[p];
-            const Rect r = rects[v];
-            d_lo[p] = (uint32_t)r.x0 | ((uint32_t)r.y0 << 16);
-            d_hi[p] = (uint32_t)r.x1 | ((uint32_t)r.y1 << 16);
-            uint32_t lo, hi, n_neg;
-            run_rows(keys[p], r, v, spans, n_per_cam, nty, lo, hi, n_neg);
-            if (n_neg) atomicAdd(&h[neg], n_neg);
-            for (uint32_t b = lo; b < hi; ++b) atomicAdd(&h[b], 1u);
-        }
-        for (int i = lane; i < n_rows; i += 64) hist[(int64_t)i * n_groups + grp] = h[i];
+    for (int i = lane; i < n_rows; i += 64) h[i] = 0u;
+    if (p < m) {
+        const Rect r = rects[v];
+        d_lo[p] = (uint32_t)r.x0 | ((uint32_t)r.y0 << 16);
+        d_hi[p] = (uint32_t)r.x1 | ((uint32_t)r.y1 << 16);
+        uint32_t lo, hi, n_neg;
+        run_rows(key, r, v, spans, n_per_cam, nty, lo, hi, n_neg);
+        if (n_neg) atomicAdd(&h[n_rows - 1], n_neg);
+        for (uint32_t b = lo; b < hi; ++b) atomicAdd(&h[b], 1u);
     }
+    for (int i = lane; i < n_rows; i += 64) hist[(int64_t)i * n_groups + grp] = h[i];
 }
 
 XSG_DEV uint32_t wave_min_u32(uint32_t x) {
@@ -1029,7 +1031,9 @@ XSG_DEV uint32_t wave_max_u32(uint32_t x) {
 
 // One wavefront per group of 64 instances: each bucket's first position for the group (the bucket's
 // base, an exclusive scan of the bucket totals, plus the group's scanned count), then the runs,
-// bucket by bucket, at consecutive positions in lane order.
+// bucket by bucket, at consecutive positions in lane order. Lane l holds the positions of buckets
+// l + 64 j in registers, and the loop over a bucket reads its position from that lane (a scalar
+// read; no LDS round trip per bucket).
 __global__ __launch_bounds__(64) void place_runs_kernel(int64_t m, const uint32_t* __restrict__ ids,
                                                         const uint32_t* __restrict__ keys,
                                                         const uint32_t* __restrict__ d_lo,
@@ -1038,51 +1042,60 @@ __global__ __launch_bounds__(64) void place_runs_kernel(int64_t m, const uint32_
                                                         const uint32_t* __restrict__ hist,
                                                         const uint32_t* __restrict__ row_tot,
                                                         uint4* __restrict__ out_rec) {
-    __shared__ uint32_t s_at[kDirectRows];
+    constexpr int kPer = kDirectRows / 64;
     const int lane = __lane_id();
     const int64_t grp = blockIdx.x;
-    // bucket bases: lane l holds buckets 4 l .. 4 l + 3
-    constexpr int kPer = kDirectRows / 64;
-    uint32_t c[kPer], sum = 0;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int b = lane * kPer + j;
-        c[j] = b < n_rows ? row_tot[b] : 0u;
-        sum += c[j];
-    }
-    uint32_t run = wave_inclusive_scan<uint32_t>(sum) - sum;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int b = lane * kPer + j;
-        if (b < n_rows) s_at[b] = run + hist[(int64_t)b * n_groups + grp];
-        run += c[j];
-    }
-    __syncthreads();
     const int64_t p = grp * 64 + lane;
+    uint32_t v = 0u, key = 0u, lo_w = 0u, hi_w = 0u;
+    if (p < m) { v = ids[p]; key = keys[p]; lo_w = d_lo[p]; hi_w = d_hi[p]; }
+    uint32_t c[kPer], at[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int b = lane + 64 * j;
+        c[j] = b < n_rows ? row_tot[b] : 0u;
+        at[j] = b < n_rows ? hist[(int64_t)b * n_groups + grp] : 0u;
+    }
+    // bucket b = lane + 64 j starts after every bucket of the lower j and the lanes below it in this j
+    uint32_t before = 0u;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t inc = wave_inclusive_scan<uint32_t>(c[j]);
+        at[j] += before + inc - c[j];
+        before += (uint32_t)__shfl((int)inc, 63, 64);
+    }
     uint32_t lo = 0u, hi = 0u, n_neg = 0u;
     uint4 rec = make_uint4(0u, 0u, 0u, 0u);
     if (p < m) {
-        const uint32_t v = ids[p], key = keys[p];
-        const Rect r = rect_of(d_lo[p], d_hi[p]);
+        const Rect r = rect_of(lo_w, hi_w);
         run_rows(key, r, v, spans, n_per_cam, nty, lo, hi, n_neg);
         rec = make_uint4(v / (uint32_t)spans, key, (uint32_t)r.x0 | ((uint32_t)r.x1 << 16), 0u);
     }
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    const uint32_t b0 = wave_min_u32(lo < hi ? lo : 0xffffffffu);
-    const uint32_t b1 = wave_max_u32(hi);
-    for (uint32_t b = b0; b < b1; ++b) {  // wave-uniform
-        const bool cov = lo <= b && b < hi;
-        const uint64_t mk = __ballot(cov);
-        if (cov) {
-            rec.w = b;
-            out_rec[s_at[b] + (uint32_t)__popcll(mk & lt)] = rec;
+    // the wave's bucket range, in scalar registers (a uniform loop)
+    const uint32_t b0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_min_u32(lo < hi ? lo : 0xffffffffu));
+    const uint32_t b1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_max_u32(hi));
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t jb0 = max(b0, (uint32_t)(64 * j)), jb1 = min(b1, (uint32_t)(64 * j + 64));
+        for (uint32_t b = jb0; b < jb1; ++b) {  // wave-uniform
+            const bool cov = lo <= b && b < hi;
+            const uint64_t mk = __ballot(cov);
+            const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)at[j], (int)(b - 64 * j));
+            if (cov) {
+                rec.w = b;
+                out_rec[base + (uint32_t)__popcll(mk & lt)] = rec;
+            }
         }
     }
     if (__ballot(n_neg > 0)) {  // negative keys: n_neg identical runs each, in lane order
-        const uint32_t neg = (uint32_t)(n_rows - 1);
-        const uint32_t at = s_at[neg] + wave_inclusive_scan<uint32_t>(n_neg) - n_neg;
-        rec.w = neg;
-        for (uint32_t q = 0; q < n_neg; ++q) out_rec[at + q] = rec;
+        const int neg = n_rows - 1;
+        uint32_t nb = 0u;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j)
+            if (neg >> 6 == j) nb = (uint32_t)__builtin_amdgcn_readlane((int)at[j], neg & 63);
+        const uint32_t at_neg = nb + wave_inclusive_scan<uint32_t>(n_neg) - n_neg;
+        rec.w = (uint32_t)neg;
+        for (uint32_t q = 0; q < n_neg; ++q) out_rec[at_neg + q] = rec;
     }
 }
 
@@ -1666,7 +1679,8 @@ CountWs count_ws_layout(const Geometry& g, void* base) {
     const size_t nr = w.direct ? (size_t)w.n_rows : 0;
     w.row_hist = (uint32_t*)(p + off); off += align256(4 * nr * w.nb * kGroupsPerCountBlock);
     w.row_part = (uint32_t*)(p + off);
-    off += align256(4 * nr * (((size_t)w.nb * kGroupsPerCountBlock + kGroupSlice - 1) / kGroupSlice));
+    const int64_t n_groups = (int64_t)w.nb * kGroupsPerCountBlock;
+    off += align256(4 * nr * (size_t)((n_groups + group_slice(n_groups) - 1) / group_slice(n_groups)));
     w.row_tot = (uint32_t*)(p + off); off += align256(4 * nr);
     w.bytes = off;
     return w;
@@ -1899,14 +1913,15 @@ extern "C" int xsg_isect_count(const xsg_isect_desc* d, int32_t* tpg, void* work
         if (w.direct) {  // per count block and row bucket, the block's runs; their scans
             const int64_t n_per_cam = g.n_cams > 1 ? g.n : 0;
             const int64_t n_groups = (int64_t)w.nb * kGroupsPerCountBlock;
-            rows_hist_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.pre_key, w.rects, g.nty,
-                                                     n_per_cam, g.spans, w.n_rows, n_groups, w.row_hist, w.drect_lo,
-                                                     w.drect_hi);
-            const dim3 sgrid((unsigned)w.n_rows, (unsigned)((n_groups + kGroupSlice - 1) / kGroupSlice));
+            rows_hist_kernel<<<w.nb * (kGroupsPerCountBlock / kWaves), kBlock, 0, s>>>(
+                w.n_virtual, w.m_dev, w.pre_id, w.pre_key, w.rects, g.nty, n_per_cam, g.spans, w.n_rows, n_groups,
+                w.row_hist, w.drect_lo, w.drect_hi);
+            const int64_t slice = group_slice(n_groups);
+            const dim3 sgrid((unsigned)w.n_rows, (unsigned)((n_groups + slice - 1) / slice));
             const bool one_slice = sgrid.y == 1;
             if (!one_slice)
-                group_slice_sum_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev, w.row_part);
-            group_slice_scan_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, w.m_dev,
+                group_slice_sum_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, slice, w.m_dev, w.row_part);
+            group_slice_scan_kernel<<<sgrid, kBlock, 0, s>>>(w.row_hist, n_groups, slice, w.m_dev,
                                                              one_slice ? nullptr : w.row_part, w.row_tot);
         } else {
             rows_reduce_kernel<<<w.nb, kBlock, 0, s>>>(w.n_virtual, w.m_dev, w.pre_id, w.rects, w.rpart, w.drect_lo,
