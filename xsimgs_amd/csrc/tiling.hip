@@ -142,6 +142,23 @@ XSG_DEV void block_key_range(uint32_t& lo, uint32_t& hi, uint32_t* s_lo, uint32_
     }
 }
 
+// Sums of three 64-bit values over a 256-thread block, on every thread (one barrier pair for all three).
+XSG_DEV void block_reduce_sum3(uint64_t& a, uint64_t& b, uint64_t& c, uint64_t (*lds)[kWaves]) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        a += (uint64_t)__shfl_xor((unsigned long long)a, off, 64);
+        b += (uint64_t)__shfl_xor((unsigned long long)b, off, 64);
+        c += (uint64_t)__shfl_xor((unsigned long long)c, off, 64);
+    }
+    const int wave = threadIdx.x >> 6;
+    if (__lane_id() == 0) { lds[0][wave] = a; lds[1][wave] = b; lds[2][wave] = c; }
+    __syncthreads();
+    a = b = c = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) { a += lds[0][w]; b += lds[1][w]; c += lds[2][w]; }
+    __syncthreads();
+}
+
 // Count pass over regular-tiling Gaussian instances (one span each). A block covers kCountTile
 // instances; it writes tiles_per_gauss and the rectangle of every instance, and the block's packed
 // count sum. The compaction takes the counts from tiles_per_gauss and the depth bits from the depths.
@@ -150,31 +167,40 @@ __global__ __launch_bounds__(kBlock) void count_regular_kernel(
     int64_t n_total, const float2* __restrict__ means2d, const float2* __restrict__ radii, float tsx, float tsy,
     int ntx, int nty, int32_t* __restrict__ tpg, Rect* __restrict__ rects, uint64_t* __restrict__ partials,
     uint64_t* __restrict__ cpart, const float* __restrict__ depths, uint32_t* __restrict__ key_range) {
-    __shared__ uint64_t lds[kWaves];
+    __shared__ uint64_t lds[3][kWaves];
     __shared__ uint32_t s_lo[kWaves], s_hi[kWaves];
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
     uint32_t lo = 0xffffffffu, hi = 0u;
     const int64_t base = (int64_t)blockIdx.x * kCountTile;
+    // every item's inputs loaded before any is binned (one memory round trip instead of one per item;
+    // indices past the end read the last instance and are not binned)
+    float2 mv[kCountItems], rv[kCountItems];
+    uint32_t kv[kCountItems];
+#pragma unroll
+    for (int k = 0; k < kCountItems; ++k) {
+        const int64_t j = min(base + (int64_t)k * kBlock + threadIdx.x, n_total - 1);
+        mv[k] = means2d[j];
+        rv[k] = radii[j];
+        kv[k] = key_range ? __float_as_uint(depths[j]) : 0u;
+    }
+#pragma unroll
     for (int k = 0; k < kCountItems; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
         if (j < n_total) {
-            const Rect r = regular_rect(means2d[j], radii[j], tsx, tsy, ntx, nty);
+            const Rect r = regular_rect(mv[k], rv[k], tsx, tsy, ntx, nty);
             const uint32_t c = rect_count(r);
             tpg[j] = (int32_t)c;  // also the compaction's count (one span per instance)
             rects[j] = r;
             acc += pack_count(c);
             acc_c += c;
             acc_r += c > 0 ? (uint32_t)(r.y1 - r.y0) : 0u;
-            if (key_range && c > 0) {
-                const uint32_t key = __float_as_uint(depths[j]);
-                lo = min(lo, key);
-                hi = max(hi, key);
+            if (c > 0) {
+                lo = min(lo, kv[k]);
+                hi = max(hi, kv[k]);
             }
         }
     }
-    acc = block_reduce_sum<uint64_t>(acc, lds);
-    acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
-    acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
+    block_reduce_sum3(acc, acc_c, acc_r, lds);
     if (key_range) block_key_range(lo, hi, s_lo, s_hi);  // block-uniform
     if (threadIdx.x == 0) {
         partials[blockIdx.x] = acc;
@@ -197,9 +223,24 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     int32_t* __restrict__ tpg, Rect* __restrict__ rects, uint32_t* __restrict__ vcnt, uint32_t* __restrict__ vkey,
     uint64_t* __restrict__ partials, uint64_t* __restrict__ cpart, uint32_t* __restrict__ seam_cnt,
     uint32_t* __restrict__ seam_ids, uint32_t* __restrict__ key_range) {
-    __shared__ uint64_t lds[kWaves];
+    __shared__ uint64_t lds[3][kWaves];
     __shared__ uint32_t s_lo[kWaves], s_hi[kWaves];
     __shared__ uint32_t s_seam;
+    // every item's inputs loaded first, before the set-up below, and before any is binned (indices
+    // past the end read the last Gaussian and are not binned)
+    const int64_t base = (int64_t)blockIdx.x * (kCountTile / 2);
+    constexpr int kItems = kCountItems / 2;
+    float2 rv[kItems], mv[kItems];
+    int fv[kItems];
+    uint32_t kv[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        const int64_t j = min(base + (int64_t)k * kBlock + threadIdx.x, n - 1);
+        rv[k] = radii[j];
+        fv[k] = flags[j];
+        mv[k] = means2d[j];
+        kv[k] = __float_as_uint(depths[j]);
+    }
     // lidar: the elevation table in LDS; when it is non-decreasing (as find_bounds_increasing
     // expects) its scans become bisections (same bounds), else they scan as the reference does
     __shared__ float s_elev[LIDAR ? kMaxLdsElev : 1];
@@ -225,13 +266,13 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
     const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     uint64_t acc = 0, acc_c = 0, acc_r = 0;
     uint32_t lo = 0xffffffffu, hi = 0u;
-    const int64_t base = (int64_t)blockIdx.x * (kCountTile / 2);
-    for (int k = 0; k < kCountItems / 2; ++k) {
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
         const int64_t j = base + (int64_t)k * kBlock + threadIdx.x;
         bool seam = false;
         if (j < n) {
-            const float2 r = radii[j];
-            const int flag = flags[j];
+            const float2 r = rv[k];
+            const int flag = fv[k];
             Rect a = {0, 0, 0, 0};
             if (!(r.x <= 0 || r.y <= 0 || flag == 0)) {
                 float u_min = 0.0f, u_max = 1.0f;
@@ -239,7 +280,7 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
                     seam = true;
                     if (cam.roll_u > 0) u_max = u_pose_of(cam); else u_min = u_pose_of(cam);
                 }
-                const float2 m = means2d[j];
+                const float2 m = mv[k];
                 const float mx = m.x / img.x, my = m.y / img.y, rx = r.x / img.x, ry = r.y / img.y;
                 if (LIDAR) {
                     a = sorted_elev ? lidar_rect<true>(mx, my, rx, ry, u_min, u_max, u_per_tile, n_elev, tab, ntx)
@@ -250,15 +291,15 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
             }
             const uint32_t ca = rect_count(a);
             tpg[j] = (int32_t)ca;
-            rects[2 * j] = a;
-            rects[2 * j + 1] = Rect{0, 0, 0, 0};
-            vcnt[2 * j] = ca;
-            vcnt[2 * j + 1] = 0u;
-            vkey[2 * j] = __float_as_uint(depths[j]);
-            vkey[2 * j + 1] = 0u;
+            // both spans of the instance, the second empty until seam_span_kernel fills it (one vector
+            // store per array; the workspace arrays are 256-byte aligned)
+            reinterpret_cast<uint4*>(rects)[j] =
+                make_uint4((uint32_t)a.x0 | ((uint32_t)a.y0 << 16), (uint32_t)a.x1 | ((uint32_t)a.y1 << 16), 0u, 0u);
+            reinterpret_cast<uint2*>(vcnt)[j] = make_uint2(ca, 0u);
+            reinterpret_cast<uint2*>(vkey)[j] = make_uint2(kv[k], 0u);
             if (ca > 0) {
-                lo = min(lo, __float_as_uint(depths[j]));
-                hi = max(hi, __float_as_uint(depths[j]));
+                lo = min(lo, kv[k]);
+                hi = max(hi, kv[k]);
             }
             acc += pack_count(ca);
             acc_c += ca;
@@ -275,9 +316,7 @@ __global__ __launch_bounds__(kBlock) void count_spherical_kernel(
             if (seam) seam_ids[base + slot + (uint32_t)__popcll(sm & lt_mask)] = (uint32_t)j;
         }
     }
-    acc = block_reduce_sum<uint64_t>(acc, lds);  // its barriers also order the LDS reservations
-    acc_c = block_reduce_sum<uint64_t>(acc_c, lds);
-    acc_r = block_reduce_sum<uint64_t>(acc_r, lds);
+    block_reduce_sum3(acc, acc_c, acc_r, lds);  // its barriers also order the LDS reservations
     if (key_range) block_key_range(lo, hi, s_lo, s_hi);  // block-uniform
     if (threadIdx.x == 0) {
         partials[blockIdx.x] = acc;
@@ -450,6 +489,17 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
     uint32_t* __restrict__ comp_off, uint32_t* __restrict__ comp_key, uint32_t* __restrict__ m_dev,
     uint64_t* __restrict__ publish) {
     __shared__ uint64_t lds[kWaves];
+    // each thread its kCountItems consecutive instances: counts and depth bits loaded first (their
+    // latency then overlaps the block's offset), one block scan places them all
+    const int64_t v0 = (int64_t)blockIdx.x * kCountTile + (int64_t)threadIdx.x * kCountItems;
+    uint32_t c[kCountItems], key[kCountItems];
+#pragma unroll
+    for (int k = 0; k < kCountItems; ++k) {
+        const int64_t v = min(v0 + k, n_virtual - 1);
+        const uint32_t cv = vcnt[v];
+        key[k] = vkey[v];
+        c[k] = v0 + k < n_virtual ? cv : 0u;
+    }
     uint64_t carry = slice_offset<uint64_t>(slice_sum, blockIdx.x / kSlice, lds) + pbase[blockIdx.x];
     if (blockIdx.x == 0) {  // block-uniform
         const uint64_t tot = slice_offset<uint64_t>(slice_sum, n_slices, lds);
@@ -467,15 +517,9 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
             publish[2] = e1;
         }
     }
-    // each thread its kCountItems consecutive instances: one block scan places them all
-    const int64_t v0 = (int64_t)blockIdx.x * kCountTile + (int64_t)threadIdx.x * kCountItems;
-    uint32_t c[kCountItems];
     uint64_t sum = 0;
 #pragma unroll
-    for (int k = 0; k < kCountItems; ++k) {
-        c[k] = v0 + k < n_virtual ? vcnt[v0 + k] : 0u;
-        sum += pack_count(c[k]);
-    }
+    for (int k = 0; k < kCountItems; ++k) sum += pack_count(c[k]);
     uint64_t tot;
     uint64_t s = carry + block_exclusive_scan<uint64_t>(sum, lds, tot);
 #pragma unroll
@@ -485,7 +529,7 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
             if (p < (uint64_t)n_virtual) {
                 comp_id[p] = (uint32_t)(v0 + k);
                 comp_off[p] = (uint32_t)s;
-                comp_key[p] = vkey[v0 + k];
+                comp_key[p] = key[k];
             }
         }
         s += pack_count(c[k]);
