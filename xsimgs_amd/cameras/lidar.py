@@ -56,11 +56,22 @@ class LidarCamera(FusedRSCamera):
     def num_beams(self):
         return self.beam_v.shape[-1]
 
+    def _beam_addr(self):
+        """The pack's address tensor for ``beam_v``, rebuilt only when ``beam_v`` moves: building it is a
+        host-to-device copy from pageable memory, which waits for every kernel already queued, so one
+        per pack kept the host from queueing a frame ahead of the GPU. (It holds the address alone,
+        which in-place changes of the beam values leave as it is.)"""
+        ptr = self.beam_v.data_ptr()
+        if self.__dict__.get("_addr_ptr") != ptr:
+            self._addr = data_addr_tensor(self.beam_v)
+            self._addr_ptr = ptr
+        return self._addr
+
     @property
     def _pack_data(self):
         if not self.beam_v.is_contiguous():
             self.beam_v = self.beam_v.contiguous()
-        return super()._pack_data + [self.limits.view(4).contiguous(), data_addr_tensor(self.beam_v)]
+        return super()._pack_data + [self.limits.view(4).contiguous(), self._beam_addr()]
 
     def isect_gs_tiles(self, points, scale, rotation, width: int, height: int, flags, radii, means2d, depths,
                        points_velocity=None, opacity=None, tile_size_x: int = 16, tile_size_y: int = 16,
