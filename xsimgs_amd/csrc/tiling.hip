@@ -1347,7 +1347,10 @@ __global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, cons
 
 // Per tile (real row, column): exclusive prefix of its segments' counts in place (the slots of a
 // tile are consecutive), and the tile's total into tile_tot. One wavefront per tile, lanes over the
-// tile's segments.
+// tile's segments, kPrefixChunks chunks of 64 loaded before any is scanned (a lidar frame's rows hold
+// hundreds of segments: one memory round trip per group of chunks instead of one per chunk).
+constexpr int kPrefixChunks = 8;
+
 __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restrict__ slots,
                                                              const uint32_t* __restrict__ seg_base, int n_real,
                                                              int ntx, uint32_t* __restrict__ tile_tot) {
@@ -1358,12 +1361,22 @@ __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restric
     const uint32_t sb = seg_base[row], nseg = seg_base[row + 1] - sb;
     uint32_t* sl = slots + (int64_t)sb * ntx + (int64_t)c * nseg;
     uint32_t carry = 0;
-    for (uint32_t k0 = 0; k0 < nseg; k0 += 64) {
-        const uint32_t k = k0 + (uint32_t)lane;
-        const uint32_t x = k < nseg ? sl[k] : 0u;
-        const uint32_t inc = wave_inclusive_scan(x);
-        if (k < nseg) sl[k] = carry + inc - x;
-        carry += (uint32_t)__shfl((int)inc, 63, 64);
+    for (uint32_t k0 = 0; k0 < nseg; k0 += 64 * kPrefixChunks) {
+        const int nc = (int)min<uint32_t>(kPrefixChunks, (nseg - k0 + 63) / 64);  // wave-uniform
+        uint32_t x[kPrefixChunks];
+#pragma unroll
+        for (int j = 0; j < kPrefixChunks; ++j) {
+            const uint32_t k = k0 + 64u * j + (uint32_t)lane;
+            x[j] = (j < nc && k < nseg) ? sl[k] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kPrefixChunks; ++j) {
+            if (j >= nc) break;
+            const uint32_t k = k0 + 64u * j + (uint32_t)lane;
+            const uint32_t inc = wave_inclusive_scan(x[j]);
+            if (k < nseg) sl[k] = carry + inc - x[j];
+            carry += (uint32_t)__shfl((int)inc, 63, 64);
+        }
     }
     if (lane == 0) tile_tot[t] = carry;
 }
