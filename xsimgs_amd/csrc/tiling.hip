@@ -142,6 +142,14 @@ XSG_DEV void block_key_range(uint32_t& lo, uint32_t& hi, uint32_t* s_lo, uint32_
     }
 }
 
+// Orders one wavefront's LDS accesses before and after it (a wavefront-private LDS buffer needs no
+// workgroup barrier, only this).
+XSG_DEV void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Sums of three 64-bit values over a 256-thread block, on every thread (one barrier pair for all three).
 XSG_DEV void block_reduce_sum3(uint64_t& a, uint64_t& b, uint64_t& c, uint64_t (*lds)[kWaves]) {
 #pragma unroll
@@ -1050,6 +1058,7 @@ __global__ __launch_bounds__(kBlock) void rows_hist_kernel(int64_t m, const uint
     if (p < m) { v = ids[p]; key = keys[p]; }
     uint32_t* h = s_h[wave];
     for (int i = lane; i < n_rows; i += 64) h[i] = 0u;
+    wave_lds_sync();
     if (p < m) {
         const Rect r = rects[v];
         d_lo[p] = (uint32_t)r.x0 | ((uint32_t)r.y0 << 16);
@@ -1059,6 +1068,7 @@ __global__ __launch_bounds__(kBlock) void rows_hist_kernel(int64_t m, const uint
         if (n_neg) atomicAdd(&h[n_rows - 1], n_neg);
         for (uint32_t b = lo; b < hi; ++b) atomicAdd(&h[b], 1u);
     }
+    wave_lds_sync();
     for (int i = lane; i < n_rows; i += 64) hist[(int64_t)i * n_groups + grp] = h[i];
 }
 
@@ -1254,9 +1264,11 @@ __global__ __launch_bounds__(kBlock) void seg_count_kernel(int n_real, const uin
 
 // seg_count_kernel with row_segments_kernel's work done by every workgroup, for up to kFusedRows row
 // buckets: each derives the row starts (from the run sort's digit totals when given, else from
-// row_start) and the segment bases, finds its own segment's row, and counts as seg_count_kernel does;
-// workgroup 0 stores the row starts and bases and each workgroup its segment's row, for the kernels
-// after it. One launch fewer per fill.
+// row_start) and the segment bases, and each of its wavefronts then counts one segment (workgroup w,
+// wavefront v: segment kWaves w + v) as seg_count_kernel does, in a wavefront-private LDS difference
+// array (the LDS instructions of one wavefront complete in order, so no barrier follows the set-up);
+// workgroup 0 stores the row starts and bases and each wavefront its segment's row, for the kernels
+// after it. One launch fewer per fill, and the set-up shared by four segments.
 constexpr int kFusedRows = 1024;
 
 __global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, const uint32_t* __restrict__ row_count,
@@ -1265,8 +1277,7 @@ __global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, cons
                                                                 uint32_t* __restrict__ seg_base,
                                                                 uint32_t* __restrict__ seg_row, int ntx,
                                                                 uint32_t* __restrict__ slots) {
-    extern __shared__ int32_t s_diff[];  // ntx + 1
-    __shared__ int32_t lds[kWaves];
+    extern __shared__ int32_t s_diff[];  // kWaves rows of ntx + 1
     __shared__ uint32_t s_rs[kFusedRows + 1], s_sb[kFusedRows + 1];
     __shared__ uint32_t s_lds[kWaves];
     const int n_real = n_rows - 1;
@@ -1309,8 +1320,9 @@ __global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, cons
             for (int r = threadIdx.x; r <= n_rows; r += kBlock) row_start[r] = s_rs[r];
         for (int r = threadIdx.x; r <= n_real; r += kBlock) seg_base[r] = s_sb[r];
     }
-    const uint32_t sg = blockIdx.x;
-    if (sg >= s_sb[n_real]) return;  // workgroup-uniform
+    const int wave = threadIdx.x >> 6, lane = __lane_id();
+    const uint32_t sg = blockIdx.x * kWaves + wave;
+    if (sg >= s_sb[n_real]) return;  // wave-uniform; no barrier follows
     // the segment's row: the last r with s_sb[r] <= sg (rows without segments share a base with the
     // next row, and the search takes the later one)
     int lo = 0, hi = n_real - 1;
@@ -1319,28 +1331,36 @@ __global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, cons
         if (s_sb[mid] <= sg) lo = mid; else hi = mid - 1;
     }
     const uint32_t row = (uint32_t)lo;
-    if (threadIdx.x == 0) seg_row[sg] = row;
+    if (lane == 0) seg_row[sg] = row;
     const uint32_t sb = s_sb[row], nseg = s_sb[row + 1] - sb;
     const uint32_t k = sg - sb;
     const int64_t b = (int64_t)s_rs[row] + (int64_t)k * kRunSeg;
-    const int64_t e = min((int64_t)s_rs[row + 1], b + kRunSeg);
-    for (int c = threadIdx.x; c <= ntx; c += kBlock) s_diff[c] = 0;
-    __syncthreads();
-    for (int64_t i = b + threadIdx.x; i < e; i += kBlock) {
-        const uint32_t x01 = rec[i].z;
-        atomicAdd(&s_diff[x01 & 0xffffu], 1);
-        atomicAdd(&s_diff[x01 >> 16], -1);
+    const int n_seg = (int)(min((int64_t)s_rs[row + 1], b + kRunSeg) - b);
+    // every run's column range loaded before any is counted
+    constexpr int kPer = kRunSeg / 64;
+    uint32_t z[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) z[j] = 64 * j + lane < n_seg ? rec[b + 64 * j + lane].z : 0u;
+    int32_t* d = s_diff + wave * (ntx + 1);
+    for (int c = lane; c <= ntx; c += 64) d[c] = 0;
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        if (64 * j + lane < n_seg) {
+            atomicAdd(&d[z[j] & 0xffffu], 1);
+            atomicAdd(&d[z[j] >> 16], -1);
+        }
     }
-    __syncthreads();
-    const int per = (ntx + kBlock - 1) / kBlock;
-    const int c0 = threadIdx.x * per, c1 = min(ntx, c0 + per);
+    wave_lds_sync();
+    // columns per lane: a run of consecutive ones, one wavefront scan of the runs' sums
+    const int per = (ntx + 63) / 64;
+    const int c0 = lane * per, c1 = min(ntx, c0 + per);
     int32_t sum = 0;
-    for (int c = c0; c < c1; ++c) sum += s_diff[c];
-    int32_t tot;
-    int32_t run = block_exclusive_scan<int32_t>(sum, lds, tot);
+    for (int c = c0; c < c1; ++c) sum += d[c];
+    int32_t run = wave_inclusive_scan<int32_t>(sum) - sum;
     uint32_t* out = slots + (int64_t)sb * ntx + k;
     for (int c = c0; c < c1; ++c) {
-        run += s_diff[c];
+        run += d[c];
         out[(int64_t)c * nseg] = (uint32_t)run;
     }
 }
@@ -2095,7 +2115,8 @@ extern "C" int xsg_isect_fill(const xsg_isect_desc* d, int64_t n_isects, int64_t
     // column counts per segment; per tile, the exclusive prefix over its segments and the tile total;
     // one exclusive scan over the tile totals
     if (fw.n_rows <= kFusedRows) {
-        seg_count_rows_kernel<<<(unsigned)fw.s_max, kBlock, sizeof(int32_t) * (g.ntx + 1), s>>>(
+        seg_count_rows_kernel<<<(unsigned)((fw.s_max + kWaves - 1) / kWaves), kBlock,
+                                sizeof(int32_t) * kWaves * (g.ntx + 1), s>>>(
             fw.n_rows, row_count, rec, fw.row_start, fw.seg_base, fw.seg_row, g.ntx, fw.slots);
     } else {
         row_segments_kernel<<<1, kBlock, 0, s>>>(fw.n_rows, row_count, fw.row_start, fw.seg_base, fw.seg_row);
