@@ -1,11 +1,11 @@
-"""Host-side camera logic (no GPU): pack layouts of the distorted / fisheye models and the
+"""Host-side camera logic (no GPU): pack layouts of the distorted / fisheye models, the
 max-radius bound of the distorted model (the fold of the radial map, or a margin past the image
-corner, whichever comes first)."""
+corner, whichever comes first) and the lidar pack's beam-table address."""
 import math
 
 import torch
 
-from xsimgs_amd.cameras import CameraPose, DistortedPerspectiveCamera, FisheyeCamera, max_valid_radius
+from xsimgs_amd.cameras import CameraPose, DistortedPerspectiveCamera, FisheyeCamera, LidarCamera, max_valid_radius
 
 STEP = 16.0 / 8191   # the radius grid the bound is read from
 
@@ -40,3 +40,25 @@ def test_pack_layouts():
     assert f.pack.shape == (1, 25)
     assert torch.allclose(f.pack[0, 17:], torch.tensor([0.3, 0.4, 0.5, 0.5, 0.1, 0.2, 0.3, 0.4]))
     assert d.undistort().pack.shape == (1, 21)
+
+
+def _packed_address(pack):
+    lo, hi = (int(b) & 0xffffffff for b in pack[0, -2:].contiguous().view(torch.int32))
+    return lo | (hi << 32)
+
+
+def test_lidar_pack_carries_the_beam_table_address():
+    # the pack's last two floats are beam_v's address (two float32 bit patterns); the address tensor is
+    # built once per address (a blocking host-to-device copy on a GPU) and rebuilt when beam_v moves
+    cam = LidarCamera(CameraPose.make(device="cpu"), torch.tensor([0.0, 2 * math.pi, -0.3, 0.6]),
+                      torch.linspace(0.0, 1.0, 16))
+    first = cam.pack
+    assert first.shape == (1, 23)
+    assert _packed_address(first) == cam.beam_v.data_ptr()
+    assert cam._beam_addr() is cam._beam_addr()
+    old = cam.beam_v
+    cam.beam_v = torch.linspace(0.0, 1.0, 16) * 0.5
+    assert cam.beam_v.data_ptr() != old.data_ptr()
+    assert _packed_address(cam.pack) == cam.beam_v.data_ptr()
+    cam.beam_v.mul_(2.0)  # values changed in place: the address, and so the pack's address, stay
+    assert _packed_address(cam.pack) == cam.beam_v.data_ptr()
