@@ -1405,11 +1405,13 @@ __global__ __launch_bounds__(kBlock) void tile_prefix_kernel(uint32_t* __restric
 // every tile of the real rows), the total -- where the negative-depth entries start -- at tile_tot[n];
 // with `offsets`, the same positions as int32 (the tile offsets). Each wavefront owns a contiguous
 // range: it sums its range (coalesced 64-entry chunks, all loads in flight), one barrier gives every
-// wavefront the sum of the ranges before it, and it then scans its range chunk by chunk (the second
-// read hits the cache): 7.7 µs at cfg2's 8160 tiles and 21 µs at the six-camera rig's 34 k. (Chunks of
-// 1024 entries across the block, two barriers per chunk, took 9 and 23-31 µs; eight consecutive entries
-// per thread, 11.9 µs at cfg2.)
+// wavefront the sum of the ranges before it, and it then scans its range chunk by chunk from the
+// registers that hold it (a range past kScanHeld chunks is read again, from the cache). Reading the
+// range again for the scan took 7.7 µs at cfg2's 8160 tiles and 21 µs at the six-camera rig's 34 k;
+// chunks of 1024 entries across the block, two barriers per chunk, 9 and 23-31 µs; eight consecutive
+// entries per thread, 11.9 µs at cfg2.
 constexpr int kScanThreads = 1024;
+constexpr int kScanHeld = 40;  // chunks of 64 a wavefront keeps in registers between its sum and its scan
 __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __restrict__ a, int64_t n,
                                                                  int32_t* __restrict__ offsets) {
     constexpr int NW = kScanThreads / 64;
@@ -1417,8 +1419,20 @@ __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __res
     const int wave = threadIdx.x >> 6, lane = __lane_id();
     const int64_t per = ((n + NW - 1) / NW + 63) / 64 * 64;  // whole chunks per wavefront
     const int64_t w0 = min(n, (int64_t)wave * per), w1 = min(n, w0 + per);
+    // up to kScanHeld chunks per wavefront (40 k tiles in all) are read once and scanned from registers
+    const bool held = per <= 64 * kScanHeld;  // block-uniform
+    uint32_t x[kScanHeld];
     uint32_t sum = 0;
-    for (int64_t i = w0 + lane; i < w1; i += 64) sum += a[i];
+    if (held) {
+#pragma unroll
+        for (int j = 0; j < kScanHeld; ++j) {
+            const int64_t i = w0 + 64 * j + lane;
+            x[j] = i < w1 ? a[i] : 0u;
+            sum += x[j];
+        }
+    } else {
+        for (int64_t i = w0 + lane; i < w1; i += 64) sum += a[i];
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off, 64);
     if (lane == 0) s_tot[wave] = sum;
@@ -1430,15 +1444,28 @@ __global__ __launch_bounds__(kScanThreads) void tile_scan_kernel(uint32_t* __res
         if (w < wave) carry += t;
         total += t;
     }
-    for (int64_t c0 = w0; c0 < w1; c0 += 64) {
-        const int64_t i = c0 + lane;
-        const uint32_t x = i < w1 ? a[i] : 0u;
-        const uint32_t inc = wave_inclusive_scan(x);
+    auto put = [&](int64_t i, uint32_t v, uint32_t inc) {
         if (i < w1) {
-            a[i] = carry + inc - x;
-            if (offsets) offsets[i] = (int32_t)(carry + inc - x);
+            a[i] = carry + inc - v;
+            if (offsets) offsets[i] = (int32_t)(carry + inc - v);
         }
-        carry += (uint32_t)__shfl((int)inc, 63, 64);
+    };
+    if (held) {
+#pragma unroll
+        for (int j = 0; j < kScanHeld; ++j) {
+            if (w0 + 64 * j >= w1) break;  // wave-uniform
+            const uint32_t inc = wave_inclusive_scan(x[j]);
+            put(w0 + 64 * j + lane, x[j], inc);
+            carry += (uint32_t)__shfl((int)inc, 63, 64);
+        }
+    } else {
+        for (int64_t c0 = w0; c0 < w1; c0 += 64) {
+            const int64_t i = c0 + lane;
+            const uint32_t v = i < w1 ? a[i] : 0u;
+            const uint32_t inc = wave_inclusive_scan(v);
+            put(i, v, inc);
+            carry += (uint32_t)__shfl((int)inc, 63, 64);
+        }
     }
     if (threadIdx.x == 0) a[n] = total;
 }
