@@ -143,7 +143,9 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict_
 }
 
 // one block per digit: exclusive scan of hist[d * nb .. d * nb + nt) over the nt tiles holding keys,
-// total into digit_total[d]
+// total into digit_total[d]. Chunks of kSortBlock counts are scanned in order; a window of kScanWindow
+// chunks is loaded before any of it is scanned (one memory round trip per window, not per chunk).
+constexpr int kScanWindow = 8;
 template <int ITEMS>
 __global__ __launch_bounds__(kSortBlock) void radix_scan_hist(uint32_t* __restrict__ hist, unsigned nb,
                                                               uint32_t* __restrict__ digit_total, int64_t n,
@@ -152,13 +154,23 @@ __global__ __launch_bounds__(kSortBlock) void radix_scan_hist(uint32_t* __restri
     const unsigned nt = active_tiles<ITEMS>(n, n_dev);
     uint32_t* h = hist + (int64_t)blockIdx.x * nb;
     uint32_t carry = 0;
-    for (unsigned start = 0; start < nt; start += kSortBlock) {
-        const unsigned i = start + threadIdx.x;
-        const uint32_t v = i < nt ? h[i] : 0u;
-        uint32_t tot;
-        const uint32_t ex = block_exclusive_scan<uint32_t>(v, lds, tot);
-        if (i < nt) h[i] = carry + ex;
-        carry += tot;
+    for (unsigned w0 = 0; w0 < nt; w0 += kSortBlock * kScanWindow) {
+        uint32_t v[kScanWindow];
+#pragma unroll
+        for (int j = 0; j < kScanWindow; ++j) {
+            const unsigned i = w0 + (unsigned)(kSortBlock * j) + threadIdx.x;
+            v[j] = i < nt ? h[i] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kScanWindow; ++j) {
+            const unsigned start = w0 + (unsigned)(kSortBlock * j);
+            if (start >= nt) break;  // block-uniform
+            const unsigned i = start + threadIdx.x;
+            uint32_t tot;
+            const uint32_t ex = block_exclusive_scan<uint32_t>(v[j], lds, tot);
+            if (i < nt) h[i] = carry + ex;
+            carry += tot;
+        }
     }
     if (threadIdx.x == 0) digit_total[blockIdx.x] = carry;
 }
