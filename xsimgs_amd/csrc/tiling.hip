@@ -870,6 +870,22 @@ __global__ __launch_bounds__(kBlock) void rows_scan_kernel(int64_t m, const uint
     }
 }
 
+// Every expansion block's first and last instance (the instances holding its first and last run): each
+// instance marks the blocks whose first or last run it holds. Every visible instance has at least one
+// run, so a block of kExpandPerBlock runs spans at most that many instances.
+__global__ __launch_bounds__(kBlock) void run_block_bounds_kernel(int64_t m, const uint32_t* __restrict__ roff,
+                                                                  int64_t n_runs, uint32_t* __restrict__ first,
+                                                                  uint32_t* __restrict__ last) {
+    const int64_t p = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (p >= m) return;
+    const int64_t o0 = roff[p], o1 = p + 1 < m ? (int64_t)roff[p + 1] : n_runs;  // the instance's runs [o0, o1)
+    for (int64_t b = o0 / kExpandPerBlock; b * kExpandPerBlock < o1; ++b) {
+        if (b * kExpandPerBlock >= o0) first[b] = (uint32_t)p;
+        const int64_t end = min(n_runs, (b + 1) * kExpandPerBlock) - 1;
+        if (end < o1) last[b] = (uint32_t)p;
+    }
+}
+
 // Merge-path expansion of the depth-ordered instances into row runs: run r gets its row bucket
 // and its record for the writers (flatten id, depth bits, column range x0 | x1 << 16, row bucket),
 // which the row sort then carries. A block writes one tile of the run sort (kExpandPerBlock runs),
@@ -885,30 +901,28 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
                                                              int64_t n_per_cam, int spans, uint32_t neg_row,
                                                              uint32_t* __restrict__ out_row,
                                                              uint4* __restrict__ out_rec,
-                                                             uint32_t* __restrict__ hist, unsigned nb) {
+                                                             uint32_t* __restrict__ hist, unsigned nb,
+                                                             const uint32_t* __restrict__ first,
+                                                             const uint32_t* __restrict__ last) {
     __shared__ uint32_t s_off[kExpandPerBlock];
     __shared__ uint32_t s_row[kExpandPerBlock];  // first row bucket of the instance, or neg_row
     __shared__ uint32_t s_fid[kExpandPerBlock];
     __shared__ uint32_t s_key[kExpandPerBlock];
     __shared__ uint32_t s_cols[kExpandPerBlock];
+    __shared__ int32_t s_inst[kExpandPerBlock];  // per run slot: the staged instance holding it
+    __shared__ int32_t s_wmax[kWaves];
     constexpr int R = 1 << RB;
     __shared__ uint32_t s_hist[R];
-    __shared__ int64_t s_range[2];
     for (int d = threadIdx.x; d < R; d += kBlock) s_hist[d] = 0;
-    const int64_t o0 = (int64_t)blockIdx.x * kExpandPerBlock;
+    for (int q = threadIdx.x; q < kExpandPerBlock; q += kBlock) s_inst[q] = 0;
+    // each XCD takes a contiguous range of blocks, so that the histogram words of neighbouring blocks
+    // (consecutive words of each digit's row) meet in one L2
+    const unsigned blk = (unsigned)xcd_tile((int)blockIdx.x, (int)gridDim.x);
+    const int64_t o0 = (int64_t)blk * kExpandPerBlock;
     const int64_t o_end = min(n_runs, o0 + kExpandPerBlock);
-    if (threadIdx.x < 2) {
-        const int64_t x = threadIdx.x == 0 ? o0 : o_end - 1;
-        int64_t lo = 0, hi = m - 1;
-        while (lo < hi) {
-            const int64_t mid = (lo + hi + 1) >> 1;
-            if ((int64_t)roff[mid] <= x) lo = mid; else hi = mid - 1;
-        }
-        s_range[threadIdx.x] = lo;
-    }
-    __syncthreads();
-    const int64_t p_lo = s_range[0];
-    const int cnt = (int)min<int64_t>(s_range[1] - p_lo + 1, kExpandPerBlock);
+    // the instances holding the block's first and last run (run_block_bounds_kernel)
+    const int64_t p_lo = first[blk];
+    const int cnt = (int)min<int64_t>((int64_t)last[blk] - p_lo + 1, kExpandPerBlock);
     for (int e = threadIdx.x; e < cnt; e += kBlock) {
         const int64_t p = p_lo + e;
         const uint32_t v = ids[p];
@@ -923,14 +937,41 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
         s_cols[e] = (uint32_t)r.x0 | ((uint32_t)r.x1 << 16);
     }
     __syncthreads();
+    // every staged instance after the first marks the slot of its first run; a running maximum over
+    // the slots then gives each run its instance (the staged instances start in increasing order)
+    for (int e = threadIdx.x + 1; e < cnt; e += kBlock) s_inst[s_off[e] - o0] = e;
+    __syncthreads();
+    {
+        constexpr int kPer = kExpandPerBlock / kBlock;  // consecutive slots per thread
+        const int q0 = threadIdx.x * kPer;
+        int32_t v[kPer];
+        int32_t run = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            run = max(run, s_inst[q0 + j]);
+            v[j] = run;
+        }
+        // maximum over the threads before this one
+        int32_t inc = run;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int32_t t = __shfl_up(inc, off, 64);
+            if (__lane_id() >= off) inc = max(inc, t);
+        }
+        const int wave = threadIdx.x >> 6;
+        if (__lane_id() == 63) s_wmax[wave] = inc;
+        __syncthreads();
+        int32_t before = __shfl_up(inc, 1, 64);
+        if (__lane_id() == 0) before = 0;
+        for (int w = 0; w < wave; ++w) before = max(before, s_wmax[w]);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) s_inst[q0 + j] = max(before, v[j]);
+    }
+    __syncthreads();
     for (int q = threadIdx.x; q < kExpandPerBlock; q += kBlock) {
         const int64_t o = o0 + q;
         if (o >= o_end) break;
-        int lo = 0, hi = cnt - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if ((int64_t)s_off[mid] <= o) lo = mid; else hi = mid - 1;
-        }
+        const int lo = s_inst[q];
         const uint32_t row0 = s_row[lo];
         const uint32_t row = row0 == neg_row ? neg_row : row0 + (uint32_t)(o - (int64_t)s_off[lo]);
         out_row[o] = row;
@@ -938,7 +979,7 @@ __global__ __launch_bounds__(kBlock) void expand_runs_kernel(int64_t n_runs, con
         atomicAdd(&s_hist[row & (R - 1)], 1u);
     }
     __syncthreads();
-    for (int d = threadIdx.x; d < R; d += kBlock) hist[(int64_t)d * nb + blockIdx.x] = s_hist[d];
+    for (int d = threadIdx.x; d < R; d += kBlock) hist[(int64_t)d * nb + blk] = s_hist[d];
 }
 
 // Scan of the per-group counts of every bucket over its first ceil(m / 64) groups, in slices of
@@ -1796,6 +1837,7 @@ struct FillWs {
     uint32_t* row_start; uint32_t* seg_base; uint32_t* seg_row;
     uint32_t* slots; uint32_t* tile_tot;
     uint32_t* hist; uint32_t* dtot;
+    uint32_t* blk_first; uint32_t* blk_last;       // each expansion block's first and last instance
     int n_rows;                                     // row buckets incl. the negative one
     int row_bits, rb, passes;                       // row bucket bits, run sort digit width and passes
     int64_t s_max;                                  // segment bound
@@ -1829,6 +1871,8 @@ FillWs fill_ws_layout(const Geometry& g, int64_t n_runs, void* base) {
     w.tile_tot = (uint32_t*)take(4 * ((size_t)(w.n_rows - 1) * g.ntx + 1));
     w.hist = (uint32_t*)take(direct ? 0 : 4 * ((size_t)1 << w.rb) * nb_r);
     w.dtot = (uint32_t*)take(direct ? 0 : 4 * ((size_t)1 << w.rb));
+    w.blk_first = (uint32_t*)take(direct ? 0 : 4 * (size_t)nb_r);
+    w.blk_last = (uint32_t*)take(direct ? 0 : 4 * (size_t)nb_r);
     w.bytes = off;
     return w;
 }
@@ -1840,9 +1884,10 @@ template <int RB>
 void expand_and_sort_runs(const FillWs& fw, const CountWs& cw, int64_t n_runs, int64_t m, int nty, int64_t n_per_cam,
                           int spans, uint32_t neg_row, uint32_t* out_row, uint4* out_rec, hipStream_t s) {
     const unsigned nb_runs = sort_blocks<kRunSortItems>(n_runs);
+    run_block_bounds_kernel<<<xsg_blocks(m, kBlock), kBlock, 0, s>>>(m, cw.roff, n_runs, fw.blk_first, fw.blk_last);
     expand_runs_kernel<RB><<<nb_runs, kBlock, 0, s>>>(n_runs, cw.roff, cw.pre_id, cw.pre_key, m, cw.drect_lo,
                                                       cw.drect_hi, nty, n_per_cam, spans, neg_row, fw.row_a, fw.rec_a,
-                                                      fw.hist, nb_runs);
+                                                      fw.hist, nb_runs, fw.blk_first, fw.blk_last);
     radix_sort_passes<uint32_t, uint4, PlainOut<uint32_t, uint4>, kRunSortItems, RB>(
         fw.row_a, fw.rec_a, fw.row_b, fw.rec_b, n_runs, 0, fw.row_bits, fw.hist, fw.dtot,
         PlainOut<uint32_t, uint4>{out_row, out_rec}, s, nullptr, /*first_hist_ready=*/true);
