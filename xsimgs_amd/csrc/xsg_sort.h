@@ -101,6 +101,20 @@ XSG_DEV unsigned active_tiles(int64_t n, const uint32_t* n_dev) {
     return (unsigned)((n + kSortBlock * ITEMS - 1) / (kSortBlock * ITEMS));
 }
 
+// The tiles a grid-striding pass visits: with at least 8 workgroups each XCD (workgroups are dispatched
+// round-robin over the 8 XCDs) takes a contiguous eighth of the tiles, so that neighbouring tiles'
+// histogram words, consecutive in each digit's row, meet in one L2; smaller grids stride plainly.
+struct TileWalk {
+    unsigned t, end, step;
+};
+XSG_DEV TileWalk tile_walk(unsigned nt) {
+    const unsigned g = gridDim.x;
+    if (g < 8u) return TileWalk{blockIdx.x, nt, g};
+    const unsigned x = blockIdx.x & 7u, r = blockIdx.x >> 3;
+    const unsigned t0 = (unsigned)((uint64_t)nt * x / 8u), t1 = (unsigned)((uint64_t)nt * (x + 1u) / 8u);
+    return TileWalk{t0 + r, t1, (g - x + 7u) >> 3};  // the XCD's workgroups: ceil((g - x) / 8)
+}
+
 // RB: bits per digit (8 by default; up to 10 for a single pass over a wider key, the digit-indexed
 // arrays then holding 1 << RB entries, R / kSortBlock per thread).
 template <typename K, int ITEMS = kSortItems, int RB = 8, bool RANGE = false>
@@ -117,7 +131,8 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict_
     const unsigned nt = active_tiles<ITEMS>(n, nullptr);
     __shared__ uint32_t cnt[kWaves][R];
     const int t = threadIdx.x, wave = t >> 6;
-    for (unsigned tile = blockIdx.x; tile < nt; tile += gridDim.x) {
+    for (TileWalk it = tile_walk(nt); it.t < it.end; it.t += it.step) {
+        const unsigned tile = it.t;
         __syncthreads();  // the previous tile's sums are read
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
@@ -224,7 +239,8 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
 #pragma unroll
         for (int j = 0; j < DPT; ++j) dprefix[j] = ex + loc[j];
     }
-    for (unsigned tile = blockIdx.x; tile < nt; tile += gridDim.x) {
+    for (TileWalk it = tile_walk(nt); it.t < it.end; it.t += it.step) {
+        const unsigned tile = it.t;
         __syncthreads();  // the previous tile's LDS contents are consumed
         const int64_t tile0 = (int64_t)tile * kTile;
         const int n_tile = (int)min<int64_t>(kTile, n - tile0);
