@@ -1362,7 +1362,8 @@ __global__ __launch_bounds__(kBlock) void seg_count_rows_kernel(int n_rows, cons
         for (int r = threadIdx.x; r <= n_real; r += kBlock) seg_base[r] = s_sb[r];
     }
     const int wave = threadIdx.x >> 6, lane = __lane_id();
-    const uint32_t sg = blockIdx.x * kWaves + wave;
+    // each XCD a contiguous range of segments: a column's counts of consecutive segments share lines
+    const uint32_t sg = (uint32_t)xcd_tile((int)blockIdx.x, (int)gridDim.x) * kWaves + wave;
     if (sg >= s_sb[n_real]) return;  // wave-uniform; no barrier follows
     // the segment's row: the last r with s_sb[r] <= sg (rows without segments share a base with the
     // next row, and the search takes the later one)
