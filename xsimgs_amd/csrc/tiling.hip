@@ -550,7 +550,7 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
 // that digit, 8 bits per pass: in LDS when it holds at most kBucketCap keys, else chunk by chunk
 // through global memory (ping-ponging between the bucket's ranges of the two arrays). The result is
 // the stable order of the keys, which is what LSD passes over all 32 bits give.
-constexpr int kBucketThreads = 512;
+constexpr int kBucketThreads = 1024;
 constexpr int kBucketWaves = kBucketThreads / 64;
 constexpr int kBucketCap = 8192;
 constexpr int kBucketSteps = kBucketCap / kBucketThreads;  // steps of 64 keys per wavefront, at most
