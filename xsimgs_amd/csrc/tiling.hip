@@ -501,12 +501,21 @@ __global__ __launch_bounds__(kBlock) void compact_kernel(
     // latency then overlaps the block's offset), one block scan places them all
     const int64_t v0 = (int64_t)blockIdx.x * kCountTile + (int64_t)threadIdx.x * kCountItems;
     uint32_t c[kCountItems], key[kCountItems];
+    static_assert(kCountItems == 4, "one 16-byte vector of counts and one of keys per thread");
+    const bool vec = v0 + kCountItems <= n_virtual && ((uintptr_t)vcnt & 15) == 0 && ((uintptr_t)vkey & 15) == 0;
+    if (vec) {  // the whole item run in range and both arrays 16-byte aligned: one vector load each
+        const uint4 cv = *reinterpret_cast<const uint4*>(vcnt + v0);
+        const uint4 kv = *reinterpret_cast<const uint4*>(vkey + v0);
+        c[0] = cv.x; c[1] = cv.y; c[2] = cv.z; c[3] = cv.w;
+        key[0] = kv.x; key[1] = kv.y; key[2] = kv.z; key[3] = kv.w;
+    } else {
 #pragma unroll
-    for (int k = 0; k < kCountItems; ++k) {
-        const int64_t v = min(v0 + k, n_virtual - 1);
-        const uint32_t cv = vcnt[v];
-        key[k] = vkey[v];
-        c[k] = v0 + k < n_virtual ? cv : 0u;
+        for (int k = 0; k < kCountItems; ++k) {
+            const int64_t v = min(v0 + k, n_virtual - 1);
+            const uint32_t cv = vcnt[v];
+            key[k] = vkey[v];
+            c[k] = v0 + k < n_virtual ? cv : 0u;
+        }
     }
     uint64_t carry = slice_offset<uint64_t>(slice_sum, blockIdx.x / kSlice, lds) + pbase[blockIdx.x];
     if (blockIdx.x == 0) {  // block-uniform
