@@ -229,6 +229,31 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
     __shared__ V svals[kTile];
     const int t = threadIdx.x, wave = t >> 6, lane = __lane_id();
     const unsigned nt = active_tiles<ITEMS>(n, nullptr);
+    const int seg0 = wave * kSeg;
+    // A tile's keys, values and histogram words are loaded into registers before the barriers and
+    // scans that precede their use (the first tile's before the digit prefix scan, each next one's
+    // while the current tile is written out), so their latency overlaps that work.
+    K key[kSteps];
+    V val[kSteps];
+    uint32_t hcol[DPT];
+    auto load_tile = [&](unsigned tile) {
+        const int64_t tile0 = (int64_t)tile * kTile;
+        const int n_tile = (int)min<int64_t>(kTile, n - tile0);
+#pragma unroll
+        for (int r = 0; r < kSteps; ++r) {
+            const int li = seg0 + r * 64 + lane;
+            key[r] = K{};
+            val[r] = V{};
+            if (li < n_tile) {
+                key[r] = keys_in[tile0 + li];
+                val[r] = vals_in[tile0 + li];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) hcol[j] = hist[(int64_t)(t * DPT + j) * nb + tile];
+    };
+    TileWalk it = tile_walk(nt);
+    if (it.t < it.end) load_tile(it.t);
     uint32_t dprefix[DPT];  // first output position of each of the thread's digits
     {
         uint32_t loc[DPT], s = 0;
@@ -239,7 +264,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
 #pragma unroll
         for (int j = 0; j < DPT; ++j) dprefix[j] = ex + loc[j];
     }
-    for (TileWalk it = tile_walk(nt); it.t < it.end; it.t += it.step) {
+    for (; it.t < it.end; it.t += it.step) {
         const unsigned tile = it.t;
         __syncthreads();  // the previous tile's LDS contents are consumed
         const int64_t tile0 = (int64_t)tile * kTile;
@@ -247,28 +272,19 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
 #pragma unroll
         for (int j = 0; j < DPT; ++j) {
             const int d = t * DPT + j;
-            gbase[d] = dprefix[j] + hist[(int64_t)d * nb + tile];
+            gbase[d] = dprefix[j] + hcol[j];
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) wcnt[w][d] = 0;
         }
         __syncthreads();
         const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-        K key[kSteps];
-        V val[kSteps];
         uint32_t rank[kSteps];
-        const int seg0 = wave * kSeg;
 #pragma unroll
         for (int r = 0; r < kSteps; ++r) {
             const int li = seg0 + r * 64 + lane;
             const bool valid = li < n_tile;
-            key[r] = K{};
-            val[r] = V{};
             uint32_t d = 0;
-            if (valid) {
-                key[r] = keys_in[tile0 + li];
-                val[r] = vals_in[tile0 + li];
-                d = pass_digit<K, RANGE>(key[r], shift, bits, kr);
-            }
+            if (valid) d = pass_digit<K, RANGE>(key[r], shift, bits, kr);
             uint64_t peers = __ballot(valid);
             for (int b = 0; b < bits; ++b) {
                 const uint64_t m = __ballot((d >> b) & 1u);
@@ -307,6 +323,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep(const K* __restric
                 svals[pos] = val[r];
             }
         }
+        if (it.t + it.step < it.end) load_tile(it.t + it.step);  // block-uniform
         __syncthreads();
         for (int i = t; i < n_tile; i += kSortBlock) {
             const K k = skeys[i];
