@@ -133,17 +133,25 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep(const K* __restrict_
     const int t = threadIdx.x, wave = t >> 6;
     for (TileWalk it = tile_walk(nt); it.t < it.end; it.t += it.step) {
         const unsigned tile = it.t;
+        // the tile's keys are loaded before the counters are cleared, so that their latency overlaps
+        // the barriers
+        const int64_t base = (int64_t)tile * (kSortBlock * ITEMS);
+        K key[ITEMS];
+#pragma unroll
+        for (int k = 0; k < ITEMS; ++k) {
+            const int64_t idx = base + (int64_t)k * kSortBlock + t;
+            key[k] = idx < n ? keys[idx] : K{};
+        }
         __syncthreads();  // the previous tile's sums are read
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
 #pragma unroll
             for (int j = 0; j < DPT; ++j) cnt[w][j * kSortBlock + t] = 0;
         __syncthreads();
-        const int64_t base = (int64_t)tile * (kSortBlock * ITEMS);
-#pragma unroll 4
+#pragma unroll
         for (int k = 0; k < ITEMS; ++k) {
             const int64_t idx = base + (int64_t)k * kSortBlock + t;
-            if (idx < n) atomicAdd(&cnt[wave][pass_digit<K, RANGE>(keys[idx], shift, bits, kr)], 1u);
+            if (idx < n) atomicAdd(&cnt[wave][pass_digit<K, RANGE>(key[k], shift, bits, kr)], 1u);
         }
         __syncthreads();
 #pragma unroll
