@@ -211,6 +211,19 @@ int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_positions, c
                             float* grad_q, float* grad_t, float* grad_v, float* grad_w, void* workspace,
                             xsg_stream_t stream);
 
+/* Extension, no reference counterpart: the parameter activations a training caller applies before
+ * the path (torch.exp of the log-scales, torch.sigmoid of the opacity logits; the reference takes
+ * activated scales and opacities, render.py:85-96) in one launch, and their gradients in one
+ * launch: scales [n, 3] = exp(log_scales), opacities [n] = sigmoid(opacity_logits);
+ * v_log_scales = v_scales * scales, v_opacity_logits = v_opacities * (1 - opacities) * opacities,
+ * bit-identical to torch's kernels. In the backward either gradient pair may be NULL (that output
+ * is then not written). */
+int xsg_activate_fwd(int64_t n, const float* log_scales, const float* opacity_logits, float* scales,
+                     float* opacities, xsg_stream_t stream);
+int xsg_activate_bwd(int64_t n, const float* scales, const float* opacities, const float* v_scales,
+                     const float* v_opacities, float* v_log_scales, float* v_opacity_logits,
+                     xsg_stream_t stream);
+
 /* ------------------------------------------------------------------ binning */
 int xsg_mask_radii(int64_t n, const uint8_t* mask, float* radii, xsg_stream_t stream);
 int xsg_mask_radii_packed(int64_t n, const uint32_t* packed_mask, float* radii, xsg_stream_t stream);

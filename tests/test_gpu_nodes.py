@@ -142,3 +142,58 @@ def test_rigid_autograd_and_torch_twin(dev):
         print(report(name, np_(a.grad), np_(b.grad)), flush=True)
         scale = max(1.0, float(b.grad.abs().max()))
         assert torch.allclose(a.grad, b.grad, rtol=1e-4, atol=1e-5 * scale), name
+
+
+def _ulps(a, b):
+    """Largest distance in float32 units in the last place between two tensors of finite values."""
+    ia = a.detach().float().cpu().contiguous().view(torch.int32).long()
+    ib = b.detach().float().cpu().contiguous().view(torch.int32).long()
+    ia = torch.where(ia < 0, -(ia & 0x7fffffff), ia)
+    ib = torch.where(ib < 0, -(ib & 0x7fffffff), ib)
+    return int((ia - ib).abs().max()) if ia.numel() else 0
+
+
+@pytest.mark.parametrize("n", [1, 63, 1000, 1_000_003])
+def test_activate_gaussians_is_torch_exp_and_sigmoid(dev, n):
+    """The fused activation op against torch.exp / torch.sigmoid and their autograd on the GPU (the
+    same float expressions: the same bits), and against float64 within a float32 rounding; logits and
+    log-scales far into the saturated ranges included."""
+    from xsimgs_amd.rendering import activate_gaussians
+    g = torch.Generator().manual_seed(n)
+    ls = torch.randn(n, 3, generator=g) * 3
+    lg = torch.randn(n, generator=g) * 6
+    if n >= 63:
+        ls[:5, 0] = torch.tensor([-100.0, -87.5, 0.0, 60.0, 88.5])
+        lg[:6] = torch.tensor([-1e4, -100.0, -17.0, 0.0, 30.0, 1e4])
+    ls, lg = ls.to(dev).requires_grad_(), lg.to(dev).requires_grad_()
+    vs, vo = torch.randn(n, 3, generator=g).to(dev), torch.randn(n, generator=g).to(dev)
+    s, o = activate_gaussians(ls, lg)
+    rs, ro = torch.exp(ls), torch.sigmoid(lg)
+    gls, glg = torch.autograd.grad((s, o), (ls, lg), (vs, vo))
+    rls, rlg = torch.autograd.grad((rs, ro), (ls, lg), (vs, vo))
+    d = {k: _ulps(a, b) for k, a, b in (("exp", s, rs), ("sigmoid", o, ro), ("v_log_scales", gls, rls),
+                                        ("v_logits", glg, rlg))}
+    print(f"activate n={n} ulps against torch: {d}")
+    assert all(v == 0 for v in d.values()), d
+    s64 = torch.exp(ls.detach().double())
+    o64 = torch.sigmoid(lg.detach().double())
+    fin = torch.isfinite(s64.float()) & (s64 > 1e-37)
+    np.testing.assert_allclose(np_(s)[np_(fin)], np_(s64)[np_(fin)], rtol=2.4e-7)
+    np.testing.assert_allclose(np_(o), np_(o64), rtol=3.6e-7, atol=1e-38)
+
+
+def test_activate_gaussians_one_sided_gradients(dev):
+    """A gradient that reaches only the scales (or only the opacities) leaves the other input's None,
+    and the one computed equals torch's."""
+    from xsimgs_amd.rendering import activate_gaussians
+    n = 4097
+    g = torch.Generator().manual_seed(5)
+    ls = (torch.randn(n, 3, generator=g)).to(dev).requires_grad_()
+    lg = (torch.randn(n, 1, generator=g) * 4).to(dev).requires_grad_()
+    s, o = activate_gaussians(ls, lg)
+    assert s.shape == (n, 3) and o.shape == (n, 1)
+    gls, glg = torch.autograd.grad((s * 2).sum(), (ls, lg), allow_unused=True)
+    assert glg is None and torch.equal(gls, torch.autograd.grad((torch.exp(ls) * 2).sum(), ls)[0])
+    s, o = activate_gaussians(ls, lg)
+    gls, glg = torch.autograd.grad((o ** 2).sum(), (ls, lg), allow_unused=True)
+    assert gls is None and torch.equal(glg, torch.autograd.grad((torch.sigmoid(lg) ** 2).sum(), lg)[0])

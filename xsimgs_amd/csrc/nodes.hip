@@ -199,6 +199,71 @@ int rigid_args(const xsg_rigid_desc* d, RigidArgs& a, const char* who) {
     return XSG_OK;
 }
 
+// The caller's parameter activations in one launch each way: the 3n scales (exp of their logs) and
+// the n opacities (sigmoid of the logits) as one range of chunks of four values, the scales' chunks
+// first; the backward multiplies each gradient by its activation's derivative, written from the
+// outputs as exp(x)' = exp(x) and sigmoid(x)' = sigmoid(x) (1 - sigmoid(x)). The float expressions
+// and their order are those of torch's exp, sigmoid, mul and sigmoid_backward kernels, so the results
+// are the same bits. VEC: every array 16-byte aligned, whole chunks move as one 16-byte access.
+XSG_DEV float act_exp(float a) { return expf(a); }
+XSG_DEV float act_sigmoid(float a) { return 1.0f / (1.0f + expf(-a)); }
+
+template <bool VEC, typename F>
+XSG_DEV void act_chunk(const float* __restrict__ x, float* __restrict__ y, int64_t i0, int64_t n, F f) {
+    if (VEC && i0 + 4 <= n) {
+        const float4 a = *reinterpret_cast<const float4*>(x + i0);
+        *reinterpret_cast<float4*>(y + i0) = make_float4(f(a.x), f(a.y), f(a.z), f(a.w));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (i0 + k < n) y[i0 + k] = f(x[i0 + k]);
+    }
+}
+
+template <bool VEC, typename F>
+XSG_DEV void act_grad_chunk(const float* __restrict__ v, const float* __restrict__ y, float* __restrict__ out,
+                            int64_t i0, int64_t n, F f) {
+    if (VEC && i0 + 4 <= n) {
+        const float4 a = *reinterpret_cast<const float4*>(v + i0);
+        const float4 b = *reinterpret_cast<const float4*>(y + i0);
+        *reinterpret_cast<float4*>(out + i0) = make_float4(f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (i0 + k < n) out[i0 + k] = f(v[i0 + k], y[i0 + k]);
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void activate_fwd_kernel(int64_t n3, int64_t n,
+                                                              const float* __restrict__ log_scales,
+                                                              const float* __restrict__ logits,
+                                                              float* __restrict__ scales,
+                                                              float* __restrict__ opacities) {
+    const int64_t q = (int64_t)blockIdx.x * kBlock + threadIdx.x, q3 = (n3 + 3) >> 2;
+    if (q < q3)
+        act_chunk<VEC>(log_scales, scales, 4 * q, n3, act_exp);
+    else
+        act_chunk<VEC>(logits, opacities, 4 * (q - q3), n, act_sigmoid);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void activate_bwd_kernel(int64_t n3, int64_t n,
+                                                              const float* __restrict__ scales,
+                                                              const float* __restrict__ opacities,
+                                                              const float* __restrict__ v_scales,
+                                                              const float* __restrict__ v_opacities,
+                                                              float* __restrict__ v_log_scales,
+                                                              float* __restrict__ v_logits) {
+    const int64_t q = (int64_t)blockIdx.x * kBlock + threadIdx.x, q3 = (n3 + 3) >> 2;
+    if (q < q3) {
+        if (v_scales) act_grad_chunk<VEC>(v_scales, scales, v_log_scales, 4 * q, n3, [](float a, float b) { return a * b; });
+    } else if (v_opacities) {
+        act_grad_chunk<VEC>(v_opacities, opacities, v_logits, 4 * (q - q3), n,
+                            [](float a, float b) { return a * (1.0f - b) * b; });
+    }
+}
+
 }  // namespace
 
 extern "C" int xsg_packed_mask_from_instances(int64_t n, const int32_t* instance_ids, const uint8_t* instance_mask,
@@ -272,5 +337,46 @@ extern "C" int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_p
         rigid_slots_out_kernel<<<xsg_blocks(13 * ni, kBlock), kBlock, 0, s>>>(slots, ni, grad_q, grad_t, grad_v,
                                                                              grad_w);
     XSG_TRY_LAUNCH("copy_gs_rigid_transform_bwd");
+    return XSG_OK;
+}
+
+static bool aligned16(std::initializer_list<const void*> ps) {  // NULL counts as aligned
+    for (const void* p : ps)
+        if (reinterpret_cast<uintptr_t>(p) % 16) return false;
+    return true;
+}
+
+extern "C" int xsg_activate_fwd(int64_t n, const float* log_scales, const float* opacity_logits, float* scales,
+                                float* opacities, xsg_stream_t stream) {
+    if (n < 0) return xsg_fail(XSG_ERR_INVALID, "activate_fwd: negative size");
+    if (n == 0) return XSG_OK;
+    if (!log_scales || !opacity_logits || !scales || !opacities)
+        return xsg_fail(XSG_ERR_INVALID, "activate_fwd: null tensor");
+    const unsigned grid = xsg_blocks((3 * n + 3) / 4 + (n + 3) / 4, kBlock);
+    const hipStream_t s = (hipStream_t)stream;
+    if (aligned16({log_scales, opacity_logits, scales, opacities}))
+        activate_fwd_kernel<true><<<grid, kBlock, 0, s>>>(3 * n, n, log_scales, opacity_logits, scales, opacities);
+    else
+        activate_fwd_kernel<false><<<grid, kBlock, 0, s>>>(3 * n, n, log_scales, opacity_logits, scales, opacities);
+    XSG_TRY_LAUNCH("activate_fwd");
+    return XSG_OK;
+}
+
+extern "C" int xsg_activate_bwd(int64_t n, const float* scales, const float* opacities, const float* v_scales,
+                                const float* v_opacities, float* v_log_scales, float* v_opacity_logits,
+                                xsg_stream_t stream) {
+    if (n < 0) return xsg_fail(XSG_ERR_INVALID, "activate_bwd: negative size");
+    if (n == 0 || (!v_scales && !v_opacities)) return XSG_OK;
+    if ((v_scales && (!scales || !v_log_scales)) || (v_opacities && (!opacities || !v_opacity_logits)))
+        return xsg_fail(XSG_ERR_INVALID, "activate_bwd: null tensor");
+    const unsigned grid = xsg_blocks((3 * n + 3) / 4 + (n + 3) / 4, kBlock);
+    const hipStream_t s = (hipStream_t)stream;
+    if (aligned16({scales, opacities, v_scales, v_opacities, v_log_scales, v_opacity_logits}))
+        activate_bwd_kernel<true><<<grid, kBlock, 0, s>>>(3 * n, n, scales, opacities, v_scales, v_opacities,
+                                                          v_log_scales, v_opacity_logits);
+    else
+        activate_bwd_kernel<false><<<grid, kBlock, 0, s>>>(3 * n, n, scales, opacities, v_scales, v_opacities,
+                                                           v_log_scales, v_opacity_logits);
+    XSG_TRY_LAUNCH("activate_bwd");
     return XSG_OK;
 }

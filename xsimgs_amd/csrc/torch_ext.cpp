@@ -582,6 +582,44 @@ std::tuple<Tensor, Tensor> radix_sort_pairs(const Tensor& keys, const Tensor& va
 
 // ------------------------------------------------------------------ scene-assembly producers
 // mask_from_instances (csrc/nodes/gs_masking.cu:29-44)
+// Extension: the caller's parameter activations, scales = exp(log_scales) and opacities =
+// sigmoid(opacity_logits), in one launch; and their gradients in one launch (either may be None).
+std::tuple<Tensor, Tensor> activate_fwd(const Tensor& log_scales, const Tensor& opacity_logits) {
+    check_same_device({log_scales, opacity_logits});
+    all_contiguous({log_scales, opacity_logits});
+    check_f32(log_scales, "log_scales");
+    check_f32(opacity_logits, "opacity_logits");
+    const int64_t n = opacity_logits.numel();
+    TORCH_CHECK(log_scales.numel() == 3 * n, "log_scales must hold three values per opacity logit");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(log_scales.device());
+    Tensor scales = at::empty_like(log_scales), opacities = at::empty_like(opacity_logits);
+    check_rc(xsg_activate_fwd(n, fptr(log_scales), fptr(opacity_logits), scales.data_ptr<float>(),
+                              opacities.data_ptr<float>(), stream_of(log_scales)));
+    return {scales, opacities};
+}
+
+std::tuple<Tensor, Tensor> activate_bwd(const Tensor& scales, const Tensor& opacities, const OptT& v_scales,
+                                        const OptT& v_opacities) {
+    std::vector<Tensor> ts{scales, opacities};
+    for (const OptT* o : {&v_scales, &v_opacities})
+        if (o->has_value()) ts.push_back(**o);
+    check_same_device(ts);
+    all_contiguous(ts);
+    for (const auto& t : ts) check_f32(t, "activation tensors");
+    const int64_t n = opacities.numel();
+    TORCH_CHECK(scales.numel() == 3 * n, "scales must hold three values per opacity");
+    TORCH_CHECK(!v_scales.has_value() || v_scales->numel() == 3 * n, "v_scales must match scales");
+    TORCH_CHECK(!v_opacities.has_value() || v_opacities->numel() == n, "v_opacities must match opacities");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(scales.device());
+    Tensor v_log_scales, v_logits;
+    if (v_scales.has_value()) v_log_scales = at::empty_like(scales);
+    if (v_opacities.has_value()) v_logits = at::empty_like(opacities);
+    check_rc(xsg_activate_bwd(n, fptr(scales), fptr(opacities), fptr(v_scales), fptr(v_opacities),
+                              v_scales.has_value() ? v_log_scales.data_ptr<float>() : nullptr,
+                              v_opacities.has_value() ? v_logits.data_ptr<float>() : nullptr, stream_of(scales)));
+    return {v_log_scales, v_logits};
+}
+
 Tensor packed_mask_from_instances(const Tensor& instance_ids, const Tensor& instance_mask) {
     check_same_device({instance_ids, instance_mask});
     all_contiguous({instance_ids, instance_mask});
@@ -1191,6 +1229,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     // scene-assembly producers (csrc/nodes/gs_masking.cu:44-47, container.cu:269-303)
     m.def("packed_mask_from_instances", &packed_mask_from_instances, py::arg("instance_ids"),
           py::arg("instance_mask"));
+    // extension: the caller's parameter activations and their gradients
+    m.def("activate_fwd", &activate_fwd, py::arg("log_scales"), py::arg("opacity_logits"));
+    m.def("activate_bwd", &activate_bwd, py::arg("scales"), py::arg("opacities"), py::arg("v_scales"),
+          py::arg("v_opacities"));
     m.def("copy_gs_rigid_transform_fwd", &copy_gs_rigid_transform_fwd, py::arg("positions"), py::arg("rotations"),
           py::arg("instance_id"), py::arg("inst_q"), py::arg("inst_t"), py::arg("inst_v"), py::arg("inst_w"),
           py::arg("inst_mask"), py::arg("out_positions"), py::arg("out_rotations"), py::arg("out_velocities"),

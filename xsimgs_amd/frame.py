@@ -1,6 +1,6 @@
 """One training frame of the hot path, as the reference's caller runs it.
 
-activations (exp scales, sigmoid opacity) -> SH colours -> UT projection -> tile binning with
+activations (exp scales, sigmoid opacity: one fused launch, its gradients another) -> SH colours -> UT projection -> tile binning with
 sort -> per-tile offsets -> camera rays -> eval3d composite forward -> composite backward ->
 SH backward -> activation gradients. The sequence is ut_gs_render's (reference
 src/xsimgs/rendering/render.py:85-187) with the intermediates kept for inspection; the
@@ -15,6 +15,7 @@ import torch
 
 from . import cameras as C
 from ._C import isect_regular_tiles_batched
+from .rendering.activate import activate_gaussians
 from .rendering.rasterize import ut_gs_rasterize, ut_gs_rasterize_batched
 from .rendering.render import ut_gs_tiling
 from .rendering.sh import spherical_harmonics_fused
@@ -66,8 +67,7 @@ def render_frame(st: FrameState, backward: bool = False, grads=None, cam_index: 
     sc = st.scene
     spec = sc.cameras[cam_index]
     cam = st.cams[cam_index]
-    scales = torch.exp(st.log_scales)
-    opac = torch.sigmoid(st.opacity_logits)
+    scales, opac = activate_gaussians(st.log_scales, st.opacity_logits)
     if st.sh is not None:
         origin = cam.pose.t
         colors = spherical_harmonics_fused(st.sh, st.means, origin, sc.sh_degree)
@@ -122,8 +122,7 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
     if not rig_batchable(st):
         raise ValueError("render_rig takes a static rig of regular-tiling cameras of one image size")
     W, H = specs[0].width, specs[0].height
-    scales = torch.exp(st.log_scales)
-    opac = torch.sigmoid(st.opacity_logits)
+    scales, opac = activate_gaussians(st.log_scales, st.opacity_logits)
     if st.sh is None:
         colors = st.colors
     elif rig_shares_origin(st):
