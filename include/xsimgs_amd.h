@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define XSG_ABI_VERSION 2
+#define XSG_ABI_VERSION 3
 
 /* return codes */
 #define XSG_OK 0
@@ -360,6 +360,12 @@ typedef struct {
      * wavefront per 16x16 tile) or 2 (two), or 0 to choose: 4 when the grid fills the GPU's wave slots
      * (3 x 1024 wavefronts), else 2. The gradients agree to float32 rounding either way. An extension. */
     int bwd_pixels_per_lane;
+    /* optional, [n_cams * n_tiles_h * n_tiles_w]: per (camera, tile) the backward's work estimate, the
+     * number of the tile's intersections up to its pixels' largest last id. xsg_eval3d_fwd writes it
+     * when non-NULL; xsg_eval3d_bwd reads it when non-NULL instead of deriving it from last_ids (a
+     * pass over every pixel). It only orders the backward's tiles: any values give the same
+     * gradients up to float32 rounding of the atomic sums. An extension. */
+    int32_t* tile_work;
 } xsg_eval3d_args;
 
 int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream);

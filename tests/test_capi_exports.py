@@ -66,7 +66,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_host_queries(lib):
     lib.xsg_abi_version.restype = C.c_int
-    assert lib.xsg_abi_version() == 2
+    assert lib.xsg_abi_version() == 3
     assert lib.xsg_camera_pack_elements(0) == 21
     assert lib.xsg_camera_pack_elements(1) == 21
     assert lib.xsg_camera_pack_elements(2) == 23

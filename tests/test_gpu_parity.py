@@ -485,6 +485,51 @@ def test_eval3d_bwd_without_ray_grads(dev, cfg0):
         assert frac_close(np_(y), np_(x), GRAD_ATOL, GRAD_RTOL) == 1.0
 
 
+def _tile_work_np(last, off, fl_n, W, H, tsx, tsy):
+    """Per tile: its intersections up to the largest last id of its pixels (the backward's launch-order
+    estimate), from the forward's last ids and the tile offsets."""
+    ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
+    o = off.reshape(-1).astype(np.int64)
+    ends = np.append(o[1:], fl_n)
+    work = np.zeros(ntx * nty, np.int64)
+    for t in range(ntx * nty):
+        ty, tx = divmod(t, ntx)
+        m = int(last[ty * tsy:(ty + 1) * tsy, tx * tsx:(tx + 1) * tsx].max())
+        work[t] = max(0, min(ends[t] - 1, m) - o[t] + 1)
+    return work
+
+
+def test_eval3d_tile_work_from_forward(dev, cfg0):
+    """The forward's per-tile work estimates (tile_work=, an extension) equal the formula on its last ids;
+    a backward that reads them, or garbage in their place (they only order the tiles), gives the
+    gradients of one that derives them itself."""
+    sc, st = cfg0
+    spec = sc.cameras[0]
+    cam, off, fl, ro, rd = _binned(st, sc, dev)
+    scales = torch.exp(st.log_scales)
+    opac = torch.sigmoid(st.opacity_logits)
+    colors = _C.spherical_harmonics_fused_fwd(0, cam.pose.t, st.means, st.sh, None, False)
+    work = torch.full((off.numel(),), -7, dtype=torch.int32, device=dev)
+    _, _, alpha, last = _C.rasterize_eval3d_fwd(st.means, st.quats, scales, colors.unsqueeze(0), opac.view(1, -1),
+                                                spec.width, spec.height, 16, 16, ro, rd, off, fl, tile_work=work)
+    want = _tile_work_np(np_(last), np_(off), fl.numel(), spec.width, spec.height, 16, 16)
+    assert want.max() > 0
+    np.testing.assert_array_equal(np_(work).astype(np.int64), want)
+    g = torch.Generator().manual_seed(13)
+    vr = (torch.randn(spec.height, spec.width, 3, generator=g) * 1e-3).to(dev)
+    vd = (torch.randn(spec.height, spec.width, generator=g) * 1e-3).to(dev)
+    va = (torch.randn(spec.height, spec.width, generator=g) * 1e-3).to(dev)
+    args = (st.means, scales, st.quats, opac, colors, ro, rd, 16, 16, off, fl, alpha, last, vr, vd, va)
+    a = _C.rasterize_eval3d_bwd(*args)
+    b = _C.rasterize_eval3d_bwd(*args, tile_work=work)
+    junk = torch.from_numpy(np.random.default_rng(3).integers(-2**31, 2**31 - 1, off.numel(),
+                                                              dtype=np.int64).astype(np.int32)).to(dev)
+    c = _C.rasterize_eval3d_bwd(*args, tile_work=junk)
+    for x, y, z in zip(a, b, c):
+        assert frac_close(np_(y), np_(x), GRAD_ATOL, GRAD_RTOL) == 1.0
+        assert frac_close(np_(z), np_(x), GRAD_ATOL, GRAD_RTOL) == 1.0
+
+
 # ------------------------------------------------------------------ scenes built for one rule each
 def _pinhole_scene(dev, seed, n=300, W=52, H=38, f=40.0):
     """Random Gaussians in front of a small pinhole camera, projected by the GPU's UT."""

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(int nblocks, 
 #pragma unroll
     for (int k = 0; k < kOrderThreads / 64; ++k) mx = max(mx, wmax[k]);
     const int shift = max(0, 32 - __clz(mx) - 8);  // work >> shift < 256
-    for (int i = threadIdx.x; i < cnt; i += kOrderThreads) atomicAdd(&hist[255 - (work[s0 + i] >> shift)], 1);
+    for (int i = threadIdx.x; i < cnt; i += kOrderThreads) atomicAdd(&hist[255 - (max(0, work[s0 + i]) >> shift)], 1);
     __syncthreads();
     if (threadIdx.x < 64) {  // exclusive scan of the 256 bins: four per lane, then across the wavefront
         const int l = threadIdx.x;
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(int nblocks, 
     }
     __syncthreads();
     for (int i = threadIdx.x; i < cnt; i += kOrderThreads) {
-        const int pos = atomicAdd(&hist[255 - (work[s0 + i] >> shift)], 1);
+        const int pos = atomicAdd(&hist[255 - (max(0, work[s0 + i]) >> shift)], 1);
         order[s0 + pos] = s0 + i;
     }
 }
@@ -257,6 +257,7 @@ extern "C" int xsg_eval3d_fwd(const xsg_eval3d_args* a, xsg_stream_t stream) {
     if ((int64_t)a->width * a->height == 0) return XSG_OK;
     p.out_rgb = a->out_rgb; p.out_depth = a->out_depth; p.out_alpha = a->out_alpha; p.out_last = a->out_last_ids;
     p.pair_counts = (unsigned long long*)a->pair_counts;
+    p.tile_work = a->tile_work;
     const bool dyn = a->velocity != nullptr || a->ray_time_delta != nullptr;
     rc = eval3d_fwd_launch(a->cdim, dyn, p, (hipStream_t)stream);
     if (rc) return rc;
@@ -304,8 +305,11 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
         const BwdWorkspace w = bwd_workspace(n, nblocks);
         int32_t* work = reinterpret_cast<int32_t*>((char*)workspace + w.work_off);
         int32_t* order = reinterpret_cast<int32_t*>((char*)workspace + w.order_off);
-        tile_work_kernel<<<(unsigned)((nblocks + kBlock / 64 - 1) / (kBlock / 64)), kBlock, 0, s>>>(
-            p.g, a->last_ids, a->tile_offsets, work);
+        if (a->tile_work)  // written by the forward
+            work = a->tile_work;
+        else
+            tile_work_kernel<<<(unsigned)((nblocks + kBlock / 64 - 1) / (kBlock / 64)), kBlock, 0, s>>>(
+                p.g, a->last_ids, a->tile_offsets, work);
         tile_order_kernel<<<8, kOrderThreads, 0, s>>>(nblocks, work, order);
         p.tile_order = order;
         rc = eval3d_bwd_launch(a->cdim, dyn, p, s);

@@ -213,6 +213,18 @@ __global__ __launch_bounds__(NT) void eval3d_fwd_kernel(Eval3dParams p) {
         for (int k = 0; k < CDIM; ++k) p.out_rgb[c.pix * CDIM + k] = pix[k];
         p.out_last[c.pix] = (int32_t)cur_idx;
     }
+    if (p.tile_work) {  // the tile's backward work: its intersections up to the largest last id
+        __shared__ int s_last[NW];
+        int m = c.inside ? (int)cur_idx : -1;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = max(m, __shfl_xor(m, off, 64));
+        if (lane == 0) s_last[wave] = m;
+        __syncthreads();
+        if (c.tr == 0) {
+            for (int k = 1; k < nw; ++k) m = max(m, s_last[k]);
+            p.tile_work[c.cam * g.n_tiles_w * g.n_tiles_h + c.tile] = max(0, min(c.range_end - 1, m) - c.range_start + 1);
+        }
+    }
 }
 
 template <int CDIM>

@@ -114,6 +114,16 @@ xsg_eval3d_args base_args(const Tensor& means, const Tensor& quats, const Tensor
     return a;
 }
 
+// optional int32 device tensor of one value per (camera, tile): the backward's work estimates, written
+// by the forward and read by the backward (an extension of this build)
+int32_t* tile_work_ptr(const OptT& tile_work, const Tensor& offsets) {
+    if (!tile_work.has_value()) return nullptr;
+    TORCH_CHECK(tile_work->scalar_type() == at::kInt && tile_work->is_contiguous() &&
+                    tile_work->numel() == offsets.numel() && tile_work->device() == offsets.device(),
+                "tile_work must be a contiguous int32 tensor of one value per (camera, tile) on the offsets' device");
+    return tile_work->data_ptr<int32_t>();
+}
+
 // optional int64[2] device tensor of evaluated / composited pair counts (an extension of this build)
 uint64_t* counts_ptr(const OptT& pair_counts, const Tensor& like) {
     if (!pair_counts.has_value()) return nullptr;
@@ -128,7 +138,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
     const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tsw, int64_t tsh,
     const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta, const Tensor& tile_offsets,
-    const Tensor& flatten_ids, const OptT& pair_counts, bool batched = false) {
+    const Tensor& flatten_ids, const OptT& pair_counts, const OptT& tile_work, bool batched = false) {
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(means.device());
     auto opt = means.options();
     const int64_t channels = colors.has_value() ? colors->size(-1) : 0;
@@ -154,6 +164,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> eval3d_fwd_impl(
     a.out_rgb = renders.data_ptr<float>(); a.out_depth = depths.data_ptr<float>();
     a.out_alpha = alphas.data_ptr<float>(); a.out_last_ids = last_ids.data_ptr<int32_t>();
     a.pair_counts = counts_ptr(pair_counts, means);
+    a.tile_work = tile_work_ptr(tile_work, tile_offsets);
     check_rc(xsg_eval3d_fwd(&a, stream_of(means)));
     return {renders, depths, alphas, last_ids};
 }
@@ -162,10 +173,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_fwd(
     const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors, const Tensor& opacities,
     int64_t image_width, int64_t image_height, int64_t tile_size_width, int64_t tile_size_height,
     const Tensor& ray_origs, const Tensor& ray_dirs, const Tensor& tile_offsets, const Tensor& flatten_ids,
-    const OptT& pair_counts) {
+    const OptT& pair_counts, const OptT& tile_work) {
     return eval3d_fwd_impl(means, std::nullopt, quats, scales, colors, opacities, image_width, image_height,
                            tile_size_width, tile_size_height, ray_origs, ray_dirs, std::nullopt, tile_offsets,
-                           flatten_ids, pair_counts);
+                           flatten_ids, pair_counts, tile_work);
 }
 
 // batched cameras (extension): outputs [C, H, W, ch], [C, H, W] x2, last ids [C, H, W]
@@ -173,22 +184,22 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_fwd_batched(
     const Tensor& means, const Tensor& quats, const Tensor& scales, const OptT& colors, const Tensor& opacities,
     int64_t image_width, int64_t image_height, int64_t tile_size_width, int64_t tile_size_height,
     const Tensor& ray_origs, const Tensor& ray_dirs, const Tensor& tile_offsets, const Tensor& flatten_ids,
-    const OptT& velocity, const OptT& ray_time_delta, const OptT& pair_counts) {
+    const OptT& velocity, const OptT& ray_time_delta, const OptT& pair_counts, const OptT& tile_work) {
     TORCH_CHECK(velocity.has_value() == ray_time_delta.has_value(),
                 "dynamic compositing needs both velocity and ray_time_delta");
     return eval3d_fwd_impl(means, velocity, quats, scales, colors, opacities, image_width, image_height,
                            tile_size_width, tile_size_height, ray_origs, ray_dirs, ray_time_delta, tile_offsets,
-                           flatten_ids, pair_counts, true);
+                           flatten_ids, pair_counts, tile_work, true);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> rasterize_eval3d_dynamic_fwd(
     const Tensor& means, const OptT& velocity, const Tensor& quats, const Tensor& scales, const OptT& colors,
     const Tensor& opacities, int64_t image_width, int64_t image_height, int64_t tile_size_width,
     int64_t tile_size_height, const Tensor& ray_origs, const Tensor& ray_dirs, const OptT& ray_time_delta,
-    const Tensor& tile_offsets, const Tensor& flatten_ids, const OptT& pair_counts) {
+    const Tensor& tile_offsets, const Tensor& flatten_ids, const OptT& pair_counts, const OptT& tile_work) {
     return eval3d_fwd_impl(means, velocity, quats, scales, colors, opacities, image_width, image_height,
                            tile_size_width, tile_size_height, ray_origs, ray_dirs, ray_time_delta, tile_offsets,
-                           flatten_ids, pair_counts);
+                           flatten_ids, pair_counts, tile_work);
 }
 
 struct BwdOut {
@@ -205,7 +216,8 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
                        int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
                        const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors,
                        const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
-                       const OptT& pair_counts, int64_t pixels_per_lane, bool batched = false) {
+                       const OptT& pair_counts, int64_t pixels_per_lane, const OptT& tile_work,
+                       bool batched = false) {
     if (v_render_colors.has_value() && !v_render_colors->is_contiguous())
         throw std::runtime_error("v_render_colors must be contiguous");
     all_contiguous({v_render_depth, v_render_alpha, render_alpha, last_ids});
@@ -263,6 +275,7 @@ BwdOut eval3d_bwd_impl(const Tensor& points, const OptT& velocity, const Tensor&
     a.v_ray_d = o.v_ray_d.has_value() ? o.v_ray_d->data_ptr<float>() : nullptr;
     a.pair_counts = counts_ptr(pair_counts, points);
     a.bwd_pixels_per_lane = (int)pixels_per_lane;
+    a.tile_work = tile_work_ptr(tile_work, tile_offsets);
     Tensor ws = workspace(points, xsg_eval3d_bwd_workspace_bytes(&a));
     check_rc(xsg_eval3d_bwd(&a, ws.data_ptr(), stream_of(points)));
     return o;
@@ -273,11 +286,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT> rasterize_eval3d_bw
     const Tensor& ray_origins, const Tensor& ray_directions, int64_t tile_size_x, int64_t tile_size_y,
     const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
     const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha, bool ray_grads,
-    const OptT& pair_counts, int64_t pixels_per_lane) {
+    const OptT& pair_counts, int64_t pixels_per_lane, const OptT& tile_work) {
     BwdOut o = eval3d_bwd_impl(points, std::nullopt, scale, quat, opacity, colors, ray_origins, ray_directions,
                                std::nullopt, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
                                last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
-                               pixels_per_lane);
+                               pixels_per_lane, tile_work);
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d};
 }
 
@@ -289,13 +302,13 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, OptT, OptT> rasteri
     const Tensor& tile_offsets, const Tensor& flatten_ids, const Tensor& render_alpha, const Tensor& last_ids,
     const OptT& v_render_colors, const Tensor& v_render_depth, const Tensor& v_render_alpha,
     const OptT& velocity, const OptT& ray_time_delta, bool ray_grads, const OptT& pair_counts,
-    int64_t pixels_per_lane) {
+    int64_t pixels_per_lane, const OptT& tile_work) {
     TORCH_CHECK(velocity.has_value() == ray_time_delta.has_value(),
                 "dynamic compositing needs both velocity and ray_time_delta");
     BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
                                ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
                                last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
-                               pixels_per_lane, true);
+                               pixels_per_lane, tile_work, true);
     const bool dyn = velocity.has_value();
     return {o.v_points, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
             dyn ? OptT(o.v_velocity) : std::nullopt, dyn ? OptT(o.v_time_delta) : std::nullopt};
@@ -306,11 +319,12 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, OptT, OptT, OptT, Tensor> ras
     const OptT& colors, const Tensor& ray_origins, const Tensor& ray_directions, const Tensor& ray_time_delta,
     int64_t tile_size_x, int64_t tile_size_y, const Tensor& tile_offsets, const Tensor& flatten_ids,
     const Tensor& render_alpha, const Tensor& last_ids, const OptT& v_render_colors, const Tensor& v_render_depth,
-    const Tensor& v_render_alpha, bool ray_grads, const OptT& pair_counts, int64_t pixels_per_lane) {
+    const Tensor& v_render_alpha, bool ray_grads, const OptT& pair_counts, int64_t pixels_per_lane,
+    const OptT& tile_work) {
     BwdOut o = eval3d_bwd_impl(points, velocity, scale, quat, opacity, colors, ray_origins, ray_directions,
                                ray_time_delta, tile_size_x, tile_size_y, tile_offsets, flatten_ids, render_alpha,
                                last_ids, v_render_colors, v_render_depth, v_render_alpha, ray_grads, pair_counts,
-                               pixels_per_lane);
+                               pixels_per_lane, tile_work);
     return {o.v_points, o.v_velocity, o.v_quat, o.v_scale, o.v_opacity, o.v_colors, o.v_ray_o, o.v_ray_d,
             o.v_time_delta};
 }
@@ -1158,7 +1172,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("rasterize_eval3d_fwd", &rasterize_eval3d_fwd, py::arg("means"), py::arg("quats"), py::arg("scales"),
           py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
           py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"), py::arg("ray_dirs"),
-          py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("pair_counts") = py::none());
+          py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("pair_counts") = py::none(),
+          py::arg("tile_work") = py::none());
     // positional like the reference (eval3d_bwd.cu:406-408); `ray_grads` (extension, default True)
     // lets autograd skip the per-pixel ray gradients when the rays do not require grad
     m.def("rasterize_eval3d_bwd", &rasterize_eval3d_bwd, py::arg("points"), py::arg("scale"), py::arg("quat"),
@@ -1166,32 +1181,33 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
           py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
           py::arg("v_render_alpha"), py::arg("ray_grads") = true, py::arg("pair_counts") = py::none(),
-          py::arg("pixels_per_lane") = 0);
+          py::arg("pixels_per_lane") = 0, py::arg("tile_work") = py::none());
     m.def("rasterize_eval3d_dynamic_fwd", &rasterize_eval3d_dynamic_fwd, py::arg("means"), py::arg("velocity"),
           py::arg("quats"), py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"),
           py::arg("image_height"), py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"),
           py::arg("ray_dirs"), py::arg("ray_time_delta"), py::arg("tile_offsets"), py::arg("flatten_ids"),
-          py::arg("pair_counts") = py::none());
+          py::arg("pair_counts") = py::none(), py::arg("tile_work") = py::none());
     m.def("rasterize_eval3d_dynamic_bwd", &rasterize_eval3d_dynamic_bwd, py::arg("points"), py::arg("velocity"),
           py::arg("scale"), py::arg("quat"), py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"),
           py::arg("ray_directions"), py::arg("ray_time_delta"), py::arg("tile_size_x"), py::arg("tile_size_y"),
           py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("render_alpha"), py::arg("last_ids"),
           py::arg("v_render_colors"), py::arg("v_render_depth"), py::arg("v_render_alpha"),
           py::arg("ray_grads") = true, py::arg("pair_counts") = py::none(),
-          py::arg("pixels_per_lane") = 0);
+          py::arg("pixels_per_lane") = 0, py::arg("tile_work") = py::none());
     // batched cameras (extension): C cameras over one scene in one launch per pass
     m.def("rasterize_eval3d_fwd_batched", &rasterize_eval3d_fwd_batched, py::arg("means"), py::arg("quats"),
           py::arg("scales"), py::arg("colors"), py::arg("opacities"), py::arg("image_width"), py::arg("image_height"),
           py::arg("tile_size_width"), py::arg("tile_size_height"), py::arg("ray_origs"), py::arg("ray_dirs"),
           py::arg("tile_offsets"), py::arg("flatten_ids"), py::arg("velocity") = py::none(),
-          py::arg("ray_time_delta") = py::none(), py::arg("pair_counts") = py::none());
+          py::arg("ray_time_delta") = py::none(), py::arg("pair_counts") = py::none(),
+          py::arg("tile_work") = py::none());
     m.def("rasterize_eval3d_bwd_batched", &rasterize_eval3d_bwd_batched, py::arg("points"), py::arg("scale"),
           py::arg("quat"), py::arg("opacity"), py::arg("colors"), py::arg("ray_origins"), py::arg("ray_directions"),
           py::arg("tile_size_x"), py::arg("tile_size_y"), py::arg("tile_offsets"), py::arg("flatten_ids"),
           py::arg("render_alpha"), py::arg("last_ids"), py::arg("v_render_colors"), py::arg("v_render_depth"),
           py::arg("v_render_alpha"), py::arg("velocity") = py::none(), py::arg("ray_time_delta") = py::none(),
           py::arg("ray_grads") = true, py::arg("pair_counts") = py::none(),
-          py::arg("pixels_per_lane") = 0);
+          py::arg("pixels_per_lane") = 0, py::arg("tile_work") = py::none());
     m.def("eval3d_supported_ndims", &eval3d_supported_ndims);
 
     // color (csrc/color/sh_bind.cpp)

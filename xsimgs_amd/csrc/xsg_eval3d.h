@@ -314,6 +314,9 @@ struct Eval3dParams {
     // optional (backward): logical (camera, tile) block launched at each position of xcd_tile's order
     const int32_t* tile_order;
     int px_hint;  // backward pixels per lane for 129..256-pixel tiles: 0 (by grid size), 2 or 4
+    // optional (forward): per (camera, tile) the backward's work estimate, the tile's intersections up
+    // to its pixels' largest last id (what tile_work_kernel derives from the last ids)
+    int32_t* tile_work;
 };
 
 int eval3d_fwd_launch(int cdim, bool dyn, const Eval3dParams& p, hipStream_t s);

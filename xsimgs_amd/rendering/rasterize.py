@@ -4,7 +4,7 @@ import torch
 
 from .._C import (rasterize_eval3d_fwd, rasterize_eval3d_bwd, rasterize_eval3d_fwd_batched,
                   rasterize_eval3d_bwd_batched)
-from ._grad import apply_grad_mask
+from ._grad import apply_grad_mask, tile_work_buffer
 
 
 class UTGSRasterize(torch.autograd.Function):
@@ -16,7 +16,8 @@ class UTGSRasterize(torch.autograd.Function):
             means=positions, quats=rotation, scales=scale, opacities=density.view(1, -1),
             colors=colors.unsqueeze(0) if colors is not None else None, ray_origs=ray_o, ray_dirs=ray_d,
             image_width=width, image_height=height, tile_size_width=tile_size_x,
-            tile_size_height=tile_size_y, tile_offsets=isect_offsets, flatten_ids=flatten_ids)
+            tile_size_height=tile_size_y, tile_offsets=isect_offsets, flatten_ids=flatten_ids,
+            tile_work=tile_work_buffer(ctx, isect_offsets))
         ctx.tile_size_x = tile_size_x
         ctx.tile_size_y = tile_size_y
         ctx.save_for_backward(positions, rotation, scale, density, colors, ray_o, ray_d, isect_offsets,
@@ -33,7 +34,7 @@ class UTGSRasterize(torch.autograd.Function):
             isect_offsets, flatten_ids, out_alpha, last_ids,
             grad_rgb.contiguous() if grad_rgb is not None else None, grad_depth.contiguous(),
             grad_alpha.contiguous(),
-            ctx.needs_input_grad[5] or ctx.needs_input_grad[6])
+            ctx.needs_input_grad[5] or ctx.needs_input_grad[6], tile_work=ctx.tile_work)
         return apply_grad_mask(ctx, list(grads) + [None, None, None, None])
 
 
@@ -57,7 +58,8 @@ class UTGSRasterizeBatched(torch.autograd.Function):
         out_rgb, out_depth, out_alpha, last_ids = rasterize_eval3d_fwd_batched(
             means=positions, quats=rotation, scales=scale, opacities=density, colors=colors, ray_origs=ray_o,
             ray_dirs=ray_d, image_width=width, image_height=height, tile_size_width=tile_size_x,
-            tile_size_height=tile_size_y, tile_offsets=isect_offsets, flatten_ids=flatten_ids)
+            tile_size_height=tile_size_y, tile_offsets=isect_offsets, flatten_ids=flatten_ids,
+            tile_work=tile_work_buffer(ctx, isect_offsets))
         ctx.tile_size_x = tile_size_x
         ctx.tile_size_y = tile_size_y
         ctx.save_for_backward(positions, rotation, scale, density, colors, ray_o, ray_d, isect_offsets,
@@ -72,7 +74,8 @@ class UTGSRasterizeBatched(torch.autograd.Function):
             positions, scale, rotation, density, colors, ray_o, ray_d, ctx.tile_size_x, ctx.tile_size_y,
             isect_offsets, flatten_ids, out_alpha, last_ids,
             grad_rgb.contiguous() if grad_rgb is not None else None, grad_depth.contiguous(),
-            grad_alpha.contiguous(), ray_grads=ctx.needs_input_grad[5] or ctx.needs_input_grad[6])
+            grad_alpha.contiguous(), ray_grads=ctx.needs_input_grad[5] or ctx.needs_input_grad[6],
+            tile_work=ctx.tile_work)
         # v_points, v_quat, v_scale, v_opacity, v_colors, v_ray_o, v_ray_d (static: no velocity terms)
         return apply_grad_mask(ctx, list(grads[:7]) + [None, None, None, None])
 

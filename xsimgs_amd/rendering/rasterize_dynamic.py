@@ -2,7 +2,7 @@
 import torch
 
 from .._C import rasterize_eval3d_dynamic_fwd, rasterize_eval3d_dynamic_bwd
-from ._grad import apply_grad_mask
+from ._grad import apply_grad_mask, tile_work_buffer
 
 
 class UTGSDynamicRasterize(torch.autograd.Function):
@@ -14,7 +14,8 @@ class UTGSDynamicRasterize(torch.autograd.Function):
             means=positions, velocity=velocity, quats=rotation, scales=scale, opacities=density.view(1, -1),
             colors=colors.unsqueeze(0) if colors is not None else None, ray_origs=ray_o, ray_dirs=ray_d,
             ray_time_delta=ray_time_delta, image_width=width, image_height=height, tile_size_width=tile_size_x,
-            tile_size_height=tile_size_y, tile_offsets=isect_offsets, flatten_ids=flatten_ids)
+            tile_size_height=tile_size_y, tile_offsets=isect_offsets, flatten_ids=flatten_ids,
+            tile_work=tile_work_buffer(ctx, isect_offsets))
         ctx.tile_size_x = tile_size_x
         ctx.tile_size_y = tile_size_y
         ctx.save_for_backward(positions, velocity, rotation, scale, density, colors, ray_o, ray_d, ray_time_delta,
@@ -31,7 +32,7 @@ class UTGSDynamicRasterize(torch.autograd.Function):
             ctx.tile_size_x, ctx.tile_size_y, isect_offsets, flatten_ids, out_alpha, last_ids,
             grad_rgb.contiguous() if grad_rgb is not None else None, grad_depth.contiguous(),
             grad_alpha.contiguous(),
-            ctx.needs_input_grad[6] or ctx.needs_input_grad[7])
+            ctx.needs_input_grad[6] or ctx.needs_input_grad[7], tile_work=ctx.tile_work)
         return apply_grad_mask(ctx, list(grads) + [None, None, None, None])
 
 
