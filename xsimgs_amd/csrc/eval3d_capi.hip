@@ -9,22 +9,23 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// Zero fill of up to five float arrays, one per grid row (blockIdx.y): 16-byte stores over the
-// aligned body, single floats before and after it.
+// Zero fill of up to five float arrays, a group of workgroups each: 16-byte stores over the aligned
+// body, single floats before and after it.
 struct ZeroList {
     float* p[5];
     int64_t n[5];
 };
 
-__global__ __launch_bounds__(kBlock) void zero_kernel(ZeroList z) {
-    float* __restrict__ p = z.p[blockIdx.y];
-    const int64_t n = z.n[blockIdx.y];
+// Workgroup g of `groups` workgroups (blockDim.x threads each) clearing array `list`.
+XSG_DEV void zero_part(const ZeroList& z, int list, int g, int groups) {
+    float* __restrict__ p = z.p[list];
+    const int64_t n = z.n[list];
     if (!p || n <= 0) return;
     const int64_t head = min<int64_t>(n, (int64_t)(((16 - ((uintptr_t)p & 15)) & 15) / 4));
     const int64_t n4 = (n - head) / 4;
     const int64_t tail = head + 4 * n4;
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    const int64_t t0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t stride = (int64_t)groups * blockDim.x;
+    const int64_t t0 = (int64_t)g * blockDim.x + threadIdx.x;
     if (t0 < head) p[t0] = 0.f;
     if (t0 < n - tail) p[tail + t0] = 0.f;
     float4* __restrict__ p4 = reinterpret_cast<float4*>(p + head);
@@ -127,15 +128,15 @@ __global__ __launch_bounds__(kBlock) void tile_work_kernel(TileGrid g, const int
     }
 }
 
-// tile_order_kernel: one workgroup per XCD (8). XCD x runs the logical blocks
+// The tile order: one workgroup of kOrderThreads per XCD (8). XCD x runs the logical blocks
 // [x q + min(x, r), + q + (x < r)) of xcd_tile; they are placed heaviest first by a counting sort on
-// the top 8 bits of the work (LDS histogram, scan, scatter; ties in no particular order).
+// the top 8 bits of the work (LDS histogram, scan, scatter; ties in no particular order). Negative
+// estimates count as zero, so that any values give a permutation.
 constexpr int kOrderThreads = 1024;
-__global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(int nblocks, const int32_t* __restrict__ work,
-                                                                   int32_t* __restrict__ order) {
+XSG_DEV void tile_order_part(int x, int nblocks, const int32_t* __restrict__ work, int32_t* __restrict__ order) {
     __shared__ int hist[256];
     __shared__ int wmax[kOrderThreads / 64];
-    const int x = blockIdx.x, q = nblocks >> 3, r = nblocks & 7;
+    const int q = nblocks >> 3, r = nblocks & 7;
     const int s0 = x * q + min(x, r), cnt = q + (x < r ? 1 : 0);
     int mx = 0;
     for (int i = threadIdx.x; i < cnt; i += kOrderThreads) mx = max(mx, work[s0 + i]);
@@ -170,6 +171,20 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(int nblocks, 
     for (int i = threadIdx.x; i < cnt; i += kOrderThreads) {
         const int pos = atomicAdd(&hist[255 - (max(0, work[s0 + i]) >> shift)], 1);
         order[s0 + pos] = s0 + i;
+    }
+}
+
+// The backward's set-up in one launch of kOrderThreads-thread workgroups: workgroups [0, n_order) (8,
+// or 0 without tiles) order one XCD's tiles each, the others clear the accumulated outputs,
+// zero_groups workgroups per array.
+__global__ __launch_bounds__(kOrderThreads) void bwd_prep_kernel(ZeroList z, int zero_groups, int n_order,
+                                                                 int nblocks, const int32_t* __restrict__ work,
+                                                                 int32_t* __restrict__ order) {
+    const int b = (int)blockIdx.x;
+    if (b < n_order) {
+        tile_order_part(b, nblocks, work, order);
+    } else {
+        zero_part(z, (b - n_order) / zero_groups, (b - n_order) % zero_groups, zero_groups);
     }
 }
 
@@ -296,21 +311,25 @@ extern "C" int xsg_eval3d_bwd(const xsg_eval3d_args* a, void* workspace, xsg_str
                       {3 * n, n, ncol, 6 * n, dyn ? 3 * n : 0}};
     int64_t longest = 0;
     for (int k = 0; k < 5; ++k) longest = std::max(longest, zl.n[k]);
-    if (longest > 0) {
-        const unsigned gx = (unsigned)std::min<int64_t>((longest / 4 + kBlock - 1) / kBlock + 1, 1024);
-        zero_kernel<<<dim3(gx, 5), kBlock, 0, s>>>(zl);
-    }
-    if ((int64_t)a->width * a->height > 0) {
-        const int nblocks = a->n_cams * a->n_tiles_w * a->n_tiles_h;
-        const BwdWorkspace w = bwd_workspace(n, nblocks);
-        int32_t* work = reinterpret_cast<int32_t*>((char*)workspace + w.work_off);
-        int32_t* order = reinterpret_cast<int32_t*>((char*)workspace + w.order_off);
+    const int zero_groups =
+        (int)std::min<int64_t>((longest / 4 + kOrderThreads - 1) / kOrderThreads + 1, 256);
+    const bool pixels = (int64_t)a->width * a->height > 0;
+    const int nblocks = a->n_cams * a->n_tiles_w * a->n_tiles_h;
+    const BwdWorkspace w = bwd_workspace(n, nblocks);
+    int32_t* work = reinterpret_cast<int32_t*>((char*)workspace + w.work_off);
+    int32_t* order = reinterpret_cast<int32_t*>((char*)workspace + w.order_off);
+    if (pixels) {
         if (a->tile_work)  // written by the forward
             work = a->tile_work;
         else
             tile_work_kernel<<<(unsigned)((nblocks + kBlock / 64 - 1) / (kBlock / 64)), kBlock, 0, s>>>(
                 p.g, a->last_ids, a->tile_offsets, work);
-        tile_order_kernel<<<8, kOrderThreads, 0, s>>>(nblocks, work, order);
+    }
+    const int n_order = pixels ? 8 : 0;
+    if (n_order > 0 || longest > 0)
+        bwd_prep_kernel<<<(unsigned)(n_order + (longest > 0 ? 5 * zero_groups : 0)), kOrderThreads, 0, s>>>(
+            zl, zero_groups, n_order, nblocks, work, order);
+    if (pixels) {
         p.tile_order = order;
         rc = eval3d_bwd_launch(a->cdim, dyn, p, s);
         if (rc) return rc;
