@@ -146,7 +146,8 @@ int xsg_sh_fwd(int degree, const float* origin, int64_t n, int dim, const float*
 
 size_t xsg_sh_bwd_workspace_bytes(int64_t n);
 /* d_coeffs (every band written), d_coeffs_dc (if has_dc), d_positions and d_origin[3] are outputs;
- * none needs zero-initialisation. */
+ * none needs zero-initialisation. d_origin may be NULL (an extension): the origin gradient, a sum over
+ * every Gaussian, is then not computed. */
 int xsg_sh_bwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
                const float* coeffs, const uint32_t* mask, int layout_3kn, const float* d_output,
                int has_dc, float* d_coeffs, float* d_coeffs_dc, float* d_positions,

@@ -69,6 +69,12 @@ def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask, sparse):
         print(report(name, np_(a), b))
         assert np_(a).shape == b.shape, name
         assert frac_close(np_(a), b, GRAD_ATOL, GRAD_RTOL) == 1.0, name
+    # origin_grad=False (extension): no origin gradient, the same bits for everything else
+    nco, ndc, npos, nori = _C.spherical_harmonics_fused_bwd(degree, D(origin), D(pos), D(coeffs), D(mask),
+                                                            layout_3kn, D(d_out), D(dc), origin_grad=False)
+    assert nori is None
+    for a, b in ((nco, dco), (ndc, ddc), (npos, dpos)):
+        assert torch.equal(a, b)
 
 
 # ------------------------------------------------------------------ projection, rays

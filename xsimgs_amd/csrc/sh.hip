@@ -378,7 +378,9 @@ __global__ __launch_bounds__(kBlock) void sh_bwd_kernel(
             }
         }
     }
-    // d_origin = -sum(d_positions) (sh_bwd.cu:306-314): wave sums, then one partial per block
+    // d_origin = -sum(d_positions) (sh_bwd.cu:306-314): wave sums, then one partial per block (none
+    // when the caller takes no origin gradient)
+    if (!origin_partial) return;
     float ox = wave_sum(-dpos.x), oy = wave_sum(-dpos.y), oz = wave_sum(-dpos.z);
     const int w = t >> 6;
     if ((t & 63) == 0) { red[0][w] = ox; red[1][w] = oy; red[2][w] = oz; }
@@ -480,8 +482,9 @@ int sh_bwd_run(int degree, const float* origin, int64_t n, int dim, const float*
     if (dim < ref_dims[degree] - (has_dc ? 1 : 0))
         return xsg_fail(XSG_ERR_INVALID, "coeffs hold %d bands, degree %d needs %d", dim, degree,
                         ref_dims[degree] - (has_dc ? 1 : 0));
+    if (!d_origin) part = nullptr;  // no origin gradient: neither partials nor their sum
     if (n == 0) {  // d_origin = 0 without a memset node (callers may capture this in a graph)
-        sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, 0, d_origin);
+        if (d_origin) sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, 0, d_origin);
         XSG_TRY_LAUNCH("sh_bwd");
         return XSG_OK;
     }
@@ -499,7 +502,7 @@ int sh_bwd_run(int degree, const float* origin, int64_t n, int dim, const float*
         case 4: XSG_B(4); break;
     }
 #undef XSG_B
-    sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, (int)nb, d_origin);
+    if (d_origin) sum_partials_kernel<<<1, kSumThreads, 0, s>>>(part, (int)nb, d_origin);
     XSG_TRY_LAUNCH("sh_bwd");
     return XSG_OK;
 }

@@ -377,11 +377,13 @@ Tensor spherical_harmonics_fused_fwd(int64_t degree_to_use, const Tensor& origin
     return out;
 }
 
-// spherical_harmonics_fused_bwd (sh_bwd.cu:317-390)
-std::tuple<Tensor, Tensor, Tensor, Tensor> spherical_harmonics_fused_bwd(int64_t degree_to_use, const Tensor& origin,
-                                                                       const Tensor& positions, const Tensor& coeffs,
-                                                                       const OptT& mask, bool layout_3kn,
-                                                                       const Tensor& d_output, const OptT& coeffs_dc) {
+// spherical_harmonics_fused_bwd (sh_bwd.cu:317-390). origin_grad = false (extension): the origin
+// gradient, a sum over every Gaussian, is not computed and comes back as None.
+std::tuple<Tensor, Tensor, Tensor, OptT> spherical_harmonics_fused_bwd(int64_t degree_to_use, const Tensor& origin,
+                                                                     const Tensor& positions, const Tensor& coeffs,
+                                                                     const OptT& mask, bool layout_3kn,
+                                                                     const Tensor& d_output, const OptT& coeffs_dc,
+                                                                     bool origin_grad) {
     all_contiguous({d_output});
     int64_t N, dim;
     sh_checks(degree_to_use, origin, positions, coeffs, mask, layout_3kn, coeffs_dc, N, dim);
@@ -390,14 +392,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> spherical_harmonics_fused_bwd(int64_t
     Tensor d_coeffs = at::empty_like(coeffs);
     Tensor d_dc = has_dc ? at::empty_like(*coeffs_dc) : at::empty({0}, coeffs.options());
     Tensor d_pos = at::empty_like(positions);
-    Tensor d_origin = at::empty({3}, origin.options());
+    Tensor d_origin = origin_grad ? at::empty({3}, origin.options()) : Tensor();
     Tensor ws = workspace(positions, xsg_sh_bwd_workspace_bytes(N));
     check_rc(xsg_sh_bwd((int)degree_to_use, fptr(origin), N, (int)dim, fptr(positions), fptr(coeffs),
                         mask.has_value() ? (const uint32_t*)mask->data_ptr() : nullptr, layout_3kn ? 1 : 0,
                         fptr(d_output), has_dc ? 1 : 0, d_coeffs.data_ptr<float>(),
                         has_dc ? d_dc.data_ptr<float>() : nullptr, d_pos.data_ptr<float>(),
-                        d_origin.data_ptr<float>(), ws.data_ptr(), stream_of(positions)));
-    return {d_coeffs, d_dc, d_pos, d_origin};
+                        origin_grad ? d_origin.data_ptr<float>() : nullptr, ws.data_ptr(), stream_of(positions)));
+    return {d_coeffs, d_dc, d_pos, origin_grad ? OptT(d_origin) : std::nullopt};
 }
 
 // ------------------------------------------------------------------ binning
@@ -1216,7 +1218,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("coeffs_dc") = py::none(), py::arg("output") = py::none());
     m.def("spherical_harmonics_fused_bwd", &spherical_harmonics_fused_bwd, py::arg("degree_to_use"),
           py::arg("origin"), py::arg("positions"), py::arg("coeffs"), py::arg("mask"), py::arg("layout_3kn"),
-          py::arg("d_output"), py::arg("coeffs_dc") = py::none());
+          py::arg("d_output"), py::arg("coeffs_dc") = py::none(), py::arg("origin_grad") = true);
 
     // tiling (csrc/tiling/bind_tiling.cpp)
     m.def("isect_offset_encode", &isect_offset_encode, py::arg("isect_ids"), py::arg("tile_width"),

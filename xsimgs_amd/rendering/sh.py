@@ -20,8 +20,10 @@ class SphericalHarmonicsFused(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         origin, positions, coeffs, mask, coeffs_dc = ctx.saved_tensors
+        # the origin gradient (a sum over every Gaussian) only when the origin needs one
         d_coeffs, d_coeffs_dc, d_positions, d_origin = spherical_harmonics_fused_bwd(
-            ctx.degree_to_use, origin, positions, coeffs, mask, ctx.layout_3kn, grad_out.contiguous(), coeffs_dc)
+            ctx.degree_to_use, origin, positions, coeffs, mask, ctx.layout_3kn, grad_out.contiguous(), coeffs_dc,
+            origin_grad=ctx.needs_input_grad[2])
         # order of the forward inputs: coeffs, positions, origin, degree_to_use, mask, layout_3kn, coeffs_dc
         return apply_grad_mask(ctx, (d_coeffs, d_positions, d_origin, None, None, None, d_coeffs_dc))
 
