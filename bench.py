@@ -305,11 +305,13 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             off = _C.isect_offset_encode(ids, ntx, nty)
             ro, rd = cam.camera_rays(W, H)
             pairs = torch.zeros(2, dtype=torch.int64, device=dev)
+            # the per-tile work estimates the forward writes for the backward, as the autograd functions pass them
+            tw = torch.empty(off.numel(), dtype=torch.int32, device=dev)
             rgb, depth, alpha, last = _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0),
                                                               opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl,
-                                                              pair_counts=pairs)
+                                                              pair_counts=pairs, tile_work=tw)
             c = dict(cam=cam, origin=origin, colors=colors, cdim=cdim, proj=(flags, radii, m2, dep), ids=ids, fl=fl,
-                     off=off, ro=ro, rd=rd, alpha=alpha, last=last, n_isects=int(fl.numel()),
+                     off=off, tw=tw, ro=ro, rd=rd, alpha=alpha, last=last, n_isects=int(fl.numel()),
                      visible=int((tpg > 0).sum()), n_flag2=int((flags == 2).sum()))
             c["fwd_evaluated"], c["contributing"] = (int(x) for x in pairs.cpu())
             n_isects = c["n_isects"]
@@ -328,14 +330,14 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 g_rgb, g_d, g_a = grads[ci]
                 bpairs = torch.zeros(2, dtype=torch.int64, device=dev)
                 bo = _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx, tsy, off, fl, alpha,
-                                             last, g_rgb, g_d, g_a, False, pair_counts=bpairs)
+                                             last, g_rgb, g_d, g_a, False, pair_counts=bpairs, tile_work=tw)
                 c["v_colors"] = bo[4]
                 c["bwd_evaluated"], c["bwd_composited"] = (int(x) for x in bpairs.cpu())
             info.append(c)
         c0 = info[0]
         cam, origin, colors, cdim = c0["cam"], c0["origin"], c0["colors"], c0["cdim"]
         flags, radii, m2, dep = c0["proj"]
-        ids, fl, off, ro, rd, alpha, last = (c0[k] for k in ("ids", "fl", "off", "ro", "rd", "alpha", "last"))
+        ids, fl, off, tw, ro, rd, alpha, last = (c0[k] for k in ("ids", "fl", "off", "tw", "ro", "rd", "alpha", "last"))
         n_isects = c0["n_isects"]
         enc_reads = 8 * int(math.ceil(math.log2(n_isects + 1))) if n_isects else 0
         stages = {
@@ -351,20 +353,22 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             "offset_encode": (lambda: _C.isect_offset_encode(ids, ntx, nty), (enc_reads + 4) * ntx * nty),
             "rays": (lambda: cam.camera_rays(W, H), 24 * W * H),
             "eval3d_fwd": (lambda: _C.rasterize_eval3d_fwd(means, quats, scales, colors.unsqueeze(0),
-                                                           opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl),
+                                                           opac.view(1, -1), W, H, tsx, tsy, ro, rd, off, fl,
+                                                           tile_work=tw),
                            (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * c0["fwd_loaded"]),
         }
         if backward:
             g_rgb, g_d, g_a = grads[0]
             stages["eval3d_bwd"] = (lambda: _C.rasterize_eval3d_bwd(means, scales, quats, opac, colors, ro, rd, tsx,
                                                                     tsy, off, fl, alpha, last, g_rgb, g_d, g_a,
-                                                                    False),
+                                                                    False, tile_work=tw),
                                     (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * c0["bwd_loaded"] +
                                     (11 + cdim) * 4 * N)
             if sh is not None:
                 v_colors = c0["v_colors"]
                 stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh, None,
-                                                                             False, v_colors, None),
+                                                                             False, v_colors, None,
+                                                                             origin_grad=False),
                                     sh_bwd_alg_bytes(K, N, v_colors))
         per_frame = {"sh_fwd", "sh_bwd"}   # one call per frame: the scenes with SH have one camera or a rig
         if rig:
@@ -376,8 +380,9 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
             off_b = torch.empty((n_cams, nty, ntx), dtype=torch.int32, device=dev)
             _, _, fl_b = _C.isect_regular_tiles_batched(m2_b, radii_b, dep_b, W, H, tsx, tsy, tile_offsets=off_b)
             col_b = colors if frame.rig_shares_origin(st) else stk("colors")
+            tw_b = torch.empty(off_b.numel(), dtype=torch.int32, device=dev)
             _, _, alpha_b, last_b = _C.rasterize_eval3d_fwd_batched(means, quats, scales, col_b, opac, W, H, tsx, tsy,
-                                                                    ro_b, rd_b, off_b, fl_b)
+                                                                    ro_b, rd_b, off_b, fl_b, tile_work=tw_b)
             n_col = 1 if col_b.dim() == 2 else n_cams
             if len({type(c["cam"]) for c in info}) == 1:
                 # the rig's cameras of one kind project in one launch, each Gaussian read once: its inputs
@@ -394,7 +399,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 sum(binning_alg_bytes(kind, N, c["n_isects"], ntx * nty, c["n_flag2"]) for c in info))
             stages["eval3d_fwd"] = (
                 lambda: _C.rasterize_eval3d_fwd_batched(means, quats, scales, col_b, opac, W, H, tsx, tsy, ro_b,
-                                                        rd_b, off_b, fl_b),
+                                                        rd_b, off_b, fl_b, tile_work=tw_b),
                 n_cams * (24 + 4 * cdim + 12) * W * H + (48 + 4 * cdim) * tot("fwd_loaded"))
             per_frame |= {"binning", "eval3d_fwd", "eval3d_bwd"}
             if backward:
@@ -402,7 +407,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 stages["eval3d_bwd"] = (
                     lambda: _C.rasterize_eval3d_bwd_batched(means, scales, quats, opac, col_b, ro_b, rd_b, tsx, tsy,
                                                             off_b, fl_b, alpha_b, last_b, gb[0], gb[1], gb[2],
-                                                            ray_grads=False),
+                                                            ray_grads=False, tile_work=tw_b),
                     n_cams * (24 + 8 + 4 * cdim + 8) * W * H + (48 + 4 * cdim) * tot("bwd_loaded") +
                     (11 + n_col * cdim) * 4 * N)
                 if sh is not None and n_col == 1:
@@ -410,7 +415,8 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                                                               off_b, fl_b, alpha_b, last_b, gb[0], gb[1], gb[2],
                                                               ray_grads=False)[4]
                     stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh,
-                                                                                 None, False, v_col_b, None),
+                                                                                 None, False, v_col_b, None,
+                                                                                 origin_grad=False),
                                         sh_bwd_alg_bytes(K, N, v_col_b))
         stages = {k: v for k, v in stages.items() if v is not None}
         timed_stages = stages
