@@ -413,7 +413,7 @@ def bench_config(name, args, steps, warmup, reps, torch, np, cpu=True, extension
                 if sh is not None and n_col == 1:
                     v_col_b = _C.rasterize_eval3d_bwd_batched(means, scales, quats, opac, col_b, ro_b, rd_b, tsx, tsy,
                                                               off_b, fl_b, alpha_b, last_b, gb[0], gb[1], gb[2],
-                                                              ray_grads=False)[4]
+                                                              ray_grads=False, tile_work=tw_b)[4]
                     stages["sh_bwd"] = (lambda: _C.spherical_harmonics_fused_bwd(sc.sh_degree, origin, means, sh,
                                                                                  None, False, v_col_b, None,
                                                                                  origin_grad=False),

@@ -1,12 +1,10 @@
 """One training frame of the hot path, as the reference's caller runs it.
 
-activations (exp scales, sigmoid opacity: one fused launch, its gradients another) -> UT projection
--> tile binning with sort -> per-tile offsets -> SH colours -> camera rays -> eval3d composite
-forward -> composite backward -> SH backward -> activation gradients. The sequence is
-ut_gs_render's (reference src/xsimgs/rendering/render.py:85-187) with the intermediates kept for
-inspection; the activations and the SH call are the caller's, as in the reference, whose caller
-evaluates the colours before the tiling: they are queued after it here (nothing before the
-compositor reads them), so that the GPU runs them while the host finishes the tiling.
+activations (exp scales, sigmoid opacity: one fused launch, its gradients another) -> SH colours -> UT projection -> tile binning with
+sort -> per-tile offsets -> camera rays -> eval3d composite forward -> composite backward ->
+SH backward -> activation gradients. The sequence is ut_gs_render's (reference
+src/xsimgs/rendering/render.py:85-187) with the intermediates kept for inspection; the
+activations and the SH call are the caller's, as in the reference.
 """
 from __future__ import annotations
 
@@ -70,19 +68,17 @@ def render_frame(st: FrameState, backward: bool = False, grads=None, cam_index: 
     spec = sc.cameras[cam_index]
     cam = st.cams[cam_index]
     scales, opac = activate_gaussians(st.log_scales, st.opacity_logits)
+    if st.sh is not None:
+        origin = cam.pose.t
+        colors = spherical_harmonics_fused(st.sh, st.means, origin, sc.sh_degree)
+    else:
+        colors = st.colors
     tsx, tsy = sc.tile_size
     with cam._freeze_ctx():
-        # The tiling goes first: its count readback waits for the GPU to reach the compaction, and the
-        # colours and rays queued after it (the compositor is the first to read them) keep the GPU busy
-        # while the host queues the rest of the binning.
-        tiles = ut_gs_tiling(cam, st.means, scales, st.quats, spec.width, spec.height, opacity=opac,
-                             tile_size_x=tsx, tile_size_y=tsy, use_phm=sc.use_phm)
-        if st.sh is not None:
-            colors = spherical_harmonics_fused(st.sh, st.means, cam.pose.t, sc.sh_degree)
-        else:
-            colors = st.colors
         ray_o, ray_d = cam.camera_rays(spec.width, spec.height, normalized_rays=True, return_origins=True,
                                        world_space=True)
+        tiles = ut_gs_tiling(cam, st.means, scales, st.quats, spec.width, spec.height, opacity=opac,
+                             tile_size_x=tsx, tile_size_y=tsy, use_phm=sc.use_phm)
         rgb, depth, alpha = ut_gs_rasterize(st.means, st.quats, scales, opac, colors, ray_o, ray_d,
                                             tiles["isect_offsets"], tiles["flatten_ids"], tsx, tsy)
     out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d,
@@ -127,6 +123,13 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
         raise ValueError("render_rig takes a static rig of regular-tiling cameras of one image size")
     W, H = specs[0].width, specs[0].height
     scales, opac = activate_gaussians(st.log_scales, st.opacity_logits)
+    if st.sh is None:
+        colors = st.colors
+    elif rig_shares_origin(st):
+        colors = spherical_harmonics_fused(st.sh, st.means, st.cams[0].pose.t, sc.sh_degree)
+    else:
+        colors = torch.stack([spherical_harmonics_fused(st.sh, st.means, cam.pose.t, sc.sh_degree)
+                              for cam in st.cams])
     tsx, tsy = sc.tile_size
     ntx, nty = (W + tsx - 1) // tsx, (H + tsy - 1) // tsy
     C, N = len(specs), st.means.shape[0]
@@ -139,6 +142,9 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
     with torch.no_grad(), contextlib.ExitStack() as frozen:
         for cam in st.cams:
             frozen.enter_context(cam._freeze_ctx())
+        for c, cam in enumerate(st.cams):
+            cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True,
+                            out=(ray_o[c], ray_d[c]))
         if one_kind:
             cam0 = st.cams[0]
             flags, radii, means2d, depths = cam0.ext_cls.projection_utgs_rig(
@@ -157,18 +163,6 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
         offsets = torch.empty((len(specs), nty, ntx), dtype=torch.int32, device=st.device)
         _, _, flatten_ids = isect_regular_tiles_batched(means2d, radii, depths, W, H, tsx, tsy, sort=True,
                                                         tile_offsets=offsets, keys=False)
-        # rays and colours after the binning, as in render_frame: they keep the GPU busy while the
-        # host queues the binning's second half after its count readback
-        for c, cam in enumerate(st.cams):
-            cam.camera_rays(W, H, normalized_rays=True, return_origins=True, world_space=True,
-                            out=(ray_o[c], ray_d[c]))
-    if st.sh is None:
-        colors = st.colors
-    elif rig_shares_origin(st):
-        colors = spherical_harmonics_fused(st.sh, st.means, st.cams[0].pose.t, sc.sh_degree)
-    else:
-        colors = torch.stack([spherical_harmonics_fused(st.sh, st.means, cam.pose.t, sc.sh_degree)
-                              for cam in st.cams])
     rgb, depth, alpha = ut_gs_rasterize_batched(st.means, st.quats, scales, opac, colors, ray_o, ray_d, offsets,
                                                 flatten_ids, tsx, tsy)
     out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d, offsets=offsets,
