@@ -478,6 +478,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(kBwdWaves<CD
                 }
 #pragma unroll
                 for (int h = 1; h < PX; ++h) {
+                    // a slot none of whose pixels reaches this Gaussian adds nothing: not evaluated
+                    if (__builtin_amdgcn_ballot_w64(px[h].inside && gidx <= px[h].bin_final) == 0) continue;
                     const BwdEval e = eval(h);
                     if (__builtin_amdgcn_ballot_w64(e.valid) != 0) {  // wave-uniform
                         any_valid = true;
