@@ -143,6 +143,12 @@ int xsg_pixel_time_bwd(int kind, const float* pack, int width, int height, const
 int xsg_sh_fwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
                const float* coeffs, const float* coeffs_dc, const uint32_t* mask, int layout_3kn,
                float* out, xsg_stream_t stream);
+/* Extension (no counterpart in the reference): xsg_sh_fwd that, with zero_masked != 0, writes zeros
+ * to the rows the mask excludes instead of leaving them as the caller had them, so a caller with a
+ * fresh output buffer needs no separate fill. zero_masked = 0 is xsg_sh_fwd. */
+int xsg_sh_fwd_ex(int degree, const float* origin, int64_t n, int dim, const float* positions,
+                  const float* coeffs, const float* coeffs_dc, const uint32_t* mask, int layout_3kn,
+                  int zero_masked, float* out, xsg_stream_t stream);
 
 size_t xsg_sh_bwd_workspace_bytes(int64_t n);
 /* d_coeffs (every band written), d_coeffs_dc (if has_dc), d_positions and d_origin[3] are outputs;
@@ -211,6 +217,15 @@ int xsg_rigid_transform_bwd(const xsg_rigid_desc* d, const float* v_positions, c
                             const float* v_velocities, float* grad_positions, float* grad_rotations,
                             float* grad_q, float* grad_t, float* grad_v, float* grad_w, void* workspace,
                             xsg_stream_t stream);
+
+/* Extension, no reference counterpart: the Gaussians some tile of a regular tiling can hold, as a packed
+ * mask in packed_mask_from_instances's format (out[(n + 31) / 32], bit i % 32 of word i / 32): set when
+ * some camera's radii of Gaussian i (radii [n_cams, n, 2], camera-major, as the UT projection writes
+ * them) pass the tiling's test, i.e. are not (r.x <= 0 or r.y <= 0). A caller that evaluates SH colours
+ * after the projection passes it as the SH mask, so that the colours of Gaussians no tile holds, which
+ * the compositor never reads, are not evaluated. */
+int xsg_packed_visibility_from_radii(int64_t n, int n_cams, const float* radii, uint32_t* out,
+                                     xsg_stream_t stream);
 
 /* Extension, no reference counterpart: the parameter activations a training caller applies before
  * the path (torch.exp of the log-scales, torch.sigmoid of the opacity logits; the reference takes

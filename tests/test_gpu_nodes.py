@@ -197,3 +197,18 @@ def test_activate_gaussians_one_sided_gradients(dev):
     s, o = activate_gaussians(ls, lg)
     gls, glg = torch.autograd.grad((o ** 2).sum(), (ls, lg), allow_unused=True)
     assert gls is None and torch.equal(glg, torch.autograd.grad((torch.sigmoid(lg) ** 2).sum(), lg)[0])
+
+
+@pytest.mark.parametrize("n_cams,n", [(1, 1), (1, 1000), (1, 100_003), (3, 4097)])
+def test_packed_visibility_mask(dev, n_cams, n):
+    """The visibility mask of the regular tilings (an extension): bit i set iff some camera's radii of
+    Gaussian i are not (r.x <= 0 or r.y <= 0), the test by which the tiling gives an instance no tile;
+    zeros, negatives and NaNs included. Packed as numpy packbits (little bit order)."""
+    g = np.random.default_rng(n + n_cams)
+    r = g.choice(np.array([0.0, -1.0, 0.5, 3.0, np.nan, -0.0], np.float32), size=(n_cams, n, 2))
+    radii = torch.from_numpy(r if n_cams > 1 else r[0]).to(dev)
+    out = _C.packed_visibility_mask(radii)
+    keep = (~((r[..., 0] <= 0) | (r[..., 1] <= 0))).any(axis=0)
+    want = np.packbits(np.pad(keep, (0, 32 * ((n + 31) // 32) - n)), bitorder="little").view(np.uint32)
+    assert out.dtype == torch.uint32 and out.shape == ((n + 31) // 32,)
+    np.testing.assert_array_equal(out.cpu().view(torch.int32).numpy().view(np.uint32), want)

@@ -35,11 +35,13 @@ def cfg0(dev):
     (0, False, False, False, False), (3, False, False, False, False), (3, True, False, False, False),
     (3, False, True, True, False), (4, True, True, False, False), (2, False, False, True, False),
     (1, True, False, True, False), (3, False, False, False, True), (3, True, False, False, True),
-    (4, False, True, True, True)])
+    (4, False, True, True, True), (3, False, False, True, True), (2, False, True, True, True)])
 def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask, sparse):
     """sparse: the colour gradient is zero for most Gaussians (those no tile composited), as in a
     frame; the backward then reads coefficients only for the rows that need them, except in blocks
-    of 256 Gaussians where most do (here: the first block dense, the second at about a third)."""
+    of 256 Gaussians where most do (here: the first block dense, the second at about a third). With a
+    mask, sparse also thins the mask (most bits clear past the first block, as a frame's visibility
+    mask is), so that the forward reads the rows of sparse blocks one by one."""
     g = torch.Generator().manual_seed(7 + degree)
     n = 3001
     K = (degree + 1) ** 2 + 2            # extra unused bands must come back zero in d_coeffs
@@ -49,6 +51,11 @@ def test_sh_fwd_bwd(dev, degree, layout_3kn, with_dc, with_mask, sparse):
     coeffs = torch.randn(3, kb, n, generator=g) if layout_3kn else torch.randn(n, kb, 3, generator=g)
     dc = (torch.randn(3, n, generator=g) if layout_3kn else torch.randn(n, 3, generator=g)) if with_dc else None
     mask = torch.randint(-2**31, 2**31 - 1, ((n + 31) // 32,), generator=g, dtype=torch.int32) if with_mask else None
+    if with_mask and sparse:
+        bits = torch.rand(n, generator=g) < 0.08
+        bits[:256] = torch.rand(256, generator=g) < 0.6
+        words = np.packbits(np.pad(bits.numpy(), (0, 32 * ((n + 31) // 32) - n)), bitorder="little")
+        mask = torch.from_numpy(words.view(np.int32).copy())
     d_out = torch.randn(n, 3, generator=g)
     if sparse:
         keep = torch.rand(n, generator=g) < 0.12
@@ -125,6 +132,37 @@ def test_isect_regular_bitexact(dev, cfg0, sort):
         off = _C.isect_offset_encode(ids, 16, 16)
         assert np.array_equal(np_(off), O.offset_encode(rids, 16, 16))
 
+
+@pytest.mark.parametrize("layout_3kn", [False, True])
+def test_sh_fwd_ex_zero_masked(dev, layout_3kn):
+    """xsg_sh_fwd_ex (an extension) through the C-ABI: with zero_masked the rows the mask excludes
+    become zeros, without it they keep what the buffer held, as xsg_sh_fwd leaves them; the other rows
+    are the oracle's either way."""
+    import ctypes
+    from xsimgs_amd import _build
+    lib = ctypes.CDLL(_build.lib_path())
+    n, degree, dim = 1000, 3, 16
+    g = np.random.default_rng(5)
+    pos = g.normal(size=(n, 3)).astype(np.float32)
+    origin = np.array([0.1, -0.2, 0.3], np.float32)
+    coeffs = g.normal(size=(3, dim, n) if layout_3kn else (n, dim, 3)).astype(np.float32)
+    keep = g.random(n) < 0.3
+    words = np.packbits(np.pad(keep, (0, 32 * ((n + 31) // 32) - n)), bitorder="little").view(np.uint32)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    tp, to, tc, tm = T(pos), T(origin), T(coeffs), T(words.view(np.int32))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    outs = []
+    for fn, extra in ((lib.xsg_sh_fwd, ()), (lib.xsg_sh_fwd_ex, (0,)), (lib.xsg_sh_fwd_ex, (1,))):
+        out = torch.full((n, 3), 7.0, device=dev)
+        assert fn(degree, P(to), ctypes.c_int64(n), dim, P(tp), P(tc), None, P(tm), int(layout_3kn), *extra,
+                  P(out), stream) == 0
+        outs.append(np_(out))
+    ref = O.sh_fwd(degree, origin, pos, coeffs, mask=words, layout_3kn=layout_3kn)
+    assert np.array_equal(outs[0], outs[1])
+    assert (outs[0][~keep] == 7.0).all() and (outs[2][~keep] == 0.0).all()
+    assert np.array_equal(outs[2][keep], outs[0][keep])
+    assert frac_close(outs[2][keep], ref[keep], RENDER_ATOL) == 1.0
 
 def test_release_thread_resources(dev, cfg0):
     """xsg_isect_count's per-thread readback buffer and event: released through the C-ABI on the thread

@@ -24,6 +24,26 @@ __global__ __launch_bounds__(kBlock) void packed_mask_kernel(int64_t n, const in
     if ((lane & 31) == 0 && word < ((n + 31) >> 5)) out[word] = lane ? (uint32_t)(b >> 32) : (uint32_t)b;
 }
 
+// Visibility of the regular tilings' Gaussians as a packed mask (an extension): bit i % 32 of word
+// i / 32 set when some camera's radii of Gaussian i pass the tiling's test (an instance whose radii are
+// not both positive, r.x <= 0 || r.y <= 0, gets no tile), so that every Gaussian a tile can hold has its
+// bit. Radii [n_cams, n, 2], camera-major.
+__global__ __launch_bounds__(kBlock) void packed_visibility_kernel(int64_t n, int n_cams,
+                                                                   const float2* __restrict__ radii,
+                                                                   uint32_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    bool v = false;
+    if (i < n)
+        for (int c = 0; c < n_cams; ++c) {
+            const float2 r = radii[(int64_t)c * n + i];
+            v = v || !(r.x <= 0.0f || r.y <= 0.0f);
+        }
+    const uint64_t b = __ballot(v);
+    const int lane = __lane_id();
+    const int64_t word = i >> 5;
+    if ((lane & 31) == 0 && word < ((n + 31) >> 5)) out[word] = lane ? (uint32_t)(b >> 32) : (uint32_t)b;
+}
+
 struct RigidArgs {
     int64_t n, n_inst, n_out, buffer_offset;
     const float* pos;
@@ -344,6 +364,17 @@ static bool aligned16(std::initializer_list<const void*> ps) {  // NULL counts a
     for (const void* p : ps)
         if (reinterpret_cast<uintptr_t>(p) % 16) return false;
     return true;
+}
+
+extern "C" int xsg_packed_visibility_from_radii(int64_t n, int n_cams, const float* radii, uint32_t* out,
+                                                xsg_stream_t stream) {
+    if (n < 0 || n_cams < 1) return xsg_fail(XSG_ERR_INVALID, "packed_visibility_from_radii: bad sizes");
+    if (n == 0) return XSG_OK;
+    if (!radii || !out) return xsg_fail(XSG_ERR_INVALID, "packed_visibility_from_radii: null tensor");
+    packed_visibility_kernel<<<xsg_blocks(n, kBlock), kBlock, 0, (hipStream_t)stream>>>(
+        n, n_cams, reinterpret_cast<const float2*>(radii), out);
+    XSG_TRY_LAUNCH("packed_visibility_from_radii");
+    return XSG_OK;
 }
 
 extern "C" int xsg_activate_fwd(int64_t n, const float* log_scales, const float* opacity_logits, float* scales,

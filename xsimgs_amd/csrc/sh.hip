@@ -204,12 +204,21 @@ __global__ __launch_bounds__(kBlock) void sh_fwd_nk3_kernel(
     __shared__ float lds[kBlock * S];
     const int64_t g0 = (int64_t)blockIdx.x * kBlock;
     const int rows = (int)min<int64_t>(kBlock, n - g0);
-    if constexpr (NB > 0) stage_rows<RL, S>(lds, coeffs + g0 * dim * 3, (int64_t)dim * 3, rows);
-    __syncthreads();
     const int t = threadIdx.x;
     const int64_t i = g0 + t;
-    if (t >= rows) return;
-    if (!mask_ok(mask, i)) {
+    const bool active = t < rows;
+    const bool valid = active && mask_ok(mask, i);
+    // A block whose rows mostly pass the mask stages them all with wide loads; a sparse block (a mask
+    // of the Gaussians some tile can hold, most of a frame's scene off screen) reads only its own rows,
+    // straight from global memory (copying them to LDS first measured slower).
+    bool staged = true;
+    if constexpr (NB > 0) {
+        staged = !mask || 4 * __syncthreads_count(valid) > rows;  // block-uniform
+        if (staged) stage_rows<RL, S>(lds, coeffs + g0 * dim * 3, (int64_t)dim * 3, rows);
+    }
+    __syncthreads();
+    if (!active) return;
+    if (!valid) {
         if (zero_masked) { out[3 * i] = 0.f; out[3 * i + 1] = 0.f; out[3 * i + 2] = 0.f; }
         return;
     }
@@ -218,13 +227,15 @@ __global__ __launch_bounds__(kBlock) void sh_fwd_nk3_kernel(
     float Y[(DEG + 1) * (DEG + 1)];
     sh_basis<DEG>(dir, Y);
     const float* row = lds + t * S;
+    const float* grow = coeffs + i * dim * 3;  // the row in global memory, when not staged
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         float dcv = 0.f;
         if constexpr (HAS_DC) dcv = dc[3 * i + c];
         auto cf = [&](int k) -> float {
-            if constexpr (HAS_DC) return k == 0 ? dcv : row[(k - 1) * 3 + c];
-            else return row[k * 3 + c];
+            const int kb = k - (HAS_DC ? 1 : 0);
+            if (HAS_DC && k == 0) return dcv;
+            return staged ? row[kb * 3 + c] : grow[kb * 3 + c];
         };
         out[3 * i + c] = sh_color<DEG>(dir, Y, cf) + 0.5f;
     }
@@ -431,6 +442,13 @@ void launch_bwd(bool l3kn, dim3 g, hipStream_t s, int64_t n, int dim, const floa
 extern "C" int xsg_sh_fwd(int degree, const float* origin, int64_t n, int dim, const float* positions,
                           const float* coeffs, const float* coeffs_dc, const uint32_t* mask,
                           int layout_3kn, float* out, xsg_stream_t stream) {
+    // masked Gaussians keep the caller's output values (the reference writes into `output` or zeros)
+    return xsg_sh_fwd_ex(degree, origin, n, dim, positions, coeffs, coeffs_dc, mask, layout_3kn, 0, out, stream);
+}
+
+extern "C" int xsg_sh_fwd_ex(int degree, const float* origin, int64_t n, int dim, const float* positions,
+                             const float* coeffs, const float* coeffs_dc, const uint32_t* mask,
+                             int layout_3kn, int zero_masked_arg, float* out, xsg_stream_t stream) {
     // sh_fwd.cu:162-245 checks
     static const int ref_dims[5] = {1, 4, 9, 16, 25};
     if (degree < 0 || degree > 4)
@@ -443,8 +461,7 @@ extern "C" int xsg_sh_fwd(int degree, const float* origin, int64_t n, int dim, c
                         coeffs_dc ? " (zero-degree coeffs passed separately)" : "");
     if (n < 0) return xsg_fail(XSG_ERR_INVALID, "xsg_sh_fwd: n < 0");
     if (n == 0) return XSG_OK;
-    // masked Gaussians keep the caller's output values (the reference writes into `output` or zeros)
-    const int zero_masked = 0;
+    const int zero_masked = (zero_masked_arg != 0 && mask) ? 1 : 0;
     const dim3 g(xsg_blocks(n, kBlock));
     const hipStream_t s = (hipStream_t)stream;
     const bool l = layout_3kn != 0;

@@ -367,13 +367,12 @@ Tensor spherical_harmonics_fused_fwd(int64_t degree_to_use, const Tensor& origin
     sh_checks(degree_to_use, origin, positions, coeffs, mask, layout_3kn, coeffs_dc, N, dim);
     if (output.has_value()) { check_same_device({origin, *output}); all_contiguous({*output}); }
     const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(positions.device());
-    // without a mask the kernel writes every row; masked rows keep the output's values (zeros here)
-    Tensor out = output.has_value() ? *output
-                 : mask.has_value()   ? at::zeros({N, 3}, positions.options())
-                                      : at::empty({N, 3}, positions.options());
-    check_rc(xsg_sh_fwd((int)degree_to_use, fptr(origin), N, (int)dim, fptr(positions), fptr(coeffs), fptr(coeffs_dc),
-                        mask.has_value() ? (const uint32_t*)mask->data_ptr() : nullptr, layout_3kn ? 1 : 0,
-                        out.data_ptr<float>(), stream_of(positions)));
+    // masked rows keep a given output's values; a fresh output gets zeros there from the kernel itself
+    Tensor out = output.has_value() ? *output : at::empty({N, 3}, positions.options());
+    check_rc(xsg_sh_fwd_ex((int)degree_to_use, fptr(origin), N, (int)dim, fptr(positions), fptr(coeffs),
+                           fptr(coeffs_dc), mask.has_value() ? (const uint32_t*)mask->data_ptr() : nullptr,
+                           layout_3kn ? 1 : 0, output.has_value() ? 0 : 1, out.data_ptr<float>(),
+                           stream_of(positions)));
     return out;
 }
 
@@ -598,6 +597,21 @@ std::tuple<Tensor, Tensor> radix_sort_pairs(const Tensor& keys, const Tensor& va
 
 // ------------------------------------------------------------------ scene-assembly producers
 // mask_from_instances (csrc/nodes/gs_masking.cu:29-44)
+// Extension: the packed mask of the Gaussians some tile of a regular tiling can hold, from the UT
+// projection's radii [N, 2] or [C, N, 2] (any camera)
+Tensor packed_visibility_mask(const Tensor& radii) {
+    check_f32(radii, "radii");
+    all_contiguous({radii});
+    TORCH_CHECK((radii.dim() == 2 || radii.dim() == 3) && radii.size(-1) == 2, "radii must be [N, 2] or [C, N, 2]");
+    const int64_t n = radii.size(-2);
+    const int n_cams = radii.dim() == 3 ? (int)radii.size(0) : 1;
+    TORCH_CHECK(n_cams >= 1, "radii must hold at least one camera");
+    const c10::hip::OptionalHIPGuardMasqueradingAsCUDA guard(radii.device());
+    Tensor out = at::empty({(n + 31) / 32}, radii.options().dtype(at::kUInt32));
+    check_rc(xsg_packed_visibility_from_radii(n, n_cams, fptr(radii), (uint32_t*)out.data_ptr(), stream_of(radii)));
+    return out;
+}
+
 // Extension: the caller's parameter activations, scales = exp(log_scales) and opacities =
 // sigmoid(opacity_logits), in one launch; and their gradients in one launch (either may be None).
 std::tuple<Tensor, Tensor> activate_fwd(const Tensor& log_scales, const Tensor& opacity_logits) {
@@ -1247,6 +1261,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     // scene-assembly producers (csrc/nodes/gs_masking.cu:44-47, container.cu:269-303)
     m.def("packed_mask_from_instances", &packed_mask_from_instances, py::arg("instance_ids"),
           py::arg("instance_mask"));
+    // extension: the visibility mask of the regular tilings' Gaussians (an SH mask)
+    m.def("packed_visibility_mask", &packed_visibility_mask, py::arg("radii"));
     // extension: the caller's parameter activations and their gradients
     m.def("activate_fwd", &activate_fwd, py::arg("log_scales"), py::arg("opacity_logits"));
     m.def("activate_bwd", &activate_bwd, py::arg("scales"), py::arg("opacities"), py::arg("v_scales"),

@@ -1,10 +1,13 @@
 """One training frame of the hot path, as the reference's caller runs it.
 
-activations (exp scales, sigmoid opacity: one fused launch, its gradients another) -> SH colours -> UT projection -> tile binning with
-sort -> per-tile offsets -> camera rays -> eval3d composite forward -> composite backward ->
-SH backward -> activation gradients. The sequence is ut_gs_render's (reference
-src/xsimgs/rendering/render.py:85-187) with the intermediates kept for inspection; the
-activations and the SH call are the caller's, as in the reference.
+activations (exp scales, sigmoid opacity: one fused launch, its gradients another) -> camera rays ->
+UT projection -> tile binning with sort -> per-tile offsets -> SH colours -> eval3d composite forward
+-> composite backward -> SH backward -> activation gradients. The sequence is ut_gs_render's
+(reference src/xsimgs/rendering/render.py:85-187) with the intermediates kept for inspection; the
+activations and the SH call are the caller's, as in the reference, whose caller evaluates the colours
+first: here they come after the projection, for the Gaussians some tile can hold only (the SH mask),
+which gives the same images and gradients. render_rig keeps the colours first and unmasked: over a
+rig most Gaussians are in some camera's view, and the mask there cost more than it saved.
 """
 from __future__ import annotations
 
@@ -14,7 +17,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import cameras as C
-from ._C import isect_regular_tiles_batched
+from ._C import isect_regular_tiles_batched, packed_visibility_mask
 from .rendering.activate import activate_gaussians
 from .rendering.rasterize import ut_gs_rasterize, ut_gs_rasterize_batched
 from .rendering.render import ut_gs_tiling
@@ -68,17 +71,13 @@ def render_frame(st: FrameState, backward: bool = False, grads=None, cam_index: 
     spec = sc.cameras[cam_index]
     cam = st.cams[cam_index]
     scales, opac = activate_gaussians(st.log_scales, st.opacity_logits)
-    if st.sh is not None:
-        origin = cam.pose.t
-        colors = spherical_harmonics_fused(st.sh, st.means, origin, sc.sh_degree)
-    else:
-        colors = st.colors
     tsx, tsy = sc.tile_size
     with cam._freeze_ctx():
         ray_o, ray_d = cam.camera_rays(spec.width, spec.height, normalized_rays=True, return_origins=True,
                                        world_space=True)
         tiles = ut_gs_tiling(cam, st.means, scales, st.quats, spec.width, spec.height, opacity=opac,
                              tile_size_x=tsx, tile_size_y=tsy, use_phm=sc.use_phm)
+        colors = _colors(st, cam.pose.t, tiles["radii"] if spec.kind in REGULAR_TILING else None)
         rgb, depth, alpha = ut_gs_rasterize(st.means, st.quats, scales, opac, colors, ray_o, ray_d,
                                             tiles["isect_offsets"], tiles["flatten_ids"], tsx, tsy)
     out = dict(rgb=rgb, depth=depth, alpha=alpha, colors=colors, ray_o=ray_o, ray_d=ray_d,
@@ -175,6 +174,18 @@ def render_rig(st: FrameState, backward: bool = False, grads=None) -> dict:
                             sh=st.sh.grad if st.sh is not None else None,
                             colors=st.colors.grad if st.colors is not None else None)
     return out
+
+
+def _colors(st: FrameState, origin, radii=None):
+    """The Gaussians' colours: SH evaluated at the origin, or the fixed colours. With the radii of a
+    regular tiling's projection ([N, 2], or [C, N, 2] for all the cameras of one origin), only the
+    Gaussians some tile can hold are evaluated (the SH mask; the others' colours are zeros). The
+    compositor reads no other Gaussian's colour, so the images are the same and so are the gradients
+    (the others' colour gradients are zeros either way)."""
+    if st.sh is None:
+        return st.colors
+    mask = packed_visibility_mask(radii.detach().contiguous()) if radii is not None else None
+    return spherical_harmonics_fused(st.sh, st.means, origin, st.scene.sh_degree, mask=mask)
 
 
 def zero_grads(st: FrameState) -> None:
