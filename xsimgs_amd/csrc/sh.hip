@@ -226,19 +226,22 @@ __global__ __launch_bounds__(kBlock) void sh_fwd_nk3_kernel(
     const f3 dir = diff * (1.0f / sqrtf(dot(diff, diff)));
     float Y[(DEG + 1) * (DEG + 1)];
     sh_basis<DEG>(dir, Y);
-    const float* row = lds + t * S;
-    const float* grow = coeffs + i * dim * 3;  // the row in global memory, when not staged
+    // the row in LDS when staged, else in global memory: one block-uniform branch, each side with
+    // plain loads from one address space (a select per coefficient slowed the unmasked kernel by 10 %)
+    auto shade = [&](const float* row) {
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        float dcv = 0.f;
-        if constexpr (HAS_DC) dcv = dc[3 * i + c];
-        auto cf = [&](int k) -> float {
-            const int kb = k - (HAS_DC ? 1 : 0);
-            if (HAS_DC && k == 0) return dcv;
-            return staged ? row[kb * 3 + c] : grow[kb * 3 + c];
-        };
-        out[3 * i + c] = sh_color<DEG>(dir, Y, cf) + 0.5f;
-    }
+        for (int c = 0; c < 3; ++c) {
+            float dcv = 0.f;
+            if constexpr (HAS_DC) dcv = dc[3 * i + c];
+            auto cf = [&](int k) -> float {
+                if constexpr (HAS_DC) return k == 0 ? dcv : row[(k - 1) * 3 + c];
+                else return row[k * 3 + c];
+            };
+            out[3 * i + c] = sh_color<DEG>(dir, Y, cf) + 0.5f;
+        }
+    };
+    if (staged) shade(lds + t * S);
+    else shade(coeffs + i * dim * 3);
 }
 
 // [3, K, N] layout (band stride N): coalesced per thread without staging.
