@@ -139,6 +139,32 @@ def test_render_frame(dev, kind):
         assert frac_close(a, b, RENDER_ATOL) > 0.999, name
 
 
+def test_render_frame_sh_mask_changes_nothing(dev, monkeypatch):
+    """render_frame evaluates the SH colours of the Gaussians some tile holds only (the others get
+    zeros). The images equal, bit for bit, those of the same frame with every Gaussian's colour (the
+    compositor reads no other colour), and so do the colours it reads; the leaf gradients agree to the
+    float32 rounding of the compositor's atomic sums, and a Gaussian with no tile gets exact zero SH
+    gradients either way."""
+    from tests._util import GRAD_ATOL, GRAD_RTOL
+    sc = synthetic.make_cfg2(n=200_000)
+    runs = []
+    for masked in (True, False):
+        if not masked:
+            monkeypatch.setattr(frame, "REGULAR_TILING", ())  # no regular tiling: colours of all Gaussians
+        st = frame.prepare(sc, dev)
+        runs.append(frame.render_frame(st, backward=True, grads=(sc.grad_rgb[0], sc.grad_depth[0], sc.grad_alpha[0])))
+    a, b = runs
+    for k in ("rgb", "depth", "alpha", "flatten_ids", "offsets"):
+        assert torch.equal(a[k], b[k]), k
+    seen = (a["radii"] > 0).all(-1)
+    assert 0 < int(seen.sum()) < seen.numel()
+    assert torch.equal(a["colors"][seen], b["colors"][seen])
+    assert not a["colors"][~seen].any()
+    for k in ("means", "quats", "log_scales", "opacity_logits", "sh"):
+        np.testing.assert_allclose(np_(a["grads"][k]), np_(b["grads"][k]), rtol=GRAD_RTOL, atol=GRAD_ATOL,
+                                   err_msg=k)
+    assert not a["grads"]["sh"][~seen].any() and not b["grads"]["sh"][~seen].any()
+
 @pytest.mark.parametrize("kind", KINDS)
 def test_valid_mask_on_folding_lens(dev, kind):
     """Lenses that fold inside the image: the validity masks agree with the oracle and the rays agree
